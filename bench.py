@@ -1,0 +1,490 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused RMSNorm + SiLU-and-mul path on one MI355X.
+
+One *step* is one pass of the hot path over one batch of synthetic input at
+the Qwen2.5-1.5B prefill shape (BASELINE configs 1 and 2): RMSNorm over
+x [2048, 1536] fp16 followed by SiLU-and-mul over gate/up [2048, 8960] fp16.
+Every step runs on the next of several buffer sets whose total footprint is
+above 1 GiB (4x the 256 MB Infinity Cache), so each step reads cold HBM.
+
+`value` is the whole job's algorithmic bandwidth over the timed steps:
+K * (RMSNorm bytes + SiLU-and-mul bytes) / elapsed, in GB/s, with the inputs
+already resident in HBM.  Algorithmic bytes: RMSNorm (2*M*N + N) * 2,
+SiLU-and-mul 3 * M * I * 2.
+
+Also reported on the same JSON line:
+  roofline      dominant kernel (SiLU-and-mul, C2): bytes / average launch
+                duration from HIP events on the launch stream, vs 8 TB/s;
+                traffic = FETCH_SIZE + WRITE_SIZE per launch from the
+                committed rocprofv3 PMC summary (profiles/), when present;
+  cpu_baseline  the reference's naive PyTorch path (restated in the oracle),
+                timed on the host cores on a bounded sample of the workload;
+  kernels       per-kernel durations and GB/s (C1, C2, C4), cold and warm;
+  decode        C3 latency per call (host-inclusive and device-only) and
+                inside a hipGraph of 28 x (RMSNorm, SiLU-and-mul, RMSNorm);
+  copy_ceiling  a plain 16-byte streaming copy on the same device.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = "llm-inference-optimizer_amd"
+PEAK_GBS = 8000.0  # MI355X HBM3E, published
+METRIC = "achieved HBM GB/s (% of 8 TB/s peak) for RMSNorm+SwiGLU; decode-row latency µs"
+MALL_BYTES = 256 * 2**20
+MIN_FOOTPRINT = 1 << 30
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="wall-clock budget of the CPU-baseline sample")
+    p.add_argument("--skip-cpu", action="store_true")
+    p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c4-silu", "c4-rms", "copy"], default=None,
+                   help="run one kernel loop only (for profiler runs)")
+    return p.parse_args()
+
+
+class Ctx:
+    """Bound C-ABI entry points.  Launch closures read `self.stream` at call
+    time, so a graph capture can redirect them to the capturing stream."""
+
+    def __init__(self):
+        import torch
+
+        sys.path.insert(0, str(ROOT))
+        self.torch = torch
+        self.pkg = importlib.import_module(PKG)
+        self.L = importlib.import_module(PKG + "._lib")
+        self.lib = self.L.load()
+        self.dev = torch.device("cuda:0")
+        torch.cuda.set_device(self.dev)
+        self.stream = torch.cuda.current_stream(self.dev).cuda_stream
+        probe_path = ROOT / PKG / "libmi355_probe.so"
+        self.probe = ctypes.CDLL(str(probe_path)) if probe_path.exists() else None
+        if self.probe is not None:
+            self.probe.mi355_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                                    ctypes.c_int, ctypes.c_void_p]
+            self.probe.mi355_probe_copy.restype = ctypes.c_int
+
+    def rms_call(self, x, w, y, eps=1e-6):
+        M, N = x.shape
+        code = self.L.DTYPE_CODE[x.dtype]
+        f = self.lib.mi355_rmsnorm_fwd
+        args = (x.data_ptr(), w.data_ptr(), y.data_ptr(), M, N, N, N, ctypes.c_float(eps), code,
+                self.L.DTYPE_CODE[w.dtype], code)
+
+        def call():
+            st = f(*args, self.stream)
+            if st:
+                self.L.check("mi355_rmsnorm_fwd", st)
+        return call
+
+    def silu_call(self, g, u, o):
+        code = self.L.DTYPE_CODE[g.dtype]
+        f = self.lib.mi355_silu_mul_fwd
+        args = (g.data_ptr(), u.data_ptr(), o.data_ptr(), g.numel(), code, code)
+
+        def call():
+            st = f(*args, self.stream)
+            if st:
+                self.L.check("mi355_silu_mul_fwd", st)
+        return call
+
+    def copy_call(self, src, dst):
+        f = self.probe.mi355_probe_copy
+        args = (src.data_ptr(), dst.data_ptr(), src.numel() * src.element_size(), 0)
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError("probe copy failed")
+        return call
+
+
+def rand(ctx, shape, seed, dtype, mean=0.0, std=1.0):
+    torch = ctx.torch
+    g = torch.Generator(device=ctx.dev)
+    g.manual_seed(seed)
+    t = torch.randn(*shape, generator=g, device=ctx.dev, dtype=torch.float32)
+    if mean != 0.0 or std != 1.0:
+        t = t.mul_(std).add_(mean)
+    return t.to(dtype)
+
+
+def n_sets(bytes_per_set: int) -> int:
+    return max(1, -(-MIN_FOOTPRINT // bytes_per_set))
+
+
+def time_loop(ctx, calls, iters, warmup=5):
+    """Average device time per iteration of `calls` (list cycled), from HIP
+    events recorded on the launch stream around `iters` back-to-back launches."""
+    torch = ctx.torch
+    for i in range(warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        calls[i % len(calls)]()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / iters  # us
+
+
+def time_graph(ctx, calls, iters, replays=5):
+    """Average device time per launch with `iters` launches captured in one
+    hipGraph (no host launch cost between kernels)."""
+    torch = ctx.torch
+    s = torch.cuda.Stream(device=ctx.dev)
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    old = ctx.stream
+    try:
+        with torch.cuda.stream(s):
+            ctx.stream = s.cuda_stream  # the closures now launch on the capture stream
+            for c in calls:
+                c()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=s):
+                for i in range(iters):
+                    calls[i % len(calls)]()
+    finally:
+        ctx.stream = old
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (replays * iters)
+
+
+def kernel_entry(name, nbytes, us, extra=None):
+    d = {"kernel": name, "bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+         "frac_of_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4)}
+    if extra:
+        d.update(extra)
+    return d
+
+
+def read_traffic(kernel_key: str):
+    """FETCH_SIZE + WRITE_SIZE per launch (bytes) recorded from rocprofv3 PMC
+    runs in profiles/traffic.json, if that summary exists."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text()).get(kernel_key)
+        return None if d is None else d.get("traffic_bytes")
+    except Exception:
+        return None
+
+
+def cpu_baseline(M, N, I, budget_s):
+    """The reference's naive PyTorch path (oracle restatement) on the host
+    cores: RMSNorm [M,N] + SiLU-and-mul [M,I] fp16, repeated for ~budget_s."""
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+
+    cores = len(os.sched_getaffinity(0))
+    env_threads = os.environ.get("OMP_NUM_THREADS")
+    if env_threads and env_threads.isdigit():
+        cores = min(cores, int(env_threads))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, N, generator=g).to(torch.float16)
+    w = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.float16)
+    gate = torch.randn(M, I, generator=g).to(torch.float16)
+    up = torch.randn(M, I, generator=g).to(torch.float16)
+    orc.naive_rmsnorm_torch(x, w)
+    orc.naive_silu_mul_torch(gate, up)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        orc.naive_rmsnorm_torch(x, w)
+        orc.naive_silu_mul_torch(gate, up)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 1000:
+            break
+    step = statistics.median(times)
+    nbytes = (2 * M * N + N) * 2 + 3 * M * I * 2
+    try:
+        model = next(line.split(":", 1)[1].strip() for line in open("/proc/cpuinfo") if line.startswith("model name"))
+    except Exception:
+        model = "unknown"
+    return {"value": round(nbytes / step / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "ms_per_step": round(step * 1e3, 3), "steps_timed": len(times),
+            "cpu_model": model,
+            "sample": f"naive torch RMSNorm [{M},{N}] + SiLU-and-mul [{M},{I}] fp16 on host tensors, "
+                      f"median of {len(times)} steps in ~{budget_s:.0f}s"}
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the fused RMSNorm/SwiGLU path is row-parallel "
+              "and needs no cross-GPU exchange); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = Ctx()
+    torch = ctx.torch
+    props = torch.cuda.get_device_properties(ctx.dev)
+    log(f"device: {props.name} ({getattr(props, 'gcnArchName', '?')}), CUs={props.multi_processor_count}")
+
+    F16, BF16 = torch.float16, torch.bfloat16
+    M, N, I = 2048, 1536, 8960
+    rms_bytes = (2 * M * N + N) * 2
+    silu_bytes = 3 * M * I * 2
+    step_bytes = rms_bytes + silu_bytes
+    nset = n_sets(step_bytes)
+
+    w = rand(ctx, (N,), 1, F16, 1.0, 0.1)
+    sets = []
+    for s in range(nset):
+        x = rand(ctx, (M, N), 100 + s, F16)
+        gate = rand(ctx, (M, I), 200 + s, F16)
+        up = rand(ctx, (M, I), 300 + s, F16)
+        y = torch.empty_like(x)
+        out = torch.empty_like(gate)
+        sets.append((ctx.rms_call(x, w, y), ctx.silu_call(gate, up, out), (x, y, gate, up, out)))
+    torch.cuda.synchronize()
+    log(f"headline: {nset} buffer sets, footprint {nset * step_bytes / 2**30:.2f} GiB")
+
+    if args.only:
+        run_only(ctx, args, sets)
+        return
+
+    # ---- timed region: K steps, each RMSNorm C1 + SiLU-and-mul C2 on the next set
+    for i in range(args.warmup):
+        r, s_, _ = sets[i % nset]
+        r()
+        s_()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        r, s_, _ = sets[i % nset]
+        r()
+        s_()
+    end.record()
+    torch.cuda.synchronize()
+    elapsed_s = start.elapsed_time(end) / 1e3
+    value = args.steps * step_bytes / elapsed_s / 1e9
+    log(f"headline: {args.steps} steps in {elapsed_s * 1e3:.2f} ms -> {value:.1f} GB/s "
+        f"({value / PEAK_GBS:.1%} of 8 TB/s)")
+
+    # ---- per-kernel average launch durations (cold HBM, rotating sets)
+    iters = max(200, args.steps)
+    silu_us = time_loop(ctx, [s[1] for s in sets], iters)
+    rms_us = time_loop(ctx, [s[0] for s in sets], iters)
+    rms_graph_us = time_graph(ctx, [s[0] for s in sets], 200)
+    silu_warm_us = time_loop(ctx, [sets[0][1]], iters)
+    rms_warm_graph_us = time_graph(ctx, [sets[0][0]], 200)
+    kernels = {
+        "c2_silu_mul_f16_2048x8960": kernel_entry("silu_mul_vec<F16,F16,4>", silu_bytes, silu_us,
+                                                  {"timing": "events over back-to-back launches, cold"}),
+        "c1_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes, rms_us,
+                                                 {"timing": "events over back-to-back launches, cold"}),
+        "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes,
+                                                       rms_graph_us, {"timing": "hipGraph of 200 launches, cold"}),
+        "c2_silu_mul_f16_2048x8960_warm": kernel_entry("silu_mul_vec<F16,F16,4>", silu_bytes, silu_warm_us,
+                                                       {"timing": "same buffers every launch (MALL-warm)"}),
+        "c1_rmsnorm_f16_2048x1536_warm_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes,
+                                                            rms_warm_graph_us,
+                                                            {"timing": "hipGraph, same buffers (MALL-warm)"}),
+    }
+    for k, v in kernels.items():
+        log(f"  {k}: {v['us']:.2f} us, {v['GBps']:.0f} GB/s ({v['frac_of_peak']:.1%})")
+
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed_s * 1e3 / args.steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) gate/up/x, N(1,0.1) weight, fp16 storage)",
+        "config": {"workload": "qwen2.5-1.5b-prefill-2048: RMSNorm x[2048,1536] + SiLU-and-mul gate/up[2048,8960]",
+                   "storage_dtype": "f16", "math_dtype": "f32", "eps": 1e-6, "buffer_sets": nset,
+                   "footprint_GiB": round(nset * step_bytes / 2**30, 3), "step_bytes": step_bytes},
+        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "kernel": "silu_mul_vec (C2 SiLU-and-mul [2048,8960] fp16)",
+                     "achieved": round(silu_bytes / silu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(silu_bytes / silu_us / 1e3 / PEAK_GBS, 4),
+                     "traffic": read_traffic("c2_silu_mul"), "algorithmic_bytes": silu_bytes,
+                     "avg_launch_us": round(silu_us, 3)},
+        "kernels": kernels,
+    }
+
+    if not args.skip_extras:
+        del sets
+        torch.cuda.empty_cache()
+        result["c4"] = bench_c4(ctx, iters=60)
+        result["decode"] = bench_decode(ctx)
+        result["copy_ceiling"] = bench_copy(ctx)
+
+    if not args.skip_cpu:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(M, N, I, args.cpu_seconds)
+        log(f"  cpu: {result['cpu_baseline']['value']} GB/s on {result['cpu_baseline']['cores']} threads")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+def run_only(ctx, args, sets):
+    """One kernel loop only, so a profiler run sees exactly one kernel name."""
+    torch = ctx.torch
+    iters = max(200, args.steps)
+    if args.only == "c2-silu":
+        us = time_loop(ctx, [s[1] for s in sets], iters)
+        log(f"c2-silu avg {us:.3f} us")
+    elif args.only == "c1-rms":
+        us = time_loop(ctx, [s[0] for s in sets], iters)
+        log(f"c1-rms avg {us:.3f} us")
+    elif args.only in ("c4-silu", "c4-rms"):
+        del sets
+        torch.cuda.empty_cache()
+        d = bench_c4(ctx, iters=60, which=args.only)
+        log(json.dumps(d))
+    elif args.only == "copy":
+        log(json.dumps(bench_copy(ctx)))
+
+
+def bench_c4(ctx, iters=60, which=None):
+    torch = ctx.torch
+    BF16 = torch.bfloat16
+    out = {}
+    if which in (None, "c4-rms"):
+        M, N = 16384, 3584
+        nbytes = (2 * M * N + N) * 2
+        w = rand(ctx, (N,), 1, BF16, 1.0, 0.1)
+        calls, keep = [], []
+        for s in range(n_sets(nbytes)):
+            x = rand(ctx, (M, N), 400 + s, BF16)
+            y = torch.empty_like(x)
+            keep.append((x, y))
+            calls.append(ctx.rms_call(x, w, y))
+        us = time_loop(ctx, calls, iters)
+        out["c4_rmsnorm_bf16_16384x3584"] = kernel_entry("rmsnorm_wave_rows<BF16,BF16,BF16,7>", nbytes, us,
+                                                         {"buffer_sets": len(calls)})
+        del keep, calls
+        torch.cuda.empty_cache()
+    if which in (None, "c4-silu"):
+        M, I = 16384, 18944
+        nbytes = 3 * M * I * 2
+        gate = rand(ctx, (M, I), 500, BF16)
+        up = rand(ctx, (M, I), 501, BF16)
+        o = torch.empty_like(gate)
+        us = time_loop(ctx, [ctx.silu_call(gate, up, o)], iters)
+        out["c4_silu_mul_bf16_16384x18944"] = kernel_entry("silu_mul_vec<BF16,BF16,4>", nbytes, us,
+                                                           {"buffer_sets": 1, "footprint_GiB": round(nbytes / 2**30, 2)})
+        del gate, up, o
+        torch.cuda.empty_cache()
+    for k, v in out.items():
+        log(f"  {k}: {v['us']:.2f} us, {v['GBps']:.0f} GB/s ({v['frac_of_peak']:.1%})")
+    return out
+
+
+def bench_decode(ctx, layers=28):
+    """C3: decode shapes.  Per call through the Python API (host-inclusive,
+    synchronised like the reference's _time_cuda), device-only from events
+    over back-to-back ABI launches, and inside a hipGraph of `layers` x
+    (RMSNorm, SiLU-and-mul, RMSNorm) on per-layer buffers."""
+    torch = ctx.torch
+    F16 = torch.float16
+    N, I = 1536, 8960
+    res = {}
+    for M in (1, 2, 4, 8, 32):
+        w = rand(ctx, (N,), 1, F16, 1.0, 0.1)
+        x = rand(ctx, (M, N), 600 + M, F16)
+        g = rand(ctx, (M, I), 700 + M, F16)
+        u = rand(ctx, (M, I), 800 + M, F16)
+
+        def api_us(fn, n=200):
+            for _ in range(10):
+                fn()
+            ts = []
+            for _ in range(n):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                ts.append((time.perf_counter() - t0) * 1e6)
+            return statistics.median(ts)
+
+        rms_api = api_us(lambda: ctx.pkg.fused_rmsnorm(x, w))
+        silu_api = api_us(lambda: ctx.pkg.fused_silu_mul(g, u))
+        y = torch.empty_like(x)
+        o = torch.empty_like(g)
+        rms_dev = time_loop(ctx, [ctx.rms_call(x, w, y)], 2000)
+        silu_dev = time_loop(ctx, [ctx.silu_call(g, u, o)], 2000)
+
+        # 28-layer graph on per-layer buffers
+        xs = [rand(ctx, (M, N), 900 + l, F16) for l in range(layers)]
+        ys = [torch.empty_like(t) for t in xs]
+        gs = [rand(ctx, (M, I), 1000 + l, F16) for l in range(layers)]
+        us_ = [rand(ctx, (M, I), 1100 + l, F16) for l in range(layers)]
+        os_ = [torch.empty_like(t) for t in gs]
+        ws = [rand(ctx, (N,), 1200 + l, F16, 1.0, 0.1) for l in range(2 * layers)]
+        zs = [torch.empty_like(t) for t in xs]
+        calls = []
+        for l in range(layers):
+            calls += [ctx.rms_call(xs[l], ws[2 * l], ys[l]), ctx.silu_call(gs[l], us_[l], os_[l]),
+                      ctx.rms_call(ys[l], ws[2 * l + 1], zs[l])]
+        per_kernel = time_graph(ctx, calls, len(calls), replays=50)
+        replay_us = per_kernel * len(calls)
+        res[f"M={M}"] = {
+            "rmsnorm_api_us": round(rms_api, 2), "silu_mul_api_us": round(silu_api, 2),
+            "rmsnorm_device_us": round(rms_dev, 3), "silu_mul_device_us": round(silu_dev, 3),
+            "graph_replay_us": round(replay_us, 2), "graph_per_layer_us": round(replay_us / layers, 3),
+            "graph_per_kernel_us": round(per_kernel, 3),
+            "rows_per_s_rmsnorm": round(M / (rms_dev * 1e-6)),
+        }
+        log(f"  decode M={M}: {res[f'M={M}']}")
+    return res
+
+
+def bench_copy(ctx, nbytes=1 << 30, iters=30):
+    """Plain 16-byte streaming copy of 1 GiB (2 GiB of traffic per launch)."""
+    if ctx.probe is None:
+        return None
+    torch = ctx.torch
+    src = torch.empty(nbytes, dtype=torch.uint8, device=ctx.dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    us = time_loop(ctx, [ctx.copy_call(src, dst)], iters)
+    d = kernel_entry("stream_copy", 2 * nbytes, us)
+    del src, dst
+    torch.cuda.empty_cache()
+    log(f"  copy ceiling: {d['GBps']:.0f} GB/s ({d['frac_of_peak']:.1%})")
+    return d
+
+
+if __name__ == "__main__":
+    main()

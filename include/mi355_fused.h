@@ -1,0 +1,100 @@
+/*
+ * mi355_fused.h -- C ABI of the MI355X (gfx950) fused RMSNorm and SiLU-and-mul
+ * kernels.
+ *
+ * The reference has no FFI: its boundary is a pair of Python launchers that
+ * hand torch tensors to Triton kernels.  Each entry point below replaces one of
+ * those launches with a plain-pointer call, so a host binding (ctypes, a torch
+ * extension, C++) can drive the HIP kernels without any torch type crossing the
+ * boundary.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (HBM).  Sizes are element counts.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default
+ *     stream).  Work is enqueued on that stream only: no allocation, no host
+ *     synchronisation, no memset, so every call may be recorded into a HIP
+ *     graph.
+ *   - The return value is MI355_OK (0) or a negative MI355_ERR_* code; the
+ *     message for the most recent failure on the calling thread is returned by
+ *     mi355_last_error().  Nothing throws across the ABI.
+ *   - Calls are reentrant; the library holds no locks.  A call only reads its
+ *     inputs and writes its outputs; outputs must not overlap inputs unless
+ *     the pointers are identical and the strides match (in-place use).
+ */
+#ifndef MI355_FUSED_H
+#define MI355_FUSED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355_ABI_VERSION 1
+
+/* Element types understood by the kernels (storage type; arithmetic is fp32). */
+enum mi355_dtype {
+  MI355_F32 = 0,
+  MI355_F16 = 1,
+  MI355_BF16 = 2
+};
+
+/* Status codes. */
+enum mi355_status {
+  MI355_OK = 0,
+  MI355_ERR_INVALID = -1,     /* bad pointer, size, stride or dtype code */
+  MI355_ERR_UNSUPPORTED = -2, /* valid request the library cannot serve */
+  MI355_ERR_HIP = -3          /* the HIP runtime reported an error */
+};
+
+/* Version of this ABI; callers check it equals MI355_ABI_VERSION. */
+int mi355_abi_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* mi355_last_error(void);
+
+/*
+ * RMSNorm over the last dimension, one row at a time:
+ *   var_r  = (sum_j x[r,j]^2) / n            (fp32 accumulation)
+ *   rstd_r = 1 / sqrt(var_r + eps)
+ *   y[r,j] = (x[r,j] * rstd_r) * w[j]        (fp32, rounded once to y_dtype)
+ *
+ * Replaces the launch of `_rmsnorm_fwd_kernel` in the reference's
+ * `fused_rmsnorm` (src/kernels/fused_rmsnorm_triton.py:52-71, kernel body
+ * :23-49).  The reference's launcher reuses x's row stride for the output
+ * (:66-68) and makes x contiguous first (:60); here both row strides are
+ * explicit, so a row-strided view needs no copy.
+ *
+ *   x       [rows, x_row_stride] elements of x_dtype; row r starts at
+ *           x + r * x_row_stride and its n elements are contiguous.
+ *   weight  [n] elements of w_dtype, contiguous.
+ *   y       [rows, y_row_stride] elements of y_dtype.
+ *   rows    >= 0 (0 is a no-op), n >= 1, both row strides >= n.
+ *   y_dtype must equal x_dtype or be MI355_F32 (the fp32 value before the
+ *   final rounding, used to check the kernel's arithmetic on its own).
+ */
+int mi355_rmsnorm_fwd(const void* x, const void* weight, void* y,
+                      int64_t rows, int64_t n,
+                      int64_t x_row_stride, int64_t y_row_stride,
+                      float eps,
+                      int x_dtype, int w_dtype, int y_dtype,
+                      void* stream);
+
+/*
+ * SiLU-and-mul, the activation step of a SwiGLU MLP, over flat memory:
+ *   out[i] = (g * sigmoid(g)) * u,  g = gate[i], u = up[i]   (fp32, rounded once)
+ *
+ * Replaces the launch of `_silu_mul_fwd_kernel` in the reference's
+ * `fused_silu_mul` (src/kernels/fused_swiglu_triton.py:39-53, kernel body
+ * :20-36).  gate, up and out are `numel` contiguous elements; gate and up
+ * share in_dtype; out_dtype must equal in_dtype or be MI355_F32.
+ */
+int mi355_silu_mul_fwd(const void* gate, const void* up, void* out,
+                       int64_t numel, int in_dtype, int out_dtype,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355_FUSED_H */

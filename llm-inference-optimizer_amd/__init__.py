@@ -1,0 +1,29 @@
+"""MI355X-native fused RMSNorm + SwiGLU path for Qwen2-style decoders.
+
+The package directory name contains hyphens, so import it by name with
+importlib after putting the repository root on ``sys.path``::
+
+    import importlib, sys
+    sys.path.insert(0, "/path/to/repo")
+    fk = importlib.import_module("llm-inference-optimizer_amd")
+    fk.patch_model_with_fused_kernels(model)
+
+Public surface (the reference's Stage 3 plugin API):
+
+* ``fused_rmsnorm(x, weight, eps=1e-6)``, ``naive_rmsnorm_reference``
+* ``fused_silu_mul(gate, up)``, ``naive_silu_mul_reference``
+* ``FusedRMSNorm``, ``FusedMLP``, ``patch_model_with_fused_kernels``,
+  ``RMSNORM_CLASS_NAMES``, ``MLP_CLASS_NAMES``
+
+The kernels live in ``libmi355_fused.so`` (gfx950 HIP, C ABI in
+``include/mi355_fused.h``), built by ``build.py``.
+"""
+from .engine.fused_norm_activation_patch import (MLP_CLASS_NAMES, RMSNORM_CLASS_NAMES, FusedMLP, FusedRMSNorm,
+                                                 patch_model_with_fused_kernels)
+from .kernels.fused_rmsnorm_hip import fused_rmsnorm, naive_rmsnorm_reference
+from .kernels.fused_swiglu_hip import fused_silu_mul, naive_silu_mul_reference
+
+__all__ = [
+    "fused_rmsnorm", "naive_rmsnorm_reference", "fused_silu_mul", "naive_silu_mul_reference",
+    "FusedRMSNorm", "FusedMLP", "patch_model_with_fused_kernels", "RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES",
+]

@@ -1,0 +1,95 @@
+"""ctypes binding of the gfx950 kernel library ``libmi355_fused.so``.
+
+The library exposes the C ABI declared in ``include/mi355_fused.h``; this
+module loads it once, declares the argument types, checks the ABI version and
+turns a non-zero status into an exception carrying the library's message.
+
+There is no fallback: if the library has not been built, every kernel call
+raises ``KernelLibraryMissing`` (build it with ``python -c "import
+__graft_entry__ as g; g.build()"`` or ``python
+llm-inference-optimizer_amd/build.py``).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libmi355_fused.so"
+ABI_VERSION = 1
+
+# dtype codes of the C ABI (enum mi355_dtype)
+F32, F16, BF16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+EXPORTED_SYMBOLS = ("mi355_abi_version", "mi355_last_error", "mi355_rmsnorm_fwd", "mi355_silu_mul_fwd")
+
+
+class KernelLibraryMissing(RuntimeError):
+    """The HIP kernel library is not built (no silent CPU fallback exists)."""
+
+
+class KernelError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn} failed with status {status}: {message}")
+        self.status = status
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the kernel library."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise KernelLibraryMissing(
+                f"{LIB_PATH} is not built; run `python -c \"import __graft_entry__ as g; g.build()\"` "
+                "from the repository root (there is no CPU fallback)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.mi355_abi_version.argtypes = []
+        L.mi355_abi_version.restype = i32
+        L.mi355_last_error.argtypes = []
+        L.mi355_last_error.restype = ctypes.c_char_p
+        L.mi355_rmsnorm_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, i32, i32, i32, vp]
+        L.mi355_rmsnorm_fwd.restype = i32
+        L.mi355_silu_mul_fwd.argtypes = [vp, vp, vp, i64, i32, i32, vp]
+        L.mi355_silu_mul_fwd.restype = i32
+        ver = L.mi355_abi_version()
+        if ver != ABI_VERSION:
+            raise KernelLibraryMissing(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+        _lib = L
+    return _lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != 0:
+        raise KernelError(fn, status, load().mi355_last_error().decode(errors="replace"))
+
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on ``device`` (as an integer)."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def rmsnorm_fwd(x_ptr: int, w_ptr: int, y_ptr: int, rows: int, n: int, x_row_stride: int,
+                y_row_stride: int, eps: float, x_dtype: int, w_dtype: int, y_dtype: int, stream: int) -> None:
+    check("mi355_rmsnorm_fwd",
+          load().mi355_rmsnorm_fwd(x_ptr, w_ptr, y_ptr, rows, n, x_row_stride, y_row_stride, eps,
+                                   x_dtype, w_dtype, y_dtype, stream))
+
+
+def silu_mul_fwd(gate_ptr: int, up_ptr: int, out_ptr: int, numel: int, in_dtype: int, out_dtype: int,
+                 stream: int) -> None:
+    check("mi355_silu_mul_fwd",
+          load().mi355_silu_mul_fwd(gate_ptr, up_ptr, out_ptr, numel, in_dtype, out_dtype, stream))

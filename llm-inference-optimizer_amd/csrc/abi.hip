@@ -1,0 +1,127 @@
+// C ABI entry points (include/mi355_fused.h): argument validation, the
+// per-thread error message and the per-device CU-count cache.  Kernels and
+// their launchers live in rmsnorm.hip and silu_mul.hip.
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+
+#include "common.h"
+
+#define MI355_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace mi355 {
+
+int rmsnorm_launch(const void* x, const void* w, void* y, int64_t rows, int n, int64_t xs,
+                   int64_t ys, float eps, int x_dtype, int w_dtype, int y_dtype,
+                   hipStream_t stream);
+int silu_mul_launch(const void* gate, const void* up, void* out, int64_t numel, int in_dtype,
+                    int out_dtype, hipStream_t stream);
+
+namespace {
+thread_local char g_error[512] = "";
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+}  // namespace
+
+bool valid_dtype(int d) { return d == MI355_F32 || d == MI355_F16 || d == MI355_BF16; }
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+int compute_units(int* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int c = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *out = c;
+      return MI355_OK;
+    }
+  }
+  int c = 0;
+  e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return hip_status(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+  if (c < 1) c = 1;
+  if (dev >= 0 && dev < kMaxDevices) g_cu_count[dev].store(c, std::memory_order_relaxed);
+  *out = c;
+  return MI355_OK;
+}
+
+}  // namespace mi355
+
+using mi355::set_error;
+using mi355::valid_dtype;
+
+MI355_EXPORT int mi355_abi_version(void) { return MI355_ABI_VERSION; }
+
+MI355_EXPORT const char* mi355_last_error(void) { return mi355::g_error; }
+
+MI355_EXPORT int mi355_rmsnorm_fwd(const void* x, const void* weight, void* y, int64_t rows,
+                                   int64_t n, int64_t x_row_stride, int64_t y_row_stride,
+                                   float eps, int x_dtype, int w_dtype, int y_dtype,
+                                   void* stream) {
+  mi355::g_error[0] = '\0';
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype) || !valid_dtype(y_dtype)) {
+    set_error("mi355_rmsnorm_fwd: unknown dtype code (x=%d, w=%d, y=%d)", x_dtype, w_dtype, y_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (y_dtype != x_dtype && y_dtype != MI355_F32) {
+    set_error("mi355_rmsnorm_fwd: y dtype must equal x dtype or be fp32 (x=%d, y=%d)", x_dtype, y_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows < 0) {
+    set_error("mi355_rmsnorm_fwd: rows must be >= 0 (got %lld)", static_cast<long long>(rows));
+    return MI355_ERR_INVALID;
+  }
+  if (n < 1 || n > 0x7fffffff) {
+    set_error("mi355_rmsnorm_fwd: n must be in [1, 2^31) (got %lld)", static_cast<long long>(n));
+    return MI355_ERR_INVALID;
+  }
+  if (rows == 0) return MI355_OK;
+  if (x == nullptr || weight == nullptr || y == nullptr) {
+    set_error("mi355_rmsnorm_fwd: null pointer (x=%p, weight=%p, y=%p)", x, weight, y);
+    return MI355_ERR_INVALID;
+  }
+  if (x_row_stride < n || y_row_stride < n) {
+    set_error("mi355_rmsnorm_fwd: row strides must be >= n (x=%lld, y=%lld, n=%lld)",
+              static_cast<long long>(x_row_stride), static_cast<long long>(y_row_stride),
+              static_cast<long long>(n));
+    return MI355_ERR_INVALID;
+  }
+  if (rows - 1 > (INT64_MAX - n) / x_row_stride || rows - 1 > (INT64_MAX - n) / y_row_stride) {
+    set_error("mi355_rmsnorm_fwd: rows * stride overflows int64");
+    return MI355_ERR_INVALID;
+  }
+  return mi355::rmsnorm_launch(x, weight, y, rows, static_cast<int>(n), x_row_stride, y_row_stride,
+                               eps, x_dtype, w_dtype, y_dtype, static_cast<hipStream_t>(stream));
+}
+
+MI355_EXPORT int mi355_silu_mul_fwd(const void* gate, const void* up, void* out, int64_t numel,
+                                    int in_dtype, int out_dtype, void* stream) {
+  mi355::g_error[0] = '\0';
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype)) {
+    set_error("mi355_silu_mul_fwd: unknown dtype code (in=%d, out=%d)", in_dtype, out_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (out_dtype != in_dtype && out_dtype != MI355_F32) {
+    set_error("mi355_silu_mul_fwd: out dtype must equal in dtype or be fp32 (in=%d, out=%d)",
+              in_dtype, out_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (numel < 0) {
+    set_error("mi355_silu_mul_fwd: numel must be >= 0 (got %lld)", static_cast<long long>(numel));
+    return MI355_ERR_INVALID;
+  }
+  if (numel == 0) return MI355_OK;
+  if (gate == nullptr || up == nullptr || out == nullptr) {
+    set_error("mi355_silu_mul_fwd: null pointer (gate=%p, up=%p, out=%p)", gate, up, out);
+    return MI355_ERR_INVALID;
+  }
+  return mi355::silu_mul_launch(gate, up, out, numel, in_dtype, out_dtype,
+                                static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,133 @@
+// Launcher for the RMSNorm kernels: picks wave-per-row, workgroup-per-row or
+// the generic kernel from the row width, alignment and dtype mix, and sizes
+// the grid.
+#include "rmsnorm_kernels.h"
+
+// Waves the launcher keeps resident per CU for the row-striding kernels
+// (gfx950: 4 SIMDs x 8 wave slots = 32).
+#ifndef MI355_RMS_WAVES_PER_CU
+#define MI355_RMS_WAVES_PER_CU 32
+#endif
+// Row counts below this use 64-thread workgroups (one wave each), so small
+// decode batches spread over as many CUs as rows.
+#ifndef MI355_RMS_SMALL_ROWS
+#define MI355_RMS_SMALL_ROWS 1024
+#endif
+
+namespace mi355 {
+namespace {
+
+struct RmsArgs {
+  const void* x;
+  const void* w;
+  void* y;
+  int64_t rows;
+  int n;
+  int64_t xs;
+  int64_t ys;
+  float eps;
+};
+
+template <typename K>
+int launch_rms(K kernel, int64_t grid, int block, const RmsArgs& a, hipStream_t s) {
+  void* args[] = {const_cast<void**>(&a.x),      const_cast<void**>(&a.w),
+                  const_cast<void**>(&a.y),      const_cast<int64_t*>(&a.rows),
+                  const_cast<int*>(&a.n),        const_cast<int64_t*>(&a.xs),
+                  const_cast<int64_t*>(&a.ys),   const_cast<float*>(&a.eps)};
+  return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(kernel),
+                                    dim3(static_cast<unsigned>(grid)), dim3(block), args, 0, s),
+                    "rmsnorm launch");
+}
+
+template <typename TX, typename TW, typename TY>
+int rms_generic(const RmsArgs& a, hipStream_t s, int cus) {
+  int64_t grid = a.rows;
+  const int64_t cap = static_cast<int64_t>(cus) * 8;
+  if (grid > cap) grid = cap;
+  return launch_rms(rmsnorm_generic<TX, TW, TY>, grid, 256, a, s);
+}
+
+template <typename TX, typename TW, typename TY>
+int rms_wave(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
+  const int block = a.rows < MI355_RMS_SMALL_ROWS ? 64 : 256;
+  const int wpb = block / 64;
+  int64_t grid = (a.rows + wpb - 1) / wpb;
+  const int64_t cap = static_cast<int64_t>(cus) * MI355_RMS_WAVES_PER_CU / wpb;
+  if (grid > cap) grid = cap;
+#define MI355_WAVE_CASE(V) \
+  return launch_rms(rmsnorm_wave_rows<TX, TW, TY, V>, grid, block, a, s)
+  switch (vpl) {
+    case 1: MI355_WAVE_CASE(1);
+    case 2: MI355_WAVE_CASE(2);
+    case 3: MI355_WAVE_CASE(3);
+    case 4: MI355_WAVE_CASE(4);
+    case 5: MI355_WAVE_CASE(5);
+    case 6: MI355_WAVE_CASE(6);
+    case 7: MI355_WAVE_CASE(7);
+    case 8: MI355_WAVE_CASE(8);
+    case 9:
+    case 10: MI355_WAVE_CASE(10);
+    case 11:
+    case 12: MI355_WAVE_CASE(12);
+    default: MI355_WAVE_CASE(16);
+  }
+#undef MI355_WAVE_CASE
+}
+
+template <typename TX, typename TW, typename TY, int BLOCK>
+int rms_block(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
+  int64_t grid = a.rows;
+  const int64_t cap = static_cast<int64_t>(cus) * (MI355_RMS_WAVES_PER_CU / (BLOCK / 64));
+  if (grid > cap) grid = cap;
+  if (vpl <= 8) return launch_rms(rmsnorm_block_rows<TX, TW, TY, 8, BLOCK>, grid, BLOCK, a, s);
+  return launch_rms(rmsnorm_block_rows<TX, TW, TY, 16, BLOCK>, grid, BLOCK, a, s);
+}
+
+// Packet path: n a multiple of the packet width, every pointer and row
+// stride 16-byte aligned.
+template <typename TX, typename TW, typename TY>
+int rms_packets(const RmsArgs& a, hipStream_t s, int cus) {
+  constexpr int W = pack_width<TX>::value;
+  const bool ok = (a.n % W) == 0 && aligned16(a.x) && aligned16(a.w) && aligned16(a.y) &&
+                  (a.xs * static_cast<int64_t>(sizeof(typename TX::bits))) % 16 == 0 &&
+                  (a.ys * static_cast<int64_t>(sizeof(typename TY::bits))) % 16 == 0;
+  if (!ok) return rms_generic<TX, TW, TY>(a, s, cus);
+  const int nvec = a.n / W;
+  const int vpl64 = (nvec + 63) / 64;
+  if (vpl64 <= 16) return rms_wave<TX, TW, TY>(a, s, cus, vpl64);
+  const int vpl256 = (nvec + 255) / 256;
+  if (vpl256 <= 16) return rms_block<TX, TW, TY, 256>(a, s, cus, vpl256);
+  const int vpl1024 = (nvec + 1023) / 1024;
+  if (vpl1024 <= 16) return rms_block<TX, TW, TY, 1024>(a, s, cus, vpl1024);
+  return rms_generic<TX, TW, TY>(a, s, cus);
+}
+
+template <typename TX, typename TY>
+int rms_by_weight(const RmsArgs& a, int w_dtype, hipStream_t s, int cus) {
+  // Packet kernels exist for a weight stored like x or in fp32; other mixes
+  // take the generic kernel.
+  if (w_dtype == TX::code) return rms_packets<TX, TX, TY>(a, s, cus);
+  if (w_dtype == MI355_F32) return rms_packets<TX, F32, TY>(a, s, cus);
+  if (w_dtype == MI355_F16) return rms_generic<TX, F16, TY>(a, s, cus);
+  return rms_generic<TX, BF16, TY>(a, s, cus);
+}
+
+}  // namespace
+
+int rmsnorm_launch(const void* x, const void* w, void* y, int64_t rows, int n, int64_t xs,
+                   int64_t ys, float eps, int x_dtype, int w_dtype, int y_dtype,
+                   hipStream_t stream) {
+  int cus = 0;
+  int st = compute_units(&cus);
+  if (st != MI355_OK) return st;
+  const RmsArgs a{x, w, y, rows, n, xs, ys, eps};
+  if (x_dtype == MI355_F16 && y_dtype == MI355_F16) return rms_by_weight<F16, F16>(a, w_dtype, stream, cus);
+  if (x_dtype == MI355_F16 && y_dtype == MI355_F32) return rms_by_weight<F16, F32>(a, w_dtype, stream, cus);
+  if (x_dtype == MI355_BF16 && y_dtype == MI355_BF16) return rms_by_weight<BF16, BF16>(a, w_dtype, stream, cus);
+  if (x_dtype == MI355_BF16 && y_dtype == MI355_F32) return rms_by_weight<BF16, F32>(a, w_dtype, stream, cus);
+  if (x_dtype == MI355_F32 && y_dtype == MI355_F32) return rms_by_weight<F32, F32>(a, w_dtype, stream, cus);
+  set_error("mi355_rmsnorm_fwd: unsupported dtype pair (x=%d, y=%d)", x_dtype, y_dtype);
+  return MI355_ERR_UNSUPPORTED;
+}
+
+}  // namespace mi355

@@ -1,0 +1,71 @@
+"""Fused RMSNorm on MI355X: drop-in for the reference's
+``src/kernels/fused_rmsnorm_triton.py``.
+
+``fused_rmsnorm`` keeps the reference launcher's signature, preconditions and
+output convention (:52-71): it normalises the last dimension, the output has
+x's dtype and shape, and a failed precondition raises ``AssertionError``.
+The computation runs in the gfx950 HIP kernels of ``libmi355_fused.so``
+(C ABI ``mi355_rmsnorm_fwd``) on torch's current stream; there is no
+Triton and no CPU fallback.
+
+Semantics are the reference Triton kernel's (:35-49): fp32 sum of squares,
+rstd = 1/sqrt(sum/n + eps), y = (x * rstd) * w in fp32, rounded once.
+
+``naive_rmsnorm_reference`` is the reference's unfused HF formula (:74-82),
+kept for callers that compare against it.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+__all__ = ["fused_rmsnorm", "naive_rmsnorm_reference"]
+
+
+def fused_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Drop-in replacement for HF's RMSNorm.forward.  x: (..., hidden_size),
+    weight: (hidden_size,).  Normalizes over the last dimension."""
+    assert x.is_cuda and weight.is_cuda, "x and weight must be ROCm GPU tensors"
+    orig_shape = x.shape
+    N = orig_shape[-1]
+    assert weight.shape == (N,), f"weight shape {tuple(weight.shape)} != ({N},)"
+    assert x.dtype in _lib.DTYPE_CODE and weight.dtype in _lib.DTYPE_CODE, (
+        f"unsupported dtypes x={x.dtype} weight={weight.dtype} (fp16, bf16, fp32)")
+    assert weight.device == x.device, "x and weight must be on the same device"
+
+    x2 = x.reshape(-1, N)
+    M = x2.shape[0]
+    # Rows only need to be contiguous along the hidden dimension: a row-strided
+    # view is passed with its stride instead of being copied.
+    if x2.stride(-1) != 1 or (M > 1 and x2.stride(0) < N):
+        x2 = x2.contiguous()
+    w = weight if weight.stride(0) == 1 else weight.contiguous()
+    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    if M == 0 or N == 0:
+        return out.reshape(orig_shape)
+
+    x_code = _lib.DTYPE_CODE[x.dtype]
+    dev = x.device
+    if dev.index is not None and dev.index != torch.cuda.current_device():
+        with torch.cuda.device(dev):
+            _launch(x2, w, out, M, N, eps, x_code, dev)
+    else:
+        _launch(x2, w, out, M, N, eps, x_code, dev)
+    return out.reshape(orig_shape)
+
+
+def _launch(x2, w, out, M, N, eps, x_code, dev):
+    _lib.rmsnorm_fwd(x2.data_ptr(), w.data_ptr(), out.data_ptr(), M, N,
+                     x2.stride(0) if M > 1 else N, N, float(eps),
+                     x_code, _lib.DTYPE_CODE[w.dtype], x_code, _lib.stream_handle(dev))
+
+
+def naive_rmsnorm_reference(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Unfused reference matching HF's RMSNorm formula: compute in fp32, cast
+    back to x's dtype, then multiply by the weight."""
+    input_dtype = x.dtype
+    hidden_states = x.to(torch.float32)
+    variance = hidden_states.pow(2).mean(-1, keepdim=True)
+    hidden_states = hidden_states * torch.rsqrt(variance + eps)
+    return weight * hidden_states.to(input_dtype)

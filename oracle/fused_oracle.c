@@ -1,0 +1,258 @@
+/*
+ * fused_oracle.c -- CPU oracle for the fused RMSNorm and SiLU-and-mul path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py load this library, and only as the checker (or
+ * the timed CPU baseline).  No product code path calls it.
+ *
+ * It restates, in plain C with explicit rounding, the reference's two
+ * formulations of each op:
+ *
+ *   mode ORACLE_TRITON  -- the fused Triton kernels: fp32 arithmetic, ONE
+ *       rounding to the output type.
+ *       RMSNorm  src/kernels/fused_rmsnorm_triton.py:41-49
+ *       SwiGLU   src/kernels/fused_swiglu_triton.py:30-36
+ *   mode ORACLE_HF      -- the naive/HF formulas the fused kernels replace:
+ *       RMSNorm rounds x*rstd to x's type before the weight multiply
+ *       (src/kernels/fused_rmsnorm_triton.py:74-82, identical to HF
+ *       Qwen2RMSNorm.forward); SwiGLU rounds silu(g) before "* up"
+ *       (src/kernels/fused_swiglu_triton.py:56-59).
+ *   *_f64               -- fp64 brute force of the same mathematics.
+ *
+ * Sum of squares: the reference reduces with tl.sum in fp32 in an order the
+ * Triton backend picks (:43).  The oracle accumulates the exact squares in
+ * fp64 and rounds the sum to fp32 once, i.e. the order-free fp32 sum; any
+ * fp32 reduction order differs from it by a few fp32 ulp, far below one
+ * fp16/bf16 ulp of the output.
+ *
+ * Storage conversions (fp16, bf16 <-> fp32, round-to-nearest-even) are
+ * written out here and checked against numpy / torch in tests/.
+ *
+ * `mutate` != 0 plants a deliberate mistake (see ORACLE_MUT_*); the tests use
+ * it to show that the checks pinning this oracle would catch such a mistake.
+ * 0 is the faithful restatement.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+enum { OR_F32 = 0, OR_F16 = 1, OR_BF16 = 2 };
+enum { ORACLE_TRITON = 0, ORACLE_HF = 1 };
+
+/* planted mistakes, RMSNorm */
+enum {
+  ORACLE_MUT_RMS_N_MINUS_1 = 1, /* divide the sum of squares by n-1 */
+  ORACLE_MUT_RMS_NO_EPS = 2,    /* drop eps */
+  ORACLE_MUT_RMS_SQRT = 3,      /* multiply by sqrt(var+eps) instead of its reciprocal */
+  ORACLE_MUT_RMS_NO_WEIGHT = 4, /* skip the weight */
+  ORACLE_MUT_RMS_W_REVERSED = 5 /* index the weight backwards */
+};
+/* planted mistakes, SiLU-and-mul */
+enum {
+  ORACLE_MUT_SILU_SIGN = 1,    /* sigmoid(-g) instead of sigmoid(g) */
+  ORACLE_MUT_SILU_SWAP = 2,    /* silu(up) * gate */
+  ORACLE_MUT_SILU_NO_UP = 3,   /* drop "* up" */
+  ORACLE_MUT_SILU_ROUND2 = 4   /* round silu(g) before "* up" in Triton mode */
+};
+
+/* ---------------------------------------------------------------- storage */
+
+static float bits_to_f32(uint32_t b) {
+  float f;
+  memcpy(&f, &b, 4);
+  return f;
+}
+static uint32_t f32_to_bits(float f) {
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  return b;
+}
+
+float oracle_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  const uint32_t m = h & 0x3ffu;
+  if (e == 0) {
+    /* zero or subnormal: m * 2^-24, exact in fp32 */
+    float v = (float)m * 5.9604644775390625e-08f;
+    return sign ? -v : v;
+  }
+  if (e == 31) return bits_to_f32(sign | 0x7f800000u | (m << 13));
+  return bits_to_f32(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+uint16_t oracle_f32_to_f16(float f) {
+  const uint32_t x = f32_to_bits(f);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu)); /* NaN, quieted */
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to inf */
+  if (ax < 0x38800000u) {
+    /* below 2^-14: fp16 subnormal (or zero).  |f| * 2^24 is exact; round it
+     * to the nearest integer, ties to even.  1024 correctly encodes 2^-14. */
+    const float t = bits_to_f32(ax) * 16777216.0f;
+    uint32_t m = (uint32_t)t;
+    const float frac = t - (float)m;
+    if (frac > 0.5f || (frac == 0.5f && (m & 1u))) m += 1u;
+    return (uint16_t)(sign | m);
+  }
+  const uint32_t mant = ax & 0x7fffffu;
+  uint32_t h = ((((ax >> 23) - 127u + 15u)) << 10) | (mant >> 13);
+  const uint32_t rem = mant & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u; /* carry into the exponent is correct */
+  return (uint16_t)(sign | h);
+}
+
+float oracle_bf16_to_f32(uint16_t b) { return bits_to_f32((uint32_t)b << 16); }
+
+uint16_t oracle_f32_to_bf16(float f) {
+  uint32_t x = f32_to_bits(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u); /* NaN, quieted */
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+
+static float load_f(const void* p, int64_t i, int dt) {
+  switch (dt) {
+    case OR_F16: return oracle_f16_to_f32(((const uint16_t*)p)[i]);
+    case OR_BF16: return oracle_bf16_to_f32(((const uint16_t*)p)[i]);
+    default: return ((const float*)p)[i];
+  }
+}
+
+static void store_f(void* p, int64_t i, int dt, float v) {
+  switch (dt) {
+    case OR_F16: ((uint16_t*)p)[i] = oracle_f32_to_f16(v); break;
+    case OR_BF16: ((uint16_t*)p)[i] = oracle_f32_to_bf16(v); break;
+    default: ((float*)p)[i] = v; break;
+  }
+}
+
+/* value of v after a round trip through storage type dt */
+static float round_to(float v, int dt) {
+  switch (dt) {
+    case OR_F16: return oracle_f16_to_f32(oracle_f32_to_f16(v));
+    case OR_BF16: return oracle_bf16_to_f32(oracle_f32_to_bf16(v));
+    default: return v;
+  }
+}
+
+static int valid_dt(int d) { return d == OR_F32 || d == OR_F16 || d == OR_BF16; }
+
+/* --------------------------------------------------------------- RMSNorm */
+
+/*
+ * y[r, :] for r < rows.  x row r starts at x + r*xs, y row r at y + r*ys.
+ *   TRITON (:41-49): var = sum/n; rstd = 1/sqrt(var+eps); y = (x*rstd)*w,
+ *                    one rounding to ydt.
+ *   HF     (:74-82): h = round_xdt(x*rstd); y = round_ydt(w*h); the caller
+ *                    passes ydt = torch's promotion of (w dtype, x dtype).
+ * Returns 0, or -1 on a bad argument.
+ */
+int oracle_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t n, int64_t xs,
+                   int64_t ys, float eps, int xdt, int wdt, int ydt, int mode, int mutate) {
+  if (!valid_dt(xdt) || !valid_dt(wdt) || !valid_dt(ydt) || n < 1 || rows < 0) return -1;
+  for (int64_t r = 0; r < rows; ++r) {
+    double ssd = 0.0;
+    for (int64_t j = 0; j < n; ++j) {
+      const double v = (double)load_f(x, r * xs + j, xdt);
+      ssd += v * v;
+    }
+    const float ss = (float)ssd;
+    const float denom = (mutate == ORACLE_MUT_RMS_N_MINUS_1) ? (float)(n - 1) : (float)n;
+    const float var = ss / denom;
+    const float add = (mutate == ORACLE_MUT_RMS_NO_EPS) ? 0.0f : eps;
+    const float rstd = (mutate == ORACLE_MUT_RMS_SQRT) ? sqrtf(var + add) : 1.0f / sqrtf(var + add);
+    for (int64_t j = 0; j < n; ++j) {
+      const float xf = load_f(x, r * xs + j, xdt);
+      const int64_t wj = (mutate == ORACLE_MUT_RMS_W_REVERSED) ? (n - 1 - j) : j;
+      const float wf = (mutate == ORACLE_MUT_RMS_NO_WEIGHT) ? 1.0f : load_f(w, wj, wdt);
+      float o;
+      if (mode == ORACLE_HF) {
+        const float h = round_to(xf * rstd, xdt);
+        o = wf * h;
+      } else {
+        o = (xf * rstd) * wf;
+      }
+      store_f(y, r * ys + j, ydt, o);
+    }
+  }
+  return 0;
+}
+
+/* fp64 brute force: y[r*n + j] = x * w / sqrt(mean(x^2) + eps), all in double. */
+int oracle_rmsnorm_f64(const void* x, const void* w, double* y, int64_t rows, int64_t n, int64_t xs,
+                       double eps, int xdt, int wdt) {
+  if (!valid_dt(xdt) || !valid_dt(wdt) || n < 1 || rows < 0) return -1;
+  for (int64_t r = 0; r < rows; ++r) {
+    double ssd = 0.0;
+    for (int64_t j = 0; j < n; ++j) {
+      const double v = (double)load_f(x, r * xs + j, xdt);
+      ssd += v * v;
+    }
+    const double rstd = 1.0 / sqrt(ssd / (double)n + eps);
+    for (int64_t j = 0; j < n; ++j)
+      y[r * n + j] = (double)load_f(x, r * xs + j, xdt) * rstd * (double)load_f(w, j, wdt);
+  }
+  return 0;
+}
+
+/* ---------------------------------------------------------- SiLU-and-mul */
+
+/*
+ *   TRITON (:30-36): out = (g * (1/(1+exp(-g)))) * u in fp32, one rounding.
+ *   HF     (:56-59): s = round_odt(g / (1 + exp(-g)))  [torch's CPU silu],
+ *                    out = round_odt(s * u).
+ */
+int oracle_silu_mul(const void* gate, const void* up, void* out, int64_t numel, int idt, int odt,
+                    int mode, int mutate) {
+  if (!valid_dt(idt) || !valid_dt(odt) || numel < 0) return -1;
+  for (int64_t i = 0; i < numel; ++i) {
+    float g = load_f(gate, i, idt);
+    float u = load_f(up, i, idt);
+    if (mutate == ORACLE_MUT_SILU_SWAP) {
+      const float t = g;
+      g = u;
+      u = t;
+    }
+    const float arg = (mutate == ORACLE_MUT_SILU_SIGN) ? g : -g;
+    float o;
+    if (mode == ORACLE_HF) {
+      const float s = round_to(g / (1.0f + expf(arg)), odt);
+      o = (mutate == ORACLE_MUT_SILU_NO_UP) ? s : s * u;
+    } else {
+      const float sig = 1.0f / (1.0f + expf(arg));
+      float s = g * sig;
+      if (mutate == ORACLE_MUT_SILU_ROUND2) s = round_to(s, odt);
+      o = (mutate == ORACLE_MUT_SILU_NO_UP) ? s : s * u;
+    }
+    store_f(out, i, odt, o);
+  }
+  return 0;
+}
+
+/* fp64 brute force: out[i] = g / (1 + exp(-g)) * u in double. */
+int oracle_silu_mul_f64(const void* gate, const void* up, double* out, int64_t numel, int idt) {
+  if (!valid_dt(idt) || numel < 0) return -1;
+  for (int64_t i = 0; i < numel; ++i) {
+    const double g = (double)load_f(gate, i, idt);
+    const double u = (double)load_f(up, i, idt);
+    out[i] = g / (1.0 + exp(-g)) * u;
+  }
+  return 0;
+}
+
+/* ------------------------------------------------- bulk conversion helpers */
+
+void oracle_f32_to_f16_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_f16(in[i]);
+}
+void oracle_f16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f16_to_f32(in[i]);
+}
+void oracle_f32_to_bf16_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_bf16(in[i]);
+}
+void oracle_bf16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_bf16_to_f32(in[i]);
+}

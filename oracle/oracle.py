@@ -1,0 +1,251 @@
+"""CPU oracle for the fused RMSNorm / SiLU-and-mul path -- TEST INFRASTRUCTURE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg import this module, and only as the checker (or the timed CPU baseline).
+The product package never imports it.
+
+Contents
+--------
+* numpy front end for ``fused_oracle.c`` (built by :func:`build` into
+  ``oracle/liboracle_fused.so`` with gcc):
+    - :func:`rmsnorm` / :func:`silu_mul` in ``mode="triton"`` restate the
+      reference's fused Triton kernels (one rounding,
+      src/kernels/fused_rmsnorm_triton.py:41-49,
+      src/kernels/fused_swiglu_triton.py:30-36);
+    - ``mode="hf"`` restates the naive/HF formulas
+      (src/kernels/fused_rmsnorm_triton.py:74-82,
+      src/kernels/fused_swiglu_triton.py:56-59);
+    - :func:`rmsnorm_f64` / :func:`silu_mul_f64` are fp64 brute force.
+* :func:`naive_rmsnorm_torch` / :func:`naive_silu_mul_torch`: the reference's
+  naive PyTorch path restated as the same torch op sequence, which bench.py
+  times on the host cores as the CPU baseline.
+* ULP helpers for comparing fp16 / bf16 outputs.
+
+16-bit arrays are passed as ``np.uint16`` bit patterns together with a dtype
+name ("f16", "bf16"); fp32 arrays as ``np.float32`` with "f32".
+
+Parity status: every function is pinned by tests/test_oracle.py (numpy /
+torch conversions, transformers' Qwen2RMSNorm, torch.nn.functional.silu,
+closed forms, fp64 brute force, planted mistakes).  Bitwise equality with the
+reference's Triton kernels themselves is unpinned (they need an NVIDIA GPU and
+Triton's backend math); the oracle stands in for them at <= 1 output ulp.
+"""
+from __future__ import annotations
+
+import ctypes
+import shutil
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+SRC = ORACLE_DIR / "fused_oracle.c"
+LIB = ORACLE_DIR / "liboracle_fused.so"
+
+DT_CODE = {"f32": 0, "f16": 1, "bf16": 2}
+MODE_CODE = {"triton": 0, "hf": 1}
+
+# planted-mistake codes (see fused_oracle.c)
+MUT_RMS = {"n_minus_1": 1, "no_eps": 2, "sqrt": 3, "no_weight": 4, "w_reversed": 5}
+MUT_SILU = {"sign": 1, "swap": 2, "no_up": 3, "round2": 4}
+
+_lib = None
+
+
+def build(force: bool = True) -> Path:
+    """Compile fused_oracle.c with gcc (no FMA contraction, no fast-math)."""
+    if LIB.exists() and not force:
+        return LIB
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("gcc not found; cannot build the oracle")
+    tmp = LIB.with_name(LIB.name + ".tmp")
+    cmd = [cc, "-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+           "-Wall", "-Werror", str(SRC), "-o", str(tmp), "-lm"]
+    subprocess.run(cmd, check=True)
+    tmp.replace(LIB)
+    return LIB
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.oracle_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, i32, i32, i32, i32, i32]
+        L.oracle_rmsnorm.restype = i32
+        L.oracle_rmsnorm_f64.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.c_double, i32, i32]
+        L.oracle_rmsnorm_f64.restype = i32
+        L.oracle_silu_mul.argtypes = [vp, vp, vp, i64, i32, i32, i32, i32]
+        L.oracle_silu_mul.restype = i32
+        L.oracle_silu_mul_f64.argtypes = [vp, vp, vp, i64, i32]
+        L.oracle_silu_mul_f64.restype = i32
+        for name in ("oracle_f32_to_f16_n", "oracle_f16_to_f32_n", "oracle_f32_to_bf16_n", "oracle_bf16_to_f32_n"):
+            getattr(L, name).argtypes = [vp, vp, i64]
+            getattr(L, name).restype = None
+        _lib = L
+    return _lib
+
+
+def _np_dtype(dt: str):
+    return np.float32 if dt == "f32" else np.uint16
+
+
+def _arr(a: np.ndarray, dt: str) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    want = _np_dtype(dt)
+    if a.dtype != want:
+        raise TypeError(f"expected {want} storage for {dt}, got {a.dtype}")
+    return a
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ----------------------------------------------------------------- RMSNorm
+
+def hf_out_dtype(xdt: str, wdt: str) -> str:
+    """torch's promotion of ``weight * h.to(x.dtype)`` (src/kernels/fused_rmsnorm_triton.py:82)."""
+    if xdt == wdt:
+        return xdt
+    return "f32"
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6, *, xdt: str, wdt: str,
+            ydt: str | None = None, mode: str = "triton", mutate: str | None = None) -> np.ndarray:
+    """x: [rows, n] storage array; w: [n].  Returns y [rows, n] in ydt storage."""
+    x = _arr(x, xdt)
+    w = _arr(w, wdt)
+    if x.ndim != 2 or w.shape != (x.shape[1],):
+        raise ValueError(f"bad shapes x={x.shape} w={w.shape}")
+    if ydt is None:
+        ydt = xdt if mode == "triton" else hf_out_dtype(xdt, wdt)
+    rows, n = x.shape
+    y = np.empty((rows, n), dtype=_np_dtype(ydt))
+    mut = 0 if mutate is None else MUT_RMS[mutate]
+    st = lib().oracle_rmsnorm(_ptr(x), _ptr(w), _ptr(y), rows, n, n, n, float(np.float32(eps)),
+                              DT_CODE[xdt], DT_CODE[wdt], DT_CODE[ydt], MODE_CODE[mode], mut)
+    if st != 0:
+        raise ValueError("oracle_rmsnorm rejected its arguments")
+    return y
+
+
+def rmsnorm_f64(x: np.ndarray, w: np.ndarray, eps: float = 1e-6, *, xdt: str, wdt: str) -> np.ndarray:
+    x = _arr(x, xdt)
+    w = _arr(w, wdt)
+    rows, n = x.shape
+    y = np.empty((rows, n), dtype=np.float64)
+    st = lib().oracle_rmsnorm_f64(_ptr(x), _ptr(w), _ptr(y), rows, n, n, float(eps), DT_CODE[xdt], DT_CODE[wdt])
+    if st != 0:
+        raise ValueError("oracle_rmsnorm_f64 rejected its arguments")
+    return y
+
+
+# ------------------------------------------------------------- SiLU-and-mul
+
+def silu_mul(gate: np.ndarray, up: np.ndarray, *, idt: str, odt: str | None = None,
+             mode: str = "triton", mutate: str | None = None) -> np.ndarray:
+    gate = _arr(gate, idt)
+    up = _arr(up, idt)
+    if gate.shape != up.shape:
+        raise ValueError("gate and up must have the same shape")
+    odt = odt or idt
+    out = np.empty(gate.shape, dtype=_np_dtype(odt))
+    mut = 0 if mutate is None else MUT_SILU[mutate]
+    st = lib().oracle_silu_mul(_ptr(gate), _ptr(up), _ptr(out), gate.size, DT_CODE[idt], DT_CODE[odt],
+                               MODE_CODE[mode], mut)
+    if st != 0:
+        raise ValueError("oracle_silu_mul rejected its arguments")
+    return out
+
+
+def silu_mul_f64(gate: np.ndarray, up: np.ndarray, *, idt: str) -> np.ndarray:
+    gate = _arr(gate, idt)
+    up = _arr(up, idt)
+    out = np.empty(gate.shape, dtype=np.float64)
+    st = lib().oracle_silu_mul_f64(_ptr(gate), _ptr(up), _ptr(out), gate.size, DT_CODE[idt])
+    if st != 0:
+        raise ValueError("oracle_silu_mul_f64 rejected its arguments")
+    return out
+
+
+# -------------------------------------------------------------- conversions
+
+def f32_to_f16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    o = np.empty(a.shape, np.uint16)
+    lib().oracle_f32_to_f16_n(_ptr(a), _ptr(o), a.size)
+    return o
+
+
+def f16_to_f32(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    o = np.empty(a.shape, np.float32)
+    lib().oracle_f16_to_f32_n(_ptr(a), _ptr(o), a.size)
+    return o
+
+
+def f32_to_bf16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    o = np.empty(a.shape, np.uint16)
+    lib().oracle_f32_to_bf16_n(_ptr(a), _ptr(o), a.size)
+    return o
+
+
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    o = np.empty(a.shape, np.float32)
+    lib().oracle_bf16_to_f32_n(_ptr(a), _ptr(o), a.size)
+    return o
+
+
+def to_f32(a: np.ndarray, dt: str) -> np.ndarray:
+    if dt == "f32":
+        return np.asarray(a, np.float32)
+    return f16_to_f32(a) if dt == "f16" else bf16_to_f32(a)
+
+
+def from_f32(a: np.ndarray, dt: str) -> np.ndarray:
+    if dt == "f32":
+        return np.ascontiguousarray(a, np.float32)
+    return f32_to_f16(a) if dt == "f16" else f32_to_bf16(a)
+
+
+# ------------------------------------------------------------- ULP helpers
+
+def ordered16(bits: np.ndarray) -> np.ndarray:
+    """Map sign-magnitude 16-bit float patterns onto a monotone integer line
+    (+0 and -0 both map to 0), so |a - b| counts representable steps."""
+    b = bits.astype(np.int32)
+    mag = b & 0x7FFF
+    return np.where(b & 0x8000, -mag, mag)
+
+
+def ulp_diff16(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    return np.abs(ordered16(a_bits) - ordered16(b_bits))
+
+
+# ---------------------------------------------- naive torch path (CPU baseline)
+
+def naive_rmsnorm_torch(x, weight, eps: float = 1e-6):
+    """The reference's unfused RMSNorm op sequence
+    (src/kernels/fused_rmsnorm_triton.py:74-82): fp32 upcast, pow, mean,
+    rsqrt, multiply, downcast, weight multiply."""
+    import torch
+
+    input_dtype = x.dtype
+    h = x.to(torch.float32)
+    variance = h.pow(2).mean(-1, keepdim=True)
+    h = h * torch.rsqrt(variance + eps)
+    return weight * h.to(input_dtype)
+
+
+def naive_silu_mul_torch(gate, up):
+    """The reference's unfused SiLU-and-mul (src/kernels/fused_swiglu_triton.py:56-59)."""
+    import torch
+
+    return torch.nn.functional.silu(gate) * up

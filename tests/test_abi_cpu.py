@@ -1,0 +1,137 @@
+"""Host-side checks of the C ABI and the Python boundary that need no GPU:
+the library loads, exports every symbol include/*.h declares, reports its
+ABI version, and rejects bad arguments (or no-ops on empty work) before any
+HIP call.  Also: the product package never imports the oracle, and the
+Python launchers raise the reference's AssertionError for host tensors."""
+import ctypes
+import importlib
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG_DIR = ROOT / "llm-inference-optimizer_amd"
+
+
+def _declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(mi355_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+@pytest.fixture(scope="module")
+def L():
+    return importlib.import_module("llm-inference-optimizer_amd._lib")
+
+
+@pytest.fixture(scope="module")
+def lib(L):
+    return L.load()
+
+
+def test_header_declares_expected_entry_points(L):
+    declared = _declared_symbols()
+    assert declared == set(L.EXPORTED_SYMBOLS), declared
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(PKG_DIR / "libmi355_fused.so"))
+    for name in _declared_symbols():
+        assert hasattr(raw, name), f"{name} declared in include/ but not exported"
+
+
+def test_abi_version(L, lib):
+    assert lib.mi355_abi_version() == L.ABI_VERSION == 1
+    hdr = (ROOT / "include" / "mi355_fused.h").read_text()
+    assert re.search(r"#define MI355_ABI_VERSION 1\b", hdr)
+
+
+def test_dtype_codes_match_header(L):
+    hdr = (ROOT / "include" / "mi355_fused.h").read_text()
+    assert re.search(r"MI355_F32 = 0", hdr) and re.search(r"MI355_F16 = 1", hdr) and re.search(r"MI355_BF16 = 2", hdr)
+    assert (L.F32, L.F16, L.BF16) == (0, 1, 2)
+
+
+# Argument validation happens before any HIP call, so these run without a GPU.
+P = 0x10000  # a fake, never-dereferenced device address
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    ((P, P, P, 4, 64, 64, 64, 1e-6, 7, 1, 1), -1, "unknown dtype"),
+    ((P, P, P, 4, 64, 64, 64, 1e-6, 1, 1, 2), -2, "y dtype"),
+    ((P, P, P, -1, 64, 64, 64, 1e-6, 1, 1, 1), -1, "rows"),
+    ((P, P, P, 4, 0, 64, 64, 1e-6, 1, 1, 1), -1, "n must be"),
+    ((P, P, P, 4, 2**31, 2**31, 2**31, 1e-6, 1, 1, 1), -1, "n must be"),
+    ((0, P, P, 4, 64, 64, 64, 1e-6, 1, 1, 1), -1, "null pointer"),
+    ((P, P, P, 4, 64, 32, 64, 1e-6, 1, 1, 1), -1, "row strides"),
+    ((P, P, P, 2**40, 64, 2**40, 64, 1e-6, 1, 1, 1), -1, "overflows"),
+])
+def test_rmsnorm_abi_rejects(lib, args, code, msg):
+    st = lib.mi355_rmsnorm_fwd(*args, None)
+    assert st == code
+    assert msg in lib.mi355_last_error().decode()
+
+
+def test_rmsnorm_abi_zero_rows_is_noop(lib):
+    assert lib.mi355_rmsnorm_fwd(0, 0, 0, 0, 64, 64, 64, 1e-6, 1, 1, 1, None) == 0
+    assert lib.mi355_last_error().decode() == ""
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    ((P, P, P, 16, 9, 1), -1, "unknown dtype"),
+    ((P, P, P, 16, 1, 2), -2, "out dtype"),
+    ((P, P, P, -5, 1, 1), -1, "numel"),
+    ((P, 0, P, 16, 1, 1), -1, "null pointer"),
+])
+def test_silu_mul_abi_rejects(lib, args, code, msg):
+    st = lib.mi355_silu_mul_fwd(*args, None)
+    assert st == code
+    assert msg in lib.mi355_last_error().decode()
+
+
+def test_silu_mul_abi_zero_numel_is_noop(lib):
+    assert lib.mi355_silu_mul_fwd(0, 0, 0, 0, 1, 1, None) == 0
+
+
+def test_python_check_raises_with_message(L, lib):
+    st = lib.mi355_silu_mul_fwd(P, P, P, -5, 1, 1, None)
+    with pytest.raises(L.KernelError, match="numel must be >= 0"):
+        L.check("mi355_silu_mul_fwd", st)
+
+
+def test_missing_library_fails_loudly(L, monkeypatch, tmp_path):
+    monkeypatch.setattr(L, "LIB_PATH", tmp_path / "nope.so")
+    monkeypatch.setattr(L, "_lib", None)
+    with pytest.raises(L.KernelLibraryMissing):
+        L.load()
+
+
+def test_launchers_assert_on_host_tensors(pkg):
+    """Same precondition as the reference (assert x.is_cuda ...): host tensors
+    are rejected with AssertionError, never computed on the CPU."""
+    x = torch.randn(4, 64, dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        pkg.fused_rmsnorm(x, torch.ones(64, dtype=torch.float16))
+    with pytest.raises(AssertionError):
+        pkg.fused_silu_mul(x, x)
+    with pytest.raises(AssertionError):
+        pkg.fused_silu_mul(x, torch.randn(4, 65, dtype=torch.float16))
+
+
+def test_product_package_never_touches_the_oracle():
+    for f in PKG_DIR.rglob("*"):
+        if f.suffix in (".py", ".hip", ".h", ".cpp"):
+            text = f.read_text()
+            assert not re.search(r"\boracle\b", text), f"{f} mentions the oracle"
+
+
+def test_bench_refuses_multi_gpu():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr

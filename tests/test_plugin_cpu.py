@@ -1,0 +1,90 @@
+"""Module-replacement plugin behaviour (host-only; no kernel runs): the same
+matching, counting, toggles and parameter sharing as the reference's
+src/engine/fused_norm_activation_patch.py:29-99, on random-init
+transformers models built locally."""
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+
+
+def _qwen2(layers=28, hidden=64, inter=128):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    cfg = Qwen2Config(vocab_size=128, hidden_size=hidden, intermediate_size=inter, num_hidden_layers=layers,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64)
+    return Qwen2ForCausalLM(cfg)
+
+
+def test_patch_counts_on_28_layer_qwen2(pkg):
+    model = _qwen2()
+    counts = pkg.patch_model_with_fused_kernels(model)
+    # 2 norms per layer + final norm; 1 MLP per layer (benchmarks/results/stage3_e2e.json:2-3)
+    assert counts == {"rmsnorm": 57, "mlp": 28}
+    layer = model.model.layers[0]
+    assert isinstance(layer.input_layernorm, pkg.FusedRMSNorm)
+    assert isinstance(layer.post_attention_layernorm, pkg.FusedRMSNorm)
+    assert isinstance(layer.mlp, pkg.FusedMLP)
+    assert isinstance(model.model.norm, pkg.FusedRMSNorm)
+    # patching twice finds nothing new: the replacements are not matched again
+    assert pkg.patch_model_with_fused_kernels(model) == {"rmsnorm": 0, "mlp": 0}
+
+
+def test_replacements_share_parameters(pkg):
+    model = _qwen2(layers=2)
+    norm = model.model.layers[1].post_attention_layernorm
+    mlp = model.model.layers[1].mlp
+    w, eps = norm.weight, norm.variance_epsilon
+    gp, up, dp = mlp.gate_proj, mlp.up_proj, mlp.down_proj
+    n_params = sum(p.numel() for p in model.parameters())
+    pkg.patch_model_with_fused_kernels(model)
+    fn = model.model.layers[1].post_attention_layernorm
+    fm = model.model.layers[1].mlp
+    assert fn.weight is w and fn.variance_epsilon == eps
+    assert fm.gate_proj is gp and fm.up_proj is up and fm.down_proj is dp
+    assert not hasattr(fm, "act_fn")
+    assert sum(p.numel() for p in model.parameters()) == n_params
+    assert dict(model.named_parameters()).keys() == dict(_qwen2(layers=2).named_parameters()).keys()
+
+
+@pytest.mark.parametrize("norm,mlp,want", [(True, False, {"rmsnorm": 9, "mlp": 0}),
+                                           (False, True, {"rmsnorm": 0, "mlp": 4}),
+                                           (False, False, {"rmsnorm": 0, "mlp": 0})])
+def test_patch_toggles(pkg, norm, mlp, want):
+    model = _qwen2(layers=4)
+    assert pkg.patch_model_with_fused_kernels(model, patch_norm=norm, patch_mlp=mlp) == want
+
+
+def test_llama_names_match(pkg):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=64, hidden_size=32, intermediate_size=64, num_hidden_layers=3,
+                      num_attention_heads=4, num_key_value_heads=2)
+    counts = pkg.patch_model_with_fused_kernels(LlamaForCausalLM(cfg))
+    assert counts == {"rmsnorm": 7, "mlp": 3}
+
+
+def test_unrecognised_architecture_patches_nothing(pkg):
+    model = torch.nn.Sequential(torch.nn.Linear(8, 8), torch.nn.LayerNorm(8), torch.nn.GELU())
+    assert pkg.patch_model_with_fused_kernels(model) == {"rmsnorm": 0, "mlp": 0}
+
+
+def test_class_name_sets_match_reference(pkg):
+    assert pkg.RMSNORM_CLASS_NAMES == {"Qwen2RMSNorm", "LlamaRMSNorm", "MistralRMSNorm", "RMSNorm"}
+    assert pkg.MLP_CLASS_NAMES == {"Qwen2MLP", "LlamaMLP", "MistralMLP"}
+
+
+def test_matching_requires_attributes(pkg):
+    class RMSNorm(torch.nn.Module):  # right name, missing variance_epsilon
+        def __init__(self):
+            super().__init__()
+            self.weight = torch.nn.Parameter(torch.ones(4))
+
+    class Qwen2MLP(torch.nn.Module):  # right name, missing down_proj
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = torch.nn.Linear(4, 8)
+            self.up_proj = torch.nn.Linear(4, 8)
+
+    root = torch.nn.Module()
+    root.norm = RMSNorm()
+    root.mlp = Qwen2MLP()
+    assert pkg.patch_model_with_fused_kernels(root) == {"rmsnorm": 0, "mlp": 0}
