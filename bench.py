@@ -310,13 +310,13 @@ def main():
     silu_warm_us = time_loop(ctx, [sets[0][1]], iters)
     rms_warm_graph_us = time_graph(ctx, [sets[0][0]], 200)
     kernels = {
-        "c2_silu_mul_f16_2048x8960": kernel_entry("silu_mul_vec<F16,F16,4>", silu_bytes, silu_us,
+        "c2_silu_mul_f16_2048x8960": kernel_entry("silu_mul_chunks<F16,F16>", silu_bytes, silu_us,
                                                   {"timing": "events over back-to-back launches, cold"}),
         "c1_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes, rms_us,
                                                  {"timing": "events over back-to-back launches, cold"}),
         "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes,
                                                        rms_graph_us, {"timing": "hipGraph of 200 launches, cold"}),
-        "c2_silu_mul_f16_2048x8960_warm": kernel_entry("silu_mul_vec<F16,F16,4>", silu_bytes, silu_warm_us,
+        "c2_silu_mul_f16_2048x8960_warm": kernel_entry("silu_mul_chunks<F16,F16>", silu_bytes, silu_warm_us,
                                                        {"timing": "same buffers every launch (MALL-warm)"}),
         "c1_rmsnorm_f16_2048x1536_warm_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes,
                                                             rms_warm_graph_us,
@@ -334,7 +334,7 @@ def main():
                    "storage_dtype": "f16", "math_dtype": "f32", "eps": 1e-6, "buffer_sets": nset,
                    "footprint_GiB": round(nset * step_bytes / 2**30, 3), "step_bytes": step_bytes},
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "kernel": "silu_mul_vec (C2 SiLU-and-mul [2048,8960] fp16)",
+        "roofline": {"bound": "hbm", "kernel": "silu_mul_chunks (C2 SiLU-and-mul [2048,8960] fp16)",
                      "achieved": round(silu_bytes / silu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(silu_bytes / silu_us / 1e3 / PEAK_GBS, 4),
                      "traffic": read_traffic("c2_silu_mul"), "algorithmic_bytes": silu_bytes,
@@ -403,7 +403,7 @@ def bench_c4(ctx, iters=60, which=None):
         up = rand(ctx, (M, I), 501, BF16)
         o = torch.empty_like(gate)
         us = time_loop(ctx, [ctx.silu_call(gate, up, o)], iters)
-        out["c4_silu_mul_bf16_16384x18944"] = kernel_entry("silu_mul_vec<BF16,BF16,4>", nbytes, us,
+        out["c4_silu_mul_bf16_16384x18944"] = kernel_entry("silu_mul_chunks<BF16,BF16>", nbytes, us,
                                                            {"buffer_sets": 1, "footprint_GiB": round(nbytes / 2**30, 2)})
         del gate, up, o
         torch.cuda.empty_cache()

@@ -28,6 +28,13 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float as_f32(uint32_t v) { return __builtin_bit_cast(float, v); }
 __device__ __forceinline__ uint32_t as_u32(float v) { return __builtin_bit_cast(uint32_t, v); }
 
+// Register barrier: an empty asm that claims to modify v, so the compiler
+// cannot keep values derived from v (e.g. its fp32 widening) live across it and
+// recomputes them from the packed form instead.  Used to keep a row in packed
+// 16-bit form between the two passes of RMSNorm, halving its VGPR footprint.
+__device__ __forceinline__ void reg_barrier(u32x4& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void reg_barrier(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
 // Storage tags.  `bits` is the raw storage type; arithmetic is always fp32.
 struct F32 { typedef uint32_t bits; static constexpr int code = MI355_F32; };
 struct F16 { typedef uint16_t bits; static constexpr int code = MI355_F16; };
@@ -195,6 +202,99 @@ __device__ __forceinline__ void store_chunk(void* p, const float (&f)[W]) {
       u32x4 o = {as_u32(f[4 * i]), as_u32(f[4 * i + 1]), as_u32(f[4 * i + 2]), as_u32(f[4 * i + 3])};
       static_cast<u32x4*>(p)[i] = o;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Raw buffer access.  A buffer resource (V#) covers [base, base + bytes); a
+// load outside it returns zeros and a store outside it is dropped by the
+// hardware, so a kernel that builds one descriptor per row or per chunk needs
+// no per-lane bounds branches.  Descriptor word 3 0x00020000 selects 32-bit
+// data format for gfx9-family untyped access (gfx950 included).  `bytes` is a
+// 32-bit count: callers keep each descriptor's extent below 4 GiB.
+//
+// Cache policy (aux) bits on gfx950: 1 = sc0, 2 = nt, 16 = sc1.  nt (streaming)
+// on loads and stores measured fastest for these single-pass kernels.
+// ---------------------------------------------------------------------------
+#ifndef MI355_LOAD_AUX
+#define MI355_LOAD_AUX 2
+#endif
+#ifndef MI355_STORE_AUX
+#define MI355_STORE_AUX 2
+#endif
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, MI355_LOAD_AUX);
+}
+__device__ __forceinline__ u32x4 buf_load16_cached(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x2 buf_load8_cached(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store16(rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, MI355_STORE_AUX);
+}
+__device__ __forceinline__ void buf_store8(rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, MI355_STORE_AUX);
+}
+
+// W elements of T at byte offset `off` of buffer r, loaded as raw dwords
+// (W * sizeof(T) is 8, 16 or 32 bytes) with the default cache policy: this
+// holds data every wave re-reads (the RMSNorm weight), which should stay in L2.
+template <typename T, int W> struct BufChunk {
+  static constexpr int DW = W * sizeof(typename T::bits) / 4;
+  uint32_t raw[DW];
+  __device__ __forceinline__ void load(rsrc_t r, uint32_t off) {
+    if constexpr (DW == 2) {
+      const u32x2 v = buf_load8_cached(r, off);
+      raw[0] = v.x; raw[1] = v.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < DW / 4; ++i) {
+        const u32x4 v = buf_load16_cached(r, off + 16u * i);
+        raw[4 * i] = v.x; raw[4 * i + 1] = v.y; raw[4 * i + 2] = v.z; raw[4 * i + 3] = v.w;
+      }
+    }
+  }
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (is_half_width<T>::value) {
+      const f32x2 p = widen2<T>(raw[i >> 1]);
+      return (i & 1) ? p.y : p.x;
+    } else {
+      return as_f32(raw[i]);
+    }
+  }
+};
+
+// Stores W fp32 values as W elements of TY at byte offset `off` of buffer r,
+// rounding each once.
+template <typename TY, int W>
+__device__ __forceinline__ void buf_store_chunk(rsrc_t r, uint32_t off, const float (&f)[W]) {
+  if constexpr (is_half_width<TY>::value) {
+    uint32_t d[W / 2];
+#pragma unroll
+    for (int i = 0; i < W / 2; ++i) {
+      f32x2 v;
+      v.x = f[2 * i];
+      v.y = f[2 * i + 1];
+      d[i] = narrow2<TY>(v);
+    }
+    if constexpr (W == 8) {
+      buf_store16(r, off, u32x4{d[0], d[1], d[2], d[3]});
+    } else {
+      buf_store8(r, off, u32x2{d[0], d[1]});
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i)
+      buf_store16(r, off + 16u * i,
+                  u32x4{as_u32(f[4 * i]), as_u32(f[4 * i + 1]), as_u32(f[4 * i + 2]), as_u32(f[4 * i + 3])});
   }
 }
 

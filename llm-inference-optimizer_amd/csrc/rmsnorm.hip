@@ -3,10 +3,10 @@
 // the grid.
 #include "rmsnorm_kernels.h"
 
-// Waves the launcher keeps resident per CU for the row-striding kernels
-// (gfx950: 4 SIMDs x 8 wave slots = 32).
+// Optional cap on the grid, in waves per CU, for the row-striding kernels;
+// 0 = one wave (or workgroup) per row, which measured fastest on MI355X.
 #ifndef MI355_RMS_WAVES_PER_CU
-#define MI355_RMS_WAVES_PER_CU 32
+#define MI355_RMS_WAVES_PER_CU 0
 #endif
 // Row counts below this use 64-thread workgroups (one wave each), so small
 // decode batches spread over as many CUs as rows.
@@ -43,7 +43,7 @@ template <typename TX, typename TW, typename TY>
 int rms_generic(const RmsArgs& a, hipStream_t s, int cus) {
   int64_t grid = a.rows;
   const int64_t cap = static_cast<int64_t>(cus) * 8;
-  if (grid > cap) grid = cap;
+  if (grid > cap) grid = cap;  // two-pass kernel: cap so the second pass finds the row in L2
   return launch_rms(rmsnorm_generic<TX, TW, TY>, grid, 256, a, s);
 }
 
@@ -52,7 +52,8 @@ int rms_wave(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
   const int block = a.rows < MI355_RMS_SMALL_ROWS ? 64 : 256;
   const int wpb = block / 64;
   int64_t grid = (a.rows + wpb - 1) / wpb;
-  const int64_t cap = static_cast<int64_t>(cus) * MI355_RMS_WAVES_PER_CU / wpb;
+  const int64_t cap = MI355_RMS_WAVES_PER_CU > 0 ? static_cast<int64_t>(cus) * MI355_RMS_WAVES_PER_CU / wpb
+                                                 : int64_t{0x7fffffff};
   if (grid > cap) grid = cap;
 #define MI355_WAVE_CASE(V) \
   return launch_rms(rmsnorm_wave_rows<TX, TW, TY, V>, grid, block, a, s)
@@ -77,10 +78,17 @@ int rms_wave(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
 template <typename TX, typename TW, typename TY, int BLOCK>
 int rms_block(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
   int64_t grid = a.rows;
-  const int64_t cap = static_cast<int64_t>(cus) * (MI355_RMS_WAVES_PER_CU / (BLOCK / 64));
+  const int64_t cap = MI355_RMS_WAVES_PER_CU > 0
+                          ? static_cast<int64_t>(cus) * (MI355_RMS_WAVES_PER_CU / (BLOCK / 64) + 1)
+                          : int64_t{0x7fffffff};
   if (grid > cap) grid = cap;
-  if (vpl <= 8) return launch_rms(rmsnorm_block_rows<TX, TW, TY, 8, BLOCK>, grid, BLOCK, a, s);
-  return launch_rms(rmsnorm_block_rows<TX, TW, TY, 16, BLOCK>, grid, BLOCK, a, s);
+  // 1024-thread workgroups get 128 VGPRs per lane: VPL 8 is the most that fits.
+  if constexpr (BLOCK == 1024) {
+    return launch_rms(rmsnorm_block_rows<TX, TW, TY, 8, BLOCK>, grid, BLOCK, a, s);
+  } else {
+    if (vpl <= 8) return launch_rms(rmsnorm_block_rows<TX, TW, TY, 8, BLOCK>, grid, BLOCK, a, s);
+    return launch_rms(rmsnorm_block_rows<TX, TW, TY, 16, BLOCK>, grid, BLOCK, a, s);
+  }
 }
 
 // Packet path: n a multiple of the packet width, every pointer and row
@@ -98,7 +106,7 @@ int rms_packets(const RmsArgs& a, hipStream_t s, int cus) {
   const int vpl256 = (nvec + 255) / 256;
   if (vpl256 <= 16) return rms_block<TX, TW, TY, 256>(a, s, cus, vpl256);
   const int vpl1024 = (nvec + 1023) / 1024;
-  if (vpl1024 <= 16) return rms_block<TX, TW, TY, 1024>(a, s, cus, vpl1024);
+  if (vpl1024 <= 8) return rms_block<TX, TW, TY, 1024>(a, s, cus, vpl1024);
   return rms_generic<TX, TW, TY>(a, s, cus);
 }
 

@@ -7,17 +7,21 @@
 //
 // Three kernels, chosen by the host launcher:
 //   rmsnorm_wave_rows   one wave64 per row, n <= 64 * VPL * W.  The row lives in
-//                       VGPRs (read from HBM exactly once), the sum of squares
-//                       is reduced with DPP + permlane swaps (no LDS), and the
-//                       wave's slice of the weight is loaded once into VGPRs
-//                       and reused for every row the wave visits.
+//                       VGPRs (read from HBM exactly once) and the sum of
+//                       squares is reduced with DPP + permlane swaps (no LDS).
+//                       Each lane's slice of the weight is loaded into VGPRs
+//                       together with the row (an L2 hit after the first
+//                       wave) and reused for every row the wave visits.
 //   rmsnorm_block_rows  one workgroup per row for wider rows; same scheme, the
 //                       per-wave partial sums meet in LDS (double-buffered so
 //                       a row costs one barrier).
 //   rmsnorm_generic     any n, alignment or dtype mix: scalar loads, two passes
 //                       over the row (the second pass re-reads x through L2).
-// All three stride over rows (grid-stride), so the launcher can cap the grid at
-// what the device holds resident.
+// Rows and the weight are read through buffer descriptors that span exactly
+// one row, so the packets past n need no lane branches, with the non-temporal
+// hint on x and y.  All three kernels stride over rows; the launcher normally
+// gives one wave (or workgroup) per row, which measured faster on MI355X than
+// a persistent grid.
 #pragma once
 
 #include "common.h"
@@ -31,122 +35,108 @@ __device__ __forceinline__ float rms_rstd(float sumsq, int n, float eps) {
   return 1.0f / __builtin_sqrtf(var + eps);
 }
 
+// Per-lane work shared by the wave and workgroup kernels: load VPL packets of
+// row r (packet index p = slot + k * STRIDE) through buffer descriptors sized
+// to the row, so packets past n read 0 and their stores drop.
+template <typename TX, typename TW, int VPL, int STRIDE>
+struct RowSlice {
+  static constexpr int W = pack_width<TX>::value;
+  static constexpr uint32_t WB = W * sizeof(typename TW::bits);  // weight bytes per packet
+  Packet<TX> xv[VPL];
+
+  __device__ __forceinline__ void load_x(rsrc_t rx, int slot) {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) xv[k].raw = buf_load16(rx, static_cast<uint32_t>(slot + k * STRIDE) * 16u);
+  }
+  __device__ __forceinline__ float sumsq() const {
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      float f[W];
+      xv[k].unpack(f);
+#pragma unroll
+      for (int e = 0; e < W; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+    }
+    return ss;
+  }
+  template <typename TY>
+  __device__ __forceinline__ void store_y(rsrc_t ry, int slot, float rstd, BufChunk<TW, W> (&wv)[VPL]) {
+    constexpr uint32_t YB = W * sizeof(typename TY::bits);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      reg_barrier(xv[k].raw);  // re-widen x here instead of keeping fp32 copies from sumsq()
+#pragma unroll
+      for (int d = 0; d < BufChunk<TW, W>::DW; ++d) reg_barrier(wv[k].raw[d]);
+      float f[W], o[W];
+      xv[k].unpack(f);
+#pragma unroll
+      for (int e = 0; e < W; ++e) o[e] = (f[e] * rstd) * wv[k].get(e);
+      buf_store_chunk<TY, W>(ry, static_cast<uint32_t>(slot + k * STRIDE) * YB, o);
+    }
+  }
+};
+
+// One wave64 per row.  The grid is normally one-shot (a wave per row); the
+// row loop only repeats when the launcher caps the grid.
 template <typename TX, typename TW, typename TY, int VPL>
 __global__ __launch_bounds__(256) void rmsnorm_wave_rows(const void* __restrict__ x,
                                                          const void* __restrict__ w,
                                                          void* __restrict__ y, int64_t rows, int n,
                                                          int64_t xs, int64_t ys, float eps) {
-  constexpr int W = pack_width<TX>::value;
-  using XB = typename TX::bits;
-  using WB = typename TW::bits;
-  using YB = typename TY::bits;
+  using S = RowSlice<TX, TW, VPL, 64>;
   const int lane = threadIdx.x & 63;
   const int waves_per_block = blockDim.x >> 6;
-  const int nvec = n / W;
+  const uint32_t xbytes = static_cast<uint32_t>(n) * sizeof(typename TX::bits);
+  const uint32_t ybytes = static_cast<uint32_t>(n) * sizeof(typename TY::bits);
 
-  Chunk<TW, W> wv[VPL];
+  BufChunk<TW, S::W> wv[VPL];
+  const rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(n) * sizeof(typename TW::bits));
 #pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + 64 * k;
-    if (v < nvec) wv[k].load(static_cast<const WB*>(w) + static_cast<int64_t>(v) * W);
-  }
+  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(lane + 64 * k) * S::WB);
 
   const int64_t step = static_cast<int64_t>(gridDim.x) * waves_per_block;
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * waves_per_block + (threadIdx.x >> 6); r < rows;
        r += step) {
-    const XB* xr = static_cast<const XB*>(x) + r * xs;
-    Packet<TX> xv[VPL];
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int v = lane + 64 * k;
-      xv[k].raw = (v < nvec) ? *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(v) * W)
-                             : u32x4{0u, 0u, 0u, 0u};
-    }
-    float ss = 0.0f;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      float f[W];
-      xv[k].unpack(f);
-#pragma unroll
-      for (int e = 0; e < W; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
-    }
-    const float rstd = rms_rstd(wave_allreduce_sum(ss), n, eps);
-
-    YB* yr = static_cast<YB*>(y) + r * ys;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int v = lane + 64 * k;
-      if (v < nvec) {
-        float f[W], o[W];
-        xv[k].unpack(f);
-#pragma unroll
-        for (int e = 0; e < W; ++e) o[e] = (f[e] * rstd) * wv[k].get(e);
-        store_chunk<TY, W>(yr + static_cast<int64_t>(v) * W, o);
-      }
-    }
+    S row;
+    row.load_x(make_rsrc(static_cast<const typename TX::bits*>(x) + r * xs, xbytes), lane);
+    const float rstd = rms_rstd(wave_allreduce_sum(row.sumsq()), n, eps);
+    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(y) + r * ys, ybytes), lane, rstd, wv);
   }
 }
 
+// One workgroup of BLOCK threads per row, for rows wider than a wave holds.
+// Per-wave partial sums meet in LDS, double-buffered so a row costs one
+// barrier.
 template <typename TX, typename TW, typename TY, int VPL, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void rmsnorm_block_rows(const void* __restrict__ x,
                                                             const void* __restrict__ w,
                                                             void* __restrict__ y, int64_t rows, int n,
                                                             int64_t xs, int64_t ys, float eps) {
-  constexpr int W = pack_width<TX>::value;
+  using S = RowSlice<TX, TW, VPL, BLOCK>;
   constexpr int NWAVE = BLOCK / 64;
-  using XB = typename TX::bits;
-  using WB = typename TW::bits;
-  using YB = typename TY::bits;
   __shared__ float partial[2][NWAVE];
   const int tid = threadIdx.x;
-  const int nvec = n / W;
+  const uint32_t xbytes = static_cast<uint32_t>(n) * sizeof(typename TX::bits);
+  const uint32_t ybytes = static_cast<uint32_t>(n) * sizeof(typename TY::bits);
 
-  Chunk<TW, W> wv[VPL];
+  BufChunk<TW, S::W> wv[VPL];
+  const rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(n) * sizeof(typename TW::bits));
 #pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = tid + BLOCK * k;
-    if (v < nvec) wv[k].load(static_cast<const WB*>(w) + static_cast<int64_t>(v) * W);
-  }
+  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + BLOCK * k) * S::WB);
 
   int buf = 0;
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    const XB* xr = static_cast<const XB*>(x) + r * xs;
-    Packet<TX> xv[VPL];
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int v = tid + BLOCK * k;
-      xv[k].raw = (v < nvec) ? *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(v) * W)
-                             : u32x4{0u, 0u, 0u, 0u};
-    }
-    float ss = 0.0f;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      float f[W];
-      xv[k].unpack(f);
-#pragma unroll
-      for (int e = 0; e < W; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
-    }
-    ss = wave_allreduce_sum(ss);
+    S row;
+    row.load_x(make_rsrc(static_cast<const typename TX::bits*>(x) + r * xs, xbytes), tid);
+    const float ss = wave_allreduce_sum(row.sumsq());
     if ((tid & 63) == 0) partial[buf][tid >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
     for (int i = 0; i < NWAVE; ++i) tot += partial[buf][i];
     buf ^= 1;  // the next row writes the other buffer; this row's barrier orders the reuse
-    const float rstd = rms_rstd(tot, n, eps);
-
-    YB* yr = static_cast<YB*>(y) + r * ys;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int v = tid + BLOCK * k;
-      if (v < nvec) {
-        float f[W], o[W];
-        xv[k].unpack(f);
-#pragma unroll
-        for (int e = 0; e < W; ++e) o[e] = (f[e] * rstd) * wv[k].get(e);
-        store_chunk<TY, W>(yr + static_cast<int64_t>(v) * W, o);
-      }
-    }
+    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(y) + r * ys, ybytes), tid,
+                             rms_rstd(tot, n, eps), wv);
   }
 }
 

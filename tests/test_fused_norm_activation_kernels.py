@@ -151,7 +151,7 @@ def test_silu_mul_fp32_value_within_tolerance(orc, cuda, numel, dtype):
 
 # ------------------------------------------------------ dtype / width matrix
 
-RMS_WIDTHS = [1, 8, 64, 100, 512, 896, 1536, 2048, 3584, 4096, 5120, 8192, 8200, 10240, 16384, 40000, 140000]
+RMS_WIDTHS = [1, 8, 64, 100, 512, 896, 1536, 2048, 3584, 4096, 5120, 8192, 8200, 10240, 16384, 40000, 65536, 65544, 140000]
 
 
 @pytest.mark.parametrize("n", RMS_WIDTHS)
