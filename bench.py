@@ -61,6 +61,9 @@ def parse_args():
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c4-silu", "c4-rms", "copy"], default=None,
                    help="run one kernel loop only (for profiler runs)")
+    p.add_argument("--rocprof-summary", nargs="+", metavar="DIR", default=None,
+                   help="summarise rocprofv3 output directories (kernel trace and/or PMC) and exit; "
+                        "no GPU needed")
     return p.parse_args()
 
 
@@ -191,14 +194,14 @@ def kernel_entry(name, nbytes, us, extra=None):
     return d
 
 
-def read_traffic(kernel_key: str):
-    """FETCH_SIZE + WRITE_SIZE per launch (bytes) recorded from rocprofv3 PMC
-    runs in profiles/traffic.json, if that summary exists."""
+def read_traffic(label: str):
+    """HBM bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE) recorded from
+    rocprofv3 PMC runs in profiles/traffic.json, if that summary exists."""
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
         return None
     try:
-        d = json.loads(p.read_text()).get(kernel_key)
+        d = json.loads(p.read_text()).get(label)
         return None if d is None else d.get("traffic_bytes")
     except Exception:
         return None
@@ -231,7 +234,7 @@ def cpu_baseline(M, N, I, budget_s):
         orc.naive_rmsnorm_torch(x, w)
         orc.naive_silu_mul_torch(gate, up)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 1000:
+        if len(times) >= 20000:
             break
     step = statistics.median(times)
     nbytes = (2 * M * N + N) * 2 + 3 * M * I * 2
@@ -246,8 +249,107 @@ def cpu_baseline(M, N, I, budget_s):
                       f"median of {len(times)} steps in ~{budget_s:.0f}s"}
 
 
+# --------------------------------------------------------- rocprof summaries
+
+# Algorithmic bytes per launch, keyed by (kernel-name fragment, grid size X):
+# used to turn rocprofv3 durations into GB/s and to set PMC traffic against
+# the ideal.  Grid sizes are in threads, as rocprofv3 reports them.
+KNOWN_LAUNCHES = {
+    ("silu_mul_chunks<mi355::F16, mi355::F16>", 1146880): ("C2 SiLU-and-mul [2048,8960] fp16", 3 * 2048 * 8960 * 2),
+    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3>", 131072): (
+        "C1 RMSNorm [2048,1536] fp16", (2 * 2048 * 1536 + 1536) * 2),
+    ("silu_mul_chunks<mi355::BF16, mi355::BF16>", 19398656): (
+        "C4 SiLU-and-mul [16384,18944] bf16", 3 * 16384 * 18944 * 2),
+    ("rmsnorm_wave_rows<mi355::BF16, mi355::BF16, mi355::BF16, 7>", 1048576): (
+        "C4 RMSNorm [16384,3584] bf16", (2 * 16384 * 3584 + 3584) * 2),
+    ("stream_copy", 67108864): ("copy probe, 1 GiB", 2 << 30),
+}
+COPY_READ_KIB = COPY_WRITE_KIB = (1 << 30) / 1024
+
+
+def _match_launch(name: str, grid: int):
+    for (frag, g), v in KNOWN_LAUNCHES.items():
+        if frag in name and g == grid:
+            return frag, v
+    return None, None
+
+
+def rocprof_summary(dirs):
+    """Markdown summary of rocprofv3 CSV output: per (kernel, grid) average
+    duration and GB/s from *_kernel_trace.csv; per-dispatch FETCH_SIZE /
+    WRITE_SIZE from *_counter_collection.csv, scaled by the factor that makes
+    the copy probe read and write exactly 1 GiB."""
+    import csv
+    import glob
+
+    out = []
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "*kernel_trace.csv"))):
+            out.append(f"### kernel trace: {f}\n")
+            out.append("| kernel | grid (threads) | launches | avg us | median us | algorithmic bytes | GB/s (avg) | % of 8 TB/s |")
+            out.append("|---|---|---|---|---|---|---|---|")
+            groups = {}
+            for r in csv.DictReader(open(f)):
+                frag, known = _match_launch(r["Kernel_Name"], int(r["Grid_Size_X"]))
+                if known is None:
+                    continue
+                groups.setdefault((frag, int(r["Grid_Size_X"])), []).append(
+                    int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+            for (frag, grid), v in groups.items():
+                label, nbytes = KNOWN_LAUNCHES[(frag, grid)]
+                v.sort()
+                avg = sum(v) / len(v) / 1e3
+                gbs = nbytes / avg / 1e3
+                out.append(f"| {frag} ({label}) | {grid} | {len(v)} | {avg:.3f} | {v[len(v) // 2] / 1e3:.3f} | "
+                           f"{nbytes} | {gbs:.0f} | {100 * gbs / PEAK_GBS:.1f} |")
+            out.append("")
+        pmc = {}
+        for f in sorted(glob.glob(os.path.join(d, "*counter_collection.csv"))):
+            for r in csv.DictReader(open(f)):
+                frag, known = _match_launch(r["Kernel_Name"], int(r["Grid_Size"]))
+                if known is None:
+                    continue
+                pmc.setdefault((frag, int(r["Grid_Size"]), r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+        if pmc:
+            globals().setdefault("_PMC", {}).update(pmc)
+    pmc = globals().get("_PMC", {})
+    traffic = {}
+    if pmc:
+        cf = pmc.get(("stream_copy", 67108864, "FETCH_SIZE"))
+        cw = pmc.get(("stream_copy", 67108864, "WRITE_SIZE"))
+        fscale = COPY_READ_KIB / (sum(cf) / len(cf)) if cf else None
+        wscale = COPY_WRITE_KIB / (sum(cw) / len(cw)) if cw else None
+        out.append("### PMC traffic (KiB per dispatch, then scaled)\n")
+        out.append(f"Calibration: the copy probe reads and writes exactly 1 GiB per launch; "
+                   f"FETCH_SIZE scale = {fscale if fscale is None else round(fscale, 5)}, "
+                   f"WRITE_SIZE scale = {wscale if wscale is None else round(wscale, 5)}.\n")
+        out.append("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled HBM bytes | algorithmic bytes | ratio |")
+        out.append("|---|---|---|---|---|---|---|")
+        keys = sorted({(k[0], k[1]) for k in pmc})
+        for frag, grid in keys:
+            fv = pmc.get((frag, grid, "FETCH_SIZE"))
+            wv = pmc.get((frag, grid, "WRITE_SIZE"))
+            if not fv or not wv or fscale is None or wscale is None:
+                continue
+            fk = sum(fv) / len(fv)
+            wk = sum(wv) / len(wv)
+            tb = (fk * fscale + wk * wscale) * 1024
+            label, nbytes = KNOWN_LAUNCHES[(frag, grid)]
+            out.append(f"| {frag} ({label}) | {len(fv)} | {fk:.1f} | {wk:.1f} | {tb:.0f} | {nbytes} | {tb / nbytes:.4f} |")
+            traffic[label] = {"traffic_bytes": round(tb), "algorithmic_bytes": nbytes,
+                              "fetch_kib": round(fk, 1), "write_kib": round(wk, 1)}
+        out.append("")
+    return "\n".join(out), traffic
+
+
 def main():
     args = parse_args()
+    if args.rocprof_summary:
+        text, traffic = rocprof_summary(args.rocprof_summary)
+        print(text)
+        if traffic:
+            print("\n```json\n" + json.dumps(traffic, indent=1) + "\n```")
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only (the fused RMSNorm/SwiGLU path is row-parallel "
@@ -337,7 +439,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "silu_mul_chunks (C2 SiLU-and-mul [2048,8960] fp16)",
                      "achieved": round(silu_bytes / silu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(silu_bytes / silu_us / 1e3 / PEAK_GBS, 4),
-                     "traffic": read_traffic("c2_silu_mul"), "algorithmic_bytes": silu_bytes,
+                     "traffic": read_traffic("C2 SiLU-and-mul [2048,8960] fp16"), "algorithmic_bytes": silu_bytes,
                      "avg_launch_us": round(silu_us, 3)},
         "kernels": kernels,
     }
