@@ -14,6 +14,17 @@
 #define MI355_RMS_SMALL_ROWS 1024
 #endif
 
+// Row split: rows needing more than WAVE_MAX_VPL packets per lane of one wave
+// are spread over several waves with at most TARGET_VPL packets per lane
+// (measured on MI355X: 1536-wide fp16 rows are fastest as 3 packets per lane
+// of one wave, 3584-wide bf16 rows as 2 packets per lane of 4 waves).
+#ifndef MI355_RMS_WAVE_MAX_VPL
+#define MI355_RMS_WAVE_MAX_VPL 4
+#endif
+#ifndef MI355_RMS_TARGET_VPL
+#define MI355_RMS_TARGET_VPL 2
+#endif
+
 namespace mi355 {
 namespace {
 
@@ -62,6 +73,7 @@ int rms_wave(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
     case 2: MI355_WAVE_CASE(2);
     case 3: MI355_WAVE_CASE(3);
     case 4: MI355_WAVE_CASE(4);
+#if MI355_RMS_WAVE_MAX_VPL > 4
     case 5: MI355_WAVE_CASE(5);
     case 6: MI355_WAVE_CASE(6);
     case 7: MI355_WAVE_CASE(7);
@@ -70,25 +82,33 @@ int rms_wave(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
     case 10: MI355_WAVE_CASE(10);
     case 11:
     case 12: MI355_WAVE_CASE(12);
-    default: MI355_WAVE_CASE(16);
+    case 13: case 14: case 15:
+    case 16: MI355_WAVE_CASE(16);
+#endif
+    default:
+      set_error("mi355_rmsnorm_fwd: internal error, no wave kernel for %d packets per lane", vpl);
+      return MI355_ERR_UNSUPPORTED;
   }
 #undef MI355_WAVE_CASE
 }
 
-template <typename TX, typename TW, typename TY, int BLOCK>
-int rms_block(const RmsArgs& a, hipStream_t s, int cus, int vpl) {
+
+template <typename TX, typename TW, typename TY>
+int rms_block(const RmsArgs& a, hipStream_t s, int cus, int waves, int vpl) {
+  (void)cus;
+  const int block = 64 * waves;
   int64_t grid = a.rows;
-  const int64_t cap = MI355_RMS_WAVES_PER_CU > 0
-                          ? static_cast<int64_t>(cus) * (MI355_RMS_WAVES_PER_CU / (BLOCK / 64) + 1)
-                          : int64_t{0x7fffffff};
-  if (grid > cap) grid = cap;
-  // 1024-thread workgroups get 128 VGPRs per lane: VPL 8 is the most that fits.
-  if constexpr (BLOCK == 1024) {
-    return launch_rms(rmsnorm_block_rows<TX, TW, TY, 8, BLOCK>, grid, BLOCK, a, s);
-  } else {
-    if (vpl <= 8) return launch_rms(rmsnorm_block_rows<TX, TW, TY, 8, BLOCK>, grid, BLOCK, a, s);
-    return launch_rms(rmsnorm_block_rows<TX, TW, TY, 16, BLOCK>, grid, BLOCK, a, s);
+  if (grid > 0x7fffffff) grid = 0x7fffffff;
+#define MI355_BLOCK_CASE(V) \
+  return launch_rms(rmsnorm_block_rows<TX, TW, TY, V>, grid, block, a, s)
+  switch (vpl) {
+    case 1: MI355_BLOCK_CASE(1);
+    case 2: MI355_BLOCK_CASE(2);
+    case 3: MI355_BLOCK_CASE(3);
+    case 4: MI355_BLOCK_CASE(4);
+    default: MI355_BLOCK_CASE(8);
   }
+#undef MI355_BLOCK_CASE
 }
 
 // Packet path: n a multiple of the packet width, every pointer and row
@@ -102,12 +122,16 @@ int rms_packets(const RmsArgs& a, hipStream_t s, int cus) {
   if (!ok) return rms_generic<TX, TW, TY>(a, s, cus);
   const int nvec = a.n / W;
   const int vpl64 = (nvec + 63) / 64;
-  if (vpl64 <= 16) return rms_wave<TX, TW, TY>(a, s, cus, vpl64);
-  const int vpl256 = (nvec + 255) / 256;
-  if (vpl256 <= 16) return rms_block<TX, TW, TY, 256>(a, s, cus, vpl256);
-  const int vpl1024 = (nvec + 1023) / 1024;
-  if (vpl1024 <= 8) return rms_block<TX, TW, TY, 1024>(a, s, cus, vpl1024);
-  return rms_generic<TX, TW, TY>(a, s, cus);
+  if (vpl64 <= MI355_RMS_WAVE_MAX_VPL) return rms_wave<TX, TW, TY>(a, s, cus, vpl64);
+  // Spread the row over enough waves (at most 16) for <= TARGET_VPL packets
+  // per lane, then use the fewest packets per lane that covers the row.
+  const int target = MI355_RMS_TARGET_VPL < 8 ? MI355_RMS_TARGET_VPL : 8;
+  int waves = (nvec + 64 * target - 1) / (64 * target);
+  if (waves > 16) waves = 16;
+  int vpl = (nvec + 64 * waves - 1) / (64 * waves);
+  if (vpl > 8) return rms_generic<TX, TW, TY>(a, s, cus);
+  waves = (nvec + 64 * vpl - 1) / (64 * vpl);  // fewest waves for that many packets per lane
+  return rms_block<TX, TW, TY>(a, s, cus, waves, vpl);
 }
 
 template <typename TX, typename TY>

@@ -84,19 +84,22 @@ __global__ __launch_bounds__(256) void rmsnorm_wave_rows(const void* __restrict_
                                                          void* __restrict__ y, int64_t rows, int n,
                                                          int64_t xs, int64_t ys, float eps) {
   using S = RowSlice<TX, TW, VPL, 64>;
+  using WC = BufChunk<TW, S::W>;
   const int lane = threadIdx.x & 63;
   const int waves_per_block = blockDim.x >> 6;
   const uint32_t xbytes = static_cast<uint32_t>(n) * sizeof(typename TX::bits);
   const uint32_t ybytes = static_cast<uint32_t>(n) * sizeof(typename TY::bits);
-
-  BufChunk<TW, S::W> wv[VPL];
-  const rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(n) * sizeof(typename TW::bits));
+  const uint32_t wbytes = static_cast<uint32_t>(n) * sizeof(typename TW::bits);
+  const rsrc_t rw = make_rsrc(w, wbytes);
+  WC wv[VPL];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(lane + 64 * k) * S::WB);
 
+  // The wave's index in its workgroup is wave-uniform; readfirstlane says so,
+  // which keeps the row's buffer descriptor in SGPRs (no waterfall loop).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t step = static_cast<int64_t>(gridDim.x) * waves_per_block;
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * waves_per_block + (threadIdx.x >> 6); r < rows;
-       r += step) {
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; r < rows; r += step) {
     S row;
     row.load_x(make_rsrc(static_cast<const typename TX::bits*>(x) + r * xs, xbytes), lane);
     const float rstd = rms_rstd(wave_allreduce_sum(row.sumsq()), n, eps);
@@ -104,39 +107,63 @@ __global__ __launch_bounds__(256) void rmsnorm_wave_rows(const void* __restrict_
   }
 }
 
-// One workgroup of BLOCK threads per row, for rows wider than a wave holds.
-// Per-wave partial sums meet in LDS, double-buffered so a row costs one
-// barrier.
-template <typename TX, typename TW, typename TY, int VPL, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void rmsnorm_block_rows(const void* __restrict__ x,
-                                                            const void* __restrict__ w,
-                                                            void* __restrict__ y, int64_t rows, int n,
-                                                            int64_t xs, int64_t ys, float eps) {
-  using S = RowSlice<TX, TW, VPL, BLOCK>;
-  constexpr int NWAVE = BLOCK / 64;
-  __shared__ float partial[2][NWAVE];
+// One workgroup per row, blockDim.x = 64 * (waves per row) <= 1024 threads;
+// lane t of the workgroup holds packets t + k * blockDim.x, k < VPL.  Used
+// for rows wider than one wave holds and, with VPL small, to spread a row over
+// several waves (fewer VGPRs and finer-grained work per wave).  Per-wave
+// partial sums meet in LDS, double-buffered so a row costs one barrier.
+template <typename TX, typename TW, typename TY, int VPL>
+__global__ __launch_bounds__(1024) void rmsnorm_block_rows(const void* __restrict__ x,
+                                                           const void* __restrict__ w,
+                                                           void* __restrict__ y, int64_t rows, int n,
+                                                           int64_t xs, int64_t ys, float eps) {
+  constexpr int W = pack_width<TX>::value;
+  constexpr uint32_t WB = W * sizeof(typename TW::bits);
+  constexpr uint32_t YB = W * sizeof(typename TY::bits);
+  __shared__ float partial[2][16];
   const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int nwave = nthreads >> 6;
   const uint32_t xbytes = static_cast<uint32_t>(n) * sizeof(typename TX::bits);
   const uint32_t ybytes = static_cast<uint32_t>(n) * sizeof(typename TY::bits);
 
-  BufChunk<TW, S::W> wv[VPL];
+  BufChunk<TW, W> wv[VPL];
   const rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(n) * sizeof(typename TW::bits));
 #pragma unroll
-  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + BLOCK * k) * S::WB);
+  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + nthreads * k) * WB);
 
   int buf = 0;
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    S row;
-    row.load_x(make_rsrc(static_cast<const typename TX::bits*>(x) + r * xs, xbytes), tid);
-    const float ss = wave_allreduce_sum(row.sumsq());
+    const rsrc_t rx = make_rsrc(static_cast<const typename TX::bits*>(x) + r * xs, xbytes);
+    Packet<TX> xv[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) xv[k].raw = buf_load16(rx, static_cast<uint32_t>(tid + nthreads * k) * 16u);
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      float f[W];
+      xv[k].unpack(f);
+#pragma unroll
+      for (int e = 0; e < W; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+    }
+    ss = wave_allreduce_sum(ss);
     if ((tid & 63) == 0) partial[buf][tid >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NWAVE; ++i) tot += partial[buf][i];
+    for (int i = 0; i < nwave; ++i) tot += partial[buf][i];
     buf ^= 1;  // the next row writes the other buffer; this row's barrier orders the reuse
-    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(y) + r * ys, ybytes), tid,
-                             rms_rstd(tot, n, eps), wv);
+    const float rstd = rms_rstd(tot, n, eps);
+
+    const rsrc_t ry = make_rsrc(static_cast<typename TY::bits*>(y) + r * ys, ybytes);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      reg_barrier(xv[k].raw);
+      float f[W], o[W];
+      xv[k].unpack(f);
+#pragma unroll
+      for (int e = 0; e < W; ++e) o[e] = (f[e] * rstd) * wv[k].get(e);
+      buf_store_chunk<TY, W>(ry, static_cast<uint32_t>(tid + nthreads * k) * YB, o);
+    }
   }
 }
 
