@@ -61,6 +61,13 @@ def parse_args():
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c4-silu", "c4-rms", "copy"], default=None,
                    help="run one kernel loop only (for profiler runs)")
+    p.add_argument("--e2e", action="store_true",
+                   help="instead of the kernel bench: TTFT and decode tok/s of a random-init Qwen2-1.5B "
+                        "architecture before and after patch_model_with_fused_kernels (the reference's "
+                        "benchmarks/run_stage3_e2e.py method)")
+    p.add_argument("--seq-lens", type=int, nargs="+", default=[128, 512, 1024, 2048])
+    p.add_argument("--gen-len", type=int, default=32)
+    p.add_argument("--trials", type=int, default=5)
     p.add_argument("--rocprof-summary", nargs="+", metavar="DIR", default=None,
                    help="summarise rocprofv3 output directories (kernel trace and/or PMC) and exit; "
                         "no GPU needed")
@@ -100,6 +107,19 @@ class Ctx:
             st = f(*args, self.stream)
             if st:
                 self.L.check("mi355_rmsnorm_fwd", st)
+        return call
+
+    def add_rms_call(self, x, r, w, y, h, eps=1e-6):
+        M, N = x.shape
+        code = self.L.DTYPE_CODE[x.dtype]
+        f = self.lib.mi355_add_rmsnorm_fwd
+        args = (x.data_ptr(), r.data_ptr(), w.data_ptr(), y.data_ptr(), h.data_ptr(), M, N, N, N, N, N,
+                ctypes.c_float(eps), code, self.L.DTYPE_CODE[w.dtype], code)
+
+        def call():
+            st = f(*args, self.stream)
+            if st:
+                self.L.check("mi355_add_rmsnorm_fwd", st)
         return call
 
     def silu_call(self, g, u, o):
@@ -356,6 +376,10 @@ def main():
               "and needs no cross-GPU exchange); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.e2e:
+        bench_e2e(args)
+        return
+
     ctx = Ctx()
     torch = ctx.torch
     props = torch.cuda.get_device_properties(ctx.dev)
@@ -447,6 +471,7 @@ def main():
     if not args.skip_extras:
         del sets
         torch.cuda.empty_cache()
+        result["add_rmsnorm"] = bench_add_rms(ctx, iters)
         result["c4"] = bench_c4(ctx, iters=60)
         result["decode"] = bench_decode(ctx)
         result["copy_ceiling"] = bench_copy(ctx)
@@ -477,6 +502,38 @@ def run_only(ctx, args, sets):
         log(json.dumps(d))
     elif args.only == "copy":
         log(json.dumps(bench_copy(ctx)))
+
+
+def bench_add_rms(ctx, iters):
+    """Residual add + RMSNorm at the C1 shape (beyond the reference): the fused
+    kernel vs the unfused pair (torch's add, then the RMSNorm kernel), cold."""
+    torch = ctx.torch
+    F16 = torch.float16
+    M, N = 2048, 1536
+    fused_bytes = (4 * M * N + N) * 2
+    w = rand(ctx, (N,), 1, F16, 1.0, 0.1)
+    sets = []
+    for s in range(n_sets(fused_bytes)):
+        x, r = rand(ctx, (M, N), 700 + s, F16), rand(ctx, (M, N), 800 + s, F16)
+        sets.append((x, r, torch.empty_like(x), torch.empty_like(x)))
+    fused = [ctx.add_rms_call(x, r, w, y, h) for x, r, y, h in sets]
+    rms = [ctx.rms_call(h, w, y) for x, r, y, h in sets]
+
+    def unfused_call(i):
+        x, r, y, h = sets[i]
+        return lambda: (torch.add(r, x, out=h), rms[i]())
+
+    fused_us = time_loop(ctx, fused, iters)
+    unfused_us = time_loop(ctx, [unfused_call(i) for i in range(len(sets))], iters)
+    out = {"c1_add_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,ADD>", fused_bytes,
+                                                        fused_us, {"buffer_sets": len(sets)}),
+           "c1_add_then_rmsnorm_unfused_us": round(unfused_us, 3),
+           "fused_speedup": round(unfused_us / fused_us, 3)}
+    log(f"  add+rmsnorm C1: fused {fused_us:.2f} us ({out['c1_add_rmsnorm_f16_2048x1536']['GBps']:.0f} GB/s), "
+        f"unfused {unfused_us:.2f} us")
+    del sets
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_c4(ctx, iters=60, which=None):
@@ -586,6 +643,76 @@ def bench_copy(ctx, nbytes=1 << 30, iters=30):
     torch.cuda.empty_cache()
     log(f"  copy ceiling: {d['GBps']:.0f} GB/s ({d['frac_of_peak']:.1%})")
     return d
+
+
+def bench_e2e(args):
+    """TTFT and decode throughput before/after the module replacement, as the
+    reference measures them (benchmarks/run_stage3_e2e.py:33-108 with
+    src/engine/profiler.py:72-204): batch 1, uniform random prompts, event-
+    timed prefill, event-timed greedy decode over HF's KV cache, mean of
+    `trials` after `warmup` runs.  The model is a random-init Qwen2 with
+    Qwen2.5-1.5B's architecture in fp16 (no Hub access here), sdpa attention."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    sys.path.insert(0, str(ROOT))
+    pkg = importlib.import_module(PKG)
+    dev = torch.device("cuda:0")
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
+                      num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=32768,
+                      rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.half().eval()
+
+    def run(ids, gen_len):
+        with torch.inference_mode():
+            torch.cuda.synchronize()
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record()
+            out = model(input_ids=ids, use_cache=True)
+            past = out.past_key_values
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            s1.record()
+            torch.cuda.synchronize()
+            d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            d0.record()
+            for _ in range(gen_len - 1):
+                out = model(input_ids=tok, past_key_values=past, use_cache=True)
+                past = out.past_key_values
+                tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            d1.record()
+            torch.cuda.synchronize()
+            return s0.elapsed_time(s1), (gen_len - 1) / (d0.elapsed_time(d1) / 1e3)
+
+    def measure(tag):
+        res = {}
+        for S in args.seq_lens:
+            g = torch.Generator()
+            g.manual_seed(S)
+            ids = torch.randint(0, cfg.vocab_size, (1, S), generator=g).to(dev)
+            for _ in range(2):
+                run(ids, args.gen_len)
+            t = [run(ids, args.gen_len) for _ in range(args.trials)]
+            res[S] = (statistics.mean(x[0] for x in t), statistics.mean(x[1] for x in t))
+            log(f"  {tag} seq {S}: TTFT {res[S][0]:.2f} ms, decode {res[S][1]:.1f} tok/s")
+        return res
+
+    before = measure("before")
+    counts = pkg.patch_model_with_fused_kernels(model)
+    log(f"patched {counts}")
+    after = measure("after")
+    rows = []
+    for S in args.seq_lens:
+        rows.append({"seq_len": S, "before_ttft_ms": round(before[S][0], 3), "after_ttft_ms": round(after[S][0], 3),
+                     "ttft_speedup": round(before[S][0] / after[S][0], 4),
+                     "before_decode_tok_s": round(before[S][1], 2), "after_decode_tok_s": round(after[S][1], 2),
+                     "decode_speedup": round(after[S][1] / before[S][1], 4)})
+    print(json.dumps({"metric": "e2e TTFT / decode tok/s speedup from patch_model_with_fused_kernels",
+                      "model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16, sdpa, batch 1",
+                      "gen_len": args.gen_len, "trials": args.trials, "patched": counts, "results": rows}),
+          flush=True)
 
 
 if __name__ == "__main__":

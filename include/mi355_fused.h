@@ -81,6 +81,34 @@ int mi355_rmsnorm_fwd(const void* x, const void* weight, void* y,
                       void* stream);
 
 /*
+ * Residual add fused with RMSNorm, per row:
+ *   h[r,j]            = x[r,j] + residual[r,j]   (fp32 add, rounded to x_dtype)
+ *   residual_out[r,j] = h[r,j]
+ *   y[r,j]            = RMSNorm(h)[r,j]          (as mi355_rmsnorm_fwd)
+ *
+ * The reference has no kernel for this; it is the "fused RMSNorm + residual"
+ * its design plans (docs/architecture-cuda.md:94) for the decoder's
+ * `hidden = residual + attn_out; normed = post_attention_layernorm(hidden)`
+ * (the HF Qwen2 decoder layer, and src/engine/paged_engine.py:138-141).  h is
+ * rounded exactly where the unfused add rounds it, so the results equal the
+ * add followed by mi355_rmsnorm_fwd bit for bit, in one pass over the rows:
+ * read x and residual, write residual_out and y.
+ *
+ *   x, residual, residual_out: x_dtype, [rows, *_row_stride], rows contiguous.
+ *   weight [n] of w_dtype; y [rows, y_row_stride] of y_dtype (x_dtype or fp32).
+ *   residual_out may be residual and y may be x (in place, same strides);
+ *   y must not overlap residual or residual_out.
+ */
+int mi355_add_rmsnorm_fwd(const void* x, const void* residual, const void* weight,
+                          void* y, void* residual_out,
+                          int64_t rows, int64_t n,
+                          int64_t x_row_stride, int64_t residual_row_stride,
+                          int64_t y_row_stride, int64_t residual_out_row_stride,
+                          float eps,
+                          int x_dtype, int w_dtype, int y_dtype,
+                          void* stream);
+
+/*
  * SiLU-and-mul, the activation step of a SwiGLU MLP, over flat memory:
  *   out[i] = (g * sigmoid(g)) * u,  g = gate[i], u = up[i]   (fp32, rounded once)
  *

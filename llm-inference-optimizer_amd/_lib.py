@@ -24,7 +24,8 @@ ABI_VERSION = 1
 F32, F16, BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
-EXPORTED_SYMBOLS = ("mi355_abi_version", "mi355_last_error", "mi355_rmsnorm_fwd", "mi355_silu_mul_fwd")
+EXPORTED_SYMBOLS = ("mi355_abi_version", "mi355_last_error", "mi355_rmsnorm_fwd", "mi355_add_rmsnorm_fwd",
+                    "mi355_silu_mul_fwd")
 
 
 class KernelLibraryMissing(RuntimeError):
@@ -63,6 +64,9 @@ def load() -> ctypes.CDLL:
         L.mi355_last_error.restype = ctypes.c_char_p
         L.mi355_rmsnorm_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, i32, i32, i32, vp]
         L.mi355_rmsnorm_fwd.restype = i32
+        L.mi355_add_rmsnorm_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float,
+                                            i32, i32, i32, vp]
+        L.mi355_add_rmsnorm_fwd.restype = i32
         L.mi355_silu_mul_fwd.argtypes = [vp, vp, vp, i64, i32, i32, vp]
         L.mi355_silu_mul_fwd.restype = i32
         ver = L.mi355_abi_version()
@@ -87,6 +91,14 @@ def rmsnorm_fwd(x_ptr: int, w_ptr: int, y_ptr: int, rows: int, n: int, x_row_str
     check("mi355_rmsnorm_fwd",
           load().mi355_rmsnorm_fwd(x_ptr, w_ptr, y_ptr, rows, n, x_row_stride, y_row_stride, eps,
                                    x_dtype, w_dtype, y_dtype, stream))
+
+
+def add_rmsnorm_fwd(x_ptr: int, r_ptr: int, w_ptr: int, y_ptr: int, ro_ptr: int, rows: int, n: int,
+                    x_row_stride: int, r_row_stride: int, y_row_stride: int, ro_row_stride: int, eps: float,
+                    x_dtype: int, w_dtype: int, y_dtype: int, stream: int) -> None:
+    check("mi355_add_rmsnorm_fwd",
+          load().mi355_add_rmsnorm_fwd(x_ptr, r_ptr, w_ptr, y_ptr, ro_ptr, rows, n, x_row_stride, r_row_stride,
+                                       y_row_stride, ro_row_stride, eps, x_dtype, w_dtype, y_dtype, stream))
 
 
 def silu_mul_fwd(gate_ptr: int, up_ptr: int, out_ptr: int, numel: int, in_dtype: int, out_dtype: int,

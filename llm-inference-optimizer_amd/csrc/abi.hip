@@ -14,6 +14,9 @@ namespace mi355 {
 int rmsnorm_launch(const void* x, const void* w, void* y, int64_t rows, int n, int64_t xs,
                    int64_t ys, float eps, int x_dtype, int w_dtype, int y_dtype,
                    hipStream_t stream);
+int add_rmsnorm_launch(const void* x, const void* r, const void* w, void* y, void* ro, int64_t rows, int n,
+                       int64_t xs, int64_t rs, int64_t ys, int64_t ros, float eps, int x_dtype, int w_dtype,
+                       int y_dtype, hipStream_t stream);
 int silu_mul_launch(const void* gate, const void* up, void* out, int64_t numel, int in_dtype,
                     int out_dtype, hipStream_t stream);
 
@@ -61,44 +64,85 @@ MI355_EXPORT int mi355_abi_version(void) { return MI355_ABI_VERSION; }
 
 MI355_EXPORT const char* mi355_last_error(void) { return mi355::g_error; }
 
+namespace {
+
+// Shared argument checks of the two RMSNorm entry points; `strides` are the
+// row strides of the row-shaped operands, `ptrs` every pointer.  Returns
+// MI355_OK (and *noop for rows == 0) or an error code with the message set.
+int check_rows(const char* fn, int64_t rows, int64_t n, const int64_t* strides, int nstrides,
+               const void* const* ptrs, int nptrs, int x_dtype, int w_dtype, int y_dtype, bool* noop) {
+  *noop = false;
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype) || !valid_dtype(y_dtype)) {
+    set_error("%s: unknown dtype code (x=%d, w=%d, y=%d)", fn, x_dtype, w_dtype, y_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (y_dtype != x_dtype && y_dtype != MI355_F32) {
+    set_error("%s: y dtype must equal x dtype or be fp32 (x=%d, y=%d)", fn, x_dtype, y_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows < 0) {
+    set_error("%s: rows must be >= 0 (got %lld)", fn, static_cast<long long>(rows));
+    return MI355_ERR_INVALID;
+  }
+  if (n < 1 || n > 0x7fffffff) {
+    set_error("%s: n must be in [1, 2^31) (got %lld)", fn, static_cast<long long>(n));
+    return MI355_ERR_INVALID;
+  }
+  if (rows == 0) {
+    *noop = true;
+    return MI355_OK;
+  }
+  for (int i = 0; i < nptrs; ++i) {
+    if (ptrs[i] == nullptr) {
+      set_error("%s: null pointer (argument %d)", fn, i);
+      return MI355_ERR_INVALID;
+    }
+  }
+  for (int i = 0; i < nstrides; ++i) {
+    if (strides[i] < n) {
+      set_error("%s: row strides must be >= n (stride %lld, n=%lld)", fn, static_cast<long long>(strides[i]),
+                static_cast<long long>(n));
+      return MI355_ERR_INVALID;
+    }
+    if (rows - 1 > (INT64_MAX - n) / strides[i]) {
+      set_error("%s: rows * stride overflows int64", fn);
+      return MI355_ERR_INVALID;
+    }
+  }
+  return MI355_OK;
+}
+
+}  // namespace
+
 MI355_EXPORT int mi355_rmsnorm_fwd(const void* x, const void* weight, void* y, int64_t rows,
                                    int64_t n, int64_t x_row_stride, int64_t y_row_stride,
                                    float eps, int x_dtype, int w_dtype, int y_dtype,
                                    void* stream) {
   mi355::g_error[0] = '\0';
-  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype) || !valid_dtype(y_dtype)) {
-    set_error("mi355_rmsnorm_fwd: unknown dtype code (x=%d, w=%d, y=%d)", x_dtype, w_dtype, y_dtype);
-    return MI355_ERR_INVALID;
-  }
-  if (y_dtype != x_dtype && y_dtype != MI355_F32) {
-    set_error("mi355_rmsnorm_fwd: y dtype must equal x dtype or be fp32 (x=%d, y=%d)", x_dtype, y_dtype);
-    return MI355_ERR_UNSUPPORTED;
-  }
-  if (rows < 0) {
-    set_error("mi355_rmsnorm_fwd: rows must be >= 0 (got %lld)", static_cast<long long>(rows));
-    return MI355_ERR_INVALID;
-  }
-  if (n < 1 || n > 0x7fffffff) {
-    set_error("mi355_rmsnorm_fwd: n must be in [1, 2^31) (got %lld)", static_cast<long long>(n));
-    return MI355_ERR_INVALID;
-  }
-  if (rows == 0) return MI355_OK;
-  if (x == nullptr || weight == nullptr || y == nullptr) {
-    set_error("mi355_rmsnorm_fwd: null pointer (x=%p, weight=%p, y=%p)", x, weight, y);
-    return MI355_ERR_INVALID;
-  }
-  if (x_row_stride < n || y_row_stride < n) {
-    set_error("mi355_rmsnorm_fwd: row strides must be >= n (x=%lld, y=%lld, n=%lld)",
-              static_cast<long long>(x_row_stride), static_cast<long long>(y_row_stride),
-              static_cast<long long>(n));
-    return MI355_ERR_INVALID;
-  }
-  if (rows - 1 > (INT64_MAX - n) / x_row_stride || rows - 1 > (INT64_MAX - n) / y_row_stride) {
-    set_error("mi355_rmsnorm_fwd: rows * stride overflows int64");
-    return MI355_ERR_INVALID;
-  }
+  const int64_t strides[] = {x_row_stride, y_row_stride};
+  const void* const ptrs[] = {x, weight, y};
+  bool noop = false;
+  const int st = check_rows("mi355_rmsnorm_fwd", rows, n, strides, 2, ptrs, 3, x_dtype, w_dtype, y_dtype, &noop);
+  if (st != MI355_OK || noop) return st;
   return mi355::rmsnorm_launch(x, weight, y, rows, static_cast<int>(n), x_row_stride, y_row_stride,
                                eps, x_dtype, w_dtype, y_dtype, static_cast<hipStream_t>(stream));
+}
+
+MI355_EXPORT int mi355_add_rmsnorm_fwd(const void* x, const void* residual, const void* weight, void* y,
+                                       void* residual_out, int64_t rows, int64_t n, int64_t x_row_stride,
+                                       int64_t residual_row_stride, int64_t y_row_stride,
+                                       int64_t residual_out_row_stride, float eps, int x_dtype, int w_dtype,
+                                       int y_dtype, void* stream) {
+  mi355::g_error[0] = '\0';
+  const int64_t strides[] = {x_row_stride, residual_row_stride, y_row_stride, residual_out_row_stride};
+  const void* const ptrs[] = {x, residual, weight, y, residual_out};
+  bool noop = false;
+  const int st =
+      check_rows("mi355_add_rmsnorm_fwd", rows, n, strides, 4, ptrs, 5, x_dtype, w_dtype, y_dtype, &noop);
+  if (st != MI355_OK || noop) return st;
+  return mi355::add_rmsnorm_launch(x, residual, weight, y, residual_out, rows, static_cast<int>(n),
+                                   x_row_stride, residual_row_stride, y_row_stride, residual_out_row_stride, eps,
+                                   x_dtype, w_dtype, y_dtype, static_cast<hipStream_t>(stream));
 }
 
 MI355_EXPORT int mi355_silu_mul_fwd(const void* gate, const void* up, void* out, int64_t numel,

@@ -95,6 +95,16 @@ template <> __device__ __forceinline__ void store_elem<BF16>(void* p, int64_t i,
   static_cast<__bf16*>(p)[i] = static_cast<__bf16>(v);
 }
 
+// v rounded to T's precision (round-to-nearest-even) and widened back.
+template <typename T> __device__ __forceinline__ float quantize(float v);
+template <> __device__ __forceinline__ float quantize<F32>(float v) { return v; }
+template <> __device__ __forceinline__ float quantize<F16>(float v) {
+  return static_cast<float>(static_cast<_Float16>(v));
+}
+template <> __device__ __forceinline__ float quantize<BF16>(float v) {
+  return static_cast<float>(static_cast<__bf16>(v));
+}
+
 // A packet of `pack_width<T>` elements held as raw dwords.  `unpack` widens it
 // to fp32; `pack` rounds fp32 values into the packet once.
 template <typename T> struct Packet {

@@ -1,9 +1,15 @@
-// RMSNorm kernels for gfx950.
+// RMSNorm kernels for gfx950, optionally fused with the residual add that
+// precedes the norm in a decoder layer.
 //
 // Semantics follow the reference's Triton kernel
 // (src/kernels/fused_rmsnorm_triton.py:35-49): per row, the sum of squares is
 // accumulated in fp32 and divided by the true n, rstd = 1 / sqrt(var + eps),
 // and y = (x * rstd) * w is computed in fp32 and rounded once to y's type.
+// With ADD, the normalised row is h = x + residual, rounded to x's type as the
+// unfused `residual + hidden_states` of an HF decoder layer rounds it; h is
+// also written out (the next residual), and y = RMSNorm(h).  The add uses the
+// same row partition and reduction order, so the fused result is bit-identical
+// to the add followed by the plain kernel.
 //
 // Three kernels, chosen by the host launcher:
 //   rmsnorm_wave_rows   one wave64 per row, n <= 64 * VPL * W.  The row lives in
@@ -12,21 +18,35 @@
 //                       Each lane's slice of the weight is loaded into VGPRs
 //                       together with the row (an L2 hit after the first
 //                       wave) and reused for every row the wave visits.
-//   rmsnorm_block_rows  one workgroup per row for wider rows; same scheme, the
-//                       per-wave partial sums meet in LDS (double-buffered so
-//                       a row costs one barrier).
+//   rmsnorm_block_rows  one workgroup per row, for rows wider than a wave holds
+//                       comfortably; the per-wave partial sums meet in LDS
+//                       (double-buffered so a row costs one barrier).
 //   rmsnorm_generic     any n, alignment or dtype mix: scalar loads, two passes
-//                       over the row (the second pass re-reads x through L2).
+//                       over the row (the second pass re-reads the row through
+//                       L2).
 // Rows and the weight are read through buffer descriptors that span exactly
 // one row, so the packets past n need no lane branches, with the non-temporal
-// hint on x and y.  All three kernels stride over rows; the launcher normally
-// gives one wave (or workgroup) per row, which measured faster on MI355X than
-// a persistent grid.
+// hint on x, residual and the outputs.  All kernels stride over rows; the
+// launcher normally gives one wave (or workgroup) per row, which measured
+// faster on MI355X than a persistent grid.
 #pragma once
 
 #include "common.h"
 
 namespace mi355 {
+
+// Kernel parameters, passed by value.  r / ro / rs / ros are used with ADD only.
+struct RmsParams {
+  const void* x;   // [rows, xs]
+  const void* r;   // residual [rows, rs]
+  const void* w;   // [n]
+  void* y;         // [rows, ys]
+  void* ro;        // residual out (h = x + r) [rows, ros]
+  int64_t rows;
+  int n;
+  int64_t xs, rs, ys, ros;  // row strides, in elements
+  float eps;
+};
 
 // rstd exactly as the reference orders it: (sum / n) + eps, sqrt, reciprocal,
 // each rounded to fp32 (correctly rounded sqrt and division).
@@ -35,18 +55,37 @@ __device__ __forceinline__ float rms_rstd(float sumsq, int n, float eps) {
   return 1.0f / __builtin_sqrtf(var + eps);
 }
 
-// Per-lane work shared by the wave and workgroup kernels: load VPL packets of
-// row r (packet index p = slot + k * STRIDE) through buffer descriptors sized
-// to the row, so packets past n read 0 and their stores drop.
-template <typename TX, typename TW, int VPL, int STRIDE>
+// One lane's share of a row: VPL packets with packet index slot + k * stride,
+// through buffer descriptors sized to the row, so packets past n read 0 and
+// their stores drop.
+template <typename TX, typename TW, int VPL>
 struct RowSlice {
   static constexpr int W = pack_width<TX>::value;
   static constexpr uint32_t WB = W * sizeof(typename TW::bits);  // weight bytes per packet
   Packet<TX> xv[VPL];
 
-  __device__ __forceinline__ void load_x(rsrc_t rx, int slot) {
+  __device__ __forceinline__ void load_x(rsrc_t rx, int slot, int stride) {
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) xv[k].raw = buf_load16(rx, static_cast<uint32_t>(slot + k * STRIDE) * 16u);
+    for (int k = 0; k < VPL; ++k) xv[k].raw = buf_load16(rx, static_cast<uint32_t>(slot + k * stride) * 16u);
+  }
+  // xv <- round(xv + residual), the row the norm then runs on.
+  __device__ __forceinline__ void add_residual(rsrc_t rr, int slot, int stride) {
+    Packet<TX> rv[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) rv[k].raw = buf_load16(rr, static_cast<uint32_t>(slot + k * stride) * 16u);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      float a[W], b[W];
+      xv[k].unpack(a);
+      rv[k].unpack(b);
+#pragma unroll
+      for (int e = 0; e < W; ++e) a[e] += b[e];
+      xv[k].pack(a);
+    }
+  }
+  __device__ __forceinline__ void store_row(rsrc_t ro, int slot, int stride) const {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) buf_store16(ro, static_cast<uint32_t>(slot + k * stride) * 16u, xv[k].raw);
   }
   __device__ __forceinline__ float sumsq() const {
     float ss = 0.0f;
@@ -60,7 +99,8 @@ struct RowSlice {
     return ss;
   }
   template <typename TY>
-  __device__ __forceinline__ void store_y(rsrc_t ry, int slot, float rstd, BufChunk<TW, W> (&wv)[VPL]) {
+  __device__ __forceinline__ void store_y(rsrc_t ry, int slot, int stride, float rstd,
+                                          BufChunk<TW, W> (&wv)[VPL]) {
     constexpr uint32_t YB = W * sizeof(typename TY::bits);
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
@@ -71,115 +111,105 @@ struct RowSlice {
       xv[k].unpack(f);
 #pragma unroll
       for (int e = 0; e < W; ++e) o[e] = (f[e] * rstd) * wv[k].get(e);
-      buf_store_chunk<TY, W>(ry, static_cast<uint32_t>(slot + k * STRIDE) * YB, o);
+      buf_store_chunk<TY, W>(ry, static_cast<uint32_t>(slot + k * stride) * YB, o);
     }
   }
 };
 
+// Loads row r into `row` (adding the residual and storing h with ADD).
+template <typename TX, typename TW, int VPL, bool ADD>
+__device__ __forceinline__ void load_row(RowSlice<TX, TW, VPL>& row, const RmsParams& p, int64_t r, int slot,
+                                         int stride) {
+  using XB = typename TX::bits;
+  const uint32_t xbytes = static_cast<uint32_t>(p.n) * sizeof(XB);
+  row.load_x(make_rsrc(static_cast<const XB*>(p.x) + r * p.xs, xbytes), slot, stride);
+  if constexpr (ADD) {
+    row.add_residual(make_rsrc(static_cast<const XB*>(p.r) + r * p.rs, xbytes), slot, stride);
+    row.store_row(make_rsrc(static_cast<XB*>(p.ro) + r * p.ros, xbytes), slot, stride);
+  }
+}
+
 // One wave64 per row.  The grid is normally one-shot (a wave per row); the
 // row loop only repeats when the launcher caps the grid.
-template <typename TX, typename TW, typename TY, int VPL>
-__global__ __launch_bounds__(256) void rmsnorm_wave_rows(const void* __restrict__ x,
-                                                         const void* __restrict__ w,
-                                                         void* __restrict__ y, int64_t rows, int n,
-                                                         int64_t xs, int64_t ys, float eps) {
-  using S = RowSlice<TX, TW, VPL, 64>;
-  using WC = BufChunk<TW, S::W>;
+template <typename TX, typename TW, typename TY, int VPL, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_wave_rows(const RmsParams p) {
+  using S = RowSlice<TX, TW, VPL>;
   const int lane = threadIdx.x & 63;
   const int waves_per_block = blockDim.x >> 6;
-  const uint32_t xbytes = static_cast<uint32_t>(n) * sizeof(typename TX::bits);
-  const uint32_t ybytes = static_cast<uint32_t>(n) * sizeof(typename TY::bits);
-  const uint32_t wbytes = static_cast<uint32_t>(n) * sizeof(typename TW::bits);
-  const rsrc_t rw = make_rsrc(w, wbytes);
-  WC wv[VPL];
+  const uint32_t ybytes = static_cast<uint32_t>(p.n) * sizeof(typename TY::bits);
+
+  BufChunk<TW, S::W> wv[VPL];
+  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
 #pragma unroll
   for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(lane + 64 * k) * S::WB);
 
   // The wave's index in its workgroup is wave-uniform; readfirstlane says so,
-  // which keeps the row's buffer descriptor in SGPRs (no waterfall loop).
+  // which keeps the row's buffer descriptors in SGPRs (no waterfall loop).
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t step = static_cast<int64_t>(gridDim.x) * waves_per_block;
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; r < rows; r += step) {
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; r < p.rows; r += step) {
     S row;
-    row.load_x(make_rsrc(static_cast<const typename TX::bits*>(x) + r * xs, xbytes), lane);
-    const float rstd = rms_rstd(wave_allreduce_sum(row.sumsq()), n, eps);
-    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(y) + r * ys, ybytes), lane, rstd, wv);
+    load_row<TX, TW, VPL, ADD>(row, p, r, lane, 64);
+    const float rstd = rms_rstd(wave_allreduce_sum(row.sumsq()), p.n, p.eps);
+    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(p.y) + r * p.ys, ybytes), lane, 64,
+                             rstd, wv);
   }
 }
 
 // One workgroup per row, blockDim.x = 64 * (waves per row) <= 1024 threads;
 // lane t of the workgroup holds packets t + k * blockDim.x, k < VPL.  Used
-// for rows wider than one wave holds and, with VPL small, to spread a row over
-// several waves (fewer VGPRs and finer-grained work per wave).  Per-wave
+// for rows wider than one wave holds comfortably: spreading a row over
+// several waves keeps VGPRs low and the work per wave fine-grained.  Per-wave
 // partial sums meet in LDS, double-buffered so a row costs one barrier.
-template <typename TX, typename TW, typename TY, int VPL>
-__global__ __launch_bounds__(1024) void rmsnorm_block_rows(const void* __restrict__ x,
-                                                           const void* __restrict__ w,
-                                                           void* __restrict__ y, int64_t rows, int n,
-                                                           int64_t xs, int64_t ys, float eps) {
-  constexpr int W = pack_width<TX>::value;
-  constexpr uint32_t WB = W * sizeof(typename TW::bits);
-  constexpr uint32_t YB = W * sizeof(typename TY::bits);
+template <typename TX, typename TW, typename TY, int VPL, bool ADD>
+__global__ __launch_bounds__(1024) void rmsnorm_block_rows(const RmsParams p) {
+  using S = RowSlice<TX, TW, VPL>;
   __shared__ float partial[2][16];
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
   const int nwave = nthreads >> 6;
-  const uint32_t xbytes = static_cast<uint32_t>(n) * sizeof(typename TX::bits);
-  const uint32_t ybytes = static_cast<uint32_t>(n) * sizeof(typename TY::bits);
+  const uint32_t ybytes = static_cast<uint32_t>(p.n) * sizeof(typename TY::bits);
 
-  BufChunk<TW, W> wv[VPL];
-  const rsrc_t rw = make_rsrc(w, static_cast<uint32_t>(n) * sizeof(typename TW::bits));
+  BufChunk<TW, S::W> wv[VPL];
+  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
 #pragma unroll
-  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + nthreads * k) * WB);
+  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + nthreads * k) * S::WB);
 
   int buf = 0;
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    const rsrc_t rx = make_rsrc(static_cast<const typename TX::bits*>(x) + r * xs, xbytes);
-    Packet<TX> xv[VPL];
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) xv[k].raw = buf_load16(rx, static_cast<uint32_t>(tid + nthreads * k) * 16u);
-    float ss = 0.0f;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      float f[W];
-      xv[k].unpack(f);
-#pragma unroll
-      for (int e = 0; e < W; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
-    }
-    ss = wave_allreduce_sum(ss);
+  for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
+    S row;
+    load_row<TX, TW, VPL, ADD>(row, p, r, tid, nthreads);
+    const float ss = wave_allreduce_sum(row.sumsq());
     if ((tid & 63) == 0) partial[buf][tid >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
     for (int i = 0; i < nwave; ++i) tot += partial[buf][i];
     buf ^= 1;  // the next row writes the other buffer; this row's barrier orders the reuse
-    const float rstd = rms_rstd(tot, n, eps);
-
-    const rsrc_t ry = make_rsrc(static_cast<typename TY::bits*>(y) + r * ys, ybytes);
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      reg_barrier(xv[k].raw);
-      float f[W], o[W];
-      xv[k].unpack(f);
-#pragma unroll
-      for (int e = 0; e < W; ++e) o[e] = (f[e] * rstd) * wv[k].get(e);
-      buf_store_chunk<TY, W>(ry, static_cast<uint32_t>(tid + nthreads * k) * YB, o);
-    }
+    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(p.y) + r * p.ys, ybytes), tid, nthreads,
+                             rms_rstd(tot, p.n, p.eps), wv);
   }
 }
 
-template <typename TX, typename TW, typename TY>
-__global__ __launch_bounds__(256) void rmsnorm_generic(const void* __restrict__ x,
-                                                       const void* __restrict__ w,
-                                                       void* __restrict__ y, int64_t rows, int n,
-                                                       int64_t xs, int64_t ys, float eps) {
+// Scalar fallback, 256 threads per row.  Pass 1 forms the row (with ADD:
+// h = round(x + r), written to ro) and its sum of squares; pass 2 re-reads
+// the row -- from ro with ADD, since ro may alias r or x -- and writes y.
+// Each element is written and re-read by the same thread, with the
+// workgroup barrier (a workgroup-scope release/acquire) in between.
+template <typename TX, typename TW, typename TY, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_generic(const RmsParams p) {
   __shared__ float partial[2][4];
   const int tid = threadIdx.x;
   int buf = 0;
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    const int64_t xo = r * xs;
+  for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
+    const int64_t xo = r * p.xs;
+    const int64_t ho = r * p.ros;
     float ss = 0.0f;
-    for (int j = tid; j < n; j += 256) {
-      const float f = load_elem<TX>(x, xo + j);
+    for (int j = tid; j < p.n; j += 256) {
+      float f = load_elem<TX>(p.x, xo + j);
+      if constexpr (ADD) {
+        f = quantize<TX>(f + load_elem<TX>(p.r, r * p.rs + j));
+        store_elem<TX>(p.ro, ho + j, f);
+      }
       ss = __builtin_fmaf(f, f, ss);
     }
     ss = wave_allreduce_sum(ss);
@@ -187,11 +217,11 @@ __global__ __launch_bounds__(256) void rmsnorm_generic(const void* __restrict__ 
     __syncthreads();
     const float tot = (partial[buf][0] + partial[buf][1]) + (partial[buf][2] + partial[buf][3]);
     buf ^= 1;
-    const float rstd = rms_rstd(tot, n, eps);
-    const int64_t yo = r * ys;
-    for (int j = tid; j < n; j += 256) {
-      const float f = load_elem<TX>(x, xo + j);
-      store_elem<TY>(y, yo + j, (f * rstd) * load_elem<TW>(w, j));
+    const float rstd = rms_rstd(tot, p.n, p.eps);
+    const int64_t yo = r * p.ys;
+    for (int j = tid; j < p.n; j += 256) {
+      const float f = ADD ? load_elem<TX>(p.ro, ho + j) : load_elem<TX>(p.x, xo + j);
+      store_elem<TY>(p.y, yo + j, (f * rstd) * load_elem<TW>(p.w, j));
     }
   }
 }

@@ -17,19 +17,29 @@ Same surface and behaviour as the reference (:29-99):
 * ``patch_model_with_fused_kernels`` returns ``{"rmsnorm": n, "mlp": n}``; an
   unrecognised architecture silently replaces nothing, so callers check
   the counts.
+
+Beyond the reference: ``fuse_residual=True`` (off by default, so the default
+behaviour and return value are the reference's) also replaces each decoder
+layer by ``FusedDecoderLayer``, which runs the post-attention residual add
+inside the post-attention RMSNorm (``fused_add_rmsnorm``) -- the "fused
+RMSNorm + residual" the reference plans (docs/architecture-cuda.md:94).  The
+result is bit-identical to the unfused layer with the fused kernels; the
+count appears as ``"add_rmsnorm"``.
 """
 from __future__ import annotations
 
 import torch
 
-from ..kernels.fused_rmsnorm_hip import fused_rmsnorm
+from ..kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm
 from ..kernels.fused_swiglu_hip import fused_silu_mul
 
-__all__ = ["RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES", "FusedRMSNorm", "FusedMLP",
-           "patch_model_with_fused_kernels"]
+__all__ = ["RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES", "DECODER_LAYER_CLASS_NAMES", "FusedRMSNorm", "FusedMLP",
+           "FusedDecoderLayer", "patch_model_with_fused_kernels"]
 
 RMSNORM_CLASS_NAMES = {"Qwen2RMSNorm", "LlamaRMSNorm", "MistralRMSNorm", "RMSNorm"}
 MLP_CLASS_NAMES = {"Qwen2MLP", "LlamaMLP", "MistralMLP"}
+DECODER_LAYER_CLASS_NAMES = {"Qwen2DecoderLayer", "LlamaDecoderLayer", "MistralDecoderLayer"}
+_DECODER_LAYER_PARTS = ("self_attn", "mlp", "input_layernorm", "post_attention_layernorm")
 
 
 class FusedRMSNorm(torch.nn.Module):
@@ -63,11 +73,51 @@ class FusedMLP(torch.nn.Module):
         return self.down_proj(activated)
 
 
+class FusedDecoderLayer(torch.nn.Module):
+    """A pre-norm decoder layer (Qwen2 / Llama / Mistral layout) whose
+    post-attention residual add runs inside the post-attention RMSNorm.
+
+    Reuses the layer's own ``self_attn``, ``mlp``, ``input_layernorm`` and
+    ``post_attention_layernorm`` modules (already replaced by the fused ones
+    if the model was patched) and follows HF's decoder-layer forward:
+    input norm -> attention -> residual add + post-attention norm (one fused
+    kernel here) -> MLP -> residual add."""
+
+    def __init__(self, orig_layer: torch.nn.Module):
+        super().__init__()
+        for name in _DECODER_LAYER_PARTS:
+            setattr(self, name, getattr(orig_layer, name))
+        # plain attributes callers may read from a layer (e.g. attention_type)
+        for key, val in vars(orig_layer).items():
+            if not key.startswith("_") and not isinstance(val, torch.nn.Module) and not hasattr(self, key):
+                setattr(self, key, val)
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None, past_key_values=None,
+                use_cache=False, position_embeddings=None, **kwargs) -> torch.Tensor:
+        residual = hidden_states
+        hidden_states = self.input_layernorm(hidden_states)
+        hidden_states, _ = self.self_attn(
+            hidden_states=hidden_states,
+            attention_mask=attention_mask,
+            position_ids=position_ids,
+            past_key_values=past_key_values,
+            use_cache=use_cache,
+            position_embeddings=position_embeddings,
+            **kwargs,
+        )
+        norm = self.post_attention_layernorm
+        hidden_states, residual = fused_add_rmsnorm(hidden_states, residual, norm.weight, norm.variance_epsilon)
+        hidden_states = self.mlp(hidden_states)
+        return residual + hidden_states
+
+
 def patch_model_with_fused_kernels(model: torch.nn.Module, patch_norm: bool = True,
-                                   patch_mlp: bool = True) -> dict:
+                                   patch_mlp: bool = True, fuse_residual: bool = False) -> dict:
     """Replace matching RMSNorm and/or MLP child modules in place (setattr on
     the parent).  Returns ``{"rmsnorm": count, "mlp": count}``.
-    ``patch_norm`` / ``patch_mlp`` enable each kernel independently."""
+    ``patch_norm`` / ``patch_mlp`` enable each kernel independently.
+    ``fuse_residual`` additionally replaces matching decoder layers by
+    ``FusedDecoderLayer`` and adds ``"add_rmsnorm": count`` to the result."""
     counts = {"rmsnorm": 0, "mlp": 0}
     for parent in list(model.modules()):
         for child_name, child in list(parent.named_children()):
@@ -80,4 +130,12 @@ def patch_model_with_fused_kernels(model: torch.nn.Module, patch_norm: bool = Tr
                     hasattr(child, attr) for attr in ("gate_proj", "up_proj", "down_proj")):
                 setattr(parent, child_name, FusedMLP(child))
                 counts["mlp"] += 1
+    if fuse_residual:
+        counts["add_rmsnorm"] = 0
+        for parent in list(model.modules()):
+            for child_name, child in list(parent.named_children()):
+                if child.__class__.__name__ in DECODER_LAYER_CLASS_NAMES and all(
+                        hasattr(child, part) for part in _DECODER_LAYER_PARTS):
+                    setattr(parent, child_name, FusedDecoderLayer(child))
+                    counts["add_rmsnorm"] += 1
     return counts

@@ -13,6 +13,11 @@ rstd = 1/sqrt(sum/n + eps), y = (x * rstd) * w in fp32, rounded once.
 
 ``naive_rmsnorm_reference`` is the reference's unfused HF formula (:74-82),
 kept for callers that compare against it.
+
+``fused_add_rmsnorm`` goes one step past the reference: the residual add that
+precedes the norm in a decoder layer (``hidden = residual + attn_out`` then
+``post_attention_layernorm(hidden)``) in the same pass, which the reference
+plans as "fused RMSNorm + residual" (docs/architecture-cuda.md:94).
 """
 from __future__ import annotations
 
@@ -20,7 +25,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["fused_rmsnorm", "naive_rmsnorm_reference"]
+__all__ = ["fused_rmsnorm", "fused_add_rmsnorm", "naive_rmsnorm_reference"]
 
 
 def fused_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
@@ -53,6 +58,49 @@ def fused_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> t
     else:
         _launch(x2, w, out, M, N, eps, x_code, dev)
     return out.reshape(orig_shape)
+
+
+def _rows(t: torch.Tensor, N: int) -> torch.Tensor:
+    """(M, N) view of t whose rows are contiguous (copying only if needed)."""
+    t2 = t.reshape(-1, N)
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < N):
+        t2 = t2.contiguous()
+    return t2
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6):
+    """Residual add fused with RMSNorm: returns ``(rmsnorm(h), h)`` with
+    ``h = residual + x`` rounded to x's dtype -- exactly what
+    ``h = residual + x; y = fused_rmsnorm(h, weight, eps)`` returns, in one
+    pass (read x and residual, write h and y).  x and residual have the same
+    shape and dtype; normalises over the last dimension."""
+    assert x.is_cuda and residual.is_cuda and weight.is_cuda, "x, residual and weight must be ROCm GPU tensors"
+    assert x.shape == residual.shape, f"shape mismatch {tuple(x.shape)} vs {tuple(residual.shape)}"
+    assert x.dtype == residual.dtype, f"dtype mismatch {x.dtype} vs {residual.dtype}"
+    orig_shape = x.shape
+    N = orig_shape[-1]
+    assert weight.shape == (N,), f"weight shape {tuple(weight.shape)} != ({N},)"
+    assert x.dtype in _lib.DTYPE_CODE and weight.dtype in _lib.DTYPE_CODE, (
+        f"unsupported dtypes x={x.dtype} weight={weight.dtype} (fp16, bf16, fp32)")
+    assert weight.device == x.device == residual.device, "x, residual and weight must be on the same device"
+    x2 = _rows(x, N)
+    r2 = _rows(residual, N)
+    M = x2.shape[0]
+    w = weight if weight.stride(0) == 1 else weight.contiguous()
+    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    h = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    if M and N:
+        code = _lib.DTYPE_CODE[x.dtype]
+        dev = x.device
+        args = (x2.data_ptr(), r2.data_ptr(), w.data_ptr(), out.data_ptr(), h.data_ptr(), M, N,
+                x2.stride(0) if M > 1 else N, r2.stride(0) if M > 1 else N, N, N, float(eps),
+                code, _lib.DTYPE_CODE[w.dtype], code)
+        if dev.index is not None and dev.index != torch.cuda.current_device():
+            with torch.cuda.device(dev):
+                _lib.add_rmsnorm_fwd(*args, _lib.stream_handle(dev))
+        else:
+            _lib.add_rmsnorm_fwd(*args, _lib.stream_handle(dev))
+    return out.reshape(orig_shape), h.reshape(orig_shape)
 
 
 def _launch(x2, w, out, M, N, eps, x_code, dev):

@@ -34,6 +34,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 enum { OR_F32 = 0, OR_F16 = 1, OR_BF16 = 2 };
@@ -178,6 +179,31 @@ int oracle_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t 
     }
   }
   return 0;
+}
+
+/*
+ * Residual add + RMSNorm (the fused kernel beyond the reference, restating
+ * the decoder layer's `hidden = residual + attn_out` followed by the norm):
+ * h = round_xdt(x + r) in fp32, written to h[rows, n]; y = RMSNorm(h) in
+ * `mode` as oracle_rmsnorm.  mutate 1: normalise the unrounded fp32 sum;
+ * mutate 2: subtract the residual.  Returns 0, or -1 on a bad argument.
+ */
+int oracle_add_rmsnorm(const void* x, const void* r, const void* w, void* y, void* h, int64_t rows, int64_t n,
+                       float eps, int xdt, int wdt, int ydt, int mode, int mutate) {
+  if (!valid_dt(xdt) || !valid_dt(wdt) || !valid_dt(ydt) || n < 1 || rows < 0) return -1;
+  for (int64_t i = 0; i < rows * n; ++i) {
+    const float a = load_f(x, i, xdt);
+    const float b = load_f(r, i, xdt);
+    store_f(h, i, xdt, mutate == 2 ? a - b : a + b);
+  }
+  if (mutate != 1) return oracle_rmsnorm(h, w, y, rows, n, n, n, eps, xdt, wdt, ydt, mode, 0);
+  /* planted mistake: the norm sees the fp32 sum before rounding */
+  float* tmp = (float*)malloc((size_t)(rows * n) * sizeof(float));
+  if (!tmp) return -1;
+  for (int64_t i = 0; i < rows * n; ++i) tmp[i] = load_f(x, i, xdt) + load_f(r, i, xdt);
+  const int st = oracle_rmsnorm(tmp, w, y, rows, n, n, n, eps, OR_F32, wdt, ydt, mode, 0);
+  free(tmp);
+  return st;
 }
 
 /* fp64 brute force: y[r*n + j] = x * w / sqrt(mean(x^2) + eps), all in double. */

@@ -16,6 +16,8 @@ Contents
       (src/kernels/fused_rmsnorm_triton.py:74-82,
       src/kernels/fused_swiglu_triton.py:56-59);
     - :func:`rmsnorm_f64` / :func:`silu_mul_f64` are fp64 brute force.
+* :func:`add_rmsnorm`: the residual add + RMSNorm fusion (beyond the
+  reference): h = round(x + residual), then RMSNorm(h) in either mode;
 * :func:`naive_rmsnorm_torch` / :func:`naive_silu_mul_torch`: the reference's
   naive PyTorch path restated as the same torch op sequence, which bench.py
   times on the host cores as the CPU baseline.
@@ -77,6 +79,8 @@ def lib() -> ctypes.CDLL:
         vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
         L.oracle_rmsnorm.argtypes = [vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, i32, i32, i32, i32, i32]
         L.oracle_rmsnorm.restype = i32
+        L.oracle_add_rmsnorm.argtypes = [vp, vp, vp, vp, vp, i64, i64, ctypes.c_float, i32, i32, i32, i32, i32]
+        L.oracle_add_rmsnorm.restype = i32
         L.oracle_rmsnorm_f64.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.c_double, i32, i32]
         L.oracle_rmsnorm_f64.restype = i32
         L.oracle_silu_mul.argtypes = [vp, vp, vp, i64, i32, i32, i32, i32]
@@ -132,6 +136,27 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6, *, xdt: str, wdt: s
     if st != 0:
         raise ValueError("oracle_rmsnorm rejected its arguments")
     return y
+
+
+def add_rmsnorm(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float = 1e-6, *, xdt: str, wdt: str,
+                ydt: str | None = None, mode: str = "triton", mutate: str | None = None):
+    """Residual add + RMSNorm: returns (y, h), h = round_xdt(x + r), y = RMSNorm(h)."""
+    x = _arr(x, xdt)
+    r = _arr(r, xdt)
+    w = _arr(w, wdt)
+    if x.ndim != 2 or r.shape != x.shape or w.shape != (x.shape[1],):
+        raise ValueError(f"bad shapes x={x.shape} r={r.shape} w={w.shape}")
+    if ydt is None:
+        ydt = xdt if mode == "triton" else hf_out_dtype(xdt, wdt)
+    rows, n = x.shape
+    y = np.empty((rows, n), dtype=_np_dtype(ydt))
+    h = np.empty((rows, n), dtype=_np_dtype(xdt))
+    mut = {None: 0, "no_round": 1, "subtract": 2}[mutate]
+    st = lib().oracle_add_rmsnorm(_ptr(x), _ptr(r), _ptr(w), _ptr(y), _ptr(h), rows, n, float(np.float32(eps)),
+                                  DT_CODE[xdt], DT_CODE[wdt], DT_CODE[ydt], MODE_CODE[mode], mut)
+    if st != 0:
+        raise ValueError("oracle_add_rmsnorm rejected its arguments")
+    return y, h
 
 
 def rmsnorm_f64(x: np.ndarray, w: np.ndarray, eps: float = 1e-6, *, xdt: str, wdt: str) -> np.ndarray:

@@ -135,3 +135,28 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    ((P, P, P, P, P, 4, 64, 64, 64, 64, 64, 1e-6, 1, 1, 7), -1, "unknown dtype"),
+    ((P, P, P, P, P, 4, 64, 64, 64, 64, 64, 1e-6, 2, 2, 1), -2, "y dtype"),
+    ((P, 0, P, P, P, 4, 64, 64, 64, 64, 64, 1e-6, 1, 1, 1), -1, "null pointer"),
+    ((P, P, P, P, 0, 4, 64, 64, 64, 64, 64, 1e-6, 1, 1, 1), -1, "null pointer"),
+    ((P, P, P, P, P, 4, 64, 64, 63, 64, 64, 1e-6, 1, 1, 1), -1, "row strides"),
+    ((P, P, P, P, P, 4, 64, 64, 64, 64, 8, 1e-6, 1, 1, 1), -1, "row strides"),
+    ((P, P, P, P, P, -2, 64, 64, 64, 64, 64, 1e-6, 1, 1, 1), -1, "rows"),
+])
+def test_add_rmsnorm_abi_rejects(lib, args, code, msg):
+    st = lib.mi355_add_rmsnorm_fwd(*args, None)
+    assert st == code
+    assert msg in lib.mi355_last_error().decode()
+
+
+def test_add_rmsnorm_abi_zero_rows_is_noop(lib):
+    assert lib.mi355_add_rmsnorm_fwd(0, 0, 0, 0, 0, 0, 64, 64, 64, 64, 64, 1e-6, 1, 1, 1, None) == 0
+
+
+def test_fused_add_rmsnorm_asserts_on_host_tensors(pkg):
+    x = torch.randn(4, 64, dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        pkg.fused_add_rmsnorm(x, x, torch.ones(64, dtype=torch.float16))

@@ -239,3 +239,38 @@ def test_planted_silu_mistake_is_caught(orc, mutate):
     hf = orc.silu_mul(storage(g), storage(u), idt="f16", mode="hf", mutate=mutate)
     d = orc.ulp_diff16(hf, storage(want))
     assert e16 > 0.5 + 1e-3 or e32 >= 2e-6 or d.max() > 1, f"planted mistake {mutate} was not caught"
+
+
+# --------------------------------------------- residual add + RMSNorm (fused)
+
+def _add_rms_vs_torch(orc, dt, n, mutate=None, rows=16, seed=40):
+    x = randn((rows, n), seed, dt)
+    r = randn((rows, n), seed + 1, dt, std=4.0)
+    w = randn((n,), seed + 2, dt, mean=1.0, std=0.1)
+    h_t = r + x                               # torch's CPU add, rounded to dt
+    y_t = _hf_rmsnorm(h_t, w, 1e-6)           # transformers' norm of the rounded sum
+    name = {F16: "f16", BF16: "bf16"}[dt]
+    y, h = orc.add_rmsnorm(storage(x), storage(r), storage(w), 1e-6, xdt=name, wdt=name, mode="hf", mutate=mutate)
+    dh = orc.ulp_diff16(h, storage(h_t))
+    dy = orc.ulp_diff16(y, storage(y_t))
+    yt, _ = orc.add_rmsnorm(storage(x), storage(r), storage(w), 1e-6, xdt=name, wdt=name, ydt="f32", mutate=mutate)
+    ref = orc.rmsnorm_f64(storage(h_t), storage(w), 1e-6, xdt=name, wdt=name)
+    rel = float(np.max(np.abs(yt.astype(np.float64) - ref) / np.maximum(np.abs(ref), 1e-30)))
+    return int(dh.max()), int(dy.max()), float((dy > 0).mean()), rel
+
+
+@pytest.mark.parametrize("dt,n", [(F16, 1536), (BF16, 3584), (F16, 100)])
+def test_oracle_add_rmsnorm_matches_torch_and_transformers(orc, dt, n):
+    """h equals torch's own fp16/bf16 add bit for bit; y equals transformers'
+    Qwen2RMSNorm of that sum (HF mode) to <= 1 ulp; the Triton-mode fp32 value
+    is within fp32 noise of fp64 on the rounded sum."""
+    dh, dy, frac, rel = _add_rms_vs_torch(orc, dt, n)
+    assert dh == 0
+    assert dy <= 1 and frac < 1e-3
+    assert rel < 2e-6
+
+
+@pytest.mark.parametrize("mutate", ["no_round", "subtract"])
+def test_planted_add_rmsnorm_mistake_is_caught(orc, mutate):
+    dh, dy, frac, rel = _add_rms_vs_torch(orc, F16, 1536, mutate=mutate)
+    assert dh > 0 or dy > 1 or frac >= 1e-3 or rel >= 2e-6, f"planted mistake {mutate} was not caught"

@@ -88,3 +88,20 @@ def test_matching_requires_attributes(pkg):
     root.norm = RMSNorm()
     root.mlp = Qwen2MLP()
     assert pkg.patch_model_with_fused_kernels(root) == {"rmsnorm": 0, "mlp": 0}
+
+
+def test_fuse_residual_replaces_decoder_layers(pkg):
+    model = _qwen2(layers=28)
+    attn0 = model.model.layers[0].self_attn
+    counts = pkg.patch_model_with_fused_kernels(model, fuse_residual=True)
+    assert counts == {"rmsnorm": 57, "mlp": 28, "add_rmsnorm": 28}
+    layer = model.model.layers[0]
+    assert isinstance(layer, pkg.FusedDecoderLayer)
+    assert layer.self_attn is attn0
+    assert isinstance(layer.input_layernorm, pkg.FusedRMSNorm)
+    assert isinstance(layer.post_attention_layernorm, pkg.FusedRMSNorm)
+    assert isinstance(layer.mlp, pkg.FusedMLP)
+    assert len(model.model.layers) == 28
+    # default call keeps the reference's return value exactly
+    assert pkg.patch_model_with_fused_kernels(_qwen2(layers=2)) == {"rmsnorm": 5, "mlp": 2}
+    assert pkg.DECODER_LAYER_CLASS_NAMES == {"Qwen2DecoderLayer", "LlamaDecoderLayer", "MistralDecoderLayer"}
