@@ -686,12 +686,15 @@ def bench_e2e(args):
             torch.cuda.synchronize()
             return s0.elapsed_time(s1), (gen_len - 1) / (d0.elapsed_time(d1) / 1e3)
 
+    def prompt(S):
+        g = torch.Generator()
+        g.manual_seed(S)
+        return torch.randint(0, cfg.vocab_size, (1, S), generator=g).to(dev)
+
     def measure(tag):
         res = {}
         for S in args.seq_lens:
-            g = torch.Generator()
-            g.manual_seed(S)
-            ids = torch.randint(0, cfg.vocab_size, (1, S), generator=g).to(dev)
+            ids = prompt(S)
             for _ in range(2):
                 run(ids, args.gen_len)
             t = [run(ids, args.gen_len) for _ in range(args.trials)]
@@ -699,19 +702,57 @@ def bench_e2e(args):
             log(f"  {tag} seq {S}: TTFT {res[S][0]:.2f} ms, decode {res[S][1]:.1f} tok/s")
         return res
 
+    def graphed_decode_tok_s(S=512, new=64):
+        """Decode tok/s with the whole decode step replayed as one HIP graph
+        (GraphedGreedyDecoder over a StaticCache), batch 1."""
+        ids = prompt(S)
+        dec = pkg.GraphedGreedyDecoder(model, 1, S + new + 8)
+        dec.generate(ids, new)  # capture
+        times = []
+        for _ in range(args.trials):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            dec.generate(ids, 2)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            dec.generate(ids, new)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            times.append(((t2 - t1) - (t1 - t0)) / (new - 2))  # subtract prefill + first step
+        return 1.0 / statistics.median(times)
+
+    # warm every shape once before timing anything
+    for S in args.seq_lens:
+        run(prompt(S), 4)
     before = measure("before")
+    graph_before = graphed_decode_tok_s()
+    log(f"  before, graphed decode: {graph_before:.1f} tok/s")
     counts = pkg.patch_model_with_fused_kernels(model)
     log(f"patched {counts}")
     after = measure("after")
+    graph_after = graphed_decode_tok_s()
+    log(f"  after, graphed decode: {graph_after:.1f} tok/s")
+    counts_fr = pkg.patch_model_with_fused_kernels(model, fuse_residual=True)
+    log(f"fused residual {counts_fr}")
+    fused_res = measure("after+fuse_residual")
+    graph_fr = graphed_decode_tok_s()
+    log(f"  after+fuse_residual, graphed decode: {graph_fr:.1f} tok/s")
     rows = []
     for S in args.seq_lens:
         rows.append({"seq_len": S, "before_ttft_ms": round(before[S][0], 3), "after_ttft_ms": round(after[S][0], 3),
                      "ttft_speedup": round(before[S][0] / after[S][0], 4),
                      "before_decode_tok_s": round(before[S][1], 2), "after_decode_tok_s": round(after[S][1], 2),
                      "decode_speedup": round(after[S][1] / before[S][1], 4)})
+    for row in rows:
+        S = row["seq_len"]
+        row["fuse_residual_ttft_ms"] = round(fused_res[S][0], 3)
+        row["fuse_residual_decode_tok_s"] = round(fused_res[S][1], 2)
     print(json.dumps({"metric": "e2e TTFT / decode tok/s speedup from patch_model_with_fused_kernels",
                       "model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16, sdpa, batch 1",
-                      "gen_len": args.gen_len, "trials": args.trials, "patched": counts, "results": rows}),
+                      "gen_len": args.gen_len, "trials": args.trials, "patched": counts, "results": rows,
+                      "graphed_decode_tok_s": {"seq_len": 512, "unpatched": round(graph_before, 1),
+                                               "patched": round(graph_after, 1),
+                                               "patched_fuse_residual": round(graph_fr, 1)}}),
           flush=True)
 
 

@@ -81,9 +81,29 @@ def check(fn: str, status: int) -> None:
         raise KernelError(fn, status, load().mi355_last_error().decode(errors="replace"))
 
 
-def stream_handle(device: torch.device) -> int:
-    """hipStream_t of torch's current stream on ``device`` (as an integer)."""
-    return torch.cuda.current_stream(device).cuda_stream
+_raw_stream = torch._C._cuda_getCurrentRawStream   # device index -> hipStream_t as int
+_current_device = torch._C._cuda_getDevice
+
+
+def stream_handle(device) -> int:
+    """hipStream_t of torch's current stream on ``device`` (torch.device or
+    index), as an integer."""
+    idx = device if isinstance(device, int) else device.index
+    return _raw_stream(_current_device() if idx is None else idx)
+
+
+def launch(fn: str, device_index: int, *args) -> None:
+    """Calls C-ABI entry point `fn` with `args` plus torch's current stream on
+    `device_index`, with that device current; raises KernelError on failure.
+    The hot path of the Python launchers (a few hundred ns above the call)."""
+    f = getattr(load(), fn)
+    if device_index == _current_device():
+        st = f(*args, _raw_stream(device_index))
+    else:
+        with torch.cuda.device(device_index):
+            st = f(*args, _raw_stream(device_index))
+    if st != 0:
+        check(fn, st)
 
 
 def rmsnorm_fwd(x_ptr: int, w_ptr: int, y_ptr: int, rows: int, n: int, x_row_stride: int,

@@ -28,44 +28,46 @@ from .. import _lib
 __all__ = ["fused_rmsnorm", "fused_add_rmsnorm", "naive_rmsnorm_reference"]
 
 
+_CODE = _lib.DTYPE_CODE
+
+
+def _rows(t: torch.Tensor, N: int):
+    """(rows view, row count, row stride) of t with contiguous rows, copying
+    only when the last dimension itself is strided."""
+    if t.is_contiguous():
+        return t, (t.numel() // N if N else 0), N
+    t2 = t.reshape(-1, N)
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < N):
+        t2 = t2.contiguous()
+    M = t2.shape[0]
+    # Rows only need to be contiguous along the hidden dimension: a row-strided
+    # view is passed with its stride instead of being copied.
+    return t2, M, (t2.stride(0) if M > 1 else N)
+
+
+def _empty_like_rows(x: torch.Tensor) -> torch.Tensor:
+    return torch.empty_like(x) if x.is_contiguous() else torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
 def fused_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """Drop-in replacement for HF's RMSNorm.forward.  x: (..., hidden_size),
     weight: (hidden_size,).  Normalizes over the last dimension."""
     assert x.is_cuda and weight.is_cuda, "x and weight must be ROCm GPU tensors"
-    orig_shape = x.shape
-    N = orig_shape[-1]
+    N = x.shape[-1]
     assert weight.shape == (N,), f"weight shape {tuple(weight.shape)} != ({N},)"
-    assert x.dtype in _lib.DTYPE_CODE and weight.dtype in _lib.DTYPE_CODE, (
+    code, wcode = _CODE.get(x.dtype), _CODE.get(weight.dtype)
+    assert code is not None and wcode is not None, (
         f"unsupported dtypes x={x.dtype} weight={weight.dtype} (fp16, bf16, fp32)")
-    assert weight.device == x.device, "x and weight must be on the same device"
-
-    x2 = x.reshape(-1, N)
-    M = x2.shape[0]
-    # Rows only need to be contiguous along the hidden dimension: a row-strided
-    # view is passed with its stride instead of being copied.
-    if x2.stride(-1) != 1 or (M > 1 and x2.stride(0) < N):
-        x2 = x2.contiguous()
-    w = weight if weight.stride(0) == 1 else weight.contiguous()
-    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
-    if M == 0 or N == 0:
-        return out.reshape(orig_shape)
-
-    x_code = _lib.DTYPE_CODE[x.dtype]
-    dev = x.device
-    if dev.index is not None and dev.index != torch.cuda.current_device():
-        with torch.cuda.device(dev):
-            _launch(x2, w, out, M, N, eps, x_code, dev)
-    else:
-        _launch(x2, w, out, M, N, eps, x_code, dev)
-    return out.reshape(orig_shape)
-
-
-def _rows(t: torch.Tensor, N: int) -> torch.Tensor:
-    """(M, N) view of t whose rows are contiguous (copying only if needed)."""
-    t2 = t.reshape(-1, N)
-    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < N):
-        t2 = t2.contiguous()
-    return t2
+    dev = x.get_device()
+    assert weight.get_device() == dev, "x and weight must be on the same device"
+    x2, M, xs = _rows(x, N)
+    if weight.stride(0) != 1:
+        weight = weight.contiguous()
+    out = _empty_like_rows(x)
+    if M and N:
+        _lib.launch("mi355_rmsnorm_fwd", dev, x2.data_ptr(), weight.data_ptr(), out.data_ptr(), M, N, xs, N,
+                    eps, code, wcode, code)
+    return out
 
 
 def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6):
@@ -77,36 +79,24 @@ def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Ten
     assert x.is_cuda and residual.is_cuda and weight.is_cuda, "x, residual and weight must be ROCm GPU tensors"
     assert x.shape == residual.shape, f"shape mismatch {tuple(x.shape)} vs {tuple(residual.shape)}"
     assert x.dtype == residual.dtype, f"dtype mismatch {x.dtype} vs {residual.dtype}"
-    orig_shape = x.shape
-    N = orig_shape[-1]
+    N = x.shape[-1]
     assert weight.shape == (N,), f"weight shape {tuple(weight.shape)} != ({N},)"
-    assert x.dtype in _lib.DTYPE_CODE and weight.dtype in _lib.DTYPE_CODE, (
+    code, wcode = _CODE.get(x.dtype), _CODE.get(weight.dtype)
+    assert code is not None and wcode is not None, (
         f"unsupported dtypes x={x.dtype} weight={weight.dtype} (fp16, bf16, fp32)")
-    assert weight.device == x.device == residual.device, "x, residual and weight must be on the same device"
-    x2 = _rows(x, N)
-    r2 = _rows(residual, N)
-    M = x2.shape[0]
-    w = weight if weight.stride(0) == 1 else weight.contiguous()
-    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
-    h = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    dev = x.get_device()
+    assert residual.get_device() == dev and weight.get_device() == dev, (
+        "x, residual and weight must be on the same device")
+    x2, M, xs = _rows(x, N)
+    r2, _, rs = _rows(residual, N)
+    if weight.stride(0) != 1:
+        weight = weight.contiguous()
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     if M and N:
-        code = _lib.DTYPE_CODE[x.dtype]
-        dev = x.device
-        args = (x2.data_ptr(), r2.data_ptr(), w.data_ptr(), out.data_ptr(), h.data_ptr(), M, N,
-                x2.stride(0) if M > 1 else N, r2.stride(0) if M > 1 else N, N, N, float(eps),
-                code, _lib.DTYPE_CODE[w.dtype], code)
-        if dev.index is not None and dev.index != torch.cuda.current_device():
-            with torch.cuda.device(dev):
-                _lib.add_rmsnorm_fwd(*args, _lib.stream_handle(dev))
-        else:
-            _lib.add_rmsnorm_fwd(*args, _lib.stream_handle(dev))
-    return out.reshape(orig_shape), h.reshape(orig_shape)
-
-
-def _launch(x2, w, out, M, N, eps, x_code, dev):
-    _lib.rmsnorm_fwd(x2.data_ptr(), w.data_ptr(), out.data_ptr(), M, N,
-                     x2.stride(0) if M > 1 else N, N, float(eps),
-                     x_code, _lib.DTYPE_CODE[w.dtype], x_code, _lib.stream_handle(dev))
+        _lib.launch("mi355_add_rmsnorm_fwd", dev, x2.data_ptr(), r2.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                    h.data_ptr(), M, N, xs, rs, N, N, eps, code, wcode, code)
+    return out, h
 
 
 def naive_rmsnorm_reference(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

@@ -22,39 +22,36 @@ from .. import _lib
 __all__ = ["fused_silu_mul", "naive_silu_mul_reference"]
 
 
+_CODE = _lib.DTYPE_CODE
+
+
 def fused_silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """Fused silu(gate) * up.  Purely elementwise -- shapes must match
     exactly, any shape is fine since the kernel treats memory as flat."""
     assert gate.shape == up.shape, f"shape mismatch {tuple(gate.shape)} vs {tuple(up.shape)}"
     assert gate.is_cuda and up.is_cuda, "gate and up must be ROCm GPU tensors"
-    assert gate.dtype in _lib.DTYPE_CODE and up.dtype in _lib.DTYPE_CODE, (
+    code, ucode = _CODE.get(gate.dtype), _CODE.get(up.dtype)
+    assert code is not None and ucode is not None, (
         f"unsupported dtypes gate={gate.dtype} up={up.dtype} (fp16, bf16, fp32)")
-    assert gate.device == up.device, "gate and up must be on the same device"
+    dev = gate.get_device()
+    assert up.get_device() == dev, "gate and up must be on the same device"
 
-    out_dtype = gate.dtype
-    if up.dtype != gate.dtype:
+    if code != ucode:
         # The reference widens each input to fp32 separately; widening both
         # here is exact, and the fp32 result is rounded once below.
         gate_c = gate.contiguous().to(torch.float32)
         up_c = up.contiguous().to(torch.float32)
+        code = _CODE[torch.float32]
     else:
-        gate_c = gate.contiguous()
-        up_c = up.contiguous()
-    out = torch.empty(gate_c.shape, dtype=gate_c.dtype, device=gate.device)
+        gate_c = gate if gate.is_contiguous() else gate.contiguous()
+        up_c = up if up.is_contiguous() else up.contiguous()
+    out = torch.empty_like(gate_c)
     n = gate_c.numel()
     if n:
-        dev = gate.device
-        code = _lib.DTYPE_CODE[gate_c.dtype]
-        if dev.index is not None and dev.index != torch.cuda.current_device():
-            with torch.cuda.device(dev):
-                _lib.silu_mul_fwd(gate_c.data_ptr(), up_c.data_ptr(), out.data_ptr(), n, code, code,
-                                  _lib.stream_handle(dev))
-        else:
-            _lib.silu_mul_fwd(gate_c.data_ptr(), up_c.data_ptr(), out.data_ptr(), n, code, code,
-                              _lib.stream_handle(dev))
-    if out.dtype != out_dtype:
-        out = out.to(out_dtype)
-    return out.reshape(gate.shape)
+        _lib.launch("mi355_silu_mul_fwd", dev, gate_c.data_ptr(), up_c.data_ptr(), out.data_ptr(), n, code, code)
+    if out.dtype != gate.dtype:
+        out = out.to(gate.dtype)
+    return out.view(gate.shape)
 
 
 def naive_silu_mul_reference(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
