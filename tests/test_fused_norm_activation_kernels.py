@@ -312,3 +312,42 @@ def test_preconditions_match_reference(pkg, cuda):
         pkg.fused_rmsnorm(x, torch.ones(64, dtype=F16))  # weight on the host
     with pytest.raises(AssertionError):
         pkg.fused_silu_mul(x, torch.zeros((4, 65), dtype=F16, device=cuda))
+
+
+# ------------------------------------------------------- beyond 4 GiB / max sizes
+
+def test_silu_mul_beyond_4gib(pkg, orc, cuda):
+    """numel > 2^31 fp16 elements (each tensor > 4 GiB): int64 packet indices
+    and per-chunk descriptors rebased past the 2^32-byte mark.  Checked on
+    slices at the start, across the 4 GiB boundary and at the tail (which has
+    numel % 8 == 5 scalar elements)."""
+    numel = (1 << 31) + 4096 + 5
+    g = torch.Generator(device=cuda)
+    g.manual_seed(123)
+    gate = torch.randn(numel, generator=g, device=cuda, dtype=torch.float32).to(F16)
+    up = torch.randn(numel, generator=g, device=cuda, dtype=torch.float32).to(F16)
+    out = pkg.fused_silu_mul(gate, up)
+    torch.cuda.synchronize()
+    for lo, hi in [(0, 8192), ((1 << 31) - 8192, (1 << 31) + 8192), (numel - 8192, numel)]:
+        ref = orc.silu_mul(storage(gate[lo:hi].cpu()), storage(up[lo:hi].cpu()), idt="f16")
+        _check16(out[lo:hi].cpu(), ref, orc, f"silu_mul [{lo}:{hi}) of {numel}")
+    del gate, up, out
+    torch.cuda.empty_cache()
+
+
+def test_rmsnorm_beyond_4gib(pkg, orc, cuda):
+    """x and y of > 4 GiB: 600000 rows x 4096 fp16; rows around the
+    2^32-byte offset and the last rows are checked against the oracle."""
+    rows, n = 600000, 4096
+    g = torch.Generator(device=cuda)
+    g.manual_seed(321)
+    x = torch.randn(rows, n, generator=g, device=cuda, dtype=torch.float32).to(F16)
+    w = randn((n,), 5, F16, mean=1.0, std=0.1)
+    y = pkg.fused_rmsnorm(x, w.to(cuda))
+    torch.cuda.synchronize()
+    boundary = (1 << 32) // (n * 2)
+    for lo, hi in [(0, 16), (boundary - 16, boundary + 16), (rows - 16, rows)]:
+        ref = orc.rmsnorm(storage(x[lo:hi].cpu()), storage(w), 1e-6, xdt="f16", wdt="f16")
+        _check16(y[lo:hi].cpu(), ref, orc, f"rmsnorm rows [{lo}:{hi}) of {rows}")
+    del x, y
+    torch.cuda.empty_cache()
