@@ -59,7 +59,7 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c4-silu", "c4-rms", "copy"], default=None,
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy"], default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e", action="store_true",
                    help="instead of the kernel bench: TTFT and decode tok/s of a random-init Qwen2-1.5B "
@@ -276,11 +276,13 @@ def cpu_baseline(M, N, I, budget_s):
 # the ideal.  Grid sizes are in threads, as rocprofv3 reports them.
 KNOWN_LAUNCHES = {
     ("silu_mul_chunks<mi355::F16, mi355::F16>", 1146880): ("C2 SiLU-and-mul [2048,8960] fp16", 3 * 2048 * 8960 * 2),
-    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3>", 131072): (
+    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3, false>", 131072): (
         "C1 RMSNorm [2048,1536] fp16", (2 * 2048 * 1536 + 1536) * 2),
+    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3, true>", 131072): (
+        "C1 residual add + RMSNorm [2048,1536] fp16", (4 * 2048 * 1536 + 1536) * 2),
     ("silu_mul_chunks<mi355::BF16, mi355::BF16>", 19398656): (
         "C4 SiLU-and-mul [16384,18944] bf16", 3 * 16384 * 18944 * 2),
-    ("rmsnorm_wave_rows<mi355::BF16, mi355::BF16, mi355::BF16, 7>", 1048576): (
+    ("rmsnorm_block_rows<mi355::BF16, mi355::BF16, mi355::BF16, 2, false>", 4194304): (
         "C4 RMSNorm [16384,3584] bf16", (2 * 16384 * 3584 + 3584) * 2),
     ("stream_copy", 67108864): ("copy probe, 1 GiB", 2 << 30),
 }
@@ -438,13 +440,13 @@ def main():
     kernels = {
         "c2_silu_mul_f16_2048x8960": kernel_entry("silu_mul_chunks<F16,F16>", silu_bytes, silu_us,
                                                   {"timing": "events over back-to-back launches, cold"}),
-        "c1_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes, rms_us,
+        "c1_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,false>", rms_bytes, rms_us,
                                                  {"timing": "events over back-to-back launches, cold"}),
-        "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes,
+        "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,false>", rms_bytes,
                                                        rms_graph_us, {"timing": "hipGraph of 200 launches, cold"}),
         "c2_silu_mul_f16_2048x8960_warm": kernel_entry("silu_mul_chunks<F16,F16>", silu_bytes, silu_warm_us,
                                                        {"timing": "same buffers every launch (MALL-warm)"}),
-        "c1_rmsnorm_f16_2048x1536_warm_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3>", rms_bytes,
+        "c1_rmsnorm_f16_2048x1536_warm_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,false>", rms_bytes,
                                                             rms_warm_graph_us,
                                                             {"timing": "hipGraph, same buffers (MALL-warm)"}),
     }
@@ -495,6 +497,10 @@ def run_only(ctx, args, sets):
     elif args.only == "c1-rms":
         us = time_loop(ctx, [s[0] for s in sets], iters)
         log(f"c1-rms avg {us:.3f} us")
+    elif args.only == "c1-add-rms":
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_add_rms(ctx, iters)))
     elif args.only in ("c4-silu", "c4-rms"):
         del sets
         torch.cuda.empty_cache()
@@ -525,7 +531,7 @@ def bench_add_rms(ctx, iters):
 
     fused_us = time_loop(ctx, fused, iters)
     unfused_us = time_loop(ctx, [unfused_call(i) for i in range(len(sets))], iters)
-    out = {"c1_add_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,ADD>", fused_bytes,
+    out = {"c1_add_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,true>", fused_bytes,
                                                         fused_us, {"buffer_sets": len(sets)}),
            "c1_add_then_rmsnorm_unfused_us": round(unfused_us, 3),
            "fused_speedup": round(unfused_us / fused_us, 3)}
@@ -551,7 +557,7 @@ def bench_c4(ctx, iters=60, which=None):
             keep.append((x, y))
             calls.append(ctx.rms_call(x, w, y))
         us = time_loop(ctx, calls, iters)
-        out["c4_rmsnorm_bf16_16384x3584"] = kernel_entry("rmsnorm_wave_rows<BF16,BF16,BF16,7>", nbytes, us,
+        out["c4_rmsnorm_bf16_16384x3584"] = kernel_entry("rmsnorm_block_rows<BF16,BF16,BF16,2,false> (4 waves per row)", nbytes, us,
                                                          {"buffer_sets": len(calls)})
         del keep, calls
         torch.cuda.empty_cache()
