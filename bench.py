@@ -22,6 +22,8 @@ Also reported on the same JSON line:
   kernels       per-kernel durations and GB/s (C1, C2, C4), cold and warm;
   decode        C3 latency per call (host-inclusive and device-only) and
                 inside a hipGraph of 28 x (RMSNorm, SiLU-and-mul, RMSNorm);
+  gate_up_silu  the fused gate/up projections + SiLU-and-mul at decode rows
+                vs the reference's two-GEMM + SiLU-and-mul chain;
   copy_ceiling  a plain 16-byte streaming copy on the same device.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -59,7 +61,8 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy"], default=None,
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up"],
+                   default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e", action="store_true",
                    help="instead of the kernel bench: TTFT and decode tok/s of a random-init Qwen2-1.5B "
@@ -131,6 +134,19 @@ class Ctx:
             st = f(*args, self.stream)
             if st:
                 self.L.check("mi355_silu_mul_fwd", st)
+        return call
+
+    def gate_up_call(self, x, wg, wu, o):
+        M, K = x.shape
+        code = self.L.DTYPE_CODE[x.dtype]
+        f = self.lib.mi355_gate_up_silu_fwd
+        args = (x.data_ptr(), wg.data_ptr(), wu.data_ptr(), o.data_ptr(), M, K, wg.shape[0], K, K, wg.shape[0],
+                code, code)
+
+        def call():
+            st = f(*args, self.stream)
+            if st:
+                self.L.check("mi355_gate_up_silu_fwd", st)
         return call
 
     def copy_call(self, src, dst):
@@ -285,6 +301,9 @@ KNOWN_LAUNCHES = {
     ("rmsnorm_block_rows<mi355::BF16, mi355::BF16, mi355::BF16, 2, false>", 4194304): (
         "C4 RMSNorm [16384,3584] bf16", (2 * 16384 * 3584 + 3584) * 2),
     ("stream_copy", 67108864): ("copy probe, 1 GiB", 2 << 30),
+    ("gate_up_silu_skinny<mi355::F16, mi355::F16, 1>", 8960 // 16 * 256): (
+        "gate/up + SiLU-and-mul, 8 rows, [8960,1536] weights, fp16",
+        2 * 8960 * 1536 * 2 + 8 * 1536 * 2 + 8 * 8960 * 2),
 }
 COPY_READ_KIB = COPY_WRITE_KIB = (1 << 30) / 1024
 
@@ -476,6 +495,7 @@ def main():
         result["add_rmsnorm"] = bench_add_rms(ctx, iters)
         result["c4"] = bench_c4(ctx, iters=60)
         result["decode"] = bench_decode(ctx)
+        result["gate_up_silu"] = bench_gate_up(ctx)
         result["copy_ceiling"] = bench_copy(ctx)
 
     if not args.skip_cpu:
@@ -508,6 +528,10 @@ def run_only(ctx, args, sets):
         log(json.dumps(d))
     elif args.only == "copy":
         log(json.dumps(bench_copy(ctx)))
+    elif args.only == "gate-up":
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_gate_up(ctx, shapes=GATE_UP_SHAPES[1:2], iters=iters, baselines=False)))
 
 
 def bench_add_rms(ctx, iters):
@@ -633,6 +657,56 @@ def bench_decode(ctx, layers=28):
             "rows_per_s_rmsnorm": round(M / (rms_dev * 1e-6)),
         }
         log(f"  decode M={M}: {res[f'M={M}']}")
+    return res
+
+
+# (rows, k, n_out, dtype name, label): decode steps of Qwen2.5-1.5B and -7B MLPs
+GATE_UP_SHAPES = [(1, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 1536, 8960, "f16", "qwen2.5-1.5b"),
+                  (32, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 3584, 18944, "bf16", "qwen2.5-7b")]
+
+
+def bench_gate_up(ctx, shapes=GATE_UP_SHAPES, iters=400, baselines=True):
+    """Gate/up projections + SiLU-and-mul at decode rows (beyond the
+    reference): the fused kernel against the reference's FusedMLP chain (two
+    GEMMs through torch / hipBLASLt, then the SiLU-and-mul kernel), on
+    per-layer weight sets whose footprint exceeds 1 GiB, so every call
+    streams its weights from HBM as a decode step walking the layers does.
+    Algorithmic bytes: both weight matrices + x + out.  Timed over
+    back-to-back launches and inside a hipGraph (no launch gaps)."""
+    torch = ctx.torch
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
+    res = {}
+    for M, K, I, dname, label in shapes:
+        dt = dts[dname]
+        wbytes = 2 * I * K * 2
+        nbytes = wbytes + M * K * 2 + M * I * 2
+        layers = n_sets(wbytes)
+        x = rand(ctx, (M, K), 1400 + M, dt)
+        ws = [(rand(ctx, (I, K), 1500 + 2 * l, dt, std=2.0 * K ** -0.5),
+               rand(ctx, (I, K), 1501 + 2 * l, dt, std=K ** -0.5)) for l in range(layers)]
+        outs = [torch.empty((M, I), dtype=dt, device=ctx.dev) for _ in range(layers)]
+        fused = [ctx.gate_up_call(x, wg, wu, o) for (wg, wu), o in zip(ws, outs)]
+        us = time_loop(ctx, fused, iters)
+        us_graph = time_graph(ctx, fused, 4 * layers)
+        key = f"{label}_M{M}_{dname}"
+        entry = kernel_entry(f"gate_up_silu_skinny<{dname.upper()},{dname.upper()},{1 if M <= 16 else 2}>",
+                             nbytes, us, {"weight_sets": layers, "graph_us": round(us_graph, 3),
+                                          "graph_GBps": round(nbytes / us_graph / 1e3, 1)})
+        if baselines:
+            silu = ctx.pkg.fused_silu_mul
+
+            def chain(wg, wu):
+                return lambda: silu(torch.matmul(x, wg.T), torch.matmul(x, wu.T))
+
+            chains = [chain(wg, wu) for wg, wu in ws]
+            c_us = time_loop(ctx, chains, iters)
+            c_graph = time_graph(ctx, chains, 4 * layers)
+            entry.update({"unfused_chain_us": round(c_us, 3), "unfused_chain_graph_us": round(c_graph, 3),
+                          "speedup_graph": round(c_graph / us_graph, 3)})
+        res[key] = entry
+        log(f"  gate_up {key}: {entry}")
+        del ws, outs, fused
+        torch.cuda.empty_cache()
     return res
 
 

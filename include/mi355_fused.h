@@ -121,6 +121,42 @@ int mi355_silu_mul_fwd(const void* gate, const void* up, void* out,
                        int64_t numel, int in_dtype, int out_dtype,
                        void* stream);
 
+/*
+ * Gate/up projections fused with SiLU-and-mul, for decode-sized batches:
+ *   g[m,n]   = sum_k x[m,k] * w_gate[n,k]     (fp32 accumulation, MFMA)
+ *   u[m,n]   = sum_k x[m,k] * w_up[n,k]
+ *   out[m,n] = (g * sigmoid(g)) * u           (fp32, rounded once to out_dtype)
+ *
+ * The reference's FusedMLP (src/engine/fused_norm_activation_patch.py:60-64)
+ * computes `fused_silu_mul(gate_proj(x), up_proj(x))`: two GEMMs whose
+ * results are rounded to x's dtype, written to HBM and read back by the
+ * SiLU-and-mul launch this call also replaces (src/kernels/
+ * fused_swiglu_triton.py:39-53).  This entry point is the "fused activation
+ * with the up/gate projections" its design plans (docs/architecture-cuda.md:94):
+ * g and u never leave registers and are not rounded before the activation,
+ * so results differ from the unfused chain by that intermediate rounding
+ * (they are closer to the exact value).  Weights use nn.Linear's layout,
+ * [n_out, k] row-major, as in HF's gate_proj / up_proj.
+ *
+ * Built for rows <= 32, where the call streams the weights once at HBM
+ * bandwidth; larger `rows` are served by 32-row tiles that each re-read the
+ * weights (a GEMM library is the better choice there).
+ *
+ *   x        [rows, x_row_stride] of dtype, 16-byte aligned.
+ *   w_gate, w_up  [n_out, w_row_stride] of dtype, 16-byte aligned.
+ *   out      [rows, out_row_stride] of out_dtype.
+ *   dtype    MI355_F16 or MI355_BF16; out_dtype = dtype or MI355_F32.
+ *   k, x_row_stride and w_row_stride are multiples of 8 (MI355_ERR_UNSUPPORTED
+ *   otherwise); strides >= k (x, w) and >= n_out (out).  rows == 0 or
+ *   n_out == 0 is a no-op.  Limits: x_row_stride and w_row_stride < 2^24,
+ *   rows <= 2097120.  out must not overlap the inputs.
+ */
+int mi355_gate_up_silu_fwd(const void* x, const void* w_gate, const void* w_up, void* out,
+                           int64_t rows, int64_t k, int64_t n_out,
+                           int64_t x_row_stride, int64_t w_row_stride, int64_t out_row_stride,
+                           int dtype, int out_dtype,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,7 +19,9 @@ and, beyond it, ``fused_add_rmsnorm`` (residual add + RMSNorm in one pass)
 with ``FusedDecoderLayer`` / ``DECODER_LAYER_CLASS_NAMES``, which
 ``patch_model_with_fused_kernels(..., fuse_residual=True)`` installs, and
 ``GraphedGreedyDecoder``, greedy decoding whose per-token step replays one
-captured HIP graph.
+captured HIP graph, and ``fused_gate_up_silu`` (gate / up projections +
+SiLU-and-mul in one kernel for decode batches), which
+``patch_model_with_fused_kernels(..., fuse_gate_up=True)`` lets FusedMLP use.
 
 The kernels live in ``libmi355_fused.so`` (gfx950 HIP, C ABI in
 ``include/mi355_fused.h``), built by ``build.py``.
@@ -29,10 +31,12 @@ from .engine.fused_norm_activation_patch import (DECODER_LAYER_CLASS_NAMES, MLP_
                                                  patch_model_with_fused_kernels)
 from .engine.graphed_decode import GraphedGreedyDecoder
 from .kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm, naive_rmsnorm_reference
+from .kernels.fused_gate_up_hip import GATE_UP_MAX_ROWS, fused_gate_up_silu, naive_gate_up_silu_reference
 from .kernels.fused_swiglu_hip import fused_silu_mul, naive_silu_mul_reference
 
 __all__ = [
     "fused_rmsnorm", "naive_rmsnorm_reference", "fused_silu_mul", "naive_silu_mul_reference",
     "FusedRMSNorm", "FusedMLP", "patch_model_with_fused_kernels", "RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES",
     "fused_add_rmsnorm", "FusedDecoderLayer", "DECODER_LAYER_CLASS_NAMES", "GraphedGreedyDecoder",
+    "fused_gate_up_silu", "naive_gate_up_silu_reference", "GATE_UP_MAX_ROWS",
 ]

@@ -25,7 +25,7 @@ F32, F16, BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTED_SYMBOLS = ("mi355_abi_version", "mi355_last_error", "mi355_rmsnorm_fwd", "mi355_add_rmsnorm_fwd",
-                    "mi355_silu_mul_fwd")
+                    "mi355_silu_mul_fwd", "mi355_gate_up_silu_fwd")
 
 
 class KernelLibraryMissing(RuntimeError):
@@ -69,6 +69,8 @@ def load() -> ctypes.CDLL:
         L.mi355_add_rmsnorm_fwd.restype = i32
         L.mi355_silu_mul_fwd.argtypes = [vp, vp, vp, i64, i32, i32, vp]
         L.mi355_silu_mul_fwd.restype = i32
+        L.mi355_gate_up_silu_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp]
+        L.mi355_gate_up_silu_fwd.restype = i32
         ver = L.mi355_abi_version()
         if ver != ABI_VERSION:
             raise KernelLibraryMissing(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
@@ -125,3 +127,11 @@ def silu_mul_fwd(gate_ptr: int, up_ptr: int, out_ptr: int, numel: int, in_dtype:
                  stream: int) -> None:
     check("mi355_silu_mul_fwd",
           load().mi355_silu_mul_fwd(gate_ptr, up_ptr, out_ptr, numel, in_dtype, out_dtype, stream))
+
+
+def gate_up_silu_fwd(x_ptr: int, wg_ptr: int, wu_ptr: int, out_ptr: int, rows: int, k: int, n_out: int,
+                     x_row_stride: int, w_row_stride: int, out_row_stride: int, dtype: int, out_dtype: int,
+                     stream: int) -> None:
+    check("mi355_gate_up_silu_fwd",
+          load().mi355_gate_up_silu_fwd(x_ptr, wg_ptr, wu_ptr, out_ptr, rows, k, n_out, x_row_stride, w_row_stride,
+                                        out_row_stride, dtype, out_dtype, stream))

@@ -1,6 +1,6 @@
 // C ABI entry points (include/mi355_fused.h): argument validation, the
 // per-thread error message and the per-device CU-count cache.  Kernels and
-// their launchers live in rmsnorm.hip and silu_mul.hip.
+// their launchers live in rmsnorm.hip, silu_mul.hip and gate_up_silu.hip.
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -19,6 +19,8 @@ int add_rmsnorm_launch(const void* x, const void* r, const void* w, void* y, voi
                        int y_dtype, hipStream_t stream);
 int silu_mul_launch(const void* gate, const void* up, void* out, int64_t numel, int in_dtype,
                     int out_dtype, hipStream_t stream);
+int gate_up_silu_launch(const void* x, const void* wg, const void* wu, void* out, int rows, int k, int n_out,
+                        int64_t xs, int64_t ws, int64_t os, int dtype, int out_dtype, hipStream_t stream);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -168,4 +170,61 @@ MI355_EXPORT int mi355_silu_mul_fwd(const void* gate, const void* up, void* out,
   }
   return mi355::silu_mul_launch(gate, up, out, numel, in_dtype, out_dtype,
                                 static_cast<hipStream_t>(stream));
+}
+
+MI355_EXPORT int mi355_gate_up_silu_fwd(const void* x, const void* w_gate, const void* w_up, void* out,
+                                        int64_t rows, int64_t k, int64_t n_out, int64_t x_row_stride,
+                                        int64_t w_row_stride, int64_t out_row_stride, int dtype, int out_dtype,
+                                        void* stream) {
+  static const char* fn = "mi355_gate_up_silu_fwd";
+  mi355::g_error[0] = '\0';
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) {
+    set_error("%s: unknown dtype code (in=%d, out=%d)", fn, dtype, out_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (dtype == MI355_F32) {
+    set_error("%s: x and the weights must be fp16 or bf16 (MFMA operands)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (out_dtype != dtype && out_dtype != MI355_F32) {
+    set_error("%s: out dtype must equal the input dtype or be fp32 (in=%d, out=%d)", fn, dtype, out_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows < 0 || n_out < 0 || k < 1) {
+    set_error("%s: need rows >= 0, n_out >= 0, k >= 1 (got %lld, %lld, %lld)", fn, static_cast<long long>(rows),
+              static_cast<long long>(n_out), static_cast<long long>(k));
+    return MI355_ERR_INVALID;
+  }
+  if (x_row_stride < k || w_row_stride < k || out_row_stride < n_out) {
+    set_error("%s: row strides must be >= k (x, w) and >= n_out (out)", fn);
+    return MI355_ERR_INVALID;
+  }
+  if (rows == 0 || n_out == 0) return MI355_OK;
+  if (x == nullptr || w_gate == nullptr || w_up == nullptr || out == nullptr) {
+    set_error("%s: null pointer", fn);
+    return MI355_ERR_INVALID;
+  }
+  // 16-byte operand loads: k, the x / weight row strides and the base
+  // pointers must be multiples of 8 elements / 16 bytes.
+  if (k % 8 != 0 || x_row_stride % 8 != 0 || w_row_stride % 8 != 0 || !mi355::aligned16(x) ||
+      !mi355::aligned16(w_gate) || !mi355::aligned16(w_up)) {
+    set_error("%s: k, the x and weight row strides must be multiples of 8 and x, w_gate, w_up 16-byte aligned", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  // Buffer descriptors cover at most 32 weight rows and 32 rows of x
+  // (< 2^31 bytes); the grid holds ceil(n_out / 32) or more x ceil(rows / 32)
+  // workgroups.
+  if (w_row_stride >= (int64_t{1} << 24) || x_row_stride >= (int64_t{1} << 24) ||
+      n_out > 0x7fffffff - 31 || rows > int64_t{65535} * 32) {
+    set_error("%s: size beyond the kernel's limits (row strides < 2^24, n_out < 2^31 - 31, "
+              "rows <= 2097120)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows - 1 > (INT64_MAX - n_out) / out_row_stride) {
+    set_error("%s: rows * out_row_stride overflows int64", fn);
+    return MI355_ERR_INVALID;
+  }
+  return mi355::gate_up_silu_launch(x, w_gate, w_up, out, static_cast<int>(rows), static_cast<int>(k),
+                                    static_cast<int>(n_out), x_row_stride, w_row_stride, out_row_stride, dtype,
+                                    out_dtype, static_cast<hipStream_t>(stream));
 }

@@ -1,0 +1,270 @@
+// Gate/up projection fused with the SiLU-and-mul epilogue, for skinny
+// activations (decode batches), plus its launcher:
+//
+//   out[m, n] = silu(g) * u,  g = sum_k x[m,k] * w_gate[n,k],  u = sum_k x[m,k] * w_up[n,k]
+//
+// g and u are fp32 MFMA accumulators that go straight into the activation;
+// the result is rounded once to the output type.  This is the "fused
+// activation with the up/gate projections" the reference plans
+// (docs/architecture-cuda.md:94) for the MLP its FusedMLP runs as two GEMMs,
+// a rounding of both to x's type and the SiLU-and-mul kernel
+// (src/engine/fused_norm_activation_patch.py:60-64).
+//
+// At decode shapes the work is weight streaming: each weight element is read
+// once per call (2 * n_out * k elements) and meets at most 32 rows of x, so
+// the kernel is bound by HBM bandwidth on the weights, not by MFMA.
+//
+// Operand layout.  The v_mfma_f32_16x16x32 B operand gives lane l column
+// n = l % 16 and k-group l / 16 (8 consecutive k each).  Giving the 16
+// columns to 16 weight rows would make each load instruction read 16 rows x
+// 64 bytes, and half-line reads like that stream from HBM at about 70% of
+// the rate of full 128-byte lines on MI355X.  Instead a B operand holds 8
+// weight rows x 64 columns: column n is weight row n % 8 and half h = n / 8
+// of a 64-column K block, so the 8 lanes of a row cover 128 contiguous
+// bytes.  The A operand stacks the (up to) 8 rows of the x tile twice: A row
+// i is x row i % 8 over half i / 8 of the same K block.  Then
+//
+//   D[i][n] = sum over the block's half of x[i % 8] * w[n % 8]  when i / 8 == n / 8
+//
+// and the product of x row a with weight row b over the block is
+// D[a][b] + D[a + 8][b + 8]; the off-diagonal quarters of D are discarded.
+// For up to 8 rows of x this costs no extra MFMA work (A rows 8..15 would
+// otherwise be padding).  x loads use the same lane -> (row, column) map.
+//
+// Decomposition: a workgroup owns 8 * G weight rows (G MFMA B operands per
+// matrix) and a tile of 8 * MT rows of x (blockIdx.y), and splits K between
+// SPLITK waves (contiguous K ranges, so a workgroup reads whole weight
+// rows).  Per 64-column K step a wave loads G B operands of w_gate, G of
+// w_up and MT A operands of x, each one 16-byte load per lane, then issues
+// 2 * G * MT MFMAs.  The loads of U steps are issued before their
+// MFMAs.  Weight rows past n_out and x rows past the tile address past their
+// buffer descriptor and read 0.  The SPLITK partial accumulators meet in
+// LDS, where the two diagonal quarters are added (in a fixed order, so
+// results do not depend on scheduling), then SiLU-and-mul and the store.
+// D layout of the gfx950 16x16x32 MFMA: lane l holds rows 4 * (l / 16) + j,
+// j < 4, of column l % 16.
+#include "common.h"
+
+// Launch shapes (split-K waves, weight row groups, K steps in flight per
+// wave) were chosen by sweeping them on MI355X at Qwen2.5 decode shapes:
+//   up to 8 rows of x, k <= 2048 and n_out < 16384: SPLITK 4, G 1 (the most
+//     workgroups), U 6 (one load group per wave at k = 1536; U 4 for
+//     k <= 1024);
+//   otherwise SPLITK 4, G 2 (x read once per 16 weight rows), U 2.
+#ifndef MI355_GU_FORCE
+#define MI355_GU_FORCE 0  // 1: always the first shape, 2: always the second (sweeps)
+#endif
+
+namespace mi355 {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Offset that lies past every descriptor the launcher admits (< 2^31 bytes).
+constexpr uint32_t kOob = 0xfffffff0u;
+
+template <typename T> __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma16<F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma16<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+struct GateUpParams {
+  const void* x;       // [rows, xs]
+  const void* wg;      // [n_out, ws]
+  const void* wu;      // [n_out, ws]
+  void* out;           // [rows, os]
+  int rows;
+  int k;               // multiple of 8
+  int n_out;
+  int64_t xs, ws, os;  // row strides in elements (xs, ws multiples of 8)
+};
+
+// Operands of N K-steps (64 columns each) of one wave.
+template <int G, int MT, int N>
+struct StepRegs {
+  u32x4 bg[N][G], bu[N][G], a[N][MT];
+};
+
+// Issues the loads of N K-steps starting at step s (byte column 128 * s);
+// steps at or past s_end address past the descriptors (no memory traffic,
+// zeros).  woff / xoff: the lane's row and in-block column, in bytes.
+template <int G, int MT, int N>
+__device__ __forceinline__ void gu_load(StepRegs<G, MT, N>& r, rsrc_t rg, rsrc_t ru, rsrc_t rx,
+                                        const uint32_t (&woff)[G], const uint32_t (&xoff)[MT], int s, int s_end) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const bool live = s + j < s_end;
+    const uint32_t c = 128u * static_cast<uint32_t>(s + j);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      r.bg[j][g] = buf_load16(rg, live ? woff[g] + c : kOob);
+      r.bu[j][g] = buf_load16(ru, live ? woff[g] + c : kOob);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) r.a[j][t] = buf_load16_cached(rx, live ? xoff[t] + c : kOob);
+  }
+}
+
+template <typename T, int G, int MT, int N>
+__device__ __forceinline__ void gu_mfma(const StepRegs<G, MT, N>& r, f32x4 (&accg)[G][MT], f32x4 (&accu)[G][MT]) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        accg[g][t] = mfma16<T>(r.a[j][t], r.bg[j][g], accg[g][t]);
+        accu[g][t] = mfma16<T>(r.a[j][t], r.bu[j][g], accu[g][t]);
+      }
+    }
+  }
+}
+
+template <typename T, typename TO, int MT, int SPLITK, int G, int U>
+__global__ __launch_bounds__(64 * SPLITK) void gate_up_silu_skinny(const GateUpParams p) {
+  using TB = typename T::bits;
+  __shared__ float red[SPLITK][G][MT][2][4][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 8 * G;
+  const int m0 = blockIdx.y * 8 * MT;
+  const int nrows_w = p.n_out - n0 < 8 * G ? p.n_out - n0 : 8 * G;
+  const int nrows_x = p.rows - m0 < 8 * MT ? p.rows - m0 : 8 * MT;
+
+  // Descriptors end right after the last valid element, so weight rows past
+  // n_out and x rows past the tile (offset >= rows * stride >= the extent,
+  // since strides >= k) read as 0.
+  const rsrc_t rg = make_rsrc(static_cast<const TB*>(p.wg) + static_cast<int64_t>(n0) * p.ws,
+                              static_cast<uint32_t>(((nrows_w - 1) * p.ws + p.k) * sizeof(TB)));
+  const rsrc_t ru = make_rsrc(static_cast<const TB*>(p.wu) + static_cast<int64_t>(n0) * p.ws,
+                              static_cast<uint32_t>(((nrows_w - 1) * p.ws + p.k) * sizeof(TB)));
+  const rsrc_t rx = make_rsrc(static_cast<const TB*>(p.x) + static_cast<int64_t>(m0) * p.xs,
+                              static_cast<uint32_t>(((nrows_x - 1) * p.xs + p.k) * sizeof(TB)));
+
+  // Lane -> (row r = l % 8 of the operand, half h = (l / 8) % 2, k-group kg = l / 16):
+  // 16-byte piece at column 32 * h + 8 * kg of each 64-column block.
+  const int r8 = lane & 7;
+  const int colb = (((lane >> 3) & 1) * 32 + (lane >> 4) * 8) * static_cast<int>(sizeof(TB));
+  uint32_t woff[G], xoff[MT];
+#pragma unroll
+  for (int g = 0; g < G; ++g) woff[g] = static_cast<uint32_t>((8 * g + r8) * p.ws * sizeof(TB) + colb);
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xoff[t] = static_cast<uint32_t>((8 * t + r8) * p.xs * sizeof(TB) + colb);
+
+  f32x4 accg[G][MT], accu[G][MT];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      accg[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      accu[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  const int kfull = p.k >> 6;  // whole 64-column steps
+  const int s_end = (kfull * (wave + 1)) / SPLITK;
+  // Every load of a group is issued before its MFMAs (sched_barrier keeps the
+  // scheduler from interleaving them), so a wave keeps U steps in flight.
+  for (int s = (kfull * wave) / SPLITK; s < s_end; s += U) {
+    StepRegs<G, MT, U> cur;
+    gu_load<G, MT, U>(cur, rg, ru, rx, woff, xoff, s, s_end);
+    __builtin_amdgcn_sched_barrier(0);
+    gu_mfma<T, G, MT, U>(cur, accg, accu);
+  }
+  if ((p.k & 63) != 0 && wave == SPLITK - 1) {
+    // Partial last block: 16-byte pieces at or past k read 0.
+    const bool live = kfull * 64 + (((lane >> 3) & 1) * 32 + (lane >> 4) * 8) < p.k;
+    const uint32_t c = 128u * static_cast<uint32_t>(kfull);
+    StepRegs<G, MT, 1> tail;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      tail.bg[0][g] = buf_load16(rg, live ? woff[g] + c : kOob);
+      tail.bu[0][g] = buf_load16(ru, live ? woff[g] + c : kOob);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tail.a[0][t] = buf_load16_cached(rx, live ? xoff[t] + c : kOob);
+    gu_mfma<T, G, MT, 1>(tail, accg, accu);
+  }
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[wave][g][t][0][j][lane] = accg[g][t][j];
+        red[wave][g][t][1][j][lane] = accu[g][t][j];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Output (x row 8t + a, weight row 8g + b) = D[a][b] + D[a + 8][b + 8]:
+  // register a % 4 of lanes 16 * (a / 4) + b and 16 * (a / 4) + 40 + b.
+  for (int o = threadIdx.x; o < 64 * G * MT; o += 64 * SPLITK) {
+    const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
+    const int g = gt % G, t = gt / G;
+    const int m = 8 * t + a, n = 8 * g + b;
+    if (m >= nrows_x || n >= nrows_w) continue;
+    const int l0 = 16 * (a >> 2) + b, j = a & 3;
+    float gs = 0.f, us = 0.f;
+#pragma unroll
+    for (int w = 0; w < SPLITK; ++w) {
+      gs += red[w][g][t][0][j][l0] + red[w][g][t][0][j][l0 + 40];
+      us += red[w][g][t][1][j][l0] + red[w][g][t][1][j][l0 + 40];
+    }
+    store_elem<TO>(p.out, static_cast<int64_t>(m0 + m) * p.os + n0 + n, silu_mul_f32(gs, us));
+  }
+}
+
+template <typename T, typename TO, int MT, int SPLITK, int G, int U>
+int gate_up_launch_tiles(const GateUpParams& p, hipStream_t s) {
+  void* args[] = {const_cast<GateUpParams*>(&p)};
+  const dim3 grid(static_cast<unsigned>((p.n_out + 8 * G - 1) / (8 * G)),
+                  static_cast<unsigned>((p.rows + 8 * MT - 1) / (8 * MT)));
+  return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(gate_up_silu_skinny<T, TO, MT, SPLITK, G, U>),
+                                    grid, dim3(64 * SPLITK), args, 0, s),
+                    "gate_up_silu launch");
+}
+
+template <typename T, typename TO, int MT>
+int gate_up_shape(const GateUpParams& p, hipStream_t s) {
+  if (MT == 1 && (MI355_GU_FORCE == 1 || (MI355_GU_FORCE == 0 && p.k <= 2048 && p.n_out < 16384))) {
+    if (p.k <= 1024) return gate_up_launch_tiles<T, TO, 1, 4, 1, 4>(p, s);
+    return gate_up_launch_tiles<T, TO, 1, 4, 1, 6>(p, s);
+  }
+  return gate_up_launch_tiles<T, TO, MT, 4, 2, 2>(p, s);
+}
+
+template <typename T, typename TO>
+int gate_up_typed(const GateUpParams& p, hipStream_t s) {
+  // x tile: the fewest 8-row MFMA tiles that cover the rows, up to 4 (32 rows)
+  // per workgroup; more rows take further 32-row tiles along grid y.
+  if (p.rows <= 8) return gate_up_shape<T, TO, 1>(p, s);
+  if (p.rows <= 16) return gate_up_shape<T, TO, 2>(p, s);
+  if (p.rows <= 24) return gate_up_shape<T, TO, 3>(p, s);
+  return gate_up_shape<T, TO, 4>(p, s);
+}
+
+}  // namespace
+
+int gate_up_silu_launch(const void* x, const void* wg, const void* wu, void* out, int rows, int k, int n_out,
+                        int64_t xs, int64_t ws, int64_t os, int dtype, int out_dtype, hipStream_t stream) {
+  const GateUpParams p{x, wg, wu, out, rows, k, n_out, xs, ws, os};
+  if (dtype == MI355_F16 && out_dtype == MI355_F16) return gate_up_typed<F16, F16>(p, stream);
+  if (dtype == MI355_F16 && out_dtype == MI355_F32) return gate_up_typed<F16, F32>(p, stream);
+  if (dtype == MI355_BF16 && out_dtype == MI355_BF16) return gate_up_typed<BF16, BF16>(p, stream);
+  if (dtype == MI355_BF16 && out_dtype == MI355_F32) return gate_up_typed<BF16, F32>(p, stream);
+  set_error("mi355_gate_up_silu_fwd: unsupported dtype pair (in=%d, out=%d)", dtype, out_dtype);
+  return MI355_ERR_UNSUPPORTED;
+}
+
+}  // namespace mi355

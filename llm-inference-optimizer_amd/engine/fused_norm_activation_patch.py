@@ -24,13 +24,18 @@ layer by ``FusedDecoderLayer``, which runs the post-attention residual add
 inside the post-attention RMSNorm (``fused_add_rmsnorm``) -- the "fused
 RMSNorm + residual" the reference plans (docs/architecture-cuda.md:94).  The
 result is bit-identical to the unfused layer with the fused kernels; the
-count appears as ``"add_rmsnorm"``.
+count appears as ``"add_rmsnorm"``.  ``fuse_gate_up=True`` (also off by
+default) lets each FusedMLP run its gate / up projections and the
+SiLU-and-mul in one kernel (``fused_gate_up_silu``) for decode-sized batches
+(<= 32 rows); the projections are then not rounded before the activation,
+which changes results by that rounding.  The count appears as ``"gate_up"``.
 """
 from __future__ import annotations
 
 import torch
 
 from ..kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm
+from ..kernels.fused_gate_up_hip import GATE_UP_MAX_ROWS, fused_gate_up_silu
 from ..kernels.fused_swiglu_hip import fused_silu_mul
 
 __all__ = ["RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES", "DECODER_LAYER_CLASS_NAMES", "FusedRMSNorm", "FusedMLP",
@@ -55,18 +60,40 @@ class FusedRMSNorm(torch.nn.Module):
         return fused_rmsnorm(hidden_states, self.weight, self.variance_epsilon)
 
 
+def _plain_linear(m: torch.nn.Module) -> bool:
+    return type(m) is torch.nn.Linear and m.bias is None
+
+
 class FusedMLP(torch.nn.Module):
     """Wraps an existing SwiGLU MLP's three projections and replaces the
     ``act_fn(gate) * up`` step with the fused SiLU-and-mul kernel.  SiLU is
-    fixed, as in the reference; the projection modules are reused."""
+    fixed, as in the reference; the projection modules are reused.
 
-    def __init__(self, orig_module: torch.nn.Module):
+    With ``fuse_gate_up=True``, inputs of at most ``GATE_UP_MAX_ROWS`` rows
+    (decode steps) whose projections are plain bias-free ``nn.Linear`` layers
+    in fp16 / bf16 with k a multiple of 8 take ``fused_gate_up_silu`` instead:
+    gate, up and the activation in one kernel.  Other inputs take the
+    reference path."""
+
+    def __init__(self, orig_module: torch.nn.Module, fuse_gate_up: bool = False):
         super().__init__()
         self.gate_proj = orig_module.gate_proj
         self.up_proj = orig_module.up_proj
         self.down_proj = orig_module.down_proj
+        self.fuse_gate_up = bool(fuse_gate_up) and self.gate_up_fusable()
+
+    def gate_up_fusable(self) -> bool:
+        """Whether the projections are ones the fused gate/up kernel can read:
+        plain bias-free Linear layers of one shape with k a multiple of 8."""
+        g, u = self.gate_proj, self.up_proj
+        return (_plain_linear(g) and _plain_linear(u) and g.weight.shape == u.weight.shape
+                and g.weight.shape[1] % 8 == 0)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.fuse_gate_up and x.numel() <= GATE_UP_MAX_ROWS * x.shape[-1]:
+            wg, wu = self.gate_proj.weight, self.up_proj.weight
+            if x.dtype == wg.dtype == wu.dtype and x.dtype in (torch.float16, torch.bfloat16):
+                return self.down_proj(fused_gate_up_silu(x, wg, wu))
         gate = self.gate_proj(x)
         up = self.up_proj(x)
         activated = fused_silu_mul(gate, up)
@@ -112,13 +139,19 @@ class FusedDecoderLayer(torch.nn.Module):
 
 
 def patch_model_with_fused_kernels(model: torch.nn.Module, patch_norm: bool = True,
-                                   patch_mlp: bool = True, fuse_residual: bool = False) -> dict:
+                                   patch_mlp: bool = True, fuse_residual: bool = False,
+                                   fuse_gate_up: bool = False) -> dict:
     """Replace matching RMSNorm and/or MLP child modules in place (setattr on
     the parent).  Returns ``{"rmsnorm": count, "mlp": count}``.
     ``patch_norm`` / ``patch_mlp`` enable each kernel independently.
     ``fuse_residual`` additionally replaces matching decoder layers by
-    ``FusedDecoderLayer`` and adds ``"add_rmsnorm": count`` to the result."""
+    ``FusedDecoderLayer`` and adds ``"add_rmsnorm": count`` to the result.
+    ``fuse_gate_up`` builds each FusedMLP with ``fuse_gate_up=True`` and adds
+    ``"gate_up": count`` (the MLPs whose projections the fused kernel can
+    read)."""
     counts = {"rmsnorm": 0, "mlp": 0}
+    if fuse_gate_up:
+        counts["gate_up"] = 0
     for parent in list(model.modules()):
         for child_name, child in list(parent.named_children()):
             cls_name = child.__class__.__name__
@@ -128,8 +161,11 @@ def patch_model_with_fused_kernels(model: torch.nn.Module, patch_norm: bool = Tr
                 counts["rmsnorm"] += 1
             elif patch_mlp and cls_name in MLP_CLASS_NAMES and all(
                     hasattr(child, attr) for attr in ("gate_proj", "up_proj", "down_proj")):
-                setattr(parent, child_name, FusedMLP(child))
+                fused = FusedMLP(child, fuse_gate_up=fuse_gate_up)
+                setattr(parent, child_name, fused)
                 counts["mlp"] += 1
+                if fused.fuse_gate_up:
+                    counts["gate_up"] += 1
     if fuse_residual:
         counts["add_rmsnorm"] = 0
         for parent in list(model.modules()):

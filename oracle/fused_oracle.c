@@ -19,6 +19,14 @@
  *       (src/kernels/fused_swiglu_triton.py:56-59).
  *   *_f64               -- fp64 brute force of the same mathematics.
  *
+ * oracle_gate_up_silu restates the MLP's activation input: the gate / up
+ * projections of x (nn.Linear weights, [n, k]) followed by SiLU-and-mul, in
+ * two modes -- the reference's FusedMLP chain, where each projection is
+ * rounded to x's type before the SiLU-and-mul kernel
+ * (src/engine/fused_norm_activation_patch.py:60-64), and the fused form
+ * without that intermediate rounding.  Projections are summed in fp64
+ * (products of 16-bit values are exact there).
+ *
  * Sum of squares: the reference reduces with tl.sum in fp32 in an order the
  * Triton backend picks (:43).  The oracle accumulates the exact squares in
  * fp64 and rounds the sum to fp32 once, i.e. the order-free fp32 sum; any
@@ -264,6 +272,70 @@ int oracle_silu_mul_f64(const void* gate, const void* up, double* out, int64_t n
     const double g = (double)load_f(gate, i, idt);
     const double u = (double)load_f(up, i, idt);
     out[i] = g / (1.0 + exp(-g)) * u;
+  }
+  return 0;
+}
+
+/* --------------------------------------------- gate/up + SiLU-and-mul */
+
+enum { ORACLE_GU_FUSED = 0, ORACLE_GU_UNFUSED = 1 };
+/* planted mistakes, gate/up + SiLU-and-mul */
+enum {
+  ORACLE_MUT_GU_TRANSPOSE = 1, /* read the weights as [k, n] instead of [n, k] */
+  ORACLE_MUT_GU_SWAP = 2,      /* silu(up) * gate */
+  ORACLE_MUT_GU_DROP_TAIL = 3, /* skip the last 8 columns of k */
+  ORACLE_MUT_GU_ROW_SHIFT = 4  /* pair output row m with x row (m + 1) % rows */
+};
+
+/*
+ *   g[m,j] = sum_c x[m,c] * wg[j,c],  u[m,j] = sum_c x[m,c] * wu[j,c]   (fp64)
+ *   FUSED   (the fused projection kernel):
+ *           out = round_odt((gf * (1 / (1 + exp(-gf)))) * uf),  gf = (float)g, uf = (float)u
+ *   UNFUSED (FusedMLP, :60-64): gate = round_dt((float)g), up = round_dt((float)u)
+ *           [the GEMMs' fp32 result rounded to x's type], then the SiLU-and-mul
+ *           kernel's formula (src/kernels/fused_swiglu_triton.py:30-36) on them.
+ *   Optional fp64 outputs (NULL to skip): g64, u64, out64 = g / (1 + exp(-g)) * u,
+ *   gabs / uabs = sum_c |x[m,c] * w[j,c]| (scale for fp32 accumulation error bounds).
+ * x: [rows, k], wg / wu: [n, k], outputs [rows, n], all contiguous.
+ */
+int oracle_gate_up_silu(const void* x, const void* wg, const void* wu, void* out, double* g64, double* u64,
+                        double* out64, double* gabs, double* uabs, int64_t rows, int64_t k, int64_t n, int dt,
+                        int odt, int mode, int mutate) {
+  if (!valid_dt(dt) || !valid_dt(odt) || rows < 0 || k < 1 || n < 0) return -1;
+  const int64_t kk = (mutate == ORACLE_MUT_GU_DROP_TAIL && k > 8) ? k - 8 : k;
+  for (int64_t m = 0; m < rows; ++m) {
+    const int64_t xm = (mutate == ORACLE_MUT_GU_ROW_SHIFT) ? (m + 1) % rows : m;
+    for (int64_t j = 0; j < n; ++j) {
+      double g = 0.0, u = 0.0, ga = 0.0, ua = 0.0;
+      for (int64_t c = 0; c < kk; ++c) {
+        const int64_t wi = (mutate == ORACLE_MUT_GU_TRANSPOSE) ? c * n + j : j * k + c;
+        const double xv = (double)load_f(x, xm * k + c, dt);
+        const double pg = xv * (double)load_f(wg, wi, dt);
+        const double pu = xv * (double)load_f(wu, wi, dt);
+        g += pg;
+        u += pu;
+        ga += fabs(pg);
+        ua += fabs(pu);
+      }
+      if (mutate == ORACLE_MUT_GU_SWAP) {
+        const double t = g;
+        g = u;
+        u = t;
+      }
+      const int64_t o = m * n + j;
+      if (g64) g64[o] = g;
+      if (u64) u64[o] = u;
+      if (gabs) gabs[o] = ga;
+      if (uabs) uabs[o] = ua;
+      if (out64) out64[o] = g / (1.0 + exp(-g)) * u;
+      float gf = (float)g, uf = (float)u;
+      if (mode == ORACLE_GU_UNFUSED) {
+        gf = round_to(gf, dt);
+        uf = round_to(uf, dt);
+      }
+      const float sig = 1.0f / (1.0f + expf(-gf));
+      store_f(out, o, odt, (gf * sig) * uf);
+    }
   }
   return 0;
 }

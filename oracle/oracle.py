@@ -18,6 +18,11 @@ Contents
     - :func:`rmsnorm_f64` / :func:`silu_mul_f64` are fp64 brute force.
 * :func:`add_rmsnorm`: the residual add + RMSNorm fusion (beyond the
   reference): h = round(x + residual), then RMSNorm(h) in either mode;
+* :func:`gate_up_silu`: the MLP's gate / up projections followed by
+  SiLU-and-mul, fused (no rounding between projection and activation) or as
+  the reference's FusedMLP chain (projections rounded to x's type,
+  src/engine/fused_norm_activation_patch.py:60-64), with the fp64 values and
+  the |x|.|w| scales that bound fp32 accumulation error;
 * :func:`naive_rmsnorm_torch` / :func:`naive_silu_mul_torch`: the reference's
   naive PyTorch path restated as the same torch op sequence, which bench.py
   times on the host cores as the CPU baseline.
@@ -51,6 +56,8 @@ MODE_CODE = {"triton": 0, "hf": 1}
 # planted-mistake codes (see fused_oracle.c)
 MUT_RMS = {"n_minus_1": 1, "no_eps": 2, "sqrt": 3, "no_weight": 4, "w_reversed": 5}
 MUT_SILU = {"sign": 1, "swap": 2, "no_up": 3, "round2": 4}
+MUT_GU = {"transpose": 1, "swap": 2, "drop_tail": 3, "row_shift": 4}
+GU_MODE = {"fused": 0, "unfused": 1}
 
 _lib = None
 
@@ -87,6 +94,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_silu_mul.restype = i32
         L.oracle_silu_mul_f64.argtypes = [vp, vp, vp, i64, i32]
         L.oracle_silu_mul_f64.restype = i32
+        L.oracle_gate_up_silu.argtypes = [vp] * 9 + [i64, i64, i64, i32, i32, i32, i32]
+        L.oracle_gate_up_silu.restype = i32
         for name in ("oracle_f32_to_f16_n", "oracle_f16_to_f32_n", "oracle_f32_to_bf16_n", "oracle_bf16_to_f32_n"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
@@ -199,6 +208,33 @@ def silu_mul_f64(gate: np.ndarray, up: np.ndarray, *, idt: str) -> np.ndarray:
 
 
 # -------------------------------------------------------------- conversions
+
+# --------------------------------------------------- gate/up + SiLU-and-mul
+
+def gate_up_silu(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, *, dt: str, odt: str | None = None,
+                 mode: str = "fused", mutate: str | None = None) -> dict:
+    """x: [rows, k], wg / wu: [n, k] in dt storage.  Returns a dict with
+    ``out`` ([rows, n], odt storage, the ``mode`` formula), ``out64``, ``g``,
+    ``u`` (fp64) and ``gabs`` / ``uabs`` (sum_k |x * w|, fp64)."""
+    x = _arr(x, dt)
+    wg = _arr(wg, dt)
+    wu = _arr(wu, dt)
+    if x.ndim != 2 or wg.ndim != 2 or wg.shape != wu.shape or wg.shape[1] != x.shape[1]:
+        raise ValueError(f"bad shapes x={x.shape} wg={wg.shape} wu={wu.shape}")
+    odt = odt or dt
+    rows, k = x.shape
+    n = wg.shape[0]
+    res = {"out": np.empty((rows, n), dtype=_np_dtype(odt))}
+    for key in ("g", "u", "out64", "gabs", "uabs"):
+        res[key] = np.empty((rows, n), dtype=np.float64)
+    mut = 0 if mutate is None else MUT_GU[mutate]
+    st = lib().oracle_gate_up_silu(_ptr(x), _ptr(wg), _ptr(wu), _ptr(res["out"]), _ptr(res["g"]), _ptr(res["u"]),
+                                   _ptr(res["out64"]), _ptr(res["gabs"]), _ptr(res["uabs"]), rows, k, n,
+                                   DT_CODE[dt], DT_CODE[odt], GU_MODE[mode], mut)
+    if st != 0:
+        raise ValueError("oracle_gate_up_silu rejected its arguments")
+    return res
+
 
 def f32_to_f16(a: np.ndarray) -> np.ndarray:
     a = np.ascontiguousarray(a, dtype=np.float32)

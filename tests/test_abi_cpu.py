@@ -97,6 +97,36 @@ def test_silu_mul_abi_zero_numel_is_noop(lib):
     assert lib.mi355_silu_mul_fwd(0, 0, 0, 0, 1, 1, None) == 0
 
 
+# (x, w_gate, w_up, out, rows, k, n_out, x_row_stride, w_row_stride, out_row_stride, dtype, out_dtype)
+@pytest.mark.parametrize("args,code,msg", [
+    ((P, P, P, P, 8, 64, 32, 64, 64, 32, 7, 1), -1, "unknown dtype"),
+    ((P, P, P, P, 8, 64, 32, 64, 64, 32, 0, 0), -2, "fp16 or bf16"),
+    ((P, P, P, P, 8, 64, 32, 64, 64, 32, 1, 2), -2, "out dtype"),
+    ((P, P, P, P, -1, 64, 32, 64, 64, 32, 1, 1), -1, "need rows"),
+    ((P, P, P, P, 8, 0, 32, 64, 64, 32, 1, 1), -1, "need rows"),
+    ((P, P, P, P, 8, 64, 32, 56, 64, 32, 1, 1), -1, "row strides"),
+    ((P, P, P, P, 8, 64, 32, 64, 64, 16, 1, 1), -1, "row strides"),
+    ((P, P, 0, P, 8, 64, 32, 64, 64, 32, 2, 2), -1, "null pointer"),
+    ((P, P, P, P, 8, 60, 32, 64, 64, 32, 1, 1), -2, "multiples of 8"),
+    ((P, P, P, P, 8, 64, 32, 68, 64, 32, 1, 1), -2, "multiples of 8"),
+    ((P + 2, P, P, P, 8, 64, 32, 64, 64, 32, 1, 1), -2, "16-byte aligned"),
+    ((P, P, P, P, 8, 64, 32, 64, 2**24, 32, 1, 1), -2, "limits"),
+    ((P, P, P, P, 8, 64, 32, 2**24, 64, 32, 1, 1), -2, "limits"),
+    ((P, P, P, P, 65535 * 32 + 1, 64, 32, 64, 64, 32, 1, 1), -2, "limits"),
+    ((P, P, P, P, 2**40, 64, 32, 64, 64, 2**40, 1, 1), -2, "limits"),
+])
+def test_gate_up_silu_abi_rejects(lib, args, code, msg):
+    st = lib.mi355_gate_up_silu_fwd(*args, None)
+    assert st == code
+    assert msg in lib.mi355_last_error().decode()
+
+
+def test_gate_up_silu_abi_empty_is_noop(lib):
+    assert lib.mi355_gate_up_silu_fwd(0, 0, 0, 0, 0, 64, 32, 64, 64, 32, 1, 1, None) == 0
+    assert lib.mi355_gate_up_silu_fwd(0, 0, 0, 0, 8, 64, 0, 64, 64, 0, 2, 0, None) == 0
+    assert lib.mi355_last_error().decode() == ""
+
+
 def test_python_check_raises_with_message(L, lib):
     st = lib.mi355_silu_mul_fwd(P, P, P, -5, 1, 1, None)
     with pytest.raises(L.KernelError, match="numel must be >= 0"):
@@ -118,6 +148,8 @@ def test_launchers_assert_on_host_tensors(pkg):
         pkg.fused_rmsnorm(x, torch.ones(64, dtype=torch.float16))
     with pytest.raises(AssertionError):
         pkg.fused_silu_mul(x, x)
+    with pytest.raises(AssertionError):
+        pkg.fused_gate_up_silu(x, torch.ones(16, 64, dtype=torch.float16), torch.ones(16, 64, dtype=torch.float16))
     with pytest.raises(AssertionError):
         pkg.fused_silu_mul(x, torch.randn(4, 65, dtype=torch.float16))
 

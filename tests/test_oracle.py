@@ -12,6 +12,8 @@ against something independent of it:
   plus fp32 noise) and closed forms: zero rows, constant rows, exact
   power-of-two scale invariance, unit RMS with a unit weight, silu special
   values;
+* the gate/up projections -- numpy's float64 GEMM, torch's float64 silu and
+  torch's own 16-bit casts composed with the pinned SiLU-and-mul oracle;
 * planted mistakes -- each deliberate error the oracle can be built with
   (``mutate``) fails at least one of the checks above.
 """
@@ -274,3 +276,58 @@ def test_oracle_add_rmsnorm_matches_torch_and_transformers(orc, dt, n):
 def test_planted_add_rmsnorm_mistake_is_caught(orc, mutate):
     dh, dy, frac, rel = _add_rms_vs_torch(orc, F16, 1536, mutate=mutate)
     assert dh > 0 or dy > 1 or frac >= 1e-3 or rel >= 2e-6, f"planted mistake {mutate} was not caught"
+
+
+# ------------------------------------------- gate/up projections + SiLU-and-mul
+
+def _gate_up_inputs(dt, rows, k, n, seed):
+    x = randn((rows, k), seed, dt)
+    wg = randn((n, k), seed + 1, dt, std=k ** -0.5 * 2.0)
+    wu = randn((n, k), seed + 2, dt, std=k ** -0.5)
+    return x, wg, wu
+
+
+def _gate_up_pins(orc, dt, rows, k, n, mutate=None, seed=50):
+    """Errors of the oracle's gate/up path against independent computations:
+    numpy's float64 GEMM for the projections, torch's float64 silu for the
+    activation, and (unfused mode) torch's own fp32 -> 16-bit casts followed
+    by the separately pinned SiLU-and-mul oracle."""
+    name = {F16: "f16", BF16: "bf16"}[dt]
+    x, wg, wu = _gate_up_inputs(dt, rows, k, n, seed)
+    x64, wg64, wu64 = (t.to(torch.float64).numpy() for t in (x, wg, wu))
+    g_np, u_np = x64 @ wg64.T, x64 @ wu64.T
+    act = (torch.nn.functional.silu(torch.from_numpy(g_np)) * torch.from_numpy(u_np)).numpy()
+    r = orc.gate_up_silu(storage(x), storage(wg), storage(wu), dt=name, mutate=mutate)
+    r32 = orc.gate_up_silu(storage(x), storage(wg), storage(wu), dt=name, odt="f32", mutate=mutate)
+    scale_g = np.abs(x64) @ np.abs(wg64).T
+    scale_u = np.abs(x64) @ np.abs(wu64).T
+    e_proj = max(float(np.max(np.abs(r["g"] - g_np) / scale_g)), float(np.max(np.abs(r["u"] - u_np) / scale_u)))
+    e_act = float(np.max(np.abs(r["out64"] - act) / np.maximum(np.abs(act), 1e-30)))
+    big = np.abs(act) > 1e-3
+    e16 = float(np.max(np.abs(orc.to_f32(r["out"], name).astype(np.float64) - act)[big] / _ulp16(act[big], name)))
+    e32 = float(np.max((np.abs(r32["out"].astype(np.float64) - act) / np.maximum(np.abs(act), 1e-30))[big]))
+    # unfused chain: fp32 projections rounded by torch to the 16-bit type, then SiLU-and-mul
+    gate16 = torch.from_numpy(g_np.astype(np.float32)).to(dt)
+    up16 = torch.from_numpy(u_np.astype(np.float32)).to(dt)
+    chain = orc.silu_mul(storage(gate16), storage(up16), idt=name)
+    unf = orc.gate_up_silu(storage(x), storage(wg), storage(wu), dt=name, mode="unfused", mutate=mutate)["out"]
+    chain_diff = int(orc.ulp_diff16(unf, chain).max())
+    return e_proj, e_act, e16, e32, chain_diff
+
+
+@pytest.mark.parametrize("dt,rows,k,n", [(F16, 8, 1536, 256), (BF16, 8, 1536, 256), (F16, 5, 72, 40),
+                                         (BF16, 33, 40, 24), (F16, 1, 8, 7)])
+def test_oracle_gate_up_silu_vs_numpy_and_torch(orc, dt, rows, k, n):
+    e_proj, e_act, e16, e32, chain_diff = _gate_up_pins(orc, dt, rows, k, n)
+    assert e_proj < 1e-13       # fp64 sums of exact products: rounding noise only
+    assert e_act < 1e-12
+    assert e32 < 2e-6           # fp32 activation of the fp64 projections
+    assert e16 <= 0.5 + 1e-3    # one rounding to the output type
+    assert chain_diff == 0      # unfused mode = torch's roundings + the SiLU-and-mul oracle
+
+
+@pytest.mark.parametrize("mutate", ["transpose", "swap", "drop_tail", "row_shift"])
+def test_planted_gate_up_mistake_is_caught(orc, mutate):
+    e_proj, e_act, e16, e32, chain_diff = _gate_up_pins(orc, F16, 5, 72, 40, mutate=mutate)
+    assert e_proj >= 1e-13 or e_act >= 1e-12 or e32 >= 2e-6 or e16 > 0.5 + 1e-3 or chain_diff != 0, (
+        f"planted mistake {mutate} was not caught")

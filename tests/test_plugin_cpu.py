@@ -105,3 +105,29 @@ def test_fuse_residual_replaces_decoder_layers(pkg):
     # default call keeps the reference's return value exactly
     assert pkg.patch_model_with_fused_kernels(_qwen2(layers=2)) == {"rmsnorm": 5, "mlp": 2}
     assert pkg.DECODER_LAYER_CLASS_NAMES == {"Qwen2DecoderLayer", "LlamaDecoderLayer", "MistralDecoderLayer"}
+
+
+def test_fuse_gate_up_is_opt_in_and_counted(pkg):
+    model = _qwen2(layers=4)
+    assert pkg.patch_model_with_fused_kernels(model, fuse_gate_up=True) == {"rmsnorm": 9, "mlp": 4, "gate_up": 4}
+    assert all(layer.mlp.fuse_gate_up for layer in model.model.layers)
+    plain = _qwen2(layers=2)
+    assert pkg.patch_model_with_fused_kernels(plain) == {"rmsnorm": 5, "mlp": 2}
+    assert not any(layer.mlp.fuse_gate_up for layer in plain.model.layers)
+
+
+def test_fuse_gate_up_skips_projections_the_kernel_cannot_read(pkg):
+    # k (the hidden size) not a multiple of 8
+    odd = _qwen2(layers=2, hidden=60)
+    assert pkg.patch_model_with_fused_kernels(odd, fuse_gate_up=True)["gate_up"] == 0
+    # projections with a bias, or not plain nn.Linear layers
+    model = _qwen2(layers=2)
+    mlp0, mlp1 = model.model.layers[0].mlp, model.model.layers[1].mlp
+    mlp0.gate_proj = torch.nn.Linear(64, 128, bias=True)
+
+    class QuantLinear(torch.nn.Linear):
+        pass
+
+    mlp1.up_proj = QuantLinear(64, 128, bias=False)
+    counts = pkg.patch_model_with_fused_kernels(model, fuse_gate_up=True)
+    assert counts["mlp"] == 2 and counts["gate_up"] == 0
