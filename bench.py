@@ -301,7 +301,7 @@ KNOWN_LAUNCHES = {
     ("rmsnorm_block_rows<mi355::BF16, mi355::BF16, mi355::BF16, 2, false>", 4194304): (
         "C4 RMSNorm [16384,3584] bf16", (2 * 16384 * 3584 + 3584) * 2),
     ("stream_copy", 67108864): ("copy probe, 1 GiB", 2 << 30),
-    ("gate_up_silu_skinny<mi355::F16, mi355::F16, 1>", 8960 // 16 * 256): (
+    ("gate_up_silu_skinny<mi355::F16, mi355::F16, 1, 4, 1, 6>", 8960 // 8 * 256): (
         "gate/up + SiLU-and-mul, 8 rows, [8960,1536] weights, fp16",
         2 * 8960 * 1536 * 2 + 8 * 1536 * 2 + 8 * 8960 * 2),
 }
@@ -689,9 +689,11 @@ def bench_gate_up(ctx, shapes=GATE_UP_SHAPES, iters=400, baselines=True):
         us = time_loop(ctx, fused, iters)
         us_graph = time_graph(ctx, fused, 4 * layers)
         key = f"{label}_M{M}_{dname}"
-        entry = kernel_entry(f"gate_up_silu_skinny<{dname.upper()},{dname.upper()},{1 if M <= 16 else 2}>",
-                             nbytes, us, {"weight_sets": layers, "graph_us": round(us_graph, 3),
-                                          "graph_GBps": round(nbytes / us_graph / 1e3, 1)})
+        entry = kernel_entry("gate_up_silu_skinny", nbytes, us,
+                             {"weight_sets": layers, "graph_us": round(us_graph, 3),
+                              "graph_GBps": round(nbytes / us_graph / 1e3, 1)})
+        if (M, K, I, dname) == (8, 1536, 8960, "f16"):
+            entry["traffic"] = read_traffic("gate/up + SiLU-and-mul, 8 rows, [8960,1536] weights, fp16")
         if baselines:
             silu = ctx.pkg.fused_silu_mul
 
@@ -782,11 +784,13 @@ def bench_e2e(args):
             log(f"  {tag} seq {S}: TTFT {res[S][0]:.2f} ms, decode {res[S][1]:.1f} tok/s")
         return res
 
-    def graphed_decode_tok_s(S=512, new=64):
-        """Decode tok/s with the whole decode step replayed as one HIP graph
-        (GraphedGreedyDecoder over a StaticCache), batch 1."""
-        ids = prompt(S)
-        dec = pkg.GraphedGreedyDecoder(model, 1, S + new + 8)
+    def graphed_decode_tok_s(S=512, new=64, B=1):
+        """Decode tokens/s (B per step) with the whole decode step replayed as
+        one HIP graph (GraphedGreedyDecoder over a StaticCache)."""
+        g = torch.Generator()
+        g.manual_seed(4)
+        ids = torch.randint(0, cfg.vocab_size, (B, S), generator=g).to(dev)
+        dec = pkg.GraphedGreedyDecoder(model, B, S + new + 8)
         dec.generate(ids, new)  # capture
         times = []
         for _ in range(args.trials):
@@ -799,24 +803,37 @@ def bench_e2e(args):
             torch.cuda.synchronize()
             t2 = time.perf_counter()
             times.append(((t2 - t1) - (t1 - t0)) / (new - 2))  # subtract prefill + first step
-        return 1.0 / statistics.median(times)
+        del dec
+        torch.cuda.empty_cache()
+        return B / statistics.median(times)
+
+    def graphed(tag):
+        r = {"b1": graphed_decode_tok_s(), "b8": graphed_decode_tok_s(B=8)}
+        log(f"  {tag}, graphed decode (seq 512): batch 1 {r['b1']:.1f} tok/s, batch 8 {r['b8']:.1f} tok/s")
+        return {k: round(v, 1) for k, v in r.items()}
 
     # warm every shape once before timing anything
     for S in args.seq_lens:
         run(prompt(S), 4)
     before = measure("before")
-    graph_before = graphed_decode_tok_s()
-    log(f"  before, graphed decode: {graph_before:.1f} tok/s")
+    graph_before = graphed("before")
     counts = pkg.patch_model_with_fused_kernels(model)
     log(f"patched {counts}")
     after = measure("after")
-    graph_after = graphed_decode_tok_s()
-    log(f"  after, graphed decode: {graph_after:.1f} tok/s")
+    graph_after = graphed("after")
     counts_fr = pkg.patch_model_with_fused_kernels(model, fuse_residual=True)
     log(f"fused residual {counts_fr}")
     fused_res = measure("after+fuse_residual")
-    graph_fr = graphed_decode_tok_s()
-    log(f"  after+fuse_residual, graphed decode: {graph_fr:.1f} tok/s")
+    graph_fr = graphed("after+fuse_residual")
+    # the same model with each FusedMLP's gate/up projections fused as well
+    n_gu = 0
+    for m in model.modules():
+        if isinstance(m, pkg.FusedMLP) and m.gate_up_fusable():
+            m.fuse_gate_up = True
+            n_gu += 1
+    log(f"fused gate/up in {n_gu} MLPs")
+    fused_gu = measure("after+fuse_residual+fuse_gate_up")
+    graph_gu = graphed("after+fuse_residual+fuse_gate_up")
     rows = []
     for S in args.seq_lens:
         rows.append({"seq_len": S, "before_ttft_ms": round(before[S][0], 3), "after_ttft_ms": round(after[S][0], 3),
@@ -827,12 +844,15 @@ def bench_e2e(args):
         S = row["seq_len"]
         row["fuse_residual_ttft_ms"] = round(fused_res[S][0], 3)
         row["fuse_residual_decode_tok_s"] = round(fused_res[S][1], 2)
+        row["fuse_gate_up_ttft_ms"] = round(fused_gu[S][0], 3)
+        row["fuse_gate_up_decode_tok_s"] = round(fused_gu[S][1], 2)
     print(json.dumps({"metric": "e2e TTFT / decode tok/s speedup from patch_model_with_fused_kernels",
                       "model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16, sdpa, batch 1",
                       "gen_len": args.gen_len, "trials": args.trials, "patched": counts, "results": rows,
-                      "graphed_decode_tok_s": {"seq_len": 512, "unpatched": round(graph_before, 1),
-                                               "patched": round(graph_after, 1),
-                                               "patched_fuse_residual": round(graph_fr, 1)}}),
+                      "fuse_gate_up_mlps": n_gu,
+                      "graphed_decode_tok_s": {"seq_len": 512, "unpatched": graph_before, "patched": graph_after,
+                                               "patched_fuse_residual": graph_fr,
+                                               "patched_fuse_residual_fuse_gate_up": graph_gu}}),
           flush=True)
 
 
