@@ -1,6 +1,7 @@
 /*
  * mi355_fused.h -- C ABI of the MI355X (gfx950) fused RMSNorm and SiLU-and-mul
- * kernels.
+ * kernels, the fused gate/up projections, and the weight-only int8 (W8A16)
+ * linear with its quantiser.
  *
  * The reference has no FFI: its boundary is a pair of Python launchers that
  * hand torch tensors to Triton kernels.  Each entry point below replaces one of
@@ -156,6 +157,55 @@ int mi355_gate_up_silu_fwd(const void* x, const void* w_gate, const void* w_up, 
                            int64_t x_row_stride, int64_t w_row_stride, int64_t out_row_stride,
                            int dtype, int out_dtype,
                            void* stream);
+
+/*
+ * Weight-only int8 linear (W8A16), per output feature n and row m:
+ *   acc[m,n] = sum_k x[m,k] * w_q[n,k]           (fp32 accumulation; int8 and
+ *                                                 16-bit x meet exactly in fp16/bf16)
+ *   out[m,n] = acc[m,n] * scale[n] + bias[n]     (one fma in fp32, rounded once)
+ *
+ * Replaces the launch of `_w8a16_matmul_kernel` in the reference's
+ * `w8a16_linear` (src/kernels/w8a16_matmul_triton.py:102-134, kernel body
+ * :39-86), which QuantizedLinearInt8.forward calls (src/quantization/
+ * int8.py:62-63).  The scale is applied once to the accumulator, as there.
+ *
+ *   x       [rows, x_row_stride] of x_dtype (MI355_F16 or MI355_BF16).
+ *   w_q     [n, w_row_stride] int8, nn.Linear's layout (out_features rows).
+ *   scale   [n] of scale_dtype (the reference's float32; fp16/bf16 accepted).
+ *   bias    [n] of bias_dtype, or NULL (then bias_dtype is ignored).
+ *   out     [rows, out_row_stride] of out_dtype = x_dtype or MI355_F32.
+ *   rows >= 0, k >= 1, n >= 0 (rows == 0 or n == 0 is a no-op); strides >= k
+ *   (x, w_q) and >= n (out).  Any alignment and k are served; the fast kernels
+ *   need k and w_row_stride multiples of 16, x_row_stride a multiple of 8 and
+ *   16-byte aligned x and w_q.  Limits: x_row_stride < 2^23, w_row_stride <
+ *   2^24, n < 2^31 - 128, rows <= 4194240.  out must not overlap the inputs.
+ *   Calls with the same shapes give identical bits (fixed summation order).
+ */
+int mi355_w8a16_linear_fwd(const void* x, const void* w_q, const void* scale, const void* bias, void* out,
+                           int64_t rows, int64_t k, int64_t n,
+                           int64_t x_row_stride, int64_t w_row_stride, int64_t out_row_stride,
+                           int x_dtype, int scale_dtype, int bias_dtype, int out_dtype,
+                           void* stream);
+
+/*
+ * Per-output-channel symmetric int8 quantisation of a weight matrix, per row n:
+ *   amax     = max_k |w[n,k]|
+ *   scale[n] = max(amax / 127, 1e-8)                     (fp32, IEEE division)
+ *   w_q[n,k] = clamp(round_half_even(w[n,k] / scale[n]), -127, 127)
+ *
+ * The arithmetic of the reference's QuantizedLinearInt8.from_linear
+ * (src/quantization/int8.py:45-50), bit for bit: w is widened to fp32
+ * (`linear.weight.detach().float()`), the scale is clamped below at 1e-8 and
+ * the quotient rounded with torch.round's ties-to-even.
+ *
+ *   w      [n, w_row_stride] of w_dtype (fp32, fp16 or bf16).
+ *   w_q    [n, q_row_stride] int8 (output).   scale  [n] fp32 (output).
+ *   n >= 0 (0 is a no-op), 1 <= k < 2^31, strides >= k.  Rows holding NaN or
+ *   Inf get unspecified codes (the reference's are undefined there too).
+ */
+int mi355_quantize_int8_fwd(const void* w, void* w_q, void* scale,
+                            int64_t n, int64_t k, int64_t w_row_stride, int64_t q_row_stride,
+                            int w_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -23,6 +23,11 @@ captured HIP graph, and ``fused_gate_up_silu`` (gate / up projections +
 SiLU-and-mul in one kernel for decode batches), which
 ``patch_model_with_fused_kernels(..., fuse_gate_up=True)`` lets FusedMLP use.
 
+The reference's weight-only int8 stage sits beside it: ``w8a16_linear`` /
+``w8a16_reference``, ``QuantizedLinearInt8`` and ``quantize_model_int8``
+(int8 weights with per-output-channel scales, HIP quantiser and W8A16
+kernels), composable with the fused-kernel patch.
+
 The kernels live in ``libmi355_fused.so`` (gfx950 HIP, C ABI in
 ``include/mi355_fused.h``), built by ``build.py``.
 """
@@ -33,10 +38,13 @@ from .engine.graphed_decode import GraphedGreedyDecoder
 from .kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm, naive_rmsnorm_reference
 from .kernels.fused_gate_up_hip import GATE_UP_MAX_ROWS, fused_gate_up_silu, naive_gate_up_silu_reference
 from .kernels.fused_swiglu_hip import fused_silu_mul, naive_silu_mul_reference
+from .kernels.w8a16_matmul_hip import quantize_int8_weight, w8a16_linear, w8a16_reference
+from .quantization.int8 import QuantizedLinearInt8, quantize_model_int8
 
 __all__ = [
     "fused_rmsnorm", "naive_rmsnorm_reference", "fused_silu_mul", "naive_silu_mul_reference",
     "FusedRMSNorm", "FusedMLP", "patch_model_with_fused_kernels", "RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES",
     "fused_add_rmsnorm", "FusedDecoderLayer", "DECODER_LAYER_CLASS_NAMES", "GraphedGreedyDecoder",
     "fused_gate_up_silu", "naive_gate_up_silu_reference", "GATE_UP_MAX_ROWS",
+    "w8a16_linear", "w8a16_reference", "quantize_int8_weight", "QuantizedLinearInt8", "quantize_model_int8",
 ]

@@ -25,7 +25,8 @@ F32, F16, BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTED_SYMBOLS = ("mi355_abi_version", "mi355_last_error", "mi355_rmsnorm_fwd", "mi355_add_rmsnorm_fwd",
-                    "mi355_silu_mul_fwd", "mi355_gate_up_silu_fwd")
+                    "mi355_silu_mul_fwd", "mi355_gate_up_silu_fwd", "mi355_w8a16_linear_fwd",
+                    "mi355_quantize_int8_fwd")
 
 
 class KernelLibraryMissing(RuntimeError):
@@ -71,6 +72,11 @@ def load() -> ctypes.CDLL:
         L.mi355_silu_mul_fwd.restype = i32
         L.mi355_gate_up_silu_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp]
         L.mi355_gate_up_silu_fwd.restype = i32
+        L.mi355_w8a16_linear_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, i32, i32,
+                                             vp]
+        L.mi355_w8a16_linear_fwd.restype = i32
+        L.mi355_quantize_int8_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i32, vp]
+        L.mi355_quantize_int8_fwd.restype = i32
         ver = L.mi355_abi_version()
         if ver != ABI_VERSION:
             raise KernelLibraryMissing(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
@@ -135,3 +141,18 @@ def gate_up_silu_fwd(x_ptr: int, wg_ptr: int, wu_ptr: int, out_ptr: int, rows: i
     check("mi355_gate_up_silu_fwd",
           load().mi355_gate_up_silu_fwd(x_ptr, wg_ptr, wu_ptr, out_ptr, rows, k, n_out, x_row_stride, w_row_stride,
                                         out_row_stride, dtype, out_dtype, stream))
+
+
+def w8a16_linear_fwd(x_ptr: int, q_ptr: int, scale_ptr: int, bias_ptr: int | None, out_ptr: int, rows: int, k: int,
+                     n: int, x_row_stride: int, w_row_stride: int, out_row_stride: int, x_dtype: int,
+                     scale_dtype: int, bias_dtype: int, out_dtype: int, stream: int) -> None:
+    check("mi355_w8a16_linear_fwd",
+          load().mi355_w8a16_linear_fwd(x_ptr, q_ptr, scale_ptr, bias_ptr, out_ptr, rows, k, n, x_row_stride,
+                                        w_row_stride, out_row_stride, x_dtype, scale_dtype, bias_dtype, out_dtype,
+                                        stream))
+
+
+def quantize_int8_fwd(w_ptr: int, q_ptr: int, scale_ptr: int, n: int, k: int, w_row_stride: int,
+                      q_row_stride: int, w_dtype: int, stream: int) -> None:
+    check("mi355_quantize_int8_fwd",
+          load().mi355_quantize_int8_fwd(w_ptr, q_ptr, scale_ptr, n, k, w_row_stride, q_row_stride, w_dtype, stream))

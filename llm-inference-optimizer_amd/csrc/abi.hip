@@ -1,6 +1,7 @@
 // C ABI entry points (include/mi355_fused.h): argument validation, the
 // per-thread error message and the per-device CU-count cache.  Kernels and
-// their launchers live in rmsnorm.hip, silu_mul.hip and gate_up_silu.hip.
+// their launchers live in rmsnorm.hip, silu_mul.hip, gate_up_silu.hip and
+// w8a16.hip.
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -21,6 +22,12 @@ int silu_mul_launch(const void* gate, const void* up, void* out, int64_t numel, 
                     int out_dtype, hipStream_t stream);
 int gate_up_silu_launch(const void* x, const void* wg, const void* wu, void* out, int rows, int k, int n_out,
                         int64_t xs, int64_t ws, int64_t os, int dtype, int out_dtype, hipStream_t stream);
+
+int w8a16_launch(const void* x, const void* q, const void* scale, const void* bias, void* out, int rows, int k,
+                 int n, int64_t xs, int64_t qs, int64_t os, int x_dtype, int scale_dtype, int bias_dtype,
+                 int out_dtype, hipStream_t stream);
+int quantize_int8_launch(const void* w, void* q, void* scale, int64_t n, int k, int64_t ws, int64_t qs, int w_dtype,
+                         hipStream_t stream);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -227,4 +234,89 @@ MI355_EXPORT int mi355_gate_up_silu_fwd(const void* x, const void* w_gate, const
   return mi355::gate_up_silu_launch(x, w_gate, w_up, out, static_cast<int>(rows), static_cast<int>(k),
                                     static_cast<int>(n_out), x_row_stride, w_row_stride, out_row_stride, dtype,
                                     out_dtype, static_cast<hipStream_t>(stream));
+}
+
+MI355_EXPORT int mi355_w8a16_linear_fwd(const void* x, const void* w_q, const void* scale, const void* bias,
+                                        void* out, int64_t rows, int64_t k, int64_t n, int64_t x_row_stride,
+                                        int64_t w_row_stride, int64_t out_row_stride, int x_dtype, int scale_dtype,
+                                        int bias_dtype, int out_dtype, void* stream) {
+  static const char* fn = "mi355_w8a16_linear_fwd";
+  mi355::g_error[0] = '\0';
+  if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype) || !valid_dtype(out_dtype) ||
+      (bias != nullptr && !valid_dtype(bias_dtype))) {
+    set_error("%s: unknown dtype code (x=%d, scale=%d, bias=%d, out=%d)", fn, x_dtype, scale_dtype, bias_dtype,
+              out_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (x_dtype == MI355_F32) {
+    set_error("%s: x must be fp16 or bf16 (MFMA operand)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (out_dtype != x_dtype && out_dtype != MI355_F32) {
+    set_error("%s: out dtype must equal x dtype or be fp32 (x=%d, out=%d)", fn, x_dtype, out_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows < 0 || n < 0 || k < 1) {
+    set_error("%s: need rows >= 0, n >= 0, k >= 1 (got %lld, %lld, %lld)", fn, static_cast<long long>(rows),
+              static_cast<long long>(n), static_cast<long long>(k));
+    return MI355_ERR_INVALID;
+  }
+  if (x_row_stride < k || w_row_stride < k || out_row_stride < n) {
+    set_error("%s: row strides must be >= k (x, w_q) and >= n (out)", fn);
+    return MI355_ERR_INVALID;
+  }
+  if (rows == 0 || n == 0) return MI355_OK;
+  if (x == nullptr || w_q == nullptr || scale == nullptr || out == nullptr) {
+    set_error("%s: null pointer", fn);
+    return MI355_ERR_INVALID;
+  }
+  // Buffer descriptors span at most 128 rows of x or of w_q (< 2^32 bytes);
+  // grids hold ceil(n / 128) x ceil(rows / 64) workgroups or more.
+  if (x_row_stride >= (int64_t{1} << 23) || w_row_stride >= (int64_t{1} << 24) || n > 0x7fffffff - 128 ||
+      rows > int64_t{65535} * 64) {
+    set_error("%s: size beyond the kernel's limits (x_row_stride < 2^23, w_row_stride < 2^24, n < 2^31 - 128, "
+              "rows <= 4194240)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (n * ((rows + 3) / 4) > int64_t{0x7fffffff} * 4) {
+    set_error("%s: n * rows too large for one launch", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows - 1 > (INT64_MAX - n) / out_row_stride) {
+    set_error("%s: rows * out_row_stride overflows int64", fn);
+    return MI355_ERR_INVALID;
+  }
+  return mi355::w8a16_launch(x, w_q, scale, bias, out, static_cast<int>(rows), static_cast<int>(k),
+                             static_cast<int>(n), x_row_stride, w_row_stride, out_row_stride, x_dtype, scale_dtype,
+                             bias_dtype, out_dtype, static_cast<hipStream_t>(stream));
+}
+
+MI355_EXPORT int mi355_quantize_int8_fwd(const void* w, void* w_q, void* scale, int64_t n, int64_t k,
+                                         int64_t w_row_stride, int64_t q_row_stride, int w_dtype, void* stream) {
+  static const char* fn = "mi355_quantize_int8_fwd";
+  mi355::g_error[0] = '\0';
+  if (!valid_dtype(w_dtype)) {
+    set_error("%s: unknown dtype code %d", fn, w_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (n < 0 || k < 1 || k > 0x7fffffff) {
+    set_error("%s: need n >= 0 and 1 <= k < 2^31 (got %lld, %lld)", fn, static_cast<long long>(n),
+              static_cast<long long>(k));
+    return MI355_ERR_INVALID;
+  }
+  if (w_row_stride < k || q_row_stride < k) {
+    set_error("%s: row strides must be >= k", fn);
+    return MI355_ERR_INVALID;
+  }
+  if (n == 0) return MI355_OK;
+  if (w == nullptr || w_q == nullptr || scale == nullptr) {
+    set_error("%s: null pointer", fn);
+    return MI355_ERR_INVALID;
+  }
+  if ((n + 3) / 4 > 0x7fffffff || n - 1 > (INT64_MAX - k) / (w_row_stride > q_row_stride ? w_row_stride : q_row_stride)) {
+    set_error("%s: n too large", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  return mi355::quantize_int8_launch(w, w_q, scale, n, static_cast<int>(k), w_row_stride, q_row_stride, w_dtype,
+                                     static_cast<hipStream_t>(stream));
 }

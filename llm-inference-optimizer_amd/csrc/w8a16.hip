@@ -1,0 +1,492 @@
+// Weight-only int8 linear (W8A16) and the int8 weight quantiser for gfx950,
+// with their launchers.
+//
+//   out[m, n] = round(acc * scale[n] + bias[n]),  acc = sum_k x[m, k] * q[n, k]
+//
+// Semantics follow the reference's Triton kernel
+// (src/kernels/w8a16_matmul_triton.py:64-86): the integer weights meet x in
+// 16-bit floating point (every int8 is exact in fp16 and in bf16, and so is
+// every product in the fp32 accumulator), the per-output-channel scale is
+// applied once to the fp32 accumulator, then the bias (fp32), then one
+// rounding to the output type.  Here scale and bias go through one fma.
+//
+// Three kernels, picked by the launcher:
+//   w8a16_skinny   rows <= 32 (decode): weight streaming.  Every weight byte is
+//                  read once per call at HBM bandwidth and meets up to 32 rows
+//                  of x on MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
+//   w8a16_tiled    more rows (prefill): an LDS-tiled MFMA GEMM; the int8 tile
+//                  is widened to fp16/bf16 once, on its way into LDS, and shared
+//                  by every wave of the workgroup.
+//   w8a16_generic  any k, stride or alignment the two above cannot take:
+//                  one wave per (output feature, 4 rows of x), fp32 fma.
+//
+// And the quantiser of QuantizedLinearInt8.from_linear
+// (src/quantization/int8.py:45-50), one wave per weight row:
+//   amax = max_k |w|,  scale = max(amax / 127, 1e-8),
+//   q = clamp(rint(w / scale), -127, 127)   (IEEE fp32 division, ties to even)
+// which is bit-identical to the reference's torch expression.
+//
+// Skinny operand layout.  The 16x16x32 MFMA's B operand gives lane l column
+// n = l % 16 and k-group l / 16 (8 consecutive k).  Each lane loads 16 int8
+// weights (one 16-byte load): weight row n % 8, columns 64 * (n / 8) +
+// 16 * (l / 16) .. + 16 of a 128-column block, so the 8 lanes of a weight row
+// cover 128 contiguous bytes (full cache lines).  The first 8 of the 16
+// weights feed one MFMA and the last 8 a second one.  The A operand stacks
+// the 8 rows of an x tile twice, row i = x row i % 8 over half i / 8 of the
+// block, with the same lane -> column map, so
+//   D[i][n] = sum over the block half of x[i % 8] * w[n % 8]  when i / 8 == n / 8
+// and the product of x row a with weight row b is D[a][b] + D[a + 8][b + 8]
+// (the off-diagonal quarters are discarded; for up to 8 rows of x they cost
+// nothing, A rows 8..15 would otherwise be padding).  D layout of the gfx950
+// 16x16x32 MFMA: lane l holds rows 4 * (l / 16) + j, j < 4, of column l % 16.
+//
+// Decomposition: a workgroup owns 8 weight rows and a tile of 8 * MT rows of x
+// (blockIdx.y) and splits the 128-column blocks of K between its waves
+// (contiguous ranges); each wave keeps U blocks of loads in flight.  Blocks
+// and 16-byte pieces past k address past the buffer descriptors (zeros, no
+// traffic), so any k that is a multiple of 16 needs no remainder loop.  The
+// per-wave partial sums meet in LDS in a fixed order.
+#include "common.h"
+
+namespace mi355 {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Offset that lies past every descriptor the launcher admits (< 2^31 bytes).
+constexpr uint32_t kOob = 0xfffffff0u;
+constexpr int kMaxSplit = 16;  // waves per skinny workgroup
+
+template <typename T> __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma16<F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma16<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// Four int8 (one dword, byte i = element i) -> four values of T in two dwords
+// (element 2j in the low half of dword j).  Exact: |q| <= 128.
+template <typename T> __device__ __forceinline__ u32x2 widen_i8x4(uint32_t d);
+template <> __device__ __forceinline__ u32x2 widen_i8x4<F16>(uint32_t d) {
+  // Bias each byte to u = q + 128 and splice it under the fp16 pattern 0x64:
+  // 0x64uu is 1024 + u exactly; subtracting 1152 leaves q.
+  const uint32_t u = d ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0,64,u1,64
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2,64,u3,64
+  const f16x2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+  const f16x2 a = __builtin_bit_cast(f16x2, lo) + off;
+  const f16x2 b = __builtin_bit_cast(f16x2, hi) + off;
+  return u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+}
+template <> __device__ __forceinline__ u32x2 widen_i8x4<BF16>(uint32_t d) {
+  // Signed byte -> fp32 (exact), then the upper half of each fp32 pattern is
+  // the bf16 pattern of the same (8-significant-bit) integer.
+  const float f0 = static_cast<float>(static_cast<int8_t>(d & 0xffu));
+  const float f1 = static_cast<float>(static_cast<int8_t>((d >> 8) & 0xffu));
+  const float f2 = static_cast<float>(static_cast<int8_t>((d >> 16) & 0xffu));
+  const float f3 = static_cast<float>(static_cast<int8_t>(d >> 24));
+  return u32x2{__builtin_amdgcn_perm(as_u32(f1), as_u32(f0), 0x07060302u),
+               __builtin_amdgcn_perm(as_u32(f3), as_u32(f2), 0x07060302u)};
+}
+
+// 16 int8 weights (one 16-byte load) -> the B operands of two MFMAs.
+template <typename T>
+__device__ __forceinline__ void widen_i8x16(u32x4 w, u32x4& b0, u32x4& b1) {
+  const u32x2 p0 = widen_i8x4<T>(w.x), p1 = widen_i8x4<T>(w.y);
+  const u32x2 p2 = widen_i8x4<T>(w.z), p3 = widen_i8x4<T>(w.w);
+  b0 = u32x4{p0.x, p0.y, p1.x, p1.y};
+  b1 = u32x4{p2.x, p2.y, p3.x, p3.y};
+}
+
+__device__ __forceinline__ float load_dyn(const void* p, int64_t i, int dt) {
+  if (dt == MI355_F16) return load_elem<F16>(p, i);
+  if (dt == MI355_BF16) return load_elem<BF16>(p, i);
+  return load_elem<F32>(p, i);
+}
+
+struct W8Params {
+  const void* x;      // [rows, xs] of T
+  const void* q;      // [n, qs] int8
+  const void* scale;  // [n] of sdt
+  const void* bias;   // [n] of bdt, or null
+  void* out;          // [rows, os] of TO
+  int rows, k, n;
+  int64_t xs, qs, os;  // row strides in elements
+  int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
+};
+
+// The epilogue shared by all kernels: scale once, then the bias, one rounding.
+template <typename TO>
+__device__ __forceinline__ void w8_store(const W8Params& p, int64_t m, int n, float acc) {
+  const float sc = load_dyn(p.scale, n, p.sdt);
+  const float v = p.bdt >= 0 ? __builtin_fmaf(acc, sc, load_dyn(p.bias, n, p.bdt)) : acc * sc;
+  store_elem<TO>(p.out, m * p.os + n, v);
+}
+
+// ------------------------------------------------------------------ skinny
+
+template <typename T, typename TO, int MT, int U>
+__global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p) {
+  using TB = typename T::bits;
+  extern __shared__ float red[];  // [nwave][MT][4][64]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwave = blockDim.x >> 6;
+  const int n0 = blockIdx.x * 8;
+  const int m0 = blockIdx.y * 8 * MT;
+  const int nrows_w = p.n - n0 < 8 ? p.n - n0 : 8;
+  const int nrows_x = p.rows - m0 < 8 * MT ? p.rows - m0 : 8 * MT;
+
+  // Descriptors end right after the last valid element, so weight rows past n
+  // and x rows past the tile (offset >= rows * stride >= the extent) read 0.
+  const rsrc_t rq = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
+                              static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  const rsrc_t rx = make_rsrc(static_cast<const TB*>(p.x) + static_cast<int64_t>(m0) * p.xs,
+                              static_cast<uint32_t>(((nrows_x - 1) * p.xs + p.k) * sizeof(TB)));
+
+  // Lane -> (row l % 8 of the operand, column 64 * ((l / 8) % 2) + 16 * (l / 16) of the block).
+  const int r8 = lane & 7;
+  const int col = ((lane >> 3) & 1) * 64 + (lane >> 4) * 16;
+  const uint32_t qoff = static_cast<uint32_t>(r8 * p.qs + col);
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xoff[t] = static_cast<uint32_t>(((8 * t + r8) * p.xs + col) * sizeof(TB));
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nblk = (p.k + 127) >> 7;
+  const int s_end = (nblk * (wave + 1)) / nwave;
+  for (int s = (nblk * wave) / nwave; s < s_end; s += U) {
+    u32x4 wq[U], xa[U][MT][2];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int c = 128 * (s + j) + col;
+      const bool live = s + j < s_end && c < p.k;
+      wq[j] = buf_load16(rq, live ? qoff + 128u * (s + j) : kOob);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const uint32_t o = xoff[t] + 256u * (s + j);
+        xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
+        xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      u32x4 b0, b1;
+      widen_i8x16<T>(wq[j], b0, b1);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        acc[t] = mfma16<T>(xa[j][t][0], b0, acc[t]);
+        acc[t] = mfma16<T>(xa[j][t][1], b1, acc[t]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[((wave * MT + t) * 4 + j) * 64 + lane] = acc[t][j];
+  }
+  __syncthreads();
+
+  // Output (x row 8t + a, weight row b) = D[a][b] + D[a + 8][b + 8]:
+  // register a % 4 of lanes 16 * (a / 4) + b and 16 * (a / 4) + 40 + b.
+  for (int o = threadIdx.x; o < 64 * MT; o += blockDim.x) {
+    const int b = o & 7, a = (o >> 3) & 7, t = o >> 6;
+    const int m = 8 * t + a;
+    if (m >= nrows_x || b >= nrows_w) continue;
+    const int l0 = 16 * (a >> 2) + b, j = a & 3;
+    float s = 0.f;
+    for (int w = 0; w < nwave; ++w) {
+      const float* r = red + ((w * MT + t) * 4 + j) * 64;
+      s += r[l0] + r[l0 + 40];
+    }
+    w8_store<TO>(p, m0 + m, n0 + b, s);
+  }
+}
+
+// ------------------------------------------------------------------- tiled
+//
+// Workgroup tile BM x BN of the output, K in steps of 64 columns, 4 waves in a
+// 2 x 2 grid, each computing (BM / 2) x (BN / 2) with 16x16x32 MFMAs.  Per K
+// step every thread loads its share of the x tile (16-byte pieces) and of the
+// int8 tile (16 weights per piece) into registers, widens the weights, and
+// stores both into the LDS buffer the waves read next; two LDS buffers, one
+// barrier per step.  LDS rows are padded by 16 bytes, so the 16-byte operand
+// reads of 8 consecutive rows fall in distinct banks.
+
+constexpr int kBK = 64;
+constexpr int kLdsRow = kBK + 8;  // elements per LDS row (144 bytes)
+
+template <typename T, typename TO, int BM, int BN>
+__global__ __launch_bounds__(256) void w8a16_tiled(const W8Params p) {
+  using TB = typename T::bits;
+  constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
+  constexpr int FM = WM / 16, FN = WN / 16; // MFMA tiles per wave
+  constexpr int XP = BM * kBK / 8 / 256;    // 16-byte x pieces per thread per step
+  constexpr int QP = BN * kBK / 16 / 256;   // 16-byte int8 pieces per thread per step
+  static_assert(XP >= 1 && QP >= 1, "tile too small for 256 threads");
+  __shared__ __attribute__((aligned(16))) TB xs_lds[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) TB ws_lds[2][BN * kLdsRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = blockIdx.x * BN;
+  const int m0 = blockIdx.y * BM;
+  const int nrows_w = p.n - n0 < BN ? p.n - n0 : BN;
+  const int nrows_x = p.rows - m0 < BM ? p.rows - m0 : BM;
+  const rsrc_t rq = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
+                              static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  const rsrc_t rx = make_rsrc(static_cast<const TB*>(p.x) + static_cast<int64_t>(m0) * p.xs,
+                              static_cast<uint32_t>(((nrows_x - 1) * p.xs + p.k) * sizeof(TB)));
+
+  // Piece i of this thread: x row (tid + 256 i) / 8, column 8 * ((tid + 256 i) % 8);
+  // int8 row (tid + 256 i) / 4, column 16 * ((tid + 256 i) % 4).
+  u32x4 xr[XP], qr[QP];
+  auto load_step = [&](int kt) {
+    const int kc = kt * kBK;
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int pc = tid + 256 * i;
+      const int c = kc + 8 * (pc & 7);
+      const uint32_t off = static_cast<uint32_t>(((pc >> 3) * p.xs + c) * sizeof(TB));
+      xr[i] = buf_load16_cached(rx, c < p.k ? off : kOob);
+    }
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+      const int pc = tid + 256 * i;
+      const int c = kc + 16 * (pc & 3);
+      const uint32_t off = static_cast<uint32_t>((pc >> 2) * p.qs + c);
+      qr[i] = buf_load16(rq, c < p.k ? off : kOob);
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int pc = tid + 256 * i;
+      *reinterpret_cast<u32x4*>(&xs_lds[buf][(pc >> 3) * kLdsRow + 8 * (pc & 7)]) = xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+      const int pc = tid + 256 * i;
+      u32x4 b0, b1;
+      widen_i8x16<T>(qr[i], b0, b1);
+      TB* dst = &ws_lds[buf][(pc >> 2) * kLdsRow + 16 * (pc & 3)];
+      reinterpret_cast<u32x4*>(dst)[0] = b0;
+      reinterpret_cast<u32x4*>(dst)[1] = b1;
+    }
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int nk = (p.k + kBK - 1) / kBK;
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+  // Operand reads: lane l -> row l % 16 of the MFMA tile, k-group l / 16.
+  const int orow = lane & 15, ocol = 8 * (lane >> 4);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_step(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      u32x4 a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        a[i] = *reinterpret_cast<const u32x4*>(&xs_lds[buf][(wm * WM + 16 * i + orow) * kLdsRow + 32 * ks + ocol]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        b[j] = *reinterpret_cast<const u32x4*>(&ws_lds[buf][(wn * WN + 16 * j + orow) * kLdsRow + 32 * ks + ocol]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<T>(a[i], b[j], acc[i][j]);
+      }
+    }
+    if (kt + 1 < nk) store_step(buf ^ 1);
+    __syncthreads();
+  }
+
+  // D of tile (i, j): lane l holds rows 4 * (l / 16) + r, r < 4, of column l % 16.
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = wn * WN + 16 * j + (lane & 15);
+    if (n >= nrows_w) continue;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = wm * WM + 16 * i + 4 * (lane >> 4) + r;
+        if (m < nrows_x) w8_store<TO>(p, m0 + m, n0 + n, acc[i][j][r]);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------- generic
+
+constexpr int kGenRows = 4;  // rows of x per wave
+
+template <typename T, typename TO>
+__global__ __launch_bounds__(256) void w8a16_generic(const W8Params p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t mblocks = (p.rows + kGenRows - 1) / kGenRows;
+  if (gw >= static_cast<int64_t>(p.n) * mblocks) return;
+  const int n = static_cast<int>(gw % p.n);
+  const int64_t m0 = (gw / p.n) * kGenRows;
+  const int8_t* qrow = static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n) * p.qs;
+  float acc[kGenRows] = {0.f, 0.f, 0.f, 0.f};
+  for (int c = lane; c < p.k; c += 64) {
+    const float qv = static_cast<float>(qrow[c]);
+#pragma unroll
+    for (int i = 0; i < kGenRows; ++i) {
+      if (m0 + i < p.rows) acc[i] = __builtin_fmaf(load_elem<T>(p.x, (m0 + i) * p.xs + c), qv, acc[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kGenRows; ++i) {
+    const float s = wave_allreduce_sum(acc[i]);
+    if (lane == 0 && m0 + i < p.rows) w8_store<TO>(p, m0 + i, n, s);
+  }
+}
+
+// --------------------------------------------------------------- quantiser
+
+template <typename TW>
+__global__ __launch_bounds__(256) void quantize_int8_rows(const void* __restrict__ w, int8_t* __restrict__ q,
+                                                          float* __restrict__ scale, int64_t n, int k, int64_t ws,
+                                                          int64_t qs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= n) return;
+  float amax = 0.f;
+  for (int c = lane; c < k; c += 64) amax = __builtin_fmaxf(amax, __builtin_fabsf(load_elem<TW>(w, r * ws + c)));
+  // max is exact and order-free; the symmetric butterfly leaves it in every lane
+  amax = __builtin_fmaxf(amax, dpp_f32<0xb1>(amax));
+  amax = __builtin_fmaxf(amax, dpp_f32<0x4e>(amax));
+  amax = __builtin_fmaxf(amax, dpp_f32<0x141>(amax));
+  amax = __builtin_fmaxf(amax, dpp_f32<0x140>(amax));
+  {
+    const uint32_t b = as_u32(amax);
+    auto s = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const uint32_t lo = s[0], hi = s[1];
+    amax = __builtin_fmaxf(as_f32(lo), as_f32(hi));
+  }
+  {
+    const uint32_t b = as_u32(amax);
+    auto s = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    const uint32_t lo = s[0], hi = s[1];
+    amax = __builtin_fmaxf(as_f32(lo), as_f32(hi));
+  }
+  float sc = amax / 127.0f;  // IEEE division (HIP's default for fp32 '/')
+  if (sc < 1e-8f) sc = 1e-8f;
+  if (lane == 0) scale[r] = sc;
+  for (int c = lane; c < k; c += 64) {
+    float v = __builtin_rintf(load_elem<TW>(w, r * ws + c) / sc);
+    v = __builtin_fminf(__builtin_fmaxf(v, -127.0f), 127.0f);
+    q[r * qs + c] = static_cast<int8_t>(static_cast<int>(v));
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+
+template <typename K>
+int launch_w8(K kernel, dim3 grid, dim3 block, size_t lds, const W8Params& p, hipStream_t s) {
+  void* args[] = {const_cast<W8Params*>(&p)};
+  return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, args, lds, s),
+                    "w8a16 launch");
+}
+
+// Skinny launch shape: enough waves in flight to cover HBM latency (about 16
+// per CU) while each wave keeps whole 128-column blocks; U blocks of loads in
+// flight per wave.
+template <typename T, typename TO, int MT>
+int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
+  const int groups = (p.n + 7) / 8;
+  const int nblk = (p.k + 127) / 128;
+  int split = (16 * cus + groups - 1) / groups;
+  if (split > kMaxSplit) split = kMaxSplit;
+  if (split > nblk) split = nblk;
+  if (split < 1) split = 1;
+  const int per_wave = (nblk + split - 1) / split;
+  const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>((p.rows + 8 * MT - 1) / (8 * MT)));
+  const dim3 block(64 * split);
+  const size_t lds = static_cast<size_t>(split) * MT * 4 * 64 * sizeof(float);
+  if constexpr (MT <= 2) {  // 4 blocks in flight fit the registers of up to 16 rows of x
+    if (per_wave >= 4) return launch_w8(w8a16_skinny<T, TO, MT, 4>, grid, block, lds, p, s);
+  }
+  if (per_wave >= 2) return launch_w8(w8a16_skinny<T, TO, MT, 2>, grid, block, lds, p, s);
+  return launch_w8(w8a16_skinny<T, TO, MT, 1>, grid, block, lds, p, s);
+}
+
+template <typename T, typename TO>
+int w8_typed(const W8Params& p, hipStream_t s, int cus) {
+  const bool vec = p.k % 16 == 0 && p.qs % 16 == 0 && p.xs % 8 == 0 && aligned16(p.x) && aligned16(p.q);
+  if (!vec) {
+    const int64_t waves = static_cast<int64_t>(p.n) * ((p.rows + kGenRows - 1) / kGenRows);
+    return launch_w8(w8a16_generic<T, TO>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, p, s);
+  }
+  if (p.rows <= 8) return w8_skinny_shape<T, TO, 1>(p, s, cus);
+  if (p.rows <= 16) return w8_skinny_shape<T, TO, 2>(p, s, cus);
+  if (p.rows <= 24) return w8_skinny_shape<T, TO, 3>(p, s, cus);
+  if (p.rows <= 32) return w8_skinny_shape<T, TO, 4>(p, s, cus);
+  // Prefill: 128 x 128 tiles when they fill the chip, else 64 x 64.
+  const int64_t big = static_cast<int64_t>((p.n + 127) / 128) * ((p.rows + 127) / 128);
+  if (big >= cus) {
+    const dim3 grid(static_cast<unsigned>((p.n + 127) / 128), static_cast<unsigned>((p.rows + 127) / 128));
+    return launch_w8(w8a16_tiled<T, TO, 128, 128>, grid, dim3(256), 0, p, s);
+  }
+  const dim3 grid(static_cast<unsigned>((p.n + 63) / 64), static_cast<unsigned>((p.rows + 63) / 64));
+  return launch_w8(w8a16_tiled<T, TO, 64, 64>, grid, dim3(256), 0, p, s);
+}
+
+}  // namespace
+
+int w8a16_launch(const void* x, const void* q, const void* scale, const void* bias, void* out, int rows, int k,
+                 int n, int64_t xs, int64_t qs, int64_t os, int x_dtype, int scale_dtype, int bias_dtype,
+                 int out_dtype, hipStream_t stream) {
+  int cus = 0;
+  const int st = compute_units(&cus);
+  if (st != MI355_OK) return st;
+  const W8Params p{x, q, scale, bias, out, rows, k, n, xs, qs, os, scale_dtype, bias ? bias_dtype : -1};
+  if (x_dtype == MI355_F16 && out_dtype == MI355_F16) return w8_typed<F16, F16>(p, stream, cus);
+  if (x_dtype == MI355_F16 && out_dtype == MI355_F32) return w8_typed<F16, F32>(p, stream, cus);
+  if (x_dtype == MI355_BF16 && out_dtype == MI355_BF16) return w8_typed<BF16, BF16>(p, stream, cus);
+  if (x_dtype == MI355_BF16 && out_dtype == MI355_F32) return w8_typed<BF16, F32>(p, stream, cus);
+  set_error("mi355_w8a16_linear_fwd: unsupported dtype pair (x=%d, out=%d)", x_dtype, out_dtype);
+  return MI355_ERR_UNSUPPORTED;
+}
+
+int quantize_int8_launch(const void* w, void* q, void* scale, int64_t n, int k, int64_t ws, int64_t qs, int w_dtype,
+                         hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>((n + 3) / 4);
+  void* args[] = {const_cast<void**>(&w), &q, &scale, &n, &k, &ws, &qs};
+  const void* kern = nullptr;
+  if (w_dtype == MI355_F32) kern = reinterpret_cast<const void*>(quantize_int8_rows<F32>);
+  else if (w_dtype == MI355_F16) kern = reinterpret_cast<const void*>(quantize_int8_rows<F16>);
+  else if (w_dtype == MI355_BF16) kern = reinterpret_cast<const void*>(quantize_int8_rows<BF16>);
+  if (!kern) {
+    set_error("mi355_quantize_int8_fwd: unsupported weight dtype %d", w_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  return hip_status(hipLaunchKernel(kern, dim3(grid), dim3(256), args, 0, stream), "quantize_int8 launch");
+}
+
+}  // namespace mi355

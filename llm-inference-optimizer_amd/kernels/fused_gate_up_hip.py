@@ -57,8 +57,11 @@ def fused_gate_up_silu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor
     rows = x2.shape[0]
     out = torch.empty((rows, n_out), dtype=out_dtype, device=x.device)
     if rows and n_out:
+        # a single row's stride is arbitrary in torch (even 0); the kernel reads one row then
+        xs = x2.stride(0) if rows > 1 else k
+        ws = w_gate.stride(0) if n_out > 1 else k
         _lib.launch("mi355_gate_up_silu_fwd", dev, x2.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(),
-                    out.data_ptr(), rows, k, n_out, x2.stride(0), w_gate.stride(0), n_out,
+                    out.data_ptr(), rows, k, n_out, xs, ws, n_out,
                     _CODE[x.dtype], _CODE[out_dtype])
     return out.view(*x.shape[:-1], n_out)
 

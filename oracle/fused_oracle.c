@@ -27,6 +27,13 @@
  * without that intermediate rounding.  Projections are summed in fp64
  * (products of 16-bit values are exact there).
  *
+ * oracle_w8a16_linear restates the weight-only int8 linear of the
+ * reference's quantisation stage: the Triton kernel's order (integer dot
+ * product in fp32, then the per-output-channel scale, then the bias,
+ * src/kernels/w8a16_matmul_triton.py:64-86) and its dequantise-first
+ * reference (:137-149); oracle_quantize_int8 restates the quantiser that
+ * produces the int8 weights (src/quantization/int8.py:45-50).
+ *
  * Sum of squares: the reference reduces with tl.sum in fp32 in an order the
  * Triton backend picks (:43).  The oracle accumulates the exact squares in
  * fp64 and rounds the sum to fp32 once, i.e. the order-free fp32 sum; any
@@ -335,6 +342,114 @@ int oracle_gate_up_silu(const void* x, const void* wg, const void* wu, void* out
       }
       const float sig = 1.0f / (1.0f + expf(-gf));
       store_f(out, o, odt, (gf * sig) * uf);
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------ W8A16 weight-only int8 linear */
+
+enum { ORACLE_W8_KERNEL = 0, ORACLE_W8_DEQUANT = 1 };
+/* planted mistakes, W8A16 linear */
+enum {
+  ORACLE_MUT_W8_TRANSPOSE = 1,   /* read q as [k, n] instead of [n, k] */
+  ORACLE_MUT_W8_UNSIGNED = 2,    /* read the int8 weights as unsigned bytes */
+  ORACLE_MUT_W8_BIAS_FIRST = 3,  /* (acc + bias) * scale */
+  ORACLE_MUT_W8_NO_BIAS = 4,     /* drop the bias */
+  ORACLE_MUT_W8_SCALE_SHIFT = 5  /* scale of output feature (j + 1) % n */
+};
+
+/*
+ * out[m, j] for x [rows, k] (xdt), q [n, k] int8, scale [n] (sdt), bias [n]
+ * (bdt, or bdt < 0 for none).  The exact dot product of x with the integer
+ * weights is formed in fp64 (every product of a 16-bit float and an int8 is
+ * exact there) and:
+ *   KERNEL  (the Triton kernel, src/kernels/w8a16_matmul_triton.py:64-86):
+ *           acc = (float)sum_c x*q  -- fp32 accumulation, order-free --
+ *           out = round_odt(fmaf(acc, scale, bias))  or  round_odt(acc * scale)
+ *           (the scale is applied once to the accumulator, then the bias).
+ *   DEQUANT (w8a16_reference, :137-149): wf = (float)q * scale (fp32, one
+ *           rounding per weight), out = round_odt((float)sum_c x*wf + bias):
+ *           the fp32 linear of the dequantised matrix, order-free.
+ * Optional fp64 outputs (NULL to skip): out64 = sum x*q*scale + bias,
+ * absacc = sum |x*q| (scale of the fp32 accumulation error).
+ * Returns 0, or -1 on a bad argument.
+ */
+int oracle_w8a16_linear(const void* x, const int8_t* q, const void* scale, const void* bias, void* out,
+                        double* out64, double* absacc, int64_t rows, int64_t k, int64_t n, int xdt, int sdt,
+                        int bdt, int odt, int mode, int mutate) {
+  if (!valid_dt(xdt) || !valid_dt(sdt) || !valid_dt(odt) || (bdt >= 0 && !valid_dt(bdt)) || rows < 0 || k < 1 ||
+      n < 1)
+    return -1;
+  const int has_bias = bdt >= 0 && bias != NULL && mutate != ORACLE_MUT_W8_NO_BIAS;
+  for (int64_t m = 0; m < rows; ++m) {
+    for (int64_t j = 0; j < n; ++j) {
+      const int64_t js = (mutate == ORACLE_MUT_W8_SCALE_SHIFT) ? (j + 1) % n : j;
+      const float sc = load_f(scale, js, sdt);
+      const float bs = has_bias ? load_f(bias, j, bdt) : 0.0f;
+      double acc = 0.0, aabs = 0.0, deq = 0.0;
+      for (int64_t c = 0; c < k; ++c) {
+        const int64_t wi = (mutate == ORACLE_MUT_W8_TRANSPOSE) ? c * n + j : j * k + c;
+        const double qv = (mutate == ORACLE_MUT_W8_UNSIGNED) ? (double)(uint8_t)q[wi] : (double)q[wi];
+        const double xv = (double)load_f(x, m * k + c, xdt);
+        acc += xv * qv;
+        aabs += fabs(xv * qv);
+        deq += xv * (double)((float)qv * sc);
+      }
+      const int64_t o = m * n + j;
+      if (out64) out64[o] = acc * (double)sc + (double)bs;
+      if (absacc) absacc[o] = aabs;
+      float v;
+      if (mode == ORACLE_W8_DEQUANT) {
+        v = (float)deq + bs;
+      } else if (mutate == ORACLE_MUT_W8_BIAS_FIRST) {
+        v = ((float)acc + bs) * sc;
+      } else {
+        v = has_bias ? fmaf((float)acc, sc, bs) : (float)acc * sc;
+      }
+      store_f(out, o, odt, v);
+    }
+  }
+  return 0;
+}
+
+/* planted mistakes, int8 quantizer */
+enum {
+  ORACLE_MUT_Q8_TRUNC = 1,   /* truncate toward zero instead of rounding */
+  ORACLE_MUT_Q8_HALF_UP = 2, /* round halves away from zero */
+  ORACLE_MUT_Q8_BY_128 = 3,  /* scale = amax / 128 */
+  ORACLE_MUT_Q8_NO_CLAMP = 4 /* no 1e-8 floor on the scale */
+};
+
+/*
+ * Per-output-channel symmetric int8 quantisation of w [n, k] (wdt), the
+ * reference's QuantizedLinearInt8.from_linear (src/quantization/int8.py:45-50):
+ *   wf = (float)w;  amax = max_c |wf|;  scale = max(amax / 127, 1e-8)   (fp32)
+ *   q  = clamp(round_half_even(wf / scale), -127, 127)                  (fp32 divide)
+ * Rows of finite weights only (NaN / Inf propagate as the arithmetic gives).
+ * Returns 0, or -1 on a bad argument.
+ */
+int oracle_quantize_int8(const void* w, int8_t* q, float* scale, int64_t n, int64_t k, int wdt, int mutate) {
+  if (!valid_dt(wdt) || n < 0 || k < 1) return -1;
+  const float floor_ = 1e-8f;
+  for (int64_t j = 0; j < n; ++j) {
+    float amax = 0.0f;
+    for (int64_t c = 0; c < k; ++c) {
+      const float a = fabsf(load_f(w, j * k + c, wdt));
+      if (a > amax) amax = a;
+    }
+    float sc = amax / ((mutate == ORACLE_MUT_Q8_BY_128) ? 128.0f : 127.0f);
+    if (mutate != ORACLE_MUT_Q8_NO_CLAMP && sc < floor_) sc = floor_; /* torch.clamp keeps NaN */
+    scale[j] = sc;
+    for (int64_t c = 0; c < k; ++c) {
+      const float t = load_f(w, j * k + c, wdt) / sc;
+      float r;
+      if (mutate == ORACLE_MUT_Q8_TRUNC) r = truncf(t);
+      else if (mutate == ORACLE_MUT_Q8_HALF_UP) r = roundf(t);
+      else r = rintf(t);
+      if (r > 127.0f) r = 127.0f;
+      if (r < -127.0f) r = -127.0f;
+      q[j * k + c] = (int8_t)r;
     }
   }
   return 0;

@@ -23,6 +23,12 @@ Contents
   the reference's FusedMLP chain (projections rounded to x's type,
   src/engine/fused_norm_activation_patch.py:60-64), with the fp64 values and
   the |x|.|w| scales that bound fp32 accumulation error;
+* :func:`w8a16_linear`: the weight-only int8 linear -- the Triton kernel's
+  order (integer dot product, then the per-channel scale, then the bias,
+  src/kernels/w8a16_matmul_triton.py:64-86) or its dequantise-first
+  reference (:137-149) -- with the fp64 value and sum |x * q|;
+* :func:`quantize_int8`: the per-output-channel int8 quantiser
+  (src/quantization/int8.py:45-50);
 * :func:`naive_rmsnorm_torch` / :func:`naive_silu_mul_torch`: the reference's
   naive PyTorch path restated as the same torch op sequence, which bench.py
   times on the host cores as the CPU baseline.
@@ -58,6 +64,9 @@ MUT_RMS = {"n_minus_1": 1, "no_eps": 2, "sqrt": 3, "no_weight": 4, "w_reversed":
 MUT_SILU = {"sign": 1, "swap": 2, "no_up": 3, "round2": 4}
 MUT_GU = {"transpose": 1, "swap": 2, "drop_tail": 3, "row_shift": 4}
 GU_MODE = {"fused": 0, "unfused": 1}
+W8_MODE = {"kernel": 0, "dequant": 1}
+MUT_W8 = {"transpose": 1, "unsigned": 2, "bias_first": 3, "no_bias": 4, "scale_shift": 5}
+MUT_Q8 = {"trunc": 1, "half_up": 2, "by_128": 3, "no_clamp": 4}
 
 _lib = None
 
@@ -96,6 +105,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_silu_mul_f64.restype = i32
         L.oracle_gate_up_silu.argtypes = [vp] * 9 + [i64, i64, i64, i32, i32, i32, i32]
         L.oracle_gate_up_silu.restype = i32
+        L.oracle_w8a16_linear.argtypes = [vp] * 7 + [i64, i64, i64, i32, i32, i32, i32, i32, i32]
+        L.oracle_w8a16_linear.restype = i32
+        L.oracle_quantize_int8.argtypes = [vp, vp, vp, i64, i64, i32, i32]
+        L.oracle_quantize_int8.restype = i32
         for name in ("oracle_f32_to_f16_n", "oracle_f16_to_f32_n", "oracle_f32_to_bf16_n", "oracle_bf16_to_f32_n"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
@@ -234,6 +247,59 @@ def gate_up_silu(x: np.ndarray, wg: np.ndarray, wu: np.ndarray, *, dt: str, odt:
     if st != 0:
         raise ValueError("oracle_gate_up_silu rejected its arguments")
     return res
+
+
+# ------------------------------------------- W8A16 weight-only int8 linear
+
+def w8a16_linear(x: np.ndarray, q: np.ndarray, scale: np.ndarray, bias: np.ndarray | None = None, *, xdt: str,
+                 sdt: str = "f32", bdt: str | None = None, odt: str | None = None, mode: str = "kernel",
+                 mutate: str | None = None) -> dict:
+    """x: [rows, k] (xdt storage), q: [n, k] int8, scale: [n] (sdt storage),
+    bias: [n] (bdt storage) or None.  Returns a dict with ``out`` ([rows, n],
+    odt storage, the ``mode`` formula), ``out64`` (fp64 exact) and ``absacc``
+    (sum_k |x * q|, fp64)."""
+    x = _arr(x, xdt)
+    q = np.ascontiguousarray(q)
+    if q.dtype != np.int8:
+        raise TypeError(f"q must be int8, got {q.dtype}")
+    scale = _arr(scale, sdt)
+    if x.ndim != 2 or q.ndim != 2 or q.shape[1] != x.shape[1] or scale.shape != (q.shape[0],):
+        raise ValueError(f"bad shapes x={x.shape} q={q.shape} scale={scale.shape}")
+    rows, k = x.shape
+    n = q.shape[0]
+    if bias is not None:
+        bdt = bdt or xdt
+        bias = _arr(bias, bdt)
+        if bias.shape != (n,):
+            raise ValueError(f"bias must be [{n}], got {bias.shape}")
+    odt = odt or xdt
+    res = {"out": np.empty((rows, n), dtype=_np_dtype(odt)), "out64": np.empty((rows, n), np.float64),
+           "absacc": np.empty((rows, n), np.float64)}
+    mut = 0 if mutate is None else MUT_W8[mutate]
+    st = lib().oracle_w8a16_linear(_ptr(x), _ptr(q), _ptr(scale), _ptr(bias) if bias is not None else None,
+                                   _ptr(res["out"]), _ptr(res["out64"]), _ptr(res["absacc"]), rows, k, n,
+                                   DT_CODE[xdt], DT_CODE[sdt], DT_CODE[bdt] if bias is not None else -1,
+                                   DT_CODE[odt], W8_MODE[mode], mut)
+    if st != 0:
+        raise ValueError("oracle_w8a16_linear rejected its arguments")
+    return res
+
+
+def quantize_int8(w: np.ndarray, *, wdt: str, mutate: str | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """Per-output-channel symmetric int8 quantisation of w [n, k] (wdt
+    storage), as QuantizedLinearInt8.from_linear (src/quantization/int8.py:45-50).
+    Returns (q int8 [n, k], scale float32 [n])."""
+    w = _arr(w, wdt)
+    if w.ndim != 2:
+        raise ValueError(f"w must be 2-D, got {w.shape}")
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    scale = np.empty((n,), np.float32)
+    mut = 0 if mutate is None else MUT_Q8[mutate]
+    st = lib().oracle_quantize_int8(_ptr(w), _ptr(q), _ptr(scale), n, k, DT_CODE[wdt], mut)
+    if st != 0:
+        raise ValueError("oracle_quantize_int8 rejected its arguments")
+    return q, scale
 
 
 def f32_to_f16(a: np.ndarray) -> np.ndarray:

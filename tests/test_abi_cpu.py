@@ -192,3 +192,62 @@ def test_fused_add_rmsnorm_asserts_on_host_tensors(pkg):
     x = torch.randn(4, 64, dtype=torch.float16)
     with pytest.raises(AssertionError):
         pkg.fused_add_rmsnorm(x, x, torch.ones(64, dtype=torch.float16))
+
+
+# (x, w_q, scale, bias, out, rows, k, n, x_row_stride, w_row_stride, out_row_stride,
+#  x_dtype, scale_dtype, bias_dtype, out_dtype)
+@pytest.mark.parametrize("args,code,msg", [
+    ((P, P, P, 0, P, 8, 64, 32, 64, 64, 32, 5, 0, 0, 1), -1, "unknown dtype"),
+    ((P, P, P, P, P, 8, 64, 32, 64, 64, 32, 1, 0, 9, 1), -1, "unknown dtype"),
+    ((P, P, P, 0, P, 8, 64, 32, 64, 64, 32, 0, 0, 0, 0), -2, "fp16 or bf16"),
+    ((P, P, P, 0, P, 8, 64, 32, 64, 64, 32, 1, 0, 0, 2), -2, "out dtype"),
+    ((P, P, P, 0, P, -1, 64, 32, 64, 64, 32, 1, 0, 0, 1), -1, "need rows"),
+    ((P, P, P, 0, P, 8, 0, 32, 64, 64, 32, 1, 0, 0, 1), -1, "need rows"),
+    ((P, P, P, 0, P, 8, 64, 32, 63, 64, 32, 1, 0, 0, 1), -1, "row strides"),
+    ((P, P, P, 0, P, 8, 64, 32, 64, 32, 32, 1, 0, 0, 1), -1, "row strides"),
+    ((P, P, P, 0, P, 8, 64, 32, 64, 64, 31, 1, 0, 0, 1), -1, "row strides"),
+    ((P, P, 0, 0, P, 8, 64, 32, 64, 64, 32, 1, 0, 0, 1), -1, "null pointer"),
+    ((P, P, P, 0, P, 8, 64, 32, 2**23, 64, 32, 1, 0, 0, 1), -2, "limits"),
+    ((P, P, P, 0, P, 8, 64, 32, 64, 2**24, 32, 1, 0, 0, 1), -2, "limits"),
+    ((P, P, P, 0, P, 65535 * 64 + 1, 64, 32, 64, 64, 32, 1, 0, 0, 1), -2, "limits"),
+])
+def test_w8a16_abi_rejects(lib, args, code, msg):
+    st = lib.mi355_w8a16_linear_fwd(*args, None)
+    assert st == code
+    assert msg in lib.mi355_last_error().decode()
+
+
+def test_w8a16_abi_empty_is_noop(lib):
+    assert lib.mi355_w8a16_linear_fwd(0, 0, 0, 0, 0, 0, 64, 32, 64, 64, 32, 1, 0, 0, 1, None) == 0
+    assert lib.mi355_w8a16_linear_fwd(0, 0, 0, 0, 0, 8, 64, 0, 64, 64, 0, 2, 0, 0, 2, None) == 0
+    assert lib.mi355_last_error().decode() == ""
+
+
+# (w, w_q, scale, n, k, w_row_stride, q_row_stride, w_dtype)
+@pytest.mark.parametrize("args,code,msg", [
+    ((P, P, P, 4, 64, 64, 64, 3), -1, "unknown dtype"),
+    ((P, P, P, -1, 64, 64, 64, 1), -1, "need n"),
+    ((P, P, P, 4, 0, 64, 64, 1), -1, "need n"),
+    ((P, P, P, 4, 64, 32, 64, 1), -1, "row strides"),
+    ((P, P, P, 4, 64, 64, 60, 1), -1, "row strides"),
+    ((P, 0, P, 4, 64, 64, 64, 0), -1, "null pointer"),
+])
+def test_quantize_int8_abi_rejects(lib, args, code, msg):
+    st = lib.mi355_quantize_int8_fwd(*args, None)
+    assert st == code
+    assert msg in lib.mi355_last_error().decode()
+
+
+def test_quantize_int8_abi_empty_is_noop(lib):
+    assert lib.mi355_quantize_int8_fwd(0, 0, 0, 0, 64, 64, 64, 1, None) == 0
+
+
+def test_w8a16_launchers_assert_on_host_tensors(pkg):
+    x = torch.randn(4, 64, dtype=torch.float16)
+    q = torch.zeros(16, 64, dtype=torch.int8)
+    with pytest.raises(AssertionError):
+        pkg.w8a16_linear(x, q, torch.ones(16))
+    with pytest.raises(AssertionError):
+        pkg.quantize_int8_weight(torch.randn(16, 64))
+    with pytest.raises(AssertionError):
+        pkg.QuantizedLinearInt8.from_linear(torch.nn.Linear(64, 16))
