@@ -61,7 +61,8 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up"],
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up",
+                                      "w8a16"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e", action="store_true",
@@ -149,6 +150,21 @@ class Ctx:
                 self.L.check("mi355_gate_up_silu_fwd", st)
         return call
 
+    def w8a16_call(self, x, q, scale, out, bias=None):
+        M, K = x.shape
+        N = q.shape[0]
+        code = self.L.DTYPE_CODE[x.dtype]
+        f = self.lib.mi355_w8a16_linear_fwd
+        args = (x.data_ptr(), q.data_ptr(), scale.data_ptr(), bias.data_ptr() if bias is not None else None,
+                out.data_ptr(), M, K, N, K, K, N, code, self.L.DTYPE_CODE[scale.dtype],
+                self.L.DTYPE_CODE[bias.dtype] if bias is not None else 0, code)
+
+        def call():
+            st = f(*args, self.stream)
+            if st:
+                self.L.check("mi355_w8a16_linear_fwd", st)
+        return call
+
     def copy_call(self, src, dst):
         f = self.probe.mi355_probe_copy
         args = (src.data_ptr(), dst.data_ptr(), src.numel() * src.element_size(), 0)
@@ -171,6 +187,25 @@ def rand(ctx, shape, seed, dtype, mean=0.0, std=1.0):
 
 def n_sets(bytes_per_set: int) -> int:
     return max(1, -(-MIN_FOOTPRINT // bytes_per_set))
+
+
+def spin_up(ctx, calls, ms=30.0):
+    """Launches `calls` (cycled) for about `ms` of device time, untimed: the
+    first launches after host-side setup run below full clocks, and a pass
+    over freshly generated buffers pays for their write-backs."""
+    torch = ctx.torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    n = 0
+    while True:
+        for c in calls:
+            c()
+        n += len(calls)
+        end.record()
+        end.synchronize()
+        if start.elapsed_time(end) >= ms or n > 100000:
+            return
 
 
 def time_loop(ctx, calls, iters, warmup=5):
@@ -496,6 +531,7 @@ def main():
         result["c4"] = bench_c4(ctx, iters=60)
         result["decode"] = bench_decode(ctx)
         result["gate_up_silu"] = bench_gate_up(ctx)
+        result["w8a16"] = bench_w8a16(ctx)
         result["copy_ceiling"] = bench_copy(ctx)
 
     if not args.skip_cpu:
@@ -532,6 +568,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up(ctx, shapes=GATE_UP_SHAPES[1:2], iters=iters, baselines=False)))
+    elif args.only == "w8a16":
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_w8a16(ctx)))
 
 
 def bench_add_rms(ctx, iters):
@@ -708,6 +748,71 @@ def bench_gate_up(ctx, shapes=GATE_UP_SHAPES, iters=400, baselines=True):
         res[key] = entry
         log(f"  gate_up {key}: {entry}")
         del ws, outs, fused
+        torch.cuda.empty_cache()
+    return res
+
+
+# (M, K, N, dtype name, label): the reference's stage-7 kernel benchmark shapes
+# (benchmarks/run_stage7_kernel.py:33-39, Qwen2.5-1.5B projections, M in
+# {1, 8, 128, 1024}) plus Qwen2.5-7B MLP decode shapes in bf16.
+W8A16_SHAPES = [(M, K, N, "f16", lab) for K, N, lab in ((1536, 1536, "q/o proj"), (1536, 256, "k/v proj"),
+                                                         (1536, 8960, "gate/up proj"), (8960, 1536, "down proj"))
+                for M in (1, 8, 128, 1024)] + [(8, 3584, 18944, "bf16", "7b gate/up proj"),
+                                               (8, 18944, 3584, "bf16", "7b down proj")]
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16
+
+
+def bench_w8a16(ctx, shapes=W8A16_SHAPES, iters=300, baselines=True):
+    """Weight-only int8 linear (the reference's stage-7 path): the W8A16
+    kernel against an fp16/bf16 torch.matmul (hipBLASLt) on the same shape,
+    as the reference's run_stage7_kernel.py compares against cuBLAS.  Both
+    rotate per-layer weight sets with a footprint above 1 GiB (cold HBM).
+    Algorithmic bytes: int8 weights + fp32 scales + x + out; flops 2*M*N*K."""
+    torch = ctx.torch
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
+    res = {}
+    for M, K, N, dname, label in shapes:
+        dt = dts[dname]
+        nbytes = N * K + 4 * N + M * K * 2 + M * N * 2
+        flops = 2.0 * M * N * K
+        sets = min(512, n_sets(N * K))
+        x = rand(ctx, (M, K), 1700 + M, dt)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(1800 + K + N)
+        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets)]
+        scales = [(torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
+        outs = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(min(sets, 8))]
+        calls = [ctx.w8a16_call(x, q, sc, outs[i % len(outs)]) for i, (q, sc) in enumerate(zip(qs, scales))]
+        spin_up(ctx, calls)
+        us = time_loop(ctx, calls, iters)
+        us_graph = time_graph(ctx, calls, max(2 * sets, 64) if sets <= 256 else sets)
+        kname = "w8a16_skinny" if M <= 32 else "w8a16_tiled"
+        entry = kernel_entry(kname, nbytes, min(us, us_graph),
+                             {"layer": label, "M": M, "K": K, "N": N, "dtype": dname, "weight_sets": sets,
+                              "eager_us": round(us, 3), "graph_us": round(us_graph, 3),
+                              "TFLOPs": round(flops / min(us, us_graph) / 1e6, 2)})
+        entry["frac_of_mfma_peak"] = round(entry["TFLOPs"] / MFMA_PEAK_TFLOPS, 4)
+        del qs, scales, calls
+        torch.cuda.empty_cache()
+        if baselines:
+            bsets = min(512, n_sets(N * K * 2))
+            ws = [rand(ctx, (N, K), 1900 + i, dt, std=0.02) for i in range(bsets)]
+
+            def mm(w, o):
+                return lambda: torch.matmul(x, w.T, out=o)
+
+            base = [mm(w, outs[i % len(outs)]) for i, w in enumerate(ws)]
+            spin_up(ctx, base)
+            b_us = time_loop(ctx, base, iters)
+            b_graph = time_graph(ctx, base, max(2 * bsets, 64) if bsets <= 256 else bsets)
+            b = min(b_us, b_graph)
+            entry.update({"fp16_matmul_us": round(b, 3), "speedup_vs_fp16_matmul": round(b / entry["us"], 3)})
+            del ws, base
+        res[f"{label.replace(' ', '_').replace('/', '')}_M{M}_{dname}"] = entry
+        log(f"  w8a16 {label} M={M} K={K} N={N} {dname}: {entry['us']:.2f} us, {entry['GBps']:.0f} GB/s "
+            f"({entry['frac_of_peak']:.1%}), {entry['TFLOPs']:.1f} TFLOP/s; fp16 matmul "
+            f"{entry.get('fp16_matmul_us', float('nan')):.2f} us")
+        del outs
         torch.cuda.empty_cache()
     return res
 

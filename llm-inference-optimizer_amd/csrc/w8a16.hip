@@ -13,7 +13,8 @@
 // Three kernels, picked by the launcher:
 //   w8a16_skinny   rows <= 32 (decode): weight streaming.  Every weight byte is
 //                  read once per call at HBM bandwidth and meets up to 32 rows
-//                  of x on MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
+//                  of x on MFMA (v_mfma_f32_16x16x32_{f16,bf16}).  Also used
+//                  for a few 32-row tiles when the tiled grid would be small.
 //   w8a16_tiled    more rows (prefill): an LDS-tiled MFMA GEMM; the int8 tile
 //                  is widened to fp16/bf16 once, on its way into LDS, and shared
 //                  by every wave of the workgroup.
@@ -40,9 +41,10 @@
 // nothing, A rows 8..15 would otherwise be padding).  D layout of the gfx950
 // 16x16x32 MFMA: lane l holds rows 4 * (l / 16) + j, j < 4, of column l % 16.
 //
-// Decomposition: a workgroup owns 8 weight rows and a tile of 8 * MT rows of x
-// (blockIdx.y) and splits the 128-column blocks of K between its waves
-// (contiguous ranges); each wave keeps U blocks of loads in flight.  Blocks
+// Decomposition: a workgroup owns 8 * G weight rows (blockIdx.y) and a tile of
+// 8 * MT rows of x (blockIdx.x) and splits the 128-column blocks of K between
+// its waves (contiguous ranges); each wave keeps U blocks of loads in flight,
+// and every x operand it loads feeds G weight groups.  Blocks
 // and 16-byte pieces past k address past the buffer descriptors (zeros, no
 // traffic), so any k that is a multiple of 16 needs no remainder loop.  The
 // per-wave partial sums meet in LDS in a fixed order.
@@ -130,17 +132,19 @@ __device__ __forceinline__ void w8_store(const W8Params& p, int64_t m, int n, fl
 
 // ------------------------------------------------------------------ skinny
 
-template <typename T, typename TO, int MT, int U>
+template <typename T, typename TO, int MT, int G, int U>
 __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p) {
   using TB = typename T::bits;
-  extern __shared__ float red[];  // [nwave][MT][4][64]
+  extern __shared__ float red[];  // [nwave][G][MT][4][64]
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwave = blockDim.x >> 6;
-  const int n0 = blockIdx.x * 8;
-  const int m0 = blockIdx.y * 8 * MT;
-  const int nrows_w = p.n - n0 < 8 ? p.n - n0 : 8;
+  // x tiles vary fastest, so the workgroups sharing a weight group run
+  // together and its re-reads (rows > 8 * MT) hit L2.
+  const int m0 = blockIdx.x * 8 * MT;
+  const int n0 = blockIdx.y * 8 * G;
+  const int nrows_w = p.n - n0 < 8 * G ? p.n - n0 : 8 * G;
   const int nrows_x = p.rows - m0 < 8 * MT ? p.rows - m0 : 8 * MT;
 
   // Descriptors end right after the last valid element, so weight rows past n
@@ -153,24 +157,28 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
   // Lane -> (row l % 8 of the operand, column 64 * ((l / 8) % 2) + 16 * (l / 16) of the block).
   const int r8 = lane & 7;
   const int col = ((lane >> 3) & 1) * 64 + (lane >> 4) * 16;
-  const uint32_t qoff = static_cast<uint32_t>(r8 * p.qs + col);
-  uint32_t xoff[MT];
+  uint32_t qoff[G], xoff[MT];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qoff[g] = static_cast<uint32_t>((8 * g + r8) * p.qs + col);
 #pragma unroll
   for (int t = 0; t < MT; ++t) xoff[t] = static_cast<uint32_t>(((8 * t + r8) * p.xs + col) * sizeof(TB));
 
-  f32x4 acc[MT];
+  f32x4 acc[G][MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   const int nblk = (p.k + 127) >> 7;
   const int s_end = (nblk * (wave + 1)) / nwave;
   for (int s = (nblk * wave) / nwave; s < s_end; s += U) {
-    u32x4 wq[U], xa[U][MT][2];
+    u32x4 wq[U][G], xa[U][MT][2];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-      const int c = 128 * (s + j) + col;
-      const bool live = s + j < s_end && c < p.k;
-      wq[j] = buf_load16(rq, live ? qoff + 128u * (s + j) : kOob);
+      const bool live = s + j < s_end && 128 * (s + j) + col < p.k;
+#pragma unroll
+      for (int g = 0; g < G; ++g) wq[j][g] = buf_load16(rq, live ? qoff[g] + 128u * (s + j) : kOob);
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         const uint32_t o = xoff[t] + 256u * (s + j);
@@ -181,36 +189,43 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-      u32x4 b0, b1;
-      widen_i8x16<T>(wq[j], b0, b1);
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        acc[t] = mfma16<T>(xa[j][t][0], b0, acc[t]);
-        acc[t] = mfma16<T>(xa[j][t][1], b1, acc[t]);
+      for (int g = 0; g < G; ++g) {
+        u32x4 b0, b1;
+        widen_i8x16<T>(wq[j][g], b0, b1);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[g][t] = mfma16<T>(xa[j][t][0], b0, acc[g][t]);
+          acc[g][t] = mfma16<T>(xa[j][t][1], b1, acc[g][t]);
+        }
       }
     }
   }
 
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
+  for (int g = 0; g < G; ++g) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[((wave * MT + t) * 4 + j) * 64 + lane] = acc[t][j];
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[(((wave * G + g) * MT + t) * 4 + j) * 64 + lane] = acc[g][t][j];
+    }
   }
   __syncthreads();
 
-  // Output (x row 8t + a, weight row b) = D[a][b] + D[a + 8][b + 8]:
+  // Output (x row 8t + a, weight row 8g + b) = D[a][b] + D[a + 8][b + 8]:
   // register a % 4 of lanes 16 * (a / 4) + b and 16 * (a / 4) + 40 + b.
-  for (int o = threadIdx.x; o < 64 * MT; o += blockDim.x) {
-    const int b = o & 7, a = (o >> 3) & 7, t = o >> 6;
-    const int m = 8 * t + a;
-    if (m >= nrows_x || b >= nrows_w) continue;
+  for (int o = threadIdx.x; o < 64 * G * MT; o += blockDim.x) {
+    const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
+    const int g = gt % G, t = gt / G;
+    const int m = 8 * t + a, n = 8 * g + b;
+    if (m >= nrows_x || n >= nrows_w) continue;
     const int l0 = 16 * (a >> 2) + b, j = a & 3;
-    float s = 0.f;
+    float sum = 0.f;
     for (int w = 0; w < nwave; ++w) {
-      const float* r = red + ((w * MT + t) * 4 + j) * 64;
-      s += r[l0] + r[l0 + 40];
+      const float* r = red + (((w * G + g) * MT + t) * 4 + j) * 64;
+      sum += r[l0] + r[l0 + 40];
     }
-    w8_store<TO>(p, m0 + m, n0 + b, s);
+    w8_store<TO>(p, m0 + m, n0 + n, sum);
   }
 }
 
@@ -414,26 +429,98 @@ int launch_w8(K kernel, dim3 grid, dim3 block, size_t lds, const W8Params& p, hi
                     "w8a16 launch");
 }
 
-// Skinny launch shape: enough waves in flight to cover HBM latency (about 16
-// per CU) while each wave keeps whole 128-column blocks; U blocks of loads in
-// flight per wave.
-template <typename T, typename TO, int MT>
-int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
-  const int groups = (p.n + 7) / 8;
+#ifdef MI355_W8_SWEEP
+// Sweep builds only: force the skinny launch shape (0 = automatic).
+int g_force_g = 0, g_force_u = 0, g_force_split = 0, g_force_path = 0;
+}  // namespace
+extern "C" __attribute__((visibility("default"))) void mi355_w8_sweep_config(int g, int u, int split, int path) {
+  g_force_g = g;
+  g_force_u = u;
+  g_force_split = split;
+  g_force_path = path;
+}
+namespace {
+#endif
+
+// Skinny launch shape, fitted to a graph-timed sweep of G x waves x U on
+// MI355X over the q/o, k/v, gate/up and down projections of Qwen2.5-0.5B,
+// 1.5B and 7B at 1, 8, 32 and 128 rows (within 1.14x of the best sampled
+// shape everywhere, within 1.05x on most):
+//   G (weight-row groups per workgroup; each x operand feeds G B operands,
+//     and a wave keeps G KiB of weights in flight) grows with the rows of x
+//     while enough workgroups remain: with 1 row, 2 only for large matrices
+//     (n / 16 >= 192 and n * k >= 12M); with <= 8 rows 4 if n / 32 >= 384,
+//     else 2 if n / 16 >= 192; beyond, the largest of 4, 2, 1 with
+//     n / (8 G) >= 160 (<= 32 rows) or 48 (several 32-row tiles);
+//   waves per workgroup (the split of K) so that about 4096 (1 row), 1536
+//     (<= 8 rows), 1024 (<= 32 rows) or 1536 (several 32-row tiles) waves run
+//     in total, within the LDS for the partial sums (<= 64 KiB), then evened
+//     out so every wave gets the same number of 128-column blocks -- or, when
+//     there are no more workgroups than CUs, rounded to a multiple of 4 so
+//     the CU's 4 SIMDs carry equal loads (7 waves on 224 CUs: 1.22x slower
+//     than 8);
+//   U (blocks in flight per wave) = 1, or 2 for narrow outputs (n <= 1536,
+//     few workgroups) whose waves own 2 or more blocks.
+template <typename T, typename TO, int MT, int G>
+int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
+  const int groups = (p.n + 8 * G - 1) / (8 * G);
   const int nblk = (p.k + 127) / 128;
-  int split = (16 * cus + groups - 1) / groups;
+  const int tiles = (p.rows + 8 * MT - 1) / (8 * MT);
+  const int64_t units = static_cast<int64_t>(groups) * tiles;
+  const int64_t waves = p.rows <= 1 ? 16 * cus : (p.rows <= 8 ? 6 * cus : (p.rows <= 32 ? 4 * cus : 6 * cus));
+  int split = static_cast<int>((waves + units / 2) / units);
+  int u = 0;
+#ifdef MI355_W8_SWEEP
+  if (g_force_split > 0) split = g_force_split;
+  if (g_force_u > 0) u = g_force_u;
+#endif
   if (split > kMaxSplit) split = kMaxSplit;
+  if (split > 64 / (G * MT)) split = 64 / (G * MT);  // partial sums: split * G * MT KiB of LDS <= 64 KiB
   if (split > nblk) split = nblk;
   if (split < 1) split = 1;
-  const int per_wave = (nblk + split - 1) / split;
-  const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>((p.rows + 8 * MT - 1) / (8 * MT)));
-  const dim3 block(64 * split);
-  const size_t lds = static_cast<size_t>(split) * MT * 4 * 64 * sizeof(float);
-  if constexpr (MT <= 2) {  // 4 blocks in flight fit the registers of up to 16 rows of x
-    if (per_wave >= 4) return launch_w8(w8a16_skinny<T, TO, MT, 4>, grid, block, lds, p, s);
+  int bpw = (nblk + split - 1) / split;
+  if (units <= cus && split > 4) {
+    // one workgroup per CU: a multiple of 4 waves keeps the CU's 4 SIMDs evenly loaded
+    split = ((split + 2) / 4) * 4;
+    if (split > 64 / (G * MT)) split = (64 / (G * MT)) / 4 * 4;
+    if (split > kMaxSplit) split = kMaxSplit;
+    bpw = (nblk + split - 1) / split;
+  } else {
+    split = (nblk + bpw - 1) / bpw;  // even blocks per wave
   }
-  if (per_wave >= 2) return launch_w8(w8a16_skinny<T, TO, MT, 2>, grid, block, lds, p, s);
-  return launch_w8(w8a16_skinny<T, TO, MT, 1>, grid, block, lds, p, s);
+  if (u == 0) u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
+  const dim3 block(64 * split);
+  const size_t lds = static_cast<size_t>(split) * G * MT * 4 * 64 * sizeof(float);
+  // register budget (128 VGPRs at 1024 threads): U * (4 G + 8 MT) operand
+  // dwords + 4 G MT accumulators <= 100
+  constexpr int umax = (100 - 4 * G * MT) / (4 * G + 8 * MT);
+#ifdef MI355_W8_SWEEP
+  if (u >= 4 && umax >= 4) return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 4 ? 4 : 1)>, grid, block, lds, p, s);
+#endif
+  if (u >= 2 && umax >= 2) return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1)>, grid, block, lds, p, s);
+  return launch_w8(w8a16_skinny<T, TO, MT, G, 1>, grid, block, lds, p, s);
+}
+
+template <typename T, typename TO, int MT>
+int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
+  int g = 1;
+  if (p.rows <= 1) {
+    if ((p.n + 15) / 16 >= 192 && static_cast<int64_t>(p.n) * p.k >= 12000000) g = 2;
+  } else if (p.rows <= 8) {
+    if ((p.n + 31) / 32 >= 384) g = 4;
+    else if ((p.n + 15) / 16 >= 192) g = 2;
+  } else {
+    const int min_groups = p.rows <= 32 ? 160 : 48;
+    if ((p.n + 31) / 32 >= min_groups) g = 4;
+    else if ((p.n + 15) / 16 >= min_groups) g = 2;
+  }
+#ifdef MI355_W8_SWEEP
+  if (g_force_g > 0) g = g_force_g;
+#endif
+  if (g >= 4) return w8_skinny_g<T, TO, MT, 4>(p, s, cus);
+  if (g == 2) return w8_skinny_g<T, TO, MT, 2>(p, s, cus);
+  return w8_skinny_g<T, TO, MT, 1>(p, s, cus);
 }
 
 template <typename T, typename TO>
@@ -447,7 +534,16 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   if (p.rows <= 16) return w8_skinny_shape<T, TO, 2>(p, s, cus);
   if (p.rows <= 24) return w8_skinny_shape<T, TO, 3>(p, s, cus);
   if (p.rows <= 32) return w8_skinny_shape<T, TO, 4>(p, s, cus);
-  // Prefill: 128 x 128 tiles when they fill the chip, else 64 x 64.
+  // More rows: the tiled GEMM once its 64 x 64 grid fills the chip; below
+  // that (e.g. 128 rows against a K-heavy down projection) 32-row skinny
+  // tiles, which re-read the weights per tile mostly from L2, measured faster.
+  const int64_t small = static_cast<int64_t>((p.n + 63) / 64) * ((p.rows + 63) / 64);
+  bool skinny = small < cus;
+#ifdef MI355_W8_SWEEP
+  if (g_force_path > 0) skinny = g_force_path == 1;
+#endif
+  if (skinny) return w8_skinny_shape<T, TO, 4>(p, s, cus);
+  // 128 x 128 tiles when they fill the chip, else 64 x 64.
   const int64_t big = static_cast<int64_t>((p.n + 127) / 128) * ((p.rows + 127) / 128);
   if (big >= cus) {
     const dim3 grid(static_cast<unsigned>((p.n + 127) / 128), static_cast<unsigned>((p.rows + 127) / 128));
