@@ -62,9 +62,11 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up",
-                                      "w8a16"],
+                                      "w8a16", "w8a16-decode"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
+    p.add_argument("--e2e-int8", action="store_true",
+                   help="fp16 vs int8-weight (W8A16) decode end to end, after the reference's run_stage7_e2e.py")
     p.add_argument("--e2e", action="store_true",
                    help="instead of the kernel bench: TTFT and decode tok/s of a random-init Qwen2-1.5B "
                         "architecture before and after patch_model_with_fused_kernels (the reference's "
@@ -339,6 +341,11 @@ KNOWN_LAUNCHES = {
     ("gate_up_silu_skinny<mi355::F16, mi355::F16, 1, 4, 1, 6>", 8960 // 8 * 256): (
         "gate/up + SiLU-and-mul, 8 rows, [8960,1536] weights, fp16",
         2 * 8960 * 1536 * 2 + 8 * 1536 * 2 + 8 * 8960 * 2),
+    ("w8a16_skinny<mi355::F16, mi355::F16, 1, 2, 1>", 192 * 560): (
+        "W8A16 1.5B gate/up, 8 rows, [8960,1536] int8, fp16", 8960 * 1536 + 4 * 8960 + 8 * 1536 * 2 + 8 * 8960 * 2),
+    ("w8a16_skinny<mi355::BF16, mi355::BF16, 1, 4, 1>", 192 * 592): (
+        "W8A16 7B gate/up, 8 rows, [18944,3584] int8, bf16",
+        18944 * 3584 + 4 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
 }
 COPY_READ_KIB = COPY_WRITE_KIB = (1 << 30) / 1024
 
@@ -366,11 +373,11 @@ def rocprof_summary(dirs):
             out.append("|---|---|---|---|---|---|---|---|")
             groups = {}
             for r in csv.DictReader(open(f)):
-                frag, known = _match_launch(r["Kernel_Name"], int(r["Grid_Size_X"]))
+                grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])  # threads
+                frag, known = _match_launch(r["Kernel_Name"], grid)
                 if known is None:
                     continue
-                groups.setdefault((frag, int(r["Grid_Size_X"])), []).append(
-                    int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+                groups.setdefault((frag, grid), []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
             for (frag, grid), v in groups.items():
                 label, nbytes = KNOWN_LAUNCHES[(frag, grid)]
                 v.sort()
@@ -434,6 +441,9 @@ def main():
 
     if args.e2e:
         bench_e2e(args)
+        return
+    if args.e2e_int8:
+        bench_e2e_int8(args)
         return
 
     ctx = Ctx()
@@ -568,10 +578,14 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up(ctx, shapes=GATE_UP_SHAPES[1:2], iters=iters, baselines=False)))
-    elif args.only == "w8a16":
+    elif args.only in ("w8a16", "w8a16-decode"):
         del sets
         torch.cuda.empty_cache()
-        log(json.dumps(bench_w8a16(ctx)))
+        if args.only == "w8a16":
+            log(json.dumps(bench_w8a16(ctx)))
+        else:  # the two decode shapes profiled under profiles/, kernel only
+            log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 8 and s[2] in (8960, 18944)],
+                                       iters=iters, baselines=False)))
 
 
 def bench_add_rms(ctx, iters):
@@ -958,6 +972,113 @@ def bench_e2e(args):
                       "graphed_decode_tok_s": {"seq_len": 512, "unpatched": graph_before, "patched": graph_after,
                                                "patched_fuse_residual": graph_fr,
                                                "patched_fuse_residual_fuse_gate_up": graph_gu}}),
+          flush=True)
+
+
+def bench_e2e_int8(args):
+    """fp16 vs int8 weights end to end, after the reference's
+    benchmarks/run_stage7_e2e.py: one model instance is measured in fp16,
+    quantised in place with quantize_model_int8 (196 linears -> W8A16 HIP
+    kernels) and measured again, then also patched with the fused RMSNorm /
+    SiLU-and-mul kernels.  Per phase: transformer-layer weight MB; the HF
+    path (eager decode over HF's KV cache) at batch 1 and 8 -- TTFT, decode
+    tok/s, peak memory -- for prompts of 128 tokens and 64 generated; and
+    decode tok/s with the whole step replayed as one HIP graph
+    (GraphedGreedyDecoder) at batch 1 and 8.  Random-init Qwen2 with
+    Qwen2.5-1.5B's architecture, fp16, sdpa (no Hub access here)."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    sys.path.insert(0, str(ROOT))
+    pkg = importlib.import_module(PKG)
+    dev = torch.device("cuda:0")
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
+                      num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=32768,
+                      rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.half().eval()
+    S, GEN, TRIALS = 128, 64, args.trials
+
+    def layer_weight_mb():
+        total = 0
+        for m in model.model.layers.modules():
+            for t in list(m.parameters(recurse=False)) + list(m.buffers(recurse=False)):
+                total += t.numel() * t.element_size()
+        return total / 2**20
+
+    def ids_for(B, seed):
+        g = torch.Generator()
+        g.manual_seed(seed)
+        return torch.randint(0, cfg.vocab_size, (B, S), generator=g).to(dev)
+
+    def hf_run(ids):
+        with torch.inference_mode():
+            torch.cuda.synchronize()
+            torch.cuda.reset_peak_memory_stats(dev)
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record()
+            out = model(input_ids=ids, use_cache=True)
+            past = out.past_key_values
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            s1.record()
+            d0.record()
+            for _ in range(GEN - 1):
+                out = model(input_ids=tok, past_key_values=past, use_cache=True)
+                past = out.past_key_values
+                tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            d1.record()
+            torch.cuda.synchronize()
+            return (s0.elapsed_time(s1), ids.shape[0] * (GEN - 1) / (d0.elapsed_time(d1) / 1e3),
+                    torch.cuda.max_memory_allocated(dev) / 2**20)
+
+    def graphed_tok_s(B):
+        ids = ids_for(B, 7)
+        dec = pkg.GraphedGreedyDecoder(model, B, S + GEN + 8)
+        dec.generate(ids, GEN)  # capture
+        times = []
+        for _ in range(TRIALS):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            dec.generate(ids, 2)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            dec.generate(ids, GEN)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            times.append(((t2 - t1) - (t1 - t0)) / (GEN - 2))
+        del dec
+        torch.cuda.empty_cache()
+        return B / statistics.median(times)
+
+    def phase(label):
+        r = {"layer_weight_mb": round(layer_weight_mb(), 1), "hf": {}, "graphed_decode_tok_s": {}}
+        for B in (1, 8):
+            ids = ids_for(B, 5)
+            for _ in range(2):
+                hf_run(ids)
+            t = [hf_run(ids) for _ in range(TRIALS)]
+            r["hf"][B] = {"ttft_ms": round(statistics.mean(x[0] for x in t), 3),
+                          "decode_tok_s": round(statistics.mean(x[1] for x in t), 1),
+                          "peak_mb": round(max(x[2] for x in t), 1)}
+            r["graphed_decode_tok_s"][B] = round(graphed_tok_s(B), 1)
+            log(f"  {label} batch {B}: TTFT {r['hf'][B]['ttft_ms']:.2f} ms, HF decode {r['hf'][B]['decode_tok_s']:.1f} "
+                f"tok/s, peak {r['hf'][B]['peak_mb']:.0f} MB; graphed decode {r['graphed_decode_tok_s'][B]:.1f} tok/s")
+        return r
+
+    fp16 = phase("fp16")
+    stats = pkg.quantize_model_int8(model)
+    log(f"quantized {stats}")
+    int8 = phase("int8")
+    counts = pkg.patch_model_with_fused_kernels(model, fuse_residual=True)
+    log(f"patched {counts}")
+    int8_fused = phase("int8+fused")
+    print(json.dumps({"metric": "fp16 vs int8-weight (W8A16) decode tok/s, after run_stage7_e2e.py",
+                      "model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16 activations, sdpa",
+                      "seq_len": S, "gen_len": GEN, "trials": TRIALS, "quantize_stats": stats,
+                      "fp16": fp16, "int8": int8, "int8_fused_kernels": int8_fused, "patched": counts}),
           flush=True)
 
 
