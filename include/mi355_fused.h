@@ -139,9 +139,10 @@ int mi355_silu_mul_fwd(const void* gate, const void* up, void* out,
  * (they are closer to the exact value).  Weights use nn.Linear's layout,
  * [n_out, k] row-major, as in HF's gate_proj / up_proj.
  *
- * Built for rows <= 32, where the call streams the weights once at HBM
- * bandwidth; larger `rows` are served by 32-row tiles that each re-read the
- * weights (a GEMM library is the better choice there).
+ * rows <= 32 stream the weights once at HBM bandwidth; more rows run an
+ * LDS-tiled MFMA GEMM over both weight matrices with SiLU-and-mul in its
+ * epilogue (32-row weight-streaming tiles when a row stride is too large for
+ * the tiled kernel's buffer descriptors).
  *
  *   x        [rows, x_row_stride] of dtype, 16-byte aligned.
  *   w_gate, w_up  [n_out, w_row_stride] of dtype, 16-byte aligned.

@@ -1,5 +1,4 @@
-// Gate/up projection fused with the SiLU-and-mul epilogue, for skinny
-// activations (decode batches), plus its launcher:
+// Gate/up projection fused with the SiLU-and-mul epilogue, plus its launcher:
 //
 //   out[m, n] = silu(g) * u,  g = sum_k x[m,k] * w_gate[n,k],  u = sum_k x[m,k] * w_up[n,k]
 //
@@ -10,9 +9,12 @@
 // a rounding of both to x's type and the SiLU-and-mul kernel
 // (src/engine/fused_norm_activation_patch.py:60-64).
 //
-// At decode shapes the work is weight streaming: each weight element is read
-// once per call (2 * n_out * k elements) and meets at most 32 rows of x, so
-// the kernel is bound by HBM bandwidth on the weights, not by MFMA.
+// At decode shapes (rows <= 32) the work is weight streaming: each weight
+// element is read once per call (2 * n_out * k elements) and meets at most 32
+// rows of x, so the skinny kernel below is bound by HBM bandwidth on the
+// weights, not by MFMA.  More rows are a GEMM (MFMA-bound): they run the
+// LDS-tiled kernel of tiled_gemm.h with both weight matrices as B operands
+// and SiLU-and-mul in its epilogue.
 //
 // Operand layout.  The v_mfma_f32_16x16x32 B operand gives lane l column
 // n = l % 16 and k-group l / 16 (8 consecutive k each).  Giving the 16
@@ -44,6 +46,7 @@
 // D layout of the gfx950 16x16x32 MFMA: lane l holds rows 4 * (l / 16) + j,
 // j < 4, of column l % 16.
 #include "common.h"
+#include "tiled_gemm.h"
 
 // Launch shapes (split-K waves, weight row groups, K steps in flight per
 // wave) were chosen by sweeping them on MI355X at Qwen2.5 decode shapes:
@@ -244,13 +247,59 @@ int gate_up_shape(const GateUpParams& p, hipStream_t s) {
   return gate_up_launch_tiles<T, TO, MT, 4, 2, 2>(p, s);
 }
 
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S>
+int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
+  using C = tiled::Cfg<T, tiled::B_16, TO, WGM, WGN, FM, FN, tiled::EPI_SILU, S>;
+  static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
+  tiled::Params tp{};
+  tp.x = p.x;
+  tp.b0 = p.wg;
+  tp.b1 = p.wu;
+  tp.out = p.out;
+  tp.rows = p.rows;
+  tp.k = p.k;
+  tp.n = p.n_out;
+  tp.xs = p.xs;
+  tp.bs = p.ws;
+  tp.os = p.os;
+  tp.sdt = MI355_F32;
+  tp.bdt = -1;
+  tp.tiles_m = (p.rows + C::BM - 1) / C::BM;
+  tp.tiles_n = (p.n_out + C::BN - 1) / C::BN;
+  tp.group_m = tp.tiles_m < 4 ? tp.tiles_m : 4;
+  void* args[] = {&tp};
+  // all LDS is static (no dynamic shared memory)
+  return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_16, TO, WGM, WGN, FM, FN,
+                                                                                      tiled::EPI_SILU, S>),
+                                    dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
+                    "gate_up_silu tiled launch");
+}
+
+// Tiled launch shapes from a sweep on MI355X (Qwen2.5-1.5B and 7B MLPs at
+// 128, 1024 and 4096 rows): up to 256 rows 128 x 64 output tiles (4 waves,
+// 4 stages) or, for n_out > 10000, 128 x 128 (8 waves, 3 stages); more rows
+// 256 x 64 (8 waves, 3 stages).  Descriptors span at most 256 rows of x and
+// 128 weight rows, each below 2^31 bytes.
+template <typename T, typename TO>
+int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
+  if (p.rows <= 256) {
+    if (p.n_out <= 10000) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(p, s);
+    return gate_up_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+  }
+  return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(p, s);
+}
+
 template <typename T, typename TO>
 int gate_up_typed(const GateUpParams& p, hipStream_t s) {
   // x tile: the fewest 8-row MFMA tiles that cover the rows, up to 4 (32 rows)
-  // per workgroup; more rows take further 32-row tiles along grid y.
+  // per workgroup; more rows take the tiled GEMM when its descriptors fit,
+  // else further 32-row skinny tiles along grid y.
   if (p.rows <= 8) return gate_up_shape<T, TO, 1>(p, s);
   if (p.rows <= 16) return gate_up_shape<T, TO, 2>(p, s);
   if (p.rows <= 24) return gate_up_shape<T, TO, 3>(p, s);
+  const bool tiled_fits = int64_t{256} * p.xs * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31) &&
+                          int64_t{128} * p.ws * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31);
+  if (p.rows > 32 && tiled_fits) return gate_up_tiled<T, TO>(p, s);
   return gate_up_shape<T, TO, 4>(p, s);
 }
 

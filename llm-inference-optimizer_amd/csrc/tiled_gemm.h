@@ -1,0 +1,543 @@
+// LDS-tiled MFMA GEMM core for gfx950, shared by the prefill-size launchers of
+// the W8A16 linear (w8a16.hip) and of the gate/up projections fused with
+// SiLU-and-mul (gate_up_silu.hip):
+//
+//   acc[m, n] = sum_k x[m, k] * b[n, k]        (both operands K-contiguous)
+//   EPI_W8    out[m, n] = round(acc * scale[n] + bias[n])     b = int8 weights
+//   EPI_SILU  out[m, n] = round(silu(acc_gate) * acc_up)      two 16-bit b
+//
+// x is [rows, xs] fp16/bf16 and every b is nn.Linear's [n, bs] layout (int8 or
+// x's 16-bit type), used in place.  Arithmetic: 16-bit products, fp32
+// accumulation (v_mfma_f32_32x32x16_{f16,bf16}), fp32 epilogue, one rounding.
+//
+// Decomposition.  A workgroup of WGM x WGN waves owns a BM x BN output tile
+// (BM = 32 FM WGM, BN = 32 FN WGN); each wave owns FM x FN 32x32 MFMA tiles.
+// K advances in steps of 64 columns through two LDS stages: the global loads
+// of step t + 1 are issued (16 bytes per lane, buffer descriptors whose
+// extent ends at the last valid element, so rows past the matrix read 0)
+// before the MFMAs of step t, and stored to the other stage after them; one
+// barrier per step.  Columns at or past k are redirected past the descriptor,
+// so any k that is a multiple of 16 (int8) or 8 (16-bit) needs no remainder
+// loop.
+//
+// K order inside a step.  The MFMA's A operand gives lane l row l % 32 and
+// 8 consecutive k of k-group h = l / 32; B likewise.  A step's 64 columns are
+// dealt so that k-group h of sub-step s (s < 4) holds columns 32 h + 8 s ..
+// + 8: a lane's A piece of sub-step s is 16-byte chunk 4 h + s of its 128-byte
+// row, and an int8 B row's 16-byte chunk 2 h + j feeds sub-steps 2 j and
+// 2 j + 1, so one LDS read serves two MFMAs.  The sum is the same (fp32
+// summation order aside) as in natural order, since A and B agree.
+//
+// LDS layout.  16-bit tiles: 128-byte rows, chunk c of row r stored at chunk
+// c ^ f(r), f(r) = (r ^ (r >> 3)) & 7.  int8 tiles: 64-byte rows, chunk c at
+// c ^ g(r), g(r) = ((r >> 1) ^ (r >> 3)) & 3.  Every 16-byte read of 8 (or
+// 16) consecutive rows at one logical chunk, and every 16-byte write of a
+// row's consecutive chunks, then falls in distinct banks for both 128- and
+// 256-byte bank rows.
+//
+// int8 weights stay int8 in LDS (half the footprint and LDS traffic of a
+// widened tile) and are widened in registers after each read: 0x64uu is the
+// fp16 pattern of 1024 + u, so (q ^ 0x80) spliced under 0x64 minus 1152 is q
+// (v_perm_b32 + v_pk_add_f16 per pair); bf16 goes through v_cvt_f32_i32.
+// Every int8 is exact in both 16-bit types.
+//
+// Grid: one workgroup per tile, 1-D.  Consecutive workgroup ids land on
+// different XCDs (round robin over 8), so ids are remapped to give each XCD
+// a contiguous range of tiles, ordered m-fastest: the x row blocks that share
+// a weight block run on one XCD and the weights are fetched from HBM once.
+#pragma once
+
+#include <type_traits>
+#include <utility>
+
+#include "common.h"
+
+namespace mi355 {
+namespace tiled {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kOob = 0xfffffff0u;  // past every descriptor the launchers admit (< 2^31 bytes)
+
+enum { EPI_W8 = 0, EPI_SILU = 1 };
+enum { B_16 = 0, B_I8 = 1, B_I8R = 2 };
+
+template <typename T> __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
+template <> __device__ __forceinline__ f32x16 mfma32<F16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+template <> __device__ __forceinline__ f32x16 mfma32<BF16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// Four int8 (byte i = element i) -> four values of T in two dwords.
+template <typename T> __device__ __forceinline__ u32x2 widen4(uint32_t d);
+template <> __device__ __forceinline__ u32x2 widen4<F16>(uint32_t d) {
+  const uint32_t u = d ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0,64,u1,64
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2,64,u3,64
+  const f16x2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+  const f16x2 a = __builtin_bit_cast(f16x2, lo) + off;
+  const f16x2 b = __builtin_bit_cast(f16x2, hi) + off;
+  return u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+}
+template <> __device__ __forceinline__ u32x2 widen4<BF16>(uint32_t d) {
+  const float f0 = static_cast<float>(static_cast<int8_t>(d & 0xffu));
+  const float f1 = static_cast<float>(static_cast<int8_t>((d >> 8) & 0xffu));
+  const float f2 = static_cast<float>(static_cast<int8_t>((d >> 16) & 0xffu));
+  const float f3 = static_cast<float>(static_cast<int8_t>(d >> 24));
+  return u32x2{__builtin_amdgcn_perm(as_u32(f1), as_u32(f0), 0x07060302u),
+               __builtin_amdgcn_perm(as_u32(f3), as_u32(f2), 0x07060302u)};
+}
+// 8 int8 in two dwords -> one MFMA operand (8 values of T).
+template <typename T> __device__ __forceinline__ u32x4 widen8(uint32_t d0, uint32_t d1) {
+  const u32x2 p = widen4<T>(d0), q = widen4<T>(d1);
+  return u32x4{p.x, p.y, q.x, q.y};
+}
+
+__device__ __forceinline__ uint32_t swz16(uint32_t r, uint32_t c) { return r * 128u + ((c ^ ((r ^ (r >> 3)) & 7u)) << 4); }
+__device__ __forceinline__ uint32_t swz8(uint32_t r, uint32_t c) {
+  return r * 64u + ((c ^ (((r >> 1) ^ (r >> 3)) & 3u)) << 4);
+}
+
+__device__ __forceinline__ u32x4 lds_read16(const uint8_t* base, uint32_t off) {
+  return *reinterpret_cast<const u32x4*>(base + off);
+}
+__device__ __forceinline__ void lds_write16(uint8_t* base, uint32_t off, u32x4 v) {
+  *reinterpret_cast<u32x4*>(base + off) = v;
+}
+
+__device__ __forceinline__ float load_dyn(const void* p, int64_t i, int dt) {
+  if (dt == MI355_F16) return load_elem<F16>(p, i);
+  if (dt == MI355_BF16) return load_elem<BF16>(p, i);
+  return load_elem<F32>(p, i);
+}
+
+struct Params {
+  const void* x;      // [rows, xs] of T
+  const void* b0;     // [n, bs]: int8 weights (EPI_W8) or w_gate (EPI_SILU)
+  const void* b1;     // [n, bs]: w_up (EPI_SILU), else unused
+  const void* scale;  // [n] of sdt (EPI_W8)
+  const void* bias;   // [n] of bdt, or null (EPI_W8)
+  void* out;          // [rows, os] of TO
+  int rows, k, n;
+  int64_t xs, bs, os;  // row strides in elements
+  int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
+  int tiles_m, tiles_n;
+  int group_m;  // m-blocks per group of the tile order (tiles_m: m fastest over the whole range)
+};
+
+template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S>
+struct Cfg {
+  // BK: how B reaches LDS -- B_16 (16-bit B, DMA), B_I8 (int8 B, DMA, int8 in
+  // LDS, widened after each LDS read) or B_I8R (int8 B through registers,
+  // widened once and stored 16-bit).
+  static constexpr bool I8 = BK != B_16, QR = BK == B_I8R;
+  static constexpr int NW = WGM * WGN, NT = 64 * NW;
+  static constexpr int BM = 32 * FM * WGM, BN = 32 * FN * WGN;
+  static constexpr int NB = EPI == EPI_SILU ? 2 : 1;  // B matrices
+  static constexpr int A_BYTES = BM * 128;             // 64 columns of 16-bit x per row
+  static constexpr int B_ROW = BK == B_I8 ? 64 : 128;  // bytes per B row per step in LDS
+  static constexpr int B_BYTES = BN * B_ROW;
+  static constexpr int STAGE = A_BYTES + NB * B_BYTES;
+  static constexpr int LDS = S * STAGE;
+  // One DMA instruction moves 64 lanes x 16 bytes = 1 KiB: 8 rows of a 16-bit
+  // tile, 16 rows of an int8 tile.
+  static constexpr int AI = A_BYTES / 1024 / NW;           // A DMA instructions per wave per step
+  static constexpr int BI = QR ? 0 : B_BYTES / 1024 / NW;  // B DMA instructions per wave per step and matrix
+  static constexpr int QP = QR ? BN * 4 / NT : 0;          // B_I8R: 16-byte register loads per thread per step
+  static constexpr int P = AI + NB * BI + QP;          // vector-memory instructions per wave per step
+  static constexpr int R = S - 2;                      // int8 B register sets in flight
+  static_assert(A_BYTES % (1024 * NW) == 0 && (QR || B_BYTES % (1024 * NW) == 0), "tile must split over the waves");
+  static_assert(!QR || (BN * 4) % NT == 0, "int8 tile must split over the threads");
+  static_assert(S >= 3 && S <= 8, "3..8 stages");
+  static_assert(P * (S - 2) < 64, "vmcnt range");
+};
+
+// Stage I of the LDS ring (one LDS variable per stage).
+template <int I, int SZ> __device__ __forceinline__ uint8_t* stage_ptr() {
+  __shared__ __attribute__((aligned(1024))) uint8_t st[SZ];
+  return st;
+}
+
+typedef __attribute__((address_space(3))) uint8_t* lds_ptr_t;
+
+// f(integral_constant<int, I>) for I = 0 .. N - 1, unrolled at compile time.
+template <typename F, size_t... I>
+__device__ __forceinline__ void static_for(F&& f, std::index_sequence<I...>) {
+  (f(std::integral_constant<int, static_cast<int>(I)>{}), ...);
+}
+
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
+
+// Global -> LDS DMA of 16 bytes per lane (gfx950 buffer_load_dwordx4 ... lds):
+// lane l's bytes land at LDS address m0 + 16 l; the global address is the
+// descriptor base + voff + soff.  Written as asm so that the compiler neither
+// tracks these LDS writes nor drains every load in flight before each LDS
+// read: the kernel orders them itself, with vmcnt waits before the barrier
+// that publishes a stage (vmcnt falls as the data reaches LDS, in issue order).
+__device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+}
+// LDS byte address of stage I (the cast of the LDS variable itself folds to a constant).
+template <int I, int SZ> __device__ __forceinline__ uint32_t stage_addr() {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)stage_ptr<I, SZ>()));
+}
+
+// Workgroup barrier that the compiler may not move memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt low
+// bits [3:0], high bits [15:14]; expcnt [6:4] = 7, lgkmcnt [11:8] = 15).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S>
+__global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
+  using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
+  constexpr bool I8 = C::I8, QR = C::QR;
+  using TB = typename T::bits;
+  constexpr int NW = C::NW, NT = C::NT, BM = C::BM, BN = C::BN, NB = C::NB, R = C::R;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  // Tile of this workgroup: contiguous ranges per XCD, m fastest.
+  const int ntiles = p.tiles_m * p.tiles_n;
+  int b = blockIdx.x;
+  if ((ntiles & 7) == 0) b = (b & 7) * (ntiles >> 3) + (b >> 3);
+  // inside the range: groups of group_m m-blocks, m fastest within a group
+  const int per_group = p.group_m * p.tiles_n;
+  const int g0 = (b / per_group) * p.group_m;
+  const int gsz = p.tiles_m - g0 < p.group_m ? p.tiles_m - g0 : p.group_m;
+  const int tm = g0 + (b % per_group) % gsz, tn = (b % per_group) / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nrows_x = p.rows - m0 < BM ? p.rows - m0 : BM;
+  const int nrows_b = p.n - n0 < BN ? p.n - n0 : BN;
+
+  constexpr int EB = I8 ? 1 : static_cast<int>(sizeof(TB));  // bytes per B element in memory
+  const rsrc_t rx = make_rsrc(static_cast<const TB*>(p.x) + static_cast<int64_t>(m0) * p.xs,
+                              static_cast<uint32_t>(((nrows_x - 1) * p.xs + p.k) * sizeof(TB)));
+  rsrc_t rb[NB];
+  rb[0] = make_rsrc(static_cast<const uint8_t*>(p.b0) + static_cast<int64_t>(n0) * p.bs * EB,
+                    static_cast<uint32_t>(((nrows_b - 1) * p.bs + p.k) * EB));
+  if constexpr (NB == 2)
+    rb[1] = make_rsrc(static_cast<const uint8_t*>(p.b1) + static_cast<int64_t>(n0) * p.bs * EB,
+                      static_cast<uint32_t>(((nrows_b - 1) * p.bs + p.k) * EB));
+
+  // DMA lane maps (16-bit tiles).  Instruction j of wave w fills the 1 KiB
+  // at tile offset 1024 (NW j + w): lane l writes physical chunk l % 8 of row
+  // 8 (NW j + w) + l / 8, so it loads the logical chunk the swizzle keeps
+  // there.  The K step enters through the scalar offset.
+  uint32_t a_goff[C::AI];
+  int a_col[C::AI];
+#pragma unroll
+  for (int j = 0; j < C::AI; ++j) {
+    const int r = 8 * (NW * j + wave) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);
+    a_goff[j] = static_cast<uint32_t>((r * p.xs + 8 * c) * sizeof(TB));
+    a_col[j] = 8 * c;
+  }
+  constexpr int BIX = C::BI > 0 ? C::BI : 1;
+  uint32_t b_goff[BIX];
+  int b_col[BIX];
+#pragma unroll
+  for (int j = 0; j < BIX; ++j) {
+    if constexpr (BK == B_I8) {  // 16 rows of 64 bytes per instruction
+      const int r = 16 * (NW * j + wave) + (lane >> 2);
+      const int c = (lane & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);
+      b_goff[j] = static_cast<uint32_t>(r * p.bs + 16 * c);
+      b_col[j] = 16 * c;
+    } else {
+      const int r = 8 * (NW * j + wave) + (lane >> 3);
+      const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);
+      b_goff[j] = static_cast<uint32_t>((r * p.bs + 8 * c) * EB);
+      b_col[j] = 8 * c;
+    }
+  }
+  // int8 B register pieces: piece c = tid + NT i -> row c / 4, 16 int8 at
+  // columns 16 (c % 4) .. + 16, widened into 16-bit chunks 2 (c % 4) and
+  // 2 (c % 4) + 1 of that row.
+  constexpr int QPX = C::QP > 0 ? C::QP : 1;
+  uint32_t q_goff[QPX], q_loff[QPX];
+  int q_col[QPX];
+#pragma unroll
+  for (int i = 0; i < QPX; ++i) {
+    const int c = tid + NT * i;
+    const int r = c >> 2, kc = c & 3;
+    q_goff[i] = static_cast<uint32_t>(r * p.bs + 16 * kc);
+    q_loff[i] = swz16(r, 2 * kc);  // chunk 2 kc; chunk 2 kc + 1 is at swz16(r, 2 kc + 1)
+    q_col[i] = 16 * kc;
+  }
+
+  const int nk = (p.k + 63) >> 6;
+  const int kfull = p.k >> 6;  // steps whose 64 columns are all inside k
+
+  // Issues the DMA of K step kt into stage I (and, for int8 B, its register
+  // loads into set Q).  Columns at or past k read 0.
+  u32x4 qreg[R > 0 ? R : 1][QPX];
+  auto issue = [&](auto I, auto Q, int kt) {
+    const uint32_t st = stage_addr<decltype(I)::value, C::STAGE>();
+    const bool full = kt < kfull;  // known true in the main loop (the compiler folds it)
+#pragma unroll
+    for (int j = 0; j < C::AI; ++j) {
+      const uint32_t kb = static_cast<uint32_t>(kt * 64 * sizeof(TB));
+      const uint32_t dst = st + 1024u * (NW * j + wave);
+      if (full) dma16(rx, a_goff[j], kb, dst);
+      else dma16(rx, kt * 64 + a_col[j] < p.k ? a_goff[j] + kb : kOob, 0, dst);
+    }
+    if constexpr (!QR) {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
+#pragma unroll
+        for (int j = 0; j < C::BI; ++j) {
+          const uint32_t dst = st + C::A_BYTES + bi * C::B_BYTES + 1024u * (NW * j + wave);
+          const uint32_t kb = static_cast<uint32_t>(kt * 64 * EB);
+          if (full) dma16(rb[bi], b_goff[j], kb, dst);
+          else dma16(rb[bi], kt * 64 + b_col[j] < p.k ? b_goff[j] + kb : kOob, 0, dst);
+        }
+      }
+    } else {
+      constexpr int q = decltype(Q)::value;
+#pragma unroll
+      for (int i = 0; i < C::QP; ++i) {
+        const uint32_t kb = static_cast<uint32_t>(kt * 64);
+        if (full) qreg[q][i] = __builtin_amdgcn_raw_buffer_load_b128(rb[0], q_goff[i], kb, 0);
+        else qreg[q][i] = __builtin_amdgcn_raw_buffer_load_b128(rb[0], kt * 64 + q_col[i] < p.k ? q_goff[i] + kb : kOob, 0, 0);
+      }
+    }
+  };
+  // int8 B: widens register set Q into stage I as 16-bit chunks.
+  auto store_q = [&](auto I, auto Q) {
+    if constexpr (QR) {
+      uint8_t* bb = stage_ptr<decltype(I)::value, C::STAGE>() + C::A_BYTES;
+      constexpr int q = decltype(Q)::value;
+#pragma unroll
+      for (int i = 0; i < C::QP; ++i) {
+        const u32x4 w = qreg[q][i];
+        lds_write16(bb, q_loff[i], widen8<T>(w.x, w.y));
+        lds_write16(bb, q_loff[i] ^ 16u, widen8<T>(w.z, w.w));  // chunk 2kc + 1: the swizzle flips bit 4 only
+      }
+    }
+  };
+
+  f32x16 acc[NB][FM][FN];
+#pragma unroll
+  for (int bi = 0; bi < NB; ++bi) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[bi][i][j][r] = 0.f;
+      }
+    }
+  }
+
+  // Operand rows of this lane inside a stage.
+  const uint32_t lrow = lane & 31, h = lane >> 5;
+  const uint32_t arow0 = wm * FM * 32 + lrow;
+  const uint32_t brow0 = wn * FN * 32 + lrow;
+
+  // A step's operands in registers: A pieces of the 4 sub-steps; B pieces
+  // per sub-step (16-bit in LDS) or per pair of sub-steps (int8 in LDS: chunk
+  // 2h + q of the row, whose first 8 bytes feed sub-step 2q, the rest 2q + 1).
+  constexpr int BQ = BK == B_I8 ? 2 : 4;
+  struct Frags {
+    u32x4 a[4][FM];
+    u32x4 b[NB][BQ][FN];
+  };
+  auto read_frags = [&](auto I, Frags& f) {
+    const uint8_t* abase = stage_ptr<decltype(I)::value, C::STAGE>();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) f.a[s][i] = lds_read16(abase, swz16(arow0 + 32 * i, 4 * h + s));
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (BK == B_I8) {
+            if (s < BQ) f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz8(brow0 + 32 * j, 2 * h + s));
+          } else {
+            f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz16(brow0 + 32 * j, 4 * h + s));
+          }
+        }
+      }
+    }
+  };
+  auto mfma_frags = [&](const Frags& f) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
+        u32x4 bf[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (BK == B_I8) {
+            const u32x4 raw = f.b[bi][s >> 1][j];
+            bf[j] = (s & 1) ? widen8<T>(raw.z, raw.w) : widen8<T>(raw.x, raw.y);
+          } else {
+            bf[j] = f.b[bi][s][j];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[bi][i][j] = mfma32<T>(bf[j], f.a[s][i], acc[bi][i][j]);
+        }
+      }
+    }
+  };
+
+  // Pipeline.  Step t computes from registers read out of stage t % S one
+  // step earlier.  In step t a wave
+  //   (int8 B) waits until its loads of step t + 1 have landed -- the DMA of
+  //     A is in the same in-order stream, so it has landed too -- and widens
+  //     its B pieces of step t + 1 into stage (t + 1) % S;
+  //   refills stage (t - 1) % S, which every wave finished reading before the
+  //     previous barrier, with step t + S - 1 (int8 B: into registers);
+  //   (16-bit B) waits for its own DMA of step t + 1;
+  //   waits for its LDS reads of step t and its B stores, meets the other
+  //     waves at the barrier -- all of step t + 1 is now in LDS -- issues the
+  //     LDS reads of step t + 1 and runs the MFMAs of step t while they land.
+  Frags fr[2];
+  if constexpr (QR) {
+    // prologue: step 0 through a register set of its own, then steps 1 .. S - 2
+    issue(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, 0);
+    wait_vmcnt<0>();
+    store_q(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    static_for([&](auto I) {
+      constexpr int st = decltype(I)::value + 1;  // step and stage 1 .. S - 2
+      if (st < nk) issue(std::integral_constant<int, st>{}, std::integral_constant<int, st % R>{}, st);
+    }, std::make_index_sequence<S - 2>{});
+  } else {
+    static_for([&](auto I) {
+      if (decltype(I)::value < nk) issue(I, std::integral_constant<int, 0>{}, decltype(I)::value);
+    }, std::make_index_sequence<S - 1>{});
+    if (S - 2 < nk) wait_vmcnt<(S - 2) * C::P>();
+    else wait_vmcnt<0>();
+  }
+  wait_lgkmcnt0();
+  lds_barrier();
+  read_frags(std::integral_constant<int, 0>{}, fr[0]);
+
+  // stage, register-set and fragment indices known at compile time
+  constexpr int UNROLL = QR ? lcm_c(lcm_c(S, 2), R) : lcm_c(S, 2);
+  // One step; GUARD = false where every condition is known to hold (all
+  // steps it touches are full 64-column steps inside k), so the main loop has
+  // no branches and the compiler's own wait-count tracking stays exact.
+  auto step = [&](auto I, auto GUARD, int t) {
+    constexpr int ii = decltype(I)::value, si = ii % S, pi = ii % 2, qi = (ii + 1) % R;
+    constexpr bool guard = decltype(GUARD)::value;
+    if constexpr (QR) {
+      if (!guard || t + 1 < nk) {
+        if (!guard || t + S - 2 < nk) wait_vmcnt<(S - 3) * C::P>();
+        else wait_vmcnt<0>();
+        store_q(std::integral_constant<int, (si + 1) % S>{}, std::integral_constant<int, qi>{});
+      }
+      if (!guard || t + S - 1 < nk)
+        issue(std::integral_constant<int, (si + S - 1) % S>{}, std::integral_constant<int, qi>{}, t + S - 1);
+    } else {
+      if (!guard || t + S - 1 < nk)
+        issue(std::integral_constant<int, (si + S - 1) % S>{}, std::integral_constant<int, 0>{}, t + S - 1);
+      if (!guard || t + 1 < nk) {
+        if (!guard || t + S - 1 < nk) wait_vmcnt<(S - 2) * C::P>();
+        else wait_vmcnt<0>();
+      }
+    }
+    if (!guard || t + 1 < nk) {
+      wait_lgkmcnt0();
+      lds_barrier();
+      read_frags(std::integral_constant<int, (si + 1) % S>{}, fr[pi ^ 1]);
+    }
+    // keep the LDS reads of step t + 1 ahead of the MFMAs of step t, and the
+    // MFMAs ahead of the next step's waits and barrier
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_frags(fr[pi]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int t0 = 0;
+  // main loop: steps t0 .. t0 + UNROLL - 1 issue steps up to t0 + UNROLL + S - 2 < kfull
+  for (; t0 + UNROLL + S - 2 < kfull; t0 += UNROLL) {
+    static_for([&](auto I) { step(I, std::false_type{}, t0 + decltype(I)::value); },
+               std::make_index_sequence<UNROLL>{});
+  }
+  for (; t0 < nk; t0 += UNROLL) {
+    static_for([&](auto I) {
+      if (t0 + decltype(I)::value < nk) step(I, std::true_type{}, t0 + decltype(I)::value);
+    }, std::make_index_sequence<UNROLL>{});
+  }
+
+  // Epilogue.  The MFMAs take the weights as their first operand, so D of a
+  // 32x32 tile is transposed: lane l, register r -> x row l % 32, output
+  // column (r & 3) + 4 (l / 32) + 8 (r / 4).  Registers 4g .. 4g + 3 are four
+  // consecutive columns of one row: one 8-byte store (16 bytes for fp32).
+  const bool vec_out = (p.os & 3) == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nl = wn * FN * 32 + 32 * j + 4 * static_cast<int>(h) + 8 * g;  // first of 4 columns
+      if (nl >= nrows_b) continue;
+      const int n = n0 + nl;
+      const bool full4 = nl + 4 <= nrows_b;
+      float sc[4] = {1.f, 1.f, 1.f, 1.f}, bz[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (EPI == EPI_W8) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (nl + e < nrows_b) {
+            sc[e] = load_dyn(p.scale, n + e, p.sdt);
+            if (p.bdt >= 0) bz[e] = load_dyn(p.bias, n + e, p.bdt);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int ml = wm * FM * 32 + 32 * i + static_cast<int>(lrow);
+        if (ml >= nrows_x) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (EPI == EPI_W8) {
+            v[e] = p.bdt >= 0 ? __builtin_fmaf(acc[0][i][j][4 * g + e], sc[e], bz[e]) : acc[0][i][j][4 * g + e] * sc[e];
+          } else {
+            v[e] = silu_mul_f32(acc[0][i][j][4 * g + e], acc[NB - 1][i][j][4 * g + e]);
+          }
+        }
+        const int64_t o = static_cast<int64_t>(m0 + ml) * p.os + n;
+        if (full4 && vec_out) {
+          if constexpr (is_half_width<TO>::value) {
+            f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
+            *reinterpret_cast<u32x2*>(static_cast<typename TO::bits*>(p.out) + o) = u32x2{narrow2<TO>(lo), narrow2<TO>(hi)};
+          } else {
+            *reinterpret_cast<u32x4*>(static_cast<float*>(p.out) + o) = u32x4{as_u32(v[0]), as_u32(v[1]), as_u32(v[2]), as_u32(v[3])};
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (nl + e < nrows_b) store_elem<TO>(p.out, o + e, v[e]);
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace tiled
+}  // namespace mi355

@@ -15,9 +15,9 @@
 //                  read once per call at HBM bandwidth and meets up to 32 rows
 //                  of x on MFMA (v_mfma_f32_16x16x32_{f16,bf16}).  Also used
 //                  for a few 32-row tiles when the tiled grid would be small.
-//   w8a16_tiled    more rows (prefill): an LDS-tiled MFMA GEMM; the int8 tile
-//                  is widened to fp16/bf16 once, on its way into LDS, and shared
-//                  by every wave of the workgroup.
+//   tiled_gemm     more rows (prefill): the LDS-tiled MFMA GEMM of
+//                  tiled_gemm.h with int8 weights kept int8 in LDS and widened
+//                  after each LDS read, scale and bias in its epilogue.
 //   w8a16_generic  any k, stride or alignment the two above cannot take:
 //                  one wave per (output feature, 4 rows of x), fp32 fma.
 //
@@ -49,6 +49,7 @@
 // traffic), so any k that is a multiple of 16 needs no remainder loop.  The
 // per-wave partial sums meet in LDS in a fixed order.
 #include "common.h"
+#include "tiled_gemm.h"
 
 namespace mi355 {
 namespace {
@@ -229,131 +230,6 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
   }
 }
 
-// ------------------------------------------------------------------- tiled
-//
-// Workgroup tile BM x BN of the output, K in steps of 64 columns, 4 waves in a
-// 2 x 2 grid, each computing (BM / 2) x (BN / 2) with 16x16x32 MFMAs.  Per K
-// step every thread loads its share of the x tile (16-byte pieces) and of the
-// int8 tile (16 weights per piece) into registers, widens the weights, and
-// stores both into the LDS buffer the waves read next; two LDS buffers, one
-// barrier per step.  LDS rows are padded by 16 bytes, so the 16-byte operand
-// reads of 8 consecutive rows fall in distinct banks.
-
-constexpr int kBK = 64;
-constexpr int kLdsRow = kBK + 8;  // elements per LDS row (144 bytes)
-
-template <typename T, typename TO, int BM, int BN>
-__global__ __launch_bounds__(256) void w8a16_tiled(const W8Params p) {
-  using TB = typename T::bits;
-  constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
-  constexpr int FM = WM / 16, FN = WN / 16; // MFMA tiles per wave
-  constexpr int XP = BM * kBK / 8 / 256;    // 16-byte x pieces per thread per step
-  constexpr int QP = BN * kBK / 16 / 256;   // 16-byte int8 pieces per thread per step
-  static_assert(XP >= 1 && QP >= 1, "tile too small for 256 threads");
-  __shared__ __attribute__((aligned(16))) TB xs_lds[2][BM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) TB ws_lds[2][BN * kLdsRow];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
-  const int nrows_w = p.n - n0 < BN ? p.n - n0 : BN;
-  const int nrows_x = p.rows - m0 < BM ? p.rows - m0 : BM;
-  const rsrc_t rq = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
-                              static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
-  const rsrc_t rx = make_rsrc(static_cast<const TB*>(p.x) + static_cast<int64_t>(m0) * p.xs,
-                              static_cast<uint32_t>(((nrows_x - 1) * p.xs + p.k) * sizeof(TB)));
-
-  // Piece i of this thread: x row (tid + 256 i) / 8, column 8 * ((tid + 256 i) % 8);
-  // int8 row (tid + 256 i) / 4, column 16 * ((tid + 256 i) % 4).
-  u32x4 xr[XP], qr[QP];
-  auto load_step = [&](int kt) {
-    const int kc = kt * kBK;
-#pragma unroll
-    for (int i = 0; i < XP; ++i) {
-      const int pc = tid + 256 * i;
-      const int c = kc + 8 * (pc & 7);
-      const uint32_t off = static_cast<uint32_t>(((pc >> 3) * p.xs + c) * sizeof(TB));
-      xr[i] = buf_load16_cached(rx, c < p.k ? off : kOob);
-    }
-#pragma unroll
-    for (int i = 0; i < QP; ++i) {
-      const int pc = tid + 256 * i;
-      const int c = kc + 16 * (pc & 3);
-      const uint32_t off = static_cast<uint32_t>((pc >> 2) * p.qs + c);
-      qr[i] = buf_load16(rq, c < p.k ? off : kOob);
-    }
-  };
-  auto store_step = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < XP; ++i) {
-      const int pc = tid + 256 * i;
-      *reinterpret_cast<u32x4*>(&xs_lds[buf][(pc >> 3) * kLdsRow + 8 * (pc & 7)]) = xr[i];
-    }
-#pragma unroll
-    for (int i = 0; i < QP; ++i) {
-      const int pc = tid + 256 * i;
-      u32x4 b0, b1;
-      widen_i8x16<T>(qr[i], b0, b1);
-      TB* dst = &ws_lds[buf][(pc >> 2) * kLdsRow + 16 * (pc & 3)];
-      reinterpret_cast<u32x4*>(dst)[0] = b0;
-      reinterpret_cast<u32x4*>(dst)[1] = b1;
-    }
-  };
-
-  f32x4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  const int nk = (p.k + kBK - 1) / kBK;
-  load_step(0);
-  store_step(0);
-  __syncthreads();
-  // Operand reads: lane l -> row l % 16 of the MFMA tile, k-group l / 16.
-  const int orow = lane & 15, ocol = 8 * (lane >> 4);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_step(kt + 1);
-#pragma unroll
-    for (int ks = 0; ks < kBK / 32; ++ks) {
-      u32x4 a[FM], b[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        a[i] = *reinterpret_cast<const u32x4*>(&xs_lds[buf][(wm * WM + 16 * i + orow) * kLdsRow + 32 * ks + ocol]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        b[j] = *reinterpret_cast<const u32x4*>(&ws_lds[buf][(wn * WN + 16 * j + orow) * kLdsRow + 32 * ks + ocol]);
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<T>(a[i], b[j], acc[i][j]);
-      }
-    }
-    if (kt + 1 < nk) store_step(buf ^ 1);
-    __syncthreads();
-  }
-
-  // D of tile (i, j): lane l holds rows 4 * (l / 16) + r, r < 4, of column l % 16.
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = wn * WN + 16 * j + (lane & 15);
-    if (n >= nrows_w) continue;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = wm * WM + 16 * i + 4 * (lane >> 4) + r;
-        if (m < nrows_x) w8_store<TO>(p, m0 + m, n0 + n, acc[i][j][r]);
-      }
-    }
-  }
-}
-
 // ----------------------------------------------------------------- generic
 
 constexpr int kGenRows = 4;  // rows of x per wave
@@ -523,6 +399,70 @@ int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
   return w8_skinny_g<T, TO, MT, 1>(p, s, cus);
 }
 
+// ------------------------------------------------------------------- tiled
+
+// Buffer descriptors of the tiled GEMM span at most 128 rows of x and 256
+// weight rows; both must stay below 2^31 bytes.
+bool tiled_fits(const W8Params& p) {
+  return int64_t{128} * p.xs * 2 < (int64_t{1} << 31) && int64_t{256} * p.qs < (int64_t{1} << 31) &&
+         static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
+}
+
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S>
+int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
+  using C = tiled::Cfg<T, tiled::B_I8, TO, WGM, WGN, FM, FN, tiled::EPI_W8, S>;
+  static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
+  tiled::Params tp{};
+  tp.x = p.x;
+  tp.b0 = p.q;
+  tp.b1 = p.q;
+  tp.scale = p.scale;
+  tp.bias = p.bias;
+  tp.out = p.out;
+  tp.rows = p.rows;
+  tp.k = p.k;
+  tp.n = p.n;
+  tp.xs = p.xs;
+  tp.bs = p.qs;
+  tp.os = p.os;
+  tp.sdt = p.sdt;
+  tp.bdt = p.bdt;
+  tp.tiles_m = (p.rows + C::BM - 1) / C::BM;
+  tp.tiles_n = (p.n + C::BN - 1) / C::BN;
+  tp.group_m = tp.tiles_m < 4 ? tp.tiles_m : 4;
+  void* args[] = {&tp};
+  // all LDS is static (no dynamic shared memory)
+  return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
+                                                                                      tiled::EPI_W8, S>),
+                                    dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
+                    "w8a16 tiled launch");
+}
+
+// Tile shape by the number T of 128 x 128 output tiles, from a sweep of tile
+// shapes x waves x LDS stages on MI355X over the q/o, k/v, gate/up and down
+// projections of Qwen2.5-1.5B and 7B at 128, 1024 and 4096 rows (every pick
+// within 5% of the best sampled configuration but one, 1024 rows x k 8960,
+// at 1.05x):
+//   T < 128 -> 64 x 64 tiles, 4 waves, 4 stages (the most workgroups);
+//   T < 320 -> 128 x 128, 8 waves, 3 stages;
+//   n <= 2048 -> 128 x 256, 8 waves, 4 stages;
+//   T < 1000 -> 128 x 64, 4 waves, 4 stages;
+//   T < 2000 -> 128 x 128, 4 waves, 3 stages;
+//   else -> 128 x 256, 8 waves, 3 stages.
+// bf16 takes 128 x 128 where fp16 takes 128 x 256: its widening needs more
+// registers, and the 128 x 256 shape would spill.
+template <typename T, typename TO>
+int w8_tiled(const W8Params& p, hipStream_t s) {
+  constexpr bool wide = std::is_same<T, F16>::value;
+  const int64_t t128 = static_cast<int64_t>((p.rows + 127) / 128) * ((p.n + 127) / 128);
+  if (t128 < 128) return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);
+  if (t128 < 320) return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+  if (p.n <= 2048) return wide ? w8_tiled_cfg<T, TO, 2, 4, 2, 2, 4>(p, s) : w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+  if (t128 < 1000) return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(p, s);
+  if (t128 < 2000) return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 3>(p, s);
+  return wide ? w8_tiled_cfg<T, TO, 2, 4, 2, 2, 3>(p, s) : w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+}
+
 template <typename T, typename TO>
 int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   const bool vec = p.k % 16 == 0 && p.qs % 16 == 0 && p.xs % 8 == 0 && aligned16(p.x) && aligned16(p.q);
@@ -534,23 +474,17 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   if (p.rows <= 16) return w8_skinny_shape<T, TO, 2>(p, s, cus);
   if (p.rows <= 24) return w8_skinny_shape<T, TO, 3>(p, s, cus);
   if (p.rows <= 32) return w8_skinny_shape<T, TO, 4>(p, s, cus);
-  // More rows: the tiled GEMM once its 64 x 64 grid fills the chip; below
-  // that (e.g. 128 rows against a K-heavy down projection) 32-row skinny
-  // tiles, which re-read the weights per tile mostly from L2, measured faster.
-  const int64_t small = static_cast<int64_t>((p.n + 63) / 64) * ((p.rows + 63) / 64);
-  bool skinny = small < cus;
+  // More rows: the tiled GEMM, except for small grids of few rows (e.g. 128
+  // rows against a K-heavy down projection), where 32-row skinny tiles with
+  // split K, which re-read the weights per tile mostly from L2, measured faster.
+  const int64_t tiles64 = static_cast<int64_t>((p.n + 63) / 64) * ((p.rows + 63) / 64);
+  bool skinny = p.rows <= 256 && tiles64 < 128;
+  if (!tiled_fits(p)) skinny = true;
 #ifdef MI355_W8_SWEEP
   if (g_force_path > 0) skinny = g_force_path == 1;
 #endif
   if (skinny) return w8_skinny_shape<T, TO, 4>(p, s, cus);
-  // 128 x 128 tiles when they fill the chip, else 64 x 64.
-  const int64_t big = static_cast<int64_t>((p.n + 127) / 128) * ((p.rows + 127) / 128);
-  if (big >= cus) {
-    const dim3 grid(static_cast<unsigned>((p.n + 127) / 128), static_cast<unsigned>((p.rows + 127) / 128));
-    return launch_w8(w8a16_tiled<T, TO, 128, 128>, grid, dim3(256), 0, p, s);
-  }
-  const dim3 grid(static_cast<unsigned>((p.n + 63) / 64), static_cast<unsigned>((p.rows + 63) / 64));
-  return launch_w8(w8a16_tiled<T, TO, 64, 64>, grid, dim3(256), 0, p, s);
+  return w8_tiled<T, TO>(p, s);
 }
 
 }  // namespace

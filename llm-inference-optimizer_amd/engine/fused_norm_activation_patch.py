@@ -26,16 +26,17 @@ RMSNorm + residual" the reference plans (docs/architecture-cuda.md:94).  The
 result is bit-identical to the unfused layer with the fused kernels; the
 count appears as ``"add_rmsnorm"``.  ``fuse_gate_up=True`` (also off by
 default) lets each FusedMLP run its gate / up projections and the
-SiLU-and-mul in one kernel (``fused_gate_up_silu``) for decode-sized batches
-(<= 32 rows); the projections are then not rounded before the activation,
-which changes results by that rounding.  The count appears as ``"gate_up"``.
+SiLU-and-mul in one kernel (``fused_gate_up_silu``: weight streaming for
+decode batches, a tiled MFMA GEMM for prefill); the projections are then not
+rounded before the activation, which changes results by that rounding.  The
+count appears as ``"gate_up"``.
 """
 from __future__ import annotations
 
 import torch
 
 from ..kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm
-from ..kernels.fused_gate_up_hip import GATE_UP_MAX_ROWS, fused_gate_up_silu
+from ..kernels.fused_gate_up_hip import fused_gate_up_silu
 from ..kernels.fused_swiglu_hip import fused_silu_mul
 
 __all__ = ["RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES", "DECODER_LAYER_CLASS_NAMES", "FusedRMSNorm", "FusedMLP",
@@ -69,11 +70,11 @@ class FusedMLP(torch.nn.Module):
     ``act_fn(gate) * up`` step with the fused SiLU-and-mul kernel.  SiLU is
     fixed, as in the reference; the projection modules are reused.
 
-    With ``fuse_gate_up=True``, inputs of at most ``GATE_UP_MAX_ROWS`` rows
-    (decode steps) whose projections are plain bias-free ``nn.Linear`` layers
-    in fp16 / bf16 with k a multiple of 8 take ``fused_gate_up_silu`` instead:
-    gate, up and the activation in one kernel.  Other inputs take the
-    reference path."""
+    With ``fuse_gate_up=True``, inputs whose projections are plain bias-free
+    ``nn.Linear`` layers in fp16 / bf16 with k a multiple of 8 take
+    ``fused_gate_up_silu`` instead (decode steps and prefill alike): gate, up
+    and the activation in one kernel.  Other inputs take the reference
+    path."""
 
     def __init__(self, orig_module: torch.nn.Module, fuse_gate_up: bool = False):
         super().__init__()
@@ -90,7 +91,7 @@ class FusedMLP(torch.nn.Module):
                 and g.weight.shape[1] % 8 == 0)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.fuse_gate_up and x.numel() <= GATE_UP_MAX_ROWS * x.shape[-1]:
+        if self.fuse_gate_up:
             wg, wu = self.gate_proj.weight, self.up_proj.weight
             if x.dtype == wg.dtype == wu.dtype and x.dtype in (torch.float16, torch.bfloat16):
                 return self.down_proj(fused_gate_up_silu(x, wg, wu))

@@ -1,4 +1,4 @@
-"""Gate/up projections fused with SiLU-and-mul, for decode-sized batches.
+"""Gate/up projections fused with SiLU-and-mul.
 
 ``fused_gate_up_silu(x, w_gate, w_up)`` returns ``silu(x @ w_gate.T) *
 (x @ w_up.T)`` in one gfx950 kernel (C ABI ``mi355_gate_up_silu_fwd``): the
@@ -10,11 +10,11 @@ written or read.  This is the fusion the reference's design lists next
 (docs/architecture-cuda.md:94).
 
 At decode sizes (rows <= 32) the call streams both weight matrices once, at
-HBM bandwidth; larger batches are GEMMs, which FusedMLP leaves to the GEMM
-library.  Because g and u are not rounded to x's dtype before the
-activation, results differ from the unfused chain by that rounding (they are
-closer to the exact value), so FusedMLP uses it only on request
-(``fuse_gate_up=True``).
+HBM bandwidth; larger batches run an LDS-tiled MFMA GEMM over both weight
+matrices with SiLU-and-mul in its epilogue.  Because g and u are not rounded
+to x's dtype before the activation, results differ from the unfused chain by
+that rounding (they are closer to the exact value), so FusedMLP uses it only
+on request (``fuse_gate_up=True``).
 """
 from __future__ import annotations
 
@@ -24,7 +24,8 @@ from .. import _lib
 
 __all__ = ["fused_gate_up_silu", "naive_gate_up_silu_reference", "GATE_UP_MAX_ROWS"]
 
-# Rows up to which the fused kernel streams the weights once (one 32-row tile).
+# Rows up to which the fused kernel streams the weights once (one 32-row
+# tile); more rows take the tiled GEMM.
 GATE_UP_MAX_ROWS = 32
 
 _CODE = _lib.DTYPE_CODE

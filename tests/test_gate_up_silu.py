@@ -73,6 +73,8 @@ def _check_vs_oracle(orc, got16, got32, x, wg, wu, dt):
     (8, 1536, 8960, F16), (1, 1536, 8960, BF16), (32, 1536, 8960, F16), (16, 896, 4864, BF16),
     (4, 3584, 18944, BF16), (5, 72, 40, F16), (33, 40, 24, BF16), (3, 8, 7, F16), (100, 256, 100, BF16),
     (17, 2048, 1000, F16),
+    # prefill rows: the tiled GEMM (each of its three launch shapes, k tails, ragged edges)
+    (64, 1536, 1000, F16), (200, 640, 10240, BF16), (300, 1552, 520, F16), (257, 96, 333, BF16),
 ])
 def test_gate_up_silu_matches_oracle(pkg, orc, cuda, rows, k, n, dt):
     x, wg, wu = _inputs(rows, k, n, dt, seed=80 + rows)
@@ -184,7 +186,31 @@ def test_large_shape_against_torch_fp64(pkg, cuda):
     assert rel < 1e-5
 
 
-def test_fused_mlp_opt_in_takes_the_fused_kernel_for_decode_rows(pkg, cuda, monkeypatch):
+@pytest.mark.parametrize("rows,k,n,dt", [(1024, 1536, 8960, F16), (2048, 3584, 4736, BF16)])
+def test_prefill_shapes_against_torch_fp64(pkg, cuda, rows, k, n, dt):
+    """Prefill-sized batches (the tiled GEMM path) against fp64 GEMMs on the
+    GPU: every output within one output ulp plus the fp32 summation bound,
+    the fp32 output within the bound."""
+    torch.manual_seed(rows)
+    x = torch.randn(rows, k, device=cuda).to(dt)
+    wg = (torch.randn(n, k, device=cuda) * (2.0 * k ** -0.5)).to(dt)
+    wu = (torch.randn(n, k, device=cuda) * k ** -0.5).to(dt)
+    got16 = pkg.fused_gate_up_silu(x, wg, wu).double()
+    got32 = pkg.fused_gate_up_silu(x, wg, wu, out_dtype=F32).double()
+    x64 = x.double()
+    g, u = x64 @ wg.double().T, x64 @ wu.double().T
+    gabs, uabs = x64.abs() @ wg.double().abs().T, x64.abs() @ wu.double().abs().T
+    exact = torch.nn.functional.silu(g) * u
+    bound = torch.from_numpy(_act_error_bound(g.cpu().numpy(), u.cpu().numpy(), gabs.cpu().numpy(),
+                                              uabs.cpu().numpy(), k)).to(cuda)
+    ulp = torch.from_numpy(_ulp(exact.cpu().numpy(), dt)).to(cuda)
+    assert float(((got32 - exact).abs() - (2.0 ** -22 * exact.abs() + bound)).max()) <= 1e-30
+    assert float(((got16 - exact).abs() - (ulp + bound + 2.0 ** -22 * exact.abs())).max()) <= 0
+    # the 16-bit output is the fp32 output rounded once
+    assert torch.equal(got16.to(dt), got32.to(dt))
+
+
+def test_fused_mlp_opt_in_takes_the_fused_kernel(pkg, cuda, monkeypatch):
     transformers = pytest.importorskip("transformers")
     from transformers import Qwen2Config, Qwen2ForCausalLM
     patch_mod = importlib.import_module("llm-inference-optimizer_amd.engine.fused_norm_activation_patch")
@@ -206,12 +232,12 @@ def test_fused_mlp_opt_in_takes_the_fused_kernel_for_decode_rows(pkg, cuda, monk
     monkeypatch.setattr(patch_mod, "fused_gate_up_silu", counting)
     ids = torch.randint(0, 512, (2, 40), device=cuda)
     with torch.inference_mode():
-        lb = base(ids[:, :8]).logits.float()       # 16 rows: fused projections
+        lb = base(ids[:, :8]).logits.float()       # 16 rows: fused projections (weight streaming)
         lf = fused(ids[:, :8]).logits.float()
         assert len(calls) == 4
-        pb = base(ids).logits.float()              # 80 rows: reference path
+        pb = base(ids).logits.float()              # 80 rows: fused projections (tiled GEMM)
         pf = fused(ids).logits.float()
-        assert len(calls) == 4
+        assert len(calls) == 8
     for a, b in ((lb, lf), (pb, pf)):
         err = (a - b).abs().max().item()
         assert err <= 0.05 * a.abs().max().item(), err

@@ -131,6 +131,33 @@ def test_bf16_matches_oracle(pkg, orc, cuda, M, K, N, bias):
     print(f"bf16 W8A16 [{M}x{K}] x [{N}x{K}]: {same:.5f} equal to the oracle")
 
 
+# Prefill shapes that land on each of the tiled GEMM's launch shapes (by the
+# number of 128 x 128 output tiles), with k tails and ragged edges.
+TILED_CASES = [
+    (300, 1552, 1000, F16, True),     # < 128 tiles: 64 x 64
+    (512, 512, 8960, F16, False),     # < 320: 128 x 128, 8 waves
+    (200, 2048, 8960, BF16, True),    # <= 256 rows but a large grid: tiled, 128 x 128
+    (4096, 256, 1536, F16, True),     # n <= 2048: 128 x 256
+    (4096, 256, 1536, BF16, False),   # (bf16: 128 x 128)
+    (1024, 272, 8960, BF16, False),   # < 1000: 128 x 64
+    (2048, 128, 8952, F16, False),    # < 2000: 128 x 128, 4 waves
+    (4096, 64, 8960, F16, True),      # the rest: 128 x 256
+    (4096, 80, 9000, BF16, True),     # (bf16: 128 x 128)
+]
+
+
+@pytest.mark.parametrize("M,K,N,dt,bias", TILED_CASES)
+def test_tiled_launch_shapes_match_oracle(pkg, orc, cuda, M, K, N, dt, bias):
+    lin = _linear(K, N, bias, cuda, dtype=dt, seed=M + N)
+    q = pkg.QuantizedLinearInt8.from_linear(lin)
+    x = _x(M, K, dt, cuda, seed=M + 3)
+    got16 = pkg.w8a16_linear(x, q.weight_q, q.scale, q.bias)
+    got32 = pkg.w8a16_linear(x, q.weight_q, q.scale, q.bias, out_dtype=F32)
+    same = _check_kernel(orc, x, q, got16, got32)
+    assert torch.equal(got16, got32.to(dt)), "the 16-bit output must be the fp32 output rounded once"
+    print(f"tiled W8A16 [{M}x{K}] x [{N}x{K}] {dt}: {same:.5f} equal to the oracle")
+
+
 @pytest.mark.parametrize("sdt,bdt", [(F16, F16), (BF16, F32), (F32, BF16)])
 def test_scale_and_bias_dtypes(pkg, orc, cuda, sdt, bdt):
     M, K, N = 6, 512, 72
