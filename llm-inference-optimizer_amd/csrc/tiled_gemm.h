@@ -11,40 +11,57 @@
 // accumulation (v_mfma_f32_32x32x16_{f16,bf16}), fp32 epilogue, one rounding.
 //
 // Decomposition.  A workgroup of WGM x WGN waves owns a BM x BN output tile
-// (BM = 32 FM WGM, BN = 32 FN WGN); each wave owns FM x FN 32x32 MFMA tiles.
-// K advances in steps of 64 columns through two LDS stages: the global loads
-// of step t + 1 are issued (16 bytes per lane, buffer descriptors whose
-// extent ends at the last valid element, so rows past the matrix read 0)
-// before the MFMAs of step t, and stored to the other stage after them; one
-// barrier per step.  Columns at or past k are redirected past the descriptor,
-// so any k that is a multiple of 16 (int8) or 8 (16-bit) needs no remainder
-// loop.
+// (BM = 32 FM WGM, BN = 32 FN WGN); each wave owns FM x FN 32x32 MFMA tiles
+// (of each B matrix).  K advances in steps of 64 columns through a ring of S
+// LDS stages filled by gfx950's global -> LDS DMA (buffer_load_dwordx4 ...
+// lds, 16 bytes per lane, no VGPR staging): step t + S - 1 is in flight while
+// step t computes.  Buffer descriptors end at the last valid element (rows
+// past the matrix read 0); the K step enters through the scalar offset, and
+// only a final partial step redirects columns at or past k past the
+// descriptor, so any k that is a multiple of 16 (int8) or 8 (16-bit) works.
 //
-// K order inside a step.  The MFMA's A operand gives lane l row l % 32 and
-// 8 consecutive k of k-group h = l / 32; B likewise.  A step's 64 columns are
-// dealt so that k-group h of sub-step s (s < 4) holds columns 32 h + 8 s ..
-// + 8: a lane's A piece of sub-step s is 16-byte chunk 4 h + s of its 128-byte
-// row, and an int8 B row's 16-byte chunk 2 h + j feeds sub-steps 2 j and
-// 2 j + 1, so one LDS read serves two MFMAs.  The sum is the same (fp32
-// summation order aside) as in natural order, since A and B agree.
+// Per step a wave waits for its own DMA of the next step (vmcnt, the later
+// steps stay in flight), meets the other waves at one barrier, issues the
+// LDS reads of the next step and then the MFMAs of this step, whose operands
+// it read one step earlier, so LDS latency hides behind the MFMAs.  The main
+// loop is unrolled so stage and register-set indices are compile-time
+// constants and has no branches (a guarded copy runs the last steps), which
+// keeps the compiler's own wait-count tracking exact; sched_barriers keep
+// the reads ahead of, and the next step's waits behind, the MFMAs.  The DMA
+// is inline asm so the compiler neither tracks its LDS writes nor drains
+// every load in flight before an LDS read; the kernel orders them itself.
+//
+// K order inside a step.  The MFMA operands give lane l row l % 32 and 8
+// consecutive k of k-group h = l / 32.  A step's 64 columns are dealt so that
+// k-group h of sub-step s (s < 4) holds columns 32 h + 8 s .. + 8: a lane's
+// 16-bit piece of sub-step s is chunk 4 h + s of its 128-byte row, and an
+// int8 row's 16-byte chunk 2 h + j feeds sub-steps 2 j and 2 j + 1.  Both
+// operands use the same order, so the sum is unchanged (fp32 order aside).
 //
 // LDS layout.  16-bit tiles: 128-byte rows, chunk c of row r stored at chunk
 // c ^ f(r), f(r) = (r ^ (r >> 3)) & 7.  int8 tiles: 64-byte rows, chunk c at
-// c ^ g(r), g(r) = ((r >> 1) ^ (r >> 3)) & 3.  Every 16-byte read of 8 (or
-// 16) consecutive rows at one logical chunk, and every 16-byte write of a
-// row's consecutive chunks, then falls in distinct banks for both 128- and
-// 256-byte bank rows.
+// c ^ g(r), g(r) = ((r >> 1) ^ (r >> 3)) & 3.  The 16-byte reads of 8 (or 16)
+// consecutive rows at one logical chunk then fall in distinct banks for 128-
+// and 256-byte bank rows (measured: no bank conflicts on the 16-bit tiles).
+// A DMA instruction fills 1 KiB of consecutive LDS, so lane l loads the
+// logical chunk that the swizzle keeps at its physical slot.
 //
-// int8 weights stay int8 in LDS (half the footprint and LDS traffic of a
-// widened tile) and are widened in registers after each read: 0x64uu is the
+// int8 weights (B_I8) stay int8 in LDS -- half the footprint, half the LDS
+// traffic -- and are widened in registers after each read: 0x64uu is the
 // fp16 pattern of 1024 + u, so (q ^ 0x80) spliced under 0x64 minus 1152 is q
 // (v_perm_b32 + v_pk_add_f16 per pair); bf16 goes through v_cvt_f32_i32.
-// Every int8 is exact in both 16-bit types.
+// Every int8 is exact in both 16-bit types.  (Widening once per workgroup
+// on a register path into a 16-bit LDS tile measured slower: those loads are
+// visible to the compiler, whose waits for them drain the DMA pipeline.)
+//
+// Epilogue.  The MFMAs take b as their first operand, so each lane ends with
+// four consecutive output columns of one row per register group: 8-byte
+// stores (16 for fp32 out).
 //
 // Grid: one workgroup per tile, 1-D.  Consecutive workgroup ids land on
 // different XCDs (round robin over 8), so ids are remapped to give each XCD
-// a contiguous range of tiles, ordered m-fastest: the x row blocks that share
-// a weight block run on one XCD and the weights are fetched from HBM once.
+// a contiguous range of tiles, ordered in groups of group_m m-blocks, m
+// fastest: the x row blocks that share a weight block run on one XCD.
 #pragma once
 
 #include <type_traits>
@@ -62,7 +79,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr uint32_t kOob = 0xfffffff0u;  // past every descriptor the launchers admit (< 2^31 bytes)
 
 enum { EPI_W8 = 0, EPI_SILU = 1 };
-enum { B_16 = 0, B_I8 = 1, B_I8R = 2 };
+enum { B_16 = 0, B_I8 = 1 };
 
 template <typename T> __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
 template <> __device__ __forceinline__ f32x16 mfma32<F16>(u32x4 a, u32x4 b, f32x16 c) {
@@ -133,27 +150,23 @@ struct Params {
 
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S>
 struct Cfg {
-  // BK: how B reaches LDS -- B_16 (16-bit B, DMA), B_I8 (int8 B, DMA, int8 in
-  // LDS, widened after each LDS read) or B_I8R (int8 B through registers,
-  // widened once and stored 16-bit).
-  static constexpr bool I8 = BK != B_16, QR = BK == B_I8R;
+  // BK: B's storage -- B_16 (x's 16-bit type) or B_I8 (int8, kept int8 in
+  // LDS and widened after each LDS read).
+  static constexpr bool I8 = BK == B_I8;
   static constexpr int NW = WGM * WGN, NT = 64 * NW;
   static constexpr int BM = 32 * FM * WGM, BN = 32 * FN * WGN;
   static constexpr int NB = EPI == EPI_SILU ? 2 : 1;  // B matrices
   static constexpr int A_BYTES = BM * 128;             // 64 columns of 16-bit x per row
-  static constexpr int B_ROW = BK == B_I8 ? 64 : 128;  // bytes per B row per step in LDS
+  static constexpr int B_ROW = I8 ? 64 : 128;          // bytes per B row per step in LDS
   static constexpr int B_BYTES = BN * B_ROW;
   static constexpr int STAGE = A_BYTES + NB * B_BYTES;
   static constexpr int LDS = S * STAGE;
   // One DMA instruction moves 64 lanes x 16 bytes = 1 KiB: 8 rows of a 16-bit
   // tile, 16 rows of an int8 tile.
-  static constexpr int AI = A_BYTES / 1024 / NW;           // A DMA instructions per wave per step
-  static constexpr int BI = QR ? 0 : B_BYTES / 1024 / NW;  // B DMA instructions per wave per step and matrix
-  static constexpr int QP = QR ? BN * 4 / NT : 0;          // B_I8R: 16-byte register loads per thread per step
-  static constexpr int P = AI + NB * BI + QP;          // vector-memory instructions per wave per step
-  static constexpr int R = S - 2;                      // int8 B register sets in flight
-  static_assert(A_BYTES % (1024 * NW) == 0 && (QR || B_BYTES % (1024 * NW) == 0), "tile must split over the waves");
-  static_assert(!QR || (BN * 4) % NT == 0, "int8 tile must split over the threads");
+  static constexpr int AI = A_BYTES / 1024 / NW;  // A DMA instructions per wave per step
+  static constexpr int BI = B_BYTES / 1024 / NW;  // B DMA instructions per wave per step and matrix
+  static constexpr int P = AI + NB * BI;          // DMA instructions per wave per step
+  static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "tile must split over the waves");
   static_assert(S >= 3 && S <= 8, "3..8 stages");
   static_assert(P * (S - 2) < 64, "vmcnt range");
 };
@@ -208,13 +221,12 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S>
 __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
-  constexpr bool I8 = C::I8, QR = C::QR;
+  constexpr bool I8 = C::I8;
   using TB = typename T::bits;
-  constexpr int NW = C::NW, NT = C::NT, BM = C::BM, BN = C::BN, NB = C::NB, R = C::R;
+  constexpr int NW = C::NW, BM = C::BM, BN = C::BN, NB = C::NB;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
 
   // Tile of this workgroup: contiguous ranges per XCD, m fastest.
@@ -253,12 +265,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     a_goff[j] = static_cast<uint32_t>((r * p.xs + 8 * c) * sizeof(TB));
     a_col[j] = 8 * c;
   }
-  constexpr int BIX = C::BI > 0 ? C::BI : 1;
-  uint32_t b_goff[BIX];
-  int b_col[BIX];
+  uint32_t b_goff[C::BI];
+  int b_col[C::BI];
 #pragma unroll
-  for (int j = 0; j < BIX; ++j) {
-    if constexpr (BK == B_I8) {  // 16 rows of 64 bytes per instruction
+  for (int j = 0; j < C::BI; ++j) {
+    if constexpr (I8) {  // 16 rows of 64 bytes per instruction
       const int r = 16 * (NW * j + wave) + (lane >> 2);
       const int c = (lane & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);
       b_goff[j] = static_cast<uint32_t>(r * p.bs + 16 * c);
@@ -270,28 +281,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       b_col[j] = 8 * c;
     }
   }
-  // int8 B register pieces: piece c = tid + NT i -> row c / 4, 16 int8 at
-  // columns 16 (c % 4) .. + 16, widened into 16-bit chunks 2 (c % 4) and
-  // 2 (c % 4) + 1 of that row.
-  constexpr int QPX = C::QP > 0 ? C::QP : 1;
-  uint32_t q_goff[QPX], q_loff[QPX];
-  int q_col[QPX];
-#pragma unroll
-  for (int i = 0; i < QPX; ++i) {
-    const int c = tid + NT * i;
-    const int r = c >> 2, kc = c & 3;
-    q_goff[i] = static_cast<uint32_t>(r * p.bs + 16 * kc);
-    q_loff[i] = swz16(r, 2 * kc);  // chunk 2 kc; chunk 2 kc + 1 is at swz16(r, 2 kc + 1)
-    q_col[i] = 16 * kc;
-  }
-
   const int nk = (p.k + 63) >> 6;
   const int kfull = p.k >> 6;  // steps whose 64 columns are all inside k
 
-  // Issues the DMA of K step kt into stage I (and, for int8 B, its register
-  // loads into set Q).  Columns at or past k read 0.
-  u32x4 qreg[R > 0 ? R : 1][QPX];
-  auto issue = [&](auto I, auto Q, int kt) {
+  // Issues the DMA of K step kt into stage I.  Columns at or past k read 0.
+  auto issue = [&](auto I, int kt) {
     const uint32_t st = stage_addr<decltype(I)::value, C::STAGE>();
     const bool full = kt < kfull;  // known true in the main loop (the compiler folds it)
 #pragma unroll
@@ -301,37 +295,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       if (full) dma16(rx, a_goff[j], kb, dst);
       else dma16(rx, kt * 64 + a_col[j] < p.k ? a_goff[j] + kb : kOob, 0, dst);
     }
-    if constexpr (!QR) {
 #pragma unroll
-      for (int bi = 0; bi < NB; ++bi) {
+    for (int bi = 0; bi < NB; ++bi) {
 #pragma unroll
-        for (int j = 0; j < C::BI; ++j) {
-          const uint32_t dst = st + C::A_BYTES + bi * C::B_BYTES + 1024u * (NW * j + wave);
-          const uint32_t kb = static_cast<uint32_t>(kt * 64 * EB);
-          if (full) dma16(rb[bi], b_goff[j], kb, dst);
-          else dma16(rb[bi], kt * 64 + b_col[j] < p.k ? b_goff[j] + kb : kOob, 0, dst);
-        }
-      }
-    } else {
-      constexpr int q = decltype(Q)::value;
-#pragma unroll
-      for (int i = 0; i < C::QP; ++i) {
-        const uint32_t kb = static_cast<uint32_t>(kt * 64);
-        if (full) qreg[q][i] = __builtin_amdgcn_raw_buffer_load_b128(rb[0], q_goff[i], kb, 0);
-        else qreg[q][i] = __builtin_amdgcn_raw_buffer_load_b128(rb[0], kt * 64 + q_col[i] < p.k ? q_goff[i] + kb : kOob, 0, 0);
-      }
-    }
-  };
-  // int8 B: widens register set Q into stage I as 16-bit chunks.
-  auto store_q = [&](auto I, auto Q) {
-    if constexpr (QR) {
-      uint8_t* bb = stage_ptr<decltype(I)::value, C::STAGE>() + C::A_BYTES;
-      constexpr int q = decltype(Q)::value;
-#pragma unroll
-      for (int i = 0; i < C::QP; ++i) {
-        const u32x4 w = qreg[q][i];
-        lds_write16(bb, q_loff[i], widen8<T>(w.x, w.y));
-        lds_write16(bb, q_loff[i] ^ 16u, widen8<T>(w.z, w.w));  // chunk 2kc + 1: the swizzle flips bit 4 only
+      for (int j = 0; j < C::BI; ++j) {
+        const uint32_t kb = static_cast<uint32_t>(kt * 64 * EB);
+        const uint32_t dst = st + C::A_BYTES + bi * C::B_BYTES + 1024u * (NW * j + wave);
+        if (full) dma16(rb[bi], b_goff[j], kb, dst);
+        else dma16(rb[bi], kt * 64 + b_col[j] < p.k ? b_goff[j] + kb : kOob, 0, dst);
       }
     }
   };
@@ -357,7 +328,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
   // A step's operands in registers: A pieces of the 4 sub-steps; B pieces
   // per sub-step (16-bit in LDS) or per pair of sub-steps (int8 in LDS: chunk
   // 2h + q of the row, whose first 8 bytes feed sub-step 2q, the rest 2q + 1).
-  constexpr int BQ = BK == B_I8 ? 2 : 4;
+  constexpr int BQ = I8 ? 2 : 4;
   struct Frags {
     u32x4 a[4][FM];
     u32x4 b[NB][BQ][FN];
@@ -372,7 +343,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       for (int bi = 0; bi < NB; ++bi) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          if constexpr (BK == B_I8) {
+          if constexpr (I8) {
             if (s < BQ) f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz8(brow0 + 32 * j, 2 * h + s));
           } else {
             f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz16(brow0 + 32 * j, 4 * h + s));
@@ -389,7 +360,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
         u32x4 bf[FN];
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          if constexpr (BK == B_I8) {
+          if constexpr (I8) {
             const u32x4 raw = f.b[bi][s >> 1][j];
             bf[j] = (s & 1) ? widen8<T>(raw.z, raw.w) : widen8<T>(raw.x, raw.y);
           } else {
@@ -406,62 +377,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
   };
 
   // Pipeline.  Step t computes from registers read out of stage t % S one
-  // step earlier.  In step t a wave
-  //   (int8 B) waits until its loads of step t + 1 have landed -- the DMA of
-  //     A is in the same in-order stream, so it has landed too -- and widens
-  //     its B pieces of step t + 1 into stage (t + 1) % S;
-  //   refills stage (t - 1) % S, which every wave finished reading before the
-  //     previous barrier, with step t + S - 1 (int8 B: into registers);
-  //   (16-bit B) waits for its own DMA of step t + 1;
-  //   waits for its LDS reads of step t and its B stores, meets the other
-  //     waves at the barrier -- all of step t + 1 is now in LDS -- issues the
-  //     LDS reads of step t + 1 and runs the MFMAs of step t while they land.
+  // step earlier.  In step t a wave refills stage (t - 1) % S, which every
+  // wave finished reading before the previous barrier, with step t + S - 1;
+  // waits for its own DMA of step t + 1 (the later steps stay in flight) and
+  // for its LDS reads of step t; meets the other waves at the barrier -- all
+  // of step t + 1 is now in LDS -- issues the LDS reads of step t + 1 and runs
+  // the MFMAs of step t while they land.
   Frags fr[2];
-  if constexpr (QR) {
-    // prologue: step 0 through a register set of its own, then steps 1 .. S - 2
-    issue(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, 0);
-    wait_vmcnt<0>();
-    store_q(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-    static_for([&](auto I) {
-      constexpr int st = decltype(I)::value + 1;  // step and stage 1 .. S - 2
-      if (st < nk) issue(std::integral_constant<int, st>{}, std::integral_constant<int, st % R>{}, st);
-    }, std::make_index_sequence<S - 2>{});
-  } else {
-    static_for([&](auto I) {
-      if (decltype(I)::value < nk) issue(I, std::integral_constant<int, 0>{}, decltype(I)::value);
-    }, std::make_index_sequence<S - 1>{});
-    if (S - 2 < nk) wait_vmcnt<(S - 2) * C::P>();
-    else wait_vmcnt<0>();
-  }
+  static_for([&](auto I) {
+    if (decltype(I)::value < nk) issue(I, decltype(I)::value);
+  }, std::make_index_sequence<S - 1>{});
+  if (S - 2 < nk) wait_vmcnt<(S - 2) * C::P>();
+  else wait_vmcnt<0>();
   wait_lgkmcnt0();
   lds_barrier();
   read_frags(std::integral_constant<int, 0>{}, fr[0]);
 
-  // stage, register-set and fragment indices known at compile time
-  constexpr int UNROLL = QR ? lcm_c(lcm_c(S, 2), R) : lcm_c(S, 2);
+  constexpr int UNROLL = lcm_c(S, 2);  // stage and fragment-set indices known at compile time
   // One step; GUARD = false where every condition is known to hold (all
   // steps it touches are full 64-column steps inside k), so the main loop has
   // no branches and the compiler's own wait-count tracking stays exact.
   auto step = [&](auto I, auto GUARD, int t) {
-    constexpr int ii = decltype(I)::value, si = ii % S, pi = ii % 2, qi = (ii + 1) % R;
+    constexpr int ii = decltype(I)::value, si = ii % S, pi = ii % 2;
     constexpr bool guard = decltype(GUARD)::value;
-    if constexpr (QR) {
-      if (!guard || t + 1 < nk) {
-        if (!guard || t + S - 2 < nk) wait_vmcnt<(S - 3) * C::P>();
-        else wait_vmcnt<0>();
-        store_q(std::integral_constant<int, (si + 1) % S>{}, std::integral_constant<int, qi>{});
-      }
-      if (!guard || t + S - 1 < nk)
-        issue(std::integral_constant<int, (si + S - 1) % S>{}, std::integral_constant<int, qi>{}, t + S - 1);
-    } else {
-      if (!guard || t + S - 1 < nk)
-        issue(std::integral_constant<int, (si + S - 1) % S>{}, std::integral_constant<int, 0>{}, t + S - 1);
-      if (!guard || t + 1 < nk) {
-        if (!guard || t + S - 1 < nk) wait_vmcnt<(S - 2) * C::P>();
-        else wait_vmcnt<0>();
-      }
-    }
+    if (!guard || t + S - 1 < nk) issue(std::integral_constant<int, (si + S - 1) % S>{}, t + S - 1);
     if (!guard || t + 1 < nk) {
+      if (!guard || t + S - 1 < nk) wait_vmcnt<(S - 2) * C::P>();
+      else wait_vmcnt<0>();
       wait_lgkmcnt0();
       lds_barrier();
       read_frags(std::integral_constant<int, (si + 1) % S>{}, fr[pi ^ 1]);

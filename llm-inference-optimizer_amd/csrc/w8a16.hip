@@ -457,10 +457,14 @@ int w8_tiled(const W8Params& p, hipStream_t s) {
   const int64_t t128 = static_cast<int64_t>((p.rows + 127) / 128) * ((p.n + 127) / 128);
   if (t128 < 128) return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);
   if (t128 < 320) return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
-  if (p.n <= 2048) return wide ? w8_tiled_cfg<T, TO, 2, 4, 2, 2, 4>(p, s) : w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+  if (p.n <= 2048) {
+    if constexpr (wide) return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 4>(p, s);
+    else return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+  }
   if (t128 < 1000) return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(p, s);
   if (t128 < 2000) return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 3>(p, s);
-  return wide ? w8_tiled_cfg<T, TO, 2, 4, 2, 2, 3>(p, s) : w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+  if constexpr (wide) return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 3>(p, s);
+  else return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
 }
 
 template <typename T, typename TO>
