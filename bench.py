@@ -24,6 +24,8 @@ Also reported on the same JSON line:
                 inside a hipGraph of 28 x (RMSNorm, SiLU-and-mul, RMSNorm);
   gate_up_silu  the fused gate/up projections + SiLU-and-mul at decode rows
                 vs the reference's two-GEMM + SiLU-and-mul chain;
+  gate_up_silu_prefill  the same at prefill rows (tiled MFMA GEMM), same baseline;
+  w8a16         the weight-only int8 linear vs fp16 torch.matmul (hipBLASLt);
   copy_ceiling  a plain 16-byte streaming copy on the same device.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -62,7 +64,7 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up",
-                                      "w8a16", "w8a16-decode"],
+                                      "gate-up-prefill", "w8a16", "w8a16-decode", "w8a16-prefill"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -346,6 +348,19 @@ KNOWN_LAUNCHES = {
     ("w8a16_skinny<mi355::BF16, mi355::BF16, 1, 4, 1>", 192 * 592): (
         "W8A16 7B gate/up, 8 rows, [18944,3584] int8, bf16",
         18944 * 3584 + 4 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
+    # MFMA-bound prefill GEMMs: (label, algorithmic bytes, flops)
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 4, 2, 2, 1, 1, 3>", 560 * 512): (
+        "gate/up + SiLU-and-mul prefill, 1024 rows, [8960,1536] weights, fp16",
+        2 * 8960 * 1536 * 2 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 4 * 1024 * 1536 * 8960),
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 4, 2, 2, 1, 1, 3>", 2240 * 512): (
+        "gate/up + SiLU-and-mul prefill, 4096 rows, [8960,1536] weights, fp16",
+        2 * 8960 * 1536 * 2 + 4096 * 1536 * 2 + 4096 * 8960 * 2, 4 * 4096 * 1536 * 8960),
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 2, 1, 0, 4>", 1120 * 256): (
+        "W8A16 prefill gate/up, 1024 rows, [8960,1536] int8, fp16",
+        8960 * 1536 + 4 * 8960 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 2 * 1024 * 1536 * 8960),
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4>", 384 * 256): (
+        "W8A16 prefill down, 1024 rows, [1536,8960] int8, fp16",
+        1536 * 8960 + 4 * 1536 + 1024 * 8960 * 2 + 1024 * 1536 * 2, 2 * 1024 * 8960 * 1536),
 }
 COPY_READ_KIB = COPY_WRITE_KIB = (1 << 30) / 1024
 
@@ -369,8 +384,9 @@ def rocprof_summary(dirs):
     for d in dirs:
         for f in sorted(glob.glob(os.path.join(d, "*kernel_trace.csv"))):
             out.append(f"### kernel trace: {f}\n")
-            out.append("| kernel | grid (threads) | launches | avg us | median us | algorithmic bytes | GB/s (avg) | % of 8 TB/s |")
-            out.append("|---|---|---|---|---|---|---|---|")
+            out.append("| kernel | grid (threads) | launches | avg us | median us | algorithmic bytes | GB/s (avg) | "
+                       "% of 8 TB/s | TFLOP/s (avg) | % of 2.5 PFLOP/s |")
+            out.append("|---|---|---|---|---|---|---|---|---|---|")
             groups = {}
             for r in csv.DictReader(open(f)):
                 grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])  # threads
@@ -379,12 +395,14 @@ def rocprof_summary(dirs):
                     continue
                 groups.setdefault((frag, grid), []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
             for (frag, grid), v in groups.items():
-                label, nbytes = KNOWN_LAUNCHES[(frag, grid)]
+                label, nbytes = KNOWN_LAUNCHES[(frag, grid)][:2]
+                flops = KNOWN_LAUNCHES[(frag, grid)][2] if len(KNOWN_LAUNCHES[(frag, grid)]) > 2 else None
                 v.sort()
                 avg = sum(v) / len(v) / 1e3
                 gbs = nbytes / avg / 1e3
+                tf = f"{flops / avg / 1e6:.1f} | {100 * flops / avg / 1e6 / MFMA_PEAK_TFLOPS:.1f}" if flops else "- | -"
                 out.append(f"| {frag} ({label}) | {grid} | {len(v)} | {avg:.3f} | {v[len(v) // 2] / 1e3:.3f} | "
-                           f"{nbytes} | {gbs:.0f} | {100 * gbs / PEAK_GBS:.1f} |")
+                           f"{nbytes} | {gbs:.0f} | {100 * gbs / PEAK_GBS:.1f} | {tf} |")
             out.append("")
         pmc = {}
         for f in sorted(glob.glob(os.path.join(d, "*counter_collection.csv"))):
@@ -417,7 +435,7 @@ def rocprof_summary(dirs):
             fk = sum(fv) / len(fv)
             wk = sum(wv) / len(wv)
             tb = (fk * fscale + wk * wscale) * 1024
-            label, nbytes = KNOWN_LAUNCHES[(frag, grid)]
+            label, nbytes = KNOWN_LAUNCHES[(frag, grid)][:2]
             out.append(f"| {frag} ({label}) | {len(fv)} | {fk:.1f} | {wk:.1f} | {tb:.0f} | {nbytes} | {tb / nbytes:.4f} |")
             traffic[label] = {"traffic_bytes": round(tb), "algorithmic_bytes": nbytes,
                               "fetch_kib": round(fk, 1), "write_kib": round(wk, 1)}
@@ -541,6 +559,7 @@ def main():
         result["c4"] = bench_c4(ctx, iters=60)
         result["decode"] = bench_decode(ctx)
         result["gate_up_silu"] = bench_gate_up(ctx)
+        result["gate_up_silu_prefill"] = bench_gate_up_prefill(ctx)
         result["w8a16"] = bench_w8a16(ctx)
         result["copy_ceiling"] = bench_copy(ctx)
 
@@ -578,11 +597,18 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up(ctx, shapes=GATE_UP_SHAPES[1:2], iters=iters, baselines=False)))
-    elif args.only in ("w8a16", "w8a16-decode"):
+    elif args.only == "gate-up-prefill":  # kernel only, the 1.5B MLP at 1024 and 4096 rows
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES[1:3], baselines=False)))
+    elif args.only in ("w8a16", "w8a16-decode", "w8a16-prefill"):
         del sets
         torch.cuda.empty_cache()
         if args.only == "w8a16":
             log(json.dumps(bench_w8a16(ctx)))
+        elif args.only == "w8a16-prefill":  # kernel only, the 1.5B gate/up and down projections at 1024 rows
+            log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 1024 and s[2] in (8960, 1536)
+                                                    and s[1] in (1536, 8960)][-2:], iters=iters, baselines=False)))
         else:  # the two decode shapes profiled under profiles/, kernel only
             log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 8 and s[2] in (8960, 18944)],
                                        iters=iters, baselines=False)))
@@ -766,13 +792,71 @@ def bench_gate_up(ctx, shapes=GATE_UP_SHAPES, iters=400, baselines=True):
     return res
 
 
+# (rows, k, n_out, dtype name, label): prefill batches of Qwen2.5-1.5B and -7B MLPs
+GATE_UP_PREFILL_SHAPES = [(128, 1536, 8960, "f16", "qwen2.5-1.5b"), (1024, 1536, 8960, "f16", "qwen2.5-1.5b"),
+                          (4096, 1536, 8960, "f16", "qwen2.5-1.5b"), (4096, 3584, 18944, "bf16", "qwen2.5-7b")]
+
+
+def bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES, iters=60, baselines=True):
+    """Gate/up projections + SiLU-and-mul at prefill rows (the tiled MFMA
+    GEMM with the activation in its epilogue) against the reference's FusedMLP
+    chain on the same weights: two torch.matmul GEMMs (hipBLASLt), each
+    rounded to x's dtype, then the SiLU-and-mul kernel.  MFMA-bound: flops
+    2 * 2 * rows * k * n_out per call; weight sets rotate as in the decode leg."""
+    torch = ctx.torch
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
+    res = {}
+    for M, K, I, dname, label in shapes:
+        dt = dts[dname]
+        flops = 4.0 * M * K * I
+        layers = min(8, n_sets(2 * I * K * 2))
+        x = rand(ctx, (M, K), 2400 + M, dt)
+        ws = [(rand(ctx, (I, K), 2500 + 2 * l, dt, std=2.0 * K ** -0.5),
+               rand(ctx, (I, K), 2501 + 2 * l, dt, std=K ** -0.5)) for l in range(layers)]
+        outs = [torch.empty((M, I), dtype=dt, device=ctx.dev) for _ in range(2)]
+        fused = [ctx.gate_up_call(x, wg, wu, outs[l % 2]) for l, (wg, wu) in enumerate(ws)]
+        spin_up(ctx, fused)
+        us = time_loop(ctx, fused, iters)
+        tf = flops / us / 1e6
+        entry = {"kernel": "tiled_gemm<2 x 16-bit B, SiLU-and-mul epilogue>", "rows": M, "k": K, "n_out": I,
+                 "dtype": dname, "us": round(us, 3), "TFLOPs": round(tf, 1),
+                 "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4), "weight_sets": layers}
+        if baselines:
+            silu = ctx.pkg.fused_silu_mul
+
+            def chain(wg, wu):
+                return lambda: silu(torch.matmul(x, wg.T), torch.matmul(x, wu.T))
+
+            chains = [chain(wg, wu) for wg, wu in ws]
+            spin_up(ctx, chains)
+            c_us = time_loop(ctx, chains, iters)
+            entry.update({"unfused_chain_us": round(c_us, 3), "unfused_chain_TFLOPs": round(flops / c_us / 1e6, 1),
+                          "speedup": round(c_us / us, 3)})
+            del chains
+        res[f"{label}_M{M}_{dname}"] = entry
+        log(f"  gate_up prefill {label} M={M}: {entry}")
+        del ws, outs, fused
+        torch.cuda.empty_cache()
+    return res
+
+
 # (M, K, N, dtype name, label): the reference's stage-7 kernel benchmark shapes
 # (benchmarks/run_stage7_kernel.py:33-39, Qwen2.5-1.5B projections, M in
 # {1, 8, 128, 1024}) plus Qwen2.5-7B MLP decode shapes in bf16.
 W8A16_SHAPES = [(M, K, N, "f16", lab) for K, N, lab in ((1536, 1536, "q/o proj"), (1536, 256, "k/v proj"),
                                                          (1536, 8960, "gate/up proj"), (8960, 1536, "down proj"))
                 for M in (1, 8, 128, 1024)] + [(8, 3584, 18944, "bf16", "7b gate/up proj"),
-                                               (8, 18944, 3584, "bf16", "7b down proj")]
+                                               (8, 18944, 3584, "bf16", "7b down proj"),
+                                               (4096, 1536, 8960, "f16", "gate/up proj"),
+                                               (4096, 8960, 1536, "f16", "down proj")]
+
+
+def w8a16_kernel_name(M, N):
+    """The kernel mi355_w8a16_linear_fwd runs for this shape (aligned inputs):
+    the split-K weight-streaming kernel for decode rows and small grids, the
+    tiled MFMA GEMM otherwise."""
+    tiles64 = ((N + 63) // 64) * ((M + 63) // 64)
+    return "w8a16_skinny" if M <= 32 or (M <= 256 and tiles64 < 128) else "tiled_gemm<int8 B>"
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16
 
 
@@ -800,7 +884,7 @@ def bench_w8a16(ctx, shapes=W8A16_SHAPES, iters=300, baselines=True):
         spin_up(ctx, calls)
         us = time_loop(ctx, calls, iters)
         us_graph = time_graph(ctx, calls, max(2 * sets, 64) if sets <= 256 else sets)
-        kname = "w8a16_skinny" if M <= 32 else "w8a16_tiled"
+        kname = w8a16_kernel_name(M, N)
         entry = kernel_entry(kname, nbytes, min(us, us_graph),
                              {"layer": label, "M": M, "K": K, "N": N, "dtype": dname, "weight_sets": sets,
                               "eager_us": round(us, 3), "graph_us": round(us_graph, 3),
