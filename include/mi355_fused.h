@@ -189,6 +189,36 @@ int mi355_w8a16_linear_fwd(const void* x, const void* w_q, const void* scale, co
                            void* stream);
 
 /*
+ * Int8 gate/up projections fused with SiLU-and-mul (W8A16 weights), per row
+ * m and output feature n:
+ *   g[m,n] = (sum_k x[m,k] * wq_gate[n,k]) * scale_gate[n]     (fp32 sums)
+ *   u[m,n] = (sum_k x[m,k] * wq_up[n,k])   * scale_up[n]
+ *   out[m,n] = round(g * sigmoid(g) * u)                       (fp32, one rounding)
+ *
+ * No counterpart in the reference: its quantised model runs
+ * QuantizedLinearInt8 gate_proj and up_proj (two `w8a16_linear` launches,
+ * src/quantization/int8.py:62-63, each rounding to x's dtype) and then the
+ * SiLU-and-mul kernel (src/engine/fused_norm_activation_patch.py:60-64).
+ * This entry point is that chain as one kernel, without the intermediate
+ * roundings -- the int8 form of mi355_gate_up_silu_fwd.  Decode rows (<= 32)
+ * stream both int8 matrices once at HBM bandwidth; more rows run the tiled
+ * MFMA GEMM.
+ *
+ *   x        [rows, x_row_stride] of x_dtype (MI355_F16 or MI355_BF16).
+ *   wq_gate, wq_up  [n_out, w_row_stride] int8 (QuantizedLinearInt8.weight_q).
+ *   scale_gate, scale_up  [n_out] of scale_dtype (the quantiser's fp32).
+ *   out      [rows, out_row_stride] of out_dtype = x_dtype or MI355_F32.
+ *   Same shape rules, alignment preferences and limits as
+ *   mi355_w8a16_linear_fwd (any k and alignment are served; no bias).
+ */
+int mi355_gate_up_silu_w8a16_fwd(const void* x, const void* wq_gate, const void* wq_up,
+                                 const void* scale_gate, const void* scale_up, void* out,
+                                 int64_t rows, int64_t k, int64_t n_out,
+                                 int64_t x_row_stride, int64_t w_row_stride, int64_t out_row_stride,
+                                 int x_dtype, int scale_dtype, int out_dtype,
+                                 void* stream);
+
+/*
  * Per-output-channel symmetric int8 quantisation of a weight matrix, per row n:
  *   amax     = max_k |w[n,k]|
  *   scale[n] = max(amax / 127, 1e-8)                     (fp32, IEEE division)

@@ -38,7 +38,7 @@ from .engine.graphed_decode import GraphedGreedyDecoder
 from .kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm, naive_rmsnorm_reference
 from .kernels.fused_gate_up_hip import GATE_UP_MAX_ROWS, fused_gate_up_silu, naive_gate_up_silu_reference
 from .kernels.fused_swiglu_hip import fused_silu_mul, naive_silu_mul_reference
-from .kernels.w8a16_matmul_hip import quantize_int8_weight, w8a16_linear, w8a16_reference
+from .kernels.w8a16_matmul_hip import fused_gate_up_silu_w8a16, quantize_int8_weight, w8a16_linear, w8a16_reference
 from .quantization.int8 import QuantizedLinearInt8, quantize_model_int8
 
 __all__ = [
@@ -47,4 +47,5 @@ __all__ = [
     "fused_add_rmsnorm", "FusedDecoderLayer", "DECODER_LAYER_CLASS_NAMES", "GraphedGreedyDecoder",
     "fused_gate_up_silu", "naive_gate_up_silu_reference", "GATE_UP_MAX_ROWS",
     "w8a16_linear", "w8a16_reference", "quantize_int8_weight", "QuantizedLinearInt8", "quantize_model_int8",
+    "fused_gate_up_silu_w8a16",
 ]

@@ -26,7 +26,7 @@ DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTED_SYMBOLS = ("mi355_abi_version", "mi355_last_error", "mi355_rmsnorm_fwd", "mi355_add_rmsnorm_fwd",
                     "mi355_silu_mul_fwd", "mi355_gate_up_silu_fwd", "mi355_w8a16_linear_fwd",
-                    "mi355_quantize_int8_fwd")
+                    "mi355_quantize_int8_fwd", "mi355_gate_up_silu_w8a16_fwd")
 
 
 class KernelLibraryMissing(RuntimeError):
@@ -77,6 +77,9 @@ def load() -> ctypes.CDLL:
         L.mi355_w8a16_linear_fwd.restype = i32
         L.mi355_quantize_int8_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i32, vp]
         L.mi355_quantize_int8_fwd.restype = i32
+        L.mi355_gate_up_silu_w8a16_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32,
+                                                   i32, vp]
+        L.mi355_gate_up_silu_w8a16_fwd.restype = i32
         ver = L.mi355_abi_version()
         if ver != ABI_VERSION:
             raise KernelLibraryMissing(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
@@ -150,6 +153,15 @@ def w8a16_linear_fwd(x_ptr: int, q_ptr: int, scale_ptr: int, bias_ptr: int | Non
           load().mi355_w8a16_linear_fwd(x_ptr, q_ptr, scale_ptr, bias_ptr, out_ptr, rows, k, n, x_row_stride,
                                         w_row_stride, out_row_stride, x_dtype, scale_dtype, bias_dtype, out_dtype,
                                         stream))
+
+
+def gate_up_silu_w8a16_fwd(x_ptr: int, qg_ptr: int, qu_ptr: int, sg_ptr: int, su_ptr: int, out_ptr: int, rows: int,
+                           k: int, n_out: int, x_row_stride: int, w_row_stride: int, out_row_stride: int,
+                           x_dtype: int, scale_dtype: int, out_dtype: int, stream: int) -> None:
+    check("mi355_gate_up_silu_w8a16_fwd",
+          load().mi355_gate_up_silu_w8a16_fwd(x_ptr, qg_ptr, qu_ptr, sg_ptr, su_ptr, out_ptr, rows, k, n_out,
+                                              x_row_stride, w_row_stride, out_row_stride, x_dtype, scale_dtype,
+                                              out_dtype, stream))
 
 
 def quantize_int8_fwd(w_ptr: int, q_ptr: int, scale_ptr: int, n: int, k: int, w_row_stride: int,

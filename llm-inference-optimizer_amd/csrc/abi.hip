@@ -28,6 +28,9 @@ int w8a16_launch(const void* x, const void* q, const void* scale, const void* bi
                  int out_dtype, hipStream_t stream);
 int quantize_int8_launch(const void* w, void* q, void* scale, int64_t n, int k, int64_t ws, int64_t qs, int w_dtype,
                          hipStream_t stream);
+int gate_up_silu_w8a16_launch(const void* x, const void* qg, const void* qu, const void* sg, const void* su, void* out,
+                              int rows, int k, int n, int64_t xs, int64_t qs, int64_t os, int x_dtype,
+                              int scale_dtype, int out_dtype, hipStream_t stream);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -289,6 +292,61 @@ MI355_EXPORT int mi355_w8a16_linear_fwd(const void* x, const void* w_q, const vo
   return mi355::w8a16_launch(x, w_q, scale, bias, out, static_cast<int>(rows), static_cast<int>(k),
                              static_cast<int>(n), x_row_stride, w_row_stride, out_row_stride, x_dtype, scale_dtype,
                              bias_dtype, out_dtype, static_cast<hipStream_t>(stream));
+}
+
+MI355_EXPORT int mi355_gate_up_silu_w8a16_fwd(const void* x, const void* wq_gate, const void* wq_up,
+                                              const void* scale_gate, const void* scale_up, void* out, int64_t rows,
+                                              int64_t k, int64_t n_out, int64_t x_row_stride, int64_t w_row_stride,
+                                              int64_t out_row_stride, int x_dtype, int scale_dtype, int out_dtype,
+                                              void* stream) {
+  static const char* fn = "mi355_gate_up_silu_w8a16_fwd";
+  mi355::g_error[0] = '\0';
+  if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype) || !valid_dtype(out_dtype)) {
+    set_error("%s: unknown dtype code (x=%d, scale=%d, out=%d)", fn, x_dtype, scale_dtype, out_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (x_dtype == MI355_F32) {
+    set_error("%s: x must be fp16 or bf16 (MFMA operand)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (out_dtype != x_dtype && out_dtype != MI355_F32) {
+    set_error("%s: out dtype must equal x dtype or be fp32 (x=%d, out=%d)", fn, x_dtype, out_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows < 0 || n_out < 0 || k < 1) {
+    set_error("%s: need rows >= 0, n_out >= 0, k >= 1 (got %lld, %lld, %lld)", fn, static_cast<long long>(rows),
+              static_cast<long long>(n_out), static_cast<long long>(k));
+    return MI355_ERR_INVALID;
+  }
+  if (x_row_stride < k || w_row_stride < k || out_row_stride < n_out) {
+    set_error("%s: row strides must be >= k (x, weights) and >= n_out (out)", fn);
+    return MI355_ERR_INVALID;
+  }
+  if (rows == 0 || n_out == 0) return MI355_OK;
+  if (x == nullptr || wq_gate == nullptr || wq_up == nullptr || scale_gate == nullptr || scale_up == nullptr ||
+      out == nullptr) {
+    set_error("%s: null pointer", fn);
+    return MI355_ERR_INVALID;
+  }
+  // the W8A16 kernels' limits
+  if (x_row_stride >= (int64_t{1} << 23) || w_row_stride >= (int64_t{1} << 24) || n_out > 0x7fffffff - 128 ||
+      rows > int64_t{65535} * 64) {
+    set_error("%s: size beyond the kernel's limits (x_row_stride < 2^23, w_row_stride < 2^24, n_out < 2^31 - 128, "
+              "rows <= 4194240)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (n_out * ((rows + 3) / 4) > int64_t{0x7fffffff} * 4) {
+    set_error("%s: n_out * rows too large for one launch", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows - 1 > (INT64_MAX - n_out) / out_row_stride) {
+    set_error("%s: rows * out_row_stride overflows int64", fn);
+    return MI355_ERR_INVALID;
+  }
+  return mi355::gate_up_silu_w8a16_launch(x, wq_gate, wq_up, scale_gate, scale_up, out, static_cast<int>(rows),
+                                          static_cast<int>(k), static_cast<int>(n_out), x_row_stride, w_row_stride,
+                                          out_row_stride, x_dtype, scale_dtype, out_dtype,
+                                          static_cast<hipStream_t>(stream));
 }
 
 MI355_EXPORT int mi355_quantize_int8_fwd(const void* w, void* w_q, void* scale, int64_t n, int64_t k,

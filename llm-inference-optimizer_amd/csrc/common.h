@@ -35,6 +35,22 @@ __device__ __forceinline__ uint32_t as_u32(float v) { return __builtin_bit_cast(
 __device__ __forceinline__ void reg_barrier(u32x4& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void reg_barrier(uint32_t& v) { asm volatile("" : "+v"(v)); }
 
+// Value barrier on an fp32 result about to be narrowed to 16 bits: the
+// compiler may not fold the operation that produced it into the conversion.
+// Without it, a final fp32 multiply followed by the narrowing can become one
+// v_fma_mixlo_f16, which rounds the exact product straight to 16 bits; that
+// differs from rounding the fp32 result whenever the fp32 rounding lands on a
+// tie of the 16-bit grid, so the 16-bit output would not always be the fp32
+// output rounded once.  Free at run time (an empty asm).
+__device__ __forceinline__ float fp32_value(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ f32x2 fp32_value(f32x2 v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 // Storage tags.  `bits` is the raw storage type; arithmetic is always fp32.
 struct F32 { typedef uint32_t bits; static constexpr int code = MI355_F32; };
 struct F16 { typedef uint16_t bits; static constexpr int code = MI355_F16; };
@@ -66,10 +82,10 @@ template <> __device__ __forceinline__ f32x2 widen2<BF16>(uint32_t d) {
 
 template <typename T> __device__ __forceinline__ uint32_t narrow2(f32x2 v);
 template <> __device__ __forceinline__ uint32_t narrow2<F16>(f32x2 v) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(fp32_value(v), f16x2));
 }
 template <> __device__ __forceinline__ uint32_t narrow2<BF16>(f32x2 v) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(fp32_value(v), bf16x2));
 }
 
 // Scalar element access for the generic (unaligned / odd-size) kernels.
@@ -89,20 +105,20 @@ template <> __device__ __forceinline__ void store_elem<F32>(void* p, int64_t i, 
   static_cast<float*>(p)[i] = v;
 }
 template <> __device__ __forceinline__ void store_elem<F16>(void* p, int64_t i, float v) {
-  static_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
+  static_cast<_Float16*>(p)[i] = static_cast<_Float16>(fp32_value(v));
 }
 template <> __device__ __forceinline__ void store_elem<BF16>(void* p, int64_t i, float v) {
-  static_cast<__bf16*>(p)[i] = static_cast<__bf16>(v);
+  static_cast<__bf16*>(p)[i] = static_cast<__bf16>(fp32_value(v));
 }
 
 // v rounded to T's precision (round-to-nearest-even) and widened back.
 template <typename T> __device__ __forceinline__ float quantize(float v);
 template <> __device__ __forceinline__ float quantize<F32>(float v) { return v; }
 template <> __device__ __forceinline__ float quantize<F16>(float v) {
-  return static_cast<float>(static_cast<_Float16>(v));
+  return static_cast<float>(static_cast<_Float16>(fp32_value(v)));
 }
 template <> __device__ __forceinline__ float quantize<BF16>(float v) {
-  return static_cast<float>(static_cast<__bf16>(v));
+  return static_cast<float>(static_cast<__bf16>(fp32_value(v)));
 }
 
 // A packet of `pack_width<T>` elements held as raw dwords.  `unpack` widens it

@@ -1,5 +1,6 @@
-// Weight-only int8 linear (W8A16) and the int8 weight quantiser for gfx950,
-// with their launchers.
+// Weight-only int8 linear (W8A16), the int8 gate/up projections fused with
+// SiLU-and-mul, and the int8 weight quantiser for gfx950, with their
+// launchers.
 //
 //   out[m, n] = round(acc * scale[n] + bias[n]),  acc = sum_k x[m, k] * q[n, k]
 //
@@ -113,14 +114,16 @@ __device__ __forceinline__ float load_dyn(const void* p, int64_t i, int dt) {
 }
 
 struct W8Params {
-  const void* x;      // [rows, xs] of T
-  const void* q;      // [n, qs] int8
-  const void* scale;  // [n] of sdt
-  const void* bias;   // [n] of bdt, or null
-  void* out;          // [rows, os] of TO
+  const void* x;       // [rows, xs] of T
+  const void* q;       // [n, qs] int8 (gate weights for the dual kernels)
+  const void* scale;   // [n] of sdt
+  const void* bias;    // [n] of bdt, or null
+  void* out;           // [rows, os] of TO
   int rows, k, n;
   int64_t xs, qs, os;  // row strides in elements
   int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
+  const void* q2;      // dual kernels: [n, qs] int8 up weights
+  const void* scale2;  // dual kernels: [n] of sdt
 };
 
 // The epilogue shared by all kernels: scale once, then the bias, one rounding.
@@ -131,12 +134,24 @@ __device__ __forceinline__ void w8_store(const W8Params& p, int64_t m, int n, fl
   store_elem<TO>(p.out, m * p.os + n, v);
 }
 
+// The dual (gate/up) epilogue: both projections scaled once, SiLU-and-mul in
+// fp32, one rounding.
+template <typename TO>
+__device__ __forceinline__ void w8_store_silu(const W8Params& p, int64_t m, int n, float acc_g, float acc_u) {
+  const float g = acc_g * load_dyn(p.scale, n, p.sdt);
+  const float u = acc_u * load_dyn(p.scale2, n, p.sdt);
+  store_elem<TO>(p.out, m * p.os + n, silu_mul_f32(g, u));
+}
+
 // ------------------------------------------------------------------ skinny
 
-template <typename T, typename TO, int MT, int G, int U>
+// DUAL: two int8 weight matrices (gate and up) against the same x, each with
+// its scale, and SiLU-and-mul in the epilogue; x is loaded once for both.
+template <typename T, typename TO, int MT, int G, int U, bool DUAL>
 __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p) {
   using TB = typename T::bits;
-  extern __shared__ float red[];  // [nwave][G][MT][4][64]
+  constexpr int NQ = DUAL ? 2 : 1;  // weight matrices
+  extern __shared__ float red[];    // [nwave][NQ][G][MT][4][64]
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -150,8 +165,12 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
 
   // Descriptors end right after the last valid element, so weight rows past n
   // and x rows past the tile (offset >= rows * stride >= the extent) read 0.
-  const rsrc_t rq = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
-                              static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  rsrc_t rq[NQ];
+  rq[0] = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
+                    static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  if constexpr (DUAL)
+    rq[1] = make_rsrc(static_cast<const int8_t*>(p.q2) + static_cast<int64_t>(n0) * p.qs,
+                      static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
   const rsrc_t rx = make_rsrc(static_cast<const TB*>(p.x) + static_cast<int64_t>(m0) * p.xs,
                               static_cast<uint32_t>(((nrows_x - 1) * p.xs + p.k) * sizeof(TB)));
 
@@ -164,22 +183,28 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
 #pragma unroll
   for (int t = 0; t < MT; ++t) xoff[t] = static_cast<uint32_t>(((8 * t + r8) * p.xs + col) * sizeof(TB));
 
-  f32x4 acc[G][MT];
+  f32x4 acc[NQ][G][MT];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[qi][g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 
   const int nblk = (p.k + 127) >> 7;
   const int s_end = (nblk * (wave + 1)) / nwave;
   for (int s = (nblk * wave) / nwave; s < s_end; s += U) {
-    u32x4 wq[U][G], xa[U][MT][2];
+    u32x4 wq[U][NQ][G], xa[U][MT][2];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
       const bool live = s + j < s_end && 128 * (s + j) + col < p.k;
 #pragma unroll
-      for (int g = 0; g < G; ++g) wq[j][g] = buf_load16(rq, live ? qoff[g] + 128u * (s + j) : kOob);
+      for (int qi = 0; qi < NQ; ++qi) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) wq[j][qi][g] = buf_load16(rq[qi], live ? qoff[g] + 128u * (s + j) : kOob);
+      }
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         const uint32_t o = xoff[t] + 256u * (s + j);
@@ -191,24 +216,31 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
 #pragma unroll
     for (int j = 0; j < U; ++j) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        u32x4 b0, b1;
-        widen_i8x16<T>(wq[j][g], b0, b1);
+      for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          acc[g][t] = mfma16<T>(xa[j][t][0], b0, acc[g][t]);
-          acc[g][t] = mfma16<T>(xa[j][t][1], b1, acc[g][t]);
+        for (int g = 0; g < G; ++g) {
+          u32x4 b0, b1;
+          widen_i8x16<T>(wq[j][qi][g], b0, b1);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            acc[qi][g][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][g][t]);
+            acc[qi][g][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][g][t]);
+          }
         }
       }
     }
   }
 
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
+    for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) red[(((wave * G + g) * MT + t) * 4 + j) * 64 + lane] = acc[g][t][j];
+      for (int t = 0; t < MT; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          red[((((wave * NQ + qi) * G + g) * MT + t) * 4 + j) * 64 + lane] = acc[qi][g][t][j];
+      }
     }
   }
   __syncthreads();
@@ -221,12 +253,17 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
     const int m = 8 * t + a, n = 8 * g + b;
     if (m >= nrows_x || n >= nrows_w) continue;
     const int l0 = 16 * (a >> 2) + b, j = a & 3;
-    float sum = 0.f;
-    for (int w = 0; w < nwave; ++w) {
-      const float* r = red + (((w * G + g) * MT + t) * 4 + j) * 64;
-      sum += r[l0] + r[l0 + 40];
+    float sum[NQ];
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      sum[qi] = 0.f;
+      for (int w = 0; w < nwave; ++w) {
+        const float* r = red + ((((w * NQ + qi) * G + g) * MT + t) * 4 + j) * 64;
+        sum[qi] += r[l0] + r[l0 + 40];
+      }
     }
-    w8_store<TO>(p, m0 + m, n0 + n, sum);
+    if constexpr (DUAL) w8_store_silu<TO>(p, m0 + m, n0 + n, sum[0], sum[NQ - 1]);
+    else w8_store<TO>(p, m0 + m, n0 + n, sum[0]);
   }
 }
 
@@ -234,27 +271,38 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
 
 constexpr int kGenRows = 4;  // rows of x per wave
 
-template <typename T, typename TO>
+template <typename T, typename TO, bool DUAL>
 __global__ __launch_bounds__(256) void w8a16_generic(const W8Params p) {
+  constexpr int NQ = DUAL ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t mblocks = (p.rows + kGenRows - 1) / kGenRows;
   if (gw >= static_cast<int64_t>(p.n) * mblocks) return;
   const int n = static_cast<int>(gw % p.n);
   const int64_t m0 = (gw / p.n) * kGenRows;
-  const int8_t* qrow = static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n) * p.qs;
-  float acc[kGenRows] = {0.f, 0.f, 0.f, 0.f};
+  const int8_t* qrow[NQ];
+  qrow[0] = static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n) * p.qs;
+  if constexpr (DUAL) qrow[1] = static_cast<const int8_t*>(p.q2) + static_cast<int64_t>(n) * p.qs;
+  float acc[NQ][kGenRows] = {};
   for (int c = lane; c < p.k; c += 64) {
-    const float qv = static_cast<float>(qrow[c]);
 #pragma unroll
-    for (int i = 0; i < kGenRows; ++i) {
-      if (m0 + i < p.rows) acc[i] = __builtin_fmaf(load_elem<T>(p.x, (m0 + i) * p.xs + c), qv, acc[i]);
+    for (int qi = 0; qi < NQ; ++qi) {
+      const float qv = static_cast<float>(qrow[qi][c]);
+#pragma unroll
+      for (int i = 0; i < kGenRows; ++i) {
+        if (m0 + i < p.rows) acc[qi][i] = __builtin_fmaf(load_elem<T>(p.x, (m0 + i) * p.xs + c), qv, acc[qi][i]);
+      }
     }
   }
 #pragma unroll
   for (int i = 0; i < kGenRows; ++i) {
-    const float s = wave_allreduce_sum(acc[i]);
-    if (lane == 0 && m0 + i < p.rows) w8_store<TO>(p, m0 + i, n, s);
+    float s[NQ];
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) s[qi] = wave_allreduce_sum(acc[qi][i]);
+    if (lane == 0 && m0 + i < p.rows) {
+      if constexpr (DUAL) w8_store_silu<TO>(p, m0 + i, n, s[0], s[NQ - 1]);
+      else w8_store<TO>(p, m0 + i, n, s[0]);
+    }
   }
 }
 
@@ -337,8 +385,9 @@ namespace {
 //     than 8);
 //   U (blocks in flight per wave) = 1, or 2 for narrow outputs (n <= 1536,
 //     few workgroups) whose waves own 2 or more blocks.
-template <typename T, typename TO, int MT, int G>
+template <typename T, typename TO, int MT, int G, bool DUAL>
 int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
+  constexpr int NQ = DUAL ? 2 : 1;
   const int groups = (p.n + 8 * G - 1) / (8 * G);
   const int nblk = (p.k + 127) / 128;
   const int tiles = (p.rows + 8 * MT - 1) / (8 * MT);
@@ -351,14 +400,14 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   if (g_force_u > 0) u = g_force_u;
 #endif
   if (split > kMaxSplit) split = kMaxSplit;
-  if (split > 64 / (G * MT)) split = 64 / (G * MT);  // partial sums: split * G * MT KiB of LDS <= 64 KiB
+  if (split > 64 / (NQ * G * MT)) split = 64 / (NQ * G * MT);  // partial sums: split * NQ * G * MT KiB <= 64 KiB
   if (split > nblk) split = nblk;
   if (split < 1) split = 1;
   int bpw = (nblk + split - 1) / split;
   if (units <= cus && split > 4) {
     // one workgroup per CU: a multiple of 4 waves keeps the CU's 4 SIMDs evenly loaded
     split = ((split + 2) / 4) * 4;
-    if (split > 64 / (G * MT)) split = (64 / (G * MT)) / 4 * 4;
+    if (split > 64 / (NQ * G * MT)) split = (64 / (NQ * G * MT)) / 4 * 4;
     if (split > kMaxSplit) split = kMaxSplit;
     bpw = (nblk + split - 1) / split;
   } else {
@@ -367,18 +416,20 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   if (u == 0) u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
   const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
   const dim3 block(64 * split);
-  const size_t lds = static_cast<size_t>(split) * G * MT * 4 * 64 * sizeof(float);
-  // register budget (128 VGPRs at 1024 threads): U * (4 G + 8 MT) operand
-  // dwords + 4 G MT accumulators <= 100
-  constexpr int umax = (100 - 4 * G * MT) / (4 * G + 8 * MT);
+  const size_t lds = static_cast<size_t>(split) * NQ * G * MT * 4 * 64 * sizeof(float);
+  // register budget (128 VGPRs at 1024 threads): U * (4 NQ G + 8 MT) operand
+  // dwords + 4 NQ G MT accumulators <= 100
+  constexpr int umax = (100 - 4 * NQ * G * MT) / (4 * NQ * G + 8 * MT);
 #ifdef MI355_W8_SWEEP
-  if (u >= 4 && umax >= 4) return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 4 ? 4 : 1)>, grid, block, lds, p, s);
+  if (u >= 4 && umax >= 4)
+    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 4 ? 4 : 1), DUAL>, grid, block, lds, p, s);
 #endif
-  if (u >= 2 && umax >= 2) return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1)>, grid, block, lds, p, s);
-  return launch_w8(w8a16_skinny<T, TO, MT, G, 1>, grid, block, lds, p, s);
+  if (u >= 2 && umax >= 2)
+    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1), DUAL>, grid, block, lds, p, s);
+  return launch_w8(w8a16_skinny<T, TO, MT, G, 1, DUAL>, grid, block, lds, p, s);
 }
 
-template <typename T, typename TO, int MT>
+template <typename T, typename TO, int MT, bool DUAL>
 int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
   int g = 1;
   if (p.rows <= 1) {
@@ -391,32 +442,42 @@ int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
     if ((p.n + 31) / 32 >= min_groups) g = 4;
     else if ((p.n + 15) / 16 >= min_groups) g = 2;
   }
+  // the dual kernel carries two weight matrices per row group: half the
+  // groups, and at most 2 (MT = 2) or 1 (MT >= 3) so its 2 G MT accumulator
+  // tiles fit the register budget
+  constexpr int gmax = !DUAL ? 4 : (MT >= 3 ? 1 : (MT == 2 ? 2 : 4));
+  if (DUAL) g = g > 1 ? g / 2 : 1;
 #ifdef MI355_W8_SWEEP
   if (g_force_g > 0) g = g_force_g;
 #endif
-  if (g >= 4) return w8_skinny_g<T, TO, MT, 4>(p, s, cus);
-  if (g == 2) return w8_skinny_g<T, TO, MT, 2>(p, s, cus);
-  return w8_skinny_g<T, TO, MT, 1>(p, s, cus);
+  if constexpr (gmax >= 4) {
+    if (g >= 4) return w8_skinny_g<T, TO, MT, 4, DUAL>(p, s, cus);
+  }
+  if constexpr (gmax >= 2) {
+    if (g >= 2) return w8_skinny_g<T, TO, MT, 2, DUAL>(p, s, cus);
+  }
+  return w8_skinny_g<T, TO, MT, 1, DUAL>(p, s, cus);
 }
 
 // ------------------------------------------------------------------- tiled
 
-// Buffer descriptors of the tiled GEMM span at most 128 rows of x and 256
-// weight rows; both must stay below 2^31 bytes.
-bool tiled_fits(const W8Params& p) {
-  return int64_t{128} * p.xs * 2 < (int64_t{1} << 31) && int64_t{256} * p.qs < (int64_t{1} << 31) &&
+// Buffer descriptors of the tiled GEMM span at most 128 rows of x (256 for
+// the dual kernel) and 256 weight rows; both must stay below 2^31 bytes.
+bool tiled_fits(const W8Params& p, bool dual) {
+  return int64_t{dual ? 256 : 128} * p.xs * 2 < (int64_t{1} << 31) && int64_t{256} * p.qs < (int64_t{1} << 31) &&
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
-template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S>
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8>
 int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
-  using C = tiled::Cfg<T, tiled::B_I8, TO, WGM, WGN, FM, FN, tiled::EPI_W8, S>;
+  using C = tiled::Cfg<T, tiled::B_I8, TO, WGM, WGN, FM, FN, EPI, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
   tiled::Params tp{};
   tp.x = p.x;
   tp.b0 = p.q;
-  tp.b1 = p.q;
+  tp.b1 = EPI == tiled::EPI_SILU_W8 ? p.q2 : p.q;
   tp.scale = p.scale;
+  tp.scale1 = p.scale2;
   tp.bias = p.bias;
   tp.out = p.out;
   tp.rows = p.rows;
@@ -433,7 +494,7 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
-                                                                                      tiled::EPI_W8, S>),
+                                                                                      EPI, S>),
                                     dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
                     "w8a16 tiled launch");
 }
@@ -467,28 +528,44 @@ int w8_tiled(const W8Params& p, hipStream_t s) {
   else return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
 }
 
+// The dual (gate/up + SiLU-and-mul) tiled GEMM: up to 256 rows and n <= 10000
+// 128 x 64 tiles (4 waves, 4 stages), else 128 x 128 (8 waves, 3 stages; fp16) --
+// the 16-bit gate/up GEMM's shapes, less its 256 x 64 one, whose 4 KiB int8
+// B tile does not split into the 8 waves' 1 KiB DMA instructions.
+// bf16 keeps the 128 x 64 shape throughout (its widening needs more
+// registers; 128 x 128 at 8 waves would spill).
 template <typename T, typename TO>
+int w8_tiled_dual(const W8Params& p, hipStream_t s) {
+  if constexpr (std::is_same<T, F16>::value) {
+    if (p.rows > 256 || p.n > 10000) return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_SILU_W8>(p, s);
+  }
+  return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 4, tiled::EPI_SILU_W8>(p, s);
+}
+
+template <typename T, typename TO, bool DUAL>
 int w8_typed(const W8Params& p, hipStream_t s, int cus) {
-  const bool vec = p.k % 16 == 0 && p.qs % 16 == 0 && p.xs % 8 == 0 && aligned16(p.x) && aligned16(p.q);
+  const bool vec = p.k % 16 == 0 && p.qs % 16 == 0 && p.xs % 8 == 0 && aligned16(p.x) && aligned16(p.q) &&
+                   (!DUAL || aligned16(p.q2));
   if (!vec) {
     const int64_t waves = static_cast<int64_t>(p.n) * ((p.rows + kGenRows - 1) / kGenRows);
-    return launch_w8(w8a16_generic<T, TO>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, p, s);
+    return launch_w8(w8a16_generic<T, TO, DUAL>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, p, s);
   }
-  if (p.rows <= 8) return w8_skinny_shape<T, TO, 1>(p, s, cus);
-  if (p.rows <= 16) return w8_skinny_shape<T, TO, 2>(p, s, cus);
-  if (p.rows <= 24) return w8_skinny_shape<T, TO, 3>(p, s, cus);
-  if (p.rows <= 32) return w8_skinny_shape<T, TO, 4>(p, s, cus);
+  if (p.rows <= 8) return w8_skinny_shape<T, TO, 1, DUAL>(p, s, cus);
+  if (p.rows <= 16) return w8_skinny_shape<T, TO, 2, DUAL>(p, s, cus);
+  if (p.rows <= 24) return w8_skinny_shape<T, TO, 3, DUAL>(p, s, cus);
+  if (p.rows <= 32) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);
   // More rows: the tiled GEMM, except for small grids of few rows (e.g. 128
   // rows against a K-heavy down projection), where 32-row skinny tiles with
   // split K, which re-read the weights per tile mostly from L2, measured faster.
   const int64_t tiles64 = static_cast<int64_t>((p.n + 63) / 64) * ((p.rows + 63) / 64);
   bool skinny = p.rows <= 256 && tiles64 < 128;
-  if (!tiled_fits(p)) skinny = true;
+  if (!tiled_fits(p, DUAL)) skinny = true;
 #ifdef MI355_W8_SWEEP
   if (g_force_path > 0) skinny = g_force_path == 1;
 #endif
-  if (skinny) return w8_skinny_shape<T, TO, 4>(p, s, cus);
-  return w8_tiled<T, TO>(p, s);
+  if (skinny) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);
+  if constexpr (DUAL) return w8_tiled_dual<T, TO>(p, s);
+  else return w8_tiled<T, TO>(p, s);
 }
 
 }  // namespace
@@ -499,12 +576,27 @@ int w8a16_launch(const void* x, const void* q, const void* scale, const void* bi
   int cus = 0;
   const int st = compute_units(&cus);
   if (st != MI355_OK) return st;
-  const W8Params p{x, q, scale, bias, out, rows, k, n, xs, qs, os, scale_dtype, bias ? bias_dtype : -1};
-  if (x_dtype == MI355_F16 && out_dtype == MI355_F16) return w8_typed<F16, F16>(p, stream, cus);
-  if (x_dtype == MI355_F16 && out_dtype == MI355_F32) return w8_typed<F16, F32>(p, stream, cus);
-  if (x_dtype == MI355_BF16 && out_dtype == MI355_BF16) return w8_typed<BF16, BF16>(p, stream, cus);
-  if (x_dtype == MI355_BF16 && out_dtype == MI355_F32) return w8_typed<BF16, F32>(p, stream, cus);
+  const W8Params p{x, q, scale, bias, out, rows, k, n, xs, qs, os, scale_dtype, bias ? bias_dtype : -1, nullptr, nullptr};
+  if (x_dtype == MI355_F16 && out_dtype == MI355_F16) return w8_typed<F16, F16, false>(p, stream, cus);
+  if (x_dtype == MI355_F16 && out_dtype == MI355_F32) return w8_typed<F16, F32, false>(p, stream, cus);
+  if (x_dtype == MI355_BF16 && out_dtype == MI355_BF16) return w8_typed<BF16, BF16, false>(p, stream, cus);
+  if (x_dtype == MI355_BF16 && out_dtype == MI355_F32) return w8_typed<BF16, F32, false>(p, stream, cus);
   set_error("mi355_w8a16_linear_fwd: unsupported dtype pair (x=%d, out=%d)", x_dtype, out_dtype);
+  return MI355_ERR_UNSUPPORTED;
+}
+
+int gate_up_silu_w8a16_launch(const void* x, const void* qg, const void* qu, const void* sg, const void* su, void* out,
+                              int rows, int k, int n, int64_t xs, int64_t qs, int64_t os, int x_dtype,
+                              int scale_dtype, int out_dtype, hipStream_t stream) {
+  int cus = 0;
+  const int st = compute_units(&cus);
+  if (st != MI355_OK) return st;
+  const W8Params p{x, qg, sg, nullptr, out, rows, k, n, xs, qs, os, scale_dtype, -1, qu, su};
+  if (x_dtype == MI355_F16 && out_dtype == MI355_F16) return w8_typed<F16, F16, true>(p, stream, cus);
+  if (x_dtype == MI355_F16 && out_dtype == MI355_F32) return w8_typed<F16, F32, true>(p, stream, cus);
+  if (x_dtype == MI355_BF16 && out_dtype == MI355_BF16) return w8_typed<BF16, BF16, true>(p, stream, cus);
+  if (x_dtype == MI355_BF16 && out_dtype == MI355_F32) return w8_typed<BF16, F32, true>(p, stream, cus);
+  set_error("mi355_gate_up_silu_w8a16_fwd: unsupported dtype pair (x=%d, out=%d)", x_dtype, out_dtype);
   return MI355_ERR_UNSUPPORTED;
 }
 

@@ -38,6 +38,8 @@ import torch
 from ..kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm
 from ..kernels.fused_gate_up_hip import fused_gate_up_silu
 from ..kernels.fused_swiglu_hip import fused_silu_mul
+from ..kernels.w8a16_matmul_hip import fused_gate_up_silu_w8a16
+from ..quantization.int8 import QuantizedLinearInt8
 
 __all__ = ["RMSNORM_CLASS_NAMES", "MLP_CLASS_NAMES", "DECODER_LAYER_CLASS_NAMES", "FusedRMSNorm", "FusedMLP",
            "FusedDecoderLayer", "patch_model_with_fused_kernels"]
@@ -70,10 +72,13 @@ class FusedMLP(torch.nn.Module):
     ``act_fn(gate) * up`` step with the fused SiLU-and-mul kernel.  SiLU is
     fixed, as in the reference; the projection modules are reused.
 
-    With ``fuse_gate_up=True``, inputs whose projections are plain bias-free
-    ``nn.Linear`` layers in fp16 / bf16 with k a multiple of 8 take
-    ``fused_gate_up_silu`` instead (decode steps and prefill alike): gate, up
-    and the activation in one kernel.  Other inputs take the reference
+    With ``fuse_gate_up=True``, fp16 / bf16 inputs whose projections are
+    plain bias-free ``nn.Linear`` layers of x's dtype with k a multiple of 8
+    take ``fused_gate_up_silu`` instead (decode steps and prefill alike), and
+    those whose projections are bias-free ``QuantizedLinearInt8`` layers take
+    ``fused_gate_up_silu_w8a16``: gate, up and the activation in one kernel.
+    The projection kind is checked at each call, so a model quantised after
+    patching switches to the int8 kernel.  Other inputs take the reference
     path."""
 
     def __init__(self, orig_module: torch.nn.Module, fuse_gate_up: bool = False):
@@ -83,18 +88,31 @@ class FusedMLP(torch.nn.Module):
         self.down_proj = orig_module.down_proj
         self.fuse_gate_up = bool(fuse_gate_up) and self.gate_up_fusable()
 
-    def gate_up_fusable(self) -> bool:
-        """Whether the projections are ones the fused gate/up kernel can read:
-        plain bias-free Linear layers of one shape with k a multiple of 8."""
+    def gate_up_kind(self) -> str | None:
+        """Which fused gate/up kernel can read the projections: ``"16bit"``
+        (plain bias-free Linear layers of one shape with k a multiple of 8),
+        ``"int8"`` (bias-free QuantizedLinearInt8 layers of one shape and
+        scale dtype) or None."""
         g, u = self.gate_proj, self.up_proj
-        return (_plain_linear(g) and _plain_linear(u) and g.weight.shape == u.weight.shape
-                and g.weight.shape[1] % 8 == 0)
+        if (_plain_linear(g) and _plain_linear(u) and g.weight.shape == u.weight.shape
+                and g.weight.shape[1] % 8 == 0):
+            return "16bit"
+        if (type(g) is QuantizedLinearInt8 and type(u) is QuantizedLinearInt8 and g.bias is None and u.bias is None
+                and g.weight_q.shape == u.weight_q.shape and g.scale.dtype == u.scale.dtype):
+            return "int8"
+        return None
+
+    def gate_up_fusable(self) -> bool:
+        return self.gate_up_kind() is not None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.fuse_gate_up:
-            wg, wu = self.gate_proj.weight, self.up_proj.weight
-            if x.dtype == wg.dtype == wu.dtype and x.dtype in (torch.float16, torch.bfloat16):
-                return self.down_proj(fused_gate_up_silu(x, wg, wu))
+        if self.fuse_gate_up and x.dtype in (torch.float16, torch.bfloat16):
+            kind = self.gate_up_kind()
+            g, u = self.gate_proj, self.up_proj
+            if kind == "16bit" and x.dtype == g.weight.dtype == u.weight.dtype:
+                return self.down_proj(fused_gate_up_silu(x, g.weight, u.weight))
+            if kind == "int8":
+                return self.down_proj(fused_gate_up_silu_w8a16(x, g.weight_q, g.scale, u.weight_q, u.scale))
         gate = self.gate_proj(x)
         up = self.up_proj(x)
         activated = fused_silu_mul(gate, up)

@@ -16,6 +16,11 @@ reference's torch expression.
 
 ``w8a16_reference`` is the reference's dequantise-then-fp32-linear check
 (:137-149), kept for API parity.
+
+``fused_gate_up_silu_w8a16(x, wq_gate, scale_gate, wq_up, scale_up)`` is the
+int8 form of ``fused_gate_up_silu``: the quantised model's gate_proj and
+up_proj (two W8A16 linears) and SiLU-and-mul as one kernel (C ABI
+``mi355_gate_up_silu_w8a16_fwd``), without rounding the projections.
 """
 from __future__ import annotations
 
@@ -23,7 +28,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["w8a16_linear", "w8a16_reference", "quantize_int8_weight"]
+__all__ = ["w8a16_linear", "w8a16_reference", "quantize_int8_weight", "fused_gate_up_silu_w8a16"]
 
 _CODE = _lib.DTYPE_CODE
 
@@ -66,6 +71,44 @@ def w8a16_linear(x: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor,
                     bias.data_ptr() if bias is not None else None, out.data_ptr(), M, K, N,
                     xs, ws, N, _CODE[x.dtype], _CODE[scale.dtype],
                     _CODE[bias.dtype] if bias is not None else 0, _CODE[out_dtype])
+    return out.reshape(*x.shape[:-1], N)
+
+
+def fused_gate_up_silu_w8a16(x: torch.Tensor, wq_gate: torch.Tensor, scale_gate: torch.Tensor,
+                             wq_up: torch.Tensor, scale_up: torch.Tensor,
+                             out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """silu((x @ wq_gate.T) * scale_gate) * ((x @ wq_up.T) * scale_up) for x
+    (..., K) fp16/bf16 and int8 weights (N, K) with (N,) scales (one float
+    dtype).  Output (..., N) in x's dtype (or ``out_dtype=torch.float32``)."""
+    assert x.is_cuda and wq_gate.is_cuda and wq_up.is_cuda, "x and the weights must be ROCm GPU tensors"
+    assert wq_gate.dtype == torch.int8 and wq_up.dtype == torch.int8, "weights must be int8"
+    assert wq_gate.shape == wq_up.shape, f"weight shapes differ: {tuple(wq_gate.shape)} vs {tuple(wq_up.shape)}"
+    N, K = wq_gate.shape
+    assert x.shape[-1] == K, f"x last dim {x.shape[-1]} != weight in_features {K}"
+    assert x.dtype in (torch.float16, torch.bfloat16), f"x must be fp16 or bf16, got {x.dtype}"
+    for sc in (scale_gate, scale_up):
+        assert sc.is_cuda and sc.shape == (N,) and sc.dtype in _CODE, (
+            f"scales must be ({N},) float GPU tensors, got {tuple(sc.shape)} {sc.dtype}")
+    assert scale_gate.dtype == scale_up.dtype, "the two scales must share a dtype"
+    dev = x.get_device()
+    assert all(t.get_device() == dev for t in (wq_gate, wq_up, scale_gate, scale_up)), "all inputs must share a device"
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    assert out_dtype in (x.dtype, torch.float32), f"out_dtype must be {x.dtype} or float32"
+
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if wq_gate.stride(-1) != 1 or wq_up.stride(-1) != 1 or wq_gate.stride(0) != wq_up.stride(0):
+        wq_gate, wq_up = wq_gate.contiguous(), wq_up.contiguous()
+    scale_gate, scale_up = scale_gate.contiguous(), scale_up.contiguous()
+    M = x2.shape[0]
+    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if M and N:
+        xs = x2.stride(0) if M > 1 else K
+        ws = wq_gate.stride(0) if N > 1 else K
+        _lib.launch("mi355_gate_up_silu_w8a16_fwd", dev, x2.data_ptr(), wq_gate.data_ptr(), wq_up.data_ptr(),
+                    scale_gate.data_ptr(), scale_up.data_ptr(), out.data_ptr(), M, K, N, xs, ws, N,
+                    _CODE[x.dtype], _CODE[scale_gate.dtype], _CODE[out_dtype])
     return out.reshape(*x.shape[:-1], N)
 
 

@@ -285,6 +285,40 @@ def w8a16_linear(x: np.ndarray, q: np.ndarray, scale: np.ndarray, bias: np.ndarr
     return res
 
 
+def gate_up_silu_w8a16(x: np.ndarray, qg: np.ndarray, sg: np.ndarray, qu: np.ndarray, su: np.ndarray, *,
+                       xdt: str, sdt: str = "f32", odt: str | None = None, mutate: str | None = None) -> dict:
+    """Int8 gate/up projections + SiLU-and-mul without intermediate rounding
+    (the quantised MLP's gate_proj / up_proj, src/quantization/int8.py:62-63,
+    and its activation, src/engine/fused_norm_activation_patch.py:60-64, as
+    one computation).  Composes the pinned pieces: ``w8a16_linear`` in its
+    kernel mode with an fp32 result (the order-free fp32 sum times the
+    scale, unrounded) for each projection, then ``silu_mul`` on those fp32
+    values with one rounding to ``odt``.  Returns ``out`` (odt storage),
+    ``out64`` = silu(g) * u of the exact scaled projections, ``g`` / ``u``
+    (fp64) and ``gabs`` / ``uabs`` = |scale| * sum_k |x * q|.
+
+    ``mutate`` plants a mistake for the tests: "swap_scales" (each projection
+    takes the other's scale), "swap_gate_up" (silu(u) * g) or
+    "round_projections" (g and u rounded to xdt first, as the unfused chain)."""
+    if mutate == "swap_scales":
+        sg, su = su, sg
+    g = w8a16_linear(x, qg, sg, xdt=xdt, sdt=sdt, odt="f32")
+    u = w8a16_linear(x, qu, su, xdt=xdt, sdt=sdt, odt="f32")
+    if mutate == "swap_gate_up":
+        g, u = u, g
+    odt = odt or xdt
+    g32, u32 = g["out"], u["out"]
+    if mutate == "round_projections":
+        g32 = to_f32(from_f32(g32, xdt), xdt)
+        u32 = to_f32(from_f32(u32, xdt), xdt)
+    out = silu_mul(g32, u32, idt="f32", odt=odt)
+    g64, u64 = g["out64"], u["out64"]
+    sgv = np.abs(to_f32(_arr(sg, sdt), sdt).astype(np.float64))
+    suv = np.abs(to_f32(_arr(su, sdt), sdt).astype(np.float64))
+    return {"out": out, "out64": g64 / (1.0 + np.exp(-g64)) * u64, "g": g64, "u": u64,
+            "gabs": g["absacc"] * sgv[None, :], "uabs": u["absacc"] * suv[None, :]}
+
+
 def quantize_int8(w: np.ndarray, *, wdt: str, mutate: str | None = None) -> tuple[np.ndarray, np.ndarray]:
     """Per-output-channel symmetric int8 quantisation of w [n, k] (wdt
     storage), as QuantizedLinearInt8.from_linear (src/quantization/int8.py:45-50).

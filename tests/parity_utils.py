@@ -32,3 +32,23 @@ def storage(t: torch.Tensor) -> np.ndarray:
 def ulp_report(got: np.ndarray, want: np.ndarray, orc) -> tuple[int, float]:
     d = orc.ulp_diff16(got, want)
     return int(d.max()) if d.size else 0, float((d > 0).mean()) if d.size else 0.0
+
+
+def ulp16(v: np.ndarray, dt) -> np.ndarray:
+    """One ulp of fp16 / bf16 at the magnitude of each (fp64) value."""
+    mant, emin = (10, -14) if dt == torch.float16 else (7, -126)
+    e = np.maximum(np.floor(np.log2(np.maximum(np.abs(v), 1e-300))), emin)
+    return 2.0 ** (e - mant)
+
+
+def act_error_bound(g, u, gabs, uabs, k):
+    """Worst-case effect of fp32 summation (any order) of the gate / up
+    projections on silu(g) * u: gamma_k * sum|x w| per projection (gabs,
+    uabs; scaled by the quantisation scale where there is one), carried
+    through the activation's derivatives."""
+    gam = k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
+    eg, eu = gam * gabs, gam * uabs
+    sig = 1.0 / (1.0 + np.exp(-g))
+    dsilu = sig * (1.0 + g * (1.0 - sig))
+    # second-order slack: |silu''| <= 0.5
+    return np.abs(dsilu * u) * eg + np.abs(g * sig) * eu + eg * eu + 0.5 * eg * eg * np.abs(u)

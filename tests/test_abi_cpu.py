@@ -251,3 +251,37 @@ def test_w8a16_launchers_assert_on_host_tensors(pkg):
         pkg.quantize_int8_weight(torch.randn(16, 64))
     with pytest.raises(AssertionError):
         pkg.QuantizedLinearInt8.from_linear(torch.nn.Linear(64, 16))
+
+
+# (x, wq_gate, wq_up, scale_gate, scale_up, out, rows, k, n_out, x_row_stride, w_row_stride,
+#  out_row_stride, x_dtype, scale_dtype, out_dtype)
+@pytest.mark.parametrize("args,code,msg", [
+    ((P, P, P, P, P, P, 8, 64, 32, 64, 64, 32, 3, 0, 1), -1, "unknown dtype"),
+    ((P, P, P, P, P, P, 8, 64, 32, 64, 64, 32, 0, 0, 0), -2, "fp16 or bf16"),
+    ((P, P, P, P, P, P, 8, 64, 32, 64, 64, 32, 1, 0, 2), -2, "out dtype"),
+    ((P, P, P, P, P, P, -1, 64, 32, 64, 64, 32, 1, 0, 1), -1, "need rows"),
+    ((P, P, P, P, P, P, 8, 0, 32, 64, 64, 32, 1, 0, 1), -1, "need rows"),
+    ((P, P, P, P, P, P, 8, 64, 32, 32, 64, 32, 1, 0, 1), -1, "row strides"),
+    ((P, P, P, P, P, P, 8, 64, 32, 64, 64, 16, 1, 0, 1), -1, "row strides"),
+    ((P, P, 0, P, P, P, 8, 64, 32, 64, 64, 32, 1, 0, 1), -1, "null pointer"),
+    ((P, P, P, P, 0, P, 8, 64, 32, 64, 64, 32, 1, 0, 1), -1, "null pointer"),
+    ((P, P, P, P, P, P, 8, 64, 32, 2**23, 64, 32, 1, 0, 1), -2, "limits"),
+    ((P, P, P, P, P, P, 65535 * 64 + 1, 64, 32, 64, 64, 32, 1, 0, 1), -2, "limits"),
+])
+def test_gate_up_w8a16_abi_rejects(lib, args, code, msg):
+    st = lib.mi355_gate_up_silu_w8a16_fwd(*args, None)
+    assert st == code
+    assert msg in lib.mi355_last_error().decode()
+
+
+def test_gate_up_w8a16_abi_empty_is_noop(lib):
+    assert lib.mi355_gate_up_silu_w8a16_fwd(0, 0, 0, 0, 0, 0, 0, 64, 32, 64, 64, 32, 1, 0, 1, None) == 0
+    assert lib.mi355_gate_up_silu_w8a16_fwd(0, 0, 0, 0, 0, 0, 8, 64, 0, 64, 64, 0, 2, 0, 2, None) == 0
+    assert lib.mi355_last_error().decode() == ""
+
+
+def test_gate_up_w8a16_launcher_asserts_on_host_tensors(pkg):
+    x = torch.randn(4, 64, dtype=torch.float16)
+    q = torch.zeros(16, 64, dtype=torch.int8)
+    with pytest.raises(AssertionError):
+        pkg.fused_gate_up_silu_w8a16(x, q, torch.ones(16), q, torch.ones(16))

@@ -173,3 +173,61 @@ def test_linear_planted_mistakes_are_caught(mutate):
     tol = 1e-4 * (np.abs(want) + 1e-2)
     assert np.all(np.abs(good - want) <= tol)
     assert not np.all(np.abs(bad - want) <= tol), f"planted mistake {mutate} not caught"
+
+
+# ------------------------------------------ int8 gate/up + SiLU-and-mul
+
+def _gu_case(rows, k, n, xdt, seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    x = torch.randn(rows, k, generator=g).to(DT[xdt])
+    qg, sg = _torch_quantize((torch.randn(n, k, generator=g) * (2.0 * k ** -0.5)).to(DT[xdt]))
+    qu, su = _torch_quantize((torch.randn(n, k, generator=g) * k ** -0.5).to(DT[xdt]))
+    return x, qg, sg, qu, su
+
+
+def _gu_closed_form(x, qg, sg, qu, su):
+    g = (_f64(x) @ qg.astype(np.float64).T) * sg.astype(np.float64)
+    u = (_f64(x) @ qu.astype(np.float64).T) * su.astype(np.float64)
+    return g / (1.0 + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+@pytest.mark.parametrize("rows,k,n", [(8, 1536, 96), (3, 100, 37), (33, 256, 64)])
+def test_gate_up_w8a16_exact_value_is_the_closed_form(xdt, rows, k, n):
+    x, qg, sg, qu, su = _gu_case(rows, k, n, xdt, seed=rows + k)
+    r = orc.gate_up_silu_w8a16(_storage(x), qg, sg, qu, su, xdt=xdt)
+    assert np.allclose(r["out64"], _gu_closed_form(x, qg, sg, qu, su), rtol=1e-12, atol=1e-14)
+    assert np.allclose(r["gabs"], (np.abs(_f64(x)) @ np.abs(qg.astype(np.float64)).T) * sg, rtol=1e-12)
+
+
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_gate_up_w8a16_single_rounding_matches_torch_fp32(xdt):
+    """torch's fp32 evaluation of the fused formula: the order-free fp32
+    projection sums times their scales, F.silu(g) * u in fp32, one cast."""
+    rows, k, n = 16, 896, 160
+    x, qg, sg, qu, su = _gu_case(rows, k, n, xdt, seed=3)
+    r = orc.gate_up_silu_w8a16(_storage(x), qg, sg, qu, su, xdt=xdt)
+    g32 = torch.from_numpy(np.float32(_f64(x) @ qg.astype(np.float64).T)) * torch.from_numpy(sg)
+    u32 = torch.from_numpy(np.float32(_f64(x) @ qu.astype(np.float64).T)) * torch.from_numpy(su)
+    want = _storage((torch.nn.functional.silu(g32) * u32).to(DT[xdt]))
+    d = orc.ulp_diff16(r["out"], want)
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+
+
+@pytest.mark.parametrize("mutate", ["swap_scales", "swap_gate_up", "round_projections"])
+def test_gate_up_w8a16_planted_mistakes_are_caught(mutate):
+    rows, k, n = 12, 512, 96
+    x, qg, sg, qu, su = _gu_case(rows, k, n, "f16", seed=11)
+    sg = sg * np.float32(1.7)  # distinct scale magnitudes, so a swap shows
+    exact = _gu_closed_form(x, qg, sg, qu, su)
+
+    def ok(out):
+        v = orc.to_f32(out, "f16").astype(np.float64)
+        ulp = np.maximum(np.abs(exact), 2.0 ** -14) * 2.0 ** -10
+        return np.mean(np.abs(v - exact) <= 0.5 * ulp + 1e-6 * np.abs(exact)) >= 0.99
+
+    good = orc.gate_up_silu_w8a16(_storage(x), qg, sg, qu, su, xdt="f16")["out"]
+    bad = orc.gate_up_silu_w8a16(_storage(x), qg, sg, qu, su, xdt="f16", mutate=mutate)["out"]
+    assert ok(good)
+    assert not ok(bad), f"planted mistake {mutate} not caught"
