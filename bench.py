@@ -26,6 +26,7 @@ Also reported on the same JSON line:
                 vs the reference's two-GEMM + SiLU-and-mul chain;
   gate_up_silu_prefill  the same at prefill rows (tiled MFMA GEMM), same baseline;
   w8a16         the weight-only int8 linear vs fp16 torch.matmul (hipBLASLt);
+  gate_up_silu_w8a16  int8 gate/up + SiLU-and-mul vs two W8A16 linears + SiLU-and-mul;
   copy_ceiling  a plain 16-byte streaming copy on the same device.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -64,7 +65,7 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up",
-                                      "gate-up-prefill", "w8a16", "w8a16-decode", "w8a16-prefill"],
+                                      "gate-up-prefill", "gate-up-w8", "w8a16", "w8a16-decode", "w8a16-prefill"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -561,6 +562,7 @@ def main():
         result["gate_up_silu"] = bench_gate_up(ctx)
         result["gate_up_silu_prefill"] = bench_gate_up_prefill(ctx)
         result["w8a16"] = bench_w8a16(ctx)
+        result["gate_up_silu_w8a16"] = bench_gate_up_w8(ctx)
         result["copy_ceiling"] = bench_copy(ctx)
 
     if not args.skip_cpu:
@@ -597,6 +599,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up(ctx, shapes=GATE_UP_SHAPES[1:2], iters=iters, baselines=False)))
+    elif args.only == "gate-up-w8":
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_gate_up_w8(ctx)))
     elif args.only == "gate-up-prefill":  # kernel only, the 1.5B MLP at 1024 and 4096 rows
         del sets
         torch.cuda.empty_cache()
@@ -836,6 +842,53 @@ def bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES, iters=60, baseline
         res[f"{label}_M{M}_{dname}"] = entry
         log(f"  gate_up prefill {label} M={M}: {entry}")
         del ws, outs, fused
+        torch.cuda.empty_cache()
+    return res
+
+
+# (rows, k, n_out, dtype name, label): int8 gate/up + SiLU-and-mul, decode and prefill rows
+GATE_UP_W8_SHAPES = [(1, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 1536, 8960, "f16", "qwen2.5-1.5b"),
+                     (32, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 3584, 18944, "bf16", "qwen2.5-7b"),
+                     (1024, 1536, 8960, "f16", "qwen2.5-1.5b")]
+
+
+def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300):
+    """Int8 gate/up projections + SiLU-and-mul (one kernel) against the
+    quantised model's chain: two W8A16 linears (this build's kernel, each
+    rounded to x's dtype) and the SiLU-and-mul kernel.  Per-layer int8
+    weight sets with a footprint above 1 GiB; eager back-to-back and hipGraph
+    timing (min).  Algorithmic bytes: both int8 matrices + both fp32 scales +
+    x + out."""
+    torch = ctx.torch
+    pkg = ctx.pkg
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
+    res = {}
+    for M, K, I, dname, label in shapes:
+        dt = dts[dname]
+        nbytes = 2 * I * K + 2 * 4 * I + M * K * 2 + M * I * 2
+        flops = 4.0 * M * K * I
+        sets = min(128, n_sets(2 * I * K))
+        x = rand(ctx, (M, K), 2600 + M, dt)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(2700 + K + I)
+        ws = [(torch.randint(-127, 128, (I, K), generator=g, device=ctx.dev, dtype=torch.int8),
+               torch.rand(I, generator=g, device=ctx.dev) * 2e-3 + 1e-4,
+               torch.randint(-127, 128, (I, K), generator=g, device=ctx.dev, dtype=torch.int8),
+               torch.rand(I, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
+        fused = [lambda w=w: pkg.fused_gate_up_silu_w8a16(x, w[0], w[1], w[2], w[3]) for w in ws]
+        spin_up(ctx, fused)
+        us = min(time_loop(ctx, fused, iters), time_graph(ctx, fused, max(2 * sets, 64)))
+        chains = [lambda w=w: pkg.fused_silu_mul(pkg.w8a16_linear(x, w[0], w[1]), pkg.w8a16_linear(x, w[2], w[3]))
+                  for w in ws]
+        spin_up(ctx, chains)
+        c_us = min(time_loop(ctx, chains, iters), time_graph(ctx, chains, max(2 * sets, 64)))
+        entry = kernel_entry("w8a16 dual (gate/up + SiLU-and-mul)", nbytes, us,
+                             {"rows": M, "k": K, "n_out": I, "dtype": dname, "weight_sets": sets,
+                              "TFLOPs": round(flops / us / 1e6, 1), "w8a16_chain_us": round(c_us, 3),
+                              "speedup": round(c_us / us, 3)})
+        res[f"{label}_M{M}_{dname}"] = entry
+        log(f"  int8 gate_up {label} M={M}: {entry}")
+        del ws, fused, chains
         torch.cuda.empty_cache()
     return res
 
@@ -1159,10 +1212,18 @@ def bench_e2e_int8(args):
     counts = pkg.patch_model_with_fused_kernels(model, fuse_residual=True)
     log(f"patched {counts}")
     int8_fused = phase("int8+fused")
+    n_gu = 0
+    for m in model.modules():
+        if isinstance(m, pkg.FusedMLP) and m.gate_up_kind() == "int8":
+            m.fuse_gate_up = True
+            n_gu += 1
+    log(f"int8 gate/up + SiLU-and-mul fused in {n_gu} MLPs")
+    int8_gu = phase("int8+fused+int8_gate_up")
     print(json.dumps({"metric": "fp16 vs int8-weight (W8A16) decode tok/s, after run_stage7_e2e.py",
                       "model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16 activations, sdpa",
                       "seq_len": S, "gen_len": GEN, "trials": TRIALS, "quantize_stats": stats,
-                      "fp16": fp16, "int8": int8, "int8_fused_kernels": int8_fused, "patched": counts}),
+                      "fp16": fp16, "int8": int8, "int8_fused_kernels": int8_fused,
+                      "int8_fused_kernels_int8_gate_up": int8_gu, "int8_gate_up_mlps": n_gu, "patched": counts}),
           flush=True)
 
 

@@ -445,8 +445,12 @@ int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
   // the dual kernel carries two weight matrices per row group: half the
   // groups, and at most 2 (MT = 2) or 1 (MT >= 3) so its 2 G MT accumulator
   // tiles fit the register budget
-  constexpr int gmax = !DUAL ? 4 : (MT >= 3 ? 1 : (MT == 2 ? 2 : 4));
-  if (DUAL) g = g > 1 ? g / 2 : 1;
+  // The dual kernel carries two weight matrices per row group: one group for
+  // a single row, else at most 2 (a sweep of G x split x U over Qwen2.5-1.5B
+  // and -7B decode rows: 8 rows 9.2 us with 2 groups vs 12.5 us with 1), and
+  // 1 for MT >= 3 so its 2 G MT accumulator tiles fit the register budget.
+  constexpr int gmax = !DUAL ? 4 : (MT >= 3 ? 1 : 2);
+  if (DUAL) g = p.rows <= 1 ? 1 : (g > 2 ? 2 : g);
 #ifdef MI355_W8_SWEEP
   if (g_force_g > 0) g = g_force_g;
 #endif
