@@ -65,7 +65,8 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up",
-                                      "gate-up-prefill", "gate-up-w8", "w8a16", "w8a16-decode", "w8a16-prefill"],
+                                      "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
+                                      "w8a16-prefill"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -349,6 +350,12 @@ KNOWN_LAUNCHES = {
     ("w8a16_skinny<mi355::BF16, mi355::BF16, 1, 4, 1>", 192 * 592): (
         "W8A16 7B gate/up, 8 rows, [18944,3584] int8, bf16",
         18944 * 3584 + 4 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
+    ("w8a16_skinny<mi355::F16, mi355::F16, 1, 2, 1, true>", 192 * 560): (
+        "int8 gate/up + SiLU-and-mul 1.5B, 8 rows, 2 x [8960,1536] int8, fp16",
+        2 * 8960 * 1536 + 8 * 8960 + 8 * 1536 * 2 + 8 * 8960 * 2),
+    ("w8a16_skinny<mi355::BF16, mi355::BF16, 1, 2, 1, true>", 64 * 1184): (
+        "int8 gate/up + SiLU-and-mul 7B, 8 rows, 2 x [18944,3584] int8, bf16",
+        2 * 18944 * 3584 + 8 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
     # MFMA-bound prefill GEMMs: (label, algorithmic bytes, flops)
     ("tiled_gemm<mi355::F16, 0, mi355::F16, 4, 2, 2, 1, 1, 3>", 560 * 512): (
         "gate/up + SiLU-and-mul prefill, 1024 rows, [8960,1536] weights, fp16",
@@ -603,6 +610,11 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_w8(ctx)))
+    elif args.only == "gate-up-w8-decode":  # the two 8-row shapes profiled under profiles/, no baseline
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_gate_up_w8(ctx, shapes=[s for s in GATE_UP_W8_SHAPES if s[0] == 8], iters=iters,
+                                        baselines=False)))
     elif args.only == "gate-up-prefill":  # kernel only, the 1.5B MLP at 1024 and 4096 rows
         del sets
         torch.cuda.empty_cache()
@@ -852,7 +864,7 @@ GATE_UP_W8_SHAPES = [(1, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 1536, 8960, "f1
                      (1024, 1536, 8960, "f16", "qwen2.5-1.5b")]
 
 
-def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300):
+def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300, baselines=True):
     """Int8 gate/up projections + SiLU-and-mul (one kernel) against the
     quantised model's chain: two W8A16 linears (this build's kernel, each
     rounded to x's dtype) and the SiLU-and-mul kernel.  Per-layer int8
@@ -878,17 +890,19 @@ def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300):
         fused = [lambda w=w: pkg.fused_gate_up_silu_w8a16(x, w[0], w[1], w[2], w[3]) for w in ws]
         spin_up(ctx, fused)
         us = min(time_loop(ctx, fused, iters), time_graph(ctx, fused, max(2 * sets, 64)))
-        chains = [lambda w=w: pkg.fused_silu_mul(pkg.w8a16_linear(x, w[0], w[1]), pkg.w8a16_linear(x, w[2], w[3]))
-                  for w in ws]
-        spin_up(ctx, chains)
-        c_us = min(time_loop(ctx, chains, iters), time_graph(ctx, chains, max(2 * sets, 64)))
         entry = kernel_entry("w8a16 dual (gate/up + SiLU-and-mul)", nbytes, us,
                              {"rows": M, "k": K, "n_out": I, "dtype": dname, "weight_sets": sets,
-                              "TFLOPs": round(flops / us / 1e6, 1), "w8a16_chain_us": round(c_us, 3),
-                              "speedup": round(c_us / us, 3)})
+                              "TFLOPs": round(flops / us / 1e6, 1)})
+        if baselines:
+            chains = [lambda w=w: pkg.fused_silu_mul(pkg.w8a16_linear(x, w[0], w[1]),
+                                                     pkg.w8a16_linear(x, w[2], w[3])) for w in ws]
+            spin_up(ctx, chains)
+            c_us = min(time_loop(ctx, chains, iters), time_graph(ctx, chains, max(2 * sets, 64)))
+            entry.update({"w8a16_chain_us": round(c_us, 3), "speedup": round(c_us / us, 3)})
+            del chains
         res[f"{label}_M{M}_{dname}"] = entry
         log(f"  int8 gate_up {label} M={M}: {entry}")
-        del ws, fused, chains
+        del ws, fused
         torch.cuda.empty_cache()
     return res
 
