@@ -27,7 +27,10 @@ Also reported on the same JSON line:
   gate_up_silu_prefill  the same at prefill rows (tiled MFMA GEMM), same baseline;
   w8a16         the weight-only int8 linear vs fp16 torch.matmul (hipBLASLt);
   gate_up_silu_w8a16  int8 gate/up + SiLU-and-mul vs two W8A16 linears + SiLU-and-mul;
-  copy_ceiling  a plain 16-byte streaming copy on the same device.
+  copy_ceiling  a plain 16-byte streaming copy on the same device;
+  ceilings      the same probe (and a two-input, one-output variant) at each
+                kernel's own byte count and access mix, cold, and each
+                kernel's time as a fraction of it.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -64,7 +67,7 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "gate-up",
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "ceilings", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill"],
                    default=None,
@@ -105,6 +108,9 @@ class Ctx:
             self.probe.mi355_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
                                                     ctypes.c_int, ctypes.c_void_p]
             self.probe.mi355_probe_copy.restype = ctypes.c_int
+            self.probe.mi355_probe_add2.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                    ctypes.c_int64, ctypes.c_void_p]
+            self.probe.mi355_probe_add2.restype = ctypes.c_int
 
     def rms_call(self, x, w, y, eps=1e-6):
         M, N = x.shape
@@ -178,6 +184,15 @@ class Ctx:
         def call():
             if f(*args, self.stream):
                 raise RuntimeError("probe copy failed")
+        return call
+
+    def add2_call(self, a, b, dst):
+        f = self.probe.mi355_probe_add2
+        args = (a.data_ptr(), b.data_ptr(), dst.data_ptr(), a.numel() * a.element_size())
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError("probe add2 failed")
         return call
 
 
@@ -571,6 +586,15 @@ def main():
         result["w8a16"] = bench_w8a16(ctx)
         result["gate_up_silu_w8a16"] = bench_gate_up_w8(ctx)
         result["copy_ceiling"] = bench_copy(ctx)
+        result["ceilings"] = bench_ceilings(ctx)
+        if result["ceilings"]:
+            pairs = [("C2 SiLU-and-mul [2048,8960] fp16", result["kernels"]["c2_silu_mul_f16_2048x8960"]),
+                     ("C1 RMSNorm [2048,1536] fp16", result["kernels"]["c1_rmsnorm_f16_2048x1536"]),
+                     ("C4 RMSNorm [16384,3584] bf16", result["c4"]["c4_rmsnorm_bf16_16384x3584"]),
+                     ("C4 SiLU-and-mul [16384,18944] bf16", result["c4"]["c4_silu_mul_bf16_16384x18944"])]
+            result["frac_of_same_size_ceiling"] = {
+                lab: round(result["ceilings"][lab]["us"] / k["us"], 4) for lab, k in pairs}
+            log(f"  kernel time / same-size probe time: {result['frac_of_same_size_ceiling']}")
 
     if not args.skip_cpu:
         log("cpu baseline ...")
@@ -602,6 +626,10 @@ def run_only(ctx, args, sets):
         log(json.dumps(d))
     elif args.only == "copy":
         log(json.dumps(bench_copy(ctx)))
+    elif args.only == "ceilings":
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_ceilings(ctx)))
     elif args.only == "gate-up":
         del sets
         torch.cuda.empty_cache()
@@ -995,6 +1023,50 @@ def bench_copy(ctx, nbytes=1 << 30, iters=30):
     torch.cuda.empty_cache()
     log(f"  copy ceiling: {d['GBps']:.0f} GB/s ({d['frac_of_peak']:.1%})")
     return d
+
+
+# (label, streams read, bytes per stream) of each benchmarked kernel's access
+# mix: RMSNorm reads one row stream and writes one (its weight row is an L2
+# hit), SiLU-and-mul reads two and writes one.
+CEILING_SHAPES = [
+    ("C1 RMSNorm [2048,1536] fp16", 1, 2048 * 1536 * 2),
+    ("C2 SiLU-and-mul [2048,8960] fp16", 2, 2048 * 8960 * 2),
+    ("C4 RMSNorm [16384,3584] bf16", 1, 16384 * 3584 * 2),
+    ("C4 SiLU-and-mul [16384,18944] bf16", 2, 16384 * 18944 * 2),
+    ("1 GiB per stream", 1, 1 << 30),
+    ("512 MiB per stream", 2, 1 << 29),
+]
+
+
+def bench_ceilings(ctx, iters=200):
+    """Achievable HBM bandwidth at each kernel's own byte count and access mix:
+    the probe copy (one read stream, one write stream) or add2 (two read
+    streams, one write stream), cold (rotating buffer sets of >= 1 GiB), the
+    same timing as the kernels.  A kernel's time over its ceiling's time is
+    the fraction of what this device moves at that size that it reaches."""
+    if ctx.probe is None:
+        return None
+    torch = ctx.torch
+    out = {}
+    for label, nread, nbytes in CEILING_SHAPES:
+        traffic = (nread + 1) * nbytes
+        nset = n_sets(traffic)
+        bufs, calls = [], []
+        for _ in range(nset):
+            ins = [torch.empty(nbytes, dtype=torch.uint8, device=ctx.dev).random_(0, 255) for _ in range(nread)]
+            dst = torch.empty(nbytes, dtype=torch.uint8, device=ctx.dev)
+            bufs.append((ins, dst))
+            calls.append(ctx.copy_call(ins[0], dst) if nread == 1 else ctx.add2_call(ins[0], ins[1], dst))
+        torch.cuda.synchronize()
+        spin_up(ctx, calls)
+        n = iters if traffic < (1 << 30) else max(20, iters // 10)
+        us = time_loop(ctx, calls, n)
+        d = kernel_entry("stream_copy" if nread == 1 else "stream_add2", traffic, us, {"buffer_sets": nset})
+        out[label] = d
+        log(f"  ceiling {label}: {us:.2f} us, {d['GBps']:.0f} GB/s ({d['frac_of_peak']:.1%})")
+        del bufs, calls
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_e2e(args):
