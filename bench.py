@@ -463,6 +463,22 @@ def rocprof_summary(dirs):
             traffic[label] = {"traffic_bytes": round(tb), "algorithmic_bytes": nbytes,
                               "fetch_kib": round(fk, 1), "write_kib": round(wk, 1)}
         out.append("")
+        occ_names = ("SQ_WAVES", "OccupancyPercent", "MeanOccupancyPerCU")
+        occ_keys = sorted({(k[0], k[1]) for k in pmc if k[2] in occ_names})
+        if occ_keys:
+            out.append("### Occupancy (per dispatch, averaged over dispatches)\n")
+            out.append("| kernel | dispatches | SQ_WAVES | OccupancyPercent (% of 32 waves per CU) | "
+                       "MeanOccupancyPerCU (waves) |")
+            out.append("|---|---|---|---|---|")
+            for frag, grid in occ_keys:
+                cells = []
+                for c in occ_names:
+                    v = pmc.get((frag, grid, c))
+                    cells.append(f"{sum(v) / len(v):.2f}" if v else "-")
+                nd = max(len(pmc.get((frag, grid, c), [])) for c in occ_names)
+                label = KNOWN_LAUNCHES[(frag, grid)][0]
+                out.append(f"| {frag} ({label}) | {nd} | " + " | ".join(cells) + " |")
+            out.append("")
     return "\n".join(out), traffic
 
 
