@@ -27,6 +27,8 @@ Also reported on the same JSON line:
   gate_up_silu_prefill  the same at prefill rows (tiled MFMA GEMM), same baseline;
   w8a16         the weight-only int8 linear vs fp16 torch.matmul (hipBLASLt);
   gate_up_silu_w8a16  int8 gate/up + SiLU-and-mul vs two W8A16 linears + SiLU-and-mul;
+  linear16_down the MLP's down projection on the HIP 16-bit linear vs torch's
+                linear (hipBLASLt) at decode rows;
   copy_ceiling  a plain 16-byte streaming copy on the same device;
   ceilings      the same probe (and a two-input, one-output variant) at each
                 kernel's own byte count and access mix, cold, and each
@@ -67,7 +69,7 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "ceilings", "gate-up",
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "ceilings", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill"],
                    default=None,
@@ -175,6 +177,20 @@ class Ctx:
             st = f(*args, self.stream)
             if st:
                 self.L.check("mi355_w8a16_linear_fwd", st)
+        return call
+
+    def linear16_call(self, x, w, out, bias=None):
+        M, K = x.shape
+        N = w.shape[0]
+        code = self.L.DTYPE_CODE[x.dtype]
+        f = self.lib.mi355_linear16_fwd
+        args = (x.data_ptr(), w.data_ptr(), bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                M, K, N, K, K, N, code, self.L.DTYPE_CODE[bias.dtype] if bias is not None else 0, code)
+
+        def call():
+            st = f(*args, self.stream)
+            if st:
+                self.L.check("mi355_linear16_fwd", st)
         return call
 
     def copy_call(self, src, dst):
@@ -371,6 +387,10 @@ KNOWN_LAUNCHES = {
     ("w8a16_skinny<mi355::BF16, mi355::BF16, 1, 2, 1, true>", 64 * 1184): (
         "int8 gate/up + SiLU-and-mul 7B, 8 rows, 2 x [18944,3584] int8, bf16",
         2 * 18944 * 3584 + 8 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
+    ("linear16_skinny<mi355::F16, mi355::F16, 1, 1, 2>", 192 * 512): (
+        "16-bit linear, 8 rows, [1536,8960] weights, fp16 (1.5B down)", 1536 * 8960 * 2 + 8 * 8960 * 2 + 8 * 1536 * 2),
+    ("linear16_skinny<mi355::BF16, mi355::BF16, 1, 2, 2>", 224 * 512): (
+        "16-bit linear, 8 rows, [3584,18944] weights, bf16 (7B down)", 3584 * 18944 * 2 + 8 * 18944 * 2 + 8 * 3584 * 2),
     # MFMA-bound prefill GEMMs: (label, algorithmic bytes, flops)
     ("tiled_gemm<mi355::F16, 0, mi355::F16, 4, 2, 2, 1, 1, 3>", 560 * 512): (
         "gate/up + SiLU-and-mul prefill, 1024 rows, [8960,1536] weights, fp16",
@@ -601,6 +621,7 @@ def main():
         result["gate_up_silu_prefill"] = bench_gate_up_prefill(ctx)
         result["w8a16"] = bench_w8a16(ctx)
         result["gate_up_silu_w8a16"] = bench_gate_up_w8(ctx)
+        result["linear16_down"] = bench_linear16(ctx)
         result["copy_ceiling"] = bench_copy(ctx)
         result["ceilings"] = bench_ceilings(ctx)
         if result["ceilings"]:
@@ -659,6 +680,11 @@ def run_only(ctx, args, sets):
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_w8(ctx, shapes=[s for s in GATE_UP_W8_SHAPES if s[0] == 8], iters=iters,
                                         baselines=False)))
+    elif args.only == "linear16":  # kernel only, the 1.5B down projection at 8 rows and the 7B one at 8 rows
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_linear16(ctx, shapes=[s for s in LINEAR16_SHAPES if s[0] == 8], iters=iters,
+                                      baselines=False)))
     elif args.only == "gate-up-prefill":  # kernel only, the 1.5B MLP at 1024 and 4096 rows
         del sets
         torch.cuda.empty_cache()
@@ -962,6 +988,55 @@ W8A16_SHAPES = [(M, K, N, "f16", lab) for K, N, lab in ((1536, 1536, "q/o proj")
                                                (4096, 8960, 1536, "f16", "down proj")]
 
 
+# (rows, k, n, dtype name, label): the MLP down projections of Qwen2.5-1.5B and -7B at decode rows
+LINEAR16_SHAPES = [(1, 8960, 1536, "f16", "qwen2.5-1.5b down"), (8, 8960, 1536, "f16", "qwen2.5-1.5b down"),
+                   (32, 8960, 1536, "f16", "qwen2.5-1.5b down"), (1, 18944, 3584, "bf16", "qwen2.5-7b down"),
+                   (8, 18944, 3584, "bf16", "qwen2.5-7b down")]
+
+
+def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
+    """The MLP's down projection at decode rows on the HIP 16-bit linear
+    (mi355_linear16_fwd, weight streaming on MFMA) against torch's linear
+    (hipBLASLt), the call FusedMLP makes otherwise, on per-layer weight sets
+    whose footprint exceeds 1 GiB (cold HBM, as a decode step walking the
+    layers).  Algorithmic bytes: weights + x + out.  Timed over back-to-back
+    launches and inside a hipGraph."""
+    torch = ctx.torch
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
+    res = {}
+    for M, K, N, dname, label in shapes:
+        dt = dts[dname]
+        wbytes = N * K * 2
+        nbytes = wbytes + M * K * 2 + M * N * 2
+        layers = n_sets(wbytes)
+        x = rand(ctx, (M, K), 1700 + M, dt)
+        ws = [rand(ctx, (N, K), 1800 + l, dt, std=K ** -0.5) for l in range(layers)]
+        outs = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(layers)]
+        calls = [ctx.linear16_call(x, w, o) for w, o in zip(ws, outs)]
+        spin_up(ctx, calls)
+        us = time_loop(ctx, calls, iters)
+        us_graph = time_graph(ctx, calls, 4 * layers)
+        best = min(us, us_graph)
+        key = f"{label}_M{M}_{dname}"
+        entry = kernel_entry("linear16_skinny", nbytes, best,
+                             {"rows": M, "k": K, "n": N, "weight_sets": layers, "eager_us": round(us, 3),
+                              "graph_us": round(us_graph, 3)})
+        if (M, K, N, dname) == (8, 8960, 1536, "f16"):
+            entry["traffic"] = read_traffic("16-bit linear, 8 rows, [1536,8960] weights, fp16 (1.5B down)")
+        if baselines:
+            tcalls = [(lambda w=w: torch.nn.functional.linear(x, w)) for w in ws]
+            t_us = time_loop(ctx, tcalls, iters)
+            t_graph = time_graph(ctx, tcalls, 4 * layers)
+            tb = min(t_us, t_graph)
+            entry.update({"torch_linear_us": round(tb, 3), "torch_linear_GBps": round(nbytes / tb / 1e3, 1),
+                          "speedup": round(tb / best, 3)})
+        res[key] = entry
+        log(f"  linear16 {key}: {entry}")
+        del ws, outs, calls
+        torch.cuda.empty_cache()
+    return res
+
+
 def w8a16_kernel_name(M, N):
     """The kernel mi355_w8a16_linear_fwd runs for this shape (aligned inputs):
     the split-K weight-streaming kernel for decode rows and small grids, the
@@ -1192,6 +1267,15 @@ def bench_e2e(args):
     log(f"fused gate/up in {n_gu} MLPs")
     fused_gu = measure("after+fuse_residual+fuse_gate_up")
     graph_gu = graphed("after+fuse_residual+fuse_gate_up")
+    # ... and each FusedMLP's down projection on the HIP 16-bit linear for decode rows
+    n_down = 0
+    for m in model.modules():
+        if isinstance(m, pkg.FusedMLP) and m.down_hip_capable():
+            m.hip_down = True
+            n_down += 1
+    log(f"HIP down projection in {n_down} MLPs")
+    hip_down = measure("after+fuse_residual+fuse_gate_up+hip_down")
+    graph_hd = graphed("after+fuse_residual+fuse_gate_up+hip_down")
     rows = []
     for S in args.seq_lens:
         rows.append({"seq_len": S, "before_ttft_ms": round(before[S][0], 3), "after_ttft_ms": round(after[S][0], 3),
@@ -1204,13 +1288,16 @@ def bench_e2e(args):
         row["fuse_residual_decode_tok_s"] = round(fused_res[S][1], 2)
         row["fuse_gate_up_ttft_ms"] = round(fused_gu[S][0], 3)
         row["fuse_gate_up_decode_tok_s"] = round(fused_gu[S][1], 2)
+        row["hip_down_ttft_ms"] = round(hip_down[S][0], 3)
+        row["hip_down_decode_tok_s"] = round(hip_down[S][1], 2)
     print(json.dumps({"metric": "e2e TTFT / decode tok/s speedup from patch_model_with_fused_kernels",
                       "model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16, sdpa, batch 1",
                       "gen_len": args.gen_len, "trials": args.trials, "patched": counts, "results": rows,
-                      "fuse_gate_up_mlps": n_gu,
+                      "fuse_gate_up_mlps": n_gu, "hip_down_mlps": n_down,
                       "graphed_decode_tok_s": {"seq_len": 512, "unpatched": graph_before, "patched": graph_after,
                                                "patched_fuse_residual": graph_fr,
-                                               "patched_fuse_residual_fuse_gate_up": graph_gu}}),
+                                               "patched_fuse_residual_fuse_gate_up": graph_gu,
+                                               "patched_fuse_residual_fuse_gate_up_hip_down": graph_hd}}),
           flush=True)
 
 

@@ -1,7 +1,8 @@
 /*
  * mi355_fused.h -- C ABI of the MI355X (gfx950) fused RMSNorm and SiLU-and-mul
- * kernels, the fused gate/up projections, and the weight-only int8 (W8A16)
- * linear with its quantiser.
+ * kernels, the fused gate/up projections, the weight-only int8 (W8A16)
+ * linear with its quantiser, and the 16-bit linear of the MLP's down
+ * projection.
  *
  * The reference has no FFI: its boundary is a pair of Python launchers that
  * hand torch tensors to Triton kernels.  Each entry point below replaces one of
@@ -237,6 +238,38 @@ int mi355_gate_up_silu_w8a16_fwd(const void* x, const void* wq_gate, const void*
 int mi355_quantize_int8_fwd(const void* w, void* w_q, void* scale,
                             int64_t n, int64_t k, int64_t w_row_stride, int64_t q_row_stride,
                             int w_dtype, void* stream);
+
+/*
+ * 16-bit linear (nn.Linear's forward with fp16 / bf16 weights), per row m
+ * and output feature n:
+ *   acc[m,n] = sum_k x[m,k] * weight[n,k]     (fp32 accumulation, MFMA)
+ *   out[m,n] = acc[m,n] + bias[n]             (fp32, rounded once to out_dtype)
+ *
+ * Replaces the down projection of the reference's FusedMLP,
+ * `self.down_proj(activated)` (src/engine/fused_norm_activation_patch.py:64),
+ * an nn.Linear that torch runs on hipBLASLt.  At decode batch sizes that call
+ * streams the whole weight matrix for a few rows; rows <= 32 here read every
+ * weight byte once at HBM bandwidth on MFMA.  More rows run the LDS-tiled
+ * MFMA GEMM (32-row weight-streaming tiles on small grids).  The fp32 sums
+ * run in this library's own order, so results may differ from hipBLASLt's
+ * in the last output bit.
+ *
+ *   x       [rows, x_row_stride] of dtype (MI355_F16 or MI355_BF16).
+ *   weight  [n, w_row_stride] of dtype, nn.Linear's layout.
+ *   bias    [n] of bias_dtype, or NULL (then bias_dtype is ignored).
+ *   out     [rows, out_row_stride] of out_dtype = dtype or MI355_F32.
+ *   rows >= 0, k >= 1, n >= 0 (rows == 0 or n == 0 is a no-op); strides >= k
+ *   (x, weight) and >= n (out).  Any alignment and k are served; the fast
+ *   kernels need k and both input row strides multiples of 8 and 16-byte
+ *   aligned x and weight.  Limits: x_row_stride and w_row_stride < 2^22,
+ *   n < 2^31 - 256, rows <= 2097120.  out must not overlap the inputs.
+ *   Calls with the same shapes give identical bits (fixed summation order).
+ */
+int mi355_linear16_fwd(const void* x, const void* weight, const void* bias, void* out,
+                       int64_t rows, int64_t k, int64_t n,
+                       int64_t x_row_stride, int64_t w_row_stride, int64_t out_row_stride,
+                       int dtype, int bias_dtype, int out_dtype,
+                       void* stream);
 
 #ifdef __cplusplus
 }

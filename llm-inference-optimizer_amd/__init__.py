@@ -21,7 +21,10 @@ with ``FusedDecoderLayer`` / ``DECODER_LAYER_CLASS_NAMES``, which
 ``GraphedGreedyDecoder``, greedy decoding whose per-token step replays one
 captured HIP graph, and ``fused_gate_up_silu`` (gate / up projections +
 SiLU-and-mul in one kernel for decode batches), which
-``patch_model_with_fused_kernels(..., fuse_gate_up=True)`` lets FusedMLP use.
+``patch_model_with_fused_kernels(..., fuse_gate_up=True)`` lets FusedMLP use,
+and ``linear16`` (a 16-bit linear that streams the weights at HBM bandwidth
+for decode batches), which ``patch_model_with_fused_kernels(...,
+hip_down=True)`` lets FusedMLP use for its down projection.
 
 The reference's weight-only int8 stage sits beside it: ``w8a16_linear`` /
 ``w8a16_reference``, ``QuantizedLinearInt8`` and ``quantize_model_int8``
@@ -38,6 +41,7 @@ from .engine.graphed_decode import GraphedGreedyDecoder
 from .kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm, naive_rmsnorm_reference
 from .kernels.fused_gate_up_hip import GATE_UP_MAX_ROWS, fused_gate_up_silu, naive_gate_up_silu_reference
 from .kernels.fused_swiglu_hip import fused_silu_mul, naive_silu_mul_reference
+from .kernels.linear16_hip import LINEAR16_MAX_ROWS, linear16
 from .kernels.w8a16_matmul_hip import fused_gate_up_silu_w8a16, quantize_int8_weight, w8a16_linear, w8a16_reference
 from .quantization.int8 import QuantizedLinearInt8, quantize_model_int8
 
@@ -47,5 +51,5 @@ __all__ = [
     "fused_add_rmsnorm", "FusedDecoderLayer", "DECODER_LAYER_CLASS_NAMES", "GraphedGreedyDecoder",
     "fused_gate_up_silu", "naive_gate_up_silu_reference", "GATE_UP_MAX_ROWS",
     "w8a16_linear", "w8a16_reference", "quantize_int8_weight", "QuantizedLinearInt8", "quantize_model_int8",
-    "fused_gate_up_silu_w8a16",
+    "fused_gate_up_silu_w8a16", "linear16", "LINEAR16_MAX_ROWS",
 ]

@@ -26,7 +26,7 @@ DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTED_SYMBOLS = ("mi355_abi_version", "mi355_last_error", "mi355_rmsnorm_fwd", "mi355_add_rmsnorm_fwd",
                     "mi355_silu_mul_fwd", "mi355_gate_up_silu_fwd", "mi355_w8a16_linear_fwd",
-                    "mi355_quantize_int8_fwd", "mi355_gate_up_silu_w8a16_fwd")
+                    "mi355_quantize_int8_fwd", "mi355_gate_up_silu_w8a16_fwd", "mi355_linear16_fwd")
 
 
 class KernelLibraryMissing(RuntimeError):
@@ -80,6 +80,8 @@ def load() -> ctypes.CDLL:
         L.mi355_gate_up_silu_w8a16_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32,
                                                    i32, vp]
         L.mi355_gate_up_silu_w8a16_fwd.restype = i32
+        L.mi355_linear16_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, i32, vp]
+        L.mi355_linear16_fwd.restype = i32
         ver = L.mi355_abi_version()
         if ver != ABI_VERSION:
             raise KernelLibraryMissing(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
@@ -168,3 +170,11 @@ def quantize_int8_fwd(w_ptr: int, q_ptr: int, scale_ptr: int, n: int, k: int, w_
                       q_row_stride: int, w_dtype: int, stream: int) -> None:
     check("mi355_quantize_int8_fwd",
           load().mi355_quantize_int8_fwd(w_ptr, q_ptr, scale_ptr, n, k, w_row_stride, q_row_stride, w_dtype, stream))
+
+
+def linear16_fwd(x_ptr: int, w_ptr: int, bias_ptr: int | None, out_ptr: int, rows: int, k: int, n: int,
+                 x_row_stride: int, w_row_stride: int, out_row_stride: int, dtype: int, bias_dtype: int,
+                 out_dtype: int, stream: int) -> None:
+    check("mi355_linear16_fwd",
+          load().mi355_linear16_fwd(x_ptr, w_ptr, bias_ptr, out_ptr, rows, k, n, x_row_stride, w_row_stride,
+                                    out_row_stride, dtype, bias_dtype, out_dtype, stream))

@@ -1,7 +1,7 @@
 // C ABI entry points (include/mi355_fused.h): argument validation, the
 // per-thread error message and the per-device CU-count cache.  Kernels and
-// their launchers live in rmsnorm.hip, silu_mul.hip, gate_up_silu.hip and
-// w8a16.hip.
+// their launchers live in rmsnorm.hip, silu_mul.hip, gate_up_silu.hip,
+// w8a16.hip and linear16.hip.
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -28,6 +28,8 @@ int w8a16_launch(const void* x, const void* q, const void* scale, const void* bi
                  int out_dtype, hipStream_t stream);
 int quantize_int8_launch(const void* w, void* q, void* scale, int64_t n, int k, int64_t ws, int64_t qs, int w_dtype,
                          hipStream_t stream);
+int linear16_launch(const void* x, const void* w, const void* bias, void* out, int rows, int k, int n, int64_t xs,
+                    int64_t ws, int64_t os, int dtype, int bias_dtype, int out_dtype, hipStream_t stream);
 int gate_up_silu_w8a16_launch(const void* x, const void* qg, const void* qu, const void* sg, const void* su, void* out,
                               int rows, int k, int n, int64_t xs, int64_t qs, int64_t os, int x_dtype,
                               int scale_dtype, int out_dtype, hipStream_t stream);
@@ -377,4 +379,55 @@ MI355_EXPORT int mi355_quantize_int8_fwd(const void* w, void* w_q, void* scale, 
   }
   return mi355::quantize_int8_launch(w, w_q, scale, n, static_cast<int>(k), w_row_stride, q_row_stride, w_dtype,
                                      static_cast<hipStream_t>(stream));
+}
+
+MI355_EXPORT int mi355_linear16_fwd(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+                                    int64_t k, int64_t n, int64_t x_row_stride, int64_t w_row_stride,
+                                    int64_t out_row_stride, int dtype, int bias_dtype, int out_dtype, void* stream) {
+  static const char* fn = "mi355_linear16_fwd";
+  mi355::g_error[0] = '\0';
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype) || (bias != nullptr && !valid_dtype(bias_dtype))) {
+    set_error("%s: unknown dtype code (in=%d, bias=%d, out=%d)", fn, dtype, bias_dtype, out_dtype);
+    return MI355_ERR_INVALID;
+  }
+  if (dtype == MI355_F32) {
+    set_error("%s: x and weight must be fp16 or bf16 (MFMA operands)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (out_dtype != dtype && out_dtype != MI355_F32) {
+    set_error("%s: out dtype must equal the input dtype or be fp32 (in=%d, out=%d)", fn, dtype, out_dtype);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows < 0 || n < 0 || k < 1) {
+    set_error("%s: need rows >= 0, n >= 0, k >= 1 (got %lld, %lld, %lld)", fn, static_cast<long long>(rows),
+              static_cast<long long>(n), static_cast<long long>(k));
+    return MI355_ERR_INVALID;
+  }
+  if (x_row_stride < k || w_row_stride < k || out_row_stride < n) {
+    set_error("%s: row strides must be >= k (x, weight) and >= n (out)", fn);
+    return MI355_ERR_INVALID;
+  }
+  if (rows == 0 || n == 0) return MI355_OK;
+  if (x == nullptr || weight == nullptr || out == nullptr) {
+    set_error("%s: null pointer", fn);
+    return MI355_ERR_INVALID;
+  }
+  // Buffer descriptors span at most 256 rows of x or of the weights (< 2^32
+  // bytes); grids hold ceil(n / 8) x ceil(rows / 32) workgroups or more.
+  if (x_row_stride >= (int64_t{1} << 22) || w_row_stride >= (int64_t{1} << 22) || n > 0x7fffffff - 256 ||
+      rows > int64_t{65535} * 32) {
+    set_error("%s: size beyond the kernel's limits (row strides < 2^22, n < 2^31 - 256, rows <= 2097120)", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (n * ((rows + 3) / 4) > int64_t{0x7fffffff} * 4) {
+    set_error("%s: n * rows too large for one launch", fn);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  if (rows - 1 > (INT64_MAX - n) / out_row_stride) {
+    set_error("%s: rows * out_row_stride overflows int64", fn);
+    return MI355_ERR_INVALID;
+  }
+  return mi355::linear16_launch(x, weight, bias, out, static_cast<int>(rows), static_cast<int>(k),
+                                static_cast<int>(n), x_row_stride, w_row_stride, out_row_stride, dtype, bias_dtype,
+                                out_dtype, static_cast<hipStream_t>(stream));
 }

@@ -1,9 +1,10 @@
 // LDS-tiled MFMA GEMM core for gfx950, shared by the prefill-size launchers of
-// the W8A16 linear (w8a16.hip) and of the gate/up projections fused with
-// SiLU-and-mul (gate_up_silu.hip):
+// the W8A16 linear (w8a16.hip), of the gate/up projections fused with
+// SiLU-and-mul (gate_up_silu.hip) and of the 16-bit linear (linear16.hip):
 //
 //   acc[m, n] = sum_k x[m, k] * b[n, k]        (both operands K-contiguous)
 //   EPI_W8    out[m, n] = round(acc * scale[n] + bias[n])     b = int8 weights
+//   EPI_LINEAR   out[m, n] = round(acc + bias[n])             b of x's 16-bit type
 //   EPI_SILU  out[m, n] = round(silu(acc_gate) * acc_up)      two 16-bit b
 //   EPI_SILU_W8  out[m, n] = round(silu(acc_gate * scale[n]) * (acc_up * scale1[n]))   two int8 b
 //
@@ -79,7 +80,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kOob = 0xfffffff0u;  // past every descriptor the launchers admit (< 2^31 bytes)
 
-enum { EPI_W8 = 0, EPI_SILU = 1, EPI_SILU_W8 = 2 };
+enum { EPI_W8 = 0, EPI_SILU = 1, EPI_SILU_W8 = 2, EPI_LINEAR = 3 };
 enum { B_16 = 0, B_I8 = 1 };
 
 template <typename T> __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
@@ -140,7 +141,7 @@ struct Params {
   const void* b0;     // [n, bs]: int8 weights (EPI_W8) or w_gate (EPI_SILU)
   const void* b1;     // [n, bs]: w_up (EPI_SILU), else unused
   const void* scale;   // [n] of sdt (EPI_W8; gate scale for EPI_SILU_W8)
-  const void* bias;    // [n] of bdt, or null (EPI_W8)
+  const void* bias;    // [n] of bdt, or null (EPI_W8, EPI_LINEAR)
   const void* scale1;  // [n] of sdt: up scale (EPI_SILU_W8)
   void* out;          // [rows, os] of TO
   int rows, k, n;
@@ -157,7 +158,7 @@ struct Cfg {
   static constexpr bool I8 = BK == B_I8;
   static constexpr int NW = WGM * WGN, NT = 64 * NW;
   static constexpr int BM = 32 * FM * WGM, BN = 32 * FN * WGN;
-  static constexpr int NB = EPI == EPI_W8 ? 1 : 2;  // B matrices
+  static constexpr int NB = (EPI == EPI_W8 || EPI == EPI_LINEAR) ? 1 : 2;  // B matrices
   static constexpr int A_BYTES = BM * 128;             // 64 columns of 16-bit x per row
   static constexpr int B_ROW = I8 ? 64 : 128;          // bytes per B row per step in LDS
   static constexpr int B_BYTES = BN * B_ROW;
@@ -442,7 +443,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       const int n = n0 + nl;
       const bool full4 = nl + 4 <= nrows_b;
       float sc[4] = {1.f, 1.f, 1.f, 1.f}, bz[4] = {0.f, 0.f, 0.f, 0.f};  // EPI_SILU_W8: bz = up scale
-      if constexpr (EPI != EPI_SILU) {
+      if constexpr (EPI == EPI_LINEAR) {
+        if (p.bdt >= 0) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (nl + e < nrows_b) bz[e] = load_dyn(p.bias, n + e, p.bdt);
+          }
+        }
+      } else if constexpr (EPI != EPI_SILU) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if (nl + e < nrows_b) {
@@ -464,6 +472,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
         for (int e = 0; e < 4; ++e) {
           if constexpr (EPI == EPI_W8) {
             v[e] = p.bdt >= 0 ? __builtin_fmaf(acc[0][i][j][4 * g + e], sc[e], bz[e]) : acc[0][i][j][4 * g + e] * sc[e];
+          } else if constexpr (EPI == EPI_LINEAR) {
+            v[e] = p.bdt >= 0 ? acc[0][i][j][4 * g + e] + bz[e] : acc[0][i][j][4 * g + e];
           } else if constexpr (EPI == EPI_SILU) {
             v[e] = silu_mul_f32(acc[0][i][j][4 * g + e], acc[NB - 1][i][j][4 * g + e]);
           } else {

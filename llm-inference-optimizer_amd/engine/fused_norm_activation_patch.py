@@ -29,7 +29,12 @@ default) lets each FusedMLP run its gate / up projections and the
 SiLU-and-mul in one kernel (``fused_gate_up_silu``: weight streaming for
 decode batches, a tiled MFMA GEMM for prefill); the projections are then not
 rounded before the activation, which changes results by that rounding.  The
-count appears as ``"gate_up"``.
+count appears as ``"gate_up"``.  ``hip_down=True`` (off by default) runs each
+FusedMLP's down projection on the HIP 16-bit linear (``linear16``: weight
+streaming on MFMA) for inputs of at most ``LINEAR16_MAX_ROWS`` rows, where
+torch's linear is far from HBM bandwidth; its fp32 sums run in another order
+than hipBLASLt's, so outputs may differ in the last bit.  The count appears as
+``"down"``.
 """
 from __future__ import annotations
 
@@ -38,6 +43,7 @@ import torch
 from ..kernels.fused_rmsnorm_hip import fused_add_rmsnorm, fused_rmsnorm
 from ..kernels.fused_gate_up_hip import fused_gate_up_silu
 from ..kernels.fused_swiglu_hip import fused_silu_mul
+from ..kernels.linear16_hip import LINEAR16_MAX_ROWS, linear16
 from ..kernels.w8a16_matmul_hip import fused_gate_up_silu_w8a16
 from ..quantization.int8 import QuantizedLinearInt8
 
@@ -79,14 +85,20 @@ class FusedMLP(torch.nn.Module):
     ``fused_gate_up_silu_w8a16``: gate, up and the activation in one kernel.
     The projection kind is checked at each call, so a model quantised after
     patching switches to the int8 kernel.  Other inputs take the reference
-    path."""
+    path.
 
-    def __init__(self, orig_module: torch.nn.Module, fuse_gate_up: bool = False):
+    With ``hip_down=True``, a down projection that is a plain ``nn.Linear``
+    of the activation's dtype (fp16 / bf16) runs on ``linear16`` for inputs
+    of at most ``LINEAR16_MAX_ROWS`` rows (decode steps); larger inputs, and
+    other projection kinds, call the module."""
+
+    def __init__(self, orig_module: torch.nn.Module, fuse_gate_up: bool = False, hip_down: bool = False):
         super().__init__()
         self.gate_proj = orig_module.gate_proj
         self.up_proj = orig_module.up_proj
         self.down_proj = orig_module.down_proj
         self.fuse_gate_up = bool(fuse_gate_up) and self.gate_up_fusable()
+        self.hip_down = bool(hip_down) and self.down_hip_capable()
 
     def gate_up_kind(self) -> str | None:
         """Which fused gate/up kernel can read the projections: ``"16bit"``
@@ -105,18 +117,33 @@ class FusedMLP(torch.nn.Module):
     def gate_up_fusable(self) -> bool:
         return self.gate_up_kind() is not None
 
+    def down_hip_capable(self) -> bool:
+        """Whether ``linear16`` can run the down projection: a plain
+        ``nn.Linear`` (bias allowed)."""
+        return type(self.down_proj) is torch.nn.Linear
+
+    def down(self, activated: torch.Tensor) -> torch.Tensor:
+        """The down projection: ``linear16`` for decode-sized 16-bit inputs
+        when ``hip_down`` is on, else the module itself."""
+        d = self.down_proj
+        if (self.hip_down and type(d) is torch.nn.Linear and activated.dtype == d.weight.dtype
+                and activated.dtype in (torch.float16, torch.bfloat16)
+                and activated.numel() <= LINEAR16_MAX_ROWS * activated.shape[-1]):
+            return linear16(activated, d.weight, d.bias)
+        return d(activated)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.fuse_gate_up and x.dtype in (torch.float16, torch.bfloat16):
             kind = self.gate_up_kind()
             g, u = self.gate_proj, self.up_proj
             if kind == "16bit" and x.dtype == g.weight.dtype == u.weight.dtype:
-                return self.down_proj(fused_gate_up_silu(x, g.weight, u.weight))
+                return self.down(fused_gate_up_silu(x, g.weight, u.weight))
             if kind == "int8":
-                return self.down_proj(fused_gate_up_silu_w8a16(x, g.weight_q, g.scale, u.weight_q, u.scale))
+                return self.down(fused_gate_up_silu_w8a16(x, g.weight_q, g.scale, u.weight_q, u.scale))
         gate = self.gate_proj(x)
         up = self.up_proj(x)
         activated = fused_silu_mul(gate, up)
-        return self.down_proj(activated)
+        return self.down(activated)
 
 
 class FusedDecoderLayer(torch.nn.Module):
@@ -159,7 +186,7 @@ class FusedDecoderLayer(torch.nn.Module):
 
 def patch_model_with_fused_kernels(model: torch.nn.Module, patch_norm: bool = True,
                                    patch_mlp: bool = True, fuse_residual: bool = False,
-                                   fuse_gate_up: bool = False) -> dict:
+                                   fuse_gate_up: bool = False, hip_down: bool = False) -> dict:
     """Replace matching RMSNorm and/or MLP child modules in place (setattr on
     the parent).  Returns ``{"rmsnorm": count, "mlp": count}``.
     ``patch_norm`` / ``patch_mlp`` enable each kernel independently.
@@ -167,10 +194,13 @@ def patch_model_with_fused_kernels(model: torch.nn.Module, patch_norm: bool = Tr
     ``FusedDecoderLayer`` and adds ``"add_rmsnorm": count`` to the result.
     ``fuse_gate_up`` builds each FusedMLP with ``fuse_gate_up=True`` and adds
     ``"gate_up": count`` (the MLPs whose projections the fused kernel can
-    read)."""
+    read).  ``hip_down`` builds each FusedMLP with ``hip_down=True`` and adds
+    ``"down": count`` (the MLPs whose down projection ``linear16`` can run)."""
     counts = {"rmsnorm": 0, "mlp": 0}
     if fuse_gate_up:
         counts["gate_up"] = 0
+    if hip_down:
+        counts["down"] = 0
     for parent in list(model.modules()):
         for child_name, child in list(parent.named_children()):
             cls_name = child.__class__.__name__
@@ -180,11 +210,13 @@ def patch_model_with_fused_kernels(model: torch.nn.Module, patch_norm: bool = Tr
                 counts["rmsnorm"] += 1
             elif patch_mlp and cls_name in MLP_CLASS_NAMES and all(
                     hasattr(child, attr) for attr in ("gate_proj", "up_proj", "down_proj")):
-                fused = FusedMLP(child, fuse_gate_up=fuse_gate_up)
+                fused = FusedMLP(child, fuse_gate_up=fuse_gate_up, hip_down=hip_down)
                 setattr(parent, child_name, fused)
                 counts["mlp"] += 1
                 if fused.fuse_gate_up:
                     counts["gate_up"] += 1
+                if fused.hip_down:
+                    counts["down"] += 1
     if fuse_residual:
         counts["add_rmsnorm"] = 0
         for parent in list(model.modules()):

@@ -34,6 +34,11 @@
  * reference (:137-149); oracle_quantize_int8 restates the quantiser that
  * produces the int8 weights (src/quantization/int8.py:45-50).
  *
+ * oracle_linear16 restates the MLP's down projection, nn.Linear with 16-bit
+ * weights (`self.down_proj(activated)`, src/engine/fused_norm_activation_
+ * patch.py:64): the dot product of x with the weight row in fp32 (formed
+ * order-free from the exact fp64 sum), the bias added in fp32, one rounding.
+ *
  * Sum of squares: the reference reduces with tl.sum in fp32 in an order the
  * Triton backend picks (:43).  The oracle accumulates the exact squares in
  * fp64 and rounds the sum to fp32 once, i.e. the order-free fp32 sum; any
@@ -407,6 +412,55 @@ int oracle_w8a16_linear(const void* x, const int8_t* q, const void* scale, const
       } else {
         v = has_bias ? fmaf((float)acc, sc, bs) : (float)acc * sc;
       }
+      store_f(out, o, odt, v);
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------- 16-bit linear */
+
+/* planted mistakes, 16-bit linear */
+enum {
+  ORACLE_MUT_L16_TRANSPOSE = 1, /* read w as [k, n] instead of [n, k] */
+  ORACLE_MUT_L16_NO_BIAS = 2,   /* drop the bias */
+  ORACLE_MUT_L16_DROP_TAIL = 3, /* skip the last 8 columns of k */
+  ORACLE_MUT_L16_ROW_SHIFT = 4, /* pair output row m with x row (m + 1) % rows */
+  ORACLE_MUT_L16_BIAS_LATE = 5  /* round the dot product to odt before adding the bias */
+};
+
+/*
+ * out[m, j] for x [rows, k] and w [n, k] (both dt storage), bias [n] (bdt, or
+ * bdt < 0 for none):
+ *   acc = (float)sum_c x[m,c] * w[j,c]   (exact fp64 sum of exact products,
+ *                                         rounded once: order-free fp32)
+ *   out = round_odt(acc + bias)           (fp32 add)  or  round_odt(acc)
+ * Optional fp64 outputs (NULL to skip): out64 = sum x*w + bias,
+ * absacc = sum |x*w| (scale of the fp32 accumulation error).
+ * Returns 0, or -1 on a bad argument.
+ */
+int oracle_linear16(const void* x, const void* w, const void* bias, void* out, double* out64, double* absacc,
+                    int64_t rows, int64_t k, int64_t n, int dt, int bdt, int odt, int mutate) {
+  if (!valid_dt(dt) || !valid_dt(odt) || (bdt >= 0 && !valid_dt(bdt)) || rows < 0 || k < 1 || n < 1) return -1;
+  const int has_bias = bdt >= 0 && bias != NULL && mutate != ORACLE_MUT_L16_NO_BIAS;
+  const int64_t kk = (mutate == ORACLE_MUT_L16_DROP_TAIL && k > 8) ? k - 8 : k;
+  for (int64_t m = 0; m < rows; ++m) {
+    const int64_t xm = (mutate == ORACLE_MUT_L16_ROW_SHIFT) ? (m + 1) % rows : m;
+    for (int64_t j = 0; j < n; ++j) {
+      const float bs = has_bias ? load_f(bias, j, bdt) : 0.0f;
+      double acc = 0.0, aabs = 0.0;
+      for (int64_t c = 0; c < kk; ++c) {
+        const int64_t wi = (mutate == ORACLE_MUT_L16_TRANSPOSE) ? c * n + j : j * k + c;
+        const double p = (double)load_f(x, xm * k + c, dt) * (double)load_f(w, wi, dt);
+        acc += p;
+        aabs += fabs(p);
+      }
+      const int64_t o = m * n + j;
+      if (out64) out64[o] = acc + (double)bs;
+      if (absacc) absacc[o] = aabs;
+      float v = (float)acc;
+      if (mutate == ORACLE_MUT_L16_BIAS_LATE) v = round_to(v, odt);
+      if (has_bias) v = v + bs;
       store_f(out, o, odt, v);
     }
   }

@@ -29,6 +29,10 @@ Contents
   reference (:137-149) -- with the fp64 value and sum |x * q|;
 * :func:`quantize_int8`: the per-output-channel int8 quantiser
   (src/quantization/int8.py:45-50);
+* :func:`linear16`: the MLP's down projection, nn.Linear with 16-bit weights
+  (src/engine/fused_norm_activation_patch.py:64): fp32 dot product (the
+  order-free fp32 value of the exact sum), the bias in fp32, one rounding,
+  with the fp64 value and sum |x * w|;
 * :func:`naive_rmsnorm_torch` / :func:`naive_silu_mul_torch`: the reference's
   naive PyTorch path restated as the same torch op sequence, which bench.py
   times on the host cores as the CPU baseline.
@@ -67,6 +71,7 @@ GU_MODE = {"fused": 0, "unfused": 1}
 W8_MODE = {"kernel": 0, "dequant": 1}
 MUT_W8 = {"transpose": 1, "unsigned": 2, "bias_first": 3, "no_bias": 4, "scale_shift": 5}
 MUT_Q8 = {"trunc": 1, "half_up": 2, "by_128": 3, "no_clamp": 4}
+MUT_L16 = {"transpose": 1, "no_bias": 2, "drop_tail": 3, "row_shift": 4, "bias_late": 5}
 
 _lib = None
 
@@ -109,6 +114,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_w8a16_linear.restype = i32
         L.oracle_quantize_int8.argtypes = [vp, vp, vp, i64, i64, i32, i32]
         L.oracle_quantize_int8.restype = i32
+        L.oracle_linear16.argtypes = [vp] * 6 + [i64, i64, i64, i32, i32, i32, i32]
+        L.oracle_linear16.restype = i32
         for name in ("oracle_f32_to_f16_n", "oracle_f16_to_f32_n", "oracle_f32_to_bf16_n", "oracle_bf16_to_f32_n"):
             getattr(L, name).argtypes = [vp, vp, i64]
             getattr(L, name).restype = None
@@ -317,6 +324,34 @@ def gate_up_silu_w8a16(x: np.ndarray, qg: np.ndarray, sg: np.ndarray, qu: np.nda
     suv = np.abs(to_f32(_arr(su, sdt), sdt).astype(np.float64))
     return {"out": out, "out64": g64 / (1.0 + np.exp(-g64)) * u64, "g": g64, "u": u64,
             "gabs": g["absacc"] * sgv[None, :], "uabs": u["absacc"] * suv[None, :]}
+
+
+def linear16(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None, *, dt: str, bdt: str | None = None,
+             odt: str | None = None, mutate: str | None = None) -> dict:
+    """x: [rows, k], w: [n, k] (dt storage), bias: [n] (bdt storage) or None.
+    Returns a dict with ``out`` ([rows, n], odt storage), ``out64`` (fp64) and
+    ``absacc`` (sum_k |x * w|, fp64)."""
+    x = _arr(x, dt)
+    w = _arr(w, dt)
+    if x.ndim != 2 or w.ndim != 2 or w.shape[1] != x.shape[1]:
+        raise ValueError(f"bad shapes x={x.shape} w={w.shape}")
+    rows, k = x.shape
+    n = w.shape[0]
+    if bias is not None:
+        bdt = bdt or dt
+        bias = _arr(bias, bdt)
+        if bias.shape != (n,):
+            raise ValueError(f"bias must be [{n}], got {bias.shape}")
+    odt = odt or dt
+    res = {"out": np.empty((rows, n), dtype=_np_dtype(odt)), "out64": np.empty((rows, n), np.float64),
+           "absacc": np.empty((rows, n), np.float64)}
+    mut = 0 if mutate is None else MUT_L16[mutate]
+    st = lib().oracle_linear16(_ptr(x), _ptr(w), _ptr(bias) if bias is not None else None, _ptr(res["out"]),
+                               _ptr(res["out64"]), _ptr(res["absacc"]), rows, k, n, DT_CODE[dt],
+                               DT_CODE[bdt] if bias is not None else -1, DT_CODE[odt], mut)
+    if st != 0:
+        raise ValueError("oracle_linear16 rejected its arguments")
+    return res
 
 
 def quantize_int8(w: np.ndarray, *, wdt: str, mutate: str | None = None) -> tuple[np.ndarray, np.ndarray]:
