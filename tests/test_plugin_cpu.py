@@ -131,3 +131,41 @@ def test_fuse_gate_up_skips_projections_the_kernel_cannot_read(pkg):
     mlp1.up_proj = QuantLinear(64, 128, bias=False)
     counts = pkg.patch_model_with_fused_kernels(model, fuse_gate_up=True)
     assert counts["mlp"] == 2 and counts["gate_up"] == 0
+
+
+def test_hip_down_is_opt_in_and_counted(pkg):
+    model = _qwen2(layers=4)
+    counts = pkg.patch_model_with_fused_kernels(model, hip_down=True)
+    assert counts == {"rmsnorm": 9, "mlp": 4, "down": 4}
+    assert all(layer.mlp.hip_down for layer in model.model.layers)
+    both = _qwen2(layers=2)
+    assert pkg.patch_model_with_fused_kernels(both, fuse_gate_up=True, hip_down=True) == {
+        "rmsnorm": 5, "mlp": 2, "gate_up": 2, "down": 2}
+    plain = _qwen2(layers=2)
+    assert pkg.patch_model_with_fused_kernels(plain) == {"rmsnorm": 5, "mlp": 2}
+    assert not any(layer.mlp.hip_down for layer in plain.model.layers)
+
+
+def test_hip_down_skips_down_projections_the_kernel_cannot_run(pkg):
+    model = _qwen2(layers=2)
+
+    class QuantLinear(torch.nn.Linear):
+        pass
+
+    model.model.layers[0].mlp.down_proj = QuantLinear(128, 64, bias=False)
+    counts = pkg.patch_model_with_fused_kernels(model, hip_down=True)
+    assert counts["mlp"] == 2 and counts["down"] == 1
+    assert not model.model.layers[0].mlp.hip_down and model.model.layers[1].mlp.hip_down
+
+
+def test_hip_down_leaves_fp32_and_large_inputs_to_the_module(pkg):
+    """fp32 activations and inputs above LINEAR16_MAX_ROWS rows call the
+    down_proj module itself (so they run on the CPU here, no kernel)."""
+    model = _qwen2(layers=1)
+    pkg.patch_model_with_fused_kernels(model, hip_down=True)
+    mlp = model.model.layers[0].mlp
+    act = torch.randn(3, 128)
+    assert torch.equal(mlp.down(act), mlp.down_proj(act))
+    big = torch.randn(pkg.LINEAR16_MAX_ROWS + 1, 128).half()
+    mlp.down_proj.half()
+    assert torch.equal(mlp.down(big), mlp.down_proj(big))
