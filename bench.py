@@ -483,13 +483,12 @@ def rocprof_summary(dirs):
             traffic[label] = {"traffic_bytes": round(tb), "algorithmic_bytes": nbytes,
                               "fetch_kib": round(fk, 1), "write_kib": round(wk, 1)}
         out.append("")
-        occ_names = ("SQ_WAVES", "OccupancyPercent", "MeanOccupancyPerCU")
+        occ_names = tuple(sorted({k[2] for k in pmc} - {"FETCH_SIZE", "WRITE_SIZE"}))
         occ_keys = sorted({(k[0], k[1]) for k in pmc if k[2] in occ_names})
         if occ_keys:
-            out.append("### Occupancy (per dispatch, averaged over dispatches)\n")
-            out.append("| kernel | dispatches | SQ_WAVES | OccupancyPercent (% of 32 waves per CU) | "
-                       "MeanOccupancyPerCU (waves) |")
-            out.append("|---|---|---|---|---|")
+            out.append("### Other counters and derived metrics (per dispatch, averaged over dispatches)\n")
+            out.append("| kernel | dispatches | " + " | ".join(occ_names) + " |")
+            out.append("|---|---|" + "---|" * len(occ_names))
             for frag, grid in occ_keys:
                 cells = []
                 for c in occ_names:
