@@ -59,3 +59,26 @@ def test_patched_graph_decode_has_fused_kernels_in_graph(pkg, cuda, model):
     counts = pkg.patch_model_with_fused_kernels(model)
     assert isinstance(model.model.layers[0].mlp, pkg.FusedMLP)
     assert counts["rmsnorm"] in (0, 57)
+
+
+def test_graph_decode_with_every_fused_kernel_matches_eager(pkg, cuda):
+    """A model patched with every opt-in kernel (residual add + RMSNorm,
+    gate/up + SiLU-and-mul, the HIP down projection) decodes the same tokens
+    with the step replayed as one HIP graph as it does eagerly."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    cfg = Qwen2Config(vocab_size=4096, hidden_size=1536, intermediate_size=8960, num_hidden_layers=4,
+                      num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=4096,
+                      rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True, attn_implementation="sdpa")
+    torch.manual_seed(5)
+    with torch.device(cuda):
+        m = Qwen2ForCausalLM(cfg)
+    m = m.half().eval()
+    counts = pkg.patch_model_with_fused_kernels(m, fuse_residual=True, fuse_gate_up=True, hip_down=True)
+    assert counts == {"rmsnorm": 9, "mlp": 4, "gate_up": 4, "down": 4, "add_rmsnorm": 4}
+    ids = _prompt(cuda, cfg.vocab_size)
+    eager = pkg.GraphedGreedyDecoder(m, B, S + NEW + 8, use_graph=False).generate(ids, NEW)
+    dec = pkg.GraphedGreedyDecoder(m, B, S + NEW + 8)
+    graphed = dec.generate(ids, NEW)
+    assert dec._graph is not None
+    assert torch.equal(graphed, eager)
+    assert torch.equal(dec.generate(ids, NEW), graphed)
