@@ -197,9 +197,24 @@ constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
 // tracks these LDS writes nor drains every load in flight before each LDS
 // read: the kernel orders them itself, with vmcnt waits before the barrier
 // that publishes a stage (vmcnt falls as the data reaches LDS, in issue order).
+// NT = true adds the non-temporal cache hint (the line is inserted for early
+// eviction).  Off for both operands: on x (A), on the weights (B) and on both
+// it measured slower on MI355X at every prefill shape of the gate/up, W8A16
+// and 16-bit-linear launchers (1.01x - 1.69x the time), the re-reads of both
+// operands by neighbouring tiles being L2 hits worth keeping.
+#ifndef MI355_DMA_A_NT
+#define MI355_DMA_A_NT 0
+#endif
+#ifndef MI355_DMA_B_NT
+#define MI355_DMA_B_NT 0
+#endif
+template <bool NT = false>
 __device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+  if constexpr (NT)
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+  else
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
 }
 // LDS byte address of stage I (the cast of the LDS variable itself folds to a constant).
 template <int I, int SZ> __device__ __forceinline__ uint32_t stage_addr() {
@@ -295,8 +310,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     for (int j = 0; j < C::AI; ++j) {
       const uint32_t kb = static_cast<uint32_t>(kt * 64 * sizeof(TB));
       const uint32_t dst = st + 1024u * (NW * j + wave);
-      if (full) dma16(rx, a_goff[j], kb, dst);
-      else dma16(rx, kt * 64 + a_col[j] < p.k ? a_goff[j] + kb : kOob, 0, dst);
+      if (full) dma16<MI355_DMA_A_NT != 0>(rx, a_goff[j], kb, dst);
+      else dma16<MI355_DMA_A_NT != 0>(rx, kt * 64 + a_col[j] < p.k ? a_goff[j] + kb : kOob, 0, dst);
     }
 #pragma unroll
     for (int bi = 0; bi < NB; ++bi) {
@@ -304,8 +319,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       for (int j = 0; j < C::BI; ++j) {
         const uint32_t kb = static_cast<uint32_t>(kt * 64 * EB);
         const uint32_t dst = st + C::A_BYTES + bi * C::B_BYTES + 1024u * (NW * j + wave);
-        if (full) dma16(rb[bi], b_goff[j], kb, dst);
-        else dma16(rb[bi], kt * 64 + b_col[j] < p.k ? b_goff[j] + kb : kOob, 0, dst);
+        if (full) dma16<MI355_DMA_B_NT != 0>(rb[bi], b_goff[j], kb, dst);
+        else dma16<MI355_DMA_B_NT != 0>(rb[bi], kt * 64 + b_col[j] < p.k ? b_goff[j] + kb : kOob, 0, dst);
       }
     }
   };
