@@ -69,7 +69,7 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "ceilings", "linear16", "gate-up",
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill"],
                    default=None,
@@ -113,6 +113,8 @@ class Ctx:
             self.probe.mi355_probe_add2.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                     ctypes.c_int64, ctypes.c_void_p]
             self.probe.mi355_probe_add2.restype = ctypes.c_int
+            self.probe.mi355_probe_empty.argtypes = [ctypes.c_void_p]
+            self.probe.mi355_probe_empty.restype = ctypes.c_int
 
     def rms_call(self, x, w, y, eps=1e-6):
         M, N = x.shape
@@ -200,6 +202,14 @@ class Ctx:
         def call():
             if f(*args, self.stream):
                 raise RuntimeError("probe copy failed")
+        return call
+
+    def empty_call(self):
+        f = self.probe.mi355_probe_empty
+
+        def call():
+            if f(self.stream):
+                raise RuntimeError("probe empty kernel failed")
         return call
 
     def add2_call(self, a, b, dst):
@@ -662,6 +672,10 @@ def run_only(ctx, args, sets):
         log(json.dumps(d))
     elif args.only == "copy":
         log(json.dumps(bench_copy(ctx)))
+    elif args.only == "decode":
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_decode(ctx)))
     elif args.only == "ceilings":
         del sets
         torch.cuda.empty_cache()
@@ -824,6 +838,21 @@ def bench_decode(ctx, layers=28):
             "rows_per_s_rmsnorm": round(M / (rms_dev * 1e-6)),
         }
         log(f"  decode M={M}: {res[f'M={M}']}")
+    if ctx.probe is not None:
+        # the floor under every decode figure: an empty kernel, and the probe
+        # copy of one 1536-wide fp16 row (one HBM round trip), back to back and
+        # as nodes of a hipGraph of the same length as the 28-layer graph
+        empty = [ctx.empty_call()]
+        src = torch.empty(1536 * 2, dtype=torch.uint8, device=ctx.dev)
+        dst = torch.empty_like(src)
+        row = [ctx.copy_call(src, dst)]
+        res["floor"] = {
+            "empty_kernel_eager_us": round(time_loop(ctx, empty, 2000), 3),
+            "empty_kernel_graph_node_us": round(time_graph(ctx, empty, 3 * layers, replays=50), 3),
+            "row_copy_eager_us": round(time_loop(ctx, row, 2000), 3),
+            "row_copy_graph_node_us": round(time_graph(ctx, row, 3 * layers, replays=50), 3),
+        }
+        log(f"  decode floor: {res['floor']}")
     return res
 
 

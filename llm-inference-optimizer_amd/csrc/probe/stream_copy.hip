@@ -3,7 +3,8 @@
 // 256-lane workgroups, one workgroup per 4 KiB, buffer descriptors per
 // workgroup, non-temporal loads and stores), and the same stream with two
 // inputs and one output (out = a + b as 32-bit integers), the access mix of
-// SiLU-and-mul without its arithmetic.  bench.py uses them
+// SiLU-and-mul without its arithmetic, and an empty kernel (the fixed cost of
+// a launch, eager and as a hipGraph node).  bench.py uses them
 // (libmi355_probe.so) to report the device's achievable HBM bandwidth for
 // each access mix, at 1 GiB and at the byte counts of the benchmarked
 // kernels; rocprofv3 runs use the copy to calibrate FETCH_SIZE / WRITE_SIZE
@@ -40,6 +41,8 @@ __global__ __launch_bounds__(kBlock) void stream_add2(const char* __restrict__ a
   const u32x4 vb = __builtin_amdgcn_raw_buffer_load_b128(rb, threadIdx.x * 16u, 0, 2);
   __builtin_amdgcn_raw_buffer_store_b128(va + vb, rd, threadIdx.x * 16u, 0, 2);
 }
+
+__global__ __launch_bounds__(64) void empty_kernel() {}
 }  // namespace
 
 // Copies `bytes` (a multiple of 16; both pointers 16-byte aligned) on
@@ -73,5 +76,12 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_add2(const voi
   hipLaunchKernelGGL(stream_add2, dim3(static_cast<unsigned>(grid)), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), static_cast<const char*>(a), static_cast<const char*>(b),
                      static_cast<char*>(dst), bytes);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// One workgroup of one wave that does nothing, on `stream`.  Returns 0 or -3
+// on a launch error.
+extern "C" __attribute__((visibility("default"))) int mi355_probe_empty(void* stream) {
+  hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream));
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
