@@ -43,6 +43,7 @@ class KernelError(RuntimeError):
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_ext = None
 
 
 def load() -> ctypes.CDLL:
@@ -87,6 +88,30 @@ def load() -> ctypes.CDLL:
             raise KernelLibraryMissing(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
         _lib = L
     return _lib
+
+
+def ext():
+    """The host-side launchers (``_mi355_torch``, a torch extension over this
+    library's C ABI; see csrc/torch_launchers.cpp), loaded once.  Raises
+    KernelLibraryMissing when it is not built."""
+    global _ext
+    if _ext is not None:
+        return _ext
+    load()
+    with _lock:
+        if _ext is None:
+            try:
+                from . import _mi355_torch as mod
+            except ImportError as e:
+                raise KernelLibraryMissing(
+                    f"the torch launcher extension _mi355_torch is not built next to {LIB_PATH} ({e}); run "
+                    "`python -c \"import __graft_entry__ as g; g.build()\"` from the repository root") from e
+            if mod.abi_version() != ABI_VERSION:
+                raise KernelLibraryMissing(f"_mi355_torch was built against ABI {mod.abi_version()}, "
+                                           f"expected {ABI_VERSION}; rebuild it")
+            mod.set_kernel_error(KernelError)
+            _ext = mod
+    return _ext
 
 
 def check(fn: str, status: int) -> None:

@@ -2,8 +2,10 @@
 
 Compiles every ``csrc/*.hip`` translation unit for gfx950 with hipcc (in
 parallel, objects under ``_build/``) and links them into one shared library
-next to this file, which ``_lib.py`` loads with ctypes.  Cross-compiles on a
-machine without a GPU.
+next to this file, which ``_lib.py`` loads with ctypes.  Then builds the
+host-side launchers (``csrc/torch_launchers.cpp``, a torch extension that
+calls that library's C ABI) into ``_mi355_torch*.so`` beside it.
+Cross-compiles on a machine without a GPU.
 
     python llm-inference-optimizer_amd/build.py            # default build
     python llm-inference-optimizer_amd/build.py -DMI355_SILU_UNROLL=2 --out /tmp/x.so
@@ -22,6 +24,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libmi355_fused.so"
 PROBE_NAME = "libmi355_probe.so"  # measurement-only copy kernel used by bench.py
+EXT_NAME = "_mi355_torch"  # host-side launchers (torch extension over the C ABI)
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32, which
@@ -73,6 +76,39 @@ def build(extra_flags: list[str] | None = None, out: Path | None = None, jobs: i
     os.replace(tmp, out)
     if out == PKG_DIR / LIB_NAME:
         build_probe()
+        build_torch_ext()
+    return out
+
+
+def ext_path() -> Path:
+    import sysconfig
+    return PKG_DIR / (EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_torch_ext() -> Path:
+    """Build the host-side launchers: a CPython extension module that takes
+    torch tensors and calls libmi355_fused.so's C ABI (linked beside it,
+    found through an $ORIGIN rpath).  Host code only, compiled with g++."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    out = ext_path()
+    tmp = out.with_name(out.name + ".tmp")
+    incs = [*cpp_extension.include_paths(device_type="cuda"), sysconfig.get_paths()["include"]]
+    libdirs = cpp_extension.library_paths(device_type="cuda")
+    cmd = [shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-DTORCH_EXTENSION_NAME={EXT_NAME}",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-I{i}" for i in incs], str(CSRC / "torch_launchers.cpp"), "-o", str(tmp),
+           f"-L{PKG_DIR}", "-lmi355_fused", *[f"-L{d}" for d in libdirs],
+           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip", "-ltorch_hip",
+           "-Wl,-rpath,$ORIGIN", *[f"-Wl,-rpath,{d}" for d in libdirs]]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch launcher build failed:\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")
+    os.replace(tmp, out)
     return out
 
 

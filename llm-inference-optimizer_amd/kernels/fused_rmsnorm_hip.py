@@ -28,46 +28,17 @@ from .. import _lib
 __all__ = ["fused_rmsnorm", "fused_add_rmsnorm", "naive_rmsnorm_reference"]
 
 
-_CODE = _lib.DTYPE_CODE
-
-
-def _rows(t: torch.Tensor, N: int):
-    """(rows view, row count, row stride) of t with contiguous rows, copying
-    only when the last dimension itself is strided."""
-    if t.is_contiguous():
-        return t, (t.numel() // N if N else 0), N
-    t2 = t.reshape(-1, N)
-    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < N):
-        t2 = t2.contiguous()
-    M = t2.shape[0]
-    # Rows only need to be contiguous along the hidden dimension: a row-strided
-    # view is passed with its stride instead of being copied.
-    return t2, M, (t2.stride(0) if M > 1 else N)
-
-
-def _empty_like_rows(x: torch.Tensor) -> torch.Tensor:
-    return torch.empty_like(x) if x.is_contiguous() else torch.empty(x.shape, dtype=x.dtype, device=x.device)
-
-
 def fused_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """Drop-in replacement for HF's RMSNorm.forward.  x: (..., hidden_size),
-    weight: (hidden_size,).  Normalizes over the last dimension."""
-    assert x.is_cuda and weight.is_cuda, "x and weight must be ROCm GPU tensors"
-    N = x.shape[-1]
-    assert weight.shape == (N,), f"weight shape {tuple(weight.shape)} != ({N},)"
-    code, wcode = _CODE.get(x.dtype), _CODE.get(weight.dtype)
-    assert code is not None and wcode is not None, (
-        f"unsupported dtypes x={x.dtype} weight={weight.dtype} (fp16, bf16, fp32)")
-    dev = x.get_device()
-    assert weight.get_device() == dev, "x and weight must be on the same device"
-    x2, M, xs = _rows(x, N)
-    if weight.stride(0) != 1:
-        weight = weight.contiguous()
-    out = _empty_like_rows(x)
-    if M and N:
-        _lib.launch("mi355_rmsnorm_fwd", dev, x2.data_ptr(), weight.data_ptr(), out.data_ptr(), M, N, xs, N,
-                    eps, code, wcode, code)
-    return out
+    weight: (hidden_size,).  Normalizes over the last dimension.
+
+    Preconditions (AssertionError, as the reference's launcher): x and weight
+    on the GPU, weight of shape (hidden_size,), fp16 / bf16 / fp32 storage,
+    one device.  A row-strided x is read in place (rows only need to be
+    contiguous along the hidden dimension); the output has x's dtype and
+    shape.  The checks, the output allocation and the launch run in the C++
+    launcher ``_mi355_torch.rmsnorm`` (csrc/torch_launchers.cpp)."""
+    return _lib.ext().rmsnorm(x, weight, eps)
 
 
 def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6):
@@ -75,28 +46,9 @@ def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Ten
     ``h = residual + x`` rounded to x's dtype -- exactly what
     ``h = residual + x; y = fused_rmsnorm(h, weight, eps)`` returns, in one
     pass (read x and residual, write h and y).  x and residual have the same
-    shape and dtype; normalises over the last dimension."""
-    assert x.is_cuda and residual.is_cuda and weight.is_cuda, "x, residual and weight must be ROCm GPU tensors"
-    assert x.shape == residual.shape, f"shape mismatch {tuple(x.shape)} vs {tuple(residual.shape)}"
-    assert x.dtype == residual.dtype, f"dtype mismatch {x.dtype} vs {residual.dtype}"
-    N = x.shape[-1]
-    assert weight.shape == (N,), f"weight shape {tuple(weight.shape)} != ({N},)"
-    code, wcode = _CODE.get(x.dtype), _CODE.get(weight.dtype)
-    assert code is not None and wcode is not None, (
-        f"unsupported dtypes x={x.dtype} weight={weight.dtype} (fp16, bf16, fp32)")
-    dev = x.get_device()
-    assert residual.get_device() == dev and weight.get_device() == dev, (
-        "x, residual and weight must be on the same device")
-    x2, M, xs = _rows(x, N)
-    r2, _, rs = _rows(residual, N)
-    if weight.stride(0) != 1:
-        weight = weight.contiguous()
-    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    h = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    if M and N:
-        _lib.launch("mi355_add_rmsnorm_fwd", dev, x2.data_ptr(), r2.data_ptr(), weight.data_ptr(), out.data_ptr(),
-                    h.data_ptr(), M, N, xs, rs, N, N, eps, code, wcode, code)
-    return out, h
+    shape and dtype; normalises over the last dimension.  Launched by the C++
+    launcher ``_mi355_torch.add_rmsnorm``."""
+    return _lib.ext().add_rmsnorm(x, residual, weight, eps)
 
 
 def naive_rmsnorm_reference(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

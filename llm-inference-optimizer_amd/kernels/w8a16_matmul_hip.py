@@ -37,41 +37,12 @@ def w8a16_linear(x: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor,
                  bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """x: (..., K) fp16/bf16.  w_q: (N, K) int8.  scale: (N,) float32 (fp16 /
     bf16 accepted).  bias: optional (N,).  Returns (..., N) in x's dtype (or
-    ``out_dtype=torch.float32``: the value before the final rounding)."""
-    assert x.is_cuda and w_q.is_cuda, "x and w_q must be ROCm GPU tensors"
-    assert w_q.dtype == torch.int8, f"w_q must be int8, got {w_q.dtype}"
-    N, K = w_q.shape
-    assert x.shape[-1] == K, f"x last dim {x.shape[-1]} != weight in_features {K}"
-    assert x.dtype in (torch.float16, torch.bfloat16), f"x must be fp16 or bf16, got {x.dtype}"
-    assert scale.is_cuda and scale.shape == (N,) and scale.dtype in _CODE, (
-        f"scale must be a ({N},) float GPU tensor, got {tuple(scale.shape)} {scale.dtype}")
-    if bias is not None:
-        assert bias.is_cuda and bias.shape == (N,) and bias.dtype in _CODE, (
-            f"bias must be a ({N},) float GPU tensor, got {tuple(bias.shape)} {bias.dtype}")
-    dev = x.get_device()
-    assert w_q.get_device() == dev and scale.get_device() == dev, "x, w_q and scale must share a device"
-    out_dtype = x.dtype if out_dtype is None else out_dtype
-    assert out_dtype in (x.dtype, torch.float32), f"out_dtype must be {x.dtype} or float32"
-
-    x2 = x.reshape(-1, K)
-    if x2.stride(-1) != 1:
-        x2 = x2.contiguous()
-    if w_q.stride(-1) != 1:
-        w_q = w_q.contiguous()
-    scale = scale.contiguous()
-    if bias is not None:
-        bias = bias.contiguous()
-    M = x2.shape[0]
-    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
-    if M and N:
-        # a single row's stride is arbitrary in torch (even 0); the kernels read one row then
-        xs = x2.stride(0) if M > 1 else K
-        ws = w_q.stride(0) if N > 1 else K
-        _lib.launch("mi355_w8a16_linear_fwd", dev, x2.data_ptr(), w_q.data_ptr(), scale.data_ptr(),
-                    bias.data_ptr() if bias is not None else None, out.data_ptr(), M, K, N,
-                    xs, ws, N, _CODE[x.dtype], _CODE[scale.dtype],
-                    _CODE[bias.dtype] if bias is not None else 0, _CODE[out_dtype])
-    return out.reshape(*x.shape[:-1], N)
+    ``out_dtype=torch.float32``: the value before the final rounding).
+    Preconditions as the reference's launcher (:108-111) plus dtype checks.
+    Launched by the C++ launcher ``_mi355_torch.w8a16_linear``."""
+    out_f32 = out_dtype is not None and out_dtype != x.dtype
+    assert not out_f32 or out_dtype == torch.float32, f"out_dtype must be {x.dtype} or float32"
+    return _lib.ext().w8a16_linear(x, w_q, scale, bias, out_f32)
 
 
 def fused_gate_up_silu_w8a16(x: torch.Tensor, wq_gate: torch.Tensor, scale_gate: torch.Tensor,
@@ -79,37 +50,11 @@ def fused_gate_up_silu_w8a16(x: torch.Tensor, wq_gate: torch.Tensor, scale_gate:
                              out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """silu((x @ wq_gate.T) * scale_gate) * ((x @ wq_up.T) * scale_up) for x
     (..., K) fp16/bf16 and int8 weights (N, K) with (N,) scales (one float
-    dtype).  Output (..., N) in x's dtype (or ``out_dtype=torch.float32``)."""
-    assert x.is_cuda and wq_gate.is_cuda and wq_up.is_cuda, "x and the weights must be ROCm GPU tensors"
-    assert wq_gate.dtype == torch.int8 and wq_up.dtype == torch.int8, "weights must be int8"
-    assert wq_gate.shape == wq_up.shape, f"weight shapes differ: {tuple(wq_gate.shape)} vs {tuple(wq_up.shape)}"
-    N, K = wq_gate.shape
-    assert x.shape[-1] == K, f"x last dim {x.shape[-1]} != weight in_features {K}"
-    assert x.dtype in (torch.float16, torch.bfloat16), f"x must be fp16 or bf16, got {x.dtype}"
-    for sc in (scale_gate, scale_up):
-        assert sc.is_cuda and sc.shape == (N,) and sc.dtype in _CODE, (
-            f"scales must be ({N},) float GPU tensors, got {tuple(sc.shape)} {sc.dtype}")
-    assert scale_gate.dtype == scale_up.dtype, "the two scales must share a dtype"
-    dev = x.get_device()
-    assert all(t.get_device() == dev for t in (wq_gate, wq_up, scale_gate, scale_up)), "all inputs must share a device"
-    out_dtype = x.dtype if out_dtype is None else out_dtype
-    assert out_dtype in (x.dtype, torch.float32), f"out_dtype must be {x.dtype} or float32"
-
-    x2 = x.reshape(-1, K)
-    if x2.stride(-1) != 1:
-        x2 = x2.contiguous()
-    if wq_gate.stride(-1) != 1 or wq_up.stride(-1) != 1 or wq_gate.stride(0) != wq_up.stride(0):
-        wq_gate, wq_up = wq_gate.contiguous(), wq_up.contiguous()
-    scale_gate, scale_up = scale_gate.contiguous(), scale_up.contiguous()
-    M = x2.shape[0]
-    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
-    if M and N:
-        xs = x2.stride(0) if M > 1 else K
-        ws = wq_gate.stride(0) if N > 1 else K
-        _lib.launch("mi355_gate_up_silu_w8a16_fwd", dev, x2.data_ptr(), wq_gate.data_ptr(), wq_up.data_ptr(),
-                    scale_gate.data_ptr(), scale_up.data_ptr(), out.data_ptr(), M, K, N, xs, ws, N,
-                    _CODE[x.dtype], _CODE[scale_gate.dtype], _CODE[out_dtype])
-    return out.reshape(*x.shape[:-1], N)
+    dtype).  Output (..., N) in x's dtype (or ``out_dtype=torch.float32``).
+    Launched by the C++ launcher ``_mi355_torch.gate_up_silu_w8a16``."""
+    out_f32 = out_dtype is not None and out_dtype != x.dtype
+    assert not out_f32 or out_dtype == torch.float32, f"out_dtype must be {x.dtype} or float32"
+    return _lib.ext().gate_up_silu_w8a16(x, wq_gate, scale_gate, wq_up, scale_up, out_f32)
 
 
 def w8a16_reference(x: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor,
