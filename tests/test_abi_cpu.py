@@ -285,3 +285,23 @@ def test_gate_up_w8a16_launcher_asserts_on_host_tensors(pkg):
     q = torch.zeros(16, 64, dtype=torch.int8)
     with pytest.raises(AssertionError):
         pkg.fused_gate_up_silu_w8a16(x, q, torch.ones(16), q, torch.ones(16))
+
+
+def test_torch_launchers_load_and_match_the_abi(L):
+    """The launchers' host side (the _mi355_torch extension over the C ABI)
+    is built beside the library and reports the same ABI version."""
+    ext = L.ext()
+    assert ext.abi_version() == L.ABI_VERSION
+    for name in ("rmsnorm", "add_rmsnorm", "silu_mul", "gate_up_silu", "linear16", "w8a16_linear",
+                 "gate_up_silu_w8a16"):
+        assert callable(getattr(ext, name))
+
+
+def test_torch_launchers_keep_the_reference_messages(pkg):
+    x = torch.randn(4, 64, dtype=torch.float16)
+    with pytest.raises(AssertionError, match="x and weight must be ROCm GPU tensors"):
+        pkg.fused_rmsnorm(x, torch.ones(64, dtype=torch.float16))
+    with pytest.raises(AssertionError, match=r"shape mismatch \(4, 64\) vs \(4, 65\)"):
+        pkg.fused_silu_mul(x, torch.randn(4, 65, dtype=torch.float16))
+    with pytest.raises(AssertionError, match="out_dtype must be torch.float16 or float32"):
+        pkg.linear16(x, x, out_dtype=torch.float64)
