@@ -369,6 +369,62 @@ __device__ __forceinline__ float silu_mul_f32(float g, float u) {
 }
 
 // ---------------------------------------------------------------------------
+// MFMA operands shared by the projection kernels (gate/up, W8A16, 16-bit
+// linear, tiled GEMM).
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer offset past every descriptor the launchers build (each < 2^31
+// bytes): a load there returns zeros and moves no data.
+constexpr uint32_t kOob = 0xfffffff0u;
+
+// v_mfma_f32_16x16x32_{f16,bf16}: A and B are 8 values of T per lane.
+template <typename T> __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma16<F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma16<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// Four int8 (one dword, byte i = element i) -> four values of T in two dwords
+// (element 2j in the low half of dword j).  Exact: |q| <= 128.
+template <typename T> __device__ __forceinline__ u32x2 widen_i8x4(uint32_t d);
+template <> __device__ __forceinline__ u32x2 widen_i8x4<F16>(uint32_t d) {
+  // Bias each byte to u = q + 128 and splice it under the fp16 pattern 0x64:
+  // 0x64uu is 1024 + u exactly; subtracting 1152 leaves q.
+  const uint32_t u = d ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0,64,u1,64
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2,64,u3,64
+  const f16x2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+  const f16x2 a = __builtin_bit_cast(f16x2, lo) + off;
+  const f16x2 b = __builtin_bit_cast(f16x2, hi) + off;
+  return u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+}
+template <> __device__ __forceinline__ u32x2 widen_i8x4<BF16>(uint32_t d) {
+  // Signed byte -> fp32 (exact), then the upper half of each fp32 pattern is
+  // the bf16 pattern of the same (8-significant-bit) integer.
+  const float f0 = static_cast<float>(static_cast<int8_t>(d & 0xffu));
+  const float f1 = static_cast<float>(static_cast<int8_t>((d >> 8) & 0xffu));
+  const float f2 = static_cast<float>(static_cast<int8_t>((d >> 16) & 0xffu));
+  const float f3 = static_cast<float>(static_cast<int8_t>(d >> 24));
+  return u32x2{__builtin_amdgcn_perm(as_u32(f1), as_u32(f0), 0x07060302u),
+               __builtin_amdgcn_perm(as_u32(f3), as_u32(f2), 0x07060302u)};
+}
+
+// Element i of a float vector stored as F32 / F16 / BF16 (dtype code dt):
+// scales and biases, whose dtype is a run-time argument.
+__device__ __forceinline__ float load_dyn(const void* p, int64_t i, int dt) {
+  if (dt == MI355_F16) return load_elem<F16>(p, i);
+  if (dt == MI355_BF16) return load_elem<BF16>(p, i);
+  return load_elem<F32>(p, i);
+}
+
+// ---------------------------------------------------------------------------
 // Host-side helpers shared by the launchers.
 // ---------------------------------------------------------------------------
 void set_error(const char* fmt, ...);

@@ -74,11 +74,7 @@
 namespace mi355 {
 namespace tiled {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr uint32_t kOob = 0xfffffff0u;  // past every descriptor the launchers admit (< 2^31 bytes)
 
 enum { EPI_W8 = 0, EPI_SILU = 1, EPI_SILU_W8 = 2, EPI_LINEAR = 3 };
 enum { B_16 = 0, B_I8 = 1 };
@@ -93,28 +89,9 @@ template <> __device__ __forceinline__ f32x16 mfma32<BF16>(u32x4 a, u32x4 b, f32
                                                  0, 0, 0);
 }
 
-// Four int8 (byte i = element i) -> four values of T in two dwords.
-template <typename T> __device__ __forceinline__ u32x2 widen4(uint32_t d);
-template <> __device__ __forceinline__ u32x2 widen4<F16>(uint32_t d) {
-  const uint32_t u = d ^ 0x80808080u;
-  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0,64,u1,64
-  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2,64,u3,64
-  const f16x2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
-  const f16x2 a = __builtin_bit_cast(f16x2, lo) + off;
-  const f16x2 b = __builtin_bit_cast(f16x2, hi) + off;
-  return u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
-}
-template <> __device__ __forceinline__ u32x2 widen4<BF16>(uint32_t d) {
-  const float f0 = static_cast<float>(static_cast<int8_t>(d & 0xffu));
-  const float f1 = static_cast<float>(static_cast<int8_t>((d >> 8) & 0xffu));
-  const float f2 = static_cast<float>(static_cast<int8_t>((d >> 16) & 0xffu));
-  const float f3 = static_cast<float>(static_cast<int8_t>(d >> 24));
-  return u32x2{__builtin_amdgcn_perm(as_u32(f1), as_u32(f0), 0x07060302u),
-               __builtin_amdgcn_perm(as_u32(f3), as_u32(f2), 0x07060302u)};
-}
 // 8 int8 in two dwords -> one MFMA operand (8 values of T).
 template <typename T> __device__ __forceinline__ u32x4 widen8(uint32_t d0, uint32_t d1) {
-  const u32x2 p = widen4<T>(d0), q = widen4<T>(d1);
+  const u32x2 p = widen_i8x4<T>(d0), q = widen_i8x4<T>(d1);
   return u32x4{p.x, p.y, q.x, q.y};
 }
 
@@ -128,12 +105,6 @@ __device__ __forceinline__ u32x4 lds_read16(const uint8_t* base, uint32_t off) {
 }
 __device__ __forceinline__ void lds_write16(uint8_t* base, uint32_t off, u32x4 v) {
   *reinterpret_cast<u32x4*>(base + off) = v;
-}
-
-__device__ __forceinline__ float load_dyn(const void* p, int64_t i, int dt) {
-  if (dt == MI355_F16) return load_elem<F16>(p, i);
-  if (dt == MI355_BF16) return load_elem<BF16>(p, i);
-  return load_elem<F32>(p, i);
 }
 
 struct Params {
