@@ -258,13 +258,22 @@ int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
                     "gate_up_silu tiled launch");
 }
 
-// Tiled launch shapes from a sweep on MI355X (Qwen2.5-1.5B and 7B MLPs at
-// 128, 1024 and 4096 rows): up to 256 rows 128 x 64 output tiles (4 waves,
-// 4 stages) or, for n_out > 10000, 128 x 128 (8 waves, 3 stages); more rows
-// 256 x 64 (8 waves, 3 stages).  Descriptors span at most 256 rows of x and
-// 128 weight rows, each below 2^31 bytes.
+// Tiled launch shapes from sweeps on MI355X (Qwen2.5-1.5B and 7B MLPs at
+// 16 - 64, 128, 1024 and 4096 rows): up to 32 rows 32 x 64 output tiles (2
+// waves) or, for n_out > 10000, 32 x 128 (4 waves); up to 64 rows 64 x 64 (4
+// waves; n_out > 10000 keeps the next shape); up to 256 rows 128 x 64 (4
+// waves, 4 stages) or, for n_out > 10000, 128 x 128 (8 waves, 3 stages);
+// more rows 256 x 64 (8 waves, 3 stages).  The small shapes run 4 stages.
+// Descriptors span at most 256 rows of x and 128 weight rows, each below
+// 2^31 bytes.
 template <typename T, typename TO>
 int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
+  const bool wide = p.n_out > 10000;
+  if (p.rows <= 32) {
+    if (wide) return gate_up_tiled_cfg<T, TO, 1, 4, 1, 1, 4>(p, s);  // 32 x 128, 4 waves
+    return gate_up_tiled_cfg<T, TO, 1, 2, 1, 1, 4>(p, s);            // 32 x 64, 2 waves
+  }
+  if (p.rows <= 64 && !wide) return gate_up_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);  // 64 x 64, 4 waves
   if (p.rows <= 256) {
     if (p.n_out <= 10000) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(p, s);
     return gate_up_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
@@ -274,15 +283,20 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
 
 template <typename T, typename TO>
 int gate_up_typed(const GateUpParams& p, hipStream_t s) {
-  // x tile: the fewest 8-row MFMA tiles that cover the rows, up to 4 (32 rows)
-  // per workgroup; more rows take the tiled GEMM when its descriptors fit,
-  // else further 32-row skinny tiles along grid y.
+  // Up to 16 rows: the weight-streaming kernel with the fewest 8-row MFMA
+  // tiles that cover the rows.  More rows take the tiled GEMM when its
+  // descriptors fit -- from 17 rows its small tiles read each weight byte
+  // once from HBM and x once per workgroup, where 3 or 4 skinny x tiles
+  // re-load x per weight piece (1.5B, 32 rows 20.0 -> 15.5 us; 7B 66.7 ->
+  // 53.8 us), as long as the output has >= 128 tile columns to spread over
+  // the CUs -- else 24- or 32-row skinny tiles along grid y.
   if (p.rows <= 8) return gate_up_shape<T, TO, 1>(p, s);
   if (p.rows <= 16) return gate_up_shape<T, TO, 2>(p, s);
-  if (p.rows <= 24) return gate_up_shape<T, TO, 3>(p, s);
   const bool tiled_fits = int64_t{256} * p.xs * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31) &&
                           int64_t{128} * p.ws * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31);
-  if (p.rows > 32 && tiled_fits) return gate_up_tiled<T, TO>(p, s);
+  const int bn = p.n_out > 10000 ? 128 : 64;
+  if (tiled_fits && (p.rows > 32 || (p.n_out + bn - 1) / bn >= 128)) return gate_up_tiled<T, TO>(p, s);
+  if (p.rows <= 24) return gate_up_shape<T, TO, 3>(p, s);
   return gate_up_shape<T, TO, 4>(p, s);
 }
 

@@ -317,6 +317,22 @@ int l16_tiled(const L16Params& p, hipStream_t s) {
   return l16_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
 }
 
+// Small tiled shapes: 32 x 64 (2 waves) or, for n > 10000, 32 x 128 (4 waves)
+// up to 32 rows; 64 x 64 (4 waves) up to 64; 4 stages.  From a sweep over
+// the Qwen2.5-1.5B / 7B down and o projections at 16 - 64 rows: at 17 - 32
+// rows they lose to split-K weight streaming on these narrow outputs (1.5B
+// down, 32 rows: 38.0 vs 22.3 us) unless the output has >= 128 tile
+// columns; at 33 - 64 rows, where streaming re-reads the weights per 32-row
+// tile, they win (7B down, 48 rows: 85.5 vs 101.6 us; 7B o 19.4 vs 22.6).
+template <typename T, typename TO>
+int l16_tiled_small(const L16Params& p, hipStream_t s) {
+  if (p.rows <= 32) {
+    if (p.n > 10000) return l16_tiled_cfg<T, TO, 1, 4, 1, 1, 4>(p, s);
+    return l16_tiled_cfg<T, TO, 1, 2, 1, 1, 4>(p, s);
+  }
+  return l16_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);
+}
+
 template <typename T, typename TO>
 int l16_typed(const L16Params& p, hipStream_t s, int cus) {
   const bool vec = p.k % 8 == 0 && p.ws % 8 == 0 && p.xs % 8 == 0 && aligned16(p.x) && aligned16(p.w);
@@ -326,6 +342,10 @@ int l16_typed(const L16Params& p, hipStream_t s, int cus) {
   }
   if (p.rows <= 8) return l16_skinny_shape<T, TO, 1>(p, s, cus);
   if (p.rows <= 16) return l16_skinny_shape<T, TO, 2>(p, s, cus);
+  if (p.rows <= 64 && l16_tiled_fits(p)) {
+    const int bn = (p.rows <= 32 && p.n > 10000) ? 128 : 64;
+    if (p.rows > 32 || (p.n + bn - 1) / bn >= 128) return l16_tiled_small<T, TO>(p, s);
+  }
   if (p.rows <= 24) return l16_skinny_shape<T, TO, 3>(p, s, cus);
   if (p.rows <= 32) return l16_skinny_shape<T, TO, 4>(p, s, cus);
   // More rows: the tiled GEMM, except for small grids of few rows, where

@@ -499,6 +499,30 @@ int w8_tiled_dual(const W8Params& p, hipStream_t s) {
   return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 4, tiled::EPI_SILU_W8>(p, s);
 }
 
+// Small tiled shapes for 17 - 64 rows: 32 x 64 (2 waves) or, for n > 10000,
+// 32 x 128 (4 waves) up to 32 rows; 64 x 64 (4 waves) up to 64; 4 stages.
+// They read each weight byte once and x once per workgroup, where 24- or
+// 32-row skinny tiles re-load x for every weight piece and more rows re-read
+// the weights per 32-row tile -- but only win with >= 128 tile columns to
+// spread over the CUs (a sweep over the Qwen2.5-1.5B / 7B projections at 16 -
+// 64 rows: int8 gate/up 7B, 32 rows 85.1 -> 40.7 us, 1.5B 21.3 -> 14.8 us;
+// the 1536-wide down and q/o projections 1.8x slower, so they keep split-K
+// weight streaming).
+bool small_tiles_pay(int rows, int n) {
+  const int bn = (rows <= 32 && n > 10000) ? 128 : 64;
+  return rows > 16 && rows <= 64 && (n + bn - 1) / bn >= 128;
+}
+
+template <typename T, typename TO, bool DUAL>
+int w8_tiled_small(const W8Params& p, hipStream_t s) {
+  constexpr int EPI = DUAL ? tiled::EPI_SILU_W8 : tiled::EPI_W8;
+  if (p.rows <= 32) {
+    if (p.n > 10000) return w8_tiled_cfg<T, TO, 1, 4, 1, 1, 4, EPI>(p, s);
+    return w8_tiled_cfg<T, TO, 1, 2, 1, 1, 4, EPI>(p, s);
+  }
+  return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4, EPI>(p, s);
+}
+
 template <typename T, typename TO, bool DUAL>
 int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   const bool vec = p.k % 16 == 0 && p.qs % 16 == 0 && p.xs % 8 == 0 && aligned16(p.x) && aligned16(p.q) &&
@@ -509,6 +533,7 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   }
   if (p.rows <= 8) return w8_skinny_shape<T, TO, 1, DUAL>(p, s, cus);
   if (p.rows <= 16) return w8_skinny_shape<T, TO, 2, DUAL>(p, s, cus);
+  if (small_tiles_pay(p.rows, p.n) && tiled_fits(p, DUAL)) return w8_tiled_small<T, TO, DUAL>(p, s);
   if (p.rows <= 24) return w8_skinny_shape<T, TO, 3, DUAL>(p, s, cus);
   if (p.rows <= 32) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);
   // More rows: the tiled GEMM, except for small grids of few rows (e.g. 128

@@ -75,6 +75,8 @@ def _check_vs_oracle(orc, got16, got32, x, wg, wu, dt):
     (17, 2048, 1000, F16),
     # prefill rows: the tiled GEMM (each of its three launch shapes, k tails, ragged edges)
     (64, 1536, 1000, F16), (200, 640, 10240, BF16), (300, 1552, 520, F16), (257, 96, 333, BF16),
+    # 17 - 64 rows: the small tiled shapes (32 x 64, 32 x 128 for n_out > 10000, 64 x 64)
+    (20, 256, 16400, BF16), (24, 1536, 8960, F16), (40, 256, 4000, F16), (63, 136, 72, BF16),
 ])
 def test_gate_up_silu_matches_oracle(pkg, orc, cuda, rows, k, n, dt):
     x, wg, wu = _inputs(rows, k, n, dt, seed=80 + rows)

@@ -65,6 +65,8 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
     # prefill rows: the dual tiled GEMM (and the skinny tiles of small grids)
     (33, 256, 100, BF16), (64, 1536, 1000, F16), (200, 640, 10240, F16), (300, 1552, 520, BF16),
     (1024, 1536, 2048, F16),
+    # 17 - 64 rows with >= 128 tile columns: the small dual tiled shapes
+    (32, 1536, 8960, F16), (20, 256, 16400, BF16), (56, 272, 8200, F16),
     # odd k: the dual generic kernel
     (5, 100, 37, F16), (40, 72, 40, BF16),
 ])

@@ -71,6 +71,9 @@ def _check_vs_oracle(orc, got16, got32, x, w, b, dt):
     # more than 32 rows: skinny tiles on small grids, the tiled GEMM otherwise (k tails, ragged edges)
     (33, 1536, 256, F16, None), (100, 256, 100, BF16, "same"), (200, 8960, 1536, F16, "f32"),
     (300, 1552, 520, BF16, None), (257, 96, 333, F16, "same"),
+    # the small tiled shapes: >= 128 tile columns at 17 - 32 rows, any 33 - 64 rows
+    (24, 512, 8192, F16, "f32"), (20, 256, 16400, BF16, None), (48, 8960, 1536, F16, "same"),
+    (64, 1000, 200, BF16, None),
 ])
 def test_linear16_matches_oracle(pkg, orc, cuda, rows, k, n, dt, bias):
     bias_dt = None if bias is None else (dt if bias == "same" else {"f32": F32, "f16": F16}[bias])

@@ -143,6 +143,10 @@ TILED_CASES = [
     (2048, 128, 8952, F16, False),    # < 2000: 128 x 128, 4 waves
     (4096, 64, 8960, F16, True),      # the rest: 128 x 256
     (4096, 80, 9000, BF16, True),     # (bf16: 128 x 128)
+    # 17 - 64 rows with >= 128 tile columns: the small tiled shapes
+    (24, 1536, 8960, F16, True),      # 32 x 64
+    (20, 256, 16400, BF16, False),    # n > 10000: 32 x 128
+    (48, 272, 8200, F16, True),       # 33 - 64 rows: 64 x 64
 ]
 
 
