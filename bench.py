@@ -1269,8 +1269,9 @@ def bench_e2e(args):
         return B / statistics.median(times)
 
     def graphed(tag):
-        r = {"b1": graphed_decode_tok_s(), "b8": graphed_decode_tok_s(B=8)}
-        log(f"  {tag}, graphed decode (seq 512): batch 1 {r['b1']:.1f} tok/s, batch 8 {r['b8']:.1f} tok/s")
+        r = {"b1": graphed_decode_tok_s(), "b8": graphed_decode_tok_s(B=8), "b32": graphed_decode_tok_s(B=32)}
+        log(f"  {tag}, graphed decode (seq 512): batch 1 {r['b1']:.1f} tok/s, batch 8 {r['b8']:.1f} tok/s, "
+            f"batch 32 {r['b32']:.1f} tok/s")
         return {k: round(v, 1) for k, v in r.items()}
 
     # warm every shape once before timing anything
