@@ -27,7 +27,10 @@ namespace py = pybind11;
 
 namespace {
 
-py::object g_kernel_error;  // the package's KernelError class
+// The package's KernelError class.  Held through a pointer that is never
+// freed: a py::object with static storage would be released after the
+// interpreter has finalised, at process exit.
+py::object* g_kernel_error = nullptr;
 
 [[noreturn]] void fail_assert(const std::string& msg) {
   PyErr_SetString(PyExc_AssertionError, msg.c_str());
@@ -37,8 +40,8 @@ py::object g_kernel_error;  // the package's KernelError class
 void check(const char* fn, int status) {
   if (status == MI355_OK) return;
   const std::string msg = mi355_last_error();
-  if (g_kernel_error) {
-    PyErr_SetObject(g_kernel_error.ptr(), py::make_tuple(fn, status, msg).ptr());
+  if (g_kernel_error != nullptr) {
+    PyErr_SetObject(g_kernel_error->ptr(), py::make_tuple(fn, status, msg).ptr());
     throw py::error_already_set();
   }
   throw std::runtime_error(std::string(fn) + " failed with status " + std::to_string(status) + ": " + msg);
@@ -378,7 +381,10 @@ at::Tensor gate_up_silu_w8a16(const at::Tensor& x, const at::Tensor& wq_gate, co
 
 PYBIND11_MODULE(_mi355_torch, m) {
   m.doc() = "Host-side launchers of the MI355X fused kernels (torch tensors -> the C ABI of libmi355_fused.so)";
-  m.def("set_kernel_error", [](py::object cls) { g_kernel_error = cls; });
+  m.def("set_kernel_error", [](py::object cls) {
+    if (g_kernel_error == nullptr) g_kernel_error = new py::object(cls);
+    else *g_kernel_error = cls;
+  });
   m.def("abi_version", []() { return mi355_abi_version(); });
   m.def("rmsnorm", &rmsnorm, py::arg("x"), py::arg("weight"), py::arg("eps"));
   m.def("add_rmsnorm", &add_rmsnorm, py::arg("x"), py::arg("residual"), py::arg("weight"), py::arg("eps"));
