@@ -230,7 +230,7 @@ int gate_up_shape(const GateUpParams& p, hipStream_t s) {
   return gate_up_launch_tiles<T, TO, MT, 4, 2, 2>(p, s);
 }
 
-template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S>
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int RING = 0>
 int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_16, TO, WGM, WGN, FM, FN, tiled::EPI_SILU, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
@@ -253,19 +253,24 @@ int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_16, TO, WGM, WGN, FM, FN,
-                                                                                      tiled::EPI_SILU, S>),
+                                                                                      tiled::EPI_SILU, S, RING>),
                                     dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
                     "gate_up_silu tiled launch");
 }
 
 // Tiled launch shapes from sweeps on MI355X (Qwen2.5-1.5B and 7B MLPs at
-// 16 - 64, 128, 1024 and 4096 rows): up to 32 rows 32 x 64 output tiles (2
-// waves) or, for n_out > 10000, 32 x 128 (4 waves); up to 64 rows 64 x 64 (4
-// waves; n_out > 10000 keeps the next shape); up to 256 rows 128 x 64 (4
-// waves, 4 stages) or, for n_out > 10000, 128 x 128 (8 waves, 3 stages);
-// more rows 256 x 64 (8 waves, 3 stages).  The small shapes run 4 stages.
-// Descriptors span at most 256 rows of x and 128 weight rows, each below
-// 2^31 bytes.
+// 16 - 64, 128, 1024, 1536, 2048 and 4096 rows): up to 32 rows 32 x 64
+// output tiles (2 waves) or, for n_out > 10000, 32 x 128 (4 waves); up to 64
+// rows 64 x 64 (4 waves; n_out > 10000 keeps the next shape); up to 256 rows
+// 128 x 64 (4 waves, 4 stages) or, for n_out > 10000, 128 x 128 (8 waves, 3
+// stages); up to 1024 rows 256 x 64 (8 waves, 3 stages); more rows 256 x 128
+// (8 waves of 128 x 32, 2 stages, the sub-step register ring): two thirds
+// of the operand bytes per MFMA of 256 x 64 through the DMA and three
+// quarters through LDS reads (1.5B, 4096 rows 251 -> 233 us; 7B, 2048 rows
+// 518 -> 469 us),
+// where at 1024 rows its fewer, larger tiles fill the CUs less evenly.  The
+// small shapes run 4 stages.  Descriptors span at most 256 rows of x and 128
+// weight rows, each below 2^31 bytes.
 template <typename T, typename TO>
 int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
   const bool wide = p.n_out > 10000;
@@ -278,7 +283,8 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
     if (p.n_out <= 10000) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(p, s);
     return gate_up_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
   }
-  return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(p, s);
+  if (p.rows <= 1024) return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(p, s);
+  return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(p, s);  // 256 x 128, 8 waves, sub-step ring
 }
 
 template <typename T, typename TO>

@@ -22,16 +22,22 @@
 // only a final partial step redirects columns at or past k past the
 // descriptor, so any k that is a multiple of 16 (int8) or 8 (16-bit) works.
 //
-// Per step a wave waits for its own DMA of the next step (vmcnt, the later
-// steps stay in flight), meets the other waves at one barrier, issues the
-// LDS reads of the next step and then the MFMAs of this step, whose operands
-// it read one step earlier, so LDS latency hides behind the MFMAs.  The main
-// loop is unrolled so stage and register-set indices are compile-time
-// constants and has no branches (a guarded copy runs the last steps), which
-// keeps the compiler's own wait-count tracking exact; sched_barriers keep
-// the reads ahead of, and the next step's waits behind, the MFMAs.  The DMA
-// is inline asm so the compiler neither tracks its LDS writes nor drains
-// every load in flight before an LDS read; the kernel orders them itself.
+// Two main loops.  The step pipeline (RING = 0, S >= 3): per step a wave
+// waits for its own DMA of the next step (vmcnt, the later steps stay in
+// flight), meets the other waves at one barrier, then alternates the MFMAs
+// of this step's sub-steps, whose operands it read one step earlier, with
+// the LDS reads of the next step's, so LDS latency hides behind the MFMAs.
+// The sub-step ring (RING = 1, 16-bit B, S = 2 allowed) reads one 16-column
+// sub-step ahead instead of one step, so a wave holds two sub-steps of
+// operands rather than two steps and a 128 x 32 wave tile of both B
+// matrices fits in the register file next to its 128 accumulators; its
+// barrier sits before the last sub-step's MFMAs.  Both loops are unrolled so
+// stage and register-set indices are compile-time constants and have no
+// branches (a guarded copy runs the last steps), which keeps the compiler's
+// own wait-count tracking exact; sched_barriers keep each group of reads
+// and MFMAs in place.  The DMA is inline asm so the compiler neither tracks
+// its LDS writes nor drains every load in flight before an LDS read; the
+// kernel orders them itself.
 //
 // K order inside a step.  The MFMA operands give lane l row l % 32 and 8
 // consecutive k of k-group h = l / 32.  A step's 64 columns are dealt so that
@@ -141,8 +147,8 @@ struct Cfg {
   static constexpr int BI = B_BYTES / 1024 / NW;  // B DMA instructions per wave per step and matrix
   static constexpr int P = AI + NB * BI;          // DMA instructions per wave per step
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "tile must split over the waves");
-  static_assert(S >= 3 && S <= 8, "3..8 stages");
-  static_assert(P * (S - 2) < 64, "vmcnt range");
+  static_assert(S >= 2 && S <= 8, "2..8 stages");
+  static_assert(P * (S - 1) < 64, "vmcnt range");
 };
 
 // Stage I of the LDS ring (one LDS variable per stage).
@@ -207,7 +213,7 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
-template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S>
+template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0>
 __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
   constexpr bool I8 = C::I8;
@@ -322,97 +328,181 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     u32x4 a[4][FM];
     u32x4 b[NB][BQ][FN];
   };
-  auto read_frags = [&](auto I, Frags& f) {
+  // LDS reads of sub-step s of one step (stage I) into f.
+  auto read_sub = [&](auto I, Frags& f, int s) {
     const uint8_t* abase = stage_ptr<decltype(I)::value, C::STAGE>();
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int i = 0; i < FM; ++i) f.a[s][i] = lds_read16(abase, swz16(arow0 + 32 * i, 4 * h + s));
 #pragma unroll
-      for (int i = 0; i < FM; ++i) f.a[s][i] = lds_read16(abase, swz16(arow0 + 32 * i, 4 * h + s));
+    for (int bi = 0; bi < NB; ++bi) {
 #pragma unroll
-      for (int bi = 0; bi < NB; ++bi) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if constexpr (I8) {
-            if (s < BQ) f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz8(brow0 + 32 * j, 2 * h + s));
-          } else {
-            f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz16(brow0 + 32 * j, 4 * h + s));
-          }
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (I8) {
+          if (s < BQ) f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz8(brow0 + 32 * j, 2 * h + s));
+        } else {
+          f.b[bi][s][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz16(brow0 + 32 * j, 4 * h + s));
         }
       }
     }
   };
-  auto mfma_frags = [&](const Frags& f) {
+  auto read_frags = [&](auto I, Frags& f) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < 4; ++s) read_sub(I, f, s);
+  };
+  // MFMAs of sub-step s from f.
+  auto mfma_sub = [&](const Frags& f, int s) {
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi) {
+      u32x4 bf[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (I8) {
+          const u32x4 raw = f.b[bi][s >> 1][j];
+          bf[j] = (s & 1) ? widen8<T>(raw.z, raw.w) : widen8<T>(raw.x, raw.y);
+        } else {
+          bf[j] = f.b[bi][s][j];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[bi][i][j] = mfma32<T>(bf[j], f.a[s][i], acc[bi][i][j]);
+      }
+    }
+  };
+
+  int t0 = 0;
+  if constexpr (!RING) {
+    // Step pipeline.  Step t computes from registers read out of stage t % S
+    // one step earlier.  In step t a wave refills stage (t - 1) % S, which
+    // every wave finished reading before the previous barrier, with step
+    // t + S - 1; waits for its own DMA of step t + 1 (the later steps stay in
+    // flight) and for its LDS reads of step t; meets the other waves at the
+    // barrier -- all of step t + 1 is now in LDS -- and then, sub-step by
+    // sub-step, runs the MFMAs of step t's sub-step s and issues the LDS reads
+    // of step t + 1's sub-step s, so a wave's MFMAs never queue behind all of
+    // its LDS reads (2-3% over all reads first).
+    static_assert(S >= 3, "the step pipeline needs 3 stages");
+    Frags fr[2];
+    static_for([&](auto I) {
+      if (decltype(I)::value < nk) issue(I, decltype(I)::value);
+    }, std::make_index_sequence<S - 1>{});
+    if (S - 2 < nk) wait_vmcnt<(S - 2) * C::P>();
+    else wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    lds_barrier();
+    read_frags(std::integral_constant<int, 0>{}, fr[0]);
+
+    constexpr int UNROLL = lcm_c(S, 2);  // stage and fragment-set indices known at compile time
+    // One step; GUARD = false where every condition is known to hold (all
+    // steps it touches are full 64-column steps inside k), so the main loop
+    // has no branches and the compiler's own wait-count tracking stays exact.
+    auto step = [&](auto I, auto GUARD, int t) {
+      constexpr int ii = decltype(I)::value, si = ii % S, pi = ii % 2;
+      constexpr bool guard = decltype(GUARD)::value;
+      if (!guard || t + S - 1 < nk) issue(std::integral_constant<int, (si + S - 1) % S>{}, t + S - 1);
+      const bool more = !guard || t + 1 < nk;
+      if (more) {
+        if (!guard || t + S - 1 < nk) wait_vmcnt<(S - 2) * C::P>();
+        else wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        lds_barrier();
+      }
+      // sched_barriers keep each group in place
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_sub(fr[pi], s);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) read_sub(std::integral_constant<int, (si + 1) % S>{}, fr[pi ^ 1], s);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // main loop: steps t0 .. t0 + UNROLL - 1 issue steps up to t0 + UNROLL + S - 2 < kfull
+    for (; t0 + UNROLL + S - 2 < kfull; t0 += UNROLL) {
+      static_for([&](auto I) { step(I, std::false_type{}, t0 + decltype(I)::value); },
+                 std::make_index_sequence<UNROLL>{});
+    }
+    for (; t0 < nk; t0 += UNROLL) {
+      static_for([&](auto I) {
+        if (t0 + decltype(I)::value < nk) step(I, std::true_type{}, t0 + decltype(I)::value);
+      }, std::make_index_sequence<UNROLL>{});
+    }
+  } else {
+    // Sub-step ring (RING = 1, 16-bit B): the LDS reads run one 16-column
+    // sub-step ahead of the MFMAs instead of one step, so a wave holds two
+    // sub-steps of operands (not two steps) and large wave tiles fit in the
+    // register file.  Sub-step s of step t is read while sub-step s - 1
+    // computes; before the MFMAs of sub-step 3 a wave waits for its DMA of
+    // step t + 1 and its reads of step t, meets the others at the barrier,
+    // refills stage t % S (now unread) with step t + S and reads sub-step 0
+    // of step t + 1.
+    static_assert(!I8, "the sub-step ring reads 16-bit B tiles");
+    struct Sub {
+      u32x4 a[FM];
+      u32x4 b[NB][FN];
+    };
+    auto read_one = [&](auto I, Sub& f, int s) {
+      const uint8_t* abase = stage_ptr<decltype(I)::value, C::STAGE>();
+#pragma unroll
+      for (int i = 0; i < FM; ++i) f.a[i] = lds_read16(abase, swz16(arow0 + 32 * i, 4 * h + s));
 #pragma unroll
       for (int bi = 0; bi < NB; ++bi) {
-        u32x4 bf[FN];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if constexpr (I8) {
-            const u32x4 raw = f.b[bi][s >> 1][j];
-            bf[j] = (s & 1) ? widen8<T>(raw.z, raw.w) : widen8<T>(raw.x, raw.y);
-          } else {
-            bf[j] = f.b[bi][s][j];
-          }
-        }
+        for (int j = 0; j < FN; ++j)
+          f.b[bi][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz16(brow0 + 32 * j, 4 * h + s));
+      }
+    };
+    auto mfma_one = [&](const Sub& f) {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
-          for (int j = 0; j < FN; ++j) acc[bi][i][j] = mfma32<T>(bf[j], f.a[s][i], acc[bi][i][j]);
+          for (int j = 0; j < FN; ++j) acc[bi][i][j] = mfma32<T>(f.b[bi][j], f.a[i], acc[bi][i][j]);
         }
       }
-    }
-  };
-
-  // Pipeline.  Step t computes from registers read out of stage t % S one
-  // step earlier.  In step t a wave refills stage (t - 1) % S, which every
-  // wave finished reading before the previous barrier, with step t + S - 1;
-  // waits for its own DMA of step t + 1 (the later steps stay in flight) and
-  // for its LDS reads of step t; meets the other waves at the barrier -- all
-  // of step t + 1 is now in LDS -- issues the LDS reads of step t + 1 and runs
-  // the MFMAs of step t while they land.
-  Frags fr[2];
-  static_for([&](auto I) {
-    if (decltype(I)::value < nk) issue(I, decltype(I)::value);
-  }, std::make_index_sequence<S - 1>{});
-  if (S - 2 < nk) wait_vmcnt<(S - 2) * C::P>();
-  else wait_vmcnt<0>();
-  wait_lgkmcnt0();
-  lds_barrier();
-  read_frags(std::integral_constant<int, 0>{}, fr[0]);
-
-  constexpr int UNROLL = lcm_c(S, 2);  // stage and fragment-set indices known at compile time
-  // One step; GUARD = false where every condition is known to hold (all
-  // steps it touches are full 64-column steps inside k), so the main loop has
-  // no branches and the compiler's own wait-count tracking stays exact.
-  auto step = [&](auto I, auto GUARD, int t) {
-    constexpr int ii = decltype(I)::value, si = ii % S, pi = ii % 2;
-    constexpr bool guard = decltype(GUARD)::value;
-    if (!guard || t + S - 1 < nk) issue(std::integral_constant<int, (si + S - 1) % S>{}, t + S - 1);
-    if (!guard || t + 1 < nk) {
-      if (!guard || t + S - 1 < nk) wait_vmcnt<(S - 2) * C::P>();
-      else wait_vmcnt<0>();
-      wait_lgkmcnt0();
-      lds_barrier();
-      read_frags(std::integral_constant<int, (si + 1) % S>{}, fr[pi ^ 1]);
-    }
-    // keep the LDS reads of step t + 1 ahead of the MFMAs of step t, and the
-    // MFMAs ahead of the next step's waits and barrier
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_frags(fr[pi]);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  int t0 = 0;
-  // main loop: steps t0 .. t0 + UNROLL - 1 issue steps up to t0 + UNROLL + S - 2 < kfull
-  for (; t0 + UNROLL + S - 2 < kfull; t0 += UNROLL) {
-    static_for([&](auto I) { step(I, std::false_type{}, t0 + decltype(I)::value); },
-               std::make_index_sequence<UNROLL>{});
-  }
-  for (; t0 < nk; t0 += UNROLL) {
+    };
+    Sub rf[2];
     static_for([&](auto I) {
-      if (t0 + decltype(I)::value < nk) step(I, std::true_type{}, t0 + decltype(I)::value);
-    }, std::make_index_sequence<UNROLL>{});
+      if (decltype(I)::value < nk) issue(I, decltype(I)::value);
+    }, std::make_index_sequence<S>{});
+    if (S - 1 < nk) wait_vmcnt<(S - 1) * C::P>();
+    else wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    lds_barrier();
+    read_one(std::integral_constant<int, 0>{}, rf[0], 0);
+    auto rstep = [&](auto I, auto GUARD, int t) {
+      constexpr int si = decltype(I)::value % S;
+      constexpr bool guard = decltype(GUARD)::value;
+      const bool more = !guard || t + 1 < nk;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (s < 3) {
+          read_one(std::integral_constant<int, si>{}, rf[(s + 1) & 1], s + 1);
+        } else if (more) {
+          if (!guard || t + S - 1 < nk) wait_vmcnt<(S - 2) * C::P>();
+          else wait_vmcnt<0>();
+          wait_lgkmcnt0();
+          lds_barrier();
+          if (!guard || t + S < nk) issue(std::integral_constant<int, si>{}, t + S);
+          read_one(std::integral_constant<int, (si + 1) % S>{}, rf[0], 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_one(rf[s & 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // main loop: steps t0 .. t0 + S - 1 issue steps up to t0 + 2 S - 1 < kfull
+    for (; t0 + 2 * S - 1 < kfull; t0 += S) {
+      static_for([&](auto I) { rstep(I, std::false_type{}, t0 + decltype(I)::value); }, std::make_index_sequence<S>{});
+    }
+    for (; t0 < nk; t0 += S) {
+      static_for([&](auto I) {
+        if (t0 + decltype(I)::value < nk) rstep(I, std::true_type{}, t0 + decltype(I)::value);
+      }, std::make_index_sequence<S>{});
+    }
   }
 
   // Epilogue.  The MFMAs take the weights as their first operand, so D of a

@@ -77,6 +77,8 @@ def _check_vs_oracle(orc, got16, got32, x, wg, wu, dt):
     (64, 1536, 1000, F16), (200, 640, 10240, BF16), (300, 1552, 520, F16), (257, 96, 333, BF16),
     # 17 - 64 rows: the small tiled shapes (32 x 64, 32 x 128 for n_out > 10000, 64 x 64)
     (20, 256, 16400, BF16), (24, 1536, 8960, F16), (40, 256, 4000, F16), (63, 136, 72, BF16),
+    # > 1024 rows: 256 x 128 tiles on the sub-step ring (main loop and k tail; tail only)
+    (1100, 1000, 300, F16), (1030, 72, 130, BF16),
 ])
 def test_gate_up_silu_matches_oracle(pkg, orc, cuda, rows, k, n, dt):
     x, wg, wu = _inputs(rows, k, n, dt, seed=80 + rows)
@@ -210,6 +212,21 @@ def test_prefill_shapes_against_torch_fp64(pkg, cuda, rows, k, n, dt):
     assert float(((got16 - exact).abs() - (ulp + bound + 2.0 ** -22 * exact.abs())).max()) <= 0
     # the 16-bit output is the fp32 output rounded once
     assert torch.equal(got16.to(dt), got32.to(dt))
+
+
+def test_tiled_launch_shapes_agree_bitwise(pkg, cuda):
+    """Every tiled launch shape (33 .. 1025 rows here: 64 x 64, 128 x 64,
+    256 x 64 and the 256 x 128 sub-step ring) adds the k products in the same
+    order, so a prefix of the rows gives the same bits whichever shape runs."""
+    torch.manual_seed(5)
+    k, n = 1536, 8960
+    x = torch.randn(1025, k, device=cuda).to(F16)
+    wg = (torch.randn(n, k, device=cuda) * (2.0 * k ** -0.5)).to(F16)
+    wu = (torch.randn(n, k, device=cuda) * k ** -0.5).to(F16)
+    full = pkg.fused_gate_up_silu(x, wg, wu, out_dtype=F32)
+    for rows in (33, 64, 65, 256, 257, 1024):
+        part = pkg.fused_gate_up_silu(x[:rows], wg, wu, out_dtype=F32)
+        assert torch.equal(part, full[:rows]), f"{rows} rows differ from the 1025-row launch"
 
 
 def test_fused_mlp_opt_in_takes_the_fused_kernel(pkg, cuda, monkeypatch):
