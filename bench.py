@@ -402,16 +402,24 @@ KNOWN_LAUNCHES = {
     ("linear16_skinny<mi355::BF16, mi355::BF16, 1, 2, 2>", 224 * 512): (
         "16-bit linear, 8 rows, [3584,18944] weights, bf16 (7B down)", 3584 * 18944 * 2 + 8 * 18944 * 2 + 8 * 3584 * 2),
     # MFMA-bound prefill GEMMs: (label, algorithmic bytes, flops)
-    ("tiled_gemm<mi355::F16, 0, mi355::F16, 4, 2, 2, 1, 1, 3>", 560 * 512): (
-        "gate/up + SiLU-and-mul prefill, 1024 rows, [8960,1536] weights, fp16",
-        2 * 8960 * 1536 * 2 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 4 * 1024 * 1536 * 8960),
-    ("tiled_gemm<mi355::F16, 0, mi355::F16, 4, 2, 2, 1, 1, 3>", 2240 * 512): (
-        "gate/up + SiLU-and-mul prefill, 4096 rows, [8960,1536] weights, fp16",
-        2 * 8960 * 1536 * 2 + 4096 * 1536 * 2 + 4096 * 8960 * 2, 4 * 4096 * 1536 * 8960),
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 2, 1, 0, 4>", 1120 * 256): (
+    # (the 1.5B gate/up at 1024 and 4096 rows runs as a column split: whole
+    # rounds of 256 x 128 tiles over the first 8192 columns, then 768 columns)
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 4, 4, 1, 1, 2, 1>", 256 * 512): (
+        "gate/up + SiLU-and-mul prefill, 1024 rows, first 8192 of 8960 columns, fp16",
+        2 * 8192 * 1536 * 2 + 1024 * 1536 * 2 + 1024 * 8192 * 2, 4 * 1024 * 1536 * 8192),
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 2, 1, 1, 1, 4, 0>", 192 * 256): (
+        "gate/up + SiLU-and-mul prefill, 1024 rows, last 768 of 8960 columns, fp16",
+        2 * 768 * 1536 * 2 + 1024 * 1536 * 2 + 1024 * 768 * 2, 4 * 1024 * 1536 * 768),
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 4, 4, 1, 1, 2, 1>", 1024 * 512): (
+        "gate/up + SiLU-and-mul prefill, 4096 rows, first 8192 of 8960 columns, fp16",
+        2 * 8192 * 1536 * 2 + 4096 * 1536 * 2 + 4096 * 8192 * 2, 4 * 4096 * 1536 * 8192),
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 2, 2, 1, 1, 2, 1>", 384 * 256): (
+        "gate/up + SiLU-and-mul prefill, 4096 rows, last 768 of 8960 columns, fp16",
+        2 * 768 * 1536 * 2 + 4096 * 1536 * 2 + 4096 * 768 * 2, 4 * 4096 * 1536 * 768),
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 2, 1, 0, 4, 0>", 1120 * 256): (
         "W8A16 prefill gate/up, 1024 rows, [8960,1536] int8, fp16",
         8960 * 1536 + 4 * 8960 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 2 * 1024 * 1536 * 8960),
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4>", 384 * 256): (
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4, 0>", 384 * 256): (
         "W8A16 prefill down, 1024 rows, [1536,8960] int8, fp16",
         1536 * 8960 + 4 * 1536 + 1024 * 8960 * 2 + 1024 * 1536 * 2, 2 * 1024 * 8960 * 1536),
 }

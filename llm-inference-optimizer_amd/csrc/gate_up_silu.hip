@@ -259,18 +259,15 @@ int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
 }
 
 // Tiled launch shapes from sweeps on MI355X (Qwen2.5-1.5B and 7B MLPs at
-// 16 - 64, 128, 1024, 1536, 2048 and 4096 rows): up to 32 rows 32 x 64
-// output tiles (2 waves) or, for n_out > 10000, 32 x 128 (4 waves); up to 64
-// rows 64 x 64 (4 waves; n_out > 10000 keeps the next shape); up to 256 rows
-// 128 x 64 (4 waves, 4 stages) or, for n_out > 10000, 128 x 128 (8 waves, 3
-// stages); up to 1024 rows 256 x 64 (8 waves, 3 stages); more rows 256 x 128
-// (8 waves of 128 x 32, 2 stages, the sub-step register ring): two thirds
-// of the operand bytes per MFMA of 256 x 64 through the DMA and three
-// quarters through LDS reads (1.5B, 4096 rows 251 -> 233 us; 7B, 2048 rows
-// 518 -> 469 us),
-// where at 1024 rows its fewer, larger tiles fill the CUs less evenly.  The
-// small shapes run 4 stages.  Descriptors span at most 256 rows of x and 128
-// weight rows, each below 2^31 bytes.
+// 16 - 64, 128 and 384 - 4096 rows): up to 32 rows 32 x 64 output tiles (2
+// waves) or, for n_out > 10000, 32 x 128 (4 waves); up to 64 rows 64 x 64 (4
+// waves; n_out > 10000 keeps the next shape); up to 128 rows 128 x 64 (4
+// waves, 4 stages) or, for n_out > 10000, 128 x 128 (8 waves, 3 stages); more
+// rows by the round count below (1.5B, 256 rows 37.9 -> 27.8 us, 384 rows
+// 48.1 -> 35.0 us, 768 rows 58.1 -> 48.7 us, 4096 rows 251 -> 233 us; 7B, 256
+// rows 118 -> 97 us, 2048 rows 518 -> 469 us).
+// The small shapes run 4 stages.  Descriptors span at most 256 rows of x and
+// 128 weight rows, each below 2^31 bytes.
 template <typename T, typename TO>
 int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
   const bool wide = p.n_out > 10000;
@@ -279,12 +276,69 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
     return gate_up_tiled_cfg<T, TO, 1, 2, 1, 1, 4>(p, s);            // 32 x 64, 2 waves
   }
   if (p.rows <= 64 && !wide) return gate_up_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);  // 64 x 64, 4 waves
-  if (p.rows <= 256) {
+  if (p.rows <= 128) {
     if (p.n_out <= 10000) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(p, s);
     return gate_up_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
   }
-  if (p.rows <= 1024) return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(p, s);
-  return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(p, s);  // 256 x 128, 8 waves, sub-step ring
+  // More rows: the plan with the fewest weighted rounds of workgroups over
+  // the CUs, in units of one round of 256 x 64 tiles (8 waves, 3 stages).
+  // One shape for the whole output: 256 x 64; 128 x 64 (4 waves, the
+  // sub-step ring at 2 stages: 64 KiB of LDS, two workgroups per CU, each
+  // with its own barriers), 1.05 a round; 256 x 128 (8 waves of 128 x 32,
+  // the sub-step ring at 2 stages), which moves two thirds of 256 x 64's
+  // operand bytes per MFMA through the DMA and three quarters through LDS
+  // reads, 1.72 a round for twice the work.  Or a column split: whole rounds
+  // of 256 x 128 tiles over the leading columns, then the remaining columns
+  // in one round of the smallest tile that covers them in one -- 64 x 64 (4
+  // waves, 0.8), 128 x 64 (4 waves, 4 stages, 1.0), 128 x 64 on the ring
+  // (two per CU, 1.05) or 256 x 64 (1.0) -- so a last, thinly filled round
+  // of large tiles becomes a full round of small ones (1.5B, 1024 rows
+  // 80.5 -> 64.6 us).  The split is two launches of one kernel on column
+  // ranges: every output element sums its k products in the same order
+  // either way.  Weights are the measured per-round times at Qwen2.5-1.5B
+  // and 7B shapes; ties keep the single launch, then 256 x 64.
+  int cus = 0;
+  const int st = compute_units(&cus);
+  if (st != MI355_OK) return st;
+  const auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+  const auto rounds = [&](int rows, int cols, int bm, int bn, int per_cu) {
+    return static_cast<double>(cdiv(cdiv(rows, bm) * cdiv(cols, bn), static_cast<int64_t>(cus) * per_cu));
+  };
+  const double c64 = rounds(p.rows, p.n_out, 256, 64, 1), c_small = 1.05 * rounds(p.rows, p.n_out, 128, 64, 2),
+               c128 = 1.72 * rounds(p.rows, p.n_out, 256, 128, 1);
+  const double single = c64 < c_small ? (c64 < c128 ? c64 : c128) : (c_small < c128 ? c_small : c128);
+
+  const int64_t per_round = cus / cdiv(p.rows, 256);  // 128-column blocks of one whole round
+  const int64_t full = per_round > 0 ? cdiv(p.n_out, 128) / per_round : 0;
+  const int lead = static_cast<int>(full * per_round * 128);  // columns in whole rounds
+  if (full >= 1 && lead < p.n_out) {
+    const int rest = p.n_out - lead;
+    const auto one_round = [&](int bm, int bn, int per_cu) { return rounds(p.rows, rest, bm, bn, per_cu) <= 1.0; };
+    int shape = 0;
+    double rest_cost = 0.0;
+    if (one_round(64, 64, 1)) shape = 1, rest_cost = 0.8;
+    else if (one_round(128, 64, 1)) shape = 2, rest_cost = 1.0;
+    else if (one_round(128, 64, 2)) shape = 3, rest_cost = 1.05;
+    else if (one_round(256, 64, 1)) shape = 4, rest_cost = 1.0;
+    if (shape != 0 && 1.72 * static_cast<double>(full) + rest_cost < single) {
+      GateUpParams head = p, tail = p;
+      head.n_out = lead;
+      tail.n_out = rest;
+      const int64_t wskip = static_cast<int64_t>(lead) * p.ws * static_cast<int64_t>(sizeof(typename T::bits));
+      tail.wg = static_cast<const uint8_t*>(p.wg) + wskip;
+      tail.wu = static_cast<const uint8_t*>(p.wu) + wskip;
+      tail.out = static_cast<uint8_t*>(p.out) + static_cast<int64_t>(lead) * static_cast<int64_t>(sizeof(typename TO::bits));
+      const int r = gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(head, s);
+      if (r != MI355_OK) return r;
+      if (shape == 1) return gate_up_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(tail, s);
+      if (shape == 2) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(tail, s);
+      if (shape == 3) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 2, 1>(tail, s);
+      return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(tail, s);
+    }
+  }
+  if (c64 == single) return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(p, s);
+  if (c_small == single) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 2, 1>(p, s);
+  return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(p, s);
 }
 
 template <typename T, typename TO>

@@ -77,7 +77,7 @@ def _check_vs_oracle(orc, got16, got32, x, wg, wu, dt):
     (64, 1536, 1000, F16), (200, 640, 10240, BF16), (300, 1552, 520, F16), (257, 96, 333, BF16),
     # 17 - 64 rows: the small tiled shapes (32 x 64, 32 x 128 for n_out > 10000, 64 x 64)
     (20, 256, 16400, BF16), (24, 1536, 8960, F16), (40, 256, 4000, F16), (63, 136, 72, BF16),
-    # > 1024 rows: 256 x 128 tiles on the sub-step ring (main loop and k tail; tail only)
+    # > 128 rows, few tiles: 256 x 64 (main loop and k tail; tail only)
     (1100, 1000, 300, F16), (1030, 72, 130, BF16),
 ])
 def test_gate_up_silu_matches_oracle(pkg, orc, cuda, rows, k, n, dt):
@@ -190,7 +190,13 @@ def test_large_shape_against_torch_fp64(pkg, cuda):
     assert rel < 1e-5
 
 
-@pytest.mark.parametrize("rows,k,n,dt", [(1024, 1536, 8960, F16), (2048, 3584, 4736, BF16)])
+@pytest.mark.parametrize("rows,k,n,dt", [
+    (1024, 1536, 8960, F16), (2048, 3584, 4736, BF16),
+    # ragged rows, k and n on the sub-step ring: 128 x 64 tiles two per CU,
+    # then 256 x 128 tiles, then a column split (6528 columns in 256 x 128
+    # tiles, the last 72 in 64 x 64)
+    (300, 264, 8200, BF16), (520, 264, 8000, F16), (1030, 264, 6600, F16),
+])
 def test_prefill_shapes_against_torch_fp64(pkg, cuda, rows, k, n, dt):
     """Prefill-sized batches (the tiled GEMM path) against fp64 GEMMs on the
     GPU: every output within one output ulp plus the fp32 summation bound,
@@ -215,18 +221,20 @@ def test_prefill_shapes_against_torch_fp64(pkg, cuda, rows, k, n, dt):
 
 
 def test_tiled_launch_shapes_agree_bitwise(pkg, cuda):
-    """Every tiled launch shape (33 .. 1025 rows here: 64 x 64, 128 x 64,
-    256 x 64 and the 256 x 128 sub-step ring) adds the k products in the same
-    order, so a prefix of the rows gives the same bits whichever shape runs."""
+    """Every tiled launch shape (33 .. 1536 rows of the 1.5B MLP: 64 x 64,
+    128 x 64 on 4 stages and on the sub-step ring, 256 x 64, 256 x 128 on the
+    ring, and the column splits at 1024 and 1025 rows) adds the k products in
+    the same order, so a prefix of the rows gives the same bits whichever
+    shape runs."""
     torch.manual_seed(5)
     k, n = 1536, 8960
-    x = torch.randn(1025, k, device=cuda).to(F16)
+    x = torch.randn(1536, k, device=cuda).to(F16)
     wg = (torch.randn(n, k, device=cuda) * (2.0 * k ** -0.5)).to(F16)
     wu = (torch.randn(n, k, device=cuda) * k ** -0.5).to(F16)
     full = pkg.fused_gate_up_silu(x, wg, wu, out_dtype=F32)
-    for rows in (33, 64, 65, 256, 257, 1024):
+    for rows in (33, 64, 65, 256, 257, 1024, 1025):
         part = pkg.fused_gate_up_silu(x[:rows], wg, wu, out_dtype=F32)
-        assert torch.equal(part, full[:rows]), f"{rows} rows differ from the 1025-row launch"
+        assert torch.equal(part, full[:rows]), f"{rows} rows differ from the 1536-row launch"
 
 
 def test_fused_mlp_opt_in_takes_the_fused_kernel(pkg, cuda, monkeypatch):
