@@ -27,9 +27,9 @@
 // flight), meets the other waves at one barrier, then alternates the MFMAs
 // of this step's sub-steps, whose operands it read one step earlier, with
 // the LDS reads of the next step's, so LDS latency hides behind the MFMAs.
-// The sub-step ring (RING = 1, 16-bit B, S = 2 allowed) reads one 16-column
-// sub-step ahead instead of one step, so a wave holds two sub-steps of
-// operands rather than two steps and a 128 x 32 wave tile of both B
+// The sub-step ring (RING = 1, S = 2 allowed) reads one 16-column sub-step
+// ahead instead of one step, so a wave holds two sub-steps of operands
+// rather than two steps and, e.g., a 128 x 32 wave tile of two 16-bit B
 // matrices fits in the register file next to its 128 accumulators; its
 // barrier sits before the last sub-step's MFMAs.  Both loops are unrolled so
 // stage and register-set indices are compile-time constants and have no
@@ -429,41 +429,59 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       }, std::make_index_sequence<UNROLL>{});
     }
   } else {
-    // Sub-step ring (RING = 1, 16-bit B): the LDS reads run one 16-column
-    // sub-step ahead of the MFMAs instead of one step, so a wave holds two
-    // sub-steps of operands (not two steps) and large wave tiles fit in the
-    // register file.  Sub-step s of step t is read while sub-step s - 1
-    // computes; before the MFMAs of sub-step 3 a wave waits for its DMA of
-    // step t + 1 and its reads of step t, meets the others at the barrier,
-    // refills stage t % S (now unread) with step t + S and reads sub-step 0
-    // of step t + 1.
-    static_assert(!I8, "the sub-step ring reads 16-bit B tiles");
+    // Sub-step ring (RING = 1): the LDS reads run one 16-column sub-step
+    // ahead of the MFMAs instead of one step, so a wave holds two sub-steps
+    // of operands (not two steps) and large wave tiles fit in the register
+    // file.  Sub-step s of step t is read while sub-step s - 1 computes;
+    // before the MFMAs of sub-step 3 a wave waits for its DMA of step t + 1
+    // and its reads of step t, meets the others at the barrier, refills
+    // stage t % S (now unread) with step t + S and reads sub-step 0 of step
+    // t + 1.  A pieces alternate between two register sets by sub-step; an
+    // int8 B read (16 bytes: sub-steps 2q and 2q + 1 of k-group h) is made
+    // with sub-step 2q's A read and B sets alternate by pair q, so a read
+    // never lands in a set that a pending MFMA still reads.
     struct Sub {
-      u32x4 a[FM];
-      u32x4 b[NB][FN];
+      u32x4 a[2][FM];
+      u32x4 b[2][NB][FN];
     };
     auto read_one = [&](auto I, Sub& f, int s) {
       const uint8_t* abase = stage_ptr<decltype(I)::value, C::STAGE>();
 #pragma unroll
-      for (int i = 0; i < FM; ++i) f.a[i] = lds_read16(abase, swz16(arow0 + 32 * i, 4 * h + s));
+      for (int i = 0; i < FM; ++i) f.a[s & 1][i] = lds_read16(abase, swz16(arow0 + 32 * i, 4 * h + s));
 #pragma unroll
       for (int bi = 0; bi < NB; ++bi) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          f.b[bi][j] = lds_read16(abase + C::A_BYTES + bi * C::B_BYTES, swz16(brow0 + 32 * j, 4 * h + s));
-      }
-    };
-    auto mfma_one = [&](const Sub& f) {
-#pragma unroll
-      for (int bi = 0; bi < NB; ++bi) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-          for (int j = 0; j < FN; ++j) acc[bi][i][j] = mfma32<T>(f.b[bi][j], f.a[i], acc[bi][i][j]);
+        for (int j = 0; j < FN; ++j) {
+          const uint8_t* bbase = abase + C::A_BYTES + bi * C::B_BYTES;
+          if constexpr (I8) {
+            if ((s & 1) == 0) f.b[(s >> 1) & 1][bi][j] = lds_read16(bbase, swz8(brow0 + 32 * j, 2 * h + (s >> 1)));
+          } else {
+            f.b[s & 1][bi][j] = lds_read16(bbase, swz16(brow0 + 32 * j, 4 * h + s));
+          }
         }
       }
     };
-    Sub rf[2];
+    auto mfma_one = [&](const Sub& f, int s) {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
+        u32x4 bf[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (I8) {
+            const u32x4 raw = f.b[(s >> 1) & 1][bi][j];
+            bf[j] = (s & 1) ? widen8<T>(raw.z, raw.w) : widen8<T>(raw.x, raw.y);
+          } else {
+            bf[j] = f.b[s & 1][bi][j];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[bi][i][j] = mfma32<T>(bf[j], f.a[s & 1][i], acc[bi][i][j]);
+        }
+      }
+    };
+    Sub rf;
     static_for([&](auto I) {
       if (decltype(I)::value < nk) issue(I, decltype(I)::value);
     }, std::make_index_sequence<S>{});
@@ -471,7 +489,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     else wait_vmcnt<0>();
     wait_lgkmcnt0();
     lds_barrier();
-    read_one(std::integral_constant<int, 0>{}, rf[0], 0);
+    read_one(std::integral_constant<int, 0>{}, rf, 0);
     auto rstep = [&](auto I, auto GUARD, int t) {
       constexpr int si = decltype(I)::value % S;
       constexpr bool guard = decltype(GUARD)::value;
@@ -480,17 +498,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       for (int s = 0; s < 4; ++s) {
         __builtin_amdgcn_sched_barrier(0);
         if (s < 3) {
-          read_one(std::integral_constant<int, si>{}, rf[(s + 1) & 1], s + 1);
+          read_one(std::integral_constant<int, si>{}, rf, s + 1);
         } else if (more) {
           if (!guard || t + S - 1 < nk) wait_vmcnt<(S - 2) * C::P>();
           else wait_vmcnt<0>();
           wait_lgkmcnt0();
           lds_barrier();
           if (!guard || t + S < nk) issue(std::integral_constant<int, si>{}, t + S);
-          read_one(std::integral_constant<int, (si + 1) % S>{}, rf[0], 0);
+          read_one(std::integral_constant<int, (si + 1) % S>{}, rf, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        mfma_one(rf[s & 1]);
+        mfma_one(rf, s);
       }
       __builtin_amdgcn_sched_barrier(0);
     };

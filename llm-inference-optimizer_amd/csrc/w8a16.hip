@@ -425,7 +425,7 @@ bool tiled_fits(const W8Params& p, bool dual) {
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
-template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8>
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8, int RING = 0>
 int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_I8, TO, WGM, WGN, FM, FN, EPI, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
@@ -451,48 +451,73 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
-                                                                                      EPI, S>),
+                                                                                      EPI, S, RING>),
                                     dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
                     "w8a16 tiled launch");
 }
 
-// Tile shape by the number T of 128 x 128 output tiles, from a sweep of tile
-// shapes x waves x LDS stages on MI355X over the q/o, k/v, gate/up and down
-// projections of Qwen2.5-1.5B and 7B at 128, 1024 and 4096 rows (every pick
-// within 5% of the best sampled configuration but one, 1024 rows x k 8960,
-// at 1.05x):
+// Outside the ring's range (below), the step pipeline's tile shape by the
+// number T of 128 x 128 output tiles, from a sweep of tile shapes x waves x
+// LDS stages on MI355X over the q/o, k/v, gate/up and down projections of
+// Qwen2.5-1.5B and 7B at 128, 1024 and 4096 rows (every pick within 5% of
+// the best sampled configuration but one, 1024 rows x k 8960, at 1.05x):
 //   T < 128 -> 64 x 64 tiles, 4 waves, 4 stages (the most workgroups);
-//   T < 320 -> 128 x 128, 8 waves, 3 stages;
-//   n <= 2048 -> 128 x 256, 8 waves, 4 stages;
-//   T < 1000 -> 128 x 64, 4 waves, 4 stages;
-//   T < 2000 -> 128 x 128, 4 waves, 3 stages;
-//   else -> 128 x 256, 8 waves, 3 stages.
+//   T < 320, or n > 2048 (fewer than two ring tiles per CU) -> 128 x 128,
+//     8 waves, 3 stages;
+//   else (n <= 2048) -> 128 x 256, 8 waves, 4 stages.
 // bf16 takes 128 x 128 where fp16 takes 128 x 256: its widening needs more
 // registers, and the 128 x 256 shape would spill.
 template <typename T, typename TO>
-int w8_tiled(const W8Params& p, hipStream_t s) {
+int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
   constexpr bool wide = std::is_same<T, F16>::value;
+  // Wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring
+  // (2 stages) at the shape whose busiest CU finishes first -- ceil(tiles /
+  // CUs) times the cost of one tile of 128 x 64 (4 waves, 40 KiB of LDS, four
+  // workgroups per CU), 256 x 128 (8 waves of 128 x 32, two per CU) or
+  // 256 x 256 (8 waves of 64 x 128), measured 1 : 3.33 : 6.4 at the
+  // Qwen2.5-1.5B and 7B gate/up and down projections (1.5B gate 512 rows
+  // 34.9 -> 26.2 us, 7B down 4096 rows 641 -> 522 us).  Fewer tiles keep the
+  // rule below, whose smaller grids spread better.
+  if (p.n > 2048) {
+    const auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+    const int64_t t_small = cdiv(p.rows, 128) * cdiv(p.n, 64);
+    if (t_small >= 2 * static_cast<int64_t>(cus)) {
+      const double c_small = static_cast<double>(cdiv(t_small, cus));
+      const double c_mid = 3.33 * static_cast<double>(cdiv(cdiv(p.rows, 256) * cdiv(p.n, 128), cus));
+      const double c_big = 6.4 * static_cast<double>(cdiv(cdiv(p.rows, 256) * cdiv(p.n, 256), cus));
+      if (c_small <= c_mid && c_small <= c_big) return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, tiled::EPI_W8, 1>(p, s);
+      if (c_mid <= c_big) return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, tiled::EPI_W8, 1>(p, s);
+      return w8_tiled_cfg<T, TO, 4, 2, 2, 4, 2, tiled::EPI_W8, 1>(p, s);
+    }
+  }
   const int64_t t128 = static_cast<int64_t>((p.rows + 127) / 128) * ((p.n + 127) / 128);
   if (t128 < 128) return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);
-  if (t128 < 320) return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
-  if (p.n <= 2048) {
-    if constexpr (wide) return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 4>(p, s);
-    else return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
-  }
-  if (t128 < 1000) return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(p, s);
-  if (t128 < 2000) return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 3>(p, s);
-  if constexpr (wide) return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 3>(p, s);
+  if (t128 < 320 || p.n > 2048) return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
+  if constexpr (wide) return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 4>(p, s);
   else return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);
 }
 
-// The dual (gate/up + SiLU-and-mul) tiled GEMM: up to 256 rows and n <= 10000
-// 128 x 64 tiles (4 waves, 4 stages), else 128 x 128 (8 waves, 3 stages; fp16) --
-// the 16-bit gate/up GEMM's shapes, less its 256 x 64 one, whose 4 KiB int8
-// B tile does not split into the 8 waves' 1 KiB DMA instructions.
-// bf16 keeps the 128 x 64 shape throughout (its widening needs more
-// registers; 128 x 128 at 8 waves would spill).
+// The dual (gate/up + SiLU-and-mul) tiled GEMM: more than 256 rows by the
+// round count below; else, up to n = 10000, 128 x 64 tiles (4 waves, 4
+// stages), beyond 128 x 128 (8 waves, 3 stages; fp16) -- the 16-bit gate/up
+// GEMM's step-pipeline shapes, less its 256 x 64 one, whose 4 KiB int8 B
+// tile does not split into the 8 waves' 1 KiB DMA instructions.  bf16 keeps
+// the 128 x 64 shape there (its widening needs more registers; 128 x 128 at
+// 8 waves would spill).
 template <typename T, typename TO>
-int w8_tiled_dual(const W8Params& p, hipStream_t s) {
+int w8_tiled_dual(const W8Params& p, hipStream_t s, int cus) {
+  // More than 256 rows: the sub-step ring (2 stages), 128 x 64 tiles (4
+  // waves, 48 KiB of LDS, three workgroups per CU) or 256 x 128 (8 waves of
+  // 128 x 32), whichever takes fewer rounds, a round of 256 x 128 weighted
+  // 1.28 (measured at the Qwen2.5-1.5B and 7B MLPs, 512 - 4096 rows: 1.5B
+  // 1024 rows 90.8 -> 70.2 us, 7B 2048 rows 719 -> 494 us).
+  if (p.rows > 256) {
+    const auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+    const double c_small = static_cast<double>(cdiv(cdiv(p.rows, 128) * cdiv(p.n, 64), 3 * static_cast<int64_t>(cus)));
+    const double c_big = 1.28 * static_cast<double>(cdiv(cdiv(p.rows, 256) * cdiv(p.n, 128), cus));
+    if (c_small <= c_big) return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, tiled::EPI_SILU_W8, 1>(p, s);
+    return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, tiled::EPI_SILU_W8, 1>(p, s);
+  }
   if constexpr (std::is_same<T, F16>::value) {
     if (p.rows > 256 || p.n > 10000) return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_SILU_W8>(p, s);
   }
@@ -546,8 +571,8 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   if (g_force_path > 0) skinny = g_force_path == 1;
 #endif
   if (skinny) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);
-  if constexpr (DUAL) return w8_tiled_dual<T, TO>(p, s);
-  else return w8_tiled<T, TO>(p, s);
+  if constexpr (DUAL) return w8_tiled_dual<T, TO>(p, s, cus);
+  else return w8_tiled<T, TO>(p, s, cus);
 }
 
 }  // namespace

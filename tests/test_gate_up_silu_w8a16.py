@@ -124,9 +124,13 @@ def test_graph_replays_match_eager(pkg, cuda, rows):
         assert torch.equal(out, want), f"replay {i} differs from eager"
 
 
-def test_prefill_shape_against_torch_fp64(pkg, cuda):
-    rows, k, n = 2048, 3584, 4736
-    x, qg, sg, qu, su = _inputs(rows, k, n, BF16, 21, cuda, pkg)
+@pytest.mark.parametrize("rows,k,n,dt", [
+    (2048, 3584, 4736, BF16),   # 128 x 64 tiles on the sub-step ring
+    (1024, 1536, 18944, BF16),  # 256 x 128 tiles on the ring
+    (1030, 272, 18900, F16),    # 256 x 128, ragged rows and n, k tail
+])
+def test_prefill_shape_against_torch_fp64(pkg, cuda, rows, k, n, dt):
+    x, qg, sg, qu, su = _inputs(rows, k, n, dt, 21, cuda, pkg)
     got16 = pkg.fused_gate_up_silu_w8a16(x, qg, sg, qu, su).double()
     got32 = pkg.fused_gate_up_silu_w8a16(x, qg, sg, qu, su, out_dtype=F32).double()
     x64 = x.double()
@@ -137,9 +141,22 @@ def test_prefill_shape_against_torch_fp64(pkg, cuda):
     exact = torch.nn.functional.silu(g) * u
     bound = torch.from_numpy(act_error_bound(g.cpu().numpy(), u.cpu().numpy(), gabs.cpu().numpy(),
                                              uabs.cpu().numpy(), k)).to(cuda)
-    ulp = torch.from_numpy(ulp16(exact.cpu().numpy(), BF16)).to(cuda)
+    ulp = torch.from_numpy(ulp16(exact.cpu().numpy(), dt)).to(cuda)
     assert float(((got32 - exact).abs() - (2.0 ** -22 * exact.abs() + bound)).max()) <= 1e-30
     assert float(((got16 - exact).abs() - (ulp + bound + 2.0 ** -22 * exact.abs())).max()) <= 0
+    assert torch.equal(got16.to(dt), got32.to(dt))
+
+
+def test_tiled_launch_shapes_agree_bitwise(pkg, cuda):
+    """The dual tiled shapes (64 .. 1024 rows of a 7B-wide MLP: 64 x 64, the
+    step pipeline's 128 x 64, 128 x 64 and 256 x 128 on the sub-step ring)
+    add the k products in the same order: row prefixes give the same bits."""
+    rows, k, n = 1024, 1536, 18944
+    x, qg, sg, qu, su = _inputs(rows, k, n, F16, 31, cuda, pkg)
+    full = pkg.fused_gate_up_silu_w8a16(x, qg, sg, qu, su, out_dtype=F32)
+    for r in (64, 256, 257):
+        part = pkg.fused_gate_up_silu_w8a16(x[:r], qg, sg, qu, su, out_dtype=F32)
+        assert torch.equal(part, full[:r]), f"{r} rows differ from the {rows}-row launch"
 
 
 def test_quantized_fused_mlp_takes_the_int8_kernel(pkg, cuda, monkeypatch):

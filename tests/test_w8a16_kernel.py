@@ -135,14 +135,17 @@ def test_bf16_matches_oracle(pkg, orc, cuda, M, K, N, bias):
 # number of 128 x 128 output tiles), with k tails and ragged edges.
 TILED_CASES = [
     (300, 1552, 1000, F16, True),     # < 128 tiles: 64 x 64
-    (512, 512, 8960, F16, False),     # < 320: 128 x 128, 8 waves
+    (320, 512, 8960, F16, False),     # < 320: 128 x 128, 8 waves
     (200, 2048, 8960, BF16, True),    # <= 256 rows but a large grid: tiled, 128 x 128
     (4096, 256, 1536, F16, True),     # n <= 2048: 128 x 256
     (4096, 256, 1536, BF16, False),   # (bf16: 128 x 128)
-    (1024, 272, 8960, BF16, False),   # < 1000: 128 x 64
-    (2048, 128, 8952, F16, False),    # < 2000: 128 x 128, 4 waves
-    (4096, 64, 8960, F16, True),      # the rest: 128 x 256
-    (4096, 80, 9000, BF16, True),     # (bf16: 128 x 128)
+    # n > 2048 with >= 2 tiles of 128 x 64 per CU: the sub-step ring
+    (512, 512, 8960, F16, False),     # 128 x 64, 4 waves (main loop and k tail)
+    (1024, 272, 8960, BF16, False),   # 128 x 64
+    (2048, 128, 8952, F16, False),    # 128 x 64, ragged n
+    (4096, 64, 8960, F16, True),      # 256 x 128, 8 waves
+    (4096, 80, 9000, BF16, True),     # 256 x 128, ragged n, k tail only
+    (4096, 32, 3584, BF16, True),     # 256 x 256, 8 waves
     # 17 - 64 rows with >= 128 tile columns: the small tiled shapes
     (24, 1536, 8960, F16, True),      # 32 x 64
     (20, 256, 16400, BF16, False),    # n > 10000: 32 x 128
@@ -243,6 +246,21 @@ def test_quantizer_row_strided_weight(pkg, orc, cuda):
     assert torch.equal(q, q2) and torch.equal(s, s2)
 
 
+def test_tiled_launch_shapes_agree_bitwise(pkg, cuda):
+    """Every tiled shape (160 .. 4096 rows, n = 3584: 64 x 64 and 128 x 128
+    on the step pipeline, 128 x 64, 256 x 128 and 256 x 256 on the sub-step
+    ring) adds the k products in the same order: row prefixes of one input
+    give the same bits whichever shape runs."""
+    K, N = 1024, 3584
+    lin = _linear(K, N, True, cuda, dtype=F16, seed=41)
+    q = pkg.QuantizedLinearInt8.from_linear(lin)
+    x = _x(4096, K, F16, cuda, seed=42)
+    full = pkg.w8a16_linear(x, q.weight_q, q.scale, q.bias, out_dtype=F32)
+    for r in (160, 600, 1200, 2048):
+        part = pkg.w8a16_linear(x[:r], q.weight_q, q.scale, q.bias, out_dtype=F32)
+        assert torch.equal(part, full[:r]), f"{r} rows differ from the 4096-row launch"
+
+
 def test_strided_views_give_identical_bits(pkg, cuda):
     M, K, N = 12, 1536, 896
     lin = _linear(K, N, True, cuda, seed=3)
@@ -318,7 +336,9 @@ def test_graph_replays_match_eager(pkg, cuda, M):
         assert torch.equal(out, want), f"replay {i} differs from eager"
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 3584, 18944), (32, 18944, 3584), (512, 3584, 4608)])
+@pytest.mark.parametrize("M,K,N", [(8, 3584, 18944), (32, 18944, 3584), (512, 3584, 4608),
+                                   # the sub-step ring's 256 x 128 and 256 x 256 tiles with a main loop
+                                   (2048, 3584, 3584), (4096, 1024, 3584)])
 def test_qwen7b_shapes_against_fp64(pkg, orc, cuda, M, K, N):
     lin = _linear(K, N, False, cuda, dtype=BF16, seed=17)
     q = pkg.QuantizedLinearInt8.from_linear(lin)
