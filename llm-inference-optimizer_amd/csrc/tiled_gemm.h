@@ -109,9 +109,6 @@ __device__ __forceinline__ uint32_t swz8(uint32_t r, uint32_t c) {
 __device__ __forceinline__ u32x4 lds_read16(const uint8_t* base, uint32_t off) {
   return *reinterpret_cast<const u32x4*>(base + off);
 }
-__device__ __forceinline__ void lds_write16(uint8_t* base, uint32_t off, u32x4 v) {
-  *reinterpret_cast<u32x4*>(base + off) = v;
-}
 
 struct Params {
   const void* x;      // [rows, xs] of T

@@ -418,10 +418,10 @@ int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
 
 // ------------------------------------------------------------------- tiled
 
-// Buffer descriptors of the tiled GEMM span at most 128 rows of x (256 for
-// the dual kernel) and 256 weight rows; both must stay below 2^31 bytes.
-bool tiled_fits(const W8Params& p, bool dual) {
-  return int64_t{dual ? 256 : 128} * p.xs * 2 < (int64_t{1} << 31) && int64_t{256} * p.qs < (int64_t{1} << 31) &&
+// Buffer descriptors of the tiled GEMM span at most 256 rows of x and 256
+// weight rows; both must stay below 2^31 bytes.
+bool tiled_fits(const W8Params& p, bool) {
+  return int64_t{256} * p.xs * 2 < (int64_t{1} << 31) && int64_t{256} * p.qs < (int64_t{1} << 31) &&
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
