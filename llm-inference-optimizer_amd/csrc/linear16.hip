@@ -279,7 +279,7 @@ bool l16_tiled_fits(const L16Params& p) {
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
-template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S>
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int RING = 0>
 int l16_tiled_cfg(const L16Params& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_16, TO, WGM, WGN, FM, FN, tiled::EPI_LINEAR, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
@@ -303,7 +303,7 @@ int l16_tiled_cfg(const L16Params& p, hipStream_t s) {
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_16, TO, WGM, WGN, FM, FN,
-                                                                                      tiled::EPI_LINEAR, S>),
+                                                                                      tiled::EPI_LINEAR, S, RING>),
                                     dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
                     "linear16 tiled launch");
 }
