@@ -416,7 +416,7 @@ KNOWN_LAUNCHES = {
     ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 2, 2, 1, 1, 2, 1>", 384 * 256): (
         "gate/up + SiLU-and-mul prefill, 4096 rows, last 768 of 8960 columns, fp16",
         2 * 768 * 1536 * 2 + 4096 * 1536 * 2 + 4096 * 768 * 2, 4 * 4096 * 1536 * 768),
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 2, 1, 0, 4, 0>", 1120 * 256): (
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 2, 1, 0, 2, 1>", 1120 * 256): (
         "W8A16 prefill gate/up, 1024 rows, [8960,1536] int8, fp16",
         8960 * 1536 + 4 * 8960 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 2 * 1024 * 1536 * 8960),
     ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4, 0>", 384 * 256): (
