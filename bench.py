@@ -442,6 +442,7 @@ def rocprof_summary(dirs):
     import glob
 
     out = []
+    pmc = {}  # (kernel fragment, grid, counter) -> per-dispatch values, over all dirs
     for d in dirs:
         for f in sorted(glob.glob(os.path.join(d, "*kernel_trace.csv"))):
             out.append(f"### kernel trace: {f}\n")
@@ -465,16 +466,12 @@ def rocprof_summary(dirs):
                 out.append(f"| {frag} ({label}) | {grid} | {len(v)} | {avg:.3f} | {v[len(v) // 2] / 1e3:.3f} | "
                            f"{nbytes} | {gbs:.0f} | {100 * gbs / PEAK_GBS:.1f} | {tf} |")
             out.append("")
-        pmc = {}
         for f in sorted(glob.glob(os.path.join(d, "*counter_collection.csv"))):
             for r in csv.DictReader(open(f)):
                 frag, known = _match_launch(r["Kernel_Name"], int(r["Grid_Size"]))
                 if known is None:
                     continue
                 pmc.setdefault((frag, int(r["Grid_Size"]), r["Counter_Name"]), []).append(float(r["Counter_Value"]))
-        if pmc:
-            globals().setdefault("_PMC", {}).update(pmc)
-    pmc = globals().get("_PMC", {})
     traffic = {}
     if pmc:
         cf = pmc.get(("stream_copy", 67108864, "FETCH_SIZE"))
