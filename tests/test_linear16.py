@@ -4,7 +4,7 @@ down projection (src/engine/fused_norm_activation_patch.py:64) runs with
 
 * parity with the oracle (``oracle.linear16``) over the down / q / k / o
   projection shapes of Qwen2.5-0.5B/1.5B/7B at decode rows, K tails, ragged
-  feature counts, > 32 rows (the skinny tiles and the tiled GEMM), bias in
+  feature counts, > 32 rows (the tiled GEMM), bias in
   three dtypes, fp16 and bf16.  The kernels sum in fp32 in their own order,
   so the bar is the exact value within one output ulp plus the worst-case
   fp32 summation error gamma_k * sum |x * w|; on top of that >= 99% of
@@ -68,7 +68,7 @@ def _check_vs_oracle(orc, got16, got32, x, w, b, dt):
     (8, 18944, 3584, BF16, None), (3, 4864, 896, BF16, None), (24, 3584, 3584, F16, None),
     # k tails (not a multiple of 64), ragged n, tiny shapes
     (5, 72, 40, F16, "f32"), (7, 8, 3, BF16, None), (9, 1000, 77, F16, "same"), (1, 8, 1, F16, None),
-    # more than 32 rows: skinny tiles on small grids, the tiled GEMM otherwise (k tails, ragged edges)
+    # more than 32 rows: the tiled GEMM (k tails, ragged edges, small grids)
     (33, 1536, 256, F16, None), (100, 256, 100, BF16, "same"), (200, 8960, 1536, F16, "f32"),
     (300, 1552, 520, BF16, None), (257, 96, 333, F16, "same"),
     # the small tiled shapes: >= 128 tile columns at 17 - 32 rows, any 33 - 64 rows
