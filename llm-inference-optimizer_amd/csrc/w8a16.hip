@@ -561,11 +561,14 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   if (small_tiles_pay(p.rows, p.n) && tiled_fits(p, DUAL)) return w8_tiled_small<T, TO, DUAL>(p, s);
   if (p.rows <= 24) return w8_skinny_shape<T, TO, 3, DUAL>(p, s, cus);
   if (p.rows <= 32) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);
-  // More rows: the tiled GEMM, except for small grids of few rows (e.g. 128
-  // rows against a K-heavy down projection), where 32-row skinny tiles with
-  // split K, which re-read the weights per tile mostly from L2, measured faster.
+  // More rows: the tiled GEMM, except where 32-row skinny tiles with split K,
+  // which re-read the int8 weights per tile mostly from L2, measured faster:
+  // tiny grids (fewer than 32 64 x 64 tiles: 1.5B k/v at 96 - 256 rows, 6.4
+  // vs 10.5 us) and narrow outputs (n < 2048) up to 128 rows (1.5B down, 128
+  // rows 30.7 vs 34.3 us).  Wider outputs and more rows re-read too much
+  // (7B down, 96 rows 105.6 vs 82.8 us; 1.5B down, 256 rows 57.6 vs 34.7).
   const int64_t tiles64 = static_cast<int64_t>((p.n + 63) / 64) * ((p.rows + 63) / 64);
-  bool skinny = p.rows <= 256 && tiles64 < 128;
+  bool skinny = p.rows <= 256 && (tiles64 < 32 || (p.rows <= 128 && p.n < 2048));
   if (!tiled_fits(p, DUAL)) skinny = true;
 #ifdef MI355_W8_SWEEP
   if (g_force_path > 0) skinny = g_force_path == 1;
