@@ -69,7 +69,7 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "copy", "ceilings", "decode", "linear16", "gate-up",
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill"],
                    default=None,
@@ -83,6 +83,19 @@ def parse_args():
     p.add_argument("--seq-lens", type=int, nargs="+", default=[128, 512, 1024, 2048])
     p.add_argument("--gen-len", type=int, default=32)
     p.add_argument("--trials", type=int, default=5)
+    p.add_argument("--variant", default=None, metavar="NAME",
+                   help="time the kernels of a variant library (build.py --variant NAME; launch-shape switches, "
+                        "same results) instead of the default one; the kernel legs only")
+    p.add_argument("--sweep", nargs="+", metavar="NAME", default=None,
+                   help="A/B sweep: time the default library and these variant libraries ('all' = every built "
+                        "variant) on the --sweep-legs, interleaved over --sweep-rounds, and check each variant's "
+                        "outputs equal the default library's bit for bit")
+    p.add_argument("--sweep-legs", nargs="+", default=["c1-rms", "c1-add-rms", "c4-rms", "c2-silu", "c4-silu"],
+                   choices=["c1-rms", "c1-add-rms", "c4-rms", "c2-silu", "c4-silu", "silu-4096x8960",
+                            "silu-8192x8960"])
+    p.add_argument("--sweep-rounds", type=int, default=3)
+    p.add_argument("--full-json", default=None, metavar="PATH",
+                   help="also write the full result (every leg) to PATH; stdout carries the compact line")
     p.add_argument("--rocprof-summary", nargs="+", metavar="DIR", default=None,
                    help="summarise rocprofv3 output directories (kernel trace and/or PMC) and exit; "
                         "no GPU needed")
@@ -93,14 +106,15 @@ class Ctx:
     """Bound C-ABI entry points.  Launch closures read `self.stream` at call
     time, so a graph capture can redirect them to the capturing stream."""
 
-    def __init__(self):
+    def __init__(self, variant=None):
         import torch
 
         sys.path.insert(0, str(ROOT))
         self.torch = torch
         self.pkg = importlib.import_module(PKG)
         self.L = importlib.import_module(PKG + "._lib")
-        self.lib = self.L.load()
+        self.lib = self.L.load() if variant is None else self.L.load_variant(variant_lib(variant))
+        self.variant = variant
         self.dev = torch.device("cuda:0")
         torch.cuda.set_device(self.dev)
         self.stream = torch.cuda.current_stream(self.dev).cuda_stream
@@ -116,6 +130,18 @@ class Ctx:
             self.probe.mi355_probe_empty.argtypes = [ctypes.c_void_p]
             self.probe.mi355_probe_empty.restype = ctypes.c_int
 
+    def with_lib(self, lib):
+        """A shallow copy whose launch closures call `lib` (a variant build)."""
+        c = object.__new__(Ctx)
+        c.__dict__.update(self.__dict__)
+        c.lib = lib
+        return c
+
+    def check(self, fn, st):
+        if st:
+            msg = self.lib.mi355_last_error().decode(errors="replace")
+            raise self.L.KernelError(fn, st, msg)
+
     def rms_call(self, x, w, y, eps=1e-6):
         M, N = x.shape
         code = self.L.DTYPE_CODE[x.dtype]
@@ -126,7 +152,7 @@ class Ctx:
         def call():
             st = f(*args, self.stream)
             if st:
-                self.L.check("mi355_rmsnorm_fwd", st)
+                self.check("mi355_rmsnorm_fwd", st)
         return call
 
     def add_rms_call(self, x, r, w, y, h, eps=1e-6):
@@ -139,7 +165,7 @@ class Ctx:
         def call():
             st = f(*args, self.stream)
             if st:
-                self.L.check("mi355_add_rmsnorm_fwd", st)
+                self.check("mi355_add_rmsnorm_fwd", st)
         return call
 
     def silu_call(self, g, u, o):
@@ -150,7 +176,7 @@ class Ctx:
         def call():
             st = f(*args, self.stream)
             if st:
-                self.L.check("mi355_silu_mul_fwd", st)
+                self.check("mi355_silu_mul_fwd", st)
         return call
 
     def gate_up_call(self, x, wg, wu, o):
@@ -163,7 +189,7 @@ class Ctx:
         def call():
             st = f(*args, self.stream)
             if st:
-                self.L.check("mi355_gate_up_silu_fwd", st)
+                self.check("mi355_gate_up_silu_fwd", st)
         return call
 
     def w8a16_call(self, x, q, scale, out, bias=None):
@@ -178,7 +204,7 @@ class Ctx:
         def call():
             st = f(*args, self.stream)
             if st:
-                self.L.check("mi355_w8a16_linear_fwd", st)
+                self.check("mi355_w8a16_linear_fwd", st)
         return call
 
     def linear16_call(self, x, w, out, bias=None):
@@ -192,7 +218,7 @@ class Ctx:
         def call():
             st = f(*args, self.stream)
             if st:
-                self.L.check("mi355_linear16_fwd", st)
+                self.check("mi355_linear16_fwd", st)
         return call
 
     def copy_call(self, src, dst):
@@ -220,6 +246,11 @@ class Ctx:
             if f(*args, self.stream):
                 raise RuntimeError("probe add2 failed")
         return call
+
+
+def variant_lib(name: str) -> Path:
+    """Path of a variant library built by `build.py --variant NAME`."""
+    return ROOT / PKG / "_variants" / f"libmi355_fused_{name}.so"
 
 
 def rand(ctx, shape, seed, dtype, mean=0.0, std=1.0):
@@ -373,14 +404,15 @@ def cpu_baseline(M, N, I, budget_s):
 # used to turn rocprofv3 durations into GB/s and to set PMC traffic against
 # the ideal.  Grid sizes are in threads, as rocprofv3 reports them.
 KNOWN_LAUNCHES = {
-    ("silu_mul_chunks<mi355::F16, mi355::F16>", 1146880): ("C2 SiLU-and-mul [2048,8960] fp16", 3 * 2048 * 8960 * 2),
-    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3, false>", 131072): (
+    ("silu_mul_chunks<mi355::F16, mi355::F16, 512, 2>", 1146880): ("C2 SiLU-and-mul [2048,8960] fp16",
+                                                                   3 * 2048 * 8960 * 2),
+    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3, 1, false, false>", 131072): (
         "C1 RMSNorm [2048,1536] fp16", (2 * 2048 * 1536 + 1536) * 2),
-    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3, true>", 131072): (
+    ("rmsnorm_wave_rows<mi355::F16, mi355::F16, mi355::F16, 3, 2, true, false>", 65536): (
         "C1 residual add + RMSNorm [2048,1536] fp16", (4 * 2048 * 1536 + 1536) * 2),
-    ("silu_mul_chunks<mi355::BF16, mi355::BF16>", 19398656): (
+    ("silu_mul_chunks<mi355::BF16, mi355::BF16, 256, 4>", 9699328): (
         "C4 SiLU-and-mul [16384,18944] bf16", 3 * 16384 * 18944 * 2),
-    ("rmsnorm_block_rows<mi355::BF16, mi355::BF16, mi355::BF16, 2, false>", 4194304): (
+    ("rmsnorm_block_rows<mi355::BF16, mi355::BF16, mi355::BF16, 2, 1, false>", 4194304): (
         "C4 RMSNorm [16384,3584] bf16", (2 * 16384 * 3584 + 3584) * 2),
     ("stream_copy", 67108864): ("copy probe, 1 GiB", 2 << 30),
     ("gate_up_silu_skinny<mi355::F16, mi355::F16, 1, 4, 1, 6>", 8960 // 8 * 256): (
@@ -444,6 +476,16 @@ def rocprof_summary(dirs):
     out = []
     pmc = {}  # (kernel fragment, grid, counter) -> per-dispatch values, over all dirs
     for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "*kernel_stats.csv"))):
+            # rocprofv3 --stats: every kernel of the run, whatever its grid
+            out.append(f"### kernel stats: {f}\n")
+            out.append("| kernel | calls | avg us | min us | max us | % of GPU time |")
+            out.append("|---|---|---|---|---|---|")
+            for r in csv.DictReader(open(f)):
+                out.append(f"| {r['Name'][:160]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                           f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} | "
+                           f"{float(r['Percentage']):.2f} |")
+            out.append("")
         for f in sorted(glob.glob(os.path.join(d, "*kernel_trace.csv"))):
             out.append(f"### kernel trace: {f}\n")
             out.append("| kernel | grid (threads) | launches | avg us | median us | algorithmic bytes | GB/s (avg) | "
@@ -537,12 +579,16 @@ def main():
         bench_e2e_int8(args)
         return
 
-    ctx = Ctx()
+    ctx = Ctx(args.variant)
     torch = ctx.torch
     props = torch.cuda.get_device_properties(ctx.dev)
-    log(f"device: {props.name} ({getattr(props, 'gcnArchName', '?')}), CUs={props.multi_processor_count}")
+    log(f"device: {props.name} ({getattr(props, 'gcnArchName', '?')}), CUs={props.multi_processor_count}"
+        + (f", variant library {args.variant}" if args.variant else ""))
+    if args.sweep:
+        run_sweep(ctx, args)
+        return
 
-    F16, BF16 = torch.float16, torch.bfloat16
+    F16 = torch.float16
     M, N, I = 2048, 1536, 8960
     rms_bytes = (2 * M * N + N) * 2
     silu_bytes = 3 * M * I * 2
@@ -560,6 +606,9 @@ def main():
         sets.append((ctx.rms_call(x, w, y), ctx.silu_call(gate, up, out), (x, y, gate, up, out)))
     torch.cuda.synchronize()
     log(f"headline: {nset} buffer sets, footprint {nset * step_bytes / 2**30:.2f} GiB")
+    # one untimed pass over every set: the generator's freshly written inputs
+    # are written back from the caches to HBM here, not inside the timed region
+    spin_up(ctx, [c for r, s_, _ in sets for c in (r, s_)], ms=5.0)
 
     if args.only:
         run_only(ctx, args, sets)
@@ -593,16 +642,15 @@ def main():
     silu_warm_us = time_loop(ctx, [sets[0][1]], iters)
     rms_warm_graph_us = time_graph(ctx, [sets[0][0]], 200)
     kernels = {
-        "c2_silu_mul_f16_2048x8960": kernel_entry("silu_mul_chunks<F16,F16>", silu_bytes, silu_us,
+        "c2_silu_mul_f16_2048x8960": kernel_entry("silu_mul_chunks", silu_bytes, silu_us,
                                                   {"timing": "events over back-to-back launches, cold"}),
-        "c1_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,false>", rms_bytes, rms_us,
+        "c1_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows", rms_bytes, rms_us,
                                                  {"timing": "events over back-to-back launches, cold"}),
-        "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,false>", rms_bytes,
+        "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows", rms_bytes,
                                                        rms_graph_us, {"timing": "hipGraph of 200 launches, cold"}),
-        "c2_silu_mul_f16_2048x8960_warm": kernel_entry("silu_mul_chunks<F16,F16>", silu_bytes, silu_warm_us,
+        "c2_silu_mul_f16_2048x8960_warm": kernel_entry("silu_mul_chunks", silu_bytes, silu_warm_us,
                                                        {"timing": "same buffers every launch (MALL-warm)"}),
-        "c1_rmsnorm_f16_2048x1536_warm_graph": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,false>", rms_bytes,
-                                                            rms_warm_graph_us,
+        "c1_rmsnorm_f16_2048x1536_warm_graph": kernel_entry("rmsnorm_wave_rows", rms_bytes, rms_warm_graph_us,
                                                             {"timing": "hipGraph, same buffers (MALL-warm)"}),
     }
     for k, v in kernels.items():
@@ -616,36 +664,31 @@ def main():
         "config": {"workload": "qwen2.5-1.5b-prefill-2048: RMSNorm x[2048,1536] + SiLU-and-mul gate/up[2048,8960]",
                    "storage_dtype": "f16", "math_dtype": "f32", "eps": 1e-6, "buffer_sets": nset,
                    "footprint_GiB": round(nset * step_bytes / 2**30, 3), "step_bytes": step_bytes},
-        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "kernel": "silu_mul_chunks (C2 SiLU-and-mul [2048,8960] fp16)",
                      "achieved": round(silu_bytes / silu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(silu_bytes / silu_us / 1e3 / PEAK_GBS, 4),
                      "traffic": read_traffic("C2 SiLU-and-mul [2048,8960] fp16"), "algorithmic_bytes": silu_bytes,
                      "avg_launch_us": round(silu_us, 3)},
-        "kernels": kernels,
     }
+    full = {"kernels": kernels}
+    if args.variant:
+        result["config"]["variant_library"] = args.variant
 
     if not args.skip_extras:
         del sets
         torch.cuda.empty_cache()
-        result["add_rmsnorm"] = bench_add_rms(ctx, iters)
-        result["c4"] = bench_c4(ctx, iters=60)
-        result["decode"] = bench_decode(ctx)
-        result["gate_up_silu"] = bench_gate_up(ctx)
-        result["gate_up_silu_prefill"] = bench_gate_up_prefill(ctx)
-        result["w8a16"] = bench_w8a16(ctx)
-        result["gate_up_silu_w8a16"] = bench_gate_up_w8(ctx)
-        result["linear16_down"] = bench_linear16(ctx)
-        result["copy_ceiling"] = bench_copy(ctx)
-        result["ceilings"] = bench_ceilings(ctx)
-        if result["ceilings"]:
-            pairs = [("C2 SiLU-and-mul [2048,8960] fp16", result["kernels"]["c2_silu_mul_f16_2048x8960"]),
-                     ("C1 RMSNorm [2048,1536] fp16", result["kernels"]["c1_rmsnorm_f16_2048x1536"]),
-                     ("C4 RMSNorm [16384,3584] bf16", result["c4"]["c4_rmsnorm_bf16_16384x3584"]),
-                     ("C4 SiLU-and-mul [16384,18944] bf16", result["c4"]["c4_silu_mul_bf16_16384x18944"])]
-            result["frac_of_same_size_ceiling"] = {
-                lab: round(result["ceilings"][lab]["us"] / k["us"], 4) for lab, k in pairs}
-            log(f"  kernel time / same-size probe time: {result['frac_of_same_size_ceiling']}")
+        full["add_rmsnorm"] = bench_add_rms(ctx, iters)
+        full["c4"] = bench_c4(ctx, iters=60)
+        full["decode"] = bench_decode(ctx)
+        full["copy_ceiling"] = bench_copy(ctx)
+        full["ceilings"] = bench_ceilings(ctx)
+        if not args.variant:  # the projection legs run the default library's launchers only
+            full["gate_up_silu"] = bench_gate_up(ctx)
+            full["gate_up_silu_prefill"] = bench_gate_up_prefill(ctx)
+            full["w8a16"] = bench_w8a16(ctx)
+            full["gate_up_silu_w8a16"] = bench_gate_up_w8(ctx)
+            full["linear16_down"] = bench_linear16(ctx)
+        result["roofline"]["per_config"] = per_config(full)
 
     if not args.skip_cpu:
         log("cpu baseline ...")
@@ -653,7 +696,51 @@ def main():
         log(f"  cpu: {result['cpu_baseline']['value']} GB/s on {result['cpu_baseline']['cores']} threads")
     else:
         result["cpu_baseline"] = None
+    if args.full_json:
+        Path(args.full_json).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.full_json).write_text(json.dumps({**result, "full": full}, indent=1))
+    log("full: " + json.dumps(full))
     print(json.dumps(result), flush=True)
+
+
+def per_config(full):
+    """The compact per-config block of the stdout line: each BASELINE config's
+    kernel time, rate and fraction of 8 TB/s (cold), the same-size probe's
+    time, and the decode-row latencies (C3) -- a few hundred bytes the driver
+    keeps whole inside `roofline`."""
+    k, c4, dec, ceil = full["kernels"], full["c4"], full["decode"], full.get("ceilings") or {}
+
+    def entry(d, probe_label=None, graph=None):
+        e = {"us": d["us"], "GBps": d["GBps"], "frac": d["frac_of_peak"]}
+        if graph is not None:
+            e["graph_us"] = graph["us"]
+            e["graph_frac"] = graph["frac_of_peak"]
+        if probe_label and probe_label in ceil:
+            e["probe_us"] = ceil[probe_label]["us"]
+        return e
+
+    pc = {
+        "C1_rmsnorm_f16_2048x1536": entry(k["c1_rmsnorm_f16_2048x1536"], "C1 RMSNorm [2048,1536] fp16",
+                                          k["c1_rmsnorm_f16_2048x1536_graph"]),
+        "C2_silu_mul_f16_2048x8960": entry(k["c2_silu_mul_f16_2048x8960"], "C2 SiLU-and-mul [2048,8960] fp16"),
+        "C4_rmsnorm_bf16_16384x3584": entry(c4["c4_rmsnorm_bf16_16384x3584"], "C4 RMSNorm [16384,3584] bf16"),
+        "C4_silu_mul_bf16_16384x18944": entry(c4["c4_silu_mul_bf16_16384x18944"],
+                                              "C4 SiLU-and-mul [16384,18944] bf16"),
+    }
+    c3 = {}
+    for m, d in dec.items():
+        if not m.startswith("M="):
+            continue
+        c3["M" + m[2:]] = {"rms_api_us": d["rmsnorm_api_us"], "silu_api_us": d["silu_mul_api_us"],
+                           "rms_dev_us": d["rmsnorm_device_us"], "silu_dev_us": d["silu_mul_device_us"],
+                           "graph_node_us": d["graph_per_kernel_us"], "graph_28_layers_us": d["graph_replay_us"]}
+    pc["C3_decode_f16_latency"] = c3
+    if "floor" in dec:
+        pc["C3_floor"] = {"empty_graph_node_us": dec["floor"]["empty_kernel_graph_node_us"],
+                          "row_copy_graph_node_us": dec["floor"]["row_copy_graph_node_us"]}
+    if full.get("copy_ceiling"):
+        pc["copy_1GiB_frac"] = full["copy_ceiling"]["frac_of_peak"]
+    return pc
 
 
 def run_only(ctx, args, sets):
@@ -675,6 +762,10 @@ def run_only(ctx, args, sets):
         torch.cuda.empty_cache()
         d = bench_c4(ctx, iters=60, which=args.only)
         log(json.dumps(d))
+    elif args.only == "c1-decomp":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"c1_decomposition": c1_decomposition(ctx), "variant": ctx.variant}), flush=True)
     elif args.only == "copy":
         log(json.dumps(bench_copy(ctx)))
     elif args.only == "decode":
@@ -720,6 +811,164 @@ def run_only(ctx, args, sets):
                                        iters=iters, baselines=False)))
 
 
+def _sweep_leg(ctx, leg):
+    """Buffers of one sweep leg: (algorithmic bytes per launch, list of buffer
+    sets, make_calls(ctx) -> one launch closure per set, outputs of set 0)."""
+    torch = ctx.torch
+    F16, BF16 = torch.float16, torch.bfloat16
+    if leg in ("c1-rms", "c4-rms"):
+        M, N, dt = (2048, 1536, F16) if leg == "c1-rms" else (16384, 3584, BF16)
+        nbytes = (2 * M * N + N) * 2
+        w = rand(ctx, (N,), 1, dt, 1.0, 0.1)
+        sets = []
+        for s_ in range(n_sets(nbytes)):
+            x = rand(ctx, (M, N), 100 + s_, dt)
+            sets.append((x, torch.empty_like(x)))
+        return nbytes, sets, lambda c: [c.rms_call(x, w, y) for x, y in sets], lambda: [sets[0][1]]
+    if leg == "c1-add-rms":
+        M, N = 2048, 1536
+        nbytes = (4 * M * N + N) * 2
+        w = rand(ctx, (N,), 1, F16, 1.0, 0.1)
+        sets = []
+        for s_ in range(n_sets(nbytes)):
+            x, r = rand(ctx, (M, N), 700 + s_, F16), rand(ctx, (M, N), 800 + s_, F16)
+            sets.append((x, r, torch.empty_like(x), torch.empty_like(x)))
+        return (nbytes, sets, lambda c: [c.add_rms_call(x, r, w, y, h) for x, r, y, h in sets],
+                lambda: [sets[0][2], sets[0][3]])
+    M, I, dt = {"c2-silu": (2048, 8960, F16), "c4-silu": (16384, 18944, BF16), "silu-4096x8960": (4096, 8960, F16),
+                "silu-8192x8960": (8192, 8960, F16)}[leg]
+    nbytes = 3 * M * I * 2
+    sets = []
+    for s_ in range(n_sets(nbytes) if nbytes < MIN_FOOTPRINT else 1):
+        g, u = rand(ctx, (M, I), 200 + s_, dt), rand(ctx, (M, I), 300 + s_, dt)
+        sets.append((g, u, torch.empty_like(g)))
+    return nbytes, sets, lambda c: [c.silu_call(g, u, o) for g, u, o in sets], lambda: [sets[0][2]]
+
+
+SWEEP_ITERS = {"c1-rms": 2000, "c1-add-rms": 2000, "c4-rms": 200, "c2-silu": 500, "c4-silu": 30,
+               "silu-4096x8960": 300, "silu-8192x8960": 150}
+
+
+def run_sweep(ctx, args):
+    """A/B of launch-shape variants: the default library and each variant
+    library time the same legs on the same buffers, interleaved round by round
+    (so drift of the box's clocks hits every library alike); each variant's
+    outputs must equal the default library's bit for bit (the switches change
+    the launch shape, never the arithmetic), except the variants that reorder
+    a row's fp32 sum of squares (held to the oracle by
+    tests/test_launch_variants.py).  Prints one JSON line."""
+    torch = ctx.torch
+    names = list(args.sweep)
+    if names == ["all"]:
+        names = sorted(p.name[len("libmi355_fused_"):-3] for p in (ROOT / PKG / "_variants").glob("libmi355_fused_*.so"))
+    libs = {"default": ctx.lib}
+    for n in names:
+        libs[n] = ctx.L.load_variant(variant_lib(n))
+    reordering = importlib.import_module(PKG + ".build").REORDERING_VARIANTS
+    ctxs = {n: ctx.with_lib(l) for n, l in libs.items()}
+    out = {"variants": names, "rounds": args.sweep_rounds, "legs": {}}
+    for leg in args.sweep_legs:
+        nbytes, sets, make_calls, outputs = _sweep_leg(ctx, leg)
+        calls = {n: make_calls(c) for n, c in ctxs.items()}
+        calls["default"][0]()
+        torch.cuda.synchronize()
+        ref = [t.clone() for t in outputs()]
+        equal = {}
+        for n in names:
+            for t in outputs():
+                t.fill_(0)
+            calls[n][0]()
+            torch.cuda.synchronize()
+            equal[n] = all(torch.equal(a, b) for a, b in zip(ref, outputs()))
+        spin_up(ctx, calls["default"])
+        times = {n: [] for n in calls}
+        graph = {n: [] for n in calls} if leg.startswith("c1") else None
+        for _ in range(args.sweep_rounds):
+            for n in calls:
+                times[n].append(time_loop(ctxs[n], calls[n], SWEEP_ITERS[leg]))
+                if graph is not None:  # the copy's closures read its stream: capture through it
+                    graph[n].append(time_graph(ctxs[n], calls[n], 200))
+        base = statistics.median(times["default"])
+        rows = {}
+        for n in calls:
+            us = statistics.median(times[n])
+            rows[n] = {"us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+                       "frac": round(nbytes / us / 1e3 / PEAK_GBS, 4), "vs_default": round(base / us, 4),
+                       "rounds_us": [round(t, 3) for t in times[n]]}
+            if graph is not None:
+                g = statistics.median(graph[n])
+                rows[n]["graph_us"] = round(g, 3)
+                rows[n]["graph_frac"] = round(nbytes / g / 1e3 / PEAK_GBS, 4)
+            if n != "default":
+                rows[n]["bitwise_equal_to_default"] = equal[n]
+                if n in reordering:  # another fp32 summation order: held to the oracle by the GPU tests
+                    rows[n]["reorders_sum"] = True
+            log(f"  sweep {leg} {n}: {rows[n]}")
+        out["legs"][leg] = {"bytes": nbytes, "buffer_sets": len(sets), "iters": SWEEP_ITERS[leg], "libs": rows}
+        del sets, calls, ref
+        torch.cuda.empty_cache()
+    bad = [(leg, n) for leg, d in out["legs"].items() for n, r in d["libs"].items()
+           if r.get("bitwise_equal_to_default") is False and not r.get("reorders_sum")]
+    out["all_bitwise_equal"] = not bad
+    print(json.dumps(out), flush=True)
+    if bad:
+        log(f"sweep: outputs differ from the default library: {bad}")
+        sys.exit(1)
+
+
+def c1_decomposition(ctx):
+    """Where C1's time goes, from the floor up (cold buffers unless noted):
+    an empty kernel and the copy of one 3 KiB row (one HBM round trip), back
+    to back and as nodes of a hipGraph; a one-row RMSNorm; the probe copy of
+    C1's own bytes; the C1 kernel back to back, in a graph, and MALL-warm in a
+    graph."""
+    torch = ctx.torch
+    F16 = torch.float16
+    M, N = 2048, 1536
+    nbytes = (2 * M * N + N) * 2
+    out = {"bytes": nbytes}
+    empty = [ctx.empty_call()]
+    src = torch.empty(N * 2, dtype=torch.uint8, device=ctx.dev)
+    dst = torch.empty_like(src)
+    row = [ctx.copy_call(src, dst)]
+    out["empty_kernel_eager_us"] = time_loop(ctx, empty, 2000)
+    out["empty_kernel_graph_node_us"] = time_graph(ctx, empty, 200, replays=20)
+    out["row_copy_eager_us"] = time_loop(ctx, row, 2000)
+    out["row_copy_graph_node_us"] = time_graph(ctx, row, 200, replays=20)
+    w = rand(ctx, (N,), 1, F16, 1.0, 0.1)
+    x1 = rand(ctx, (1, N), 5, F16)
+    y1 = torch.empty_like(x1)
+    one = [ctx.rms_call(x1, w, y1)]
+    out["one_row_rmsnorm_eager_us"] = time_loop(ctx, one, 2000)
+    out["one_row_rmsnorm_graph_node_us"] = time_graph(ctx, one, 200, replays=20)
+    half = M * N * 2
+    bufs = [(torch.empty(half, dtype=torch.uint8, device=ctx.dev).random_(0, 255),
+             torch.empty(half, dtype=torch.uint8, device=ctx.dev)) for _ in range(n_sets(2 * half))]
+    copies = [ctx.copy_call(a, b) for a, b in bufs]
+    spin_up(ctx, copies)
+    out["same_size_copy_eager_us"] = time_loop(ctx, copies, 2000)
+    out["same_size_copy_graph_us"] = time_graph(ctx, copies, 200, replays=20)
+    del bufs, copies
+    sets = []
+    for s_ in range(n_sets(nbytes)):
+        x = rand(ctx, (M, N), 100 + s_, F16)
+        sets.append((x, torch.empty_like(x)))
+    rms = [ctx.rms_call(x, w, y) for x, y in sets]
+    spin_up(ctx, rms)
+    out["c1_eager_us"] = time_loop(ctx, rms, 2000)
+    out["c1_graph_us"] = time_graph(ctx, rms, 200, replays=20)
+    out["c1_warm_graph_us"] = time_graph(ctx, rms[:1], 200, replays=20)
+    for k in list(out):
+        if k.endswith("_us"):
+            out[k] = round(out[k], 3)
+    out["c1_graph_frac"] = round(nbytes / out["c1_graph_us"] / 1e3 / PEAK_GBS, 4)
+    out["c1_eager_frac"] = round(nbytes / out["c1_eager_us"] / 1e3 / PEAK_GBS, 4)
+    out["us_for_80pct"] = round(nbytes / (0.8 * PEAK_GBS) / 1e3, 3)
+    del sets, rms
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_add_rms(ctx, iters):
     """Residual add + RMSNorm at the C1 shape (beyond the reference): the fused
     kernel vs the unfused pair (torch's add, then the RMSNorm kernel), cold."""
@@ -741,7 +990,7 @@ def bench_add_rms(ctx, iters):
 
     fused_us = time_loop(ctx, fused, iters)
     unfused_us = time_loop(ctx, [unfused_call(i) for i in range(len(sets))], iters)
-    out = {"c1_add_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows<F16,F16,F16,3,true>", fused_bytes,
+    out = {"c1_add_rmsnorm_f16_2048x1536": kernel_entry("rmsnorm_wave_rows (add)", fused_bytes,
                                                         fused_us, {"buffer_sets": len(sets)}),
            "c1_add_then_rmsnorm_unfused_us": round(unfused_us, 3),
            "fused_speedup": round(unfused_us / fused_us, 3)}
@@ -766,8 +1015,9 @@ def bench_c4(ctx, iters=60, which=None):
             y = torch.empty_like(x)
             keep.append((x, y))
             calls.append(ctx.rms_call(x, w, y))
+        spin_up(ctx, calls)
         us = time_loop(ctx, calls, iters)
-        out["c4_rmsnorm_bf16_16384x3584"] = kernel_entry("rmsnorm_block_rows<BF16,BF16,BF16,2,false> (4 waves per row)", nbytes, us,
+        out["c4_rmsnorm_bf16_16384x3584"] = kernel_entry("rmsnorm_block_rows", nbytes, us,
                                                          {"buffer_sets": len(calls)})
         del keep, calls
         torch.cuda.empty_cache()
@@ -777,8 +1027,9 @@ def bench_c4(ctx, iters=60, which=None):
         gate = rand(ctx, (M, I), 500, BF16)
         up = rand(ctx, (M, I), 501, BF16)
         o = torch.empty_like(gate)
+        spin_up(ctx, [ctx.silu_call(gate, up, o)])
         us = time_loop(ctx, [ctx.silu_call(gate, up, o)], iters)
-        out["c4_silu_mul_bf16_16384x18944"] = kernel_entry("silu_mul_chunks<BF16,BF16>", nbytes, us,
+        out["c4_silu_mul_bf16_16384x18944"] = kernel_entry("silu_mul_chunks", nbytes, us,
                                                            {"buffer_sets": 1, "footprint_GiB": round(nbytes / 2**30, 2)})
         del gate, up, o
         torch.cuda.empty_cache()

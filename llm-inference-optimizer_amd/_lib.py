@@ -46,6 +46,39 @@ _lib: ctypes.CDLL | None = None
 _ext = None
 
 
+def _declare(L: ctypes.CDLL, path: Path) -> ctypes.CDLL:
+    """Declares the C ABI's argument and return types on `L` and checks its
+    ABI version."""
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    L.mi355_abi_version.argtypes = []
+    L.mi355_abi_version.restype = i32
+    L.mi355_last_error.argtypes = []
+    L.mi355_last_error.restype = ctypes.c_char_p
+    L.mi355_rmsnorm_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, i32, i32, i32, vp]
+    L.mi355_rmsnorm_fwd.restype = i32
+    L.mi355_add_rmsnorm_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float,
+                                        i32, i32, i32, vp]
+    L.mi355_add_rmsnorm_fwd.restype = i32
+    L.mi355_silu_mul_fwd.argtypes = [vp, vp, vp, i64, i32, i32, vp]
+    L.mi355_silu_mul_fwd.restype = i32
+    L.mi355_gate_up_silu_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp]
+    L.mi355_gate_up_silu_fwd.restype = i32
+    L.mi355_w8a16_linear_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, i32, i32,
+                                         vp]
+    L.mi355_w8a16_linear_fwd.restype = i32
+    L.mi355_quantize_int8_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i32, vp]
+    L.mi355_quantize_int8_fwd.restype = i32
+    L.mi355_gate_up_silu_w8a16_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32,
+                                               i32, vp]
+    L.mi355_gate_up_silu_w8a16_fwd.restype = i32
+    L.mi355_linear16_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, i32, vp]
+    L.mi355_linear16_fwd.restype = i32
+    ver = L.mi355_abi_version()
+    if ver != ABI_VERSION:
+        raise KernelLibraryMissing(f"{path} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+    return L
+
+
 def load() -> ctypes.CDLL:
     """Load (once) and return the kernel library."""
     global _lib
@@ -58,36 +91,19 @@ def load() -> ctypes.CDLL:
             raise KernelLibraryMissing(
                 f"{LIB_PATH} is not built; run `python -c \"import __graft_entry__ as g; g.build()\"` "
                 "from the repository root (there is no CPU fallback)")
-        L = ctypes.CDLL(str(LIB_PATH))
-        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
-        L.mi355_abi_version.argtypes = []
-        L.mi355_abi_version.restype = i32
-        L.mi355_last_error.argtypes = []
-        L.mi355_last_error.restype = ctypes.c_char_p
-        L.mi355_rmsnorm_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, i32, i32, i32, vp]
-        L.mi355_rmsnorm_fwd.restype = i32
-        L.mi355_add_rmsnorm_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float,
-                                            i32, i32, i32, vp]
-        L.mi355_add_rmsnorm_fwd.restype = i32
-        L.mi355_silu_mul_fwd.argtypes = [vp, vp, vp, i64, i32, i32, vp]
-        L.mi355_silu_mul_fwd.restype = i32
-        L.mi355_gate_up_silu_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp]
-        L.mi355_gate_up_silu_fwd.restype = i32
-        L.mi355_w8a16_linear_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, i32, i32,
-                                             vp]
-        L.mi355_w8a16_linear_fwd.restype = i32
-        L.mi355_quantize_int8_fwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i32, vp]
-        L.mi355_quantize_int8_fwd.restype = i32
-        L.mi355_gate_up_silu_w8a16_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32,
-                                                   i32, vp]
-        L.mi355_gate_up_silu_w8a16_fwd.restype = i32
-        L.mi355_linear16_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, i32, vp]
-        L.mi355_linear16_fwd.restype = i32
-        ver = L.mi355_abi_version()
-        if ver != ABI_VERSION:
-            raise KernelLibraryMissing(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
-        _lib = L
+        _lib = _declare(ctypes.CDLL(str(LIB_PATH)), LIB_PATH)
     return _lib
+
+
+def load_variant(path) -> ctypes.CDLL:
+    """A separately built copy of the kernel library (`build.py -D... --out
+    <path>`: the same kernels with other launch-shape switches), declared like
+    the default one but not cached.  For side-by-side timing; the package's
+    launchers always use the default library."""
+    path = Path(path).resolve()
+    if not path.exists():
+        raise KernelLibraryMissing(f"{path} is not built")
+    return _declare(ctypes.CDLL(str(path)), path)
 
 
 def ext():

@@ -9,6 +9,17 @@ Cross-compiles on a machine without a GPU.
 
     python llm-inference-optimizer_amd/build.py            # default build
     python llm-inference-optimizer_amd/build.py -DMI355_SILU_UNROLL=2 --out /tmp/x.so
+    python llm-inference-optimizer_amd/build.py --variant rms_block_rows2 [...]
+    python llm-inference-optimizer_amd/build.py --variant all
+
+A *variant* (``VARIANTS`` below) is the library with one translation unit
+rebuilt under other launch-shape switches, written to
+``_variants/libmi355_fused_<name>.so``; ``bench.py --sweep <name>...`` times
+its kernels beside the default build's.  The switches change how rows and
+chunks are spread over waves and workgroups; the arithmetic is the same, and
+the outputs are bit-identical to the default library's except where a
+variant changes the order of a row's fp32 sum of squares
+(``REORDERING_VARIANTS``).
 """
 from __future__ import annotations
 
@@ -80,6 +91,95 @@ def build(extra_flags: list[str] | None = None, out: Path | None = None, jobs: i
     return out
 
 
+# name -> (translation unit, -D switches).  The alternatives to the shipped
+# launch shapes that the design measured, kept buildable so every A/B can be
+# rerun from the repository.
+VARIANTS = {
+    # RMSNorm: rows held per wave / per workgroup iteration (loads of all of
+    # them in flight before the first reduction)
+    "rms_wave_rows2": ("rmsnorm", ["-DMI355_RMS_WAVE_ROWS=2"]),
+    "rms_wave_rows4": ("rmsnorm", ["-DMI355_RMS_WAVE_ROWS=4"]),
+    "rms_add_wave_rows1": ("rmsnorm", ["-DMI355_RMS_WAVE_ROWS_ADD=1"]),
+    "rms_add_wave_rows4": ("rmsnorm", ["-DMI355_RMS_WAVE_ROWS_ADD=4"]),
+    "rms_block_rows2": ("rmsnorm", ["-DMI355_RMS_BLOCK_ROWS=2"]),
+    "rms_block_rows4": ("rmsnorm", ["-DMI355_RMS_BLOCK_ROWS=4"]),
+    # RMSNorm: rows up to 8 packets per lane as one wave (C4: one wave x 7
+    # packets instead of 4 waves x 2), with 1 or 2 rows per wave
+    "rms_one_wave": ("rmsnorm", ["-DMI355_RMS_WAVE_MAX_VPL=8"]),
+    "rms_one_wave_rows2": ("rmsnorm", ["-DMI355_RMS_WAVE_MAX_VPL=8", "-DMI355_RMS_WAVE_ROWS=2"]),
+    # RMSNorm: the weight row staged in LDS and broadcast to the waves of a
+    # workgroup (instead of each wave loading its packets from L2)
+    "rms_weight_lds": ("rmsnorm", ["-DMI355_RMS_WEIGHT_LDS=1"]),
+    "rms_weight_lds_block1024": ("rmsnorm", ["-DMI355_RMS_WEIGHT_LDS=1", "-DMI355_RMS_WAVE_BLOCK=1024"]),
+    # RMSNorm: persistent grids (waves per CU), rows striding over them
+    "rms_persistent8": ("rmsnorm", ["-DMI355_RMS_WAVES_PER_CU=8"]),
+    "rms_persistent16": ("rmsnorm", ["-DMI355_RMS_WAVES_PER_CU=16"]),
+    "rms_block_persistent4": ("rmsnorm", ["-DMI355_RMS_BLOCKS_PER_CU=4"]),
+    "rms_block_persistent8": ("rmsnorm", ["-DMI355_RMS_BLOCKS_PER_CU=8"]),
+    # RMSNorm: workgroup size of the wave-per-row kernel
+    "rms_wave_block64": ("rmsnorm", ["-DMI355_RMS_WAVE_BLOCK=64"]),
+    "rms_wave_block512": ("rmsnorm", ["-DMI355_RMS_WAVE_BLOCK=512"]),
+    # SiLU-and-mul below 2^27 elements (C2): packets per lane, workgroup size
+    "silu_unroll1": ("silu_mul", ["-DMI355_SILU_UNROLL=1"]),
+    "silu_unroll3": ("silu_mul", ["-DMI355_SILU_UNROLL=3"]),
+    "silu_unroll4_block256": ("silu_mul", ["-DMI355_SILU_UNROLL=4", "-DMI355_SILU_BLOCK=256"]),
+    "silu_block1024": ("silu_mul", ["-DMI355_SILU_BLOCK=1024"]),
+    # SiLU-and-mul from 2^27 elements (C4): the small-size shape, other chunks
+    "silu_large_block512_unroll2": ("silu_mul", ["-DMI355_SILU_LARGE_BLOCK=512", "-DMI355_SILU_LARGE_UNROLL=2"]),
+    "silu_large_block256_unroll8": ("silu_mul", ["-DMI355_SILU_LARGE_UNROLL=8"]),
+    "silu_large_block128_unroll8": ("silu_mul", ["-DMI355_SILU_LARGE_BLOCK=128", "-DMI355_SILU_LARGE_UNROLL=8"]),
+    # SiLU-and-mul: every size on one shape, and the load order
+    "silu_large_shape_everywhere": ("silu_mul", ["-DMI355_SILU_LARGE_MIN_NUMEL=0"]),
+    "silu_load_order1": ("silu_mul", ["-DMI355_SILU_LOAD_ORDER=1"]),
+    # RMSNorm: keep the row's fp32 widening live between the two passes
+    # instead of re-widening the packed row (more VGPRs, fewer conversions),
+    # per kernel: the shipped choice is the wave kernel re-widening and the
+    # workgroup kernel keeping fp32
+    "rms_wave_keep_f32": ("rmsnorm", ["-DMI355_RMS_KEEP_F32_WAVE=1"]),
+    "rms_block_rewiden": ("rmsnorm", ["-DMI355_RMS_KEEP_F32_BLOCK=0"]),
+}
+VARIANT_DIR = PKG_DIR / "_variants"
+# Variants that spread a row over waves differently from the default build:
+# the fp32 sum of squares then adds in another order, so an output may differ
+# from the default library's in its last bit (both stay within one ulp of the
+# exactly rounded result).  Every other variant is bit-identical to the
+# default library.
+REORDERING_VARIANTS = frozenset({"rms_one_wave", "rms_one_wave_rows2"})
+
+
+def variant_path(name: str) -> Path:
+    return VARIANT_DIR / f"libmi355_fused_{name}.so"
+
+
+def build_variant(name: str) -> Path:
+    """The library with VARIANTS[name]'s translation unit recompiled under its
+    switches and every other unit from the default build's objects."""
+    unit, flags = VARIANTS[name]
+    default_dir = PKG_DIR / "_build" / "default"
+    objdir = PKG_DIR / "_build" / f"variant_{name}"
+    objdir.mkdir(parents=True, exist_ok=True)
+    objs = []
+    for src in sorted(CSRC.glob("*.hip")):
+        if src.stem == unit:
+            obj = objdir / (src.stem + ".o")
+            _compile(src, obj, flags)
+        else:
+            obj = default_dir / (src.stem + ".o")
+            if not obj.exists():
+                default_dir.mkdir(parents=True, exist_ok=True)
+                _compile(src, obj, [])
+        objs.append(obj)
+    out = variant_path(name)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def ext_path() -> Path:
     import sysconfig
     return PKG_DIR / (EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
@@ -126,6 +226,15 @@ def build_probe() -> Path:
 
 if __name__ == "__main__":
     args = sys.argv[1:]
+    if args[:1] == ["--variant"]:
+        names = list(VARIANTS) if args[1:] == ["all"] else args[1:]
+        unknown = [n for n in names if n not in VARIANTS]
+        if unknown or not names:
+            sys.exit(f"unknown variant(s) {unknown}; known: {', '.join(VARIANTS)}")
+        with cf.ThreadPoolExecutor(max_workers=min(8, len(names))) as ex:
+            for path in ex.map(build_variant, names):
+                print(path)
+        sys.exit(0)
     out = None
     if "--out" in args:
         i = args.index("--out")

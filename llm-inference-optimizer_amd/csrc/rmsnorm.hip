@@ -1,37 +1,68 @@
 // Launcher for the RMSNorm kernels (plain and residual-add fused): picks
 // wave-per-row, workgroup-per-row or the generic kernel from the row width,
 // alignment and dtype mix, and sizes the grid.
+//
+// The -D switches below select launch shapes; the defaults are the shapes
+// measured fastest on MI355X.  A variant library built with other values
+// (`build.py -DMI355_RMS_... --out <lib>`) runs the same kernels with the
+// same results, so bench.py can time the alternatives side by side.
 #include "rmsnorm_kernels.h"
 
-// Optional cap on the grid, in waves per CU, for the row-striding kernels;
-// 0 = one wave (or workgroup) per row, which measured fastest on MI355X.
+// Optional caps on the grid (a persistent grid, rows striding over it):
+// waves per CU for the wave-per-row kernel, workgroups per CU for the
+// workgroup-per-row kernel; 0 = one wave (or workgroup) per row group.
 #ifndef MI355_RMS_WAVES_PER_CU
 #define MI355_RMS_WAVES_PER_CU 0
 #endif
-// Row counts below this use 64-thread workgroups (one wave each), so small
-// decode batches spread over as many CUs as rows.
+#ifndef MI355_RMS_BLOCKS_PER_CU
+#define MI355_RMS_BLOCKS_PER_CU 0
+#endif
+// Row counts below this use 64-thread workgroups (one wave each) and one row
+// per wave, so small decode batches spread over as many CUs as rows.
 #ifndef MI355_RMS_SMALL_ROWS
 #define MI355_RMS_SMALL_ROWS 1024
 #endif
 // Row split: rows needing more than WAVE_MAX_VPL packets per lane of one wave
 // are spread over several waves with at most TARGET_VPL packets per lane
-// (measured on MI355X: 1536-wide fp16 rows are fastest as 3 packets per lane
-// of one wave, 3584-wide bf16 rows as 2 packets per lane of 4 waves).
+// (1536-wide fp16 rows run as 3 packets per lane of one wave, 3584-wide bf16
+// rows as 2 packets per lane of 4 waves).
 #ifndef MI355_RMS_WAVE_MAX_VPL
 #define MI355_RMS_WAVE_MAX_VPL 4
 #endif
 #ifndef MI355_RMS_TARGET_VPL
 #define MI355_RMS_TARGET_VPL 2
 #endif
+static_assert(MI355_RMS_WAVE_MAX_VPL >= 1 && MI355_RMS_WAVE_MAX_VPL <= 8, "wave kernels exist for 1-8 packets per lane");
+// Rows each wave (wave-per-row kernel) or each workgroup iteration
+// (workgroup-per-row kernel) holds at once, from MI355_RMS_SMALL_ROWS rows up:
+// all their loads are in flight together, behind one reduction (and, for the
+// workgroup kernel, one barrier).  The fused residual add moves twice the
+// bytes of a row and measured 1.06x faster with two rows per wave at the
+// 2048 x 1536 fp16 shape; the plain norm is fastest with one.
+#ifndef MI355_RMS_WAVE_ROWS
+#define MI355_RMS_WAVE_ROWS 1
+#endif
+#ifndef MI355_RMS_WAVE_ROWS_ADD
+#define MI355_RMS_WAVE_ROWS_ADD 2
+#endif
+#ifndef MI355_RMS_BLOCK_ROWS
+#define MI355_RMS_BLOCK_ROWS 1
+#endif
+// 1: the wave-per-row kernel stages the weight row in LDS once per
+// workgroup and broadcasts it to its waves, instead of each wave loading its
+// weight packets from L2.
+#ifndef MI355_RMS_WEIGHT_LDS
+#define MI355_RMS_WEIGHT_LDS 0
+#endif
 
 namespace mi355 {
 namespace {
 
 template <typename K>
-int launch_rms(K kernel, int64_t grid, int block, const RmsParams& p, hipStream_t s) {
+int launch_rms(K kernel, int64_t grid, int block, const RmsParams& p, hipStream_t s, size_t lds = 0) {
   void* args[] = {const_cast<RmsParams*>(&p)};
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(kernel),
-                                    dim3(static_cast<unsigned>(grid)), dim3(block), args, 0, s),
+                                    dim3(static_cast<unsigned>(grid)), dim3(block), args, lds, s),
                     "rmsnorm launch");
 }
 
@@ -43,16 +74,30 @@ int rms_generic(const RmsParams& p, hipStream_t s, int cus) {
   return launch_rms(rmsnorm_generic<TX, TW, TY, ADD>, grid, 256, p, s);
 }
 
-template <typename TX, typename TW, typename TY, bool ADD>
-int rms_wave(const RmsParams& p, hipStream_t s, int cus, int vpl) {
-  const int block = p.rows < MI355_RMS_SMALL_ROWS ? 64 : 256;
+template <typename TX, typename TW, typename TY, int VPL, int R, bool ADD>
+int rms_wave_shape(const RmsParams& p, hipStream_t s, int cus, int block) {
   const int wpb = block / 64;
-  int64_t grid = (p.rows + wpb - 1) / wpb;
+  const int64_t per_block = static_cast<int64_t>(wpb) * R;
+  int64_t grid = (p.rows + per_block - 1) / per_block;
   const int64_t cap = MI355_RMS_WAVES_PER_CU > 0 ? static_cast<int64_t>(cus) * MI355_RMS_WAVES_PER_CU / wpb
                                                  : int64_t{0x7fffffff};
   if (grid > cap) grid = cap;
-#define MI355_WAVE_CASE(V) \
-  return launch_rms(rmsnorm_wave_rows<TX, TW, TY, V, ADD>, grid, block, p, s)
+  if (grid < 1) grid = 1;
+  constexpr bool wlds = MI355_RMS_WEIGHT_LDS != 0;
+  constexpr size_t lds = wlds ? 64u * VPL * pack_width<TX>::value * sizeof(typename TW::bits) : 0u;
+  return launch_rms(rmsnorm_wave_rows<TX, TW, TY, VPL, R, ADD, wlds>, grid, block, p, s, lds);
+}
+
+template <typename TX, typename TW, typename TY, int VPL, bool ADD>
+int rms_wave_rows(const RmsParams& p, hipStream_t s, int cus) {
+  constexpr int R = ADD ? MI355_RMS_WAVE_ROWS_ADD : MI355_RMS_WAVE_ROWS;
+  if (p.rows < MI355_RMS_SMALL_ROWS) return rms_wave_shape<TX, TW, TY, VPL, 1, ADD>(p, s, cus, 64);
+  return rms_wave_shape<TX, TW, TY, VPL, R, ADD>(p, s, cus, MI355_RMS_WAVE_BLOCK);
+}
+
+template <typename TX, typename TW, typename TY, bool ADD>
+int rms_wave(const RmsParams& p, hipStream_t s, int cus, int vpl) {
+#define MI355_WAVE_CASE(V) return rms_wave_rows<TX, TW, TY, V, ADD>(p, s, cus)
   switch (vpl) {
     case 1: MI355_WAVE_CASE(1);
     case 2: MI355_WAVE_CASE(2);
@@ -63,12 +108,6 @@ int rms_wave(const RmsParams& p, hipStream_t s, int cus, int vpl) {
     case 6: MI355_WAVE_CASE(6);
     case 7: MI355_WAVE_CASE(7);
     case 8: MI355_WAVE_CASE(8);
-    case 9:
-    case 10: MI355_WAVE_CASE(10);
-    case 11:
-    case 12: MI355_WAVE_CASE(12);
-    case 13: case 14: case 15:
-    case 16: MI355_WAVE_CASE(16);
 #endif
     default:
       set_error("rmsnorm: internal error, no wave kernel for %d packets per lane", vpl);
@@ -77,13 +116,23 @@ int rms_wave(const RmsParams& p, hipStream_t s, int cus, int vpl) {
 #undef MI355_WAVE_CASE
 }
 
-template <typename TX, typename TW, typename TY, bool ADD>
-int rms_block(const RmsParams& p, hipStream_t s, int waves, int vpl) {
-  const int block = 64 * waves;
-  int64_t grid = p.rows;
+template <typename TX, typename TW, typename TY, int VPL, bool ADD>
+int rms_block_rows(const RmsParams& p, hipStream_t s, int cus, int block) {
+  const bool multi = p.rows >= MI355_RMS_SMALL_ROWS && MI355_RMS_BLOCK_ROWS > 1;
+  constexpr int R = MI355_RMS_BLOCK_ROWS > 1 ? MI355_RMS_BLOCK_ROWS : 1;
+  const int64_t per_block = multi ? R : 1;
+  int64_t grid = (p.rows + per_block - 1) / per_block;
+  if (MI355_RMS_BLOCKS_PER_CU > 0 && grid > static_cast<int64_t>(cus) * MI355_RMS_BLOCKS_PER_CU)
+    grid = static_cast<int64_t>(cus) * MI355_RMS_BLOCKS_PER_CU;
   if (grid > 0x7fffffff) grid = 0x7fffffff;
-#define MI355_BLOCK_CASE(V) \
-  return launch_rms(rmsnorm_block_rows<TX, TW, TY, V, ADD>, grid, block, p, s)
+  if (multi) return launch_rms(rmsnorm_block_rows<TX, TW, TY, VPL, R, ADD>, grid, block, p, s);
+  return launch_rms(rmsnorm_block_rows<TX, TW, TY, VPL, 1, ADD>, grid, block, p, s);
+}
+
+template <typename TX, typename TW, typename TY, bool ADD>
+int rms_block(const RmsParams& p, hipStream_t s, int cus, int waves, int vpl) {
+  const int block = 64 * waves;
+#define MI355_BLOCK_CASE(V) return rms_block_rows<TX, TW, TY, V, ADD>(p, s, cus, block)
   switch (vpl) {
     case 1: MI355_BLOCK_CASE(1);
     case 2: MI355_BLOCK_CASE(2);
@@ -119,7 +168,7 @@ int rms_packets(const RmsParams& p, hipStream_t s, int cus) {
   const int vpl = (nvec + 64 * waves - 1) / (64 * waves);
   if (vpl > 8) return rms_generic<TX, TW, TY, ADD>(p, s, cus);
   waves = (nvec + 64 * vpl - 1) / (64 * vpl);
-  return rms_block<TX, TW, TY, ADD>(p, s, waves, vpl);
+  return rms_block<TX, TW, TY, ADD>(p, s, cus, waves, vpl);
 }
 
 template <typename TX, typename TY, bool ADD>

@@ -33,6 +33,23 @@
 
 #include "common.h"
 
+// Threads per workgroup of the wave-per-row kernel above the decode sizes
+// (below them, 64: one wave per workgroup, so a few rows spread over CUs).
+#ifndef MI355_RMS_WAVE_BLOCK
+#define MI355_RMS_WAVE_BLOCK 256
+#endif
+// 1: let the compiler keep the fp32 widening of the row (and weight) from the
+// sum-of-squares pass live for the scaling pass, instead of re-widening the
+// packed 16-bit form there (fewer conversions, more VGPRs).  Measured on
+// MI355X: the workgroup-per-row kernel gains 1% at 16384 x 3584 bf16 (39.24
+// vs 39.62 us, 46 vs 37 VGPRs); the wave-per-row kernel does not gain.
+#ifndef MI355_RMS_KEEP_F32_WAVE
+#define MI355_RMS_KEEP_F32_WAVE 0
+#endif
+#ifndef MI355_RMS_KEEP_F32_BLOCK
+#define MI355_RMS_KEEP_F32_BLOCK 1
+#endif
+
 namespace mi355 {
 
 // Kernel parameters, passed by value.  r / ro / rs / ros are used with ADD only.
@@ -57,22 +74,26 @@ __device__ __forceinline__ float rms_rstd(float sumsq, int n, float eps) {
 
 // One lane's share of a row: VPL packets with packet index slot + k * stride,
 // through buffer descriptors sized to the row, so packets past n read 0 and
-// their stores drop.
+// their stores drop.  A row past the last one gets descriptors of 0 bytes:
+// every access reads 0 or drops, so a kernel that holds several rows at once
+// needs no branch for a ragged last group.
 template <typename TX, typename TW, int VPL>
 struct RowSlice {
   static constexpr int W = pack_width<TX>::value;
   static constexpr uint32_t WB = W * sizeof(typename TW::bits);  // weight bytes per packet
   Packet<TX> xv[VPL];
+  Packet<TX> rv[VPL];  // residual packets (ADD only; dead otherwise)
 
   __device__ __forceinline__ void load_x(rsrc_t rx, int slot, int stride) {
 #pragma unroll
     for (int k = 0; k < VPL; ++k) xv[k].raw = buf_load16(rx, static_cast<uint32_t>(slot + k * stride) * 16u);
   }
-  // xv <- round(xv + residual), the row the norm then runs on.
-  __device__ __forceinline__ void add_residual(rsrc_t rr, int slot, int stride) {
-    Packet<TX> rv[VPL];
+  __device__ __forceinline__ void load_residual(rsrc_t rr, int slot, int stride) {
 #pragma unroll
     for (int k = 0; k < VPL; ++k) rv[k].raw = buf_load16(rr, static_cast<uint32_t>(slot + k * stride) * 16u);
+  }
+  // xv <- round(xv + residual), the row the norm then runs on.
+  __device__ __forceinline__ void add_residual() {
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
       float a[W], b[W];
@@ -98,15 +119,17 @@ struct RowSlice {
     }
     return ss;
   }
-  template <typename TY>
+  template <typename TY, bool KEEP_F32>
   __device__ __forceinline__ void store_y(rsrc_t ry, int slot, int stride, float rstd,
                                           BufChunk<TW, W> (&wv)[VPL]) {
     constexpr uint32_t YB = W * sizeof(typename TY::bits);
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
-      reg_barrier(xv[k].raw);  // re-widen x here instead of keeping fp32 copies from sumsq()
+      if constexpr (!KEEP_F32) {
+        reg_barrier(xv[k].raw);  // re-widen x here instead of keeping fp32 copies from sumsq()
 #pragma unroll
-      for (int d = 0; d < BufChunk<TW, W>::DW; ++d) reg_barrier(wv[k].raw[d]);
+        for (int d = 0; d < BufChunk<TW, W>::DW; ++d) reg_barrier(wv[k].raw[d]);
+      }
       float f[W], o[W];
       xv[k].unpack(f);
 #pragma unroll
@@ -116,59 +139,114 @@ struct RowSlice {
   }
 };
 
-// Loads row r into `row` (adding the residual and storing h with ADD).
-template <typename TX, typename TW, int VPL, bool ADD>
-__device__ __forceinline__ void load_row(RowSlice<TX, TW, VPL>& row, const RmsParams& p, int64_t r, int slot,
-                                         int stride) {
+// Byte extent of row r of a matrix of n-element rows: the whole row, or 0
+// past the last row.
+template <typename T>
+__device__ __forceinline__ uint32_t row_bytes(const RmsParams& p, int64_t r) {
+  return r < p.rows ? static_cast<uint32_t>(p.n) * sizeof(typename T::bits) : 0u;
+}
+
+// The R rows r0 .. r0 + R - 1 of one iteration: every load of every row is
+// issued before the first wait, then (ADD) each row becomes h = x + residual,
+// stored as the new residual.
+template <typename TX, typename TW, int VPL, int R, bool ADD>
+__device__ __forceinline__ void load_rows(RowSlice<TX, TW, VPL> (&row)[R], const RmsParams& p, int64_t r0,
+                                          int slot, int stride) {
   using XB = typename TX::bits;
-  const uint32_t xbytes = static_cast<uint32_t>(p.n) * sizeof(XB);
-  row.load_x(make_rsrc(static_cast<const XB*>(p.x) + r * p.xs, xbytes), slot, stride);
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    row[i].load_x(make_rsrc(static_cast<const XB*>(p.x) + (r0 + i) * p.xs, row_bytes<TX>(p, r0 + i)), slot, stride);
   if constexpr (ADD) {
-    row.add_residual(make_rsrc(static_cast<const XB*>(p.r) + r * p.rs, xbytes), slot, stride);
-    row.store_row(make_rsrc(static_cast<XB*>(p.ro) + r * p.ros, xbytes), slot, stride);
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      row[i].load_residual(make_rsrc(static_cast<const XB*>(p.r) + (r0 + i) * p.rs, row_bytes<TX>(p, r0 + i)), slot,
+                           stride);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      row[i].add_residual();
+      row[i].store_row(make_rsrc(static_cast<XB*>(p.ro) + (r0 + i) * p.ros, row_bytes<TX>(p, r0 + i)), slot,
+                       stride);
+    }
   }
 }
 
-// One wave64 per row.  The grid is normally one-shot (a wave per row); the
-// row loop only repeats when the launcher caps the grid.
-template <typename TX, typename TW, typename TY, int VPL, bool ADD>
-__global__ __launch_bounds__(256) void rmsnorm_wave_rows(const RmsParams p) {
+// The lane's weight packets lane + 64 * k, k < VPL.  With WLDS the workgroup
+// first stages the weight row in LDS (each thread copies 16-byte pieces, so
+// the row is read from L2 once per workgroup instead of once per wave) and
+// every wave then reads its packets from there; otherwise each wave loads its
+// packets itself (an L2 hit after the first wave).  `lds` holds at least
+// 64 * VPL * WB bytes.
+template <typename TW, int W, int VPL, bool WLDS>
+__device__ __forceinline__ void load_weight(BufChunk<TW, W> (&wv)[VPL], const RmsParams& p, int lane,
+                                            uint32_t* lds) {
+  constexpr uint32_t WB = W * sizeof(typename TW::bits);
+  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
+  if constexpr (WLDS) {
+    constexpr uint32_t units = 64u * VPL * WB / 16u;
+    for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
+      const u32x4 v = buf_load16_cached(rw, u * 16u);
+      lds[4 * u] = v.x; lds[4 * u + 1] = v.y; lds[4 * u + 2] = v.z; lds[4 * u + 3] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const uint32_t* q = lds + static_cast<uint32_t>(lane + 64 * k) * (WB / 4u);
+#pragma unroll
+      for (int d = 0; d < BufChunk<TW, W>::DW; ++d) wv[k].raw[d] = q[d];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(lane + 64 * k) * WB);
+  }
+}
+
+// One wave64 per R rows (R consecutive rows per wave, all loaded before the
+// first reduction).  The grid is normally one-shot; the row loop only repeats
+// when the launcher caps the grid.  WLDS: stage the weight through LDS (the
+// launcher passes 64 * VPL * WB bytes of dynamic LDS).
+template <typename TX, typename TW, typename TY, int VPL, int R, bool ADD, bool WLDS>
+__global__ __launch_bounds__(MI355_RMS_WAVE_BLOCK) void rmsnorm_wave_rows(const RmsParams p) {
   using S = RowSlice<TX, TW, VPL>;
+  extern __shared__ uint32_t wlds[];
   const int lane = threadIdx.x & 63;
   const int waves_per_block = blockDim.x >> 6;
-  const uint32_t ybytes = static_cast<uint32_t>(p.n) * sizeof(typename TY::bits);
 
   BufChunk<TW, S::W> wv[VPL];
-  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(lane + 64 * k) * S::WB);
+  load_weight<TW, S::W, VPL, WLDS>(wv, p, lane, wlds);
 
   // The wave's index in its workgroup is wave-uniform; readfirstlane says so,
   // which keeps the row's buffer descriptors in SGPRs (no waterfall loop).
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t step = static_cast<int64_t>(gridDim.x) * waves_per_block;
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; r < p.rows; r += step) {
-    S row;
-    load_row<TX, TW, VPL, ADD>(row, p, r, lane, 64);
-    const float rstd = rms_rstd(wave_allreduce_sum(row.sumsq()), p.n, p.eps);
-    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(p.y) + r * p.ys, ybytes), lane, 64,
-                             rstd, wv);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * waves_per_block * R;
+  for (int64_t r0 = (static_cast<int64_t>(blockIdx.x) * waves_per_block + wave) * R; r0 < p.rows; r0 += step) {
+    S row[R];
+    load_rows<TX, TW, VPL, R, ADD>(row, p, r0, lane, 64);
+    float ss[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) ss[i] = row[i].sumsq();
+#pragma unroll
+    for (int i = 0; i < R; ++i) ss[i] = wave_allreduce_sum(ss[i]);
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      row[i].template store_y<TY, MI355_RMS_KEEP_F32_WAVE != 0>(
+          make_rsrc(static_cast<typename TY::bits*>(p.y) + (r0 + i) * p.ys, row_bytes<TY>(p, r0 + i)), lane, 64,
+          rms_rstd(ss[i], p.n, p.eps), wv);
   }
 }
 
-// One workgroup per row, blockDim.x = 64 * (waves per row) <= 1024 threads;
-// lane t of the workgroup holds packets t + k * blockDim.x, k < VPL.  Used
-// for rows wider than one wave holds comfortably: spreading a row over
-// several waves keeps VGPRs low and the work per wave fine-grained.  Per-wave
-// partial sums meet in LDS, double-buffered so a row costs one barrier.
-template <typename TX, typename TW, typename TY, int VPL, bool ADD>
+// One workgroup per R rows, blockDim.x = 64 * (waves per row) <= 1024
+// threads; lane t of the workgroup holds packets t + k * blockDim.x, k < VPL,
+// of each of its rows.  Used for rows wider than one wave holds comfortably:
+// spreading a row over several waves keeps VGPRs low and the work per wave
+// fine-grained.  Per-wave partial sums meet in LDS, double-buffered so an
+// iteration (R rows) costs one barrier.
+template <typename TX, typename TW, typename TY, int VPL, int R, bool ADD>
 __global__ __launch_bounds__(1024) void rmsnorm_block_rows(const RmsParams p) {
   using S = RowSlice<TX, TW, VPL>;
-  __shared__ float partial[2][16];
+  __shared__ float partial[2][R][16];
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
   const int nwave = nthreads >> 6;
-  const uint32_t ybytes = static_cast<uint32_t>(p.n) * sizeof(typename TY::bits);
 
   BufChunk<TW, S::W> wv[VPL];
   const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
@@ -176,17 +254,31 @@ __global__ __launch_bounds__(1024) void rmsnorm_block_rows(const RmsParams p) {
   for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + nthreads * k) * S::WB);
 
   int buf = 0;
-  for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
-    S row;
-    load_row<TX, TW, VPL, ADD>(row, p, r, tid, nthreads);
-    const float ss = wave_allreduce_sum(row.sumsq());
-    if ((tid & 63) == 0) partial[buf][tid >> 6] = ss;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * R; r0 < p.rows; r0 += static_cast<int64_t>(gridDim.x) * R) {
+    S row[R];
+    load_rows<TX, TW, VPL, R, ADD>(row, p, r0, tid, nthreads);
+    float ss[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) ss[i] = row[i].sumsq();
+#pragma unroll
+    for (int i = 0; i < R; ++i) ss[i] = wave_allreduce_sum(ss[i]);
+    if ((tid & 63) == 0) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) partial[buf][i][tid >> 6] = ss[i];
+    }
     __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < nwave; ++i) tot += partial[buf][i];
-    buf ^= 1;  // the next row writes the other buffer; this row's barrier orders the reuse
-    row.template store_y<TY>(make_rsrc(static_cast<typename TY::bits*>(p.y) + r * p.ys, ybytes), tid, nthreads,
-                             rms_rstd(tot, p.n, p.eps), wv);
+    float tot[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      tot[i] = 0.0f;
+      for (int j = 0; j < nwave; ++j) tot[i] += partial[buf][i][j];
+    }
+    buf ^= 1;  // the next iteration writes the other buffer; this one's barrier orders the reuse
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      row[i].template store_y<TY, MI355_RMS_KEEP_F32_BLOCK != 0>(
+          make_rsrc(static_cast<typename TY::bits*>(p.y) + (r0 + i) * p.ys, row_bytes<TY>(p, r0 + i)), tid,
+          nthreads, rms_rstd(tot[i], p.n, p.eps), wv);
   }
 }
 

@@ -6,19 +6,21 @@
 // tensors are treated as flat memory, as the reference does.
 //
 // silu_mul_chunks: a one-shot grid; block b owns the contiguous chunk of
-// BLOCK * UNROLL 16-byte packets starting at packet b * BLOCK * UNROLL (16 KiB
-// of gate and of up with the defaults).  Lane t moves packets t + j * BLOCK,
-// so every load instruction of a wave covers 1 KiB of contiguous memory.  All
-// 2 * UNROLL loads of a lane are issued before any arithmetic.  Accesses go
+// B * U 16-byte packets starting at packet b * B * U (16 KiB of gate and of
+// up with either shipped shape).  Lane t moves packets t + j * B, so every
+// load instruction of a wave covers 1 KiB of contiguous memory.  All 2 * U
+// loads of a lane are issued before any arithmetic.  Accesses go
 // through per-block buffer descriptors sized to the chunk, so the ragged last
 // chunk needs no lane branches (out-of-range loads read 0, stores drop), and
 // carry the non-temporal hint: every byte is touched once.  The numel % W
 // element tail is finished with scalar accesses by the last block.
 // silu_mul_generic: scalar grid-stride loop for misaligned pointers.
 //
-// Launch shape (BLOCK 512, UNROLL 2, nt loads and stores, one block per
-// chunk rather than a persistent grid) is the fastest measured on MI355X for
-// both the 110 MB and the 1.9 GB BASELINE shapes.
+// Launch shape (nt loads and stores, one block per chunk rather than a
+// persistent grid), measured on MI355X: 512 lanes x 2 packets per lane below
+// MI355_SILU_LARGE_MIN_NUMEL elements (the 110 MB C2 shape: 18.41 vs 18.77
+// us for 256 x 4; 440 MB: 67.70 vs 67.96 us), 256 lanes x 4 packets from
+// there (the 1.86 GB C4 shape: 288.6 vs 291.4 us).
 #include "common.h"
 
 #ifndef MI355_SILU_BLOCK
@@ -27,17 +29,27 @@
 #ifndef MI355_SILU_UNROLL
 #define MI355_SILU_UNROLL 2
 #endif
+#ifndef MI355_SILU_LARGE_BLOCK
+#define MI355_SILU_LARGE_BLOCK 256
+#endif
+#ifndef MI355_SILU_LARGE_UNROLL
+#define MI355_SILU_LARGE_UNROLL 4
+#endif
+#ifndef MI355_SILU_LARGE_MIN_NUMEL
+#define MI355_SILU_LARGE_MIN_NUMEL (int64_t{1} << 27)
+#endif
+// Load issue order of a lane's packets: 0 = gate j, up j, gate j+1, ...;
+// 1 = every gate packet, then every up packet.
+#ifndef MI355_SILU_LOAD_ORDER
+#define MI355_SILU_LOAD_ORDER 0
+#endif
 
 namespace mi355 {
 
-template <typename TI, typename TO>
-__global__ __launch_bounds__(MI355_SILU_BLOCK) void silu_mul_chunks(const void* __restrict__ gate,
-                                                                    const void* __restrict__ up,
-                                                                    void* __restrict__ out,
-                                                                    int64_t numel) {
+template <typename TI, typename TO, int B, int U>
+__global__ __launch_bounds__(B) void silu_mul_chunks(const void* __restrict__ gate, const void* __restrict__ up,
+                                                     void* __restrict__ out, int64_t numel) {
   constexpr int W = pack_width<TI>::value;
-  constexpr int B = MI355_SILU_BLOCK;
-  constexpr int U = MI355_SILU_UNROLL;
   constexpr int OUT_BYTES = W * sizeof(typename TO::bits);  // output bytes per packet
   const int64_t npk = numel / W;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * B * U;
@@ -49,11 +61,18 @@ __global__ __launch_bounds__(MI355_SILU_BLOCK) void silu_mul_chunks(const void* 
   const rsrc_t ro = make_rsrc(static_cast<char*>(out) + first * OUT_BYTES, count * OUT_BYTES);
 
   Packet<TI> gv[U], uv[U];
+  if constexpr (MI355_SILU_LOAD_ORDER == 0) {
 #pragma unroll
-  for (int j = 0; j < U; ++j) {
-    const uint32_t off = (threadIdx.x + j * B) * 16u;
-    gv[j].raw = buf_load16(rg, off);
-    uv[j].raw = buf_load16(ru, off);
+    for (int j = 0; j < U; ++j) {
+      const uint32_t off = (threadIdx.x + j * B) * 16u;
+      gv[j].raw = buf_load16(rg, off);
+      uv[j].raw = buf_load16(ru, off);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < U; ++j) gv[j].raw = buf_load16(rg, (threadIdx.x + j * B) * 16u);
+#pragma unroll
+    for (int j = 0; j < U; ++j) uv[j].raw = buf_load16(ru, (threadIdx.x + j * B) * 16u);
   }
 #pragma unroll
   for (int j = 0; j < U; ++j) {
@@ -98,9 +117,22 @@ int launch_silu(K kernel, int64_t grid, int block, const SiluArgs& a, hipStream_
                     "silu_mul launch");
 }
 
+template <typename TI, typename TO, int B, int U>
+int silu_chunked(const SiluArgs& a, hipStream_t s) {
+  constexpr int W = pack_width<TI>::value;
+  const int64_t npk = a.numel / W;
+  constexpr int64_t chunk = static_cast<int64_t>(B) * U;
+  int64_t grid = (npk + chunk - 1) / chunk;
+  if (grid < 1) grid = 1;  // numel < W: the single block runs the scalar tail
+  if (grid > 0x7fffffff) {
+    set_error("mi355_silu_mul_fwd: numel %lld needs more than 2^31 workgroups", static_cast<long long>(a.numel));
+    return MI355_ERR_UNSUPPORTED;
+  }
+  return launch_silu(silu_mul_chunks<TI, TO, B, U>, grid, B, a, s);
+}
+
 template <typename TI, typename TO>
 int silu_typed(const SiluArgs& a, hipStream_t s, int cus) {
-  constexpr int W = pack_width<TI>::value;
   const bool vec_ok = aligned16(a.gate) && aligned16(a.up) && aligned16(a.out);
   if (!vec_ok) {
     int64_t grid = (a.numel + 255) / 256;
@@ -108,15 +140,9 @@ int silu_typed(const SiluArgs& a, hipStream_t s, int cus) {
     if (grid > cap) grid = cap;
     return launch_silu(silu_mul_generic<TI, TO>, grid, 256, a, s);
   }
-  const int64_t npk = a.numel / W;
-  constexpr int64_t chunk = static_cast<int64_t>(MI355_SILU_BLOCK) * MI355_SILU_UNROLL;
-  int64_t grid = (npk + chunk - 1) / chunk;
-  if (grid < 1) grid = 1;  // numel < W: the single block runs the scalar tail
-  if (grid > 0x7fffffff) {
-    set_error("mi355_silu_mul_fwd: numel %lld needs more than 2^31 workgroups", static_cast<long long>(a.numel));
-    return MI355_ERR_UNSUPPORTED;
-  }
-  return launch_silu(silu_mul_chunks<TI, TO>, grid, MI355_SILU_BLOCK, a, s);
+  if (a.numel >= MI355_SILU_LARGE_MIN_NUMEL)
+    return silu_chunked<TI, TO, MI355_SILU_LARGE_BLOCK, MI355_SILU_LARGE_UNROLL>(a, s);
+  return silu_chunked<TI, TO, MI355_SILU_BLOCK, MI355_SILU_UNROLL>(a, s);
 }
 
 }  // namespace

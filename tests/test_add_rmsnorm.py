@@ -31,6 +31,8 @@ def _lib():
     (2048, 1536, F16, F16), (16384, 3584, BF16, BF16),
     (1, 1536, F16, F16), (8, 1536, F16, F16), (32, 1536, F16, F16),
     (7, 100, F16, F16), (5, 8200, BF16, BF16), (9, 896, F16, F32), (6, 2048, F32, F32), (3, 40000, BF16, BF16),
+    # from 1024 rows up a wave holds two rows: an odd count leaves a lone row
+    (1025, 1536, F16, F16), (2049, 2048, F16, F32), (1031, 896, BF16, BF16),
 ])
 def test_add_rmsnorm_matches_oracle(pkg, orc, cuda, rows, n, dt, wdt):
     x = randn((rows, n), 50, dt)
@@ -50,7 +52,7 @@ def test_add_rmsnorm_matches_oracle(pkg, orc, cuda, rows, n, dt, wdt):
 
 
 @pytest.mark.parametrize("rows,n,dt", [(2048, 1536, F16), (16384, 3584, BF16), (8, 1536, F16),
-                                       (7, 100, F16), (5, 8200, BF16)])
+                                       (7, 100, F16), (5, 8200, BF16), (1027, 1536, F16)])
 def test_add_rmsnorm_equals_add_then_norm(pkg, cuda, rows, n, dt):
     x = randn((rows, n), 60, dt).to(cuda)
     r = randn((rows, n), 61, dt, std=4.0).to(cuda)
@@ -62,11 +64,13 @@ def test_add_rmsnorm_equals_add_then_norm(pkg, cuda, rows, n, dt):
     assert torch.equal(y1, y2)
 
 
-def test_add_rmsnorm_in_place_through_abi(pkg, cuda):
+@pytest.mark.parametrize("rows", [64, 1025])
+def test_add_rmsnorm_in_place_through_abi(pkg, cuda, rows):
     """residual_out = residual and y = x (the in-place form a decoder loop
-    uses): same bits as the out-of-place call."""
+    uses): same bits as the out-of-place call, also where each wave holds two
+    rows (1025 rows: the last wave holds one)."""
     L = _lib()
-    rows, n = 64, 1536
+    n = 1536
     x = randn((rows, n), 70, F16).to(cuda)
     r = randn((rows, n), 71, F16).to(cuda)
     w = randn((n,), 72, F16, mean=1.0, std=0.1).to(cuda)

@@ -2,6 +2,7 @@
 roofline figures, the rocprofv3 summary (durations -> GB/s, PMC counters ->
 HBM traffic through the copy-probe calibration), and the one-GPU contract."""
 import csv
+import importlib
 import importlib.util
 import subprocess
 import sys
@@ -47,7 +48,7 @@ def _write(path, rows):
 
 
 def test_rocprof_summary_turns_traces_and_counters_into_rates(bench, tmp_path):
-    c2 = "void mi355::silu_mul_chunks<mi355::F16, mi355::F16>(mi355::SiluArgs)"
+    c2 = "void mi355::silu_mul_chunks<mi355::F16, mi355::F16, 512, 2>(void const*, void const*, void*, long)"
     copy = "stream_copy(unsigned int const*, unsigned int*, unsigned long)"
     _write(tmp_path / "run_kernel_trace.csv", [
         {"Kernel_Name": c2, "Grid_Size_X": 1146880, "Grid_Size_Y": 1, "Grid_Size_Z": 1,
@@ -91,3 +92,40 @@ def test_more_than_one_gpu_is_refused():
                        cwd=str(ROOT), timeout=300)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def _kernel(bench, nbytes, us):
+    return bench.kernel_entry("k", nbytes, us)
+
+
+def test_per_config_block_carries_every_config_and_decode_latency(bench):
+    # the compact block the driver keeps inside `roofline`: C1 / C2 / C4
+    # fractions, same-size probe times, and the C3 decode latencies per M
+    k = {"c1_rmsnorm_f16_2048x1536": _kernel(bench, 12_585_984, 4.0),
+         "c1_rmsnorm_f16_2048x1536_graph": _kernel(bench, 12_585_984, 3.5),
+         "c2_silu_mul_f16_2048x8960": _kernel(bench, 110_100_480, 18.0)}
+    c4 = {"c4_rmsnorm_bf16_16384x3584": _kernel(bench, 234_888_192, 39.5),
+          "c4_silu_mul_bf16_16384x18944": _kernel(bench, 1_862_270_976, 286.0)}
+    dec = {f"M={m}": {"rmsnorm_api_us": 15.0, "silu_mul_api_us": 15.5, "rmsnorm_device_us": 3.9,
+                      "silu_mul_device_us": 4.1, "graph_per_kernel_us": 1.7 + m / 100,
+                      "graph_replay_us": 84 * (1.7 + m / 100)} for m in (1, 2, 4, 8, 32)}
+    dec["floor"] = {"empty_kernel_graph_node_us": 1.6, "row_copy_graph_node_us": 1.6}
+    ceil = {lab: {"us": 1.0} for lab, _, _ in bench.CEILING_SHAPES}
+    pc = bench.per_config({"kernels": k, "c4": c4, "decode": dec, "ceilings": ceil,
+                           "copy_ceiling": {"frac_of_peak": 0.82}})
+    assert pc["C1_rmsnorm_f16_2048x1536"]["frac"] == round(12_585_984 / 4.0 / 1e3 / 8000, 4)
+    assert pc["C1_rmsnorm_f16_2048x1536"]["graph_us"] == 3.5
+    assert pc["C4_silu_mul_bf16_16384x18944"]["frac"] == round(1_862_270_976 / 286.0 / 1e3 / 8000, 4)
+    assert set(pc["C3_decode_f16_latency"]) == {"M1", "M2", "M4", "M8", "M32"}
+    assert pc["C3_decode_f16_latency"]["M8"]["graph_node_us"] == 1.78
+    assert all("probe_us" in pc[c] for c in ("C1_rmsnorm_f16_2048x1536", "C2_silu_mul_f16_2048x8960",
+                                             "C4_rmsnorm_bf16_16384x3584", "C4_silu_mul_bf16_16384x18944"))
+    import json
+    assert len(json.dumps(pc)) < 2500  # the whole stdout line stays far below the driver's 16 KB tail
+
+
+def test_variant_names_resolve_to_build_outputs(bench):
+    b = importlib.import_module("llm-inference-optimizer_amd.build")
+    for name in b.VARIANTS:
+        assert bench.variant_lib(name) == b.variant_path(name)
+    assert b.REORDERING_VARIANTS <= set(b.VARIANTS)

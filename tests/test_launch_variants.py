@@ -1,0 +1,124 @@
+"""Launch-shape variants (``build.py --variant NAME``) compute what the
+default library computes.
+
+A variant rebuilds one translation unit under other launch-shape switches:
+several rows held per wave or per workgroup (rows past the last one get
+0-byte buffer descriptors), the weight staged through LDS, persistent grids,
+other workgroup sizes, other SiLU-and-mul chunkings.  These may not change a
+bit of any output, so each is checked bitwise against the default library
+(itself checked against the oracle in test_fused_norm_activation_kernels.py)
+on the BASELINE shapes and on ragged row counts that leave a partial group
+of rows at the end.  The variants that spread a row over waves differently
+(so the fp32 sum of squares adds in another order) are held to the oracle's
+1-ulp bar instead, and their residual output (no reduction) still bitwise.
+Variants that are not built are skipped.
+"""
+import importlib
+
+import pytest
+import torch
+
+from parity_utils import DT_NAME, storage, ulp_report
+
+L = importlib.import_module("llm-inference-optimizer_amd._lib")
+B = importlib.import_module("llm-inference-optimizer_amd.build")
+
+RMS_VARIANTS = [n for n, (unit, _) in B.VARIANTS.items() if unit == "rmsnorm"]
+SILU_VARIANTS = [n for n, (unit, _) in B.VARIANTS.items() if unit == "silu_mul"]
+
+# (rows, n, x dtype, weight dtype): C1, C4, row counts one past / a few past a
+# multiple of 2 and 4 rows per group, narrow and wide rows, an fp32 weight,
+# and decode rows (below the multi-row threshold)
+RMS_SHAPES = [
+    (2048, 1536, torch.float16, torch.float16),
+    (16384, 3584, torch.bfloat16, torch.bfloat16),
+    (1025, 1536, torch.float16, torch.float16),
+    (3003, 3584, torch.bfloat16, torch.bfloat16),
+    (1027, 896, torch.bfloat16, torch.bfloat16),
+    (1029, 4096, torch.float16, torch.float32),
+    (2049, 2048, torch.float16, torch.float16),
+    (8, 1536, torch.float16, torch.float16),
+]
+SILU_NUMELS = [2048 * 8960, 1_234_567, 8 * 37, 3 * 8960]
+
+
+def abi_stream():
+    return L.stream_handle(torch.cuda.current_device())
+
+
+def _variant(name):
+    path = B.variant_path(name)
+    if not path.exists():
+        pytest.skip(f"variant {name} not built (python llm-inference-optimizer_amd/build.py --variant {name})")
+    return L.load_variant(path)
+
+
+def _gen(seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _rms(lib, x, w, y, add=None):
+    rows, n = x.shape
+    c = L.DTYPE_CODE
+    if add is None:
+        st = lib.mi355_rmsnorm_fwd(x.data_ptr(), w.data_ptr(), y.data_ptr(), rows, n, n, n, 1e-6, c[x.dtype],
+                                   c[w.dtype], c[y.dtype], abi_stream())
+    else:
+        r, h = add
+        st = lib.mi355_add_rmsnorm_fwd(x.data_ptr(), r.data_ptr(), w.data_ptr(), y.data_ptr(), h.data_ptr(), rows,
+                                       n, n, n, n, n, 1e-6, c[x.dtype], c[w.dtype], c[y.dtype], abi_stream())
+    assert st == 0, lib.mi355_last_error().decode()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", RMS_VARIANTS)
+def test_rmsnorm_variant_is_bitwise_the_default(name, orc, cuda):
+    lib = _variant(name)
+    ref_lib = L.load()
+    for i, (rows, n, dt, wdt) in enumerate(RMS_SHAPES):
+        print(f"variant {name}: rmsnorm rows={rows} n={n} {dt} weight {wdt}", flush=True)
+        x = torch.randn(rows, n, generator=_gen(10 + i)).to(dt).to(cuda)
+        r = torch.randn(rows, n, generator=_gen(40 + i)).to(dt).to(cuda)
+        w = (1 + 0.1 * torch.randn(n, generator=_gen(70 + i))).to(wdt).to(cuda)
+        outs = {}
+        for tag, lb in (("default", ref_lib), (name, lib)):
+            y = torch.full_like(x, float("nan"))
+            _rms(lb, x, w, y)
+            ya, ha = torch.full_like(x, float("nan")), torch.full_like(x, float("nan"))
+            _rms(lb, x, w, ya, add=(r, ha))
+            torch.cuda.synchronize()
+            outs[tag] = (y, ya, ha)
+        if name not in B.REORDERING_VARIANTS:
+            for a, b in zip(outs["default"], outs[name]):
+                assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (name, rows, n, dt)
+            continue
+        y, ya, ha = outs[name]
+        assert torch.equal(ha.view(torch.int16), outs["default"][2].view(torch.int16)), (name, rows, n, dt)
+        d, wd = DT_NAME[dt], DT_NAME[wdt]
+        for got, src in ((y, x), (ya, ha)):
+            want = orc.rmsnorm(storage(src), storage(w), 1e-6, xdt=d, wdt=wd)
+            mx, frac = ulp_report(storage(got).reshape(want.shape), want, orc)
+            assert mx <= 1 and frac <= 0.01, (name, rows, n, dt, mx, frac)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", SILU_VARIANTS)
+def test_silu_mul_variant_is_bitwise_the_default(name, cuda):
+    lib = _variant(name)
+    ref_lib = L.load()
+    for i, numel in enumerate(SILU_NUMELS):
+        for dt in (torch.float16, torch.bfloat16):
+            print(f"variant {name}: silu_mul numel={numel} {dt}", flush=True)
+            g = torch.randn(numel, generator=_gen(100 + i)).to(dt).to(cuda)
+            u = torch.randn(numel, generator=_gen(200 + i)).to(dt).to(cuda)
+            outs = []
+            for lb in (ref_lib, lib):
+                o = torch.full_like(g, float("nan"))
+                c = L.DTYPE_CODE[dt]
+                st = lb.mi355_silu_mul_fwd(g.data_ptr(), u.data_ptr(), o.data_ptr(), numel, c, c, abi_stream())
+                assert st == 0, lb.mi355_last_error().decode()
+                torch.cuda.synchronize()
+                outs.append(o)
+            assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, numel, dt)
