@@ -116,6 +116,27 @@ Rows rows_of(const at::Tensor& t, int64_t n) {
   return {t2, m, m > 1 ? t2.stride(0) : n};
 }
 
+// x as [rows, k] rows a projection kernel can stream: unit element stride
+// and, over more than one row, rows that do not overlap (row stride >= k).
+// A broadcast or overlapping view -- expand() gives row stride 0 -- is
+// copied, as the reference's `x.reshape(-1, K).contiguous()` copies it.
+at::Tensor matrix_rows(const at::Tensor& x, int64_t k) {
+  at::Tensor x2 = x.reshape({-1, k});
+  if (x2.stride(-1) != 1 || (x2.size(0) > 1 && x2.stride(0) < k)) x2 = x2.contiguous();
+  return x2;
+}
+
+// Weight matrices [n, k] the kernels stream row by row: each with unit
+// element stride and non-overlapping rows, and (for a pair read together)
+// one shared row stride; copied otherwise.
+bool streamable(const at::Tensor& w) {
+  return w.stride(-1) == 1 && (w.size(0) <= 1 || w.stride(0) >= w.size(1));
+}
+std::pair<at::Tensor, at::Tensor> weight_pair(const at::Tensor& a, const at::Tensor& b) {
+  if (streamable(a) && streamable(b) && a.stride(0) == b.stride(0)) return {a, b};
+  return {a.contiguous(), b.contiguous()};
+}
+
 std::vector<int64_t> with_last(at::IntArrayRef s, int64_t last) {
   std::vector<int64_t> v(s.begin(), s.end());
   v.back() = last;
@@ -231,13 +252,8 @@ at::Tensor gate_up_silu(const at::Tensor& x, const at::Tensor& w_gate, const at:
   const at::ScalarType odt = out_f32 ? at::kFloat : x.scalar_type();
 
   const int64_t n_out = w_gate.size(0);
-  at::Tensor x2 = x.reshape({-1, k});
-  if (x2.stride(-1) != 1) x2 = x2.contiguous();
-  at::Tensor wg = w_gate, wu = w_up;
-  if (wg.stride(-1) != 1 || wu.stride(-1) != 1 || wg.stride(0) != wu.stride(0)) {
-    wg = wg.contiguous();
-    wu = wu.contiguous();
-  }
+  const at::Tensor x2 = matrix_rows(x, k);
+  const auto [wg, wu] = weight_pair(w_gate, w_up);
   const int64_t rows = x2.size(0);
   at::Tensor out = at::empty({rows, n_out}, x.options().dtype(odt));
   if (rows && n_out) {
@@ -274,9 +290,8 @@ at::Tensor linear16(const at::Tensor& x, const at::Tensor& weight, const c10::op
     fail_assert("x, weight and bias must share a device");
   const at::ScalarType odt = out_f32 ? at::kFloat : x.scalar_type();
 
-  at::Tensor x2 = x.reshape({-1, K});
-  if (x2.stride(-1) != 1) x2 = x2.contiguous();
-  const at::Tensor w = weight.stride(-1) != 1 ? weight.contiguous() : weight;
+  const at::Tensor x2 = matrix_rows(x, K);
+  const at::Tensor w = streamable(weight) ? weight : weight.contiguous();
   const at::Tensor b = has_bias ? bias->contiguous() : at::Tensor();
   const int64_t M = x2.size(0);
   at::Tensor out = at::empty({M, N}, x.options().dtype(odt));
@@ -311,12 +326,12 @@ at::Tensor w8a16_linear(const at::Tensor& x, const at::Tensor& w_q, const at::Te
     fail_assert("bias must be a (" + std::to_string(N) + ",) float GPU tensor, got " + shape_str(bias->sizes()) + " " +
                 dtype_str(bias->scalar_type()));
   const int dev = x.get_device();
-  if (w_q.get_device() != dev || scale.get_device() != dev) fail_assert("x, w_q and scale must share a device");
+  if (w_q.get_device() != dev || scale.get_device() != dev || (has_bias && bias->get_device() != dev))
+    fail_assert("x, w_q, scale and bias must share a device");
   const at::ScalarType odt = out_f32 ? at::kFloat : x.scalar_type();
 
-  at::Tensor x2 = x.reshape({-1, K});
-  if (x2.stride(-1) != 1) x2 = x2.contiguous();
-  const at::Tensor q = w_q.stride(-1) != 1 ? w_q.contiguous() : w_q;
+  const at::Tensor x2 = matrix_rows(x, K);
+  const at::Tensor q = streamable(w_q) ? w_q : w_q.contiguous();
   const at::Tensor s = scale.contiguous();
   const at::Tensor b = has_bias ? bias->contiguous() : at::Tensor();
   const int64_t M = x2.size(0);
@@ -356,13 +371,8 @@ at::Tensor gate_up_silu_w8a16(const at::Tensor& x, const at::Tensor& wq_gate, co
   }
   const at::ScalarType odt = out_f32 ? at::kFloat : x.scalar_type();
 
-  at::Tensor x2 = x.reshape({-1, K});
-  if (x2.stride(-1) != 1) x2 = x2.contiguous();
-  at::Tensor qg = wq_gate, qu = wq_up;
-  if (qg.stride(-1) != 1 || qu.stride(-1) != 1 || qg.stride(0) != qu.stride(0)) {
-    qg = qg.contiguous();
-    qu = qu.contiguous();
-  }
+  const at::Tensor x2 = matrix_rows(x, K);
+  const auto [qg, qu] = weight_pair(wq_gate, wq_up);
   const at::Tensor sg = scale_gate.contiguous(), su = scale_up.contiguous();
   const int64_t M = x2.size(0);
   at::Tensor out = at::empty({M, N}, x.options().dtype(odt));

@@ -27,8 +27,10 @@ class GraphedGreedyDecoder:
     ``batch_size`` and ``max_cache_len`` fix the static buffers (one graph per
     decoder).  ``generate(input_ids, max_new_tokens)`` returns the prompt
     followed by the generated tokens, like ``generate_graphed`` in the
-    reference (:177-186).  ``use_graph=False`` runs the identical static-cache
-    step eagerly (for comparison)."""
+    reference (:177-186); with ``return_logits=True`` it also returns the
+    last-position logits behind each generated token, [batch, new, vocab]
+    (the prefill's, then each step's).  ``use_graph=False`` runs the
+    identical static-cache step eagerly (for comparison)."""
 
     def __init__(self, model, batch_size: int, max_cache_len: int, use_graph: bool = True):
         from transformers import StaticCache
@@ -44,9 +46,10 @@ class GraphedGreedyDecoder:
         self._pos0 = self._pos.view(())  # 0-d view for the cache's write counters
         self._pos_ids = torch.zeros((batch_size, 1), dtype=torch.long, device=self.device)
         self._next = None
+        self._logits = None
         self._graph = None
 
-    def _step(self) -> torch.Tensor:
+    def _step(self) -> tuple[torch.Tensor, torch.Tensor]:
         # HF's StaticLayer writes at its own device-side counter
         # (cumulative_length) and bumps it in place; pin every layer's counter
         # to the cache position first, so warm-up, capture and replays all
@@ -55,7 +58,8 @@ class GraphedGreedyDecoder:
         torch._foreach_copy_(counters, [self._pos0] * len(counters))
         out = self.model(input_ids=self._tok, past_key_values=self.cache, cache_position=self._pos,
                          position_ids=self._pos_ids, use_cache=True)
-        return out.logits[:, -1].argmax(-1, keepdim=True)
+        logits = out.logits[:, -1]
+        return logits, logits.argmax(-1, keepdim=True)
 
     def _capture(self) -> None:
         side = torch.cuda.Stream(device=self.device)
@@ -66,10 +70,10 @@ class GraphedGreedyDecoder:
         torch.cuda.synchronize(self.device)
         self._graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self._graph):
-            self._next = self._step()
+            self._logits, self._next = self._step()
 
     @torch.inference_mode()
-    def generate(self, input_ids: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, return_logits: bool = False):
         B, S = input_ids.shape
         if B != self.batch_size:
             raise ValueError(f"batch size {B} != the decoder's {self.batch_size}")
@@ -79,18 +83,24 @@ class GraphedGreedyDecoder:
         pos = torch.arange(S, device=self.device)
         out = self.model(input_ids=input_ids, past_key_values=self.cache, cache_position=pos,
                          position_ids=pos.unsqueeze(0).expand(B, S), use_cache=True)
-        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        logits = out.logits[:, -1]
+        tok = logits.argmax(-1, keepdim=True)
         toks = [tok]
+        step_logits = [logits.to(torch.float32, copy=True)] if return_logits else None
         for i in range(max_new_tokens - 1):
             self._tok.copy_(tok)
             self._pos.fill_(S + i)
             self._pos_ids.fill_(S + i)
             if not self.use_graph:
-                tok = self._step()
+                logits, tok = self._step()
             else:
                 if self._graph is None:
                     self._capture()
                 self._graph.replay()
-                tok = self._next.clone()
+                logits, tok = self._logits, self._next.clone()
             toks.append(tok)
-        return torch.cat([input_ids] + toks, dim=1)
+            if return_logits:
+                # a copy: the graph's output buffer is rewritten by the next replay
+                step_logits.append(logits.to(torch.float32, copy=True))
+        ids = torch.cat([input_ids] + toks, dim=1)
+        return (ids, torch.stack(step_logits, dim=1)) if return_logits else ids

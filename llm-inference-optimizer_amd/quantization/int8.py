@@ -1,21 +1,33 @@
-"""INT8 weight-only quantisation of a loaded model, by module replacement.
+"""Weight-only int8 (W8A16) for the decoder's linear layers, by module
+replacement.
 
-Mirrors the reference's quantisation stage (src/quantization/int8.py): every
-``nn.Linear`` inside ``model.model.layers`` (q/k/v/o and gate/up/down) is
-replaced in its parent's registry by a ``QuantizedLinearInt8`` holding int8
-weights and one fp32 scale per output feature; embeddings and ``lm_head``
-keep their dtype (for Qwen2.5-1.5B they are tied).  The replacement modules
-are plain callables, so HF's forward and the graph-captured decoder use them
-unchanged, and they compose with ``patch_model_with_fused_kernels`` (FusedMLP
-calls its projections as modules).
+Interface: the reference's quantisation stage (src/quantization/int8.py:32-100)
+-- the ``QuantizedLinearInt8`` module (buffers ``weight_q``, ``scale``,
+``bias``; ``from_linear``, ``dequantized_weight``, ``num_bytes``) and
+``quantize_model_int8(model)`` returning ``layers_quantized`` /
+``bytes_before`` / ``bytes_after``.
 
-Both the quantiser and the forward run as gfx950 HIP kernels
-(``quantize_int8_weight`` and ``w8a16_linear``); there is no torch or CPU
-fallback, so the model must be on the GPU.
+What the modules hold and run here:
+
+* ``weight_q`` -- the int8 codes, [out_features, in_features], in nn.Linear's
+  own row order, so the HIP kernels stream them as they are (no repacking);
+* ``scale`` -- one fp32 step per output feature; an output feature's weights
+  are ``weight_q[j] * scale[j]``;
+* ``bias`` -- the original bias (its own dtype) or None.
+
+Quantisation (``quantize_int8_weight``: one wave per weight row, on the GPU)
+and the product (``w8a16_linear``: int8 codes widened in registers, fp32
+accumulation, the scale applied per output feature in the epilogue) are both
+gfx950 HIP kernels; nothing falls back to torch or the CPU, so a model must
+be on the GPU to be quantised or run.  Only the linears inside
+``model.model.layers`` are replaced (attention q/k/v/o and the MLP's
+gate/up/down); the embedding and ``lm_head`` keep their dtype.  The modules
+are ordinary callables, so HF's forward, ``patch_model_with_fused_kernels``
+(whose FusedMLP then runs the int8 gate/up kernel) and the graph-captured
+decoder all use them unchanged.
 """
 from __future__ import annotations
 
-import gc
 from typing import Optional
 
 import torch
@@ -26,35 +38,48 @@ from ..kernels.w8a16_matmul_hip import quantize_int8_weight, w8a16_linear
 __all__ = ["QuantizedLinearInt8", "quantize_model_int8"]
 
 
+def _nbytes(*tensors: Optional[torch.Tensor]) -> int:
+    return sum(t.numel() * t.element_size() for t in tensors if t is not None)
+
+
 class QuantizedLinearInt8(nn.Module):
-    """Drop-in replacement for nn.Linear holding int8 weights plus a
-    per-output-channel float32 scale (src/quantization/int8.py:32-63).
-    Weights and scales are buffers: an inference-only module."""
+    """An ``nn.Linear`` stand-in whose weight is stored as int8 codes plus one
+    fp32 scale per output feature: ``y = x @ (weight_q * scale[:, None]).T +
+    bias``, computed by the W8A16 kernel without ever forming the 16-bit
+    weight.  It has no parameters (inference only); codes, scales and bias
+    are buffers, so ``.to()``, ``state_dict`` and graph capture see them."""
 
     def __init__(self, weight_q: torch.Tensor, scale: torch.Tensor, bias: Optional[torch.Tensor]):
         super().__init__()
+        if weight_q.dtype != torch.int8 or weight_q.dim() != 2:
+            raise ValueError(f"weight_q must be a 2-D int8 tensor, got {weight_q.dtype} {tuple(weight_q.shape)}")
+        if scale.shape != weight_q.shape[:1]:
+            raise ValueError(f"scale must hold one value per output feature ({weight_q.shape[0]}), "
+                             f"got {tuple(scale.shape)}")
+        self.out_features, self.in_features = weight_q.shape
         self.register_buffer("weight_q", weight_q)
         self.register_buffer("scale", scale)
-        self.register_buffer("bias", bias)  # None is allowed
-        self.out_features, self.in_features = weight_q.shape
+        self.register_buffer("bias", bias)
 
     @classmethod
     def from_linear(cls, linear: nn.Linear) -> "QuantizedLinearInt8":
-        """Quantise ``linear`` (on the GPU) with the HIP quantiser: scale =
-        max(max|w_row| / 127, 1e-8), w_q = clamp(round(w / scale), -127, 127)."""
-        w_q, scale = quantize_int8_weight(linear.weight)
-        bias = linear.bias.detach().clone() if linear.bias is not None else None
-        return cls(w_q, scale, bias)
+        """Quantises ``linear`` on its GPU: per output feature, scale =
+        max(max|w| / 127, 1e-8) and codes = clamp(round-half-even(w / scale),
+        -127, 127).  The bias is copied, not shared."""
+        codes, scale = quantize_int8_weight(linear.weight)
+        bias = None if linear.bias is None else linear.bias.detach().clone()
+        return cls(codes, scale, bias)
 
     def dequantized_weight(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
-        return (self.weight_q.float() * self.scale[:, None]).to(dtype)
+        """The dense [out_features, in_features] weight the codes stand for,
+        in ``dtype`` (for checks and comparisons; the forward never builds
+        it)."""
+        dense = self.weight_q.to(torch.float32) * self.scale.to(torch.float32).unsqueeze(1)
+        return dense.to(dtype)
 
     def num_bytes(self) -> int:
-        total = self.weight_q.numel() * self.weight_q.element_size()
-        total += self.scale.numel() * self.scale.element_size()
-        if self.bias is not None:
-            total += self.bias.numel() * self.bias.element_size()
-        return total
+        """Bytes of device memory the module holds: codes, scales and bias."""
+        return _nbytes(self.weight_q, self.scale, self.bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return w8a16_linear(x, self.weight_q, self.scale, self.bias)
@@ -63,38 +88,26 @@ class QuantizedLinearInt8(nn.Module):
         return f"in_features={self.in_features}, out_features={self.out_features}, bias={self.bias is not None}"
 
 
-def _linear_bytes(linear: nn.Linear) -> int:
-    total = linear.weight.numel() * linear.weight.element_size()
-    if linear.bias is not None:
-        total += linear.bias.numel() * linear.bias.element_size()
-    return total
-
-
 def quantize_model_int8(model: nn.Module) -> dict:
-    """Replaces every nn.Linear inside ``model.model.layers`` with a
-    QuantizedLinearInt8, in place (src/quantization/int8.py:73-100).  Returns
-    ``{"layers_quantized", "bytes_before", "bytes_after"}``; callers should
-    check ``layers_quantized > 0`` (an unrecognised layout quantises nothing)."""
-    layers_root = model.model.layers
-    layers_quantized = 0
-    bytes_before = 0
-    bytes_after = 0
-
-    for parent in list(layers_root.modules()):
-        for child_name, child in list(parent.named_children()):
-            if isinstance(child, nn.Linear):
-                bytes_before += _linear_bytes(child)
-                quantized = QuantizedLinearInt8.from_linear(child)
-                bytes_after += quantized.num_bytes()
-                setattr(parent, child_name, quantized)
-                layers_quantized += 1
-
-    gc.collect()
+    """Replaces, in place, every ``nn.Linear`` under ``model.model.layers``
+    with a ``QuantizedLinearInt8`` and reports how many were replaced and the
+    bytes of those layers before and after (weights, scales, biases).  A
+    model whose decoder layers hold no ``nn.Linear`` is left as it is and
+    reports 0 replacements, so callers should check the count."""
+    decoder_layers = model.model.layers
+    # (parent, attribute) of every linear, listed before the first swap so the
+    # walk never visits a replacement; each 16-bit linear is released as soon
+    # as its replacement is in place.
+    slots = [(parent, name) for parent in decoder_layers.modules()
+             for name, child in parent.named_children() if isinstance(child, nn.Linear)]
+    bytes_16bit = bytes_int8 = 0
+    for parent, name in slots:
+        linear = getattr(parent, name)
+        quantized = QuantizedLinearInt8.from_linear(linear)
+        bytes_16bit += _nbytes(linear.weight, linear.bias)
+        bytes_int8 += quantized.num_bytes()
+        setattr(parent, name, quantized)
+        del linear
     if torch.cuda.is_available():
-        torch.cuda.empty_cache()
-
-    return {
-        "layers_quantized": layers_quantized,
-        "bytes_before": bytes_before,
-        "bytes_after": bytes_after,
-    }
+        torch.cuda.empty_cache()  # hand the released 16-bit weights back to the device
+    return {"layers_quantized": len(slots), "bytes_before": bytes_16bit, "bytes_after": bytes_int8}

@@ -18,7 +18,7 @@ F16 = torch.float16
 LAYERS, N, I = 28, 1536, 8960
 
 
-@pytest.mark.parametrize("M", [1, 8, 32])
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 32])  # config 3's decode batch sizes
 def test_28_layer_graph_replays_match_eager(pkg, cuda, M):
     xs = [torch.empty((M, N), dtype=F16, device=cuda) for _ in range(LAYERS)]
     gs = [torch.empty((M, I), dtype=F16, device=cuda) for _ in range(LAYERS)]

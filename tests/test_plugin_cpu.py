@@ -169,3 +169,34 @@ def test_hip_down_leaves_fp32_and_large_inputs_to_the_module(pkg):
     big = torch.randn(pkg.LINEAR16_MAX_ROWS + 1, 128).half()
     mlp.down_proj.half()
     assert torch.equal(mlp.down(big), mlp.down_proj(big))
+
+
+def test_quantized_linear_module_host_side(pkg):
+    """QuantizedLinearInt8's host-side surface (the reference's interface,
+    src/quantization/int8.py:32-63): buffers, sizes, the dense weight the
+    codes stand for, and shape checks."""
+    codes = torch.tensor([[1, -2, 127], [0, -127, 5]], dtype=torch.int8)
+    scale = torch.tensor([0.5, 0.25], dtype=torch.float32)
+    bias = torch.tensor([1.0, -1.0], dtype=torch.float16)
+    q = pkg.QuantizedLinearInt8(codes, scale, bias)
+    assert (q.in_features, q.out_features) == (3, 2)
+    assert dict(q.named_buffers()).keys() == {"weight_q", "scale", "bias"} and not list(q.parameters())
+    want = torch.tensor([[0.5, -1.0, 63.5], [0.0, -31.75, 1.25]])
+    assert torch.equal(q.dequantized_weight(), want)
+    assert q.dequantized_weight(torch.float16).dtype == torch.float16
+    assert q.num_bytes() == 6 + 8 + 4
+    assert pkg.QuantizedLinearInt8(codes, scale, None).num_bytes() == 14
+    assert "bias=True" in repr(q)
+    with pytest.raises(ValueError):
+        pkg.QuantizedLinearInt8(codes.float(), scale, None)
+    with pytest.raises(ValueError):
+        pkg.QuantizedLinearInt8(codes, scale[:1], None)
+
+
+def test_quantize_model_without_linears_reports_zero(pkg):
+    """A model whose decoder layers hold no nn.Linear is left untouched and
+    reports zero replacements (no GPU needed: nothing is quantised)."""
+    model = torch.nn.Module()
+    model.model = torch.nn.Module()
+    model.model.layers = torch.nn.ModuleList([torch.nn.LayerNorm(8) for _ in range(3)])
+    assert pkg.quantize_model_int8(model) == {"layers_quantized": 0, "bytes_before": 0, "bytes_after": 0}
