@@ -99,3 +99,33 @@ def test_kernel_matches_silu_fixture(pkg, cuda, path):
     big = np.abs(f["y_exact"]) > 1e-3
     err = np.abs(out - f["y_exact"])[big] / _ulp_bound(f["y_exact"][big], dt)
     assert err.max() <= 0.5 + 1e-2, err.max()
+
+
+# ---- the package's naive references (the reference's naive_rmsnorm_reference /
+# naive_silu_mul_reference, src/kernels/fused_rmsnorm_triton.py:74-82 and
+# fused_swiglu_triton.py:56-59) on CPU tensors: HF's two-rounding formula, so
+# they must reproduce the fixtures' y_hf -- written from transformers'
+# Qwen2RMSNorm and torch's F.silu -- bit for bit, and the oracle's HF mode.
+
+@pytest.mark.parametrize("path", RMS, ids=lambda p: p.stem)
+def test_naive_rmsnorm_reference_reproduces_hf(pkg, orc, path):
+    g = _load(path)
+    xdt, wdt, hdt = DT[str(g["xdt"])], DT[str(g["wdt"])], DT[str(g["hf_dt"])]
+    x, w = _to_torch(g["x"], xdt), _to_torch(g["w"], wdt)
+    y = pkg.naive_rmsnorm_reference(x, w, float(g["eps"]))
+    assert y.dtype == TORCH_DT[hdt]
+    got = y.numpy() if hdt == "f32" else y.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, g["y_hf"]), path.stem
+    hf = orc.rmsnorm(g["x"], g["w"], float(g["eps"]), xdt=xdt, wdt=wdt, mode="hf")
+    assert np.array_equal(got, hf), path.stem
+
+
+@pytest.mark.parametrize("path", SILU, ids=lambda p: p.stem)
+def test_naive_silu_mul_reference_reproduces_hf(pkg, orc, path):
+    g = _load(path)
+    dt = DT[str(g["dt"])]
+    gate, up = _to_torch(g["gate"], dt), _to_torch(g["up"], dt)
+    y = pkg.naive_silu_mul_reference(gate, up)
+    got = y.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, g["y_hf"]), path.stem
+    assert np.array_equal(got, orc.silu_mul(g["gate"], g["up"], idt=dt, mode="hf")), path.stem
