@@ -71,7 +71,7 @@ def parse_args():
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
-                                      "w8a16-prefill"],
+                                      "w8a16-prefill", "w8a16-prefill-1.5b"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -475,6 +475,7 @@ def rocprof_summary(dirs):
 
     out = []
     pmc = {}  # (kernel fragment, grid, counter) -> per-dispatch values, over all dirs
+    pmc_all = {}  # the same for every kernel, by shortened name
     for d in dirs:
         for f in sorted(glob.glob(os.path.join(d, "*kernel_stats.csv"))):
             # rocprofv3 --stats: every kernel of the run, whatever its grid
@@ -510,6 +511,8 @@ def rocprof_summary(dirs):
             out.append("")
         for f in sorted(glob.glob(os.path.join(d, "*counter_collection.csv"))):
             for r in csv.DictReader(open(f)):
+                name = _short_name(r["Kernel_Name"])
+                pmc_all.setdefault((name, int(r["Grid_Size"]), r["Counter_Name"]), []).append(float(r["Counter_Value"]))
                 frag, known = _match_launch(r["Kernel_Name"], int(r["Grid_Size"]))
                 if known is None:
                     continue
@@ -555,7 +558,29 @@ def rocprof_summary(dirs):
                 label = KNOWN_LAUNCHES[(frag, grid)][0]
                 out.append(f"| {frag} ({label}) | {nd} | " + " | ".join(cells) + " |")
             out.append("")
+    derived = sorted({k[2] for k in pmc_all} - {"FETCH_SIZE", "WRITE_SIZE"})
+    if derived:
+        keys = sorted({(k[0], k[1]) for k in pmc_all if k[2] in derived})
+        out.append("### Counters of every kernel (per dispatch, averaged; grid in threads)\n")
+        out.append("| kernel | grid | dispatches | " + " | ".join(derived) + " |")
+        out.append("|---|---|---|" + "---|" * len(derived))
+        for name, grid in keys:
+            cells = []
+            for c in derived:
+                v = pmc_all.get((name, grid, c))
+                cells.append(f"{sum(v) / len(v):.2f}" if v else "-")
+            nd = max(len(pmc_all.get((name, grid, c), [])) for c in derived)
+            out.append(f"| {name} | {grid} | {nd} | " + " | ".join(cells) + " |")
+        out.append("")
     return "\n".join(out), traffic
+
+
+def _short_name(name: str) -> str:
+    """A kernel's name without its parameter list, namespaces or `void `."""
+    n = name.split("(")[0] if not name.startswith("(") else name
+    for pre in ("void ", "mi355::", "(anonymous namespace)::", "tiled::"):
+        n = n.replace(pre, "")
+    return n[:110]
 
 
 def main():
@@ -798,11 +823,15 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES[1:3], baselines=False)))
-    elif args.only in ("w8a16", "w8a16-decode", "w8a16-prefill"):
+    elif args.only in ("w8a16", "w8a16-decode", "w8a16-prefill", "w8a16-prefill-1.5b"):
         del sets
         torch.cuda.empty_cache()
         if args.only == "w8a16":
             log(json.dumps(bench_w8a16(ctx)))
+        elif args.only == "w8a16-prefill-1.5b":  # the 1.5B gate/up and down projections at 1024 and 4096 rows,
+            # each against fp16 hipBLASLt on the same shape
+            log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] in (1024, 4096)
+                                                    and s[3] == "f16" and s[4] in ("gate/up proj", "down proj")])))
         elif args.only == "w8a16-prefill":  # kernel only, the 1.5B gate/up and down projections at 1024 rows
             log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 1024 and s[2] in (8960, 1536)
                                                     and s[1] in (1536, 8960)][-2:], iters=iters, baselines=False)))
