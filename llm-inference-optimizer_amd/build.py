@@ -131,6 +131,12 @@ VARIANTS = {
     # SiLU-and-mul: every size on one shape, and the load order
     "silu_large_shape_everywhere": ("silu_mul", ["-DMI355_SILU_LARGE_MIN_NUMEL=0"]),
     "silu_load_order1": ("silu_mul", ["-DMI355_SILU_LOAD_ORDER=1"]),
+    # W8A16 tiled GEMM (prefill rows): widen each sub-step's int8 weights right
+    # before its own MFMAs instead of one sub-step ahead
+    "tiled_widen_in_place": ("w8a16", ["-DMI355_TILED_WIDEN_AHEAD=0"]),
+    # W8A16 tiled GEMM: one tile configuration for every prefill launch
+    # (MI355_W8_FORCE in w8a16.hip lists them)
+    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 18)},
     # RMSNorm: keep the row's fp32 widening live between the two passes
     # instead of re-widening the packed row (more VGPRs, fewer conversions),
     # per kernel: the shipped choice is the wave kernel re-widening and the

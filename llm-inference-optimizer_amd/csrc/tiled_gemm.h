@@ -210,6 +210,14 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
+// int8 B: widen each sub-step's weights one sub-step ahead, into a second
+// register set, after the previous sub-step's MFMAs are issued, so the
+// widening VALU work runs beside the MFMAs instead of in front of them
+// (0: widen right before the sub-step's own MFMAs).
+#ifndef MI355_TILED_WIDEN_AHEAD
+#define MI355_TILED_WIDEN_AHEAD 1
+#endif
+
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0>
 __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
@@ -368,6 +376,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     }
   };
 
+  // Widen-ahead (int8 B): wb[s & 1] holds sub-step s's B operands, widened
+  // from the raw int8 pair read (16 bytes: sub-steps 2q, 2q + 1) during the
+  // previous sub-step, behind that sub-step's MFMAs.
+  constexpr bool WA = I8 && MI355_TILED_WIDEN_AHEAD != 0;
+  u32x4 wb[2][NB][FN];
+  auto widen_into = [&](const u32x4 (&raw)[NB][FN], int s, u32x4 (&out)[NB][FN]) {
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        out[bi][j] = (s & 1) ? widen8<T>(raw[bi][j].z, raw[bi][j].w) : widen8<T>(raw[bi][j].x, raw[bi][j].y);
+    }
+  };
+  auto mfma_wide = [&](const u32x4 (&a)[FM], const u32x4 (&bw)[NB][FN]) {
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[bi][i][j] = mfma32<T>(bw[bi][j], a[i], acc[bi][i][j]);
+      }
+    }
+  };
+
   int t0 = 0;
   if constexpr (!RING) {
     // Step pipeline.  Step t computes from registers read out of stage t % S
@@ -381,6 +413,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     // its LDS reads (2-3% over all reads first).
     static_assert(S >= 3, "the step pipeline needs 3 stages");
     Frags fr[2];
+    // raw int8 pair q of a step's fragments as one [NB][FN] set
+    auto raw_pair = [&](const Frags& f, int q, u32x4 (&out)[NB][FN]) {
+#pragma unroll
+      for (int bi = 0; bi < NB; ++bi) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) out[bi][j] = f.b[bi][q][j];
+      }
+    };
+    auto widen_step_sub = [&](const Frags& f, int s, u32x4 (&out)[NB][FN]) {
+      u32x4 raw[NB][FN];
+      raw_pair(f, (s >> 1) & (BQ - 1), raw);
+      widen_into(raw, s, out);
+    };
     static_for([&](auto I) {
       if (decltype(I)::value < nk) issue(I, decltype(I)::value);
     }, std::make_index_sequence<S - 1>{});
@@ -389,6 +434,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     wait_lgkmcnt0();
     lds_barrier();
     read_frags(std::integral_constant<int, 0>{}, fr[0]);
+    if constexpr (WA) widen_step_sub(fr[0], 0, wb[0]);
 
     constexpr int UNROLL = lcm_c(S, 2);  // stage and fragment-set indices known at compile time
     // One step; GUARD = false where every condition is known to hold (all
@@ -409,9 +455,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         __builtin_amdgcn_sched_barrier(0);
-        mfma_sub(fr[pi], s);
+        if constexpr (WA) mfma_wide(fr[pi].a[s], wb[s & 1]);
+        else mfma_sub(fr[pi], s);
         __builtin_amdgcn_sched_barrier(0);
         if (more) read_sub(std::integral_constant<int, (si + 1) % S>{}, fr[pi ^ 1], s);
+        if constexpr (WA) {
+          // the next sub-step's weights: this step's (already in registers)
+          // or, after the last sub-step, the next step's pair 0 (read in
+          // this step's first group)
+          __builtin_amdgcn_sched_barrier(0);
+          if (s < 3) widen_step_sub(fr[pi], s + 1, wb[(s + 1) & 1]);
+          else if (more) widen_step_sub(fr[pi ^ 1], 0, wb[0]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -435,8 +490,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     // stage t % S (now unread) with step t + S and reads sub-step 0 of step
     // t + 1.  A pieces alternate between two register sets by sub-step; an
     // int8 B read (16 bytes: sub-steps 2q and 2q + 1 of k-group h) is made
-    // with sub-step 2q's A read and B sets alternate by pair q, so a read
-    // never lands in a set that a pending MFMA still reads.
+    // with sub-step q's A read into set q, so a read never lands in a set
+    // that a pending MFMA (or widening) still reads.
     struct Sub {
       u32x4 a[2][FM];
       u32x4 b[2][NB][FN];
@@ -451,7 +506,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
         for (int j = 0; j < FN; ++j) {
           const uint8_t* bbase = abase + C::A_BYTES + bi * C::B_BYTES;
           if constexpr (I8) {
-            if ((s & 1) == 0) f.b[(s >> 1) & 1][bi][j] = lds_read16(bbase, swz8(brow0 + 32 * j, 2 * h + (s >> 1)));
+            // raw pair q (sub-steps 2q, 2q + 1) read with sub-step q's A, a
+            // sub-step or more before its first use: set q was last read
+            // two sub-steps earlier
+            if (s < 2) f.b[s][bi][j] = lds_read16(bbase, swz8(brow0 + 32 * j, 2 * h + s));
           } else {
             f.b[s & 1][bi][j] = lds_read16(bbase, swz16(brow0 + 32 * j, 4 * h + s));
           }
@@ -487,6 +545,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     wait_lgkmcnt0();
     lds_barrier();
     read_one(std::integral_constant<int, 0>{}, rf, 0);
+    if constexpr (WA) widen_into(rf.b[0], 0, wb[0]);
     auto rstep = [&](auto I, auto GUARD, int t) {
       constexpr int si = decltype(I)::value % S;
       constexpr bool guard = decltype(GUARD)::value;
@@ -505,7 +564,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
           read_one(std::integral_constant<int, (si + 1) % S>{}, rf, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        mfma_one(rf, s);
+        if constexpr (WA) {
+          mfma_wide(rf.a[s & 1], wb[s & 1]);
+          // the next sub-step's weights, from the raw pair read at sub-step
+          // 2q (the wait for a pair read in this group lands here, behind
+          // the MFMAs just issued)
+          __builtin_amdgcn_sched_barrier(0);
+          if (s < 3) widen_into(rf.b[((s + 1) >> 1) & 1], s + 1, wb[(s + 1) & 1]);
+          else if (more) widen_into(rf.b[0], 0, wb[0]);
+        } else {
+          mfma_one(rf, s);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     };

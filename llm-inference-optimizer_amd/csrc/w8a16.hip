@@ -467,23 +467,57 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
 //   else (n <= 2048) -> 128 x 256, 8 waves, 4 stages.
 // bf16 takes 128 x 128 where fp16 takes 128 x 256: its widening needs more
 // registers, and the 128 x 256 shape would spill.
+// MI355_W8_FORCE = n (> 0): every prefill-size single-matrix launch takes
+// tile configuration n below instead of the launch plan (a measurement
+// switch for variant builds; all configurations compute the same results).
+#ifndef MI355_W8_FORCE
+#define MI355_W8_FORCE 0
+#endif
+
+template <typename T, typename TO>
+int w8_tiled_forced(const W8Params& p, hipStream_t s) {
+  using tiled::EPI_W8;
+  switch (MI355_W8_FORCE) {
+    case 1: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, EPI_W8, 1>(p, s);  // 128 x 64, 4 waves of 64 x 32
+    case 2: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32
+    case 3: return w8_tiled_cfg<T, TO, 4, 2, 2, 4, 2, EPI_W8, 1>(p, s);  // 256 x 256, 8 waves of 64 x 128
+    case 4: return w8_tiled_cfg<T, TO, 2, 2, 2, 4, 2, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 64 x 128
+    case 5: return w8_tiled_cfg<T, TO, 1, 4, 4, 2, 2, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 128 x 64
+    case 6: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 2, EPI_W8, 1>(p, s);  // 128 x 256, 8 waves of 64 x 64
+    case 7: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 2, EPI_W8, 1>(p, s);  // 256 x 128, 4 waves of 128 x 64
+    case 8: return w8_tiled_cfg<T, TO, 1, 4, 2, 4, 2, EPI_W8, 1>(p, s);  // 64 x 512, 4 waves of 64 x 128
+    case 9: return w8_tiled_cfg<T, TO, 2, 2, 2, 4, 3, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves, 3 stages
+    case 10: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 4>(p, s);             // 128 x 256, 8 waves, step pipeline
+    case 11: return w8_tiled_cfg<T, TO, 1, 4, 4, 2, 3, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 128 x 64, 3 stages
+    case 12: return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 2, EPI_W8, 1>(p, s);  // 128 x 128, 4 waves of 64 x 64
+    case 13: return w8_tiled_cfg<T, TO, 2, 2, 1, 2, 2, EPI_W8, 1>(p, s);  // 64 x 128, 4 waves of 32 x 64
+    case 14: return w8_tiled_cfg<T, TO, 1, 4, 2, 1, 2, EPI_W8, 1>(p, s);  // 64 x 128, 4 waves of 64 x 32
+    case 15: return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 3, EPI_W8, 1>(p, s);  // 128 x 128, 4 waves, 3 stages
+    case 16: return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 3, EPI_W8, 1>(p, s);  // 64 x 64, 4 waves, ring, 3 stages
+    default: return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);             // 64 x 64, 4 waves, step pipeline
+  }
+}
+
 template <typename T, typename TO>
 int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
+  if constexpr (MI355_W8_FORCE > 0) return w8_tiled_forced<T, TO>(p, s);
   constexpr bool wide = std::is_same<T, F16>::value;
   // Wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring
   // (2 stages) at the shape whose busiest CU finishes first -- ceil(tiles /
   // CUs) times the cost of one tile of 128 x 64 (4 waves, 40 KiB of LDS, four
   // workgroups per CU), 256 x 128 (8 waves of 128 x 32, two per CU) or
-  // 256 x 256 (8 waves of 64 x 128), measured 1 : 3.33 : 6.4 at the
+  // 256 x 256 (8 waves of 64 x 128), measured about 1 : 3.8 : 6.4 at the
   // Qwen2.5-1.5B and 7B gate/up and down projections (1.5B gate 512 rows
-  // 34.9 -> 26.2 us, 7B down 4096 rows 641 -> 522 us).  Fewer tiles keep the
-  // rule below, whose smaller grids spread better.
+  // 34.9 -> 26.2 us, 7B down 4096 rows 641 -> 522 us; the 3.8 from a later
+  // sweep, where 128 x 64 tiles took 158-160 us at 1.5B gate/up 4096 rows
+  // against 165-168 us for 256 x 128).  Fewer tiles keep the rule below,
+  // whose smaller grids spread better.
   if (p.n > 2048) {
     const auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
     const int64_t t_small = cdiv(p.rows, 128) * cdiv(p.n, 64);
     if (t_small >= 2 * static_cast<int64_t>(cus)) {
       const double c_small = static_cast<double>(cdiv(t_small, cus));
-      const double c_mid = 3.33 * static_cast<double>(cdiv(cdiv(p.rows, 256) * cdiv(p.n, 128), cus));
+      const double c_mid = 3.8 * static_cast<double>(cdiv(cdiv(p.rows, 256) * cdiv(p.n, 128), cus));
       const double c_big = 6.4 * static_cast<double>(cdiv(cdiv(p.rows, 256) * cdiv(p.n, 256), cus));
       if (c_small <= c_mid && c_small <= c_big) return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, tiled::EPI_W8, 1>(p, s);
       if (c_mid <= c_big) return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, tiled::EPI_W8, 1>(p, s);
