@@ -144,6 +144,13 @@ VARIANTS = {
     "rms_wave_keep_f32": ("rmsnorm", ["-DMI355_RMS_KEEP_F32_WAVE=1"]),
     "rms_block_rewiden": ("rmsnorm", ["-DMI355_RMS_KEEP_F32_BLOCK=0"]),
 }
+# Built with every default build (``__graft_entry__.build``), so the GPU tests
+# of tests/test_launch_variants.py run on them: one variant per distinct code
+# path of the kernels (several rows per wave and per workgroup, a row over
+# one wave, the LDS weight, a persistent grid, another SiLU-and-mul chunk,
+# the W8A16 widening order).
+CORE_VARIANTS = ("rms_wave_rows2", "rms_block_rows2", "rms_one_wave", "rms_weight_lds", "rms_persistent8",
+                 "rms_block_persistent4", "silu_unroll1", "silu_large_block512_unroll2", "tiled_widen_in_place")
 VARIANT_DIR = PKG_DIR / "_variants"
 # Variants that spread a row over waves differently from the default build:
 # the fp32 sum of squares then adds in another order, so an output may differ
@@ -155,6 +162,13 @@ REORDERING_VARIANTS = frozenset({"rms_one_wave", "rms_one_wave_rows2"})
 
 def variant_path(name: str) -> Path:
     return VARIANT_DIR / f"libmi355_fused_{name}.so"
+
+
+def build_variants(names=CORE_VARIANTS) -> list[Path]:
+    """Builds the named variants in parallel (the default objects must be
+    current: call after build())."""
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(names))) as ex:
+        return list(ex.map(build_variant, names))
 
 
 def build_variant(name: str) -> Path:

@@ -122,3 +122,37 @@ def test_silu_mul_variant_is_bitwise_the_default(name, cuda):
                 torch.cuda.synchronize()
                 outs.append(o)
             assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, numel, dt)
+
+
+W8_VARIANTS = [n for n, (unit, _) in B.VARIANTS.items() if unit == "w8a16"]
+# prefill-size W8A16 shapes (rows, k, n, dtype) through the tiled GEMM: the
+# 1.5B gate/up and down projections, ragged rows / n, a k tail, bf16
+W8_SHAPES = [(1024, 1536, 8960, torch.float16), (300, 8960, 1536, torch.float16),
+             (1030, 272, 6600, torch.float16), (520, 1536, 4736, torch.bfloat16)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", W8_VARIANTS)
+def test_w8a16_variant_is_bitwise_the_default(name, cuda):
+    """W8A16 variants (the widening order, forced tile configurations): every
+    tile shape and pipeline adds the k products in the same order, so the
+    outputs equal the default library's bit for bit."""
+    lib = _variant(name)
+    ref_lib = L.load()
+    for i, (rows, k, n, dt) in enumerate(W8_SHAPES):
+        print(f"variant {name}: w8a16 rows={rows} k={k} n={n} {dt}", flush=True)
+        x = torch.randn(rows, k, generator=_gen(300 + i)).to(dt).to(cuda)
+        q = torch.randint(-127, 128, (n, k), generator=_gen(400 + i), dtype=torch.int8).to(cuda)
+        scale = (torch.rand(n, generator=_gen(500 + i)) * 1e-3 + 1e-4).to(cuda)
+        bias = torch.randn(n, generator=_gen(600 + i)).to(dt).to(cuda)
+        c = L.DTYPE_CODE
+        outs = []
+        for lb in (ref_lib, lib):
+            o = torch.full((rows, n), float("nan"), dtype=dt, device=cuda)
+            st = lb.mi355_w8a16_linear_fwd(x.data_ptr(), q.data_ptr(), scale.data_ptr(), bias.data_ptr(),
+                                           o.data_ptr(), rows, k, n, k, k, n, c[dt], L.F32, c[dt], c[dt],
+                                           abi_stream())
+            assert st == 0, lb.mi355_last_error().decode()
+            torch.cuda.synchronize()
+            outs.append(o)
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, rows, k, n, dt)
