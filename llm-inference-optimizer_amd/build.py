@@ -134,6 +134,11 @@ VARIANTS = {
     # W8A16 tiled GEMM (prefill rows): widen each sub-step's int8 weights right
     # before its own MFMAs instead of one sub-step ahead
     "tiled_widen_in_place": ("w8a16", ["-DMI355_TILED_WIDEN_AHEAD=0"]),
+    # W8A16 tiled GEMM: an L2 prefetch wave per workgroup, 2 / 4 / 8 K steps
+    # past the LDS ring
+    "tiled_prefetch2": ("w8a16", ["-DMI355_TILED_PREFETCH=2"]),
+    "tiled_prefetch4": ("w8a16", ["-DMI355_TILED_PREFETCH=4"]),
+    "tiled_prefetch8": ("w8a16", ["-DMI355_TILED_PREFETCH=8"]),
     # W8A16 tiled GEMM: one tile configuration for every prefill launch
     # (MI355_W8_FORCE in w8a16.hip lists them)
     **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 18)},

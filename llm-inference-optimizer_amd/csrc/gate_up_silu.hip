@@ -254,7 +254,7 @@ int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_16, TO, WGM, WGN, FM, FN,
                                                                                       tiled::EPI_SILU, S, RING>),
-                                    dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
+                                    dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::BLOCK), args, 0, s),
                     "gate_up_silu tiled launch");
 }
 

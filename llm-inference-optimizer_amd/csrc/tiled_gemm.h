@@ -83,6 +83,15 @@ namespace tiled {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 enum { EPI_W8 = 0, EPI_SILU = 1, EPI_SILU_W8 = 2, EPI_LINEAR = 3 };
+
+// MI355_TILED_PREFETCH = P > 0: one more wave per workgroup streams the
+// workgroup's operand lines of the K step P steps past the LDS ring's
+// furthest DMA into L2 (DMA loads into a 256-byte LDS sink, so no VGPRs and
+// its own vmcnt: the MFMA waves never wait on it), in step with the ring
+// through the same barriers.  0 = no prefetch wave.
+#ifndef MI355_TILED_PREFETCH
+#define MI355_TILED_PREFETCH 0
+#endif
 enum { B_16 = 0, B_I8 = 1 };
 
 template <typename T> __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
@@ -131,6 +140,8 @@ struct Cfg {
   // LDS and widened after each LDS read).
   static constexpr bool I8 = BK == B_I8;
   static constexpr int NW = WGM * WGN, NT = 64 * NW;
+  // threads per workgroup: the MFMA waves, plus the L2 prefetch wave when on
+  static constexpr int BLOCK = NT + (MI355_TILED_PREFETCH > 0 ? 64 : 0);
   static constexpr int BM = 32 * FM * WGM, BN = 32 * FN * WGN;
   static constexpr int NB = (EPI == EPI_W8 || EPI == EPI_LINEAR) ? 1 : 2;  // B matrices
   static constexpr int A_BYTES = BM * 128;             // 64 columns of 16-bit x per row
@@ -190,6 +201,14 @@ __device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t soff, ui
   else
     asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
 }
+// 4 bytes per lane into LDS (buffer_load_dword ... lds): the prefetch wave's
+// loads, whose data lands in a sink nobody reads.
+__device__ __forceinline__ void dma4(rsrc_t r, uint32_t voff, uint32_t lds_addr) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
+  const uint32_t soff = 0;
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+}
+
 // LDS byte address of stage I (the cast of the LDS variable itself folds to a constant).
 template <int I, int SZ> __device__ __forceinline__ uint32_t stage_addr() {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)stage_ptr<I, SZ>()));
@@ -219,7 +238,7 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc
 #endif
 
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0>
-__global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
+__global__ __launch_bounds__(64 * WGM * WGN + (MI355_TILED_PREFETCH > 0 ? 64 : 0)) void tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
   constexpr bool I8 = C::I8;
   using TB = typename T::bits;
@@ -252,6 +271,48 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
     rb[1] = make_rsrc(static_cast<const uint8_t*>(p.b1) + static_cast<int64_t>(n0) * p.bs * EB,
                       static_cast<uint32_t>(((nrows_b - 1) * p.bs + p.k) * EB));
 
+  const int nk = (p.k + 63) >> 6;
+  if constexpr (MI355_TILED_PREFETCH > 0) {
+    if (wave == NW) {
+      // The prefetch wave: before the ring's first barrier, steps S .. S + P - 1;
+      // after barrier t (when the MFMA waves start refilling with step t + S
+      // or so), step t + S + P - 1.  Two dwords per 128-byte line (each half
+      // a 64-byte sector) of every x row and weight row of the tile; rows and
+      // columns past the matrix fall outside the descriptors (no traffic).
+      __shared__ uint32_t sink[64];
+      const uint32_t sink_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)sink));
+      auto pf = [&](int u) {
+        if (u >= nk) return;
+#pragma unroll
+        for (int r = lane; r < BM; r += 64) {
+          const uint32_t off = static_cast<uint32_t>((r * p.xs + u * 64) * sizeof(TB));
+          dma4(rx, off, sink_addr);
+          dma4(rx, off + 64, sink_addr);
+        }
+        // int8 rows hold 64 bytes per step: a new 128-byte line every other step
+        if (!I8 || (u & 1) == 0) {
+#pragma unroll
+          for (int bi = 0; bi < NB; ++bi) {
+#pragma unroll
+            for (int r = lane; r < BN; r += 64) {
+              const uint32_t off = static_cast<uint32_t>((r * p.bs + u * 64) * EB);
+              dma4(rb[bi], off, sink_addr);
+              dma4(rb[bi], off + 64, sink_addr);
+            }
+          }
+        }
+      };
+      for (int u = S; u < S + MI355_TILED_PREFETCH; ++u) pf(u);
+      lds_barrier();
+      for (int t = 1; t < nk; ++t) {
+        pf(t + S + MI355_TILED_PREFETCH - 1);
+        lds_barrier();  // one per K step, as the MFMA waves
+      }
+      wait_vmcnt<0>();  // its LDS writes land before the workgroup ends
+      return;
+    }
+  }
+
   // DMA lane maps (16-bit tiles).  Instruction j of wave w fills the 1 KiB
   // at tile offset 1024 (NW j + w): lane l writes physical chunk l % 8 of row
   // 8 (NW j + w) + l / 8, so it loads the logical chunk the swizzle keeps
@@ -281,7 +342,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void tiled_gemm(const Params p) {
       b_col[j] = 8 * c;
     }
   }
-  const int nk = (p.k + 63) >> 6;
   const int kfull = p.k >> 6;  // steps whose 64 columns are all inside k
 
   // Issues the DMA of K step kt into stage I.  Columns at or past k read 0.

@@ -452,7 +452,7 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
                                                                                       EPI, S, RING>),
-                                    dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::NT), args, 0, s),
+                                    dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::BLOCK), args, 0, s),
                     "w8a16 tiled launch");
 }
 
