@@ -94,6 +94,10 @@ def parse_args():
                    choices=["c1-rms", "c1-add-rms", "c4-rms", "c2-silu", "c4-silu", "silu-4096x8960",
                             "silu-8192x8960"])
     p.add_argument("--sweep-rounds", type=int, default=3)
+    p.add_argument("--w8-skinny-sweep", nargs="*", metavar="SHAPE", default=None,
+                   help="launch-shape sweep of the W8A16 decode (skinny) kernel on the sweep variant builds "
+                        "(build.py --variant w8_skinny_sweep w8_skinny_sweep_pipe): G x waves x U x split of K "
+                        "over workgroups, per decode shape (default: all of W8_SKINNY_SWEEP_SHAPES)")
     p.add_argument("--full-json", default=None, metavar="PATH",
                    help="also write the full result (every leg) to PATH; stdout carries the compact line")
     p.add_argument("--rocprof-summary", nargs="+", metavar="DIR", default=None,
@@ -612,6 +616,9 @@ def main():
     if args.sweep:
         run_sweep(ctx, args)
         return
+    if args.w8_skinny_sweep is not None:
+        w8_skinny_sweep(ctx, args.w8_skinny_sweep)
+        return
 
     F16 = torch.float16
     M, N, I = 2048, 1536, 8960
@@ -942,6 +949,104 @@ def run_sweep(ctx, args):
     print(json.dumps(out), flush=True)
     if bad:
         log(f"sweep: outputs differ from the default library: {bad}")
+        sys.exit(1)
+
+
+# (rows, k, n, dtype, label): the 1.5B down, gate/up and q/o projections and
+# the 7B down and gate/up projections at decode rows.
+W8_SKINNY_SWEEP_SHAPES = [
+    (8, 8960, 1536, "f16", "down1.5b"), (1, 8960, 1536, "f16", "down1.5b"),
+    (8, 1536, 8960, "f16", "gateup1.5b"), (1, 1536, 8960, "f16", "gateup1.5b"),
+    (8, 1536, 1536, "f16", "o1.5b"),
+    (8, 18944, 3584, "bf16", "down7b"), (8, 3584, 18944, "bf16", "gateup7b"),
+]
+
+
+def w8_skinny_sweep(ctx, only):
+    """The W8A16 decode kernel (w8a16_skinny) under forced launch shapes, on
+    the sweep builds: weight-row groups per workgroup G, waves per workgroup
+    (the split of K inside a workgroup), blocks in flight per wave U, and the
+    split of K over KS workgroups (partial sums meeting through device memory,
+    the last workgroup to arrive adding them in order), with the shipped main
+    loop (w8_skinny_sweep) and with U blocks kept in flight throughout
+    (w8_skinny_sweep_pipe, KS = 1).  Cold weights (rotating sets), hipGraph
+    timing; every shape's output is checked against the default library's
+    (fp32 order may differ: within 2e-3 of the largest output) and KS > 1
+    results for being the same bits on three calls.  Prints one JSON line."""
+    torch = ctx.torch
+    libs = {}
+    for name in ("w8_skinny_sweep", "w8_skinny_sweep_pipe"):
+        path = variant_lib(name)
+        if not path.exists():
+            raise SystemExit(f"{path} missing: python llm-inference-optimizer_amd/build.py --variant {name}")
+        lib = ctx.L.load_variant(path)
+        lib.mi355_w8_sweep_config.argtypes = [ctypes.c_int] * 4
+        lib.mi355_w8_sweep_config.restype = None
+        lib.mi355_w8_sweep_ks.argtypes = [ctypes.c_int]
+        lib.mi355_w8_sweep_ks.restype = ctypes.c_int
+        if lib.mi355_w8_sweep_ks(0) != 0:
+            raise SystemExit(f"{name}: the split-K scratch is not addressable")
+        libs[name] = lib
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
+    grid = [("w8_skinny_sweep", g, 1, sp, u) for g in (1, 2, 4, 8) for sp in (2, 3, 4, 6, 8, 12, 16) for u in (1, 2, 4)]
+    grid += [("w8_skinny_sweep", g, ks, sp, 1) for g in (1, 2, 4, 8) for ks in (2, 3, 4, 6, 8) for sp in (4, 8, 16)]
+    grid += [("w8_skinny_sweep_pipe", g, 1, sp, u) for g in (1, 2, 4) for sp in (2, 3, 4, 6, 8, 12, 16) for u in (2, 4)]
+    out = {"shapes": {}}
+    bad = []
+    for M, K, N, dn, lab in W8_SKINNY_SWEEP_SHAPES:
+        if only and lab not in only:
+            continue
+        dt = dts[dn]
+        sets = min(64, n_sets(N * K))
+        x = rand(ctx, (M, K), 1700 + M, dt)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(5)
+        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets)]
+        sc = [(torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
+        outs = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(4)]
+        ref = torch.empty((M, N), dtype=dt, device=ctx.dev)
+        ctx.w8a16_call(x, qs[0], sc[0], ref)()
+        ref_max = ref.float().abs().max().item()
+        base = [ctx.w8a16_call(x, q, s, outs[i % 4]) for i, (q, s) in enumerate(zip(qs, sc))]
+        spin_up(ctx, base)
+        t_default = time_graph(ctx, base, max(2 * sets, 64))
+        rows = []
+        for lname, G, KS, split, U in grid:
+            lib = libs[lname]
+            c = ctx.with_lib(lib)
+            lib.mi355_w8_sweep_config(G, U, split, 1)
+            lib.mi355_w8_sweep_ks(KS)
+            o = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(3)]
+            for oi in o:
+                c.w8a16_call(x, qs[0], sc[0], oi)()
+            torch.cuda.synchronize()
+            same_bits = all(torch.equal(o[0], oi) for oi in o[1:])
+            err = (o[0].float() - ref.float()).abs().max().item() / max(ref_max, 1e-6)
+            us = time_graph(c, [c.w8a16_call(x, q, s, outs[i % 4]) for i, (q, s) in enumerate(zip(qs, sc))],
+                            max(2 * sets, 64))
+            r = {"lib": lname, "G": G, "KS": KS, "waves": split, "U": U, "us": round(us, 3)}
+            rows.append(r)
+            if err > 2e-3 or not same_bits:
+                bad.append(dict(r, shape=f"{lab} M={M}", err=err, same_bits=same_bits))
+        for lib in libs.values():
+            lib.mi355_w8_sweep_config(0, 0, 0, 0)
+            lib.mi355_w8_sweep_ks(0)
+        best = min(rows, key=lambda r: r["us"])
+        by_ks = {ks: min(r["us"] for r in rows if r["KS"] == ks and r["lib"] == "w8_skinny_sweep")
+                 for ks in (1, 2, 3, 4, 6, 8)}
+        pipe_best = min(r["us"] for r in rows if r["lib"] == "w8_skinny_sweep_pipe")
+        key = f"{lab}_M{M}"
+        out["shapes"][key] = {"rows": M, "k": K, "n": N, "dtype": dn, "default_us": round(t_default, 3),
+                              "best": best, "best_us_by_KS": by_ks, "best_us_pipelined_loop": pipe_best,
+                              "configs": rows}
+        log(f"  w8 skinny sweep {key}: default {t_default:.2f} us; best {best}; by KS {by_ks}; "
+            f"pipelined loop best {pipe_best:.2f} us")
+        del qs, sc, base
+        torch.cuda.empty_cache()
+    out["mismatches"] = bad
+    print(json.dumps(out), flush=True)
+    if bad:
+        log(f"w8 skinny sweep: results off or not reproducible: {bad[:5]}")
         sys.exit(1)
 
 

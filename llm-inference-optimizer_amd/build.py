@@ -139,6 +139,12 @@ VARIANTS = {
     "tiled_prefetch2": ("w8a16", ["-DMI355_TILED_PREFETCH=2"]),
     "tiled_prefetch4": ("w8a16", ["-DMI355_TILED_PREFETCH=4"]),
     "tiled_prefetch8": ("w8a16", ["-DMI355_TILED_PREFETCH=8"]),
+    # W8A16 decode (skinny) kernels: the launch-shape sweep build, whose
+    # mi355_w8_sweep_config / mi355_w8_sweep_ks force G x waves x U and a
+    # split of K over workgroups (bench.py --w8-skinny-sweep), with the
+    # main loop as shipped and with U blocks kept in flight throughout
+    "w8_skinny_sweep": ("w8a16", ["-DMI355_W8_SWEEP"]),
+    "w8_skinny_sweep_pipe": ("w8a16", ["-DMI355_W8_SWEEP", "-DMI355_W8_PIPE=1"]),
     # W8A16 tiled GEMM: one tile configuration for every prefill launch
     # (MI355_W8_FORCE in w8a16.hip lists them)
     **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 18)},

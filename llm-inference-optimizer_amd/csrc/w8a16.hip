@@ -56,6 +56,18 @@ namespace mi355 {
 namespace {
 
 constexpr int kMaxSplit = 16;  // waves per skinny workgroup
+#ifdef MI355_W8_SWEEP
+// s_waitcnt operand for vmcnt(0) with the other counters left alone (gfx9
+// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int kWaitVmcnt0 = 0x0F70;
+#endif
+
+// MI355_W8_PIPE = 1: the skinny kernels keep U blocks in flight per wave at
+// all times (a slot is refilled as soon as it is consumed) instead of issuing
+// U blocks, waiting for all of them, then consuming them.
+#ifndef MI355_W8_PIPE
+#define MI355_W8_PIPE 0
+#endif
 
 // 16 int8 weights (one 16-byte load) -> the B operands of two MFMAs.
 template <typename T>
@@ -77,6 +89,10 @@ struct W8Params {
   int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
   const void* q2;      // dual kernels: [n, qs] int8 up weights
   const void* scale2;  // dual kernels: [n] of sdt
+  // Sweep builds only: the skinny kernels with K split over workgroups
+  // (gridDim.z > 1) as well.
+  float* part;     // [units][gridDim.z][NQ][64 G MT] fp32 partial sums
+  unsigned* cnt;   // [units] arrival counters, zero between calls
 };
 
 // The epilogue shared by all kernels: scale once, then the bias, one rounding.
@@ -146,43 +162,67 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
     }
   }
 
-  const int nblk = (p.k + 127) >> 7;
-  const int s_end = (nblk * (wave + 1)) / nwave;
-  for (int s = (nblk * wave) / nwave; s < s_end; s += U) {
-    u32x4 wq[U][NQ][G], xa[U][MT][2];
+  // This workgroup's share of the 128-column blocks (all of them unless K is
+  // split over workgroups too), split again over its waves.
+  const int nblk_all = (p.k + 127) >> 7;
+  const int z0 = (nblk_all * static_cast<int>(blockIdx.z)) / static_cast<int>(gridDim.z);
+  const int nblk = (nblk_all * (static_cast<int>(blockIdx.z) + 1)) / static_cast<int>(gridDim.z) - z0;
+  const int s_begin = z0 + (nblk * wave) / nwave;
+  const int s_end = z0 + (nblk * (wave + 1)) / nwave;
+  // Block s into slot (wq, xa); blocks past the wave's range or past k load
+  // zeros without touching memory.
+  auto issue = [&](u32x4 (&wq)[NQ][G], u32x4 (&xa)[MT][2], int s) {
+    const bool live = s < s_end && 128 * s + col < p.k;
 #pragma unroll
-    for (int j = 0; j < U; ++j) {
-      const bool live = s + j < s_end && 128 * (s + j) + col < p.k;
+    for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) wq[j][qi][g] = buf_load16(rq[qi], live ? qoff[g] + 128u * (s + j) : kOob);
-      }
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const uint32_t o = xoff[t] + 256u * (s + j);
-        xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
-        xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
-      }
+      for (int g = 0; g < G; ++g) wq[qi][g] = buf_load16(rq[qi], live ? qoff[g] + 128u * s : kOob);
     }
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < U; ++j) {
+    for (int t = 0; t < MT; ++t) {
+      const uint32_t o = xoff[t] + 256u * s;
+      xa[t][0] = buf_load16_cached(rx, live ? o : kOob);
+      xa[t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
+    }
+  };
+  auto consume = [&](const u32x4 (&wq)[NQ][G], const u32x4 (&xa)[MT][2]) {
 #pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
+    for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          u32x4 b0, b1;
-          widen_i8x16<T>(wq[j][qi][g], b0, b1);
+      for (int g = 0; g < G; ++g) {
+        u32x4 b0, b1;
+        widen_i8x16<T>(wq[qi][g], b0, b1);
 #pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            acc[qi][g][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][g][t]);
-            acc[qi][g][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][g][t]);
-          }
+        for (int t = 0; t < MT; ++t) {
+          acc[qi][g][t] = mfma16<T>(xa[t][0], b0, acc[qi][g][t]);
+          acc[qi][g][t] = mfma16<T>(xa[t][1], b1, acc[qi][g][t]);
         }
       }
     }
+  };
+  u32x4 wq[U][NQ][G], xa[U][MT][2];
+#if MI355_W8_PIPE
+  // U slots in flight at all times: each slot is refilled with the block U
+  // ahead as soon as its own block has been consumed.
+#pragma unroll
+  for (int j = 0; j < U; ++j) issue(wq[j], xa[j], s_begin + j);
+  for (int s = s_begin; s < s_end; s += U) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      consume(wq[j], xa[j]);
+      issue(wq[j], xa[j], s + U + j);
+    }
   }
+#else
+  // U blocks issued together, then consumed together.
+  for (int s = s_begin; s < s_end; s += U) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) issue(wq[j], xa[j], s + j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < U; ++j) consume(wq[j], xa[j]);
+  }
+#endif
 
 #pragma unroll
   for (int qi = 0; qi < NQ; ++qi) {
@@ -200,6 +240,64 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
 
   // Output (x row 8t + a, weight row 8g + b) = D[a][b] + D[a + 8][b + 8]:
   // register a % 4 of lanes 16 * (a / 4) + b and 16 * (a / 4) + 40 + b.
+#ifdef MI355_W8_SWEEP
+  if (gridDim.z > 1) {
+    // Sweep builds only (no faster than the shipped shapes at any decode
+    // shape but one): K split over workgroups too.  Each workgroup stores
+    // its partial sums; the last to arrive adds all of them in workgroup
+    // order (the same bits whatever the arrival order), applies the epilogue
+    // and re-arms the counter.
+    constexpr int NO = 64 * G * MT;
+    const unsigned unit = blockIdx.y * gridDim.x + blockIdx.x;
+    float* const part = p.part + static_cast<size_t>(unit) * gridDim.z * NQ * NO;
+    for (int o = threadIdx.x; o < NO; o += blockDim.x) {
+      const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
+      const int g = gt % G, t = gt / G;
+      const int l0 = 16 * (a >> 2) + b, j = a & 3;
+#pragma unroll
+      for (int qi = 0; qi < NQ; ++qi) {
+        float sum = 0.f;
+        for (int w = 0; w < nwave; ++w) {
+          const float* r = red + ((((w * NQ + qi) * G + g) * MT + t) * 4 + j) * 64;
+          sum += r[l0] + r[l0 + 40];
+        }
+        __hip_atomic_store(part + (static_cast<size_t>(blockIdx.z) * NQ + qi) * NO + o, sum, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // The partial sums are device-scope stores (written through to where
+    // every XCD reads them) and each wave waits for their acknowledgement
+    // before the barrier, so they are in place before the arrival count;
+    // the last workgroup reads them with device-scope loads.  (An agent-scope
+    // fence would do the same by writing back and invalidating the whole L2
+    // of the XCD, which costs microseconds per wave.)
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __shared__ unsigned last;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      last = __hip_atomic_fetch_add(p.cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.z - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int o = threadIdx.x; o < NO; o += blockDim.x) {
+      const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
+      const int g = gt % G, t = gt / G;
+      const int m = 8 * t + a, n = 8 * g + b;
+      if (m >= nrows_x || n >= nrows_w) continue;
+      float sum[NQ];
+#pragma unroll
+      for (int qi = 0; qi < NQ; ++qi) {
+        sum[qi] = 0.f;
+        for (unsigned z = 0; z < gridDim.z; ++z)
+          sum[qi] += __hip_atomic_load(part + (static_cast<size_t>(z) * NQ + qi) * NO + o, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if constexpr (DUAL) w8_store_silu<TO>(p, m0 + m, n0 + n, sum[0], sum[NQ - 1]);
+      else w8_store<TO>(p, m0 + m, n0 + n, sum[0]);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(p.cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+#endif
   for (int o = threadIdx.x; o < 64 * G * MT; o += blockDim.x) {
     const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
     const int g = gt % G, t = gt / G;
@@ -308,13 +406,21 @@ int launch_w8(K kernel, dim3 grid, dim3 block, size_t lds, const W8Params& p, hi
 
 #ifdef MI355_W8_SWEEP
 // Sweep builds only: force the skinny launch shape (0 = automatic).
-int g_force_g = 0, g_force_u = 0, g_force_split = 0, g_force_path = 0;
+int g_force_g = 0, g_force_u = 0, g_force_split = 0, g_force_path = 0, g_force_ks = 0;
+__device__ __align__(256) unsigned char g_sweep_scratch[(8 << 20) + (64 << 10)];
+void* g_sweep_scratch_ptr = nullptr;
 }  // namespace
 extern "C" __attribute__((visibility("default"))) void mi355_w8_sweep_config(int g, int u, int split, int path) {
   g_force_g = g;
   g_force_u = u;
   g_force_split = split;
   g_force_path = path;
+}
+extern "C" __attribute__((visibility("default"))) int mi355_w8_sweep_ks(int ks) {
+  g_force_ks = ks;
+  if (!g_sweep_scratch_ptr && hipGetSymbolAddress(&g_sweep_scratch_ptr, HIP_SYMBOL(g_sweep_scratch)) != hipSuccess)
+    return -1;
+  return 0;
 }
 namespace {
 #endif
@@ -367,19 +473,35 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
     split = (nblk + bpw - 1) / bpw;  // even blocks per wave
   }
   if (u == 0) u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
-  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
+  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
+#ifdef MI355_W8_SWEEP
+  W8Params ps = p;
+  if (g_force_ks > 1 && g_sweep_scratch_ptr) {
+    const size_t part_bytes = static_cast<size_t>(units) * g_force_ks * NQ * 64 * G * MT * sizeof(float);
+    if (part_bytes <= (8u << 20) && units <= 16384) {
+      grid.z = static_cast<unsigned>(g_force_ks);
+      ps.part = static_cast<float*>(g_sweep_scratch_ptr);
+      ps.cnt = reinterpret_cast<unsigned*>(static_cast<unsigned char*>(g_sweep_scratch_ptr) + (8 << 20));
+    }
+  }
+  const W8Params& pl = ps;
+#else
+  const W8Params& pl = p;
+#endif
   const dim3 block(64 * split);
   const size_t lds = static_cast<size_t>(split) * NQ * G * MT * 4 * 64 * sizeof(float);
   // register budget (128 VGPRs at 1024 threads): U * (4 NQ G + 8 MT) operand
   // dwords + 4 NQ G MT accumulators <= 100
   constexpr int umax = (100 - 4 * NQ * G * MT) / (4 * NQ * G + 8 * MT);
 #ifdef MI355_W8_SWEEP
+  if (u >= 8 && umax >= 8)
+    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 8 ? 8 : 1), DUAL>, grid, block, lds, pl, s);
   if (u >= 4 && umax >= 4)
-    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 4 ? 4 : 1), DUAL>, grid, block, lds, p, s);
+    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 4 ? 4 : 1), DUAL>, grid, block, lds, pl, s);
 #endif
   if (u >= 2 && umax >= 2)
-    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1), DUAL>, grid, block, lds, p, s);
-  return launch_w8(w8a16_skinny<T, TO, MT, G, 1, DUAL>, grid, block, lds, p, s);
+    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1), DUAL>, grid, block, lds, pl, s);
+  return launch_w8(w8a16_skinny<T, TO, MT, G, 1, DUAL>, grid, block, lds, pl, s);
 }
 
 template <typename T, typename TO, int MT, bool DUAL>
@@ -402,13 +524,20 @@ int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
   // a single row, else at most 2 (a sweep of G x split x U over Qwen2.5-1.5B
   // and -7B decode rows: 8 rows 9.2 us with 2 groups vs 12.5 us with 1), and
   // 1 for MT >= 3 so its 2 G MT accumulator tiles fit the register budget.
+#ifdef MI355_W8_SWEEP
+  constexpr int gmax = !DUAL ? (MT == 1 ? 8 : 4) : (MT >= 3 ? 1 : (MT == 1 ? 4 : 2));
+#else
   constexpr int gmax = !DUAL ? 4 : (MT >= 3 ? 1 : 2);
+#endif
   if (DUAL) g = p.rows <= 1 ? 1 : (g > 2 ? 2 : g);
 #ifdef MI355_W8_SWEEP
   if (g_force_g > 0) g = g_force_g;
 #endif
+  if constexpr (gmax >= 8) {
+    if (g >= 8) return w8_skinny_g<T, TO, MT, (gmax >= 8 ? 8 : 1), DUAL>(p, s, cus);
+  }
   if constexpr (gmax >= 4) {
-    if (g >= 4) return w8_skinny_g<T, TO, MT, 4, DUAL>(p, s, cus);
+    if (g >= 4) return w8_skinny_g<T, TO, MT, (gmax >= 4 ? 4 : 1), DUAL>(p, s, cus);
   }
   if constexpr (gmax >= 2) {
     if (g >= 2) return w8_skinny_g<T, TO, MT, 2, DUAL>(p, s, cus);

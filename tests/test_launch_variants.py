@@ -128,15 +128,19 @@ W8_VARIANTS = [n for n, (unit, _) in B.VARIANTS.items() if unit == "w8a16"]
 # prefill-size W8A16 shapes (rows, k, n, dtype) through the tiled GEMM: the
 # 1.5B gate/up and down projections, ragged rows / n, a k tail, bf16
 W8_SHAPES = [(1024, 1536, 8960, torch.float16), (300, 8960, 1536, torch.float16),
-             (1030, 272, 6600, torch.float16), (520, 1536, 4736, torch.bfloat16)]
+             (1030, 272, 6600, torch.float16), (520, 1536, 4736, torch.bfloat16),
+             # decode rows through the skinny kernel (the sweep builds' own code)
+             (8, 8960, 1536, torch.float16), (1, 1536, 8960, torch.float16), (5, 3584, 1000, torch.bfloat16),
+             (24, 1536, 2048, torch.float16)]
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", W8_VARIANTS)
 def test_w8a16_variant_is_bitwise_the_default(name, cuda):
-    """W8A16 variants (the widening order, forced tile configurations): every
-    tile shape and pipeline adds the k products in the same order, so the
-    outputs equal the default library's bit for bit."""
+    """W8A16 variants (the widening order, forced tile configurations, the
+    skinny kernel's sweep builds left on their automatic shapes): every tile
+    shape and pipeline adds the k products in the same order, so the outputs
+    equal the default library's bit for bit."""
     lib = _variant(name)
     ref_lib = L.load()
     for i, (rows, k, n, dt) in enumerate(W8_SHAPES):
@@ -156,3 +160,56 @@ def test_w8a16_variant_is_bitwise_the_default(name, cuda):
             torch.cuda.synchronize()
             outs.append(o)
         assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, rows, k, n, dt)
+
+
+# Forced skinny shapes of the sweep build: (G, waves, U, KS).  KS > 1 splits K
+# over workgroups (partial sums through device memory, added by the last
+# workgroup to arrive in workgroup order).
+W8_FORCED = [(1, 8, 2, 1), (4, 4, 1, 3), (8, 8, 1, 4), (2, 16, 1, 2), (1, 4, 4, 6)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("forced", W8_FORCED)
+def test_w8_skinny_sweep_forced_shapes(forced, cuda):
+    """The sweep build under forced launch shapes (as bench.py
+    --w8-skinny-sweep drives it) gives the default library's result up to the
+    fp32 order of its sums, and the same bits on every call, also when K is
+    split over workgroups.  Every product is exact, so two orders differ by
+    fp32 rounding of the running sums: about sqrt(k) * 2^-24 of the partial
+    sums' size (~1e-6 of the largest output here), then one output rounding;
+    a split's partial sums lost or counted twice would be off by O(1) of the
+    output."""
+    import ctypes
+    lib = _variant("w8_skinny_sweep")
+    lib.mi355_w8_sweep_config.argtypes = [ctypes.c_int] * 4
+    lib.mi355_w8_sweep_config.restype = None
+    lib.mi355_w8_sweep_ks.argtypes = [ctypes.c_int]
+    lib.mi355_w8_sweep_ks.restype = ctypes.c_int
+    ref_lib = L.load()
+    G, waves, U, KS = forced
+    c = L.DTYPE_CODE
+    try:
+        for i, (rows, k, n, dt) in enumerate([(8, 8960, 1536, torch.float16), (3, 3584, 1000, torch.bfloat16)]):
+            print(f"w8 skinny forced {forced}: rows={rows} k={k} n={n} {dt}", flush=True)
+            x = torch.randn(rows, k, generator=_gen(700 + i)).to(dt).to(cuda)
+            q = torch.randint(-127, 128, (n, k), generator=_gen(800 + i), dtype=torch.int8).to(cuda)
+            scale = (torch.rand(n, generator=_gen(900 + i)) * 1e-3 + 1e-4).to(cuda)
+            outs = []
+            for lb, cfg in ((ref_lib, None), (lib, forced), (lib, forced), (lib, forced)):
+                if cfg is not None:
+                    lib.mi355_w8_sweep_config(G, U, waves, 1)
+                    assert lib.mi355_w8_sweep_ks(KS) == 0
+                o = torch.full((rows, n), float("nan"), dtype=dt, device=cuda)
+                st = lb.mi355_w8a16_linear_fwd(x.data_ptr(), q.data_ptr(), scale.data_ptr(), None, o.data_ptr(),
+                                               rows, k, n, k, k, n, c[dt], L.F32, -1, c[dt], abi_stream())
+                assert st == 0, lb.mi355_last_error().decode()
+                torch.cuda.synchronize()
+                outs.append(o)
+            ref, got = outs[0].float(), outs[1].float()
+            assert torch.isfinite(got).all()
+            tol = torch.finfo(dt).eps * ref.abs() + 1e-5 * ref.abs().max()
+            assert ((got - ref).abs() <= tol).all(), (forced, rows, k, n, (got - ref).abs().max().item())
+            assert torch.equal(outs[1], outs[2]) and torch.equal(outs[1], outs[3]), forced
+    finally:
+        lib.mi355_w8_sweep_config(0, 0, 0, 0)
+        lib.mi355_w8_sweep_ks(0)
