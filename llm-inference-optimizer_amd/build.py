@@ -159,9 +159,11 @@ VARIANTS = {
 # of tests/test_launch_variants.py run on them: one variant per distinct code
 # path of the kernels (several rows per wave and per workgroup, a row over
 # one wave, the LDS weight, a persistent grid, another SiLU-and-mul chunk,
-# the W8A16 widening order).
+# the W8A16 widening order, the W8A16 decode kernel's sweep builds with their
+# split of K over workgroups and pipelined loop).
 CORE_VARIANTS = ("rms_wave_rows2", "rms_block_rows2", "rms_one_wave", "rms_weight_lds", "rms_persistent8",
-                 "rms_block_persistent4", "silu_unroll1", "silu_large_block512_unroll2", "tiled_widen_in_place")
+                 "rms_block_persistent4", "silu_unroll1", "silu_large_block512_unroll2", "tiled_widen_in_place",
+                 "w8_skinny_sweep", "w8_skinny_sweep_pipe")
 VARIANT_DIR = PKG_DIR / "_variants"
 # Variants that spread a row over waves differently from the default build:
 # the fp32 sum of squares then adds in another order, so an output may differ
