@@ -71,7 +71,7 @@ def parse_args():
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
-                                      "w8a16-prefill", "w8a16-prefill-1.5b"],
+                                      "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -845,6 +845,8 @@ def run_only(ctx, args, sets):
         else:  # the two decode shapes profiled under profiles/, kernel only
             log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 8 and s[2] in (8960, 18944)],
                                        iters=iters, baselines=False)))
+    elif args.only == "prefill-core":
+        print(json.dumps(bench_prefill_core(ctx)), flush=True)
 
 
 def _sweep_leg(ctx, leg):
@@ -1515,6 +1517,48 @@ def bench_w8a16(ctx, shapes=W8A16_SHAPES, iters=300, baselines=True):
             f"({entry['frac_of_peak']:.1%}), {entry['TFLOPs']:.1f} TFLOP/s; fp16 matmul "
             f"{entry.get('fp16_matmul_us', float('nan')):.2f} us")
         del outs
+        torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill_core(ctx, shapes=((1024, 1536, 8960), (1024, 8960, 1536), (4096, 1536, 8960),
+                                      (4096, 8960, 1536)), iters=200):
+    """The tiled GEMM core at prefill rows with each kind of B operand, next
+    to hipBLASLt: the 1.5B gate/up and down projections (fp16 x) through
+    mi355_linear16_fwd (16-bit weights), mi355_w8a16_linear_fwd (int8 weights,
+    widened after each LDS read) and torch.matmul on the 16-bit weights.  If
+    widening the int8 weights were what held the W8A16 GEMM back, the 16-bit
+    path of the same core would be the faster one.  Cold weights (rotating
+    sets), min of eager and hipGraph timing, us."""
+    torch = ctx.torch
+    F16 = torch.float16
+    res = {}
+    for M, K, N in shapes:
+        x = rand(ctx, (M, K), 3, F16)
+        outs = [torch.empty((M, N), dtype=F16, device=ctx.dev) for _ in range(4)]
+        sets = min(64, n_sets(N * K * 2))
+        ws = [rand(ctx, (N, K), 10 + i, F16, std=0.02) for i in range(sets)]
+        entry = {}
+        for name, calls in (("linear16_us", [ctx.linear16_call(x, w, outs[i % 4]) for i, w in enumerate(ws)]),
+                            ("hipblaslt_fp16_us", [(lambda w=w, o=outs[i % 4]: torch.matmul(x, w.T, out=o))
+                                                   for i, w in enumerate(ws)])):
+            spin_up(ctx, calls)
+            entry[name] = round(min(time_loop(ctx, calls, iters), time_graph(ctx, calls, 2 * sets)), 3)
+        del ws
+        torch.cuda.empty_cache()
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(1)
+        sets8 = min(128, n_sets(N * K))
+        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets8)]
+        sc = [(torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets8)]
+        calls = [ctx.w8a16_call(x, q, s_, outs[i % 4]) for i, (q, s_) in enumerate(zip(qs, sc))]
+        spin_up(ctx, calls)
+        entry["w8a16_us"] = round(min(time_loop(ctx, calls, iters), time_graph(ctx, calls, 2 * sets8)), 3)
+        for k_ in ("linear16_us", "w8a16_us"):
+            entry[k_.replace("_us", "_vs_hipblaslt")] = round(entry["hipblaslt_fp16_us"] / entry[k_], 3)
+        res[f"M{M}_K{K}_N{N}"] = entry
+        log(f"  prefill core M={M} K={K} N={N}: {entry}")
+        del qs, sc, calls, outs
         torch.cuda.empty_cache()
     return res
 
