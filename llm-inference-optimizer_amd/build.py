@@ -116,6 +116,15 @@ VARIANTS = {
     "rms_persistent16": ("rmsnorm", ["-DMI355_RMS_WAVES_PER_CU=16"]),
     "rms_block_persistent4": ("rmsnorm", ["-DMI355_RMS_BLOCKS_PER_CU=4"]),
     "rms_block_persistent8": ("rmsnorm", ["-DMI355_RMS_BLOCKS_PER_CU=8"]),
+    # RMSNorm: wide rows streamed through a persistent grid, S rows in flight
+    # per workgroup (rmsnorm_block_stream), workgroups per CU
+    "rms_stream2": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=2"]),
+    "rms_stream4": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=4"]),
+    "rms_stream4_wg2": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=4", "-DMI355_RMS_STREAM_BLOCKS_PER_CU=2"]),
+    "rms_stream4_wg8": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=4", "-DMI355_RMS_STREAM_BLOCKS_PER_CU=8"]),
+    "rms_stream4_vpl1": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=4", "-DMI355_RMS_TARGET_VPL=1"]),
+    "rms_stream8_vpl1_wg2": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=8", "-DMI355_RMS_TARGET_VPL=1",
+                                         "-DMI355_RMS_STREAM_BLOCKS_PER_CU=2"]),
     # RMSNorm: workgroup size of the wave-per-row kernel
     "rms_wave_block64": ("rmsnorm", ["-DMI355_RMS_WAVE_BLOCK=64"]),
     "rms_wave_block512": ("rmsnorm", ["-DMI355_RMS_WAVE_BLOCK=512"]),
@@ -165,12 +174,13 @@ CORE_VARIANTS = ("rms_wave_rows2", "rms_block_rows2", "rms_one_wave", "rms_weigh
                  "rms_block_persistent4", "silu_unroll1", "silu_large_block512_unroll2", "tiled_widen_in_place",
                  "w8_skinny_sweep", "w8_skinny_sweep_pipe")
 VARIANT_DIR = PKG_DIR / "_variants"
-# Variants that spread a row over waves differently from the default build:
-# the fp32 sum of squares then adds in another order, so an output may differ
+# Variants that spread a row over waves differently from the default build
+# (one wave per wide row; one packet per lane over more waves): the fp32 sum
+# of squares then adds in another order, so an output may differ
 # from the default library's in its last bit (both stay within one ulp of the
 # exactly rounded result).  Every other variant is bit-identical to the
 # default library.
-REORDERING_VARIANTS = frozenset({"rms_one_wave", "rms_one_wave_rows2"})
+REORDERING_VARIANTS = frozenset({"rms_one_wave", "rms_one_wave_rows2", "rms_stream4_vpl1", "rms_stream8_vpl1_wg2"})
 
 
 def variant_path(name: str) -> Path:

@@ -48,6 +48,16 @@ static_assert(MI355_RMS_WAVE_MAX_VPL >= 1 && MI355_RMS_WAVE_MAX_VPL <= 8, "wave 
 #ifndef MI355_RMS_BLOCK_ROWS
 #define MI355_RMS_BLOCK_ROWS 1
 #endif
+// > 1: from MI355_RMS_SMALL_ROWS rows up, rows wide enough for the
+// workgroup-per-row kernel stream through a persistent grid of
+// MI355_RMS_STREAM_BLOCKS_PER_CU workgroups per CU, each keeping this many
+// rows in flight (rmsnorm_block_stream); 0 = one workgroup per row.
+#ifndef MI355_RMS_STREAM_ROWS
+#define MI355_RMS_STREAM_ROWS 0
+#endif
+#ifndef MI355_RMS_STREAM_BLOCKS_PER_CU
+#define MI355_RMS_STREAM_BLOCKS_PER_CU 4
+#endif
 // 1: the wave-per-row kernel stages the weight row in LDS once per
 // workgroup and broadcasts it to its waves, instead of each wave loading its
 // weight packets from L2.
@@ -118,6 +128,12 @@ int rms_wave(const RmsParams& p, hipStream_t s, int cus, int vpl) {
 
 template <typename TX, typename TW, typename TY, int VPL, bool ADD>
 int rms_block_rows(const RmsParams& p, hipStream_t s, int cus, int block) {
+  // (only where the ring of rows fits the register file next to the rest)
+  if constexpr (MI355_RMS_STREAM_ROWS > 1 && VPL * MI355_RMS_STREAM_ROWS <= 8) {
+    const int64_t cap = static_cast<int64_t>(cus) * MI355_RMS_STREAM_BLOCKS_PER_CU;
+    if (p.rows >= MI355_RMS_SMALL_ROWS && p.rows > cap)
+      return launch_rms(rmsnorm_block_stream<TX, TW, TY, VPL, MI355_RMS_STREAM_ROWS, ADD>, cap, block, p, s);
+  }
   const bool multi = p.rows >= MI355_RMS_SMALL_ROWS && MI355_RMS_BLOCK_ROWS > 1;
   constexpr int R = MI355_RMS_BLOCK_ROWS > 1 ? MI355_RMS_BLOCK_ROWS : 1;
   const int64_t per_block = multi ? R : 1;

@@ -24,6 +24,9 @@
 //   rmsnorm_generic     any n, alignment or dtype mix: scalar loads, two passes
 //                       over the row (the second pass re-reads the row through
 //                       L2).
+// (rmsnorm_block_stream, the workgroup-per-row kernel streaming its rows
+// through a persistent grid, is built only under MI355_RMS_STREAM_ROWS: it
+// measured slower than one workgroup per row.)
 // Rows and the weight are read through buffer descriptors that span exactly
 // one row, so the packets past n need no lane branches, with the non-temporal
 // hint on x, residual and the outputs.  All kernels stride over rows; the
@@ -279,6 +282,63 @@ __global__ __launch_bounds__(1024) void rmsnorm_block_rows(const RmsParams p) {
       row[i].template store_y<TY, MI355_RMS_KEEP_F32_BLOCK != 0>(
           make_rsrc(static_cast<typename TY::bits*>(p.y) + (r0 + i) * p.ys, row_bytes<TY>(p, r0 + i)), tid,
           nthreads, rms_rstd(tot[i], p.n, p.eps), wv);
+  }
+}
+
+// Workgroup-per-row kernel on a persistent grid that streams its rows: the
+// workgroup visits rows blockIdx.x + i * gridDim.x and keeps S of them in
+// flight in a ring of register slots, refilling a slot with the row S visits
+// ahead as soon as its own row is stored.  Per row the arithmetic and the
+// reduction order are rmsnorm_block_rows' (so are the bits); what changes is
+// that a workgroup never waits for a row with nothing else in flight.
+template <typename TX, typename TW, typename TY, int VPL, int S, bool ADD>
+__global__ __launch_bounds__(1024) void rmsnorm_block_stream(const RmsParams p) {
+  using RS = RowSlice<TX, TW, VPL>;
+  using XB = typename TX::bits;
+  __shared__ float partial[2][16];
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int nwave = nthreads >> 6;
+
+  BufChunk<TW, RS::W> wv[VPL];
+  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + nthreads * k) * RS::WB);
+
+  const int64_t g = gridDim.x;
+  // Loads of row r into a slot (past the last row: 0-byte descriptors, no
+  // traffic).
+  auto fetch = [&](RS& row, int64_t r) {
+    row.load_x(make_rsrc(static_cast<const XB*>(p.x) + r * p.xs, row_bytes<TX>(p, r)), tid, nthreads);
+    if constexpr (ADD)
+      row.load_residual(make_rsrc(static_cast<const XB*>(p.r) + r * p.rs, row_bytes<TX>(p, r)), tid, nthreads);
+  };
+  RS ring[S];
+#pragma unroll
+  for (int j = 0; j < S; ++j) fetch(ring[j], blockIdx.x + j * g);
+
+  int buf = 0;
+  for (int64_t r0 = blockIdx.x; r0 < p.rows; r0 += S * g) {
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const int64_t r = r0 + j * g;
+      if (r >= p.rows) break;  // uniform over the workgroup
+      RS& row = ring[j];
+      if constexpr (ADD) {
+        row.add_residual();
+        row.store_row(make_rsrc(static_cast<XB*>(p.ro) + r * p.ros, row_bytes<TX>(p, r)), tid, nthreads);
+      }
+      float ss = wave_allreduce_sum(row.sumsq());
+      if ((tid & 63) == 0) partial[buf][tid >> 6] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+      for (int w = 0; w < nwave; ++w) tot += partial[buf][w];
+      buf ^= 1;  // the next row writes the other buffer; this row's barrier orders the reuse
+      row.template store_y<TY, MI355_RMS_KEEP_F32_BLOCK != 0>(
+          make_rsrc(static_cast<typename TY::bits*>(p.y) + r * p.ys, row_bytes<TY>(p, r)), tid, nthreads,
+          rms_rstd(tot, p.n, p.eps), wv);
+      fetch(row, r + S * g);
+    }
   }
 }
 
