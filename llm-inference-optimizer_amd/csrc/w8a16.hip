@@ -623,7 +623,14 @@ int w8_tiled_forced(const W8Params& p, hipStream_t s) {
     case 14: return w8_tiled_cfg<T, TO, 1, 4, 2, 1, 2, EPI_W8, 1>(p, s);  // 64 x 128, 4 waves of 64 x 32
     case 15: return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 3, EPI_W8, 1>(p, s);  // 128 x 128, 4 waves, 3 stages
     case 16: return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 3, EPI_W8, 1>(p, s);  // 64 x 64, 4 waves, ring, 3 stages
-    default: return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);             // 64 x 64, 4 waves, step pipeline
+    case 17: return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);             // 64 x 64, 4 waves, step pipeline
+    // large tiles (fewer operand bytes per flop) behind deeper LDS rings
+    case 18: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 3, EPI_W8, 1>(p, s);  // 256 x 128, 4 waves of 128 x 64, ring, 3 stages
+    case 19: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 4, EPI_W8, 1>(p, s);  // 256 x 128, 4 waves of 128 x 64, ring, 4 stages
+    case 20: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 3>(p, s);             // 256 x 128, 4 waves of 128 x 64, step, 3 stages
+    case 21: return w8_tiled_cfg<T, TO, 2, 2, 4, 4, 3, EPI_W8, 1>(p, s);  // 256 x 256, 4 waves of 128 x 128, ring, 3 stages
+    case 22: return w8_tiled_cfg<T, TO, 2, 2, 2, 4, 4, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 64 x 128, ring, 4 stages
+    default: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 4, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 4 stages
   }
 }
 
