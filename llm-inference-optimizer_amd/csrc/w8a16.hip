@@ -162,11 +162,16 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
     }
   }
 
-  // This workgroup's share of the 128-column blocks (all of them unless K is
-  // split over workgroups too), split again over its waves.
+  // This workgroup's share of the 128-column blocks (all of them unless a
+  // sweep build splits K over workgroups too), split again over its waves.
   const int nblk_all = (p.k + 127) >> 7;
+#ifdef MI355_W8_SWEEP
   const int z0 = (nblk_all * static_cast<int>(blockIdx.z)) / static_cast<int>(gridDim.z);
   const int nblk = (nblk_all * (static_cast<int>(blockIdx.z) + 1)) / static_cast<int>(gridDim.z) - z0;
+#else
+  constexpr int z0 = 0;
+  const int nblk = nblk_all;
+#endif
   const int s_begin = z0 + (nblk * wave) / nwave;
   const int s_end = z0 + (nblk * (wave + 1)) / nwave;
   // Block s into slot (wq, xa); blocks past the wave's range or past k load
