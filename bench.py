@@ -71,7 +71,8 @@ def parse_args():
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
-                                      "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core"],
+                                      "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
+                                      "gate-up-w8-prefill", "w8a16-prefill-wide"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -194,6 +195,19 @@ class Ctx:
             st = f(*args, self.stream)
             if st:
                 self.check("mi355_gate_up_silu_fwd", st)
+        return call
+
+    def gate_up_w8_call(self, x, qg, sg, qu, su, o):
+        M, K = x.shape
+        code = self.L.DTYPE_CODE[x.dtype]
+        f = self.lib.mi355_gate_up_silu_w8a16_fwd
+        args = (x.data_ptr(), qg.data_ptr(), qu.data_ptr(), sg.data_ptr(), su.data_ptr(), o.data_ptr(), M, K,
+                qg.shape[0], K, K, qg.shape[0], code, self.L.DTYPE_CODE[sg.dtype], code)
+
+        def call():
+            st = f(*args, self.stream)
+            if st:
+                self.check("mi355_gate_up_silu_w8a16_fwd", st)
         return call
 
     def w8a16_call(self, x, q, scale, out, bias=None):
@@ -458,6 +472,13 @@ KNOWN_LAUNCHES = {
     ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4, 0>", 384 * 256): (
         "W8A16 prefill down, 1024 rows, [1536,8960] int8, fp16",
         1536 * 8960 + 4 * 1536 + 1024 * 8960 * 2 + 1024 * 1536 * 2, 2 * 1024 * 8960 * 1536),
+    # the wide-output plan from 1024 rows: 128 x 128 tiles of 8 waves, 3-stage ring
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 2, 1, 0, 3, 1>", 560 * 512): (
+        "W8A16 prefill gate/up, 1024 rows, [8960,1536] int8, fp16 (128x128 tiles)",
+        8960 * 1536 + 4 * 8960 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 2 * 1024 * 1536 * 8960),
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 2, 1, 0, 3, 1>", 2240 * 512): (
+        "W8A16 prefill gate/up, 4096 rows, [8960,1536] int8, fp16 (128x128 tiles)",
+        8960 * 1536 + 4 * 8960 + 4096 * 1536 * 2 + 4096 * 8960 * 2, 2 * 4096 * 1536 * 8960),
 }
 COPY_READ_KIB = COPY_WRITE_KIB = (1 << 30) / 1024
 
@@ -816,6 +837,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_w8(ctx)))
+    elif args.only == "gate-up-w8-prefill":  # prefill rows of the 1.5B and 7B MLPs, kernel only
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_gate_up_w8(ctx, shapes=GATE_UP_W8_PREFILL_SHAPES, iters=100, baselines=False)))
     elif args.only == "gate-up-w8-decode":  # the two 8-row shapes profiled under profiles/, no baseline
         del sets
         torch.cuda.empty_cache()
@@ -830,6 +855,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES[1:3], baselines=False)))
+    elif args.only == "w8a16-prefill-wide":  # wide outputs at prefill rows: 1.5B and 7B gate/up, n = 4736
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_w8a16(ctx, shapes=W8A16_WIDE_PREFILL_SHAPES, iters=100, baselines=False)))
     elif args.only in ("w8a16", "w8a16-decode", "w8a16-prefill", "w8a16-prefill-1.5b"):
         del sets
         torch.cuda.empty_cache()
@@ -1352,11 +1381,14 @@ def bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES, iters=60, baseline
 GATE_UP_W8_SHAPES = [(1, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 1536, 8960, "f16", "qwen2.5-1.5b"),
                      (32, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 3584, 18944, "bf16", "qwen2.5-7b"),
                      (1024, 1536, 8960, "f16", "qwen2.5-1.5b")]
+GATE_UP_W8_PREFILL_SHAPES = [(1024, 1536, 8960, "f16", "qwen2.5-1.5b"), (4096, 1536, 8960, "f16", "qwen2.5-1.5b"),
+                             (1024, 3584, 18944, "bf16", "qwen2.5-7b"), (4096, 3584, 18944, "bf16", "qwen2.5-7b")]
 
 
 def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300, baselines=True):
-    """Int8 gate/up projections + SiLU-and-mul (one kernel) against the
-    quantised model's chain: two W8A16 linears (this build's kernel, each
+    """Int8 gate/up projections + SiLU-and-mul (one kernel, through its C ABI
+    entry point, so a --variant library's kernels are the ones timed) against
+    the quantised model's chain: two W8A16 linears (this build's kernel, each
     rounded to x's dtype) and the SiLU-and-mul kernel.  Per-layer int8
     weight sets with a footprint above 1 GiB; eager back-to-back and hipGraph
     timing (min).  Algorithmic bytes: both int8 matrices + both fp32 scales +
@@ -1377,7 +1409,8 @@ def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300, baselines=True):
                torch.rand(I, generator=g, device=ctx.dev) * 2e-3 + 1e-4,
                torch.randint(-127, 128, (I, K), generator=g, device=ctx.dev, dtype=torch.int8),
                torch.rand(I, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
-        fused = [lambda w=w: pkg.fused_gate_up_silu_w8a16(x, w[0], w[1], w[2], w[3]) for w in ws]
+        outs = [torch.empty((M, I), dtype=dt, device=ctx.dev) for _ in range(4)]
+        fused = [ctx.gate_up_w8_call(x, w[0], w[1], w[2], w[3], outs[i % 4]) for i, w in enumerate(ws)]
         spin_up(ctx, fused)
         us = min(time_loop(ctx, fused, iters), time_graph(ctx, fused, max(2 * sets, 64)))
         entry = kernel_entry("w8a16 dual (gate/up + SiLU-and-mul)", nbytes, us,
@@ -1392,7 +1425,7 @@ def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300, baselines=True):
             del chains
         res[f"{label}_M{M}_{dname}"] = entry
         log(f"  int8 gate_up {label} M={M}: {entry}")
-        del ws, fused
+        del ws, fused, outs
         torch.cuda.empty_cache()
     return res
 
@@ -1407,6 +1440,13 @@ W8A16_SHAPES = [(M, K, N, "f16", lab) for K, N, lab in ((1536, 1536, "q/o proj")
                                                (4096, 1536, 8960, "f16", "gate/up proj"),
                                                (4096, 8960, 1536, "f16", "down proj")]
 
+
+# (rows, k, n, dtype name, label): W8A16 single GEMMs with wide outputs at prefill rows
+W8A16_WIDE_PREFILL_SHAPES = [(1024, 1536, 8960, "f16", "gate/up proj"), (4096, 1536, 8960, "f16", "gate/up proj"),
+                             (1024, 3584, 18944, "bf16", "7b gate/up proj"),
+                             (4096, 3584, 18944, "bf16", "7b gate/up proj"), (1024, 1536, 4736, "f16", "n 4736"),
+                             (1024, 18944, 3584, "bf16", "7b down proj"), (4096, 18944, 3584, "bf16", "7b down proj"),
+                             (1024, 3584, 3584, "bf16", "7b o proj")]
 
 # (rows, k, n, dtype name, label): the MLP down projections of Qwen2.5-1.5B and -7B at decode rows
 LINEAR16_SHAPES = [(1, 8960, 1536, "f16", "qwen2.5-1.5b down"), (8, 8960, 1536, "f16", "qwen2.5-1.5b down"),

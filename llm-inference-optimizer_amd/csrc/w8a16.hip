@@ -635,7 +635,18 @@ int w8_tiled_forced(const W8Params& p, hipStream_t s) {
     case 20: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 3>(p, s);             // 256 x 128, 4 waves of 128 x 64, step, 3 stages
     case 21: return w8_tiled_cfg<T, TO, 2, 2, 4, 4, 3, EPI_W8, 1>(p, s);  // 256 x 256, 4 waves of 128 x 128, ring, 3 stages
     case 22: return w8_tiled_cfg<T, TO, 2, 2, 2, 4, 4, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 64 x 128, ring, 4 stages
-    default: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 4, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 4 stages
+    case 23: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 4, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 4 stages
+    // more waves per workgroup issuing the DMA
+    case 24: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 2 stages
+    case 25: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 3 stages
+    case 26: return w8_tiled_cfg<T, TO, 2, 8, 2, 1, 2, EPI_W8, 1>(p, s);  // 128 x 256, 16 waves of 64 x 32, ring, 2 stages
+    case 27: return w8_tiled_cfg<T, TO, 4, 2, 2, 2, 2, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 64 x 64, ring, 2 stages
+    case 28: return w8_tiled_cfg<T, TO, 4, 2, 2, 2, 3, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 64 x 64, ring, 3 stages
+    case 29: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 4>(p, s);             // 128 x 128, 8 waves of 64 x 32, step, 4 stages
+    case 30: return w8_tiled_cfg<T, TO, 4, 2, 1, 2, 3, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 32 x 64, ring, 3 stages
+    case 31: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 4, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 4 stages
+    case 32: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 3, EPI_W8, 1>(p, s);  // 128 x 256, 8 waves of 64 x 64, ring, 3 stages
+    default: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
   }
 }
 
@@ -643,7 +654,18 @@ template <typename T, typename TO>
 int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
   if constexpr (MI355_W8_FORCE > 0) return w8_tiled_forced<T, TO>(p, s);
   constexpr bool wide = std::is_same<T, F16>::value;
-  // Wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring
+  // Wide outputs from 1024 rows at gate/up and o-projection depths (k <=
+  // 4096): 128 x 128 tiles of 8 waves (64 x 32 each) behind a 3-stage ring,
+  // two workgroups per CU, so 16 waves per CU issue the global -> LDS DMA
+  // that bounds this GEMM, for 40% fewer operand bytes per flop than 128 x 64
+  // tiles.  Measured against the plan below and forced configurations 1-33:
+  // 1.5B gate/up 1024 rows 45.8 vs 49.8 us, 4096 rows 138.6 vs 155.8 us; 7B
+  // gate/up (bf16) 149.4 vs 178.5 and 556.9 vs 582.2 us; 7B o projection and
+  // n = 4736 even.  The deep 7B down projection (k = 18944) at 4096 rows
+  // keeps the plan below (512.7 vs 533.8 us).
+  if (p.n > 2048 && p.rows >= 1024 && p.k <= 4096)
+    return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(p, s);
+  // Below 1024 rows, wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring
   // (2 stages) at the shape whose busiest CU finishes first -- ceil(tiles /
   // CUs) times the cost of one tile of 128 x 64 (4 waves, 40 KiB of LDS, four
   // workgroups per CU), 256 x 128 (8 waves of 128 x 32, two per CU) or
@@ -679,8 +701,32 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
 // tile does not split into the 8 waves' 1 KiB DMA instructions.  bf16 keeps
 // the 128 x 64 shape there (its widening needs more registers; 128 x 128 at
 // 8 waves would spill).
+// MI355_W8_DUAL_FORCE = n (> 0): every dual (gate/up + SiLU-and-mul) launch
+// above 256 rows takes configuration n below (a measurement switch for
+// variant builds; every configuration computes the same results).
+#ifndef MI355_W8_DUAL_FORCE
+#define MI355_W8_DUAL_FORCE 0
+#endif
+
+template <typename T, typename TO>
+int w8_tiled_dual_forced(const W8Params& p, hipStream_t s) {
+  using tiled::EPI_SILU_W8;
+  switch (MI355_W8_DUAL_FORCE) {
+    case 1: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, EPI_SILU_W8, 1>(p, s);  // 128 x 64, 4 waves, ring, 2 stages
+    case 2: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, EPI_SILU_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 2 stages
+    case 3: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 2 stages
+    case 4: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 3 stages
+    case 5: return w8_tiled_cfg<T, TO, 4, 2, 1, 2, 2, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 32 x 64, ring, 2 stages
+    case 6: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 3, EPI_SILU_W8, 1>(p, s);  // 128 x 64, 4 waves, ring, 3 stages
+    default: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_SILU_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
+  }
+}
+
 template <typename T, typename TO>
 int w8_tiled_dual(const W8Params& p, hipStream_t s, int cus) {
+  if constexpr (MI355_W8_DUAL_FORCE > 0) {
+    if (p.rows > 256) return w8_tiled_dual_forced<T, TO>(p, s);
+  }
   // More than 256 rows: the sub-step ring (2 stages), 128 x 64 tiles (4
   // waves, 48 KiB of LDS, three workgroups per CU) or 256 x 128 (8 waves of
   // 128 x 32), whichever takes fewer rounds, a round of 256 x 128 weighted

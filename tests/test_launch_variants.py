@@ -174,6 +174,40 @@ def test_w8a16_variant_is_bitwise_the_default(name, cuda):
         assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, rows, k, n, dt)
 
 
+# int8 gate/up + SiLU-and-mul above 256 rows through the tiled GEMM: the
+# 1.5B MLP, ragged rows / n, bf16 at the 7B widths
+W8_DUAL_SHAPES = [(1024, 1536, 8960, torch.float16), (300, 1536, 4736, torch.float16),
+                  (520, 3584, 2000, torch.bfloat16)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", W8_VARIANTS)
+def test_w8a16_dual_variant_is_bitwise_the_default(name, cuda):
+    """The int8 gate/up + SiLU-and-mul kernel under every W8A16 variant (the
+    forced dual tile configurations above all): the same products added in
+    the same order, so the same bits as the default library."""
+    lib = _variant(name)
+    ref_lib = L.load()
+    c = L.DTYPE_CODE
+    for i, (rows, k, n, dt) in enumerate(W8_DUAL_SHAPES):
+        print(f"variant {name}: gate/up w8a16 rows={rows} k={k} n={n} {dt}", flush=True)
+        x = torch.randn(rows, k, generator=_gen(1300 + i)).to(dt).to(cuda)
+        qg = torch.randint(-127, 128, (n, k), generator=_gen(1400 + i), dtype=torch.int8).to(cuda)
+        qu = torch.randint(-127, 128, (n, k), generator=_gen(1500 + i), dtype=torch.int8).to(cuda)
+        sg = (torch.rand(n, generator=_gen(1600 + i)) * 1e-3 + 1e-4).to(cuda)
+        su = (torch.rand(n, generator=_gen(1700 + i)) * 1e-3 + 1e-4).to(cuda)
+        outs = []
+        for lb in (ref_lib, lib):
+            o = torch.full((rows, n), float("nan"), dtype=dt, device=cuda)
+            st = lb.mi355_gate_up_silu_w8a16_fwd(x.data_ptr(), qg.data_ptr(), qu.data_ptr(), sg.data_ptr(),
+                                                 su.data_ptr(), o.data_ptr(), rows, k, n, k, k, n, c[dt], L.F32,
+                                                 c[dt], abi_stream())
+            assert st == 0, lb.mi355_last_error().decode()
+            torch.cuda.synchronize()
+            outs.append(o)
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, rows, k, n, dt)
+
+
 # Forced skinny shapes of the sweep build: (G, waves, U, KS).  KS > 1 splits K
 # over workgroups (partial sums through device memory, added by the last
 # workgroup to arrive in workgroup order).
