@@ -72,7 +72,7 @@ def parse_args():
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
-                                      "gate-up-w8-prefill", "w8a16-prefill-wide"],
+                                      "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -855,10 +855,11 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES[1:3], baselines=False)))
-    elif args.only == "w8a16-prefill-wide":  # wide outputs at prefill rows: 1.5B and 7B gate/up, n = 4736
+    elif args.only in ("w8a16-prefill-wide", "w8a16-prefill-narrow"):  # prefill rows, kernel only
         del sets
         torch.cuda.empty_cache()
-        log(json.dumps(bench_w8a16(ctx, shapes=W8A16_WIDE_PREFILL_SHAPES, iters=100, baselines=False)))
+        shapes = W8A16_WIDE_PREFILL_SHAPES if args.only.endswith("wide") else W8A16_NARROW_PREFILL_SHAPES
+        log(json.dumps(bench_w8a16(ctx, shapes=shapes, iters=100, baselines=False)))
     elif args.only in ("w8a16", "w8a16-decode", "w8a16-prefill", "w8a16-prefill-1.5b"):
         del sets
         torch.cuda.empty_cache()
@@ -1447,6 +1448,13 @@ W8A16_WIDE_PREFILL_SHAPES = [(1024, 1536, 8960, "f16", "gate/up proj"), (4096, 1
                              (4096, 3584, 18944, "bf16", "7b gate/up proj"), (1024, 1536, 4736, "f16", "n 4736"),
                              (1024, 18944, 3584, "bf16", "7b down proj"), (4096, 18944, 3584, "bf16", "7b down proj"),
                              (1024, 3584, 3584, "bf16", "7b o proj")]
+# W8A16 single GEMMs with narrow (1536-wide) outputs at prefill rows: the 1.5B down and q/o projections
+W8A16_NARROW_PREFILL_SHAPES = [(1024, 8960, 1536, "f16", "down proj"), (4096, 8960, 1536, "f16", "down proj"),
+                               (2048, 8960, 1536, "f16", "down proj"), (1024, 1536, 1536, "f16", "q/o proj"),
+                               (4096, 1536, 1536, "f16", "q/o proj"), (512, 8960, 1536, "f16", "down proj"),
+                               (768, 8960, 1536, "f16", "down proj"), (1280, 8960, 1536, "f16", "down proj"),
+                               (512, 1536, 1536, "f16", "q/o proj"), (1024, 1536, 2048, "f16", "n 2048"),
+                               (1024, 1536, 1024, "f16", "n 1024")]
 
 # (rows, k, n, dtype name, label): the MLP down projections of Qwen2.5-1.5B and -7B at decode rows
 LINEAR16_SHAPES = [(1, 8960, 1536, "f16", "qwen2.5-1.5b down"), (8, 8960, 1536, "f16", "qwen2.5-1.5b down"),

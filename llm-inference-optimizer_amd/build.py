@@ -156,7 +156,7 @@ VARIANTS = {
     "w8_skinny_sweep_pipe": ("w8a16", ["-DMI355_W8_SWEEP", "-DMI355_W8_PIPE=1"]),
     # W8A16 tiled GEMM: one tile configuration for every prefill launch
     # (MI355_W8_FORCE in w8a16.hip lists them)
-    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 34)},
+    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 37)},
     # W8A16 gate/up + SiLU-and-mul tiled GEMM above 256 rows: one tile
     # configuration for every launch (MI355_W8_DUAL_FORCE in w8a16.hip)
     **{f"w8_dual_cfg{i}": ("w8a16", [f"-DMI355_W8_DUAL_FORCE={i}"]) for i in range(1, 8)},
@@ -172,10 +172,11 @@ VARIANTS = {
 # path of the kernels (several rows per wave and per workgroup, a row over
 # one wave, the LDS weight, a persistent grid, another SiLU-and-mul chunk,
 # the W8A16 widening order, the W8A16 decode kernel's sweep builds with their
-# split of K over workgroups and pipelined loop).
+# split of K over workgroups and pipelined loop, the 256 x 128 and 256 x 256
+# W8A16 tiles that the launch plan now picks only for k > 4096).
 CORE_VARIANTS = ("rms_wave_rows2", "rms_block_rows2", "rms_one_wave", "rms_weight_lds", "rms_persistent8",
                  "rms_block_persistent4", "silu_unroll1", "silu_large_block512_unroll2", "tiled_widen_in_place",
-                 "w8_skinny_sweep", "w8_skinny_sweep_pipe")
+                 "w8_skinny_sweep", "w8_skinny_sweep_pipe", "w8_tile_cfg2", "w8_tile_cfg3")
 VARIANT_DIR = PKG_DIR / "_variants"
 # Variants that spread a row over waves differently from the default build
 # (one wave per wide row; one packet per lane over more waves): the fp32 sum

@@ -646,7 +646,11 @@ int w8_tiled_forced(const W8Params& p, hipStream_t s) {
     case 30: return w8_tiled_cfg<T, TO, 4, 2, 1, 2, 3, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 32 x 64, ring, 3 stages
     case 31: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 4, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 4 stages
     case 32: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 3, EPI_W8, 1>(p, s);  // 128 x 256, 8 waves of 64 x 64, ring, 3 stages
-    default: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
+    case 33: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
+    // narrow outputs: 64 x 128 tiles of 8 waves
+    case 34: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 3, EPI_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 3 stages
+    case 35: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4, EPI_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 4 stages
+    default: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4>(p, s);             // 64 x 128, 8 waves of 32 x 32, step, 4 stages
   }
 }
 
@@ -687,6 +691,16 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
       return w8_tiled_cfg<T, TO, 4, 2, 2, 4, 2, tiled::EPI_W8, 1>(p, s);
     }
   }
+  // Narrow outputs (n <= 2048) whose 64 x 128 tiles number between half and
+  // all of the CUs: 8 waves of 32 x 32 per tile behind a 4-stage ring, one
+  // tile per CU with 8 waves issuing its DMA (forced configurations 17 and
+  // 34-36 against the plan below: 1.5B down 1024 rows 49.8 vs 59.4 us, 1280
+  // rows 51.6 vs 60.6; q/o 1024 rows 13.8 vs 15.6; n = 2048 14.1 vs 18.5;
+  // 768 rows even).  Fewer tiles (512-row down and q/o, n = 1024) and more
+  // (2048 rows and up) run faster on the shapes below.
+  const int64_t t64x128 = static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 127) / 128);
+  if (p.n <= 2048 && 2 * t64x128 > cus && t64x128 <= cus)
+    return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4, tiled::EPI_W8, 1>(p, s);
   const int64_t t128 = static_cast<int64_t>((p.rows + 127) / 128) * ((p.n + 127) / 128);
   if (t128 < 128) return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);
   if (t128 < 320 || p.n > 2048) return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(p, s);

@@ -135,17 +135,24 @@ def test_bf16_matches_oracle(pkg, orc, cuda, M, K, N, bias):
 # number of 128 x 128 output tiles), with k tails and ragged edges.
 TILED_CASES = [
     (300, 1552, 1000, F16, True),     # < 128 tiles: 64 x 64
-    (320, 512, 8960, F16, False),     # < 320: 128 x 128, 8 waves
+    (320, 512, 8960, F16, False),     # < 320: 128 x 128, 8 waves, step pipeline
     (200, 2048, 8960, BF16, True),    # <= 256 rows but a large grid: tiled, 128 x 128
     (4096, 256, 1536, F16, True),     # n <= 2048: 128 x 256
     (4096, 256, 1536, BF16, False),   # (bf16: 128 x 128)
-    # n > 2048 with >= 2 tiles of 128 x 64 per CU: the sub-step ring
+    # n <= 2048 with between cus / 2 and cus tiles of 64 x 128: 8 waves, ring
+    (1024, 1536, 1536, F16, True),    # 192 tiles
+    (1000, 272, 2000, BF16, False),   # 256 tiles, ragged rows and n, k tail
+    # n > 2048 below 1024 rows with >= 2 tiles of 128 x 64 per CU: the sub-step ring
     (512, 512, 8960, F16, False),     # 128 x 64, 4 waves (main loop and k tail)
-    (1024, 272, 8960, BF16, False),   # 128 x 64
-    (2048, 128, 8952, F16, False),    # 128 x 64, ragged n
-    (4096, 64, 8960, F16, True),      # 256 x 128, 8 waves
-    (4096, 80, 9000, BF16, True),     # 256 x 128, ragged n, k tail only
-    (4096, 32, 3584, BF16, True),     # 256 x 256, 8 waves
+    # n > 2048 from 1024 rows, k <= 4096: 128 x 128 tiles of 8 waves, 3-stage ring
+    (1024, 272, 8960, BF16, False),
+    (2048, 128, 8952, F16, False),    # ragged n
+    (4096, 64, 8960, F16, True),
+    (4096, 80, 9000, BF16, True),     # ragged n, k tail only
+    (4096, 32, 3584, BF16, True),
+    # (the 256 x 128 and 256 x 256 sub-step rings, now taken only at k > 4096,
+    # are checked bit for bit against this library by the w8_tile_cfg2 / 3
+    # variants in test_launch_variants.py)
     # 17 - 64 rows with >= 128 tile columns: the small tiled shapes
     (24, 1536, 8960, F16, True),      # 32 x 64
     (20, 256, 16400, BF16, False),    # n > 10000: 32 x 128
