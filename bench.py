@@ -472,6 +472,11 @@ KNOWN_LAUNCHES = {
     ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4, 0>", 384 * 256): (
         "W8A16 prefill down, 1024 rows, [1536,8960] int8, fp16",
         1536 * 8960 + 4 * 1536 + 1024 * 8960 * 2 + 1024 * 1536 * 2, 2 * 1024 * 8960 * 1536),
+    # narrow outputs filling half to all of the CUs: 64 x 128 tiles of 8 waves (the
+    # 1024-row q/o projection launches the same grid; its launches mix into this row)
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 1, 1, 0, 4, 1>", 192 * 512): (
+        "W8A16 prefill down, 1024 rows, [1536,8960] int8, fp16 (64x128 tiles)",
+        1536 * 8960 + 4 * 1536 + 1024 * 8960 * 2 + 1024 * 1536 * 2, 2 * 1024 * 8960 * 1536),
     # the wide-output plan from 1024 rows: 128 x 128 tiles of 8 waves, 3-stage ring
     ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 2, 1, 0, 3, 1>", 560 * 512): (
         "W8A16 prefill gate/up, 1024 rows, [8960,1536] int8, fp16 (128x128 tiles)",
