@@ -156,7 +156,7 @@ VARIANTS = {
     "w8_skinny_sweep_pipe": ("w8a16", ["-DMI355_W8_SWEEP", "-DMI355_W8_PIPE=1"]),
     # W8A16 tiled GEMM: one tile configuration for every prefill launch
     # (MI355_W8_FORCE in w8a16.hip lists them)
-    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 37)},
+    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 39)},
     # W8A16 gate/up + SiLU-and-mul tiled GEMM above 256 rows: one tile
     # configuration for every launch (MI355_W8_DUAL_FORCE in w8a16.hip)
     **{f"w8_dual_cfg{i}": ("w8a16", [f"-DMI355_W8_DUAL_FORCE={i}"]) for i in range(1, 8)},

@@ -650,7 +650,10 @@ int w8_tiled_forced(const W8Params& p, hipStream_t s) {
     // narrow outputs: 64 x 128 tiles of 8 waves
     case 34: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 3, EPI_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 3 stages
     case 35: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4, EPI_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 4 stages
-    default: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4>(p, s);             // 64 x 128, 8 waves of 32 x 32, step, 4 stages
+    case 36: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4>(p, s);             // 64 x 128, 8 waves of 32 x 32, step, 4 stages
+    // 192-row tiles: fewer rounds of tiles at 1024 and 4096 rows
+    case 37: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 2 stages
+    default: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 3, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 3 stages
   }
 }
 
