@@ -237,8 +237,22 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc
 #define MI355_TILED_WIDEN_AHEAD 1
 #endif
 
+// MI355_TILED_MIN_WAVES_PER_SIMD = w > 0: every tiled kernel is compiled to
+// fit w waves per SIMD (at most 512 / w registers a lane), so register-heavy
+// tiles can run two workgroups per CU (a measurement switch for variant
+// builds; 0 = the compiler's own choice).
+#ifndef MI355_TILED_MIN_WAVES_PER_SIMD
+#define MI355_TILED_MIN_WAVES_PER_SIMD 0
+#endif
+#if MI355_TILED_MIN_WAVES_PER_SIMD > 0
+#define MI355_TILED_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(MI355_TILED_MIN_WAVES_PER_SIMD)))
+#else
+#define MI355_TILED_WAVES_ATTR
+#endif
+
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0>
-__global__ __launch_bounds__(64 * WGM * WGN + (MI355_TILED_PREFETCH > 0 ? 64 : 0)) void tiled_gemm(const Params p) {
+__global__ __launch_bounds__(64 * WGM * WGN + (MI355_TILED_PREFETCH > 0 ? 64 : 0)) MI355_TILED_WAVES_ATTR void
+tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
   constexpr bool I8 = C::I8;
   using TB = typename T::bits;
