@@ -125,6 +125,10 @@ VARIANTS = {
     "rms_stream4_vpl1": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=4", "-DMI355_RMS_TARGET_VPL=1"]),
     "rms_stream8_vpl1_wg2": ("rmsnorm", ["-DMI355_RMS_STREAM_ROWS=8", "-DMI355_RMS_TARGET_VPL=1",
                                          "-DMI355_RMS_STREAM_BLOCKS_PER_CU=2"]),
+    # RMSNorm: packets per lane of the workgroup-per-row kernel (C4: 7 waves x
+    # 1 packet, 2 waves x 4, against the shipped 4 x 2)
+    "rms_target_vpl1": ("rmsnorm", ["-DMI355_RMS_TARGET_VPL=1"]),
+    "rms_target_vpl4": ("rmsnorm", ["-DMI355_RMS_TARGET_VPL=4"]),
     # RMSNorm: workgroup size of the wave-per-row kernel
     "rms_wave_block64": ("rmsnorm", ["-DMI355_RMS_WAVE_BLOCK=64"]),
     "rms_wave_block512": ("rmsnorm", ["-DMI355_RMS_WAVE_BLOCK=512"]),
@@ -187,7 +191,8 @@ VARIANT_DIR = PKG_DIR / "_variants"
 # from the default library's in its last bit (both stay within one ulp of the
 # exactly rounded result).  Every other variant is bit-identical to the
 # default library.
-REORDERING_VARIANTS = frozenset({"rms_one_wave", "rms_one_wave_rows2", "rms_stream4_vpl1", "rms_stream8_vpl1_wg2"})
+REORDERING_VARIANTS = frozenset({"rms_one_wave", "rms_one_wave_rows2", "rms_stream4_vpl1", "rms_stream8_vpl1_wg2",
+                                 "rms_target_vpl1", "rms_target_vpl4"})
 
 
 def variant_path(name: str) -> Path:
