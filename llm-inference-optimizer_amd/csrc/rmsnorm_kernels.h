@@ -55,6 +55,12 @@
 
 namespace mi355 {
 
+// Whether the workgroup-per-row kernels keep the fp32 widening of a lane's
+// `packets` row packets live between the passes: at most 4 packets (8 would
+// hold 64 fp32 values a lane and spill).
+template <int packets>
+constexpr bool kKeepF32Block = MI355_RMS_KEEP_F32_BLOCK != 0 && packets <= 4;
+
 // Kernel parameters, passed by value.  r / ro / rs / ros are used with ADD only.
 struct RmsParams {
   const void* x;   // [rows, xs]
@@ -279,7 +285,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_block_rows(const RmsParams p) {
     buf ^= 1;  // the next iteration writes the other buffer; this one's barrier orders the reuse
 #pragma unroll
     for (int i = 0; i < R; ++i)
-      row[i].template store_y<TY, MI355_RMS_KEEP_F32_BLOCK != 0>(
+      row[i].template store_y<TY, kKeepF32Block<VPL * R>>(
           make_rsrc(static_cast<typename TY::bits*>(p.y) + (r0 + i) * p.ys, row_bytes<TY>(p, r0 + i)), tid,
           nthreads, rms_rstd(tot[i], p.n, p.eps), wv);
   }
@@ -334,7 +340,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_block_stream(const RmsParams p) 
       float tot = 0.0f;
       for (int w = 0; w < nwave; ++w) tot += partial[buf][w];
       buf ^= 1;  // the next row writes the other buffer; this row's barrier orders the reuse
-      row.template store_y<TY, MI355_RMS_KEEP_F32_BLOCK != 0>(
+      row.template store_y<TY, kKeepF32Block<VPL>>(
           make_rsrc(static_cast<typename TY::bits*>(p.y) + r * p.ys, row_bytes<TY>(p, r)), tid, nthreads,
           rms_rstd(tot, p.n, p.eps), wv);
       fetch(row, r + S * g);
