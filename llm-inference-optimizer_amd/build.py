@@ -160,7 +160,7 @@ VARIANTS = {
     "w8_skinny_sweep_pipe": ("w8a16", ["-DMI355_W8_SWEEP", "-DMI355_W8_PIPE=1"]),
     # W8A16 tiled GEMM: one tile configuration for every prefill launch
     # (MI355_W8_FORCE in w8a16.hip lists them)
-    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 39)},
+    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 40)},
     # 192 x 128 tiles of 8 waves squeezed to 4 waves per SIMD (two
     # workgroups per CU; a few VGPRs spill)
     "w8_tile_cfg37_wpe4": ("w8a16", ["-DMI355_W8_FORCE=37", "-DMI355_TILED_MIN_WAVES_PER_SIMD=4"]),

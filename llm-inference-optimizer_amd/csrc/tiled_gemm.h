@@ -244,15 +244,18 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc
 #ifndef MI355_TILED_MIN_WAVES_PER_SIMD
 #define MI355_TILED_MIN_WAVES_PER_SIMD 0
 #endif
-#if MI355_TILED_MIN_WAVES_PER_SIMD > 0
-#define MI355_TILED_WAVES_ATTR __attribute__((amdgpu_waves_per_eu(MI355_TILED_MIN_WAVES_PER_SIMD)))
-#else
-#define MI355_TILED_WAVES_ATTR
-#endif
 
-template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0>
-__global__ __launch_bounds__(64 * WGM * WGN + (MI355_TILED_PREFETCH > 0 ? 64 : 0)) MI355_TILED_WAVES_ATTR void
-tiled_gemm(const Params p) {
+// The occupancy one configuration is compiled for: its own WPE waves per SIMD
+// when WPE > 0, else the switch above, else 1 (no register cap).
+template <int WPE>
+constexpr int kMinWavesPerSimd = WPE > 0 ? WPE : (MI355_TILED_MIN_WAVES_PER_SIMD > 0 ? MI355_TILED_MIN_WAVES_PER_SIMD : 1);
+
+// WPE > 0 caps the registers of this configuration alone so that WPE waves fit
+// on each SIMD (a 192 x 128 tile of 8 waves at WPE = 4 fits in 128 VGPRs and
+// runs two workgroups per CU).
+template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0, int WPE = 0>
+__global__ __launch_bounds__(64 * WGM * WGN + (MI355_TILED_PREFETCH > 0 ? 64 : 0))
+__attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
   constexpr bool I8 = C::I8;
   using TB = typename T::bits;

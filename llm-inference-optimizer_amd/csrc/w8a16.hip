@@ -559,7 +559,8 @@ bool tiled_fits(const W8Params& p, bool) {
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
-template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8, int RING = 0>
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8, int RING = 0,
+          int WPE = 0>
 int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_I8, TO, WGM, WGN, FM, FN, EPI, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
@@ -585,7 +586,7 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
-                                                                                      EPI, S, RING>),
+                                                                                      EPI, S, RING, WPE>),
                                     dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::BLOCK), args, 0, s),
                     "w8a16 tiled launch");
 }
@@ -653,7 +654,9 @@ int w8_tiled_forced(const W8Params& p, hipStream_t s) {
     case 36: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4>(p, s);             // 64 x 128, 8 waves of 32 x 32, step, 4 stages
     // 192-row tiles: fewer rounds of tiles at 1024 and 4096 rows
     case 37: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 2 stages
-    default: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 3, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 3 stages
+    case 38: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 3, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 3 stages
+    // 192 x 128, 8 waves of 96 x 32, ring, 2 stages, registers capped for 4 waves per SIMD (two workgroups per CU)
+    default: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1, 4>(p, s);
   }
 }
 
@@ -670,8 +673,18 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
   // gate/up (bf16) 149.4 vs 178.5 and 556.9 vs 582.2 us; 7B o projection and
   // n = 4736 even.  The deep 7B down projection (k = 18944) at 4096 rows
   // keeps the plan below (512.7 vs 533.8 us).
-  if (p.n > 2048 && p.rows >= 1024 && p.k <= 4096)
+  // Where 192 x 128 tiles (8 waves of 96 x 32, 2-stage ring) fit in one
+  // round of two workgroups per CU and 128 x 128 tiles would need a second,
+  // the 192 x 128 tile with its registers capped at 128 (4 waves per SIMD,
+  // so two workgroups fit on a CU): 1.5B gate/up at 1024 rows, 420 tiles
+  // against 560 of 128 x 128 on 512 slots, 43.7 vs 47.0 us.
+  if (p.n > 2048 && p.rows >= 1024 && p.k <= 4096) {
+    const int64_t cols = (p.n + 127) / 128;
+    const int64_t t192 = (p.rows + 191) / 192 * cols, t128x128 = (p.rows + 127) / 128 * cols;
+    if (t192 <= 2 * static_cast<int64_t>(cus) && t128x128 > 2 * static_cast<int64_t>(cus))
+      return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, tiled::EPI_W8, 1, 4>(p, s);
     return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(p, s);
+  }
   // Below 1024 rows, wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring
   // (2 stages) at the shape whose busiest CU finishes first -- ceil(tiles /
   // CUs) times the cost of one tile of 128 x 64 (4 waves, 40 KiB of LDS, four

@@ -4,6 +4,7 @@ HBM traffic through the copy-probe calibration), and the one-GPU contract."""
 import csv
 import importlib
 import importlib.util
+import re
 import subprocess
 import sys
 from pathlib import Path
@@ -38,6 +39,20 @@ def test_every_prefill_gemm_launch_carries_its_flops(bench):
     for (frag, grid), v in bench.KNOWN_LAUNCHES.items():
         if frag.startswith("tiled_gemm<"):
             assert len(v) == 3 and v[2] > 0, frag
+
+
+def test_tiled_gemm_fragments_name_every_template_argument(bench):
+    # the trace matches a fragment as a substring of the demangled kernel name,
+    # which lists every template argument, defaulted ones included: a fragment
+    # short of the kernel's arity matches nothing
+    src = (ROOT / "llm-inference-optimizer_amd" / "csrc" / "tiled_gemm.h").read_text()
+    decl = re.search(r"template <([^>]*)>\s*__global__[^\n]*\n[^\n]*tiled_gemm\(", src)
+    assert decl, "tiled_gemm kernel declaration not found"
+    arity = len(decl.group(1).split(","))
+    frags = [frag for frag, _ in bench.KNOWN_LAUNCHES if frag.startswith("tiled_gemm<")]
+    assert frags
+    for frag in frags:
+        assert len(frag[len("tiled_gemm<"):-1].split(",")) == arity, frag
 
 
 def _write(path, rows):

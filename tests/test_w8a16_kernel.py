@@ -145,11 +145,14 @@ TILED_CASES = [
     # n > 2048 below 1024 rows with >= 2 tiles of 128 x 64 per CU: the sub-step ring
     (512, 512, 8960, F16, False),     # 128 x 64, 4 waves (main loop and k tail)
     # n > 2048 from 1024 rows, k <= 4096: 128 x 128 tiles of 8 waves, 3-stage ring
-    (1024, 272, 8960, BF16, False),
     (2048, 128, 8952, F16, False),    # ragged n
     (4096, 64, 8960, F16, True),
     (4096, 80, 9000, BF16, True),     # ragged n, k tail only
     (4096, 32, 3584, BF16, True),
+    # ... except where 192 x 128 tiles fit in one round of two workgroups per
+    # CU and 128 x 128 tiles do not: 192 x 128, registers capped at 128
+    (1024, 272, 8960, BF16, False),   # 420 tiles
+    (1200, 400, 8000, F16, True),     # 441 tiles: ragged rows and n, k tail
     # (the 256 x 128 and 256 x 256 sub-step rings, now taken only at k > 4096,
     # are checked bit for bit against this library by the w8_tile_cfg2 / 3
     # variants in test_launch_variants.py)
