@@ -160,13 +160,13 @@ VARIANTS = {
     "w8_skinny_sweep_pipe": ("w8a16", ["-DMI355_W8_SWEEP", "-DMI355_W8_PIPE=1"]),
     # W8A16 tiled GEMM: one tile configuration for every prefill launch
     # (MI355_W8_FORCE in w8a16.hip lists them)
-    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 40)},
+    **{f"w8_tile_cfg{i}": ("w8a16", [f"-DMI355_W8_FORCE={i}"]) for i in range(1, 43)},
     # 192 x 128 tiles of 8 waves squeezed to 4 waves per SIMD (two
     # workgroups per CU; a few VGPRs spill)
     "w8_tile_cfg37_wpe4": ("w8a16", ["-DMI355_W8_FORCE=37", "-DMI355_TILED_MIN_WAVES_PER_SIMD=4"]),
     # W8A16 gate/up + SiLU-and-mul tiled GEMM above 256 rows: one tile
     # configuration for every launch (MI355_W8_DUAL_FORCE in w8a16.hip)
-    **{f"w8_dual_cfg{i}": ("w8a16", [f"-DMI355_W8_DUAL_FORCE={i}"]) for i in range(1, 8)},
+    **{f"w8_dual_cfg{i}": ("w8a16", [f"-DMI355_W8_DUAL_FORCE={i}"]) for i in range(1, 9)},
     # RMSNorm: keep the row's fp32 widening live between the two passes
     # instead of re-widening the packed row (more VGPRs, fewer conversions),
     # per kernel: the shipped choice is the wave kernel re-widening and the

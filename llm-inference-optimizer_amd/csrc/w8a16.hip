@@ -655,8 +655,11 @@ int w8_tiled_forced(const W8Params& p, hipStream_t s) {
     // 192-row tiles: fewer rounds of tiles at 1024 and 4096 rows
     case 37: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 2 stages
     case 38: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 3, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 3 stages
-    // 192 x 128, 8 waves of 96 x 32, ring, 2 stages, registers capped for 4 waves per SIMD (two workgroups per CU)
-    default: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1, 4>(p, s);
+    // registers capped for more workgroups per CU (the last template argument: waves per SIMD)
+    case 39: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1, 4>(p, s);  // 192 x 128, 8 waves, ring, 2 stages; 2 per CU
+    case 40: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_W8, 1, 6>(p, s);  // 128 x 128, 8 waves, ring, 2 stages; 3 per CU
+    case 41: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, EPI_W8, 1, 4>(p, s);  // 256 x 128, 8 waves, ring, 2 stages; 2 per CU
+    default: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 2, EPI_W8, 1, 4>(p, s);  // 128 x 256, 8 waves of 64 x 64, ring, 2 stages; 2 per CU
   }
 }
 
@@ -748,7 +751,9 @@ int w8_tiled_dual_forced(const W8Params& p, hipStream_t s) {
     case 4: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 3 stages
     case 5: return w8_tiled_cfg<T, TO, 4, 2, 1, 2, 2, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 32 x 64, ring, 2 stages
     case 6: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 3, EPI_SILU_W8, 1>(p, s);  // 128 x 64, 4 waves, ring, 3 stages
-    default: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_SILU_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
+    case 7: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_SILU_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
+    // registers capped for 4 waves per SIMD: 128 x 128, 8 waves of 64 x 32, ring, 2 stages, two workgroups per CU
+    default: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_SILU_W8, 1, 4>(p, s);
   }
 }
 
