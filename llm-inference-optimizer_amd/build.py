@@ -166,7 +166,7 @@ VARIANTS = {
     "w8_tile_cfg37_wpe4": ("w8a16", ["-DMI355_W8_FORCE=37", "-DMI355_TILED_MIN_WAVES_PER_SIMD=4"]),
     # W8A16 gate/up + SiLU-and-mul tiled GEMM above 256 rows: one tile
     # configuration for every launch (MI355_W8_DUAL_FORCE in w8a16.hip)
-    **{f"w8_dual_cfg{i}": ("w8a16", [f"-DMI355_W8_DUAL_FORCE={i}"]) for i in range(1, 9)},
+    **{f"w8_dual_cfg{i}": ("w8a16", [f"-DMI355_W8_DUAL_FORCE={i}"]) for i in range(1, 12)},
     # RMSNorm: keep the row's fp32 widening live between the two passes
     # instead of re-widening the packed row (more VGPRs, fewer conversions),
     # per kernel: the shipped choice is the wave kernel re-widening and the

@@ -753,7 +753,10 @@ int w8_tiled_dual_forced(const W8Params& p, hipStream_t s) {
     case 6: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 3, EPI_SILU_W8, 1>(p, s);  // 128 x 64, 4 waves, ring, 3 stages
     case 7: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_SILU_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
     // registers capped for 4 waves per SIMD: 128 x 128, 8 waves of 64 x 32, ring, 2 stages, two workgroups per CU
-    default: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_SILU_W8, 1, 4>(p, s);
+    case 8: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_SILU_W8, 1, 4>(p, s);
+    case 9: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 3, EPI_SILU_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 3 stages
+    case 10: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 2, EPI_SILU_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 2 stages
+    default: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4, EPI_SILU_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 4 stages
   }
 }
 
