@@ -998,6 +998,10 @@ W8_SKINNY_SWEEP_SHAPES = [
     (8, 1536, 8960, "f16", "gateup1.5b"), (1, 1536, 8960, "f16", "gateup1.5b"),
     (8, 1536, 1536, "f16", "o1.5b"),
     (8, 18944, 3584, "bf16", "down7b"), (8, 3584, 18944, "bf16", "gateup7b"),
+    # 1-row 7B projections and the 7B o and 0.5B down projections
+    (1, 18944, 3584, "bf16", "down7b"), (1, 3584, 18944, "bf16", "gateup7b"),
+    (1, 3584, 3584, "bf16", "o7b"), (8, 3584, 3584, "bf16", "o7b"),
+    (1, 4864, 896, "f16", "down0.5b"), (8, 4864, 896, "f16", "down0.5b"),
 ]
 
 

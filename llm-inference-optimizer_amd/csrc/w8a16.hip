@@ -448,7 +448,8 @@ namespace {
 //     the CU's 4 SIMDs carry equal loads (7 waves on 224 CUs: 1.22x slower
 //     than 8);
 //   U (blocks in flight per wave) = 1, or 2 for narrow outputs (n <= 1536,
-//     few workgroups) whose waves own 2 or more blocks.
+//     few workgroups) whose waves own 2 or more blocks -- then, with one row
+//     and one workgroup per CU, at most 12 waves.
 template <typename T, typename TO, int MT, int G, bool DUAL>
 int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   constexpr int NQ = DUAL ? 2 : 1;
@@ -477,7 +478,18 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   } else {
     split = (nblk + bpw - 1) / bpw;  // even blocks per wave
   }
-  if (u == 0) u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
+  if (u == 0) {
+    u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
+    // One row, one workgroup per CU, 2 blocks in flight per wave: at most 12
+    // waves (a graph-timed sweep of the Qwen2.5-1.5B and 0.5B down
+    // projections at one row: k = 8960, 12 waves 5.99 us against 6.72 us
+    // for 16; k = 4864, 4.76 against 4.86; with 1 block in flight 16 waves
+    // stay ahead at every 1-row shape swept).
+    if (p.rows <= 1 && u == 2 && units <= cus && split > 12) {
+      split = 12;
+      bpw = (nblk + split - 1) / split;
+    }
+  }
   dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
 #ifdef MI355_W8_SWEEP
   W8Params ps = p;

@@ -119,7 +119,7 @@ def test_kernel_matches_dequantized_reference(pkg, orc, cuda, K, N, M, bias):
 
 @pytest.mark.parametrize("M,K,N,bias", [(1, 1536, 8960, False), (8, 3584, 512, True), (24, 896, 4864, True),
                                         (32, 1536, 256, False), (64, 1536, 1536, True), (300, 640, 200, False),
-                                        (5, 100, 37, True)])
+                                        (5, 100, 37, True), (1, 4864, 896, True)])
 def test_bf16_matches_oracle(pkg, orc, cuda, M, K, N, bias):
     lin = _linear(K, N, bias, cuda, dtype=BF16, seed=M)
     q = pkg.QuantizedLinearInt8.from_linear(lin)
