@@ -454,36 +454,36 @@ KNOWN_LAUNCHES = {
     # MFMA-bound prefill GEMMs: (label, algorithmic bytes, flops)
     # (the 1.5B gate/up at 1024 and 4096 rows runs as a column split: whole
     # rounds of 256 x 128 tiles over the first 8192 columns, then 768 columns)
-    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 4, 4, 1, 1, 2, 1, 0>", 256 * 512): (
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 4, 4, 1, 1, 2, 1, 0, 0>", 256 * 512): (
         "gate/up + SiLU-and-mul prefill, 1024 rows, first 8192 of 8960 columns, fp16",
         2 * 8192 * 1536 * 2 + 1024 * 1536 * 2 + 1024 * 8192 * 2, 4 * 1024 * 1536 * 8192),
-    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 2, 1, 1, 1, 4, 0, 0>", 192 * 256): (
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 2, 1, 1, 1, 4, 0, 0, 0>", 192 * 256): (
         "gate/up + SiLU-and-mul prefill, 1024 rows, last 768 of 8960 columns, fp16",
         2 * 768 * 1536 * 2 + 1024 * 1536 * 2 + 1024 * 768 * 2, 4 * 1024 * 1536 * 768),
-    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 4, 4, 1, 1, 2, 1, 0>", 1024 * 512): (
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 4, 4, 1, 1, 2, 1, 0, 0>", 1024 * 512): (
         "gate/up + SiLU-and-mul prefill, 4096 rows, first 8192 of 8960 columns, fp16",
         2 * 8192 * 1536 * 2 + 4096 * 1536 * 2 + 4096 * 8192 * 2, 4 * 4096 * 1536 * 8192),
-    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 2, 2, 1, 1, 2, 1, 0>", 384 * 256): (
+    ("tiled_gemm<mi355::F16, 0, mi355::F16, 2, 2, 2, 1, 1, 2, 1, 0, 0>", 384 * 256): (
         "gate/up + SiLU-and-mul prefill, 4096 rows, last 768 of 8960 columns, fp16",
         2 * 768 * 1536 * 2 + 4096 * 1536 * 2 + 4096 * 768 * 2, 4 * 4096 * 1536 * 768),
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 2, 1, 0, 2, 1, 0>", 1120 * 256): (
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 2, 1, 0, 2, 1, 0, 0>", 1120 * 256): (
         "W8A16 prefill gate/up, 1024 rows, [8960,1536] int8, fp16",
         8960 * 1536 + 4 * 8960 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 2 * 1024 * 1536 * 8960),
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4, 0, 0>", 384 * 256): (
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 2, 1, 1, 0, 4, 0, 0, 0>", 384 * 256): (
         "W8A16 prefill down, 1024 rows, [1536,8960] int8, fp16",
         1536 * 8960 + 4 * 1536 + 1024 * 8960 * 2 + 1024 * 1536 * 2, 2 * 1024 * 8960 * 1536),
     # narrow outputs filling half to all of the CUs: 64 x 128 tiles of 8 waves (the
     # 1024-row q/o projection launches the same grid; its launches mix into this row)
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 1, 1, 0, 4, 1, 0>", 192 * 512): (
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 1, 1, 0, 4, 1, 0, 0>", 192 * 512): (
         "W8A16 prefill down, 1024 rows, [1536,8960] int8, fp16 (64x128 tiles)",
         1536 * 8960 + 4 * 1536 + 1024 * 8960 * 2 + 1024 * 1536 * 2, 2 * 1024 * 8960 * 1536),
     # the wide-output plan from 1024 rows: 128 x 128 tiles of 8 waves, 3-stage ring
     # (at 1024 rows its 560 tiles would take two rounds of 512 slots: there the
     # 192 x 128 tile of 8 waves, registers capped for two workgroups per CU)
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 3, 1, 0, 2, 1, 4>", 420 * 512): (
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 3, 1, 0, 2, 1, 4, 1>", 420 * 512): (
         "W8A16 prefill gate/up, 1024 rows, [8960,1536] int8, fp16 (192x128 tiles)",
         8960 * 1536 + 4 * 8960 + 1024 * 1536 * 2 + 1024 * 8960 * 2, 2 * 1024 * 1536 * 8960),
-    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 2, 1, 0, 3, 1, 0>", 2240 * 512): (
+    ("tiled_gemm<mi355::F16, 1, mi355::F16, 2, 4, 2, 1, 0, 3, 1, 0, 0>", 2240 * 512): (
         "W8A16 prefill gate/up, 4096 rows, [8960,1536] int8, fp16 (128x128 tiles)",
         8960 * 1536 + 4 * 8960 + 4096 * 1536 * 2 + 4096 * 8960 * 2, 2 * 4096 * 1536 * 8960),
 }

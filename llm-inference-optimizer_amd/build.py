@@ -147,6 +147,10 @@ VARIANTS = {
     # W8A16 tiled GEMM (prefill rows): widen each sub-step's int8 weights right
     # before its own MFMAs instead of one sub-step ahead
     "tiled_widen_in_place": ("w8a16", ["-DMI355_TILED_WIDEN_AHEAD=0"]),
+    # W8A16 tiled GEMM: the configuration with XCD ranges for any tile count
+    # (192 x 128, registers capped) keeps the dispatch order when the count
+    # is not a multiple of 8
+    "w8_xcd_dispatch_order": ("w8a16", ["-DMI355_TILED_XCD_RAGGED=0"]),
     # W8A16 tiled GEMM: an L2 prefetch wave per workgroup, 2 / 4 / 8 K steps
     # past the LDS ring
     "tiled_prefetch2": ("w8a16", ["-DMI355_TILED_PREFETCH=2"]),

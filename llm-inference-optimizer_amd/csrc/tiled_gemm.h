@@ -69,7 +69,8 @@
 // Grid: one workgroup per tile, 1-D.  Consecutive workgroup ids land on
 // different XCDs (round robin over 8), so ids are remapped to give each XCD
 // a contiguous range of tiles, ordered in groups of group_m m-blocks, m
-// fastest: the x row blocks that share a weight block run on one XCD.
+// fastest: the x row blocks that share a weight block run on one XCD (tile
+// counts that are not a multiple of 8: see XR below).
 #pragma once
 
 #include <type_traits>
@@ -237,6 +238,13 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc
 #define MI355_TILED_WIDEN_AHEAD 1
 #endif
 
+// MI355_TILED_XCD_RAGGED = 0: the configurations compiled with XR = 1 (below)
+// keep the dispatch order for tile counts that are not a multiple of 8 as
+// well (a measurement switch for variant builds).
+#ifndef MI355_TILED_XCD_RAGGED
+#define MI355_TILED_XCD_RAGGED 1
+#endif
+
 // MI355_TILED_MIN_WAVES_PER_SIMD = w > 0: every tiled kernel is compiled to
 // fit w waves per SIMD (at most 512 / w registers a lane), so register-heavy
 // tiles can run two workgroups per CU (a measurement switch for variant
@@ -252,8 +260,13 @@ constexpr int kMinWavesPerSimd = WPE > 0 ? WPE : (MI355_TILED_MIN_WAVES_PER_SIMD
 
 // WPE > 0 caps the registers of this configuration alone so that WPE waves fit
 // on each SIMD (a 192 x 128 tile of 8 waves at WPE = 4 fits in 128 VGPRs and
-// runs two workgroups per CU).
-template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0, int WPE = 0>
+// runs two workgroups per CU).  XR = 1 gives the XCDs contiguous tile ranges
+// when the tile count is not a multiple of 8 too (the first count mod 8 XCDs,
+// which receive one workgroup more, take ranges one tile longer); XR = 0
+// keeps the dispatch order for such counts.  (XR is a template argument so
+// that the configurations without it keep their code.)
+template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0, int WPE = 0,
+          int XR = 0>
 __global__ __launch_bounds__(64 * WGM * WGN + (MI355_TILED_PREFETCH > 0 ? 64 : 0))
 __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
@@ -268,7 +281,13 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
   // Tile of this workgroup: contiguous ranges per XCD, m fastest.
   const int ntiles = p.tiles_m * p.tiles_n;
   int b = blockIdx.x;
-  if ((ntiles & 7) == 0) b = (b & 7) * (ntiles >> 3) + (b >> 3);
+  if constexpr (XR != 0 && MI355_TILED_XCD_RAGGED != 0) {
+    // XCD x = b % 8 runs ids x, x + 8, ...: ceil((ntiles - x) / 8) of them
+    const int q = ntiles >> 3, r = ntiles & 7, x = b & 7;
+    b = x * q + (x < r ? x : r) + (b >> 3);
+  } else {
+    if ((ntiles & 7) == 0) b = (b & 7) * (ntiles >> 3) + (b >> 3);
+  }
   // inside the range: groups of group_m m-blocks, m fastest within a group
   const int per_group = p.group_m * p.tiles_n;
   const int g0 = (b / per_group) * p.group_m;

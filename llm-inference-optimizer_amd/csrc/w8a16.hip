@@ -572,7 +572,7 @@ bool tiled_fits(const W8Params& p, bool) {
 }
 
 template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8, int RING = 0,
-          int WPE = 0>
+          int WPE = 0, int XR = 0>
 int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_I8, TO, WGM, WGN, FM, FN, EPI, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
@@ -598,7 +598,7 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
-                                                                                      EPI, S, RING, WPE>),
+                                                                                      EPI, S, RING, WPE, XR>),
                                     dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::BLOCK), args, 0, s),
                     "w8a16 tiled launch");
 }
@@ -668,7 +668,7 @@ int w8_tiled_forced(const W8Params& p, hipStream_t s) {
     case 37: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 2 stages
     case 38: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 3, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 3 stages
     // registers capped for more workgroups per CU (the last template argument: waves per SIMD)
-    case 39: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1, 4>(p, s);  // 192 x 128, 8 waves, ring, 2 stages; 2 per CU
+    case 39: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1, 4, 1>(p, s);  // 192 x 128, 8 waves, ring, 2 stages; 2 per CU
     case 40: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_W8, 1, 6>(p, s);  // 128 x 128, 8 waves, ring, 2 stages; 3 per CU
     case 41: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, EPI_W8, 1, 4>(p, s);  // 256 x 128, 8 waves, ring, 2 stages; 2 per CU
     default: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 2, EPI_W8, 1, 4>(p, s);  // 128 x 256, 8 waves of 64 x 64, ring, 2 stages; 2 per CU
@@ -692,12 +692,14 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
   // round of two workgroups per CU and 128 x 128 tiles would need a second,
   // the 192 x 128 tile with its registers capped at 128 (4 waves per SIMD,
   // so two workgroups fit on a CU): 1.5B gate/up at 1024 rows, 420 tiles
-  // against 560 of 128 x 128 on 512 slots, 43.7 vs 47.0 us.
+  // against 560 of 128 x 128 on 512 slots, 43.0 vs 46.8 us.  Its tile counts
+  // here are rarely multiples of 8, so it gives the XCDs contiguous tile
+  // ranges for any count (XR = 1; 43.2 vs 44.4 us at 420 tiles).
   if (p.n > 2048 && p.rows >= 1024 && p.k <= 4096) {
     const int64_t cols = (p.n + 127) / 128;
     const int64_t t192 = (p.rows + 191) / 192 * cols, t128x128 = (p.rows + 127) / 128 * cols;
     if (t192 <= 2 * static_cast<int64_t>(cus) && t128x128 > 2 * static_cast<int64_t>(cus))
-      return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, tiled::EPI_W8, 1, 4>(p, s);
+      return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, tiled::EPI_W8, 1, 4, 1>(p, s);
     return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(p, s);
   }
   // Below 1024 rows, wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring
