@@ -571,6 +571,13 @@ bool tiled_fits(const W8Params& p, bool) {
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
+// MI355_W8_GROUP_M: m-blocks per group of the tiled GEMM's tile order inside
+// each XCD's range (m fastest within a group; a measurement switch for
+// variant builds).
+#ifndef MI355_W8_GROUP_M
+#define MI355_W8_GROUP_M 4
+#endif
+
 template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8, int RING = 0,
           int WPE = 0, int XR = 0>
 int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
@@ -594,7 +601,7 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   tp.bdt = p.bdt;
   tp.tiles_m = (p.rows + C::BM - 1) / C::BM;
   tp.tiles_n = (p.n + C::BN - 1) / C::BN;
-  tp.group_m = tp.tiles_m < 4 ? tp.tiles_m : 4;
+  tp.group_m = tp.tiles_m < MI355_W8_GROUP_M ? tp.tiles_m : MI355_W8_GROUP_M;
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
