@@ -72,7 +72,8 @@ def parse_args():
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
-                                      "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow"],
+                                      "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
+                                      "gate-up-prefill-sweep"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -862,6 +863,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES[1:3], baselines=False)))
+    elif args.only == "gate-up-prefill-sweep":  # every prefill row count of the MLP table, with the unfused chain
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SWEEP_SHAPES)))
     elif args.only in ("w8a16-prefill-wide", "w8a16-prefill-narrow"):  # prefill rows, kernel only
         del sets
         torch.cuda.empty_cache()
@@ -1344,6 +1349,11 @@ def bench_gate_up(ctx, shapes=GATE_UP_SHAPES, iters=400, baselines=True):
 # (rows, k, n_out, dtype name, label): prefill batches of Qwen2.5-1.5B and -7B MLPs
 GATE_UP_PREFILL_SHAPES = [(128, 1536, 8960, "f16", "qwen2.5-1.5b"), (1024, 1536, 8960, "f16", "qwen2.5-1.5b"),
                           (4096, 1536, 8960, "f16", "qwen2.5-1.5b"), (4096, 3584, 18944, "bf16", "qwen2.5-7b")]
+# the Qwen2.5-0.5B, 1.5B and 7B MLPs over prefill row counts (--only gate-up-prefill-sweep)
+GATE_UP_PREFILL_SWEEP_SHAPES = (
+    [(m, 1536, 8960, "f16", "qwen2.5-1.5b") for m in (64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096)]
+    + [(m, 3584, 18944, "bf16", "qwen2.5-7b") for m in (256, 512, 1024, 1536, 1792, 2048, 4096)]
+    + [(m, 896, 4864, "bf16", "qwen2.5-0.5b") for m in (256, 1024, 4096)])
 
 
 def bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SHAPES, iters=60, baselines=True):

@@ -151,6 +151,10 @@ VARIANTS = {
     # (192 x 128, registers capped) keeps the dispatch order when the count
     # is not a multiple of 8
     "w8_xcd_dispatch_order": ("w8a16", ["-DMI355_TILED_XCD_RAGGED=0"]),
+    "gate_up_xcd_dispatch_order": ("gate_up_silu", ["-DMI355_TILED_XCD_RAGGED=0"]),
+    # 16-bit gate/up + SiLU-and-mul: the column split's whole rounds cut at
+    # 128-column blocks of every row block
+    "gate_up_rounds_by_columns": ("gate_up_silu", ["-DMI355_GU_ROUNDS_BY_COLUMNS=1"]),
     # W8A16 tiled GEMM: m-blocks per group of the tile order (default 4)
     **{f"w8_group_m{g}": ("w8a16", [f"-DMI355_W8_GROUP_M={g}"]) for g in (1, 2, 8, 16, 64)},
     # W8A16 tiled GEMM: an L2 prefetch wave per workgroup, 2 / 4 / 8 K steps

@@ -230,7 +230,14 @@ int gate_up_shape(const GateUpParams& p, hipStream_t s) {
   return gate_up_launch_tiles<T, TO, MT, 4, 2, 2>(p, s);
 }
 
-template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int RING = 0>
+// MI355_GU_ROUNDS_BY_COLUMNS = 1: the column split's whole rounds hold only
+// whole 128-column blocks of every row block (cus / row blocks of them per
+// round; a measurement switch for variant builds).
+#ifndef MI355_GU_ROUNDS_BY_COLUMNS
+#define MI355_GU_ROUNDS_BY_COLUMNS 0
+#endif
+
+template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int RING = 0, int XR = 0>
 int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_16, TO, WGM, WGN, FM, FN, tiled::EPI_SILU, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
@@ -253,7 +260,7 @@ int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_16, TO, WGM, WGN, FM, FN,
-                                                                                      tiled::EPI_SILU, S, RING>),
+                                                                                      tiled::EPI_SILU, S, RING, 0, XR>),
                                     dim3(static_cast<unsigned>(tp.tiles_m * tp.tiles_n)), dim3(C::BLOCK), args, 0, s),
                     "gate_up_silu tiled launch");
 }
@@ -293,7 +300,11 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
   // waves, 0.8), 128 x 64 (4 waves, 4 stages, 1.0), 128 x 64 on the ring
   // (two per CU, 1.05) or 256 x 64 (1.0) -- so a last, thinly filled round
   // of large tiles becomes a full round of small ones (1.5B, 1024 rows
-  // 80.5 -> 64.6 us).  The split is two launches of one kernel on column
+  // 80.5 -> 64.6 us).  The whole rounds are counted in tiles, not in
+  // 128-column blocks per round: with 6 row blocks, 3 rounds on 256 CUs hold
+  // 128 column blocks, where 3 x 42 blocks of whole columns per round left 4
+  // CUs idle each round and the rest too wide for one round of small tiles
+  // (7B, 1536 rows: 368 -> 355 us).  The split is two launches of one kernel on column
   // ranges: every output element sums its k products in the same order
   // either way.  Weights are the measured per-round times at Qwen2.5-1.5B
   // and 7B shapes; ties keep the single launch, then 256 x 64.
@@ -308,10 +319,26 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
                c128 = 1.72 * rounds(p.rows, p.n_out, 256, 128, 1);
   const double single = c64 < c_small ? (c64 < c128 ? c64 : c128) : (c_small < c128 ? c_small : c128);
 
-  const int64_t per_round = cus / cdiv(p.rows, 256);  // 128-column blocks of one whole round
+  // 256 x 128 tiles; a tile count that is not a multiple of 8 still gets
+  // contiguous tile ranges per XCD (XR; 1.5B at 768 rows, 210 tiles, 49.0 ->
+  // 46.3 us; at 1536 rows, 420 tiles, 93.6 -> 90.5 us)
+  const auto big_tiles = [&](const GateUpParams& q) {
+    if (cdiv(q.rows, 256) * cdiv(q.n_out, 128) % 8 != 0) return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1, 1>(q, s);
+    return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(q, s);
+  };
+  // whole rounds of 256 x 128 tiles, and the 128-column blocks that fill
+  // them (a round need not end at a column boundary: the head launch's
+  // tiles fill its rounds in order)
+  const int64_t tiles_m = cdiv(p.rows, 256);
+#if MI355_GU_ROUNDS_BY_COLUMNS
+  const int64_t per_round = cus / tiles_m;  // 128-column blocks of one whole round
   const int64_t full = per_round > 0 ? cdiv(p.n_out, 128) / per_round : 0;
-  const int lead = static_cast<int>(full * per_round * 128);  // columns in whole rounds
-  if (full >= 1 && lead < p.n_out) {
+  const int lead = static_cast<int>(full * per_round * 128);
+#else
+  const int64_t full = cdiv(p.n_out, 128) * tiles_m / cus;
+  const int lead = static_cast<int>(full * cus / tiles_m * 128);  // columns in whole rounds
+#endif
+  if (full >= 1 && lead > 0 && lead < p.n_out) {
     const int rest = p.n_out - lead;
     const auto one_round = [&](int bm, int bn, int per_cu) { return rounds(p.rows, rest, bm, bn, per_cu) <= 1.0; };
     int shape = 0;
@@ -328,7 +355,7 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
       tail.wg = static_cast<const uint8_t*>(p.wg) + wskip;
       tail.wu = static_cast<const uint8_t*>(p.wu) + wskip;
       tail.out = static_cast<uint8_t*>(p.out) + static_cast<int64_t>(lead) * static_cast<int64_t>(sizeof(typename TO::bits));
-      const int r = gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(head, s);
+      const int r = big_tiles(head);
       if (r != MI355_OK) return r;
       if (shape == 1) return gate_up_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(tail, s);
       if (shape == 2) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(tail, s);
@@ -338,7 +365,7 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
   }
   if (c64 == single) return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(p, s);
   if (c_small == single) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 2, 1>(p, s);
-  return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(p, s);
+  return big_tiles(p);
 }
 
 template <typename T, typename TO>

@@ -196,6 +196,9 @@ def test_large_shape_against_torch_fp64(pkg, cuda):
     # then 256 x 128 tiles, then a column split (6528 columns in 256 x 128
     # tiles, the last 72 in 64 x 64)
     (300, 264, 8200, BF16), (520, 264, 8000, F16), (1030, 264, 6600, F16),
+    # whole rounds that end inside a 128-column block: 768 tiles of 256 x 128
+    # over 16384 columns (6 row blocks), then 2560 columns of 128 x 64 tiles
+    (1536, 264, 18944, BF16),
 ])
 def test_prefill_shapes_against_torch_fp64(pkg, cuda, rows, k, n, dt):
     """Prefill-sized batches (the tiled GEMM path) against fp64 GEMMs on the

@@ -208,6 +208,41 @@ def test_w8a16_dual_variant_is_bitwise_the_default(name, cuda):
         assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, rows, k, n, dt)
 
 
+GATE_UP_VARIANTS = _variants_of("gate_up_silu")
+# 16-bit gate/up + SiLU-and-mul at prefill rows whose 256 x 128 tile counts
+# are not multiples of 8 (420, 189, 210 tiles), the 1.5B MLP at 1024 rows
+# (the column split), and a column split whose whole rounds end inside a
+# 128-column block (6 row blocks x 18944 columns)
+GATE_UP_SHAPES = [(1536, 1536, 8960, torch.float16), (520, 264, 8000, torch.float16),
+                  (768, 512, 8960, torch.bfloat16), (1024, 1536, 8960, torch.float16),
+                  (1536, 264, 18944, torch.bfloat16)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", GATE_UP_VARIANTS)
+def test_gate_up_variant_is_bitwise_the_default(name, cuda):
+    """16-bit gate/up + SiLU-and-mul variants (the tile order over the XCDs,
+    the column split's cut): every output element sums its k products in the
+    same order, so the same bits as the default library."""
+    lib = _variant(name)
+    ref_lib = L.load()
+    c = L.DTYPE_CODE
+    for i, (rows, k, n, dt) in enumerate(GATE_UP_SHAPES):
+        print(f"variant {name}: gate/up rows={rows} k={k} n={n} {dt}", flush=True)
+        x = torch.randn(rows, k, generator=_gen(2300 + i)).to(dt).to(cuda)
+        wg = (torch.randn(n, k, generator=_gen(2400 + i)) * 0.05).to(dt).to(cuda)
+        wu = (torch.randn(n, k, generator=_gen(2500 + i)) * 0.05).to(dt).to(cuda)
+        outs = []
+        for lb in (ref_lib, lib):
+            o = torch.full((rows, n), float("nan"), dtype=dt, device=cuda)
+            st = lb.mi355_gate_up_silu_fwd(x.data_ptr(), wg.data_ptr(), wu.data_ptr(), o.data_ptr(), rows, k, n,
+                                           k, k, n, c[dt], c[dt], abi_stream())
+            assert st == 0, lb.mi355_last_error().decode()
+            torch.cuda.synchronize()
+            outs.append(o)
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (name, rows, k, n, dt)
+
+
 # Forced skinny shapes of the sweep build: (G, waves, U, KS).  KS > 1 splits K
 # over workgroups (partial sums through device memory, added by the last
 # workgroup to arrive in workgroup order).
