@@ -155,6 +155,9 @@ VARIANTS = {
     # 16-bit gate/up + SiLU-and-mul: the column split's whole rounds cut at
     # 128-column blocks of every row block
     "gate_up_rounds_by_columns": ("gate_up_silu", ["-DMI355_GU_ROUNDS_BY_COLUMNS=1"]),
+    # 16-bit gate/up + SiLU-and-mul: the column split's rest in one shape
+    # (4: 256 x 64; 5: 128 x 128 of 8 waves) whenever it fits one round
+    **{f"gate_up_rest_shape{f}": ("gate_up_silu", [f"-DMI355_GU_REST_SHAPE={f}"]) for f in (4, 5)},
     # W8A16 tiled GEMM: m-blocks per group of the tile order (default 4)
     **{f"w8_group_m{g}": ("w8a16", [f"-DMI355_W8_GROUP_M={g}"]) for g in (1, 2, 8, 16, 64)},
     # W8A16 tiled GEMM: an L2 prefetch wave per workgroup, 2 / 4 / 8 K steps

@@ -236,6 +236,12 @@ int gate_up_shape(const GateUpParams& p, hipStream_t s) {
 #ifndef MI355_GU_ROUNDS_BY_COLUMNS
 #define MI355_GU_ROUNDS_BY_COLUMNS 0
 #endif
+// MI355_GU_REST_SHAPE = f > 0: the column split's remaining columns take
+// shape f of the plan below whenever it covers them in one round (a
+// measurement switch for variant builds).
+#ifndef MI355_GU_REST_SHAPE
+#define MI355_GU_REST_SHAPE 0
+#endif
 
 template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int RING = 0, int XR = 0>
 int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
@@ -347,6 +353,14 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
     else if (one_round(128, 64, 1)) shape = 2, rest_cost = 1.0;
     else if (one_round(128, 64, 2)) shape = 3, rest_cost = 1.05;
     else if (one_round(256, 64, 1)) shape = 4, rest_cost = 1.0;
+#if MI355_GU_REST_SHAPE > 0
+    {
+      // measurement switch: the rest in shape MI355_GU_REST_SHAPE when it fits one round
+      // (5: 128 x 128, 8 waves, 3-stage step pipeline)
+      constexpr int f = MI355_GU_REST_SHAPE;
+      if (shape != 0 && one_round(f == 1 ? 64 : (f == 4 ? 256 : 128), f == 5 ? 128 : 64, f == 3 ? 2 : 1)) shape = f;
+    }
+#endif
     if (shape != 0 && 1.72 * static_cast<double>(full) + rest_cost < single) {
       GateUpParams head = p, tail = p;
       head.n_out = lead;
@@ -360,6 +374,9 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
       if (shape == 1) return gate_up_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(tail, s);
       if (shape == 2) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(tail, s);
       if (shape == 3) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 2, 1>(tail, s);
+#if MI355_GU_REST_SHAPE > 0
+      if (shape == 5) return gate_up_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(tail, s);
+#endif
       return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(tail, s);
     }
   }
