@@ -73,7 +73,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep"],
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -867,10 +867,11 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_prefill(ctx, shapes=GATE_UP_PREFILL_SWEEP_SHAPES)))
-    elif args.only in ("w8a16-prefill-wide", "w8a16-prefill-narrow"):  # prefill rows, kernel only
+    elif args.only in ("w8a16-prefill-wide", "w8a16-prefill-narrow", "w8a16-prefill-ragged"):  # kernel only
         del sets
         torch.cuda.empty_cache()
-        shapes = W8A16_WIDE_PREFILL_SHAPES if args.only.endswith("wide") else W8A16_NARROW_PREFILL_SHAPES
+        shapes = {"wide": W8A16_WIDE_PREFILL_SHAPES, "narrow": W8A16_NARROW_PREFILL_SHAPES,
+                  "ragged": W8A16_RAGGED_PREFILL_SHAPES}[args.only.rsplit("-", 1)[1]]
         log(json.dumps(bench_w8a16(ctx, shapes=shapes, iters=100, baselines=False)))
     elif args.only in ("w8a16", "w8a16-decode", "w8a16-prefill", "w8a16-prefill-1.5b"):
         del sets
@@ -1404,7 +1405,10 @@ GATE_UP_W8_SHAPES = [(1, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 1536, 8960, "f1
                      (32, 1536, 8960, "f16", "qwen2.5-1.5b"), (8, 3584, 18944, "bf16", "qwen2.5-7b"),
                      (1024, 1536, 8960, "f16", "qwen2.5-1.5b")]
 GATE_UP_W8_PREFILL_SHAPES = [(1024, 1536, 8960, "f16", "qwen2.5-1.5b"), (4096, 1536, 8960, "f16", "qwen2.5-1.5b"),
-                             (1024, 3584, 18944, "bf16", "qwen2.5-7b"), (4096, 3584, 18944, "bf16", "qwen2.5-7b")]
+                             (1024, 3584, 18944, "bf16", "qwen2.5-7b"), (4096, 3584, 18944, "bf16", "qwen2.5-7b"),
+                             # row counts whose tile counts are not multiples of 8
+                             (1400, 1536, 8960, "f16", "qwen2.5-1.5b"), (2900, 1536, 8960, "f16", "qwen2.5-1.5b"),
+                             (1100, 3584, 18944, "bf16", "qwen2.5-7b")]
 
 
 def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300, baselines=True):
@@ -1477,6 +1481,12 @@ W8A16_NARROW_PREFILL_SHAPES = [(1024, 8960, 1536, "f16", "down proj"), (4096, 89
                                (768, 8960, 1536, "f16", "down proj"), (1280, 8960, 1536, "f16", "down proj"),
                                (512, 1536, 1536, "f16", "q/o proj"), (1024, 1536, 2048, "f16", "n 2048"),
                                (1024, 1536, 1024, "f16", "n 1024")]
+
+# W8A16 single GEMMs at prefill row counts whose tile counts are not multiples of 8
+W8A16_RAGGED_PREFILL_SHAPES = [(1400, 1536, 8960, "f16", "gate/up proj"), (2900, 1536, 8960, "f16", "gate/up proj"),
+                               (1100, 3584, 18944, "bf16", "7b gate/up proj"), (700, 1536, 8960, "f16", "gate/up proj"),
+                               (1300, 8960, 1536, "f16", "down proj"), (1900, 8960, 1536, "f16", "down proj"),
+                               (1100, 18944, 3584, "bf16", "7b down proj")]
 
 # (rows, k, n, dtype name, label): the MLP down projections of Qwen2.5-1.5B and -7B at decode rows
 LINEAR16_SHAPES = [(1, 8960, 1536, "f16", "qwen2.5-1.5b down"), (8, 8960, 1536, "f16", "qwen2.5-1.5b down"),

@@ -147,9 +147,8 @@ VARIANTS = {
     # W8A16 tiled GEMM (prefill rows): widen each sub-step's int8 weights right
     # before its own MFMAs instead of one sub-step ahead
     "tiled_widen_in_place": ("w8a16", ["-DMI355_TILED_WIDEN_AHEAD=0"]),
-    # W8A16 tiled GEMM: the configuration with XCD ranges for any tile count
-    # (192 x 128, registers capped) keeps the dispatch order when the count
-    # is not a multiple of 8
+    # W8A16 tiled GEMMs (single and gate/up + SiLU-and-mul): tile counts that
+    # are not a multiple of 8 keep the dispatch order instead of XCD ranges
     "w8_xcd_dispatch_order": ("w8a16", ["-DMI355_TILED_XCD_RAGGED=0"]),
     "gate_up_xcd_dispatch_order": ("gate_up_silu", ["-DMI355_TILED_XCD_RAGGED=0"]),
     # 16-bit gate/up + SiLU-and-mul: the column split's whole rounds cut at

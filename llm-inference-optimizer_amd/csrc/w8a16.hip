@@ -583,6 +583,16 @@ template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int 
 int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_I8, TO, WGM, WGN, FM, FN, EPI, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
+  // A tile count that is not a multiple of 8 takes the instantiation that
+  // gives the XCDs contiguous tile ranges for any count (XR = 1; the
+  // multiples of 8 keep the other, whose code predates it).  Prefill row
+  // counts are mostly not powers of two: 1.5B gate/up at 1400 rows (770
+  // tiles of 128 x 128) 66.1 -> 58.3 us, 2900 rows 112.0 -> 103.8 us, 7B
+  // gate/up at 1100 rows 179.2 -> 174.9 us; the narrow outputs even.
+  if constexpr (XR == 0) {
+    const int64_t ntiles = static_cast<int64_t>((p.rows + C::BM - 1) / C::BM) * ((p.n + C::BN - 1) / C::BN);
+    if (ntiles % 8 != 0) return w8_tiled_cfg<T, TO, WGM, WGN, FM, FN, S, EPI, RING, WPE, 1>(p, s);
+  }
   tiled::Params tp{};
   tp.x = p.x;
   tp.b0 = p.q;
@@ -699,9 +709,9 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
   // round of two workgroups per CU and 128 x 128 tiles would need a second,
   // the 192 x 128 tile with its registers capped at 128 (4 waves per SIMD,
   // so two workgroups fit on a CU): 1.5B gate/up at 1024 rows, 420 tiles
-  // against 560 of 128 x 128 on 512 slots, 43.0 vs 46.8 us.  Its tile counts
-  // here are rarely multiples of 8, so it gives the XCDs contiguous tile
-  // ranges for any count (XR = 1; 43.2 vs 44.4 us at 420 tiles).
+  // against 560 of 128 x 128 on 512 slots, 43.0 vs 46.8 us.  (Its tile
+  // counts here are rarely multiples of 8: XR below, 43.2 vs 44.4 us at 420
+  // tiles.)
   if (p.n > 2048 && p.rows >= 1024 && p.k <= 4096) {
     const int64_t cols = (p.n + 127) / 128;
     const int64_t t192 = (p.rows + 191) / 192 * cols, t128x128 = (p.rows + 127) / 128 * cols;
