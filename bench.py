@@ -1352,8 +1352,9 @@ GATE_UP_PREFILL_SHAPES = [(128, 1536, 8960, "f16", "qwen2.5-1.5b"), (1024, 1536,
                           (4096, 1536, 8960, "f16", "qwen2.5-1.5b"), (4096, 3584, 18944, "bf16", "qwen2.5-7b")]
 # the Qwen2.5-0.5B, 1.5B and 7B MLPs over prefill row counts (--only gate-up-prefill-sweep)
 GATE_UP_PREFILL_SWEEP_SHAPES = (
-    [(m, 1536, 8960, "f16", "qwen2.5-1.5b") for m in (64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096)]
-    + [(m, 3584, 18944, "bf16", "qwen2.5-7b") for m in (256, 512, 1024, 1536, 1792, 2048, 4096)]
+    [(m, 1536, 8960, "f16", "qwen2.5-1.5b") for m in (64, 128, 256, 384, 512, 768, 1024, 1400, 1536, 2048, 2900, 3072,
+                                                       4096)]
+    + [(m, 3584, 18944, "bf16", "qwen2.5-7b") for m in (256, 512, 1024, 1100, 1536, 1792, 2048, 4096)]
     + [(m, 896, 4864, "bf16", "qwen2.5-0.5b") for m in (256, 1024, 4096)])
 
 

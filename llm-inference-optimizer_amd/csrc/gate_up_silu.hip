@@ -247,6 +247,14 @@ template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int 
 int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   using C = tiled::Cfg<T, tiled::B_16, TO, WGM, WGN, FM, FN, tiled::EPI_SILU, S>;
   static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
+  // a tile count that is not a multiple of 8: the instantiation with
+  // contiguous tile ranges per XCD for any count (XR = 1; 1.5B at 384 rows
+  // 34.7 -> 29.7 us, at 1400 rows 92.5 -> 87.3 us, 7B at 1792 rows 435.8 ->
+  // 412.3 us)
+  if constexpr (XR == 0) {
+    const int64_t ntiles = static_cast<int64_t>((p.rows + C::BM - 1) / C::BM) * ((p.n_out + C::BN - 1) / C::BN);
+    if (ntiles % 8 != 0) return gate_up_tiled_cfg<T, TO, WGM, WGN, FM, FN, S, RING, 1>(p, s);
+  }
   tiled::Params tp{};
   tp.x = p.x;
   tp.b0 = p.wg;
@@ -325,13 +333,10 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
                c128 = 1.72 * rounds(p.rows, p.n_out, 256, 128, 1);
   const double single = c64 < c_small ? (c64 < c128 ? c64 : c128) : (c_small < c128 ? c_small : c128);
 
-  // 256 x 128 tiles; a tile count that is not a multiple of 8 still gets
-  // contiguous tile ranges per XCD (XR; 1.5B at 768 rows, 210 tiles, 49.0 ->
-  // 46.3 us; at 1536 rows, 420 tiles, 93.6 -> 90.5 us)
-  const auto big_tiles = [&](const GateUpParams& q) {
-    if (cdiv(q.rows, 256) * cdiv(q.n_out, 128) % 8 != 0) return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1, 1>(q, s);
-    return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(q, s);
-  };
+  // 256 x 128 tiles (a ragged tile count gets XCD ranges, as every launch
+  // does: 1.5B at 768 rows, 210 tiles, 49.0 -> 46.3 us; at 1536 rows, 420
+  // tiles, 93.6 -> 90.5 us)
+  const auto big_tiles = [&](const GateUpParams& q) { return gate_up_tiled_cfg<T, TO, 2, 4, 4, 1, 2, 1>(q, s); };
   // whole rounds of 256 x 128 tiles, and the 128-column blocks that fill
   // them (a round need not end at a column boundary: the head launch's
   // tiles fill its rounds in order)
