@@ -195,7 +195,8 @@ VARIANTS = {
 # W8A16 tiles that the launch plan now picks only for k > 4096).
 CORE_VARIANTS = ("rms_wave_rows2", "rms_block_rows2", "rms_one_wave", "rms_weight_lds", "rms_persistent8",
                  "rms_block_persistent4", "silu_unroll1", "silu_large_block512_unroll2", "tiled_widen_in_place",
-                 "w8_skinny_sweep", "w8_skinny_sweep_pipe", "w8_tile_cfg2", "w8_tile_cfg3")
+                 "w8_skinny_sweep", "w8_skinny_sweep_pipe", "w8_tile_cfg2", "w8_tile_cfg3",
+                 "gate_up_xcd_dispatch_order")
 VARIANT_DIR = PKG_DIR / "_variants"
 # Variants that spread a row over waves differently from the default build
 # (one wave per wide row; one packet per lane over more waves): the fp32 sum
