@@ -100,6 +100,9 @@ def parse_args():
                    help="launch-shape sweep of the W8A16 decode (skinny) kernel on the sweep variant builds "
                         "(build.py --variant w8_skinny_sweep w8_skinny_sweep_pipe): G x waves x U x split of K "
                         "over workgroups, per decode shape (default: all of W8_SKINNY_SWEEP_SHAPES)")
+    p.add_argument("--w8-dual-skinny-sweep", action="store_true",
+                   help="launch-shape sweep of the int8 gate/up + SiLU-and-mul decode kernel on the w8_skinny_sweep "
+                        "build: G x waves x U x split of K over workgroups, per decode shape")
     p.add_argument("--full-json", default=None, metavar="PATH",
                    help="also write the full result (every leg) to PATH; stdout carries the compact line")
     p.add_argument("--rocprof-summary", nargs="+", metavar="DIR", default=None,
@@ -648,6 +651,9 @@ def main():
     if args.w8_skinny_sweep is not None:
         w8_skinny_sweep(ctx, args.w8_skinny_sweep)
         return
+    if args.w8_dual_skinny_sweep:
+        w8_dual_skinny_sweep(ctx)
+        return
 
     F16 = torch.float16
     M, N, I = 2048, 1536, 8960
@@ -1097,6 +1103,90 @@ def w8_skinny_sweep(ctx, only):
     print(json.dumps(out), flush=True)
     if bad:
         log(f"w8 skinny sweep: results off or not reproducible: {bad[:5]}")
+        sys.exit(1)
+
+
+# (rows, k, n_out, dtype, label): the int8 gate/up + SiLU-and-mul kernel at
+# decode rows of the Qwen2.5-1.5B and 7B MLPs
+W8_DUAL_SKINNY_SWEEP_SHAPES = [
+    (8, 1536, 8960, "f16", "gateup1.5b"), (1, 1536, 8960, "f16", "gateup1.5b"),
+    (8, 3584, 18944, "bf16", "gateup7b"), (1, 3584, 18944, "bf16", "gateup7b"),
+    (4, 1536, 8960, "f16", "gateup1.5b"), (2, 3584, 18944, "bf16", "gateup7b"),
+    (8, 896, 4864, "bf16", "gateup0.5b"), (1, 896, 4864, "bf16", "gateup0.5b"),
+]
+
+
+def w8_dual_skinny_sweep(ctx):
+    """The int8 gate/up + SiLU-and-mul decode kernel (w8a16_skinny with two
+    weight matrices) under forced launch shapes of the w8_skinny_sweep build:
+    weight-row groups G, waves per workgroup, blocks in flight U, and a split
+    of K over KS workgroups.  Cold weights, hipGraph timing; every shape's
+    output is checked against the default library's (within 2e-3 of the
+    largest output) and for the same bits on three calls.  One JSON line."""
+    torch = ctx.torch
+    path = variant_lib("w8_skinny_sweep")
+    if not path.exists():
+        raise SystemExit(f"{path} missing: python llm-inference-optimizer_amd/build.py --variant w8_skinny_sweep")
+    lib = ctx.L.load_variant(path)
+    lib.mi355_w8_sweep_config.argtypes = [ctypes.c_int] * 4
+    lib.mi355_w8_sweep_config.restype = None
+    lib.mi355_w8_sweep_ks.argtypes = [ctypes.c_int]
+    lib.mi355_w8_sweep_ks.restype = ctypes.c_int
+    if lib.mi355_w8_sweep_ks(0) != 0:
+        raise SystemExit("w8_skinny_sweep: the split-K scratch is not addressable")
+    c = ctx.with_lib(lib)
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
+    grid = [(g, 1, sp, u) for g in (1, 2, 4) for sp in (2, 3, 4, 6, 8, 12, 16) for u in (1, 2)]
+    grid += [(g, ks, sp, 1) for g in (1, 2, 4) for ks in (2, 4) for sp in (4, 8)]
+    out = {"shapes": {}}
+    bad = []
+    for M, K, N, dn, lab in W8_DUAL_SKINNY_SWEEP_SHAPES:
+        dt = dts[dn]
+        sets = min(32, n_sets(2 * N * K))
+        x = rand(ctx, (M, K), 1900 + M, dt)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(7)
+        w = [(torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8),
+              torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4,
+              torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8),
+              torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
+        outs = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(4)]
+        ref = torch.empty((M, N), dtype=dt, device=ctx.dev)
+        ctx.gate_up_w8_call(x, *w[0], ref)()
+        ref_max = ref.float().abs().max().item()
+        base = [ctx.gate_up_w8_call(x, *ws, outs[i % 4]) for i, ws in enumerate(w)]
+        spin_up(ctx, base)
+        t_default = time_graph(ctx, base, max(2 * sets, 64))
+        rows = []
+        for G, KS, split, U in grid:
+            lib.mi355_w8_sweep_config(G, U, split, 1)
+            lib.mi355_w8_sweep_ks(KS)
+            o = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(3)]
+            for oi in o:
+                c.gate_up_w8_call(x, *w[0], oi)()
+            torch.cuda.synchronize()
+            same_bits = all(torch.equal(o[0], oi) for oi in o[1:])
+            err = (o[0].float() - ref.float()).abs().max().item() / max(ref_max, 1e-6)
+            us = time_graph(c, [c.gate_up_w8_call(x, *ws, outs[i % 4]) for i, ws in enumerate(w)],
+                            max(2 * sets, 64))
+            r = {"G": G, "KS": KS, "waves": split, "U": U, "us": round(us, 3)}
+            rows.append(r)
+            if err > 2e-3 or not same_bits:
+                bad.append(dict(r, shape=f"{lab} M={M}", err=err, same_bits=same_bits))
+        lib.mi355_w8_sweep_config(0, 0, 0, 0)
+        lib.mi355_w8_sweep_ks(0)
+        best = min(rows, key=lambda r: r["us"])
+        best_ks1 = min((r for r in rows if r["KS"] == 1), key=lambda r: r["us"])
+        key = f"{lab}_M{M}"
+        out["shapes"][key] = {"rows": M, "k": K, "n_out": N, "dtype": dn, "default_us": round(t_default, 3),
+                              "best": best, "best_ks1": best_ks1, "configs": rows}
+        log(f"  w8 dual skinny sweep {key}: default {t_default:.2f} us; best {best}; best at KS = 1 {best_ks1}")
+        del w, base
+        torch.cuda.empty_cache()
+    out["mismatches"] = bad
+    print(json.dumps(out), flush=True)
+    if bad:
+        log(f"w8 dual skinny sweep: results off or not reproducible: {bad[:5]}")
         sys.exit(1)
 
 

@@ -478,6 +478,18 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   } else {
     split = (nblk + bpw - 1) / bpw;  // even blocks per wave
   }
+  // The dual kernel with up to 8 rows, 2 groups and more than 4 workgroups
+  // per CU: 2 waves per workgroup (the 7B MLP at 1, 2 and 8 rows: 24.0 /
+  // 24.6 / 28.0 us, against 26.3 us with 3 waves at 1 row and 30.6 / 31.2
+  // us with 1 wave at 2 and 8 rows, in the same sweep).
+  bool forced_split = false;
+#ifdef MI355_W8_SWEEP
+  forced_split = g_force_split > 0;
+#endif
+  if (DUAL && MT == 1 && G == 2 && units > 4 * static_cast<int64_t>(cus) && nblk >= 2 && !forced_split) {
+    split = 2;
+    bpw = (nblk + 1) / 2;
+  }
   if (u == 0) {
     u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
     // One row, one workgroup per CU, 2 blocks in flight per wave: at most 12
@@ -534,19 +546,23 @@ int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
     if ((p.n + 31) / 32 >= min_groups) g = 4;
     else if ((p.n + 15) / 16 >= min_groups) g = 2;
   }
-  // the dual kernel carries two weight matrices per row group: half the
-  // groups, and at most 2 (MT = 2) or 1 (MT >= 3) so its 2 G MT accumulator
-  // tiles fit the register budget
   // The dual kernel carries two weight matrices per row group: one group for
-  // a single row, else at most 2 (a sweep of G x split x U over Qwen2.5-1.5B
-  // and -7B decode rows: 8 rows 9.2 us with 2 groups vs 12.5 us with 1), and
-  // 1 for MT >= 3 so its 2 G MT accumulator tiles fit the register budget.
+  // a single row unless the matrices are large (below), else at most 2 (a
+  // sweep of G x split x U over Qwen2.5-1.5B and -7B decode rows: 8 rows 9.2
+  // us with 2 groups vs 12.5 us with 1), and 1 for MT >= 3 so its 2 G MT
+  // accumulator tiles fit the register budget.
 #ifdef MI355_W8_SWEEP
   constexpr int gmax = !DUAL ? (MT == 1 ? 8 : 4) : (MT >= 3 ? 1 : (MT == 1 ? 4 : 2));
 #else
   constexpr int gmax = !DUAL ? 4 : (MT >= 3 ? 1 : 2);
 #endif
-  if (DUAL) g = p.rows <= 1 ? 1 : (g > 2 ? 2 : g);
+  // One row: 2 groups once single groups would make more than 8 workgroups
+  // per CU (the 7B MLP: 27.5 -> 24.0 us in a graph-timed sweep of G x waves
+  // x U; the 1.5B and 0.5B MLPs keep 1).
+  if (DUAL) {
+    if (p.rows <= 1) g = (p.n + 7) / 8 > 8 * cus ? 2 : 1;
+    else g = g > 2 ? 2 : g;
+  }
 #ifdef MI355_W8_SWEEP
   if (g_force_g > 0) g = g_force_g;
 #endif
