@@ -440,8 +440,9 @@ namespace {
 //     (n / 16 >= 192 and n * k >= 12M); with <= 8 rows 4 if n / 32 >= 384,
 //     else 2 if n / 16 >= 192; beyond, the largest of 4, 2, 1 with
 //     n / (8 G) >= 160 (<= 32 rows) or 48 (several 32-row tiles);
-//   waves per workgroup (the split of K) so that about 4096 (1 row), 1536
-//     (<= 8 rows), 1024 (<= 32 rows) or 1536 (several 32-row tiles) waves run
+//   waves per workgroup (the split of K) so that about 4096 (1 row; 3072
+//     for the dual kernel), 1536 (<= 8 rows), 1024 (<= 32 rows) or 1536
+//     (several 32-row tiles) waves run
 //     in total, within the LDS for the partial sums (<= 64 KiB), then evened
 //     out so every wave gets the same number of 128-column blocks -- or, when
 //     there are no more workgroups than CUs, rounded to a multiple of 4 so
@@ -457,7 +458,10 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   const int nblk = (p.k + 127) / 128;
   const int tiles = (p.rows + 8 * MT - 1) / (8 * MT);
   const int64_t units = static_cast<int64_t>(groups) * tiles;
-  const int64_t waves = p.rows <= 1 ? 16 * cus : (p.rows <= 8 ? 6 * cus : (p.rows <= 32 ? 4 * cus : 6 * cus));
+  // (the dual kernel moves two weight blocks per wave and step: 12 waves per
+  // CU at one row -- 1.5B MLP 8.04 -> 7.47 us, 0.5B 5.15 -> 4.97 us)
+  const int64_t waves = p.rows <= 1 ? (DUAL ? 12 : 16) * cus
+                                    : (p.rows <= 8 ? 6 * cus : (p.rows <= 32 ? 4 * cus : 6 * cus));
   int split = static_cast<int>((waves + units / 2) / units);
   int u = 0;
 #ifdef MI355_W8_SWEEP
