@@ -448,7 +448,7 @@ KNOWN_LAUNCHES = {
     ("w8a16_skinny<mi355::F16, mi355::F16, 1, 2, 1, true>", 192 * 560): (
         "int8 gate/up + SiLU-and-mul 1.5B, 8 rows, 2 x [8960,1536] int8, fp16",
         2 * 8960 * 1536 + 8 * 8960 + 8 * 1536 * 2 + 8 * 8960 * 2),
-    ("w8a16_skinny<mi355::BF16, mi355::BF16, 1, 2, 1, true>", 64 * 1184): (
+    ("w8a16_skinny<mi355::BF16, mi355::BF16, 1, 2, 1, true>", 128 * 1184): (  # 2 waves per workgroup
         "int8 gate/up + SiLU-and-mul 7B, 8 rows, 2 x [18944,3584] int8, bf16",
         2 * 18944 * 3584 + 8 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
     ("linear16_skinny<mi355::F16, mi355::F16, 1, 1, 2>", 192 * 512): (
