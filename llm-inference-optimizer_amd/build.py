@@ -157,6 +157,10 @@ VARIANTS = {
     # 16-bit gate/up + SiLU-and-mul: the column split's rest in one shape
     # (4: 256 x 64; 5: 128 x 128 of 8 waves) whenever it fits one round
     **{f"gate_up_rest_shape{f}": ("gate_up_silu", [f"-DMI355_GU_REST_SHAPE={f}"]) for f in (4, 5)},
+    # W8A16 tiled GEMM, wide outputs from 1024 rows: the column split (whole
+    # rounds of 128 x 128, the rest in 128 x 64) when the last round is more
+    # than half full (1) or whenever the rest fits one round (2)
+    **{f"w8_colsplit{m}": ("w8a16", [f"-DMI355_W8_COLSPLIT={m}"]) for m in (1, 2)},
     # W8A16 tiled GEMM: m-blocks per group of the tile order (default 4)
     **{f"w8_group_m{g}": ("w8a16", [f"-DMI355_W8_GROUP_M={g}"]) for g in (1, 2, 8, 16, 64)},
     # W8A16 tiled GEMM: an L2 prefetch wave per workgroup, 2 / 4 / 8 K steps

@@ -591,6 +591,18 @@ bool tiled_fits(const W8Params& p, bool) {
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
+// Bytes per element of a scale / bias dtype code.
+inline int64_t dtype_size(int dt) { return dt == MI355_F32 ? 4 : 2; }
+
+// MI355_W8_COLSPLIT = 1 / 2: wide outputs from 1024 rows split their columns
+// into whole rounds of 128 x 128 tiles and a round of 128 x 64 tiles, when
+// the last round of 128 x 128 tiles would be more than half full (1) or
+// whenever the rest fits one round (2) (a measurement switch for variant
+// builds; 0 = one launch).
+#ifndef MI355_W8_COLSPLIT
+#define MI355_W8_COLSPLIT 0
+#endif
+
 // MI355_W8_GROUP_M: m-blocks per group of the tiled GEMM's tile order inside
 // each XCD's range (m fastest within a group; a measurement switch for
 // variant builds).
@@ -737,6 +749,33 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
     const int64_t t192 = (p.rows + 191) / 192 * cols, t128x128 = (p.rows + 127) / 128 * cols;
     if (t192 <= 2 * static_cast<int64_t>(cus) && t128x128 > 2 * static_cast<int64_t>(cus))
       return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, tiled::EPI_W8, 1, 4, 1>(p, s);
+#if MI355_W8_COLSPLIT
+    {
+      // Column split: whole rounds of 128 x 128 tiles (two per CU) over the
+      // leading columns, the rest in one round of 128 x 64 tiles (4 waves,
+      // four per CU), instead of a last, partly filled round of 128 x 128.
+      // Every output element sums its k products in the same order either way.
+      const int64_t tm = (p.rows + 127) / 128, slots = 2 * static_cast<int64_t>(cus);
+      const int64_t full = cols * tm / slots, remainder = t128x128 - full * slots;
+      const int lead = static_cast<int>(full * slots / tm * 128);
+      const bool want = MI355_W8_COLSPLIT == 2 || remainder > cus;
+      if (want && full >= 1 && lead > 0 && lead < p.n) {
+        const int rest = p.n - lead;
+        if (tm * ((rest + 63) / 64) <= 4 * static_cast<int64_t>(cus)) {
+          W8Params head = p, tail = p;
+          head.n = lead;
+          tail.n = rest;
+          tail.q = static_cast<const int8_t*>(p.q) + static_cast<int64_t>(lead) * p.qs;
+          tail.scale = static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(lead) * dtype_size(p.sdt);
+          if (p.bdt >= 0) tail.bias = static_cast<const uint8_t*>(p.bias) + static_cast<int64_t>(lead) * dtype_size(p.bdt);
+          tail.out = static_cast<uint8_t*>(p.out) + static_cast<int64_t>(lead) * static_cast<int64_t>(sizeof(typename TO::bits));
+          const int r = w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(head, s);
+          if (r != MI355_OK) return r;
+          return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, tiled::EPI_W8, 1>(tail, s);
+        }
+      }
+    }
+#endif
     return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(p, s);
   }
   // Below 1024 rows, wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring

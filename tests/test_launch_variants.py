@@ -141,6 +141,9 @@ W8_VARIANTS = _variants_of("w8a16")
 # 1.5B gate/up and down projections, ragged rows / n, a k tail, bf16
 W8_SHAPES = [(1024, 1536, 8960, torch.float16), (300, 8960, 1536, torch.float16),
              (1030, 272, 6600, torch.float16), (520, 1536, 4736, torch.bfloat16),
+             # wide outputs whose 128 x 128 tiles end on a partial round (770 and
+             # 2240 tiles): the column-split builds run two launches there
+             (1400, 264, 8960, torch.float16), (4096, 64, 8960, torch.bfloat16),
              # decode rows through the skinny kernel (the sweep builds' own code)
              (8, 8960, 1536, torch.float16), (1, 1536, 8960, torch.float16), (5, 3584, 1000, torch.bfloat16),
              (24, 1536, 2048, torch.float16)]
