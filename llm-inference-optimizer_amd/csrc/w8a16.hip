@@ -742,7 +742,7 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
   // the 192 x 128 tile with its registers capped at 128 (4 waves per SIMD,
   // so two workgroups fit on a CU): 1.5B gate/up at 1024 rows, 420 tiles
   // against 560 of 128 x 128 on 512 slots, 43.0 vs 46.8 us.  (Its tile
-  // counts here are rarely multiples of 8: XR below, 43.2 vs 44.4 us at 420
+  // counts here are rarely multiples of 8: XR = 1, 43.2 vs 44.4 us at 420
   // tiles.)
   if (p.n > 2048 && p.rows >= 1024 && p.k <= 4096) {
     const int64_t cols = (p.n + 127) / 128;
@@ -767,8 +767,10 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
           tail.n = rest;
           tail.q = static_cast<const int8_t*>(p.q) + static_cast<int64_t>(lead) * p.qs;
           tail.scale = static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(lead) * dtype_size(p.sdt);
-          if (p.bdt >= 0) tail.bias = static_cast<const uint8_t*>(p.bias) + static_cast<int64_t>(lead) * dtype_size(p.bdt);
-          tail.out = static_cast<uint8_t*>(p.out) + static_cast<int64_t>(lead) * static_cast<int64_t>(sizeof(typename TO::bits));
+          if (p.bdt >= 0)
+            tail.bias = static_cast<const uint8_t*>(p.bias) + static_cast<int64_t>(lead) * dtype_size(p.bdt);
+          tail.out = static_cast<uint8_t*>(p.out) +
+                     static_cast<int64_t>(lead) * static_cast<int64_t>(sizeof(typename TO::bits));
           const int r = w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(head, s);
           if (r != MI355_OK) return r;
           return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, tiled::EPI_W8, 1>(tail, s);
