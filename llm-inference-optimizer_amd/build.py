@@ -157,6 +157,8 @@ VARIANTS = {
     # 16-bit gate/up + SiLU-and-mul: the column split's rest in one shape
     # (4: 256 x 64; 5: 128 x 128 of 8 waves) whenever it fits one round
     **{f"gate_up_rest_shape{f}": ("gate_up_silu", [f"-DMI355_GU_REST_SHAPE={f}"]) for f in (4, 5)},
+    # 16-bit gate/up + SiLU-and-mul: m-blocks per group of the tile order (default 4)
+    **{f"gate_up_group_m{g}": ("gate_up_silu", [f"-DMI355_GU_GROUP_M={g}"]) for g in (2, 8, 64)},
     # W8A16 tiled GEMM, wide outputs from 1024 rows: the column split (whole
     # rounds of 128 x 128, the rest in 128 x 64) when the last round is more
     # than half full (1) or whenever the rest fits one round (2)

@@ -236,6 +236,11 @@ int gate_up_shape(const GateUpParams& p, hipStream_t s) {
 #ifndef MI355_GU_ROUNDS_BY_COLUMNS
 #define MI355_GU_ROUNDS_BY_COLUMNS 0
 #endif
+// MI355_GU_GROUP_M: m-blocks per group of the tile order inside each XCD's
+// range (m fastest within a group; a measurement switch for variant builds).
+#ifndef MI355_GU_GROUP_M
+#define MI355_GU_GROUP_M 4
+#endif
 // MI355_GU_REST_SHAPE = f > 0: the column split's remaining columns take
 // shape f of the plan below whenever it covers them in one round (a
 // measurement switch for variant builds).
@@ -270,7 +275,7 @@ int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   tp.bdt = -1;
   tp.tiles_m = (p.rows + C::BM - 1) / C::BM;
   tp.tiles_n = (p.n_out + C::BN - 1) / C::BN;
-  tp.group_m = tp.tiles_m < 4 ? tp.tiles_m : 4;
+  tp.group_m = tp.tiles_m < MI355_GU_GROUP_M ? tp.tiles_m : MI355_GU_GROUP_M;
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_16, TO, WGM, WGN, FM, FN,
