@@ -163,6 +163,9 @@ VARIANTS = {
     # rounds of 128 x 128, the rest in 128 x 64) when the last round is more
     # than half full (1) or whenever the rest fits one round (2)
     **{f"w8_colsplit{m}": ("w8a16", [f"-DMI355_W8_COLSPLIT={m}"]) for m in (1, 2)},
+    # W8A16 tiled GEMM: tiles ordered in 2 / 4 / 8 column bands before the
+    # XCD ranges (every single-matrix launch)
+    **{f"w8_bands{b}": ("w8a16", [f"-DMI355_W8_BANDS={b}"]) for b in (2, 4, 8)},
     # W8A16 tiled GEMM: m-blocks per group of the tile order (default 4)
     **{f"w8_group_m{g}": ("w8a16", [f"-DMI355_W8_GROUP_M={g}"]) for g in (1, 2, 8, 16, 64)},
     # W8A16 tiled GEMM: an L2 prefetch wave per workgroup, 2 / 4 / 8 K steps

@@ -133,6 +133,7 @@ struct Params {
   int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
   int tiles_m, tiles_n;
   int group_m;  // m-blocks per group of the tile order (tiles_m: m fastest over the whole range)
+  int bands;    // XR = 2: column bands of the tile order (each band's tiles in group order)
 };
 
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S>
@@ -289,10 +290,23 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
     if ((ntiles & 7) == 0) b = (b & 7) * (ntiles >> 3) + (b >> 3);
   }
   // inside the range: groups of group_m m-blocks, m fastest within a group
-  const int per_group = p.group_m * p.tiles_n;
+  // (XR = 2: first split into column bands of bw tile columns, band-major, so
+  // an XCD's range covers a band's columns rather than every column)
+  int tn_base = 0, width = p.tiles_n;
+  if constexpr (XR == 2) {
+    const int bw = (p.tiles_n + p.bands - 1) / p.bands;
+    const int per_band = p.tiles_m * bw;
+    const int nb = (p.tiles_n + bw - 1) / bw;  // bands actually used (none empty)
+    int j = b / per_band;
+    if (j > nb - 1) j = nb - 1;
+    b -= j * per_band;
+    tn_base = j * bw;
+    width = p.tiles_n - tn_base < bw ? p.tiles_n - tn_base : bw;
+  }
+  const int per_group = p.group_m * width;
   const int g0 = (b / per_group) * p.group_m;
   const int gsz = p.tiles_m - g0 < p.group_m ? p.tiles_m - g0 : p.group_m;
-  const int tm = g0 + (b % per_group) % gsz, tn = (b % per_group) / gsz;
+  const int tm = g0 + (b % per_group) % gsz, tn = tn_base + (b % per_group) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
   const int nrows_x = p.rows - m0 < BM ? p.rows - m0 : BM;
   const int nrows_b = p.n - n0 < BN ? p.n - n0 : BN;

@@ -603,6 +603,14 @@ inline int64_t dtype_size(int dt) { return dt == MI355_F32 ? 4 : 2; }
 #define MI355_W8_COLSPLIT 0
 #endif
 
+// MI355_W8_BANDS = b > 1: every single-matrix tiled launch orders its tiles
+// in b column bands (XR = 2 of the tiled core) before the XCD ranges, so an
+// XCD reads a band's weights rather than all of them (a measurement switch
+// for variant builds; 1 = no bands).
+#ifndef MI355_W8_BANDS
+#define MI355_W8_BANDS 1
+#endif
+
 // MI355_W8_GROUP_M: m-blocks per group of the tiled GEMM's tile order inside
 // each XCD's range (m fastest within a group; a measurement switch for
 // variant builds).
@@ -621,6 +629,8 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   // counts are mostly not powers of two: 1.5B gate/up at 1400 rows (770
   // tiles of 128 x 128) 66.1 -> 58.3 us, 2900 rows 112.0 -> 103.8 us, 7B
   // gate/up at 1100 rows 179.2 -> 174.9 us; the narrow outputs even.
+  if constexpr (XR != 2 && MI355_W8_BANDS > 1 && EPI == tiled::EPI_W8)
+    return w8_tiled_cfg<T, TO, WGM, WGN, FM, FN, S, EPI, RING, WPE, 2>(p, s);
   if constexpr (XR == 0) {
     const int64_t ntiles = static_cast<int64_t>((p.rows + C::BM - 1) / C::BM) * ((p.n + C::BN - 1) / C::BN);
     if (ntiles % 8 != 0) return w8_tiled_cfg<T, TO, WGM, WGN, FM, FN, S, EPI, RING, WPE, 1>(p, s);
@@ -644,6 +654,7 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   tp.tiles_m = (p.rows + C::BM - 1) / C::BM;
   tp.tiles_n = (p.n + C::BN - 1) / C::BN;
   tp.group_m = tp.tiles_m < MI355_W8_GROUP_M ? tp.tiles_m : MI355_W8_GROUP_M;
+  tp.bands = MI355_W8_BANDS;
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
