@@ -69,11 +69,13 @@ def parse_args():
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
+    p.add_argument("--skip-e2e", action="store_true", help="no end-to-end before/after leg")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged"],
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "stage3",
+                                      "e2e-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -85,24 +87,6 @@ def parse_args():
     p.add_argument("--seq-lens", type=int, nargs="+", default=[128, 512, 1024, 2048])
     p.add_argument("--gen-len", type=int, default=32)
     p.add_argument("--trials", type=int, default=5)
-    p.add_argument("--variant", default=None, metavar="NAME",
-                   help="time the kernels of a variant library (build.py --variant NAME; launch-shape switches, "
-                        "same results) instead of the default one; the kernel legs only")
-    p.add_argument("--sweep", nargs="+", metavar="NAME", default=None,
-                   help="A/B sweep: time the default library and these variant libraries ('all' = every built "
-                        "variant) on the --sweep-legs, interleaved over --sweep-rounds, and check each variant's "
-                        "outputs equal the default library's bit for bit")
-    p.add_argument("--sweep-legs", nargs="+", default=["c1-rms", "c1-add-rms", "c4-rms", "c2-silu", "c4-silu"],
-                   choices=["c1-rms", "c1-add-rms", "c4-rms", "c2-silu", "c4-silu", "silu-4096x8960",
-                            "silu-8192x8960"])
-    p.add_argument("--sweep-rounds", type=int, default=3)
-    p.add_argument("--w8-skinny-sweep", nargs="*", metavar="SHAPE", default=None,
-                   help="launch-shape sweep of the W8A16 decode (skinny) kernel on the sweep variant builds "
-                        "(build.py --variant w8_skinny_sweep w8_skinny_sweep_pipe): G x waves x U x split of K "
-                        "over workgroups, per decode shape (default: all of W8_SKINNY_SWEEP_SHAPES)")
-    p.add_argument("--w8-dual-skinny-sweep", action="store_true",
-                   help="launch-shape sweep of the int8 gate/up + SiLU-and-mul decode kernel on the w8_skinny_sweep "
-                        "build: G x waves x U x split of K over workgroups, per decode shape")
     p.add_argument("--full-json", default=None, metavar="PATH",
                    help="also write the full result (every leg) to PATH; stdout carries the compact line")
     p.add_argument("--rocprof-summary", nargs="+", metavar="DIR", default=None,
@@ -115,15 +99,14 @@ class Ctx:
     """Bound C-ABI entry points.  Launch closures read `self.stream` at call
     time, so a graph capture can redirect them to the capturing stream."""
 
-    def __init__(self, variant=None):
+    def __init__(self):
         import torch
 
         sys.path.insert(0, str(ROOT))
         self.torch = torch
         self.pkg = importlib.import_module(PKG)
         self.L = importlib.import_module(PKG + "._lib")
-        self.lib = self.L.load() if variant is None else self.L.load_variant(variant_lib(variant))
-        self.variant = variant
+        self.lib = self.L.load()
         self.dev = torch.device("cuda:0")
         torch.cuda.set_device(self.dev)
         self.stream = torch.cuda.current_stream(self.dev).cuda_stream
@@ -138,13 +121,23 @@ class Ctx:
             self.probe.mi355_probe_add2.restype = ctypes.c_int
             self.probe.mi355_probe_empty.argtypes = [ctypes.c_void_p]
             self.probe.mi355_probe_empty.restype = ctypes.c_int
-
-    def with_lib(self, lib):
-        """A shallow copy whose launch closures call `lib` (a variant build)."""
-        c = object.__new__(Ctx)
-        c.__dict__.update(self.__dict__)
-        c.lib = lib
-        return c
+            self.probe.mi355_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                                    ctypes.c_void_p]
+            self.probe.mi355_probe_read.restype = ctypes.c_int
+            i32 = ctypes.c_int
+            self.probe.mi355_probe_w8_stream.argtypes = [ctypes.c_void_p, i32, i32, ctypes.c_int64, ctypes.c_void_p,
+                                                         i32, ctypes.c_int64, i32, i32, i32, i32, i32, i32, i32,
+                                                         ctypes.c_void_p, ctypes.c_void_p]
+            self.probe.mi355_probe_w8_stream.restype = ctypes.c_int
+            vp = ctypes.c_void_p
+            self.probe.mi355_probe_w8a16_stream.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32,
+                                                            i32, vp]
+            self.probe.mi355_probe_w8a16_stream.restype = ctypes.c_int
+            self.probe.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
+            self.probe.mi355_probe_w8a16_stream_plan.restype = None
+            self.probe.mi355_probe_w8a16_stream_loads.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
+                                                                  vp, vp]
+            self.probe.mi355_probe_w8a16_stream_loads.restype = ctypes.c_int
 
     def check(self, fn, st):
         if st:
@@ -260,6 +253,61 @@ class Ctx:
                 raise RuntimeError("probe empty kernel failed")
         return call
 
+    def read_call(self, src, sink):
+        f = self.probe.mi355_probe_read
+        args = (src.data_ptr(), src.numel() * src.element_size(), sink.data_ptr())
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError("probe read failed")
+        return call
+
+    def w8_stream_call(self, q, sink, rpw, waves, g, u, layout=0, x=None, xl=1, stagger=0):
+        """The int8 weight stream of a decode kernel's launch shape, without
+        its MFMAs, reduction and epilogue (csrc/probe/w8_stream.hip)."""
+        n, k = q.shape
+        f = self.probe.mi355_probe_w8_stream
+        args = (q.data_ptr(), n, k, k, x.data_ptr() if x is not None else None, x.shape[0] if x is not None else 0,
+                x.shape[1] if x is not None else 0, rpw, waves, g, u, layout, xl, stagger, sink.data_ptr())
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError(f"probe w8 stream failed for {args[5:12]}")
+        return call
+
+    def w8_stream_plan(self, rows, k, n, dual, cus):
+        """The W8A16 decode kernel's launch plan (rpw, r4, waves, u), from the
+        same source the library compiles."""
+        out4 = (ctypes.c_int * 4)()
+        self.probe.mi355_probe_w8a16_stream_plan(rows, k, n, int(dual), cus, out4)
+        return tuple(out4)
+
+    def w8_stream_loads_call(self, x, q, sink, rpw, r4, waves, u, with_x):
+        """The W8A16 decode kernel's loads alone at a launch shape."""
+        M, K = x.shape
+        N = q.shape[0]
+        f = self.probe.mi355_probe_w8a16_stream_loads
+        args = (x.data_ptr(), q.data_ptr(), M, K, N, rpw, r4, waves, u, int(with_x), sink.data_ptr())
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError(f"probe w8a16 stream loads failed for {args[2:10]}")
+        return call
+
+    def w8_stream_plan_call(self, x, q, scale, out, rpw, r4, waves, u, q2=None, scale2=None):
+        """The W8A16 decode kernel with a forced launch shape (fp16 x and out,
+        fp32 scales; csrc/probe/w8_stream_plan.hip)."""
+        M, K = x.shape
+        N = q.shape[0]
+        f = self.probe.mi355_probe_w8a16_stream
+        args = (x.data_ptr(), q.data_ptr(), scale.data_ptr(), q2.data_ptr() if q2 is not None else None,
+                scale2.data_ptr() if scale2 is not None else None, out.data_ptr(), M, K, N, rpw, r4, waves, u)
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError(f"probe w8a16 stream failed for {args[6:]}")
+        return call
+
     def add2_call(self, a, b, dst):
         f = self.probe.mi355_probe_add2
         args = (a.data_ptr(), b.data_ptr(), dst.data_ptr(), a.numel() * a.element_size())
@@ -268,11 +316,6 @@ class Ctx:
             if f(*args, self.stream):
                 raise RuntimeError("probe add2 failed")
         return call
-
-
-def variant_lib(name: str) -> Path:
-    """Path of a variant library built by `build.py --variant NAME`."""
-    return ROOT / PKG / "_variants" / f"libmi355_fused_{name}.so"
 
 
 def rand(ctx, shape, seed, dtype, mean=0.0, std=1.0):
@@ -640,20 +683,10 @@ def main():
         bench_e2e_int8(args)
         return
 
-    ctx = Ctx(args.variant)
+    ctx = Ctx()
     torch = ctx.torch
     props = torch.cuda.get_device_properties(ctx.dev)
-    log(f"device: {props.name} ({getattr(props, 'gcnArchName', '?')}), CUs={props.multi_processor_count}"
-        + (f", variant library {args.variant}" if args.variant else ""))
-    if args.sweep:
-        run_sweep(ctx, args)
-        return
-    if args.w8_skinny_sweep is not None:
-        w8_skinny_sweep(ctx, args.w8_skinny_sweep)
-        return
-    if args.w8_dual_skinny_sweep:
-        w8_dual_skinny_sweep(ctx)
-        return
+    log(f"device: {props.name} ({getattr(props, 'gcnArchName', '?')}), CUs={props.multi_processor_count}")
 
     F16 = torch.float16
     M, N, I = 2048, 1536, 8960
@@ -738,8 +771,6 @@ def main():
                      "avg_launch_us": round(silu_us, 3)},
     }
     full = {"kernels": kernels}
-    if args.variant:
-        result["config"]["variant_library"] = args.variant
 
     if not args.skip_extras:
         del sets
@@ -749,12 +780,17 @@ def main():
         full["decode"] = bench_decode(ctx)
         full["copy_ceiling"] = bench_copy(ctx)
         full["ceilings"] = bench_ceilings(ctx)
-        if not args.variant:  # the projection legs run the default library's launchers only
-            full["gate_up_silu"] = bench_gate_up(ctx)
-            full["gate_up_silu_prefill"] = bench_gate_up_prefill(ctx)
-            full["w8a16"] = bench_w8a16(ctx)
-            full["gate_up_silu_w8a16"] = bench_gate_up_w8(ctx)
-            full["linear16_down"] = bench_linear16(ctx)
+        full["gate_up_silu"] = bench_gate_up(ctx)
+        full["gate_up_silu_prefill"] = bench_gate_up_prefill(ctx)
+        full["w8a16"] = bench_w8a16(ctx)
+        full["gate_up_silu_w8a16"] = bench_gate_up_w8(ctx)
+        full["linear16_down"] = bench_linear16(ctx)
+        full["stage3"] = bench_stage3_table(ctx)
+        result["stage3_kernels"] = full["stage3"]
+        result["w8a16_decode"] = w8a16_decode_block(full["w8a16"])
+        if not args.skip_e2e:
+            full["e2e"] = bench_e2e_compact(ctx)
+            result["e2e_stage3"] = full["e2e"]
         result["roofline"]["per_config"] = per_config(full)
 
     if not args.skip_cpu:
@@ -770,6 +806,17 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def w8a16_decode_block(w8):
+    """The W8A16 linear at decode rows (<= 32), compact: graph-node us, GB/s
+    and fraction of 8 TB/s, and the speedup over fp16 hipBLASLt."""
+    out = {}
+    for key, e in w8.items():
+        if e["M"] <= 32:
+            out[key] = {"us": e["us"], "GBps": e["GBps"], "frac": e["frac_of_peak"],
+                        "vs_fp16_matmul": e.get("speedup_vs_fp16_matmul")}
+    return out
+
+
 def per_config(full):
     """The compact per-config block of the stdout line: each BASELINE config's
     kernel time, rate and fraction of 8 TB/s (cold), the same-size probe's
@@ -777,8 +824,8 @@ def per_config(full):
     keeps whole inside `roofline`."""
     k, c4, dec, ceil = full["kernels"], full["c4"], full["decode"], full.get("ceilings") or {}
 
-    def entry(d, probe_label=None, graph=None):
-        e = {"us": d["us"], "GBps": d["GBps"], "frac": d["frac_of_peak"]}
+    def entry(d, rows, probe_label=None, graph=None):
+        e = {"us": d["us"], "GBps": d["GBps"], "frac": d["frac_of_peak"], "rows_per_s": round(rows / d["us"] * 1e6)}
         if graph is not None:
             e["graph_us"] = graph["us"]
             e["graph_frac"] = graph["frac_of_peak"]
@@ -787,20 +834,25 @@ def per_config(full):
         return e
 
     pc = {
-        "C1_rmsnorm_f16_2048x1536": entry(k["c1_rmsnorm_f16_2048x1536"], "C1 RMSNorm [2048,1536] fp16",
+        "C1_rmsnorm_f16_2048x1536": entry(k["c1_rmsnorm_f16_2048x1536"], 2048, "C1 RMSNorm [2048,1536] fp16",
                                           k["c1_rmsnorm_f16_2048x1536_graph"]),
-        "C2_silu_mul_f16_2048x8960": entry(k["c2_silu_mul_f16_2048x8960"], "C2 SiLU-and-mul [2048,8960] fp16"),
-        "C4_rmsnorm_bf16_16384x3584": entry(c4["c4_rmsnorm_bf16_16384x3584"], "C4 RMSNorm [16384,3584] bf16"),
-        "C4_silu_mul_bf16_16384x18944": entry(c4["c4_silu_mul_bf16_16384x18944"],
+        "C2_silu_mul_f16_2048x8960": entry(k["c2_silu_mul_f16_2048x8960"], 2048,
+                                           "C2 SiLU-and-mul [2048,8960] fp16"),
+        "C4_rmsnorm_bf16_16384x3584": entry(c4["c4_rmsnorm_bf16_16384x3584"], 16384,
+                                            "C4 RMSNorm [16384,3584] bf16"),
+        "C4_silu_mul_bf16_16384x18944": entry(c4["c4_silu_mul_bf16_16384x18944"], 16384,
                                               "C4 SiLU-and-mul [16384,18944] bf16"),
     }
     c3 = {}
     for m, d in dec.items():
         if not m.startswith("M="):
             continue
+        rows = int(m[2:])
         c3["M" + m[2:]] = {"rms_api_us": d["rmsnorm_api_us"], "silu_api_us": d["silu_mul_api_us"],
                            "rms_dev_us": d["rmsnorm_device_us"], "silu_dev_us": d["silu_mul_device_us"],
-                           "graph_node_us": d["graph_per_kernel_us"], "graph_28_layers_us": d["graph_replay_us"]}
+                           "graph_node_us": d["graph_per_kernel_us"], "graph_28_layers_us": d["graph_replay_us"],
+                           "rms_rows_per_s": round(rows / d["rmsnorm_device_us"] * 1e6),
+                           "silu_rows_per_s": round(rows / d["silu_mul_device_us"] * 1e6)}
     pc["C3_decode_f16_latency"] = c3
     if "floor" in dec:
         pc["C3_floor"] = {"empty_graph_node_us": dec["floor"]["empty_kernel_graph_node_us"],
@@ -832,7 +884,7 @@ def run_only(ctx, args, sets):
     elif args.only == "c1-decomp":
         del sets
         torch.cuda.empty_cache()
-        print(json.dumps({"c1_decomposition": c1_decomposition(ctx), "variant": ctx.variant}), flush=True)
+        print(json.dumps({"c1_decomposition": c1_decomposition(ctx)}), flush=True)
     elif args.only == "copy":
         log(json.dumps(bench_copy(ctx)))
     elif args.only == "decode":
@@ -897,297 +949,26 @@ def run_only(ctx, args, sets):
                                        iters=iters, baselines=False)))
     elif args.only == "prefill-core":
         print(json.dumps(bench_prefill_core(ctx)), flush=True)
-
-
-def _sweep_leg(ctx, leg):
-    """Buffers of one sweep leg: (algorithmic bytes per launch, list of buffer
-    sets, make_calls(ctx) -> one launch closure per set, outputs of set 0)."""
-    torch = ctx.torch
-    F16, BF16 = torch.float16, torch.bfloat16
-    if leg in ("c1-rms", "c4-rms"):
-        M, N, dt = (2048, 1536, F16) if leg == "c1-rms" else (16384, 3584, BF16)
-        nbytes = (2 * M * N + N) * 2
-        w = rand(ctx, (N,), 1, dt, 1.0, 0.1)
-        sets = []
-        for s_ in range(n_sets(nbytes)):
-            x = rand(ctx, (M, N), 100 + s_, dt)
-            sets.append((x, torch.empty_like(x)))
-        return nbytes, sets, lambda c: [c.rms_call(x, w, y) for x, y in sets], lambda: [sets[0][1]]
-    if leg == "c1-add-rms":
-        M, N = 2048, 1536
-        nbytes = (4 * M * N + N) * 2
-        w = rand(ctx, (N,), 1, F16, 1.0, 0.1)
-        sets = []
-        for s_ in range(n_sets(nbytes)):
-            x, r = rand(ctx, (M, N), 700 + s_, F16), rand(ctx, (M, N), 800 + s_, F16)
-            sets.append((x, r, torch.empty_like(x), torch.empty_like(x)))
-        return (nbytes, sets, lambda c: [c.add_rms_call(x, r, w, y, h) for x, r, y, h in sets],
-                lambda: [sets[0][2], sets[0][3]])
-    M, I, dt = {"c2-silu": (2048, 8960, F16), "c4-silu": (16384, 18944, BF16), "silu-4096x8960": (4096, 8960, F16),
-                "silu-8192x8960": (8192, 8960, F16)}[leg]
-    nbytes = 3 * M * I * 2
-    sets = []
-    for s_ in range(n_sets(nbytes) if nbytes < MIN_FOOTPRINT else 1):
-        g, u = rand(ctx, (M, I), 200 + s_, dt), rand(ctx, (M, I), 300 + s_, dt)
-        sets.append((g, u, torch.empty_like(g)))
-    return nbytes, sets, lambda c: [c.silu_call(g, u, o) for g, u, o in sets], lambda: [sets[0][2]]
-
-
-SWEEP_ITERS = {"c1-rms": 2000, "c1-add-rms": 2000, "c4-rms": 200, "c2-silu": 500, "c4-silu": 30,
-               "silu-4096x8960": 300, "silu-8192x8960": 150}
-
-
-def run_sweep(ctx, args):
-    """A/B of launch-shape variants: the default library and each variant
-    library time the same legs on the same buffers, interleaved round by round
-    (so drift of the box's clocks hits every library alike); each variant's
-    outputs must equal the default library's bit for bit (the switches change
-    the launch shape, never the arithmetic), except the variants that reorder
-    a row's fp32 sum of squares (held to the oracle by
-    tests/test_launch_variants.py).  Prints one JSON line."""
-    torch = ctx.torch
-    names = list(args.sweep)
-    if names == ["all"]:
-        names = sorted(p.name[len("libmi355_fused_"):-3] for p in (ROOT / PKG / "_variants").glob("libmi355_fused_*.so"))
-    libs = {"default": ctx.lib}
-    for n in names:
-        libs[n] = ctx.L.load_variant(variant_lib(n))
-    reordering = importlib.import_module(PKG + ".build").REORDERING_VARIANTS
-    ctxs = {n: ctx.with_lib(l) for n, l in libs.items()}
-    out = {"variants": names, "rounds": args.sweep_rounds, "legs": {}}
-    for leg in args.sweep_legs:
-        nbytes, sets, make_calls, outputs = _sweep_leg(ctx, leg)
-        calls = {n: make_calls(c) for n, c in ctxs.items()}
-        calls["default"][0]()
-        torch.cuda.synchronize()
-        ref = [t.clone() for t in outputs()]
-        equal = {}
-        for n in names:
-            for t in outputs():
-                t.fill_(0)
-            calls[n][0]()
-            torch.cuda.synchronize()
-            equal[n] = all(torch.equal(a, b) for a, b in zip(ref, outputs()))
-        spin_up(ctx, calls["default"])
-        times = {n: [] for n in calls}
-        graph = {n: [] for n in calls} if leg.startswith("c1") else None
-        for _ in range(args.sweep_rounds):
-            for n in calls:
-                times[n].append(time_loop(ctxs[n], calls[n], SWEEP_ITERS[leg]))
-                if graph is not None:  # the copy's closures read its stream: capture through it
-                    graph[n].append(time_graph(ctxs[n], calls[n], 200))
-        base = statistics.median(times["default"])
-        rows = {}
-        for n in calls:
-            us = statistics.median(times[n])
-            rows[n] = {"us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
-                       "frac": round(nbytes / us / 1e3 / PEAK_GBS, 4), "vs_default": round(base / us, 4),
-                       "rounds_us": [round(t, 3) for t in times[n]]}
-            if graph is not None:
-                g = statistics.median(graph[n])
-                rows[n]["graph_us"] = round(g, 3)
-                rows[n]["graph_frac"] = round(nbytes / g / 1e3 / PEAK_GBS, 4)
-            if n != "default":
-                rows[n]["bitwise_equal_to_default"] = equal[n]
-                if n in reordering:  # another fp32 summation order: held to the oracle by the GPU tests
-                    rows[n]["reorders_sum"] = True
-            log(f"  sweep {leg} {n}: {rows[n]}")
-        out["legs"][leg] = {"bytes": nbytes, "buffer_sets": len(sets), "iters": SWEEP_ITERS[leg], "libs": rows}
-        del sets, calls, ref
+    elif args.only == "stage3":
+        del sets
         torch.cuda.empty_cache()
-    bad = [(leg, n) for leg, d in out["legs"].items() for n, r in d["libs"].items()
-           if r.get("bitwise_equal_to_default") is False and not r.get("reorders_sum")]
-    out["all_bitwise_equal"] = not bad
-    print(json.dumps(out), flush=True)
-    if bad:
-        log(f"sweep: outputs differ from the default library: {bad}")
-        sys.exit(1)
-
-
-# (rows, k, n, dtype, label): the 1.5B down, gate/up and q/o projections and
-# the 7B down and gate/up projections at decode rows.
-W8_SKINNY_SWEEP_SHAPES = [
-    (8, 8960, 1536, "f16", "down1.5b"), (1, 8960, 1536, "f16", "down1.5b"),
-    (8, 1536, 8960, "f16", "gateup1.5b"), (1, 1536, 8960, "f16", "gateup1.5b"),
-    (8, 1536, 1536, "f16", "o1.5b"),
-    (8, 18944, 3584, "bf16", "down7b"), (8, 3584, 18944, "bf16", "gateup7b"),
-    # 1-row 7B projections and the 7B o and 0.5B down projections
-    (1, 18944, 3584, "bf16", "down7b"), (1, 3584, 18944, "bf16", "gateup7b"),
-    (1, 3584, 3584, "bf16", "o7b"), (8, 3584, 3584, "bf16", "o7b"),
-    (1, 4864, 896, "f16", "down0.5b"), (8, 4864, 896, "f16", "down0.5b"),
-]
-
-
-def w8_skinny_sweep(ctx, only):
-    """The W8A16 decode kernel (w8a16_skinny) under forced launch shapes, on
-    the sweep builds: weight-row groups per workgroup G, waves per workgroup
-    (the split of K inside a workgroup), blocks in flight per wave U, and the
-    split of K over KS workgroups (partial sums meeting through device memory,
-    the last workgroup to arrive adding them in order), with the shipped main
-    loop (w8_skinny_sweep) and with U blocks kept in flight throughout
-    (w8_skinny_sweep_pipe, KS = 1).  Cold weights (rotating sets), hipGraph
-    timing; every shape's output is checked against the default library's
-    (fp32 order may differ: within 2e-3 of the largest output) and KS > 1
-    results for being the same bits on three calls.  Prints one JSON line."""
-    torch = ctx.torch
-    libs = {}
-    for name in ("w8_skinny_sweep", "w8_skinny_sweep_pipe"):
-        path = variant_lib(name)
-        if not path.exists():
-            raise SystemExit(f"{path} missing: python llm-inference-optimizer_amd/build.py --variant {name}")
-        lib = ctx.L.load_variant(path)
-        lib.mi355_w8_sweep_config.argtypes = [ctypes.c_int] * 4
-        lib.mi355_w8_sweep_config.restype = None
-        lib.mi355_w8_sweep_ks.argtypes = [ctypes.c_int]
-        lib.mi355_w8_sweep_ks.restype = ctypes.c_int
-        if lib.mi355_w8_sweep_ks(0) != 0:
-            raise SystemExit(f"{name}: the split-K scratch is not addressable")
-        libs[name] = lib
-    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
-    grid = [("w8_skinny_sweep", g, 1, sp, u) for g in (1, 2, 4, 8) for sp in (2, 3, 4, 6, 8, 12, 16) for u in (1, 2, 4)]
-    grid += [("w8_skinny_sweep", g, ks, sp, 1) for g in (1, 2, 4, 8) for ks in (2, 3, 4, 6, 8) for sp in (4, 8, 16)]
-    grid += [("w8_skinny_sweep_pipe", g, 1, sp, u) for g in (1, 2, 4) for sp in (2, 3, 4, 6, 8, 12, 16) for u in (2, 4)]
-    out = {"shapes": {}}
-    bad = []
-    for M, K, N, dn, lab in W8_SKINNY_SWEEP_SHAPES:
-        if only and lab not in only:
-            continue
-        dt = dts[dn]
-        sets = min(64, n_sets(N * K))
-        x = rand(ctx, (M, K), 1700 + M, dt)
-        g = torch.Generator(device=ctx.dev)
-        g.manual_seed(5)
-        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets)]
-        sc = [(torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
-        outs = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(4)]
-        ref = torch.empty((M, N), dtype=dt, device=ctx.dev)
-        ctx.w8a16_call(x, qs[0], sc[0], ref)()
-        ref_max = ref.float().abs().max().item()
-        base = [ctx.w8a16_call(x, q, s, outs[i % 4]) for i, (q, s) in enumerate(zip(qs, sc))]
-        spin_up(ctx, base)
-        t_default = time_graph(ctx, base, max(2 * sets, 64))
-        rows = []
-        for lname, G, KS, split, U in grid:
-            lib = libs[lname]
-            c = ctx.with_lib(lib)
-            lib.mi355_w8_sweep_config(G, U, split, 1)
-            lib.mi355_w8_sweep_ks(KS)
-            o = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(3)]
-            for oi in o:
-                c.w8a16_call(x, qs[0], sc[0], oi)()
-            torch.cuda.synchronize()
-            same_bits = all(torch.equal(o[0], oi) for oi in o[1:])
-            err = (o[0].float() - ref.float()).abs().max().item() / max(ref_max, 1e-6)
-            us = time_graph(c, [c.w8a16_call(x, q, s, outs[i % 4]) for i, (q, s) in enumerate(zip(qs, sc))],
-                            max(2 * sets, 64))
-            r = {"lib": lname, "G": G, "KS": KS, "waves": split, "U": U, "us": round(us, 3)}
-            rows.append(r)
-            if err > 2e-3 or not same_bits:
-                bad.append(dict(r, shape=f"{lab} M={M}", err=err, same_bits=same_bits))
-        for lib in libs.values():
-            lib.mi355_w8_sweep_config(0, 0, 0, 0)
-            lib.mi355_w8_sweep_ks(0)
-        best = min(rows, key=lambda r: r["us"])
-        by_ks = {ks: min(r["us"] for r in rows if r["KS"] == ks and r["lib"] == "w8_skinny_sweep")
-                 for ks in (1, 2, 3, 4, 6, 8)}
-        pipe_best = min(r["us"] for r in rows if r["lib"] == "w8_skinny_sweep_pipe")
-        key = f"{lab}_M{M}"
-        out["shapes"][key] = {"rows": M, "k": K, "n": N, "dtype": dn, "default_us": round(t_default, 3),
-                              "best": best, "best_us_by_KS": by_ks, "best_us_pipelined_loop": pipe_best,
-                              "configs": rows}
-        log(f"  w8 skinny sweep {key}: default {t_default:.2f} us; best {best}; by KS {by_ks}; "
-            f"pipelined loop best {pipe_best:.2f} us")
-        del qs, sc, base
+        print(json.dumps({"stage3_kernels": bench_stage3_table(ctx)}), flush=True)
+    elif args.only == "e2e-compact":
+        del sets
         torch.cuda.empty_cache()
-    out["mismatches"] = bad
-    print(json.dumps(out), flush=True)
-    if bad:
-        log(f"w8 skinny sweep: results off or not reproducible: {bad[:5]}")
-        sys.exit(1)
-
-
-# (rows, k, n_out, dtype, label): the int8 gate/up + SiLU-and-mul kernel at
-# decode rows of the Qwen2.5-1.5B and 7B MLPs
-W8_DUAL_SKINNY_SWEEP_SHAPES = [
-    (8, 1536, 8960, "f16", "gateup1.5b"), (1, 1536, 8960, "f16", "gateup1.5b"),
-    (8, 3584, 18944, "bf16", "gateup7b"), (1, 3584, 18944, "bf16", "gateup7b"),
-    (4, 1536, 8960, "f16", "gateup1.5b"), (2, 3584, 18944, "bf16", "gateup7b"),
-    (8, 896, 4864, "bf16", "gateup0.5b"), (1, 896, 4864, "bf16", "gateup0.5b"),
-]
-
-
-def w8_dual_skinny_sweep(ctx):
-    """The int8 gate/up + SiLU-and-mul decode kernel (w8a16_skinny with two
-    weight matrices) under forced launch shapes of the w8_skinny_sweep build:
-    weight-row groups G, waves per workgroup, blocks in flight U, and a split
-    of K over KS workgroups.  Cold weights, hipGraph timing; every shape's
-    output is checked against the default library's (within 2e-3 of the
-    largest output) and for the same bits on three calls.  One JSON line."""
-    torch = ctx.torch
-    path = variant_lib("w8_skinny_sweep")
-    if not path.exists():
-        raise SystemExit(f"{path} missing: python llm-inference-optimizer_amd/build.py --variant w8_skinny_sweep")
-    lib = ctx.L.load_variant(path)
-    lib.mi355_w8_sweep_config.argtypes = [ctypes.c_int] * 4
-    lib.mi355_w8_sweep_config.restype = None
-    lib.mi355_w8_sweep_ks.argtypes = [ctypes.c_int]
-    lib.mi355_w8_sweep_ks.restype = ctypes.c_int
-    if lib.mi355_w8_sweep_ks(0) != 0:
-        raise SystemExit("w8_skinny_sweep: the split-K scratch is not addressable")
-    c = ctx.with_lib(lib)
-    dts = {"f16": torch.float16, "bf16": torch.bfloat16}
-    grid = [(g, 1, sp, u) for g in (1, 2, 4) for sp in (2, 3, 4, 6, 8, 12, 16) for u in (1, 2)]
-    grid += [(g, ks, sp, 1) for g in (1, 2, 4) for ks in (2, 4) for sp in (4, 8)]
-    out = {"shapes": {}}
-    bad = []
-    for M, K, N, dn, lab in W8_DUAL_SKINNY_SWEEP_SHAPES:
-        dt = dts[dn]
-        sets = min(32, n_sets(2 * N * K))
-        x = rand(ctx, (M, K), 1900 + M, dt)
-        g = torch.Generator(device=ctx.dev)
-        g.manual_seed(7)
-        w = [(torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8),
-              torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4,
-              torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8),
-              torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
-        outs = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(4)]
-        ref = torch.empty((M, N), dtype=dt, device=ctx.dev)
-        ctx.gate_up_w8_call(x, *w[0], ref)()
-        ref_max = ref.float().abs().max().item()
-        base = [ctx.gate_up_w8_call(x, *ws, outs[i % 4]) for i, ws in enumerate(w)]
-        spin_up(ctx, base)
-        t_default = time_graph(ctx, base, max(2 * sets, 64))
-        rows = []
-        for G, KS, split, U in grid:
-            lib.mi355_w8_sweep_config(G, U, split, 1)
-            lib.mi355_w8_sweep_ks(KS)
-            o = [torch.empty((M, N), dtype=dt, device=ctx.dev) for _ in range(3)]
-            for oi in o:
-                c.gate_up_w8_call(x, *w[0], oi)()
-            torch.cuda.synchronize()
-            same_bits = all(torch.equal(o[0], oi) for oi in o[1:])
-            err = (o[0].float() - ref.float()).abs().max().item() / max(ref_max, 1e-6)
-            us = time_graph(c, [c.gate_up_w8_call(x, *ws, outs[i % 4]) for i, ws in enumerate(w)],
-                            max(2 * sets, 64))
-            r = {"G": G, "KS": KS, "waves": split, "U": U, "us": round(us, 3)}
-            rows.append(r)
-            if err > 2e-3 or not same_bits:
-                bad.append(dict(r, shape=f"{lab} M={M}", err=err, same_bits=same_bits))
-        lib.mi355_w8_sweep_config(0, 0, 0, 0)
-        lib.mi355_w8_sweep_ks(0)
-        best = min(rows, key=lambda r: r["us"])
-        best_ks1 = min((r for r in rows if r["KS"] == 1), key=lambda r: r["us"])
-        key = f"{lab}_M{M}"
-        out["shapes"][key] = {"rows": M, "k": K, "n_out": N, "dtype": dn, "default_us": round(t_default, 3),
-                              "best": best, "best_ks1": best_ks1, "configs": rows}
-        log(f"  w8 dual skinny sweep {key}: default {t_default:.2f} us; best {best}; best at KS = 1 {best_ks1}")
-        del w, base
+        print(json.dumps({"e2e_stage3": bench_e2e_compact(ctx)}), flush=True)
+    elif args.only == "w8-stream-sweep":
+        del sets
         torch.cuda.empty_cache()
-    out["mismatches"] = bad
-    print(json.dumps(out), flush=True)
-    if bad:
-        log(f"w8 dual skinny sweep: results off or not reproducible: {bad[:5]}")
-        sys.exit(1)
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx)}), flush=True)
+    elif args.only == "w8-layouts":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8_stream_layouts": w8_layout_sweep(ctx)}), flush=True)
+    elif args.only == "w8-decomp":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_decode_decomposition": w8_decode_decomposition(ctx)}), flush=True)
 
 
 def c1_decomposition(ctx):
@@ -1240,6 +1021,274 @@ def c1_decomposition(ctx):
     out["us_for_80pct"] = round(nbytes / (0.8 * PEAK_GBS) / 1e3, 3)
     del sets, rms
     torch.cuda.empty_cache()
+    return out
+
+
+STAGE3_ROWS = (64, 256, 1024, 8192, 32768)
+
+
+def _time_per_call(torch, fn, trials=20, warmup=5):
+    """Mean device time of one call including its launch, timed as the
+    reference's benchmarks/run_stage3_kernels.py:34-49 times it: synchronize,
+    record an event, call, record, synchronize, per trial."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(trials):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    return statistics.mean(ts) * 1e3  # us
+
+
+def bench_stage3_table(ctx, rows=STAGE3_ROWS, hidden=1536, inter=8960, trials=20):
+    """The reference's Stage 3 kernel table (benchmarks/run_stage3_kernels.py:
+    52-121, results in benchmarks/results/stage3_kernels.json:4-93) on this
+    device: for each row count, the package's naive path (the unfused torch
+    ops of naive_rmsnorm_reference / naive_silu_mul_reference) against the
+    fused HIP kernel through the package's drop-in API (fused_rmsnorm /
+    fused_silu_mul: the C++ launcher allocates the output and launches), fp16,
+    per call including the launch, the same buffers every call (as the
+    reference), mean of `trials`.  `cold_us` is the fused kernel's device time
+    alone (C ABI, hipGraph nodes over buffer sets rotating over up to 1 GiB,
+    at most 512 sets).  GB/s and rows/s are from the per-call time; the
+    algorithmic bytes are RMSNorm (2 M N + N) * 2, SiLU-and-mul 3 M I * 2."""
+    torch = ctx.torch
+    pkg = ctx.pkg
+    F16 = torch.float16
+    out = {"rmsnorm_N1536": {}, "silu_mul_I8960": {}}
+    for M in rows:
+        x = rand(ctx, (M, hidden), 0, F16)
+        w = rand(ctx, (hidden,), 1, F16)
+        naive = _time_per_call(torch, lambda: pkg.naive_rmsnorm_reference(x, w), trials)
+        fused = _time_per_call(torch, lambda: pkg.fused_rmsnorm(x, w), trials)
+        nbytes = (2 * M * hidden + hidden) * 2
+        sets = min(512, n_sets(nbytes))
+        bufs = [(rand(ctx, (M, hidden), 10 + i, F16), torch.empty((M, hidden), dtype=F16, device=ctx.dev))
+                for i in range(sets)]
+        calls = [ctx.rms_call(a, w, b) for a, b in bufs]
+        spin_up(ctx, calls, ms=5.0)
+        cold = time_graph(ctx, calls, max(sets, 64))
+        del bufs, calls
+        out["rmsnorm_N1536"][str(M)] = {
+            "naive_us": round(naive, 2), "fused_us": round(fused, 2), "speedup": round(naive / fused, 2),
+            "GBps": round(nbytes / fused / 1e3, 1), "rows_per_s": round(M / fused * 1e6),
+            "cold_us": round(cold, 2), "cold_GBps": round(nbytes / cold / 1e3, 1)}
+        del x
+        gate = rand(ctx, (M, inter), 2, F16)
+        up = rand(ctx, (M, inter), 3, F16)
+        naive = _time_per_call(torch, lambda: pkg.naive_silu_mul_reference(gate, up), trials)
+        fused = _time_per_call(torch, lambda: pkg.fused_silu_mul(gate, up), trials)
+        nbytes = 3 * M * inter * 2
+        sets = min(512, n_sets(nbytes))
+        bufs = [(rand(ctx, (M, inter), 20 + i, F16), rand(ctx, (M, inter), 30 + i, F16),
+                 torch.empty((M, inter), dtype=F16, device=ctx.dev)) for i in range(sets)]
+        calls = [ctx.silu_call(g_, u_, o_) for g_, u_, o_ in bufs]
+        spin_up(ctx, calls, ms=5.0)
+        cold = time_graph(ctx, calls, max(sets, 64))
+        del bufs, calls, gate, up
+        torch.cuda.empty_cache()
+        out["silu_mul_I8960"][str(M)] = {
+            "naive_us": round(naive, 2), "fused_us": round(fused, 2), "speedup": round(naive / fused, 2),
+            "GBps": round(nbytes / fused / 1e3, 1), "rows_per_s": round(M / fused * 1e6),
+            "cold_us": round(cold, 2), "cold_GBps": round(nbytes / cold / 1e3, 1)}
+        log(f"  stage3 M={M}: rmsnorm {json.dumps(out['rmsnorm_N1536'][str(M)])}; "
+            f"silu_mul {json.dumps(out['silu_mul_I8960'][str(M)])}")
+    return out
+
+
+# The decomposed decode shapes: (label, rows, k, n) of the Qwen2.5-1.5B down
+# and gate/up projections.
+W8_DECOMP_SHAPES = [("down_M1", 1, 8960, 1536), ("down_M8", 8, 8960, 1536),
+                    ("gateup_M1", 1, 1536, 8960), ("gateup_M8", 8, 1536, 8960)]
+
+
+def w8_decode_decomposition(ctx):
+    """Where the W8A16 decode kernel's time goes, at the Qwen2.5-1.5B down
+    (k 8960, n 1536) and gate/up (k 1536, n 8960) projections with 1 and 8
+    rows of fp16 x, every figure a hipGraph node over cold weights (sets
+    rotating over >= 1 GiB): an empty kernel; the read floor (the weights'
+    bytes read by the copy probe's shape) and a copy moving the same bytes;
+    the kernel's own loads alone at its launch plan (csrc/probe/
+    w8_stream_plan.hip: the same descriptors, offsets and chunk split, no
+    MFMA, reduction or epilogue), the weights only and the weights with x;
+    and the kernel itself (through the C ABI)."""
+    torch = ctx.torch
+    F16 = torch.float16
+    cus = torch.cuda.get_device_properties(ctx.dev).multi_processor_count
+    out = {"empty_graph_node_us": round(time_graph(ctx, [ctx.empty_call()], 200, replays=20), 3)}
+    sink = torch.zeros(1024, dtype=torch.int32, device=ctx.dev)
+    for label, M, K, N in W8_DECOMP_SHAPES:
+        wbytes = N * K
+        sets = n_sets(wbytes)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(2100 + K)
+        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets)]
+        scales = [(torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
+        x = rand(ctx, (M, K), 2200 + M, F16)
+        o = torch.empty((M, N), dtype=F16, device=ctx.dev)
+        nodes = max(2 * sets, 64)
+
+        def graph_us(calls):
+            spin_up(ctx, calls, ms=5.0)
+            return round(time_graph(ctx, calls, nodes, replays=5), 3)
+
+        rpw, r4, waves, u = ctx.w8_stream_plan(M, K, N, False, cus)
+        d = {"M": M, "K": K, "N": N, "weight_bytes": wbytes, "weight_sets": sets,
+             "plan": {"rows_per_wg": rpw, "waves": waves, "chunks_in_flight": u, "workgroups": -(-N // rpw)}}
+        d["read_floor_us"] = graph_us([ctx.read_call(q, sink) for q in qs])
+        half = wbytes // 2 // 16 * 16
+        cbufs = [(q.view(-1)[:half], q.view(-1)[half:2 * half]) for q in qs]
+        d["same_size_copy_us"] = graph_us([ctx.copy_call(a, b) for a, b in cbufs])
+        del cbufs
+        d["weight_loads_us"] = graph_us([ctx.w8_stream_loads_call(x, q, sink, rpw, r4, waves, u, False) for q in qs])
+        d["weight_and_x_loads_us"] = graph_us([ctx.w8_stream_loads_call(x, q, sink, rpw, r4, waves, u, True)
+                                               for q in qs])
+        d["kernel_us"] = graph_us([ctx.w8a16_call(x, q, sc, o) for q, sc in zip(qs, scales)])
+        d["read_floor_GBps"] = round(wbytes / d["read_floor_us"] / 1e3, 1)
+        d["kernel_GBps"] = round((wbytes + 4 * N + 2 * M * (K + N)) / d["kernel_us"] / 1e3, 1)
+        d["kernel_over_weight_loads"] = round(d["kernel_us"] / d["weight_loads_us"], 3)
+        d["kernel_over_read_floor"] = round(d["kernel_us"] / d["read_floor_us"], 3)
+        out[label] = d
+        log(f"  w8 decomp {label}: " + json.dumps(d))
+        del qs, scales
+        torch.cuda.empty_cache()
+    return out
+
+
+# Load-layout sampling of the weight-stream probe at 8 rows of x: launch
+# shapes (rpw, waves, G, U) per projection, crossed with the weight lane
+# layouts WL, the x lane layouts XL (0 = no x) and the per-workgroup stagger.
+W8_LAYOUT_SHAPES = {
+    1536: [(6, 16, 1, 8), (8, 16, 1, 8)],
+    8960: [(8, 3, 1, 4), (16, 3, 2, 4), (32, 6, 4, 2)],
+}
+
+
+def w8_layout_sweep(ctx):
+    """The weight-stream probe (csrc/probe/w8_stream.hip) at the Qwen2.5-1.5B
+    down and gate/up projections with 8 rows of fp16 x, over its weight and x
+    lane layouts and the stagger: graph-node us, cold weights."""
+    torch = ctx.torch
+    sink = torch.zeros(1024, dtype=torch.int32, device=ctx.dev)
+    out = {}
+    for label, K, N in (("down", 8960, 1536), ("gateup", 1536, 8960)):
+        sets = n_sets(N * K)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(2300 + K)
+        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets)]
+        x = rand(ctx, (8, K), 2400, torch.float16)
+        nodes = max(2 * sets, 64)
+        res = {}
+        for rpw, wv, gg, uu in W8_LAYOUT_SHAPES[N]:
+            for wl in (0, 2, 3):
+                for xl in (0, 1, 2, 3):
+                    for st in (0, 1):
+                        calls = [ctx.w8_stream_call(q, sink, rpw, wv, gg, uu, layout=wl, x=x if xl else None,
+                                                    xl=xl or 1, stagger=st) for q in qs]
+                        spin_up(ctx, calls, ms=3.0)
+                        res[f"rpw{rpw}_w{wv}_G{gg}_U{uu}_WL{wl}_XL{xl}_S{st}"] = round(
+                            time_graph(ctx, calls, nodes, replays=5), 3)
+        out[label] = res
+        log(f"  w8 layouts {label}: {json.dumps(res)}")
+        del qs
+        torch.cuda.empty_cache()
+    return out
+
+
+def _w8_stream_shapes(nchunk, dual, mt4):
+    """Launch shapes (rpw, r4, waves, u) of the W8A16 decode kernel sampled by
+    w8_stream_sweep: rows per workgroup 4-16, 1-16 waves, 1 or 2 chunks in
+    flight, without the register-spilling combinations."""
+    out = []
+    for rpw in (4, 6, 8, 12, 16):
+        r4 = 1 if rpw <= 4 else (2 if rpw <= 8 else 4)
+        for waves in (1, 2, 3, 4, 6, 8, 12, 16):
+            if waves > nchunk:
+                continue
+            per_wave = -(-nchunk // waves)
+            for u in (1, 2):
+                if u > 1 and u > per_wave:
+                    continue
+                if dual and r4 == 4 and u >= 2:  # spills registers
+                    continue
+                out.append((rpw, r4, waves, u))
+    return out
+
+
+# (label, rows, k, n, dual) of the decode sweep: the Qwen2.5-1.5B projections
+# and MLP, then the 7B, 0.5B and small 1.5B projections.
+W8_STREAM_SWEEP_SHAPES = [
+    ("down_M1", 1, 8960, 1536, False), ("down_M8", 8, 8960, 1536, False),
+    ("gateup_M1", 1, 1536, 8960, False), ("gateup_M8", 8, 1536, 8960, False),
+    ("dual_gateup_M1", 1, 1536, 8960, True), ("dual_gateup_M8", 8, 1536, 8960, True),
+    ("down7b_M1", 1, 18944, 3584, False), ("down7b_M8", 8, 18944, 3584, False),
+    ("gateup7b_M1", 1, 3584, 18944, False), ("gateup7b_M8", 8, 3584, 18944, False),
+    ("o7b_M8", 8, 3584, 3584, False), ("down0.5b_M8", 8, 4864, 896, False),
+    ("o1.5b_M8", 8, 1536, 1536, False), ("kv1.5b_M8", 8, 1536, 256, False), ("o1.5b_M4", 4, 1536, 1536, False),
+    ("dual7b_M1", 1, 3584, 18944, True), ("dual7b_M8", 8, 3584, 18944, True), ("dual0.5b_M8", 8, 896, 4864, True),
+]
+
+
+def w8_stream_sweep(ctx):
+    """The W8A16 decode kernel (w8a16_stream) over launch shapes, through the
+    probe library's forced-shape entry point, at the Qwen2.5-1.5B down and
+    gate/up projections and the int8 gate/up + SiLU-and-mul MLP, 1 and 8 rows
+    of fp16 x: graph-node us over cold weights, each shape's output checked
+    against the library's (within 2e-3 of the largest output: the fp32
+    summation order differs with the split of K)."""
+    torch = ctx.torch
+    F16 = torch.float16
+    out = {}
+    for label, M, K, N, dual in W8_STREAM_SWEEP_SHAPES:
+        nq = 2 if dual else 1
+        sets = n_sets(nq * N * K)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(2500 + K + M)
+        qs = [torch.randint(-127, 128, (nq, N, K), generator=g, device=ctx.dev, dtype=torch.int8)
+              for _ in range(sets)]
+        scs = [(torch.rand(nq, N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
+        x = rand(ctx, (M, K), 2600 + M, F16)
+        o = torch.empty((M, N), dtype=F16, device=ctx.dev)
+        ref = torch.empty_like(o)
+        nodes = max(2 * sets, 64)
+        if dual:
+            lib_calls = [ctx.gate_up_w8_call(x, q[0], sc[0], q[1], sc[1], o) for q, sc in zip(qs, scs)]
+            ctx.gate_up_w8_call(x, qs[0][0], scs[0][0], qs[0][1], scs[0][1], ref)()
+        else:
+            lib_calls = [ctx.w8a16_call(x, q[0], sc[0], o) for q, sc in zip(qs, scs)]
+            ctx.w8a16_call(x, qs[0][0], scs[0][0], ref)()
+        torch.cuda.synchronize()
+        spin_up(ctx, lib_calls, ms=5.0)
+        res = {"library_us": round(time_graph(ctx, lib_calls, nodes, replays=5), 3)}
+        tol = 2e-3 * ref.float().abs().max().item()
+        bad = []
+        nchunk = -(-K // 256)
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, 1 if M <= 4 else 2):
+            def mk(q, sc):
+                if dual:
+                    return ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u, q[1], sc[1])
+                return ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u)
+            calls = [mk(q, sc) for q, sc in zip(qs, scs)]
+            calls[0]()
+            torch.cuda.synchronize()
+            err = (o.float() - ref.float()).abs().max().item()
+            if not err <= tol:
+                bad.append((rpw, r4, waves, u, err))
+            spin_up(ctx, calls, ms=3.0)
+            res[f"rpw{rpw}_w{waves}_u{u}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
+        best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
+        out[label] = {"best": best, "best_us": res[best], "library_us": res["library_us"], "mismatches": bad,
+                      "shapes": res}
+        log(f"  w8 stream sweep {label}: library {res['library_us']} us, best {best} {res[best]} us, "
+            f"{len(bad)} mismatches {bad[:3]}")
+        del qs, scs
+        torch.cuda.empty_cache()
     return out
 
 
@@ -1505,7 +1554,7 @@ GATE_UP_W8_PREFILL_SHAPES = [(1024, 1536, 8960, "f16", "qwen2.5-1.5b"), (4096, 1
 
 def bench_gate_up_w8(ctx, shapes=GATE_UP_W8_SHAPES, iters=300, baselines=True):
     """Int8 gate/up projections + SiLU-and-mul (one kernel, through its C ABI
-    entry point, so a --variant library's kernels are the ones timed) against
+    entry point) against
     the quantised model's chain: two W8A16 linears (this build's kernel, each
     rounded to x's dtype) and the SiLU-and-mul kernel.  Per-layer int8
     weight sets with a footprint above 1 GiB; eager back-to-back and hipGraph
@@ -1794,6 +1843,90 @@ def bench_ceilings(ctx, iters=200):
     return out
 
 
+def _e2e_model(torch, dev):
+    """A random-init Qwen2 with Qwen2.5-1.5B's architecture (28 layers, hidden
+    1536, intermediate 8960, 12 / 2 heads, vocab 151936) in fp16 on `dev`,
+    sdpa attention: the reference's e2e model without Hub access."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
+                      num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=32768,
+                      rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    return model.half().eval()
+
+
+def _e2e_run(torch, model, ids, gen_len):
+    """One prefill (TTFT, ms, event-timed) and gen_len - 1 greedy decode steps
+    over HF's KV cache (tokens/s), as the reference's profiler times them
+    (src/engine/profiler.py:72-204)."""
+    with torch.inference_mode():
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        out = model(input_ids=ids, use_cache=True)
+        past = out.past_key_values
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        s1.record()
+        torch.cuda.synchronize()
+        d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        d0.record()
+        for _ in range(gen_len - 1):
+            out = model(input_ids=tok, past_key_values=past, use_cache=True)
+            past = out.past_key_values
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        d1.record()
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1), (gen_len - 1) / (d0.elapsed_time(d1) / 1e3)
+
+
+def _e2e_prompt(torch, model, S, dev):
+    g = torch.Generator()
+    g.manual_seed(S)
+    return torch.randint(0, model.config.vocab_size, (1, S), generator=g).to(dev)
+
+
+def _e2e_measure(torch, model, seq_lens, gen_len, trials, dev, tag, warmup=2):
+    """{S: (mean TTFT ms, mean decode tok/s)} over `trials` runs after `warmup`."""
+    res = {}
+    for S in seq_lens:
+        ids = _e2e_prompt(torch, model, S, dev)
+        for _ in range(warmup):
+            _e2e_run(torch, model, ids, gen_len)
+        t = [_e2e_run(torch, model, ids, gen_len) for _ in range(trials)]
+        res[S] = (statistics.mean(x[0] for x in t), statistics.mean(x[1] for x in t))
+        log(f"  {tag} seq {S}: TTFT {res[S][0]:.2f} ms, decode {res[S][1]:.1f} tok/s")
+    return res
+
+
+def bench_e2e_compact(ctx, seq_lens=(128, 512, 1024, 2048), gen_len=32, trials=3):
+    """The reference's Stage 3 end-to-end table (benchmarks/run_stage3_e2e.py:
+    33-108, results in benchmarks/results/stage3_e2e.json:9-39) in the
+    default bench run: TTFT and decode tokens/s at batch 1, 32 generated
+    tokens, before and after patch_model_with_fused_kernels (57 RMSNorm, 28
+    MLP replacements) on the same model instance, mean of `trials` runs after
+    2 warm-up runs per sequence length."""
+    torch = ctx.torch
+    model = _e2e_model(torch, ctx.dev)
+    for S in seq_lens:
+        _e2e_run(torch, model, _e2e_prompt(torch, model, S, ctx.dev), 4)
+    before = _e2e_measure(torch, model, seq_lens, gen_len, trials, ctx.dev, "e2e before")
+    counts = ctx.pkg.patch_model_with_fused_kernels(model)
+    after = _e2e_measure(torch, model, seq_lens, gen_len, trials, ctx.dev, "e2e after")
+    del model
+    torch.cuda.empty_cache()
+    return {"model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16, sdpa, batch 1", "gen_len": gen_len,
+            "trials": trials, "patched": counts, "seq_len": list(seq_lens),
+            "ttft_ms_before": [round(before[S][0], 2) for S in seq_lens],
+            "ttft_ms_after": [round(after[S][0], 2) for S in seq_lens],
+            "ttft_speedup": [round(before[S][0] / after[S][0], 3) for S in seq_lens],
+            "decode_tok_s_before": [round(before[S][1], 1) for S in seq_lens],
+            "decode_tok_s_after": [round(after[S][1], 1) for S in seq_lens],
+            "decode_speedup": [round(after[S][1] / before[S][1], 3) for S in seq_lens]}
+
+
 def bench_e2e(args):
     """TTFT and decode throughput before/after the module replacement, as the
     reference measures them (benchmarks/run_stage3_e2e.py:33-108 with
@@ -1802,54 +1935,21 @@ def bench_e2e(args):
     `trials` after `warmup` runs.  The model is a random-init Qwen2 with
     Qwen2.5-1.5B's architecture in fp16 (no Hub access here), sdpa attention."""
     import torch
-    from transformers import Qwen2Config, Qwen2ForCausalLM
 
     sys.path.insert(0, str(ROOT))
     pkg = importlib.import_module(PKG)
     dev = torch.device("cuda:0")
-    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
-                      num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=32768,
-                      rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True, attn_implementation="sdpa")
-    torch.manual_seed(0)
-    with torch.device(dev):
-        model = Qwen2ForCausalLM(cfg)
-    model = model.half().eval()
+    model = _e2e_model(torch, dev)
+    cfg = model.config
 
     def run(ids, gen_len):
-        with torch.inference_mode():
-            torch.cuda.synchronize()
-            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s0.record()
-            out = model(input_ids=ids, use_cache=True)
-            past = out.past_key_values
-            tok = out.logits[:, -1].argmax(-1, keepdim=True)
-            s1.record()
-            torch.cuda.synchronize()
-            d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            d0.record()
-            for _ in range(gen_len - 1):
-                out = model(input_ids=tok, past_key_values=past, use_cache=True)
-                past = out.past_key_values
-                tok = out.logits[:, -1].argmax(-1, keepdim=True)
-            d1.record()
-            torch.cuda.synchronize()
-            return s0.elapsed_time(s1), (gen_len - 1) / (d0.elapsed_time(d1) / 1e3)
+        return _e2e_run(torch, model, ids, gen_len)
 
     def prompt(S):
-        g = torch.Generator()
-        g.manual_seed(S)
-        return torch.randint(0, cfg.vocab_size, (1, S), generator=g).to(dev)
+        return _e2e_prompt(torch, model, S, dev)
 
     def measure(tag):
-        res = {}
-        for S in args.seq_lens:
-            ids = prompt(S)
-            for _ in range(2):
-                run(ids, args.gen_len)
-            t = [run(ids, args.gen_len) for _ in range(args.trials)]
-            res[S] = (statistics.mean(x[0] for x in t), statistics.mean(x[1] for x in t))
-            log(f"  {tag} seq {S}: TTFT {res[S][0]:.2f} ms, decode {res[S][1]:.1f} tok/s")
-        return res
+        return _e2e_measure(torch, model, args.seq_lens, args.gen_len, args.trials, dev, tag)
 
     def graphed_decode_tok_s(S=512, new=64, B=1):
         """Decode tokens/s (B per step) with the whole decode step replayed as

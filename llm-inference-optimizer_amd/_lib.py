@@ -95,17 +95,6 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
-def load_variant(path) -> ctypes.CDLL:
-    """A separately built copy of the kernel library (`build.py -D... --out
-    <path>`: the same kernels with other launch-shape switches), declared like
-    the default one but not cached.  For side-by-side timing; the package's
-    launchers always use the default library."""
-    path = Path(path).resolve()
-    if not path.exists():
-        raise KernelLibraryMissing(f"{path} is not built")
-    return _declare(ctypes.CDLL(str(path)), path)
-
-
 def ext():
     """The host-side launchers (``_mi355_torch``, a torch extension over this
     library's C ABI; see csrc/torch_launchers.cpp), loaded once.  Raises

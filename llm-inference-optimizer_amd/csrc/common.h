@@ -242,12 +242,7 @@ __device__ __forceinline__ void store_chunk(void* p, const float (&f)[W]) {
 // Cache policy (aux) bits on gfx950: 1 = sc0, 2 = nt, 16 = sc1.  nt (streaming)
 // on loads and stores measured fastest for these single-pass kernels.
 // ---------------------------------------------------------------------------
-#ifndef MI355_LOAD_AUX
-#define MI355_LOAD_AUX 2
-#endif
-#ifndef MI355_STORE_AUX
-#define MI355_STORE_AUX 2
-#endif
+constexpr int kStreamAux = 2;  // nt
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
@@ -255,7 +250,7 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, MI355_LOAD_AUX);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kStreamAux);
 }
 __device__ __forceinline__ u32x4 buf_load16_cached(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
@@ -264,10 +259,10 @@ __device__ __forceinline__ u32x2 buf_load8_cached(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
 }
 __device__ __forceinline__ void buf_store16(rsrc_t r, uint32_t off, u32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, MI355_STORE_AUX);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStreamAux);
 }
 __device__ __forceinline__ void buf_store8(rsrc_t r, uint32_t off, u32x2 v) {
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, MI355_STORE_AUX);
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kStreamAux);
 }
 
 // W elements of T at byte offset `off` of buffer r, loaded as raw dwords

@@ -54,9 +54,6 @@
 //     workgroups), U 6 (one load group per wave at k = 1536; U 4 for
 //     k <= 1024);
 //   otherwise SPLITK 4, G 2 (x read once per 16 weight rows), U 2.
-#ifndef MI355_GU_FORCE
-#define MI355_GU_FORCE 0  // 1: always the first shape, 2: always the second (sweeps)
-#endif
 
 namespace mi355 {
 namespace {
@@ -223,30 +220,16 @@ int gate_up_launch_tiles(const GateUpParams& p, hipStream_t s) {
 
 template <typename T, typename TO, int MT>
 int gate_up_shape(const GateUpParams& p, hipStream_t s) {
-  if (MT == 1 && (MI355_GU_FORCE == 1 || (MI355_GU_FORCE == 0 && p.k <= 2048 && p.n_out < 16384))) {
+  if (MT == 1 && p.k <= 2048 && p.n_out < 16384) {
     if (p.k <= 1024) return gate_up_launch_tiles<T, TO, 1, 4, 1, 4>(p, s);
     return gate_up_launch_tiles<T, TO, 1, 4, 1, 6>(p, s);
   }
   return gate_up_launch_tiles<T, TO, MT, 4, 2, 2>(p, s);
 }
 
-// MI355_GU_ROUNDS_BY_COLUMNS = 1: the column split's whole rounds hold only
-// whole 128-column blocks of every row block (cus / row blocks of them per
-// round; a measurement switch for variant builds).
-#ifndef MI355_GU_ROUNDS_BY_COLUMNS
-#define MI355_GU_ROUNDS_BY_COLUMNS 0
-#endif
-// MI355_GU_GROUP_M: m-blocks per group of the tile order inside each XCD's
-// range (m fastest within a group; a measurement switch for variant builds).
-#ifndef MI355_GU_GROUP_M
-#define MI355_GU_GROUP_M 4
-#endif
-// MI355_GU_REST_SHAPE = f > 0: the column split's remaining columns take
-// shape f of the plan below whenever it covers them in one round (a
-// measurement switch for variant builds).
-#ifndef MI355_GU_REST_SHAPE
-#define MI355_GU_REST_SHAPE 0
-#endif
+// m-blocks per group of the tiled GEMM's tile order inside each XCD's range
+// (m fastest within a group).
+constexpr int kGuGroupM = 4;
 
 template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int RING = 0, int XR = 0>
 int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
@@ -275,7 +258,7 @@ int gate_up_tiled_cfg(const GateUpParams& p, hipStream_t s) {
   tp.bdt = -1;
   tp.tiles_m = (p.rows + C::BM - 1) / C::BM;
   tp.tiles_n = (p.n_out + C::BN - 1) / C::BN;
-  tp.group_m = tp.tiles_m < MI355_GU_GROUP_M ? tp.tiles_m : MI355_GU_GROUP_M;
+  tp.group_m = tp.tiles_m < kGuGroupM ? tp.tiles_m : kGuGroupM;
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_16, TO, WGM, WGN, FM, FN,
@@ -346,14 +329,8 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
   // them (a round need not end at a column boundary: the head launch's
   // tiles fill its rounds in order)
   const int64_t tiles_m = cdiv(p.rows, 256);
-#if MI355_GU_ROUNDS_BY_COLUMNS
-  const int64_t per_round = cus / tiles_m;  // 128-column blocks of one whole round
-  const int64_t full = per_round > 0 ? cdiv(p.n_out, 128) / per_round : 0;
-  const int lead = static_cast<int>(full * per_round * 128);
-#else
   const int64_t full = cdiv(p.n_out, 128) * tiles_m / cus;
   const int lead = static_cast<int>(full * cus / tiles_m * 128);  // columns in whole rounds
-#endif
   if (full >= 1 && lead > 0 && lead < p.n_out) {
     const int rest = p.n_out - lead;
     const auto one_round = [&](int bm, int bn, int per_cu) { return rounds(p.rows, rest, bm, bn, per_cu) <= 1.0; };
@@ -363,14 +340,6 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
     else if (one_round(128, 64, 1)) shape = 2, rest_cost = 1.0;
     else if (one_round(128, 64, 2)) shape = 3, rest_cost = 1.05;
     else if (one_round(256, 64, 1)) shape = 4, rest_cost = 1.0;
-#if MI355_GU_REST_SHAPE > 0
-    {
-      // measurement switch: the rest in shape MI355_GU_REST_SHAPE when it fits one round
-      // (5: 128 x 128, 8 waves, 3-stage step pipeline)
-      constexpr int f = MI355_GU_REST_SHAPE;
-      if (shape != 0 && one_round(f == 1 ? 64 : (f == 4 ? 256 : 128), f == 5 ? 128 : 64, f == 3 ? 2 : 1)) shape = f;
-    }
-#endif
     if (shape != 0 && 1.72 * static_cast<double>(full) + rest_cost < single) {
       GateUpParams head = p, tail = p;
       head.n_out = lead;
@@ -384,9 +353,6 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
       if (shape == 1) return gate_up_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(tail, s);
       if (shape == 2) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 4>(tail, s);
       if (shape == 3) return gate_up_tiled_cfg<T, TO, 2, 2, 2, 1, 2, 1>(tail, s);
-#if MI355_GU_REST_SHAPE > 0
-      if (shape == 5) return gate_up_tiled_cfg<T, TO, 2, 4, 2, 1, 3>(tail, s);
-#endif
       return gate_up_tiled_cfg<T, TO, 4, 2, 2, 1, 3>(tail, s);
     }
   }

@@ -193,19 +193,6 @@ int launch_l16(K kernel, dim3 grid, dim3 block, size_t lds, const L16Params& p, 
                     "linear16 launch");
 }
 
-#ifdef MI355_L16_SWEEP
-// Sweep builds only: force the skinny launch shape (0 = automatic).
-int g_force_g = 0, g_force_u = 0, g_force_split = 0, g_force_path = 0;
-}  // namespace
-extern "C" __attribute__((visibility("default"))) void mi355_l16_sweep_config(int g, int u, int split, int path) {
-  g_force_g = g;
-  g_force_u = u;
-  g_force_split = split;
-  g_force_path = path;
-}
-namespace {
-#endif
-
 // Skinny launch shape, fitted to a sweep of G x U x waves per workgroup on
 // MI355X over the down, o and q projections of Qwen2.5-0.5B, 1.5B and 7B at
 // 1, 8 and 32 rows (every pick within 1.06x of the best sampled shape):
@@ -228,10 +215,6 @@ int l16_skinny_g(const L16Params& p, hipStream_t s, int cus) {
   const int64_t units = static_cast<int64_t>(groups) * tiles;
   int split = p.rows <= 1 ? 16 / G : 8;
   int u = MT == 1 ? 2 : 1;
-#ifdef MI355_L16_SWEEP
-  if (g_force_split > 0) split = g_force_split;
-  if (g_force_u > 0) u = g_force_u;
-#endif
   if (split > kMaxSplit) split = kMaxSplit;
   if (split > 64 / (G * MT)) split = 64 / (G * MT);  // partial sums: split * G * MT KiB <= 64 KiB
   if (split > nblk) split = nblk;
@@ -252,20 +235,13 @@ int l16_skinny_g(const L16Params& p, hipStream_t s, int cus) {
   // register budget (128 VGPRs at 1024 threads): U (4 G + 4 MT) operand
   // dwords + 4 G MT accumulators <= 100
   constexpr int umax = (100 - 4 * G * MT) / (4 * G + 4 * MT);
-#ifdef MI355_L16_SWEEP
-  if (u >= 4 && umax >= 4) return launch_l16(linear16_skinny<T, TO, MT, G, (umax >= 4 ? 4 : 1)>, grid, block, lds, p, s);
-#endif
   if (u >= 2 && umax >= 2) return launch_l16(linear16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1)>, grid, block, lds, p, s);
   return launch_l16(linear16_skinny<T, TO, MT, G, 1>, grid, block, lds, p, s);
 }
 
 template <typename T, typename TO, int MT>
 int l16_skinny_shape(const L16Params& p, hipStream_t s, int cus) {
-  int g = (p.n + 15) / 16 >= (3 * cus) / 4 ? 2 : 1;
-#ifdef MI355_L16_SWEEP
-  if (g_force_g > 0) g = g_force_g;
-  if (g >= 4) return l16_skinny_g<T, TO, MT, 4>(p, s, cus);
-#endif
+  const int g = (p.n + 15) / 16 >= (3 * cus) / 4 ? 2 : 1;
   if (g >= 2) return l16_skinny_g<T, TO, MT, 2>(p, s, cus);
   return l16_skinny_g<T, TO, MT, 1>(p, s, cus);
 }
@@ -352,11 +328,7 @@ int l16_typed(const L16Params& p, hipStream_t s, int cus) {
   // tiles with split K re-read 16-bit weights per tile: at 96 - 256 rows of
   // the Qwen2.5-1.5B / 7B down and o projections 1.7 - 4.0x slower than the
   // tiled GEMM even on small grids, e.g. 7B down, 256 rows 350.9 vs 87.8 us.)
-  bool skinny = !l16_tiled_fits(p);
-#ifdef MI355_L16_SWEEP
-  if (g_force_path > 0) skinny = g_force_path == 1;
-#endif
-  if (skinny) return l16_skinny_shape<T, TO, 4>(p, s, cus);
+  if (!l16_tiled_fits(p)) return l16_skinny_shape<T, TO, 4>(p, s, cus);
   return l16_tiled<T, TO>(p, s);
 }
 

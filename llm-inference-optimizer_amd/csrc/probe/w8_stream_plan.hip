@@ -1,0 +1,145 @@
+// Measurement helpers, not part of the kernel ABI: the W8A16 decode kernel
+// (w8a16_stream.h, the same source the library compiles) launched with a
+// launch shape chosen by the caller instead of its launch plan, so bench.py
+// can time the plan against other shapes on the same inputs (fp16 x and
+// output, fp32 scales, no bias); the plan itself; and the kernel's loads
+// alone at a launch shape, for the decomposition of its time.
+#include <cstdarg>
+#include <cstdio>
+
+#include "../w8a16_stream.h"
+
+namespace mi355 {
+// The library's set_error keeps a per-thread message; here a failing launch
+// is reported through the status code alone.
+void set_error(const char*, ...) {}
+}  // namespace mi355
+
+namespace {
+
+// The loads of w8a16_stream at launch shape (rpw, waves, U), and nothing
+// else: the same descriptors, lane offsets, chunk split and U-chunk groups,
+// every loaded dword folded into one XOR that guards a store the data never
+// trigger (so no load can be dropped); without X only the weights.
+template <int R4, int MT4, int U, bool X>
+__global__ __launch_bounds__(1024) void w8a16_stream_loads(const mi355::W8Params p, const int rpw,
+                                                           uint32_t* sink) {
+  using namespace mi355;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwave = blockDim.x >> 6;
+  const int n0 = blockIdx.x * rpw;
+  const int nrows_w = p.n - n0 < rpw ? p.n - n0 : rpw;
+  const rsrc_t rq = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
+                              static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((p.rows - 1) * p.xs + p.k) * 2));
+  const int quad = lane & 3, set_row = (lane & 15) >> 2, kg = lane >> 4;
+  const int piece = 16 * quad + 64 * kg;
+  uint32_t qoff[R4], xoff[MT4];
+#pragma unroll
+  for (int r = 0; r < R4; ++r) qoff[r] = static_cast<uint32_t>((4 * r + set_row) * p.qs + piece);
+#pragma unroll
+  for (int t = 0; t < MT4; ++t) xoff[t] = static_cast<uint32_t>(((4 * t + set_row) * p.xs + piece) * 2);
+  const int nchunk = (p.k + 255) >> 8;
+  const int c0 = (nchunk * wave) / nwave, c1 = (nchunk * (wave + 1)) / nwave;
+  uint32_t h = 0;
+  for (int c = c0; c < c1; c += U) {
+    u32x4 wq[U][R4], xa[U][MT4][2];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const bool live = c + j < c1 && 256 * (c + j) + piece < p.k;
+#pragma unroll
+      for (int r = 0; r < R4; ++r) wq[j][r] = buf_load16(rq, live ? qoff[r] + 256u * (c + j) : kOob);
+      if constexpr (X) {
+#pragma unroll
+        for (int t = 0; t < MT4; ++t) {
+          const uint32_t o = xoff[t] + 512u * (c + j);
+          xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
+          xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+#pragma unroll
+      for (int r = 0; r < R4; ++r) h ^= (wq[j][r].x ^ wq[j][r].y) ^ (wq[j][r].z ^ wq[j][r].w);
+      if constexpr (X) {
+#pragma unroll
+        for (int t = 0; t < MT4; ++t)
+          h ^= (xa[j][t][0].x ^ xa[j][t][0].w) ^ (xa[j][t][1].y ^ xa[j][t][1].z) ^ (xa[j][t][0].y ^ xa[j][t][0].z) ^
+               (xa[j][t][1].x ^ xa[j][t][1].w);
+      }
+    }
+  }
+  if (h == 0x9e3779b9u) sink[threadIdx.x] = h;
+}
+
+template <int R4, int MT4, bool X>
+const void* loads_kernel(int u) {
+  if (u >= 2) return reinterpret_cast<const void*>(w8a16_stream_loads<R4, MT4, 2, X>);
+  return reinterpret_cast<const void*>(w8a16_stream_loads<R4, MT4, 1, X>);
+}
+
+template <bool X>
+const void* loads_kernel_r4(int r4, int mt4, int u) {
+  if (r4 == 4) return mt4 == 1 ? loads_kernel<4, 1, X>(u) : loads_kernel<4, 2, X>(u);
+  if (r4 == 2) return mt4 == 1 ? loads_kernel<2, 1, X>(u) : loads_kernel<2, 2, X>(u);
+  return mt4 == 1 ? loads_kernel<1, 1, X>(u) : loads_kernel<1, 2, X>(u);
+}
+
+}  // namespace
+
+// The launch plan the library picks for `rows` x [n, k] int8 weights (dual:
+// two matrices) on a device with `cus` CUs: out4 = {rpw, r4, waves, u}.
+extern "C" __attribute__((visibility("default"))) void mi355_probe_w8a16_stream_plan(int rows, int k, int n, int dual,
+                                                                                   int cus, int* out4) {
+  const mi355::StreamPlan sp = mi355::w8_stream_plan(rows, k, n, dual != 0, cus);
+  out4[0] = sp.rpw;
+  out4[1] = sp.r4;
+  out4[2] = sp.waves;
+  out4[3] = sp.u;
+}
+
+// The loads of the W8A16 decode kernel alone (w8a16_stream_loads above) at
+// launch shape (rpw, r4, waves, u) for x [rows <= 8, k] fp16 and q [n, k]
+// int8: the weights only (with_x 0) or the weights and x (with_x 1).  `sink`
+// holds at least 1024 dwords.  Returns 0, -1 on bad arguments, -3 on a
+// launch error.
+extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_loads(
+    const void* x, const void* q, int rows, int k, int n, int rpw, int r4, int waves, int u, int with_x, void* sink,
+    void* stream) {
+  if (!x || !q || !sink || rows < 1 || rows > 8 || k < 16 || (k & 15) || n < 1 || rpw < 1 ||
+      (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2))
+    return -1;
+  const mi355::W8Params p{x, q, nullptr, nullptr, nullptr, rows, k, n, k, k, n, MI355_F32, -1, nullptr, nullptr};
+  const int mt4 = rows <= 4 ? 1 : 2;
+  const void* kern = with_x ? loads_kernel_r4<true>(r4, mt4, u) : loads_kernel_r4<false>(r4, mt4, u);
+  int rpw_arg = rpw;
+  void* args[] = {const_cast<mi355::W8Params*>(&p), &rpw_arg, &sink};
+  const unsigned grid = static_cast<unsigned>((n + rpw - 1) / rpw);
+  if (hipLaunchKernel(kern, dim3(grid), dim3(64 * waves), args, 0, static_cast<hipStream_t>(stream)) != hipSuccess)
+    return -3;
+  return 0;
+}
+
+// out [rows, n] = W8A16(x [rows, k], q [n, k], scale [n]) (q2 / scale2 not
+// NULL: the gate/up + SiLU-and-mul kernel with q, scale the gate and q2,
+// scale2 the up weights), launched with rpw weight rows per workgroup, r4
+// 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves and u chunks in flight
+// (1 or 2).  rows <= 8, k a multiple of 16, every pointer 16-byte
+// aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.
+extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
+    const void* x, const void* q, const void* scale, const void* q2, const void* scale2, void* out, int rows, int k,
+    int n, int rpw, int r4, int waves, int u, void* stream) {
+  if (!x || !q || !scale || !out || rows < 1 || rows > 8 || k < 16 || (k & 15) || n < 1 || rpw < 1 ||
+      (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2) ||
+      (!q2) != (!scale2))
+    return -1;
+  const mi355::W8Params p{x, q, scale, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, q2, scale2};
+  const mi355::StreamPlan sp{rpw, r4, waves, u};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int st = q2 ? mi355::w8_stream_launch<mi355::F16, mi355::F16, true>(p, sp, s)
+                    : mi355::w8_stream_launch<mi355::F16, mi355::F16, false>(p, sp, s);
+  return st == MI355_OK ? 0 : -3;
+}

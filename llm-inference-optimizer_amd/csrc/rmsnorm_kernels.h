@@ -24,9 +24,6 @@
 //   rmsnorm_generic     any n, alignment or dtype mix: scalar loads, two passes
 //                       over the row (the second pass re-reads the row through
 //                       L2).
-// (rmsnorm_block_stream, the workgroup-per-row kernel streaming its rows
-// through a persistent grid, is built only under MI355_RMS_STREAM_ROWS: it
-// measured slower than one workgroup per row.)
 // Rows and the weight are read through buffer descriptors that span exactly
 // one row, so the packets past n need no lane branches, with the non-temporal
 // hint on x, residual and the outputs.  All kernels stride over rows; the
@@ -36,30 +33,21 @@
 
 #include "common.h"
 
-// Threads per workgroup of the wave-per-row kernel above the decode sizes
-// (below them, 64: one wave per workgroup, so a few rows spread over CUs).
-#ifndef MI355_RMS_WAVE_BLOCK
-#define MI355_RMS_WAVE_BLOCK 256
-#endif
-// 1: let the compiler keep the fp32 widening of the row (and weight) from the
-// sum-of-squares pass live for the scaling pass, instead of re-widening the
-// packed 16-bit form there (fewer conversions, more VGPRs).  Measured on
-// MI355X: the workgroup-per-row kernel gains 1% at 16384 x 3584 bf16 (39.24
-// vs 39.62 us, 46 vs 37 VGPRs); the wave-per-row kernel does not gain.
-#ifndef MI355_RMS_KEEP_F32_WAVE
-#define MI355_RMS_KEEP_F32_WAVE 0
-#endif
-#ifndef MI355_RMS_KEEP_F32_BLOCK
-#define MI355_RMS_KEEP_F32_BLOCK 1
-#endif
-
 namespace mi355 {
 
-// Whether the workgroup-per-row kernels keep the fp32 widening of a lane's
-// `packets` row packets live between the passes: at most 4 packets (8 would
-// hold 64 fp32 values a lane and spill).
+// Threads per workgroup of the wave-per-row kernel above the decode sizes
+// (below them, 64: one wave per workgroup, so a few rows spread over CUs).
+constexpr int kRmsWaveBlock = 256;
+
+// Whether the workgroup-per-row kernel keeps the fp32 widening of a lane's
+// `packets` row packets (and weight) live from the sum-of-squares pass to the
+// scaling pass, instead of re-widening the packed 16-bit form there (fewer
+// conversions, more VGPRs): measured on MI355X, 1% faster at 16384 x 3584
+// bf16 (39.24 vs 39.62 us, 46 vs 37 VGPRs), for at most 4 packets (8 would
+// hold 64 fp32 values a lane and spill).  The wave-per-row kernel re-widens:
+// keeping fp32 there gains nothing.
 template <int packets>
-constexpr bool kKeepF32Block = MI355_RMS_KEEP_F32_BLOCK != 0 && packets <= 4;
+constexpr bool kKeepF32Block = packets <= 4;
 
 // Kernel parameters, passed by value.  r / ro / rs / ros are used with ADD only.
 struct RmsParams {
@@ -179,49 +167,21 @@ __device__ __forceinline__ void load_rows(RowSlice<TX, TW, VPL> (&row)[R], const
   }
 }
 
-// The lane's weight packets lane + 64 * k, k < VPL.  With WLDS the workgroup
-// first stages the weight row in LDS (each thread copies 16-byte pieces, so
-// the row is read from L2 once per workgroup instead of once per wave) and
-// every wave then reads its packets from there; otherwise each wave loads its
-// packets itself (an L2 hit after the first wave).  `lds` holds at least
-// 64 * VPL * WB bytes.
-template <typename TW, int W, int VPL, bool WLDS>
-__device__ __forceinline__ void load_weight(BufChunk<TW, W> (&wv)[VPL], const RmsParams& p, int lane,
-                                            uint32_t* lds) {
-  constexpr uint32_t WB = W * sizeof(typename TW::bits);
-  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
-  if constexpr (WLDS) {
-    constexpr uint32_t units = 64u * VPL * WB / 16u;
-    for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
-      const u32x4 v = buf_load16_cached(rw, u * 16u);
-      lds[4 * u] = v.x; lds[4 * u + 1] = v.y; lds[4 * u + 2] = v.z; lds[4 * u + 3] = v.w;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const uint32_t* q = lds + static_cast<uint32_t>(lane + 64 * k) * (WB / 4u);
-#pragma unroll
-      for (int d = 0; d < BufChunk<TW, W>::DW; ++d) wv[k].raw[d] = q[d];
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(lane + 64 * k) * WB);
-  }
-}
-
 // One wave64 per R rows (R consecutive rows per wave, all loaded before the
 // first reduction).  The grid is normally one-shot; the row loop only repeats
-// when the launcher caps the grid.  WLDS: stage the weight through LDS (the
-// launcher passes 64 * VPL * WB bytes of dynamic LDS).
-template <typename TX, typename TW, typename TY, int VPL, int R, bool ADD, bool WLDS>
-__global__ __launch_bounds__(MI355_RMS_WAVE_BLOCK) void rmsnorm_wave_rows(const RmsParams p) {
+// when a grid is capped.  Each lane loads its weight packets lane + 64 k,
+// k < VPL, once (an L2 hit after the first wave) and reuses them for every
+// row it visits.
+template <typename TX, typename TW, typename TY, int VPL, int R, bool ADD>
+__global__ __launch_bounds__(kRmsWaveBlock) void rmsnorm_wave_rows(const RmsParams p) {
   using S = RowSlice<TX, TW, VPL>;
-  extern __shared__ uint32_t wlds[];
   const int lane = threadIdx.x & 63;
   const int waves_per_block = blockDim.x >> 6;
 
   BufChunk<TW, S::W> wv[VPL];
-  load_weight<TW, S::W, VPL, WLDS>(wv, p, lane, wlds);
+  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(lane + 64 * k) * S::WB);
 
   // The wave's index in its workgroup is wave-uniform; readfirstlane says so,
   // which keeps the row's buffer descriptors in SGPRs (no waterfall loop).
@@ -237,7 +197,7 @@ __global__ __launch_bounds__(MI355_RMS_WAVE_BLOCK) void rmsnorm_wave_rows(const 
     for (int i = 0; i < R; ++i) ss[i] = wave_allreduce_sum(ss[i]);
 #pragma unroll
     for (int i = 0; i < R; ++i)
-      row[i].template store_y<TY, MI355_RMS_KEEP_F32_WAVE != 0>(
+      row[i].template store_y<TY, false>(
           make_rsrc(static_cast<typename TY::bits*>(p.y) + (r0 + i) * p.ys, row_bytes<TY>(p, r0 + i)), lane, 64,
           rms_rstd(ss[i], p.n, p.eps), wv);
   }
@@ -288,63 +248,6 @@ __global__ __launch_bounds__(1024) void rmsnorm_block_rows(const RmsParams p) {
       row[i].template store_y<TY, kKeepF32Block<VPL * R>>(
           make_rsrc(static_cast<typename TY::bits*>(p.y) + (r0 + i) * p.ys, row_bytes<TY>(p, r0 + i)), tid,
           nthreads, rms_rstd(tot[i], p.n, p.eps), wv);
-  }
-}
-
-// Workgroup-per-row kernel on a persistent grid that streams its rows: the
-// workgroup visits rows blockIdx.x + i * gridDim.x and keeps S of them in
-// flight in a ring of register slots, refilling a slot with the row S visits
-// ahead as soon as its own row is stored.  Per row the arithmetic and the
-// reduction order are rmsnorm_block_rows' (so are the bits); what changes is
-// that a workgroup never waits for a row with nothing else in flight.
-template <typename TX, typename TW, typename TY, int VPL, int S, bool ADD>
-__global__ __launch_bounds__(1024) void rmsnorm_block_stream(const RmsParams p) {
-  using RS = RowSlice<TX, TW, VPL>;
-  using XB = typename TX::bits;
-  __shared__ float partial[2][16];
-  const int tid = threadIdx.x;
-  const int nthreads = blockDim.x;
-  const int nwave = nthreads >> 6;
-
-  BufChunk<TW, RS::W> wv[VPL];
-  const rsrc_t rw = make_rsrc(p.w, static_cast<uint32_t>(p.n) * sizeof(typename TW::bits));
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) wv[k].load(rw, static_cast<uint32_t>(tid + nthreads * k) * RS::WB);
-
-  const int64_t g = gridDim.x;
-  // Loads of row r into a slot (past the last row: 0-byte descriptors, no
-  // traffic).
-  auto fetch = [&](RS& row, int64_t r) {
-    row.load_x(make_rsrc(static_cast<const XB*>(p.x) + r * p.xs, row_bytes<TX>(p, r)), tid, nthreads);
-    if constexpr (ADD)
-      row.load_residual(make_rsrc(static_cast<const XB*>(p.r) + r * p.rs, row_bytes<TX>(p, r)), tid, nthreads);
-  };
-  RS ring[S];
-#pragma unroll
-  for (int j = 0; j < S; ++j) fetch(ring[j], blockIdx.x + j * g);
-
-  int buf = 0;
-  for (int64_t r0 = blockIdx.x; r0 < p.rows; r0 += S * g) {
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      const int64_t r = r0 + j * g;
-      if (r >= p.rows) break;  // uniform over the workgroup
-      RS& row = ring[j];
-      if constexpr (ADD) {
-        row.add_residual();
-        row.store_row(make_rsrc(static_cast<XB*>(p.ro) + r * p.ros, row_bytes<TX>(p, r)), tid, nthreads);
-      }
-      float ss = wave_allreduce_sum(row.sumsq());
-      if ((tid & 63) == 0) partial[buf][tid >> 6] = ss;
-      __syncthreads();
-      float tot = 0.0f;
-      for (int w = 0; w < nwave; ++w) tot += partial[buf][w];
-      buf ^= 1;  // the next row writes the other buffer; this row's barrier orders the reuse
-      row.template store_y<TY, kKeepF32Block<VPL>>(
-          make_rsrc(static_cast<typename TY::bits*>(p.y) + r * p.ys, row_bytes<TY>(p, r)), tid, nthreads,
-          rms_rstd(tot, p.n, p.eps), wv);
-      fetch(row, r + S * g);
-    }
   }
 }
 

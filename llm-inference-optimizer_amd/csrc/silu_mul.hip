@@ -18,33 +18,17 @@
 //
 // Launch shape (nt loads and stores, one block per chunk rather than a
 // persistent grid), measured on MI355X: 512 lanes x 2 packets per lane below
-// MI355_SILU_LARGE_MIN_NUMEL elements (the 110 MB C2 shape: 18.41 vs 18.77
-// us for 256 x 4; 440 MB: 67.70 vs 67.96 us), 256 lanes x 4 packets from
-// there (the 1.86 GB C4 shape: 288.6 vs 291.4 us).
+// 2^27 elements (the 110 MB C2 shape: 18.41 vs 18.77 us for 256 x 4; 440 MB:
+// 67.70 vs 67.96 us), 256 lanes x 4 packets from there (the 1.86 GB C4
+// shape: 288.6 vs 291.4 us).  A lane issues its loads in the order gate j,
+// up j, gate j + 1, ...
 #include "common.h"
 
-#ifndef MI355_SILU_BLOCK
-#define MI355_SILU_BLOCK 512
-#endif
-#ifndef MI355_SILU_UNROLL
-#define MI355_SILU_UNROLL 2
-#endif
-#ifndef MI355_SILU_LARGE_BLOCK
-#define MI355_SILU_LARGE_BLOCK 256
-#endif
-#ifndef MI355_SILU_LARGE_UNROLL
-#define MI355_SILU_LARGE_UNROLL 4
-#endif
-#ifndef MI355_SILU_LARGE_MIN_NUMEL
-#define MI355_SILU_LARGE_MIN_NUMEL (int64_t{1} << 27)
-#endif
-// Load issue order of a lane's packets: 0 = gate j, up j, gate j+1, ...;
-// 1 = every gate packet, then every up packet.
-#ifndef MI355_SILU_LOAD_ORDER
-#define MI355_SILU_LOAD_ORDER 0
-#endif
-
 namespace mi355 {
+
+constexpr int kSiluBlock = 512, kSiluUnroll = 2;
+constexpr int kSiluLargeBlock = 256, kSiluLargeUnroll = 4;
+constexpr int64_t kSiluLargeMinNumel = int64_t{1} << 27;
 
 template <typename TI, typename TO, int B, int U>
 __global__ __launch_bounds__(B) void silu_mul_chunks(const void* __restrict__ gate, const void* __restrict__ up,
@@ -61,18 +45,11 @@ __global__ __launch_bounds__(B) void silu_mul_chunks(const void* __restrict__ ga
   const rsrc_t ro = make_rsrc(static_cast<char*>(out) + first * OUT_BYTES, count * OUT_BYTES);
 
   Packet<TI> gv[U], uv[U];
-  if constexpr (MI355_SILU_LOAD_ORDER == 0) {
 #pragma unroll
-    for (int j = 0; j < U; ++j) {
-      const uint32_t off = (threadIdx.x + j * B) * 16u;
-      gv[j].raw = buf_load16(rg, off);
-      uv[j].raw = buf_load16(ru, off);
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < U; ++j) gv[j].raw = buf_load16(rg, (threadIdx.x + j * B) * 16u);
-#pragma unroll
-    for (int j = 0; j < U; ++j) uv[j].raw = buf_load16(ru, (threadIdx.x + j * B) * 16u);
+  for (int j = 0; j < U; ++j) {
+    const uint32_t off = (threadIdx.x + j * B) * 16u;
+    gv[j].raw = buf_load16(rg, off);
+    uv[j].raw = buf_load16(ru, off);
   }
 #pragma unroll
   for (int j = 0; j < U; ++j) {
@@ -140,9 +117,8 @@ int silu_typed(const SiluArgs& a, hipStream_t s, int cus) {
     if (grid > cap) grid = cap;
     return launch_silu(silu_mul_generic<TI, TO>, grid, 256, a, s);
   }
-  if (a.numel >= MI355_SILU_LARGE_MIN_NUMEL)
-    return silu_chunked<TI, TO, MI355_SILU_LARGE_BLOCK, MI355_SILU_LARGE_UNROLL>(a, s);
-  return silu_chunked<TI, TO, MI355_SILU_BLOCK, MI355_SILU_UNROLL>(a, s);
+  if (a.numel >= kSiluLargeMinNumel) return silu_chunked<TI, TO, kSiluLargeBlock, kSiluLargeUnroll>(a, s);
+  return silu_chunked<TI, TO, kSiluBlock, kSiluUnroll>(a, s);
 }
 
 }  // namespace

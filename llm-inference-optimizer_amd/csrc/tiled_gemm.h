@@ -85,14 +85,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 enum { EPI_W8 = 0, EPI_SILU = 1, EPI_SILU_W8 = 2, EPI_LINEAR = 3 };
 
-// MI355_TILED_PREFETCH = P > 0: one more wave per workgroup streams the
-// workgroup's operand lines of the K step P steps past the LDS ring's
-// furthest DMA into L2 (DMA loads into a 256-byte LDS sink, so no VGPRs and
-// its own vmcnt: the MFMA waves never wait on it), in step with the ring
-// through the same barriers.  0 = no prefetch wave.
-#ifndef MI355_TILED_PREFETCH
-#define MI355_TILED_PREFETCH 0
-#endif
 enum { B_16 = 0, B_I8 = 1 };
 
 template <typename T> __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
@@ -133,7 +125,6 @@ struct Params {
   int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
   int tiles_m, tiles_n;
   int group_m;  // m-blocks per group of the tile order (tiles_m: m fastest over the whole range)
-  int bands;    // XR = 2: column bands of the tile order (each band's tiles in group order)
 };
 
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S>
@@ -142,8 +133,7 @@ struct Cfg {
   // LDS and widened after each LDS read).
   static constexpr bool I8 = BK == B_I8;
   static constexpr int NW = WGM * WGN, NT = 64 * NW;
-  // threads per workgroup: the MFMA waves, plus the L2 prefetch wave when on
-  static constexpr int BLOCK = NT + (MI355_TILED_PREFETCH > 0 ? 64 : 0);
+  static constexpr int BLOCK = NT;  // threads per workgroup
   static constexpr int BM = 32 * FM * WGM, BN = 32 * FN * WGN;
   static constexpr int NB = (EPI == EPI_W8 || EPI == EPI_LINEAR) ? 1 : 2;  // B matrices
   static constexpr int A_BYTES = BM * 128;             // 64 columns of 16-bit x per row
@@ -184,31 +174,13 @@ constexpr int lcm_c(int a, int b) { return a / gcd_c(a, b) * b; }
 // tracks these LDS writes nor drains every load in flight before each LDS
 // read: the kernel orders them itself, with vmcnt waits before the barrier
 // that publishes a stage (vmcnt falls as the data reaches LDS, in issue order).
-// NT = true adds the non-temporal cache hint (the line is inserted for early
-// eviction).  Off for both operands: on x (A), on the weights (B) and on both
-// it measured slower on MI355X at every prefill shape of the gate/up, W8A16
-// and 16-bit-linear launchers (1.01x - 1.69x the time), the re-reads of both
-// operands by neighbouring tiles being L2 hits worth keeping.
-#ifndef MI355_DMA_A_NT
-#define MI355_DMA_A_NT 0
-#endif
-#ifndef MI355_DMA_B_NT
-#define MI355_DMA_B_NT 0
-#endif
-template <bool NT = false>
+// No non-temporal hint: on x, on the weights and on both it measured slower
+// on MI355X at every prefill shape of the gate/up, W8A16 and 16-bit-linear
+// launchers (1.01x - 1.69x the time), the re-reads of both operands by
+// neighbouring tiles being L2 hits worth keeping.
 __device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
-  if constexpr (NT)
-    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
-  else
-    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
-}
-// 4 bytes per lane into LDS (buffer_load_dword ... lds): the prefetch wave's
-// loads, whose data lands in a sink nobody reads.
-__device__ __forceinline__ void dma4(rsrc_t r, uint32_t voff, uint32_t lds_addr) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
-  const uint32_t soff = 0;
-  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0) : "memory");
 }
 
 // LDS byte address of stage I (the cast of the LDS variable itself folds to a constant).
@@ -231,33 +203,10 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
-// int8 B: widen each sub-step's weights one sub-step ahead, into a second
-// register set, after the previous sub-step's MFMAs are issued, so the
-// widening VALU work runs beside the MFMAs instead of in front of them
-// (0: widen right before the sub-step's own MFMAs).
-#ifndef MI355_TILED_WIDEN_AHEAD
-#define MI355_TILED_WIDEN_AHEAD 1
-#endif
-
-// MI355_TILED_XCD_RAGGED = 0: the configurations compiled with XR = 1 (below)
-// keep the dispatch order for tile counts that are not a multiple of 8 as
-// well (a measurement switch for variant builds).
-#ifndef MI355_TILED_XCD_RAGGED
-#define MI355_TILED_XCD_RAGGED 1
-#endif
-
-// MI355_TILED_MIN_WAVES_PER_SIMD = w > 0: every tiled kernel is compiled to
-// fit w waves per SIMD (at most 512 / w registers a lane), so register-heavy
-// tiles can run two workgroups per CU (a measurement switch for variant
-// builds; 0 = the compiler's own choice).
-#ifndef MI355_TILED_MIN_WAVES_PER_SIMD
-#define MI355_TILED_MIN_WAVES_PER_SIMD 0
-#endif
-
 // The occupancy one configuration is compiled for: its own WPE waves per SIMD
-// when WPE > 0, else the switch above, else 1 (no register cap).
+// when WPE > 0, else 1 (no register cap).
 template <int WPE>
-constexpr int kMinWavesPerSimd = WPE > 0 ? WPE : (MI355_TILED_MIN_WAVES_PER_SIMD > 0 ? MI355_TILED_MIN_WAVES_PER_SIMD : 1);
+constexpr int kMinWavesPerSimd = WPE > 0 ? WPE : 1;
 
 // WPE > 0 caps the registers of this configuration alone so that WPE waves fit
 // on each SIMD (a 192 x 128 tile of 8 waves at WPE = 4 fits in 128 VGPRs and
@@ -265,10 +214,13 @@ constexpr int kMinWavesPerSimd = WPE > 0 ? WPE : (MI355_TILED_MIN_WAVES_PER_SIMD
 // when the tile count is not a multiple of 8 too (the first count mod 8 XCDs,
 // which receive one workgroup more, take ranges one tile longer); XR = 0
 // keeps the dispatch order for such counts.  (XR is a template argument so
-// that the configurations without it keep their code.)
+// that the configurations without it keep their code.)  The int8 B operand
+// is widened one sub-step ahead, into a second register set, after the
+// previous sub-step's MFMAs are issued, so the widening VALU work runs beside
+// the MFMAs instead of in front of them.
 template <typename T, int BK, typename TO, int WGM, int WGN, int FM, int FN, int EPI, int S, int RING = 0, int WPE = 0,
           int XR = 0>
-__global__ __launch_bounds__(64 * WGM * WGN + (MI355_TILED_PREFETCH > 0 ? 64 : 0))
+__global__ __launch_bounds__(64 * WGM * WGN)
 __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(const Params p) {
   using C = Cfg<T, BK, TO, WGM, WGN, FM, FN, EPI, S>;
   constexpr bool I8 = C::I8;
@@ -282,7 +234,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
   // Tile of this workgroup: contiguous ranges per XCD, m fastest.
   const int ntiles = p.tiles_m * p.tiles_n;
   int b = blockIdx.x;
-  if constexpr (XR != 0 && MI355_TILED_XCD_RAGGED != 0) {
+  if constexpr (XR != 0) {
     // XCD x = b % 8 runs ids x, x + 8, ...: ceil((ntiles - x) / 8) of them
     const int q = ntiles >> 3, r = ntiles & 7, x = b & 7;
     b = x * q + (x < r ? x : r) + (b >> 3);
@@ -290,23 +242,10 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
     if ((ntiles & 7) == 0) b = (b & 7) * (ntiles >> 3) + (b >> 3);
   }
   // inside the range: groups of group_m m-blocks, m fastest within a group
-  // (XR = 2: first split into column bands of bw tile columns, band-major, so
-  // an XCD's range covers a band's columns rather than every column)
-  int tn_base = 0, width = p.tiles_n;
-  if constexpr (XR == 2) {
-    const int bw = (p.tiles_n + p.bands - 1) / p.bands;
-    const int per_band = p.tiles_m * bw;
-    const int nb = (p.tiles_n + bw - 1) / bw;  // bands actually used (none empty)
-    int j = b / per_band;
-    if (j > nb - 1) j = nb - 1;
-    b -= j * per_band;
-    tn_base = j * bw;
-    width = p.tiles_n - tn_base < bw ? p.tiles_n - tn_base : bw;
-  }
-  const int per_group = p.group_m * width;
+  const int per_group = p.group_m * p.tiles_n;
   const int g0 = (b / per_group) * p.group_m;
   const int gsz = p.tiles_m - g0 < p.group_m ? p.tiles_m - g0 : p.group_m;
-  const int tm = g0 + (b % per_group) % gsz, tn = tn_base + (b % per_group) / gsz;
+  const int tm = g0 + (b % per_group) % gsz, tn = (b % per_group) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
   const int nrows_x = p.rows - m0 < BM ? p.rows - m0 : BM;
   const int nrows_b = p.n - n0 < BN ? p.n - n0 : BN;
@@ -322,47 +261,6 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
                       static_cast<uint32_t>(((nrows_b - 1) * p.bs + p.k) * EB));
 
   const int nk = (p.k + 63) >> 6;
-  if constexpr (MI355_TILED_PREFETCH > 0) {
-    if (wave == NW) {
-      // The prefetch wave: before the ring's first barrier, steps S .. S + P - 1;
-      // after barrier t (when the MFMA waves start refilling with step t + S
-      // or so), step t + S + P - 1.  Two dwords per 128-byte line (each half
-      // a 64-byte sector) of every x row and weight row of the tile; rows and
-      // columns past the matrix fall outside the descriptors (no traffic).
-      __shared__ uint32_t sink[64];
-      const uint32_t sink_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)sink));
-      auto pf = [&](int u) {
-        if (u >= nk) return;
-#pragma unroll
-        for (int r = lane; r < BM; r += 64) {
-          const uint32_t off = static_cast<uint32_t>((r * p.xs + u * 64) * sizeof(TB));
-          dma4(rx, off, sink_addr);
-          dma4(rx, off + 64, sink_addr);
-        }
-        // int8 rows hold 64 bytes per step: a new 128-byte line every other step
-        if (!I8 || (u & 1) == 0) {
-#pragma unroll
-          for (int bi = 0; bi < NB; ++bi) {
-#pragma unroll
-            for (int r = lane; r < BN; r += 64) {
-              const uint32_t off = static_cast<uint32_t>((r * p.bs + u * 64) * EB);
-              dma4(rb[bi], off, sink_addr);
-              dma4(rb[bi], off + 64, sink_addr);
-            }
-          }
-        }
-      };
-      for (int u = S; u < S + MI355_TILED_PREFETCH; ++u) pf(u);
-      lds_barrier();
-      for (int t = 1; t < nk; ++t) {
-        pf(t + S + MI355_TILED_PREFETCH - 1);
-        lds_barrier();  // one per K step, as the MFMA waves
-      }
-      wait_vmcnt<0>();  // its LDS writes land before the workgroup ends
-      return;
-    }
-  }
-
   // DMA lane maps (16-bit tiles).  Instruction j of wave w fills the 1 KiB
   // at tile offset 1024 (NW j + w): lane l writes physical chunk l % 8 of row
   // 8 (NW j + w) + l / 8, so it loads the logical chunk the swizzle keeps
@@ -402,8 +300,8 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
     for (int j = 0; j < C::AI; ++j) {
       const uint32_t kb = static_cast<uint32_t>(kt * 64 * sizeof(TB));
       const uint32_t dst = st + 1024u * (NW * j + wave);
-      if (full) dma16<MI355_DMA_A_NT != 0>(rx, a_goff[j], kb, dst);
-      else dma16<MI355_DMA_A_NT != 0>(rx, kt * 64 + a_col[j] < p.k ? a_goff[j] + kb : kOob, 0, dst);
+      if (full) dma16(rx, a_goff[j], kb, dst);
+      else dma16(rx, kt * 64 + a_col[j] < p.k ? a_goff[j] + kb : kOob, 0, dst);
     }
 #pragma unroll
     for (int bi = 0; bi < NB; ++bi) {
@@ -411,8 +309,8 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
       for (int j = 0; j < C::BI; ++j) {
         const uint32_t kb = static_cast<uint32_t>(kt * 64 * EB);
         const uint32_t dst = st + C::A_BYTES + bi * C::B_BYTES + 1024u * (NW * j + wave);
-        if (full) dma16<MI355_DMA_B_NT != 0>(rb[bi], b_goff[j], kb, dst);
-        else dma16<MI355_DMA_B_NT != 0>(rb[bi], kt * 64 + b_col[j] < p.k ? b_goff[j] + kb : kOob, 0, dst);
+        if (full) dma16(rb[bi], b_goff[j], kb, dst);
+        else dma16(rb[bi], kt * 64 + b_col[j] < p.k ? b_goff[j] + kb : kOob, 0, dst);
       }
     }
   };
@@ -489,7 +387,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<WPE>))) void tiled_gemm(cons
   // Widen-ahead (int8 B): wb[s & 1] holds sub-step s's B operands, widened
   // from the raw int8 pair read (16 bytes: sub-steps 2q, 2q + 1) during the
   // previous sub-step, behind that sub-step's MFMAs.
-  constexpr bool WA = I8 && MI355_TILED_WIDEN_AHEAD != 0;
+  constexpr bool WA = I8;
   u32x4 wb[2][NB][FN];
   auto widen_into = [&](const u32x4 (&raw)[NB][FN], int s, u32x4 (&out)[NB][FN]) {
 #pragma unroll

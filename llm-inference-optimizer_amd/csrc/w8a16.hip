@@ -11,15 +11,17 @@
 // applied once to the fp32 accumulator, then the bias (fp32), then one
 // rounding to the output type.  Here scale and bias go through one fma.
 //
-// Three kernels, picked by the launcher:
-//   w8a16_skinny   rows <= 32 (decode): weight streaming.  Every weight byte is
-//                  read once per call at HBM bandwidth and meets up to 32 rows
-//                  of x on MFMA (v_mfma_f32_16x16x32_{f16,bf16}).  Also used
-//                  for a few 32-row tiles when the tiled grid would be small.
+// Four kernels, picked by the launcher:
+//   w8a16_stream   rows <= 8 (decode; w8a16_stream.h): weight streaming with
+//                  lane-coalesced loads, every weight byte read once per call
+//                  at HBM bandwidth, MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
+//   w8a16_skinny   9 - 32 rows, and a few 32-row tiles where the tiled grid
+//                  would be small: weight streaming with up to 32 rows of x
+//                  per workgroup (MFMA, the same instruction).
 //   tiled_gemm     more rows (prefill): the LDS-tiled MFMA GEMM of
 //                  tiled_gemm.h with int8 weights kept int8 in LDS and widened
 //                  after each LDS read, scale and bias in its epilogue.
-//   w8a16_generic  any k, stride or alignment the two above cannot take:
+//   w8a16_generic  any k, stride or alignment the three above cannot take:
 //                  one wave per (output feature, 4 rows of x), fp32 fma.
 //
 // And the quantiser of QuantizedLinearInt8.from_linear
@@ -38,79 +40,24 @@
 // block, with the same lane -> column map, so
 //   D[i][n] = sum over the block half of x[i % 8] * w[n % 8]  when i / 8 == n / 8
 // and the product of x row a with weight row b is D[a][b] + D[a + 8][b + 8]
-// (the off-diagonal quarters are discarded; for up to 8 rows of x they cost
-// nothing, A rows 8..15 would otherwise be padding).  D layout of the gfx950
+// (the off-diagonal quarters are discarded).  D layout of the gfx950
 // 16x16x32 MFMA: lane l holds rows 4 * (l / 16) + j, j < 4, of column l % 16.
 //
-// Decomposition: a workgroup owns 8 * G weight rows (blockIdx.y) and a tile of
-// 8 * MT rows of x (blockIdx.x) and splits the 128-column blocks of K between
-// its waves (contiguous ranges); each wave keeps U blocks of loads in flight,
-// and every x operand it loads feeds G weight groups.  Blocks
-// and 16-byte pieces past k address past the buffer descriptors (zeros, no
+// Skinny decomposition: a workgroup owns 8 * G weight rows (blockIdx.y) and a
+// tile of 8 * MT rows of x (blockIdx.x) and splits the 128-column blocks of K
+// between its waves (contiguous ranges); each wave keeps U blocks of loads in
+// flight, and every x operand it loads feeds G weight groups.  Blocks and
+// 16-byte pieces past k address past the buffer descriptors (zeros, no
 // traffic), so any k that is a multiple of 16 needs no remainder loop.  The
 // per-wave partial sums meet in LDS in a fixed order.
 #include "common.h"
 #include "tiled_gemm.h"
+#include "w8a16_stream.h"
 
 namespace mi355 {
 namespace {
 
 constexpr int kMaxSplit = 16;  // waves per skinny workgroup
-#ifdef MI355_W8_SWEEP
-// s_waitcnt operand for vmcnt(0) with the other counters left alone (gfx9
-// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-constexpr int kWaitVmcnt0 = 0x0F70;
-#endif
-
-// MI355_W8_PIPE = 1: the skinny kernels keep U blocks in flight per wave at
-// all times (a slot is refilled as soon as it is consumed) instead of issuing
-// U blocks, waiting for all of them, then consuming them.
-#ifndef MI355_W8_PIPE
-#define MI355_W8_PIPE 0
-#endif
-
-// 16 int8 weights (one 16-byte load) -> the B operands of two MFMAs.
-template <typename T>
-__device__ __forceinline__ void widen_i8x16(u32x4 w, u32x4& b0, u32x4& b1) {
-  const u32x2 p0 = widen_i8x4<T>(w.x), p1 = widen_i8x4<T>(w.y);
-  const u32x2 p2 = widen_i8x4<T>(w.z), p3 = widen_i8x4<T>(w.w);
-  b0 = u32x4{p0.x, p0.y, p1.x, p1.y};
-  b1 = u32x4{p2.x, p2.y, p3.x, p3.y};
-}
-
-struct W8Params {
-  const void* x;       // [rows, xs] of T
-  const void* q;       // [n, qs] int8 (gate weights for the dual kernels)
-  const void* scale;   // [n] of sdt
-  const void* bias;    // [n] of bdt, or null
-  void* out;           // [rows, os] of TO
-  int rows, k, n;
-  int64_t xs, qs, os;  // row strides in elements
-  int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
-  const void* q2;      // dual kernels: [n, qs] int8 up weights
-  const void* scale2;  // dual kernels: [n] of sdt
-  // Sweep builds only: the skinny kernels with K split over workgroups
-  // (gridDim.z > 1) as well.
-  float* part;     // [units][gridDim.z][NQ][64 G MT] fp32 partial sums
-  unsigned* cnt;   // [units] arrival counters, zero between calls
-};
-
-// The epilogue shared by all kernels: scale once, then the bias, one rounding.
-template <typename TO>
-__device__ __forceinline__ void w8_store(const W8Params& p, int64_t m, int n, float acc) {
-  const float sc = load_dyn(p.scale, n, p.sdt);
-  const float v = p.bdt >= 0 ? __builtin_fmaf(acc, sc, load_dyn(p.bias, n, p.bdt)) : acc * sc;
-  store_elem<TO>(p.out, m * p.os + n, v);
-}
-
-// The dual (gate/up) epilogue: both projections scaled once, SiLU-and-mul in
-// fp32, one rounding.
-template <typename TO>
-__device__ __forceinline__ void w8_store_silu(const W8Params& p, int64_t m, int n, float acc_g, float acc_u) {
-  const float g = acc_g * load_dyn(p.scale, n, p.sdt);
-  const float u = acc_u * load_dyn(p.scale2, n, p.sdt);
-  store_elem<TO>(p.out, m * p.os + n, silu_mul_f32(g, u));
-}
 
 // ------------------------------------------------------------------ skinny
 
@@ -162,18 +109,10 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
     }
   }
 
-  // This workgroup's share of the 128-column blocks (all of them unless a
-  // sweep build splits K over workgroups too), split again over its waves.
-  const int nblk_all = (p.k + 127) >> 7;
-#ifdef MI355_W8_SWEEP
-  const int z0 = (nblk_all * static_cast<int>(blockIdx.z)) / static_cast<int>(gridDim.z);
-  const int nblk = (nblk_all * (static_cast<int>(blockIdx.z) + 1)) / static_cast<int>(gridDim.z) - z0;
-#else
-  constexpr int z0 = 0;
-  const int nblk = nblk_all;
-#endif
-  const int s_begin = z0 + (nblk * wave) / nwave;
-  const int s_end = z0 + (nblk * (wave + 1)) / nwave;
+  // The 128-column blocks of K, split over the waves.
+  const int nblk = (p.k + 127) >> 7;
+  const int s_begin = (nblk * wave) / nwave;
+  const int s_end = (nblk * (wave + 1)) / nwave;
   // Block s into slot (wq, xa); blocks past the wave's range or past k load
   // zeros without touching memory.
   auto issue = [&](u32x4 (&wq)[NQ][G], u32x4 (&xa)[MT][2], int s) {
@@ -206,19 +145,6 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
     }
   };
   u32x4 wq[U][NQ][G], xa[U][MT][2];
-#if MI355_W8_PIPE
-  // U slots in flight at all times: each slot is refilled with the block U
-  // ahead as soon as its own block has been consumed.
-#pragma unroll
-  for (int j = 0; j < U; ++j) issue(wq[j], xa[j], s_begin + j);
-  for (int s = s_begin; s < s_end; s += U) {
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-      consume(wq[j], xa[j]);
-      issue(wq[j], xa[j], s + U + j);
-    }
-  }
-#else
   // U blocks issued together, then consumed together.
   for (int s = s_begin; s < s_end; s += U) {
 #pragma unroll
@@ -227,7 +153,6 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
 #pragma unroll
     for (int j = 0; j < U; ++j) consume(wq[j], xa[j]);
   }
-#endif
 
 #pragma unroll
   for (int qi = 0; qi < NQ; ++qi) {
@@ -245,64 +170,6 @@ __global__ __launch_bounds__(64 * kMaxSplit) void w8a16_skinny(const W8Params p)
 
   // Output (x row 8t + a, weight row 8g + b) = D[a][b] + D[a + 8][b + 8]:
   // register a % 4 of lanes 16 * (a / 4) + b and 16 * (a / 4) + 40 + b.
-#ifdef MI355_W8_SWEEP
-  if (gridDim.z > 1) {
-    // Sweep builds only (no faster than the shipped shapes at any decode
-    // shape but one): K split over workgroups too.  Each workgroup stores
-    // its partial sums; the last to arrive adds all of them in workgroup
-    // order (the same bits whatever the arrival order), applies the epilogue
-    // and re-arms the counter.
-    constexpr int NO = 64 * G * MT;
-    const unsigned unit = blockIdx.y * gridDim.x + blockIdx.x;
-    float* const part = p.part + static_cast<size_t>(unit) * gridDim.z * NQ * NO;
-    for (int o = threadIdx.x; o < NO; o += blockDim.x) {
-      const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
-      const int g = gt % G, t = gt / G;
-      const int l0 = 16 * (a >> 2) + b, j = a & 3;
-#pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
-        float sum = 0.f;
-        for (int w = 0; w < nwave; ++w) {
-          const float* r = red + ((((w * NQ + qi) * G + g) * MT + t) * 4 + j) * 64;
-          sum += r[l0] + r[l0 + 40];
-        }
-        __hip_atomic_store(part + (static_cast<size_t>(blockIdx.z) * NQ + qi) * NO + o, sum, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    // The partial sums are device-scope stores (written through to where
-    // every XCD reads them) and each wave waits for their acknowledgement
-    // before the barrier, so they are in place before the arrival count;
-    // the last workgroup reads them with device-scope loads.  (An agent-scope
-    // fence would do the same by writing back and invalidating the whole L2
-    // of the XCD, which costs microseconds per wave.)
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __shared__ unsigned last;
-    __syncthreads();
-    if (threadIdx.x == 0)
-      last = __hip_atomic_fetch_add(p.cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.z - 1;
-    __syncthreads();
-    if (!last) return;
-    for (int o = threadIdx.x; o < NO; o += blockDim.x) {
-      const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
-      const int g = gt % G, t = gt / G;
-      const int m = 8 * t + a, n = 8 * g + b;
-      if (m >= nrows_x || n >= nrows_w) continue;
-      float sum[NQ];
-#pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
-        sum[qi] = 0.f;
-        for (unsigned z = 0; z < gridDim.z; ++z)
-          sum[qi] += __hip_atomic_load(part + (static_cast<size_t>(z) * NQ + qi) * NO + o, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if constexpr (DUAL) w8_store_silu<TO>(p, m0 + m, n0 + n, sum[0], sum[NQ - 1]);
-      else w8_store<TO>(p, m0 + m, n0 + n, sum[0]);
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(p.cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-#endif
   for (int o = threadIdx.x; o < 64 * G * MT; o += blockDim.x) {
     const int b = o & 7, a = (o >> 3) & 7, gt = o >> 6;
     const int g = gt % G, t = gt / G;
@@ -409,48 +276,21 @@ int launch_w8(K kernel, dim3 grid, dim3 block, size_t lds, const W8Params& p, hi
                     "w8a16 launch");
 }
 
-#ifdef MI355_W8_SWEEP
-// Sweep builds only: force the skinny launch shape (0 = automatic).
-int g_force_g = 0, g_force_u = 0, g_force_split = 0, g_force_path = 0, g_force_ks = 0;
-__device__ __align__(256) unsigned char g_sweep_scratch[(8 << 20) + (64 << 10)];
-void* g_sweep_scratch_ptr = nullptr;
-}  // namespace
-extern "C" __attribute__((visibility("default"))) void mi355_w8_sweep_config(int g, int u, int split, int path) {
-  g_force_g = g;
-  g_force_u = u;
-  g_force_split = split;
-  g_force_path = path;
-}
-extern "C" __attribute__((visibility("default"))) int mi355_w8_sweep_ks(int ks) {
-  g_force_ks = ks;
-  if (!g_sweep_scratch_ptr && hipGetSymbolAddress(&g_sweep_scratch_ptr, HIP_SYMBOL(g_sweep_scratch)) != hipSuccess)
-    return -1;
-  return 0;
-}
-namespace {
-#endif
-
-// Skinny launch shape, fitted to a graph-timed sweep of G x waves x U on
-// MI355X over the q/o, k/v, gate/up and down projections of Qwen2.5-0.5B,
-// 1.5B and 7B at 1, 8, 32 and 128 rows (within 1.14x of the best sampled
-// shape everywhere, within 1.05x on most):
-//   G (weight-row groups per workgroup; each x operand feeds G B operands,
-//     and a wave keeps G KiB of weights in flight) grows with the rows of x
-//     while enough workgroups remain: with 1 row, 2 only for large matrices
-//     (n / 16 >= 192 and n * k >= 12M); with <= 8 rows 4 if n / 32 >= 384,
-//     else 2 if n / 16 >= 192; beyond, the largest of 4, 2, 1 with
-//     n / (8 G) >= 160 (<= 32 rows) or 48 (several 32-row tiles);
-//   waves per workgroup (the split of K) so that about 4096 (1 row; 3072
-//     for the dual kernel), 1536 (<= 8 rows), 1024 (<= 32 rows) or 1536
-//     (several 32-row tiles) waves run
-//     in total, within the LDS for the partial sums (<= 64 KiB), then evened
-//     out so every wave gets the same number of 128-column blocks -- or, when
-//     there are no more workgroups than CUs, rounded to a multiple of 4 so
-//     the CU's 4 SIMDs carry equal loads (7 waves on 224 CUs: 1.22x slower
-//     than 8);
-//   U (blocks in flight per wave) = 1, or 2 for narrow outputs (n <= 1536,
-//     few workgroups) whose waves own 2 or more blocks -- then, with one row
-//     and one workgroup per CU, at most 12 waves.
+// Skinny launch shape (9 - 32 rows, and the 32-row tiles of small grids),
+// fitted to a graph-timed sweep of G x waves x U on MI355X over the q/o, k/v,
+// gate/up and down projections of Qwen2.5-0.5B, 1.5B and 7B:
+//   G (weight-row groups per workgroup; each x operand feeds G B operands)
+//     the largest of 4, 2, 1 with n / (8 G) >= 160 (<= 32 rows) or 48
+//     (several 32-row tiles); the dual kernel at most 2, and 1 for MT >= 3 so
+//     its 2 G MT accumulator tiles fit the register budget;
+//   waves per workgroup (the split of K) so that about 1024 (<= 32 rows) or
+//     1536 (several 32-row tiles) waves run in total, within the LDS for the
+//     partial sums (<= 64 KiB), then evened out so every wave gets the same
+//     number of 128-column blocks -- or, when there are no more workgroups
+//     than CUs, rounded to a multiple of 4 so the CU's 4 SIMDs carry equal
+//     loads;
+//   U (blocks in flight per wave) = 2 for narrow outputs (n <= 1536) whose
+//     waves own 2 or more blocks, else 1.
 template <typename T, typename TO, int MT, int G, bool DUAL>
 int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   constexpr int NQ = DUAL ? 2 : 1;
@@ -458,16 +298,8 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   const int nblk = (p.k + 127) / 128;
   const int tiles = (p.rows + 8 * MT - 1) / (8 * MT);
   const int64_t units = static_cast<int64_t>(groups) * tiles;
-  // (the dual kernel moves two weight blocks per wave and step: 12 waves per
-  // CU at one row -- 1.5B MLP 8.04 -> 7.47 us, 0.5B 5.15 -> 4.97 us)
-  const int64_t waves = p.rows <= 1 ? (DUAL ? 12 : 16) * cus
-                                    : (p.rows <= 8 ? 6 * cus : (p.rows <= 32 ? 4 * cus : 6 * cus));
+  const int64_t waves = (p.rows <= 32 ? 4 : 6) * static_cast<int64_t>(cus);
   int split = static_cast<int>((waves + units / 2) / units);
-  int u = 0;
-#ifdef MI355_W8_SWEEP
-  if (g_force_split > 0) split = g_force_split;
-  if (g_force_u > 0) u = g_force_u;
-#endif
   if (split > kMaxSplit) split = kMaxSplit;
   if (split > 64 / (NQ * G * MT)) split = 64 / (NQ * G * MT);  // partial sums: split * NQ * G * MT KiB <= 64 KiB
   if (split > nblk) split = nblk;
@@ -482,97 +314,25 @@ int w8_skinny_g(const W8Params& p, hipStream_t s, int cus) {
   } else {
     split = (nblk + bpw - 1) / bpw;  // even blocks per wave
   }
-  // The dual kernel with up to 8 rows, 2 groups and more than 4 workgroups
-  // per CU: 2 waves per workgroup (the 7B MLP at 1, 2 and 8 rows: 24.0 /
-  // 24.6 / 28.0 us, against 26.3 us with 3 waves at 1 row and 30.6 / 31.2
-  // us with 1 wave at 2 and 8 rows, in the same sweep).
-  bool forced_split = false;
-#ifdef MI355_W8_SWEEP
-  forced_split = g_force_split > 0;
-#endif
-  if (DUAL && MT == 1 && G == 2 && units > 4 * static_cast<int64_t>(cus) && nblk >= 2 && !forced_split) {
-    split = 2;
-    bpw = (nblk + 1) / 2;
-  }
-  if (u == 0) {
-    u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
-    // One row, one workgroup per CU, 2 blocks in flight per wave: at most 12
-    // waves (a graph-timed sweep of the Qwen2.5-1.5B and 0.5B down
-    // projections at one row: k = 8960, 12 waves 5.99 us against 6.72 us
-    // for 16; k = 4864, 4.76 against 4.86; with 1 block in flight 16 waves
-    // stay ahead at every 1-row shape swept).
-    if (p.rows <= 1 && u == 2 && units <= cus && split > 12) {
-      split = 12;
-      bpw = (nblk + split - 1) / split;
-    }
-  }
-  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
-#ifdef MI355_W8_SWEEP
-  W8Params ps = p;
-  if (g_force_ks > 1 && g_sweep_scratch_ptr) {
-    const size_t part_bytes = static_cast<size_t>(units) * g_force_ks * NQ * 64 * G * MT * sizeof(float);
-    if (part_bytes <= (8u << 20) && units <= 16384) {
-      grid.z = static_cast<unsigned>(g_force_ks);
-      ps.part = static_cast<float*>(g_sweep_scratch_ptr);
-      ps.cnt = reinterpret_cast<unsigned*>(static_cast<unsigned char*>(g_sweep_scratch_ptr) + (8 << 20));
-    }
-  }
-  const W8Params& pl = ps;
-#else
-  const W8Params& pl = p;
-#endif
+  const int u = (p.n <= 1536 && bpw >= 2) ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
   const dim3 block(64 * split);
   const size_t lds = static_cast<size_t>(split) * NQ * G * MT * 4 * 64 * sizeof(float);
   // register budget (128 VGPRs at 1024 threads): U * (4 NQ G + 8 MT) operand
   // dwords + 4 NQ G MT accumulators <= 100
   constexpr int umax = (100 - 4 * NQ * G * MT) / (4 * NQ * G + 8 * MT);
-#ifdef MI355_W8_SWEEP
-  if (u >= 8 && umax >= 8)
-    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 8 ? 8 : 1), DUAL>, grid, block, lds, pl, s);
-  if (u >= 4 && umax >= 4)
-    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 4 ? 4 : 1), DUAL>, grid, block, lds, pl, s);
-#endif
   if (u >= 2 && umax >= 2)
-    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1), DUAL>, grid, block, lds, pl, s);
-  return launch_w8(w8a16_skinny<T, TO, MT, G, 1, DUAL>, grid, block, lds, pl, s);
+    return launch_w8(w8a16_skinny<T, TO, MT, G, (umax >= 2 ? 2 : 1), DUAL>, grid, block, lds, p, s);
+  return launch_w8(w8a16_skinny<T, TO, MT, G, 1, DUAL>, grid, block, lds, p, s);
 }
 
 template <typename T, typename TO, int MT, bool DUAL>
 int w8_skinny_shape(const W8Params& p, hipStream_t s, int cus) {
+  const int min_groups = p.rows <= 32 ? 160 : 48;
   int g = 1;
-  if (p.rows <= 1) {
-    if ((p.n + 15) / 16 >= 192 && static_cast<int64_t>(p.n) * p.k >= 12000000) g = 2;
-  } else if (p.rows <= 8) {
-    if ((p.n + 31) / 32 >= 384) g = 4;
-    else if ((p.n + 15) / 16 >= 192) g = 2;
-  } else {
-    const int min_groups = p.rows <= 32 ? 160 : 48;
-    if ((p.n + 31) / 32 >= min_groups) g = 4;
-    else if ((p.n + 15) / 16 >= min_groups) g = 2;
-  }
-  // The dual kernel carries two weight matrices per row group: one group for
-  // a single row unless the matrices are large (below), else at most 2 (a
-  // sweep of G x split x U over Qwen2.5-1.5B and -7B decode rows: 8 rows 9.2
-  // us with 2 groups vs 12.5 us with 1), and 1 for MT >= 3 so its 2 G MT
-  // accumulator tiles fit the register budget.
-#ifdef MI355_W8_SWEEP
-  constexpr int gmax = !DUAL ? (MT == 1 ? 8 : 4) : (MT >= 3 ? 1 : (MT == 1 ? 4 : 2));
-#else
+  if ((p.n + 31) / 32 >= min_groups) g = 4;
+  else if ((p.n + 15) / 16 >= min_groups) g = 2;
   constexpr int gmax = !DUAL ? 4 : (MT >= 3 ? 1 : 2);
-#endif
-  // One row: 2 groups once single groups would make more than 8 workgroups
-  // per CU (the 7B MLP: 27.5 -> 24.0 us in a graph-timed sweep of G x waves
-  // x U; the 1.5B and 0.5B MLPs keep 1).
-  if (DUAL) {
-    if (p.rows <= 1) g = (p.n + 7) / 8 > 8 * cus ? 2 : 1;
-    else g = g > 2 ? 2 : g;
-  }
-#ifdef MI355_W8_SWEEP
-  if (g_force_g > 0) g = g_force_g;
-#endif
-  if constexpr (gmax >= 8) {
-    if (g >= 8) return w8_skinny_g<T, TO, MT, (gmax >= 8 ? 8 : 1), DUAL>(p, s, cus);
-  }
   if constexpr (gmax >= 4) {
     if (g >= 4) return w8_skinny_g<T, TO, MT, (gmax >= 4 ? 4 : 1), DUAL>(p, s, cus);
   }
@@ -591,32 +351,9 @@ bool tiled_fits(const W8Params& p, bool) {
          static_cast<int64_t>((p.rows + 63) / 64) * ((p.n + 63) / 64) < (int64_t{1} << 31);
 }
 
-// Bytes per element of a scale / bias dtype code.
-inline int64_t dtype_size(int dt) { return dt == MI355_F32 ? 4 : 2; }
-
-// MI355_W8_COLSPLIT = 1 / 2: wide outputs from 1024 rows split their columns
-// into whole rounds of 128 x 128 tiles and a round of 128 x 64 tiles, when
-// the last round of 128 x 128 tiles would be more than half full (1) or
-// whenever the rest fits one round (2) (a measurement switch for variant
-// builds; 0 = one launch).
-#ifndef MI355_W8_COLSPLIT
-#define MI355_W8_COLSPLIT 0
-#endif
-
-// MI355_W8_BANDS = b > 1: every single-matrix tiled launch orders its tiles
-// in b column bands (XR = 2 of the tiled core) before the XCD ranges, so an
-// XCD reads a band's weights rather than all of them (a measurement switch
-// for variant builds; 1 = no bands).
-#ifndef MI355_W8_BANDS
-#define MI355_W8_BANDS 1
-#endif
-
-// MI355_W8_GROUP_M: m-blocks per group of the tiled GEMM's tile order inside
-// each XCD's range (m fastest within a group; a measurement switch for
-// variant builds).
-#ifndef MI355_W8_GROUP_M
-#define MI355_W8_GROUP_M 4
-#endif
+// m-blocks per group of the tiled GEMM's tile order inside each XCD's range
+// (m fastest within a group).
+constexpr int kW8GroupM = 4;
 
 template <typename T, typename TO, int WGM, int WGN, int FM, int FN, int S, int EPI = tiled::EPI_W8, int RING = 0,
           int WPE = 0, int XR = 0>
@@ -629,8 +366,6 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   // counts are mostly not powers of two: 1.5B gate/up at 1400 rows (770
   // tiles of 128 x 128) 66.1 -> 58.3 us, 2900 rows 112.0 -> 103.8 us, 7B
   // gate/up at 1100 rows 179.2 -> 174.9 us; the narrow outputs even.
-  if constexpr (XR != 2 && MI355_W8_BANDS > 1 && EPI == tiled::EPI_W8)
-    return w8_tiled_cfg<T, TO, WGM, WGN, FM, FN, S, EPI, RING, WPE, 2>(p, s);
   if constexpr (XR == 0) {
     const int64_t ntiles = static_cast<int64_t>((p.rows + C::BM - 1) / C::BM) * ((p.n + C::BN - 1) / C::BN);
     if (ntiles % 8 != 0) return w8_tiled_cfg<T, TO, WGM, WGN, FM, FN, S, EPI, RING, WPE, 1>(p, s);
@@ -653,8 +388,7 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
   tp.bdt = p.bdt;
   tp.tiles_m = (p.rows + C::BM - 1) / C::BM;
   tp.tiles_n = (p.n + C::BN - 1) / C::BN;
-  tp.group_m = tp.tiles_m < MI355_W8_GROUP_M ? tp.tiles_m : MI355_W8_GROUP_M;
-  tp.bands = MI355_W8_BANDS;
+  tp.group_m = tp.tiles_m < kW8GroupM ? tp.tiles_m : kW8GroupM;
   void* args[] = {&tp};
   // all LDS is static (no dynamic shared memory)
   return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(tiled::tiled_gemm<T, tiled::B_I8, TO, WGM, WGN, FM, FN,
@@ -674,70 +408,8 @@ int w8_tiled_cfg(const W8Params& p, hipStream_t s) {
 //   else (n <= 2048) -> 128 x 256, 8 waves, 4 stages.
 // bf16 takes 128 x 128 where fp16 takes 128 x 256: its widening needs more
 // registers, and the 128 x 256 shape would spill.
-// MI355_W8_FORCE = n (> 0): every prefill-size single-matrix launch takes
-// tile configuration n below instead of the launch plan (a measurement
-// switch for variant builds; all configurations compute the same results).
-#ifndef MI355_W8_FORCE
-#define MI355_W8_FORCE 0
-#endif
-
-template <typename T, typename TO>
-int w8_tiled_forced(const W8Params& p, hipStream_t s) {
-  using tiled::EPI_W8;
-  switch (MI355_W8_FORCE) {
-    case 1: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, EPI_W8, 1>(p, s);  // 128 x 64, 4 waves of 64 x 32
-    case 2: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32
-    case 3: return w8_tiled_cfg<T, TO, 4, 2, 2, 4, 2, EPI_W8, 1>(p, s);  // 256 x 256, 8 waves of 64 x 128
-    case 4: return w8_tiled_cfg<T, TO, 2, 2, 2, 4, 2, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 64 x 128
-    case 5: return w8_tiled_cfg<T, TO, 1, 4, 4, 2, 2, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 128 x 64
-    case 6: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 2, EPI_W8, 1>(p, s);  // 128 x 256, 8 waves of 64 x 64
-    case 7: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 2, EPI_W8, 1>(p, s);  // 256 x 128, 4 waves of 128 x 64
-    case 8: return w8_tiled_cfg<T, TO, 1, 4, 2, 4, 2, EPI_W8, 1>(p, s);  // 64 x 512, 4 waves of 64 x 128
-    case 9: return w8_tiled_cfg<T, TO, 2, 2, 2, 4, 3, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves, 3 stages
-    case 10: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 4>(p, s);             // 128 x 256, 8 waves, step pipeline
-    case 11: return w8_tiled_cfg<T, TO, 1, 4, 4, 2, 3, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 128 x 64, 3 stages
-    case 12: return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 2, EPI_W8, 1>(p, s);  // 128 x 128, 4 waves of 64 x 64
-    case 13: return w8_tiled_cfg<T, TO, 2, 2, 1, 2, 2, EPI_W8, 1>(p, s);  // 64 x 128, 4 waves of 32 x 64
-    case 14: return w8_tiled_cfg<T, TO, 1, 4, 2, 1, 2, EPI_W8, 1>(p, s);  // 64 x 128, 4 waves of 64 x 32
-    case 15: return w8_tiled_cfg<T, TO, 2, 2, 2, 2, 3, EPI_W8, 1>(p, s);  // 128 x 128, 4 waves, 3 stages
-    case 16: return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 3, EPI_W8, 1>(p, s);  // 64 x 64, 4 waves, ring, 3 stages
-    case 17: return w8_tiled_cfg<T, TO, 2, 2, 1, 1, 4>(p, s);             // 64 x 64, 4 waves, step pipeline
-    // large tiles (fewer operand bytes per flop) behind deeper LDS rings
-    case 18: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 3, EPI_W8, 1>(p, s);  // 256 x 128, 4 waves of 128 x 64, ring, 3 stages
-    case 19: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 4, EPI_W8, 1>(p, s);  // 256 x 128, 4 waves of 128 x 64, ring, 4 stages
-    case 20: return w8_tiled_cfg<T, TO, 2, 2, 4, 2, 3>(p, s);             // 256 x 128, 4 waves of 128 x 64, step, 3 stages
-    case 21: return w8_tiled_cfg<T, TO, 2, 2, 4, 4, 3, EPI_W8, 1>(p, s);  // 256 x 256, 4 waves of 128 x 128, ring, 3 stages
-    case 22: return w8_tiled_cfg<T, TO, 2, 2, 2, 4, 4, EPI_W8, 1>(p, s);  // 128 x 256, 4 waves of 64 x 128, ring, 4 stages
-    case 23: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 4, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 4 stages
-    // more waves per workgroup issuing the DMA
-    case 24: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 2 stages
-    case 25: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 3 stages
-    case 26: return w8_tiled_cfg<T, TO, 2, 8, 2, 1, 2, EPI_W8, 1>(p, s);  // 128 x 256, 16 waves of 64 x 32, ring, 2 stages
-    case 27: return w8_tiled_cfg<T, TO, 4, 2, 2, 2, 2, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 64 x 64, ring, 2 stages
-    case 28: return w8_tiled_cfg<T, TO, 4, 2, 2, 2, 3, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 64 x 64, ring, 3 stages
-    case 29: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 4>(p, s);             // 128 x 128, 8 waves of 64 x 32, step, 4 stages
-    case 30: return w8_tiled_cfg<T, TO, 4, 2, 1, 2, 3, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 32 x 64, ring, 3 stages
-    case 31: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 4, EPI_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 4 stages
-    case 32: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 3, EPI_W8, 1>(p, s);  // 128 x 256, 8 waves of 64 x 64, ring, 3 stages
-    case 33: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
-    // narrow outputs: 64 x 128 tiles of 8 waves
-    case 34: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 3, EPI_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 3 stages
-    case 35: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4, EPI_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 4 stages
-    case 36: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4>(p, s);             // 64 x 128, 8 waves of 32 x 32, step, 4 stages
-    // 192-row tiles: fewer rounds of tiles at 1024 and 4096 rows
-    case 37: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 2 stages
-    case 38: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 3, EPI_W8, 1>(p, s);  // 192 x 128, 8 waves of 96 x 32, ring, 3 stages
-    // registers capped for more workgroups per CU (the last template argument: waves per SIMD)
-    case 39: return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, EPI_W8, 1, 4, 1>(p, s);  // 192 x 128, 8 waves, ring, 2 stages; 2 per CU
-    case 40: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_W8, 1, 6>(p, s);  // 128 x 128, 8 waves, ring, 2 stages; 3 per CU
-    case 41: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, EPI_W8, 1, 4>(p, s);  // 256 x 128, 8 waves, ring, 2 stages; 2 per CU
-    default: return w8_tiled_cfg<T, TO, 2, 4, 2, 2, 2, EPI_W8, 1, 4>(p, s);  // 128 x 256, 8 waves of 64 x 64, ring, 2 stages; 2 per CU
-  }
-}
-
 template <typename T, typename TO>
 int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
-  if constexpr (MI355_W8_FORCE > 0) return w8_tiled_forced<T, TO>(p, s);
   constexpr bool wide = std::is_same<T, F16>::value;
   // Wide outputs from 1024 rows at gate/up and o-projection depths (k <=
   // 4096): 128 x 128 tiles of 8 waves (64 x 32 each) behind a 3-stage ring,
@@ -760,35 +432,6 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
     const int64_t t192 = (p.rows + 191) / 192 * cols, t128x128 = (p.rows + 127) / 128 * cols;
     if (t192 <= 2 * static_cast<int64_t>(cus) && t128x128 > 2 * static_cast<int64_t>(cus))
       return w8_tiled_cfg<T, TO, 2, 4, 3, 1, 2, tiled::EPI_W8, 1, 4, 1>(p, s);
-#if MI355_W8_COLSPLIT
-    {
-      // Column split: whole rounds of 128 x 128 tiles (two per CU) over the
-      // leading columns, the rest in one round of 128 x 64 tiles (4 waves,
-      // four per CU), instead of a last, partly filled round of 128 x 128.
-      // Every output element sums its k products in the same order either way.
-      const int64_t tm = (p.rows + 127) / 128, slots = 2 * static_cast<int64_t>(cus);
-      const int64_t full = cols * tm / slots, remainder = t128x128 - full * slots;
-      const int lead = static_cast<int>(full * slots / tm * 128);
-      const bool want = MI355_W8_COLSPLIT == 2 || remainder > cus;
-      if (want && full >= 1 && lead > 0 && lead < p.n) {
-        const int rest = p.n - lead;
-        if (tm * ((rest + 63) / 64) <= 4 * static_cast<int64_t>(cus)) {
-          W8Params head = p, tail = p;
-          head.n = lead;
-          tail.n = rest;
-          tail.q = static_cast<const int8_t*>(p.q) + static_cast<int64_t>(lead) * p.qs;
-          tail.scale = static_cast<const uint8_t*>(p.scale) + static_cast<int64_t>(lead) * dtype_size(p.sdt);
-          if (p.bdt >= 0)
-            tail.bias = static_cast<const uint8_t*>(p.bias) + static_cast<int64_t>(lead) * dtype_size(p.bdt);
-          tail.out = static_cast<uint8_t*>(p.out) +
-                     static_cast<int64_t>(lead) * static_cast<int64_t>(sizeof(typename TO::bits));
-          const int r = w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(head, s);
-          if (r != MI355_OK) return r;
-          return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, tiled::EPI_W8, 1>(tail, s);
-        }
-      }
-    }
-#endif
     return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, tiled::EPI_W8, 1>(p, s);
   }
   // Below 1024 rows, wide outputs with at least two 128 x 64 tiles per CU: the sub-step ring
@@ -837,37 +480,8 @@ int w8_tiled(const W8Params& p, hipStream_t s, int cus) {
 // tile does not split into the 8 waves' 1 KiB DMA instructions.  bf16 keeps
 // the 128 x 64 shape there (its widening needs more registers; 128 x 128 at
 // 8 waves would spill).
-// MI355_W8_DUAL_FORCE = n (> 0): every dual (gate/up + SiLU-and-mul) launch
-// above 256 rows takes configuration n below (a measurement switch for
-// variant builds; every configuration computes the same results).
-#ifndef MI355_W8_DUAL_FORCE
-#define MI355_W8_DUAL_FORCE 0
-#endif
-
-template <typename T, typename TO>
-int w8_tiled_dual_forced(const W8Params& p, hipStream_t s) {
-  using tiled::EPI_SILU_W8;
-  switch (MI355_W8_DUAL_FORCE) {
-    case 1: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 2, EPI_SILU_W8, 1>(p, s);  // 128 x 64, 4 waves, ring, 2 stages
-    case 2: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 2, EPI_SILU_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 2 stages
-    case 3: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 2 stages
-    case 4: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 3, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 64 x 32, ring, 3 stages
-    case 5: return w8_tiled_cfg<T, TO, 4, 2, 1, 2, 2, EPI_SILU_W8, 1>(p, s);  // 128 x 128, 8 waves of 32 x 64, ring, 2 stages
-    case 6: return w8_tiled_cfg<T, TO, 2, 2, 2, 1, 3, EPI_SILU_W8, 1>(p, s);  // 128 x 64, 4 waves, ring, 3 stages
-    case 7: return w8_tiled_cfg<T, TO, 2, 4, 4, 1, 3, EPI_SILU_W8, 1>(p, s);  // 256 x 128, 8 waves of 128 x 32, ring, 3 stages
-    // registers capped for 4 waves per SIMD: 128 x 128, 8 waves of 64 x 32, ring, 2 stages, two workgroups per CU
-    case 8: return w8_tiled_cfg<T, TO, 2, 4, 2, 1, 2, EPI_SILU_W8, 1, 4>(p, s);
-    case 9: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 3, EPI_SILU_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 3 stages
-    case 10: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 2, EPI_SILU_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 2 stages
-    default: return w8_tiled_cfg<T, TO, 2, 4, 1, 1, 4, EPI_SILU_W8, 1>(p, s);  // 64 x 128, 8 waves of 32 x 32, ring, 4 stages
-  }
-}
-
 template <typename T, typename TO>
 int w8_tiled_dual(const W8Params& p, hipStream_t s, int cus) {
-  if constexpr (MI355_W8_DUAL_FORCE > 0) {
-    if (p.rows > 256) return w8_tiled_dual_forced<T, TO>(p, s);
-  }
   // More than 256 rows: the sub-step ring (2 stages), 128 x 64 tiles (4
   // waves, 48 KiB of LDS, three workgroups per CU) or 256 x 128 (8 waves of
   // 128 x 32), whichever takes fewer rounds, a round of 256 x 128 weighted
@@ -918,7 +532,7 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
     const int64_t waves = static_cast<int64_t>(p.n) * ((p.rows + kGenRows - 1) / kGenRows);
     return launch_w8(w8a16_generic<T, TO, DUAL>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, p, s);
   }
-  if (p.rows <= 8) return w8_skinny_shape<T, TO, 1, DUAL>(p, s, cus);
+  if (p.rows <= 8) return w8_stream_launch<T, TO, DUAL>(p, w8_stream_plan(p.rows, p.k, p.n, DUAL, cus), s);
   if (p.rows <= 16) return w8_skinny_shape<T, TO, 2, DUAL>(p, s, cus);
   if (small_tiles_pay(p.rows, p.n) && tiled_fits(p, DUAL)) return w8_tiled_small<T, TO, DUAL>(p, s);
   if (p.rows <= 24) return w8_skinny_shape<T, TO, 3, DUAL>(p, s, cus);
@@ -932,9 +546,6 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   const int64_t tiles64 = static_cast<int64_t>((p.n + 63) / 64) * ((p.rows + 63) / 64);
   bool skinny = p.rows <= 256 && (tiles64 < 32 || (p.rows <= 128 && p.n < 2048));
   if (!tiled_fits(p, DUAL)) skinny = true;
-#ifdef MI355_W8_SWEEP
-  if (g_force_path > 0) skinny = g_force_path == 1;
-#endif
   if (skinny) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);
   if constexpr (DUAL) return w8_tiled_dual<T, TO>(p, s, cus);
   else return w8_tiled<T, TO>(p, s, cus);
@@ -948,7 +559,8 @@ int w8a16_launch(const void* x, const void* q, const void* scale, const void* bi
   int cus = 0;
   const int st = compute_units(&cus);
   if (st != MI355_OK) return st;
-  const W8Params p{x, q, scale, bias, out, rows, k, n, xs, qs, os, scale_dtype, bias ? bias_dtype : -1, nullptr, nullptr};
+  const W8Params p{x, q, scale, bias, out, rows, k, n, xs, qs, os, scale_dtype, bias ? bias_dtype : -1, nullptr,
+                   nullptr};
   if (x_dtype == MI355_F16 && out_dtype == MI355_F16) return w8_typed<F16, F16, false>(p, stream, cus);
   if (x_dtype == MI355_F16 && out_dtype == MI355_F32) return w8_typed<F16, F32, false>(p, stream, cus);
   if (x_dtype == MI355_BF16 && out_dtype == MI355_BF16) return w8_typed<BF16, BF16, false>(p, stream, cus);

@@ -1,0 +1,303 @@
+// The W8A16 decode kernel (up to 8 rows of x): int8 weight streaming with
+// lane-coalesced loads, plus its launch plan.  Shared by the W8A16 linear and
+// the int8 gate/up + SiLU-and-mul launchers (w8a16.hip).
+//
+//   out[m, n] = round(acc * scale[n] + bias[n]),  acc = sum_k x[m, k] * q[n, k]
+//   (DUAL: out[m, n] = round(silu(acc_g * scale_g[n]) * (acc_u * scale_u[n])))
+//
+// Load layout.  The weights are read 4 rows x 256 bytes per load instruction:
+// lane l reads 16 bytes of weight row 4 r + (l % 16) / 4 (4-row set r of the
+// workgroup) at byte 16 (l % 4) + 64 (l / 16) of a 256-byte chunk of K, so
+// every quad of lanes reads 64 contiguous bytes and each row's 256 bytes come
+// from 16 lanes.  (The 8 rows x 128 bytes of w8a16_skinny's layout, with
+// consecutive lanes on different rows, streams the same bytes about 10%
+// slower on MI355X, and its x loads cost twice as much; see the weight-stream
+// probe in csrc/probe/w8_stream.hip.)
+//
+// MFMA mapping (v_mfma_f32_16x16x32_{f16,bf16}: A lane l holds A[l % 16][8 (l
+// / 16) + e], B lane l holds B[8 (l / 16) + e][l % 16], e < 8; D lane l holds
+// D[4 (l / 16) + j][l % 16], j < 4).  A lane's 16 int8 weights are widened
+// into two B operands (bytes 0-7, 8-15), so B column c = l % 16 is weight row
+// 4 r + c / 4 over the k-subset
+//   S(c % 4) = {16 (c % 4) + 64 g + e : g < 4, e < 8}   (+ 8 for the second),
+// and A row i = 4 m' + q is x row m' of a 4-row x set over S(q): lane l loads
+// x[(l % 16) / 4][16 (l % 4) + 64 (l / 16) .. + 16] (two 16-byte loads).
+// Then D[4 m' + q][4 r' + q] = sum over S(q) of x[m'] * w[r'], the products
+// with i % 4 != c % 4 are discarded, and
+//   acc(x row m', weight row r') = sum_q D[4 m' + q][4 r' + q],
+// which lane 16 m' + 4 r' + q holds in its register q: each lane keeps its own
+// register l % 4 and a quad sum (two DPP adds, one fixed order) finishes it.
+// An 8-row x tile takes two A sets (MT4 = 2), so the MFMA work is twice the
+// minimum -- far below what the weight stream leaves idle.
+//
+// Decomposition.  A workgroup owns rpw <= 4 R4 consecutive weight rows and all
+// rows of x; its waves split the 256-byte chunks of K into contiguous ranges
+// and keep U chunks of loads in flight (issued together, then consumed).  The
+// per-wave sums meet in LDS and are added in wave order, so a call's bits do
+// not depend on scheduling.  Weight rows past the workgroup's share and x rows
+// past `rows` lie past their buffer descriptors (zeros, no traffic); pieces
+// past k are redirected past the descriptors, so any k that is a multiple of
+// 16 needs no remainder loop.
+#pragma once
+
+#include "common.h"
+
+namespace mi355 {
+
+struct W8Params {
+  const void* x;       // [rows, xs] of T
+  const void* q;       // [n, qs] int8 (gate weights for the dual kernels)
+  const void* scale;   // [n] of sdt
+  const void* bias;    // [n] of bdt, or null
+  void* out;           // [rows, os] of TO
+  int rows, k, n;
+  int64_t xs, qs, os;  // row strides in elements
+  int sdt, bdt;        // dtype codes of scale and bias (bdt < 0: no bias)
+  const void* q2;      // dual kernels: [n, qs] int8 up weights
+  const void* scale2;  // dual kernels: [n] of sdt
+};
+
+// The epilogue shared by all kernels: scale once, then the bias, one rounding.
+template <typename TO>
+__device__ __forceinline__ void w8_store(const W8Params& p, int64_t m, int n, float acc) {
+  const float sc = load_dyn(p.scale, n, p.sdt);
+  const float v = p.bdt >= 0 ? __builtin_fmaf(acc, sc, load_dyn(p.bias, n, p.bdt)) : acc * sc;
+  store_elem<TO>(p.out, m * p.os + n, v);
+}
+
+// The dual (gate/up) epilogue: both projections scaled once, SiLU-and-mul in
+// fp32, one rounding.
+template <typename TO>
+__device__ __forceinline__ void w8_store_silu(const W8Params& p, int64_t m, int n, float acc_g, float acc_u) {
+  const float g = acc_g * load_dyn(p.scale, n, p.sdt);
+  const float u = acc_u * load_dyn(p.scale2, n, p.sdt);
+  store_elem<TO>(p.out, m * p.os + n, silu_mul_f32(g, u));
+}
+
+// 16 int8 weights (one 16-byte load) -> the B operands of two MFMAs.
+template <typename T>
+__device__ __forceinline__ void widen_i8x16(u32x4 w, u32x4& b0, u32x4& b1) {
+  const u32x2 p0 = widen_i8x4<T>(w.x), p1 = widen_i8x4<T>(w.y);
+  const u32x2 p2 = widen_i8x4<T>(w.z), p3 = widen_i8x4<T>(w.w);
+  b0 = u32x4{p0.x, p0.y, p1.x, p1.y};
+  b1 = u32x4{p2.x, p2.y, p3.x, p3.y};
+}
+
+// Launch shape of w8a16_stream.
+struct StreamPlan {
+  int rpw;    // weight rows per workgroup (<= 4 R4)
+  int r4;     // 4-row weight sets per workgroup (R4: 1, 2 or 4)
+  int waves;  // waves per workgroup (the split of K)
+  int u;      // 256-byte chunks in flight per wave (1 or 2)
+};
+
+template <typename T, typename TO, int R4, int MT4, int U, bool DUAL>
+__global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int rpw) {
+  using TB = typename T::bits;
+  constexpr int NQ = DUAL ? 2 : 1;
+  extern __shared__ float red[];  // [nwave][NQ][R4][MT4][16]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwave = blockDim.x >> 6;
+  const int n0 = blockIdx.x * rpw;
+  const int nrows_w = p.n - n0 < rpw ? p.n - n0 : rpw;
+
+  // Descriptors end right after the last valid element: weight rows past the
+  // workgroup's share and x rows past `rows` (offset >= rows * stride >= the
+  // extent) read 0.
+  rsrc_t rq[NQ];
+  rq[0] = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
+                    static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  if constexpr (DUAL)
+    rq[1] = make_rsrc(static_cast<const int8_t*>(p.q2) + static_cast<int64_t>(n0) * p.qs,
+                      static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((p.rows - 1) * p.xs + p.k) * sizeof(TB)));
+
+  const int quad = lane & 3, set_row = (lane & 15) >> 2, kg = lane >> 4;
+  const int piece = 16 * quad + 64 * kg;  // the lane's 16 k of a 256-column chunk
+  uint32_t qoff[R4], xoff[MT4];
+#pragma unroll
+  for (int r = 0; r < R4; ++r) qoff[r] = static_cast<uint32_t>((4 * r + set_row) * p.qs + piece);
+#pragma unroll
+  for (int t = 0; t < MT4; ++t) xoff[t] = static_cast<uint32_t>(((4 * t + set_row) * p.xs + piece) * sizeof(TB));
+
+  // Scales (and bias) of the outputs this thread stores, loaded now so their
+  // latency hides behind the weight stream instead of following it.
+  constexpr int NOUT = 16 * R4 * MT4;
+  constexpr int OPT = (NOUT + 63) / 64;  // outputs per thread with one wave
+  float osc[OPT][NQ], obias[OPT];
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) {
+    const int o = threadIdx.x + i * blockDim.x;
+    const int nn = 4 * ((o >> 4) % R4) + (o & 3);
+    const bool mine = o < NOUT && nn < nrows_w;
+    osc[i][0] = mine ? load_dyn(p.scale, n0 + nn, p.sdt) : 0.f;
+    if constexpr (DUAL) osc[i][NQ - 1] = mine ? load_dyn(p.scale2, n0 + nn, p.sdt) : 0.f;
+    obias[i] = mine && !DUAL && p.bdt >= 0 ? load_dyn(p.bias, n0 + nn, p.bdt) : 0.f;
+  }
+
+  f32x4 acc[NQ][R4][MT4];
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi) {
+#pragma unroll
+    for (int r = 0; r < R4; ++r) {
+#pragma unroll
+      for (int t = 0; t < MT4; ++t) acc[qi][r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  const int nchunk = (p.k + 255) >> 8;
+  const int c0 = (nchunk * wave) / nwave, c1 = (nchunk * (wave + 1)) / nwave;
+  for (int c = c0; c < c1; c += U) {
+    u32x4 wq[U][NQ][R4], xa[U][MT4][2];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const bool live = c + j < c1 && 256 * (c + j) + piece < p.k;
+#pragma unroll
+      for (int qi = 0; qi < NQ; ++qi) {
+#pragma unroll
+        for (int r = 0; r < R4; ++r) wq[j][qi][r] = buf_load16(rq[qi], live ? qoff[r] + 256u * (c + j) : kOob);
+      }
+#pragma unroll
+      for (int t = 0; t < MT4; ++t) {
+        const uint32_t o = xoff[t] + 256u * sizeof(TB) * (c + j);
+        xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
+        xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
+      }
+    }
+    // every load of the group ahead of its MFMAs: U chunks in flight per wave
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+#pragma unroll
+      for (int qi = 0; qi < NQ; ++qi) {
+#pragma unroll
+        for (int r = 0; r < R4; ++r) {
+          u32x4 b0, b1;
+          widen_i8x16<T>(wq[j][qi][r], b0, b1);
+#pragma unroll
+          for (int t = 0; t < MT4; ++t) {
+            acc[qi][r][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][r][t]);
+            acc[qi][r][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][r][t]);
+          }
+        }
+      }
+    }
+  }
+
+  // Each lane keeps its diagonal register (l % 4), a quad sum adds the four
+  // k-subsets, and lane 16 m' + 4 r' (quad 0) writes acc(x row m', weight row
+  // r') of each set to slot 4 m' + r'.
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi) {
+#pragma unroll
+    for (int r = 0; r < R4; ++r) {
+#pragma unroll
+      for (int t = 0; t < MT4; ++t) {
+        const f32x4 a = acc[qi][r][t];
+        float v = quad == 0 ? a.x : (quad == 1 ? a.y : (quad == 2 ? a.z : a.w));
+        v += dpp_f32<0xb1>(v);  // quad_perm [1,0,3,2]
+        v += dpp_f32<0x4e>(v);  // quad_perm [2,3,0,1]
+        if (quad == 0) red[(((wave * NQ + qi) * R4 + r) * MT4 + t) * 16 + (lane >> 2)] = v;
+      }
+    }
+  }
+  __syncthreads();
+
+  // Output (x row 4 t + m', weight row 4 r + r') = sum over waves, in order;
+  // then the epilogue of w8_store / w8_store_silu with the preloaded scales.
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) {
+    const int o = threadIdx.x + i * blockDim.x;
+    if (o >= NOUT) break;
+    const int slot = o & 15, rt = o >> 4;
+    const int r = rt % R4, t = rt / R4;
+    const int m = 4 * t + (slot >> 2), nn = 4 * r + (slot & 3);
+    if (m >= p.rows || nn >= nrows_w) continue;
+    float sum[NQ];
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      sum[qi] = 0.f;
+      for (int w = 0; w < nwave; ++w) sum[qi] += red[(((w * NQ + qi) * R4 + r) * MT4 + t) * 16 + slot];
+    }
+    const int64_t off = static_cast<int64_t>(m) * p.os + n0 + nn;
+    if constexpr (DUAL) {
+      store_elem<TO>(p.out, off, silu_mul_f32(sum[0] * osc[i][0], sum[NQ - 1] * osc[i][NQ - 1]));
+    } else {
+      store_elem<TO>(p.out, off, p.bdt >= 0 ? __builtin_fmaf(sum[0], osc[i][0], obias[i]) : sum[0] * osc[i][0]);
+    }
+  }
+}
+
+// Launch plan for `rows` <= 8 rows of x against [n, k] int8 weights (two
+// matrices when dual), fitted to a graph-timed sweep of rows per workgroup x
+// waves x chunks in flight on MI355X over the Qwen2.5-0.5B, 1.5B and 7B
+// decode projections and MLPs at 1, 4 and 8 rows (bench.py --only
+// w8-stream-sweep; every pick within 1.11x of the best sampled shape, 1.03x
+// on geometric average, the best one at the 1.5B gate/up and down and the 7B
+// projections with 8 rows):
+//   rows per workgroup: 8 (two 4-row sets); narrow outputs (n <= 2048, or
+//     fewer 8-row workgroups than CUs) as few as give every CU a workgroup,
+//     4 to 8; 16 with more than 4 rows of x and k >= 3072, where every
+//     workgroup re-reads a long x (half the x re-reads of 8); the dual
+//     kernel 4 with up to 4 rows of x, else 8 (or 16 as above);
+//   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
+//     8-row workgroups); else about 14 per CU with up to 4 rows of x, 12 (one
+//     workgroup per CU) or 10 with more, 7 for 16-row workgroups; at least 2
+//     and at most 16 waves, no more than 256-column chunks, and a multiple
+//     of 4 above 8 when there is at most one workgroup per CU, so the CU's
+//     4 SIMDs carry equal loads (14 waves: 1.06x the time of 12);
+//   1 chunk in flight per wave (the CU's waves keep enough bytes in flight).
+inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
+  const bool two_sets = rows > 4;  // x rows in two 4-row sets
+  const int nchunk = (k + 255) / 256;
+  StreamPlan sp{8, 2, 1, 1};
+  if (n <= 2048 || (n + 7) / 8 < cus) {
+    sp.rpw = (n + cus - 1) / cus;
+    sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
+  } else if (two_sets && k >= 3072) {
+    sp.rpw = 16;
+  }
+  if (dual && sp.rpw < 16) sp.rpw = two_sets ? 8 : 4;
+  sp.r4 = sp.rpw <= 4 ? 1 : (sp.rpw <= 8 ? 2 : 4);
+  const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
+  int64_t waves;
+  if (dual) {
+    waves = two_sets && sp.rpw < 16 ? 2 : 3;
+  } else {
+    const int per_cu = sp.rpw == 16 ? 7 : (two_sets ? (wgs <= cus ? 12 : 10) : 14);
+    waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
+  }
+  if (waves > 16) waves = 16;
+  if (waves > nchunk) waves = nchunk;
+  if (waves < 2) waves = nchunk < 2 ? nchunk : 2;
+  if (wgs <= cus && waves > 8) waves = waves / 4 * 4;
+  sp.waves = static_cast<int>(waves);
+  return sp;
+}
+
+// Launches w8a16_stream with plan `sp` (rows <= 8; k, qs multiples of 16,
+// xs a multiple of 8, x and q 16-byte aligned -- the launcher checks these).
+template <typename T, typename TO, bool DUAL>
+int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
+  constexpr int NQ = DUAL ? 2 : 1;
+  const int mt4 = p.rows <= 4 ? 1 : 2;
+  const dim3 grid(static_cast<unsigned>((p.n + sp.rpw - 1) / sp.rpw));
+  const dim3 block(64 * sp.waves);
+  const size_t lds = static_cast<size_t>(sp.waves) * NQ * sp.r4 * mt4 * 16 * sizeof(float);
+  void* args[] = {const_cast<W8Params*>(&p), const_cast<int*>(&sp.rpw)};
+  const void* kern = nullptr;
+#define MI355_W8S(R4, MT4, U) kern = reinterpret_cast<const void*>(w8a16_stream<T, TO, R4, MT4, U, DUAL>)
+#define MI355_W8S_U(R4, MT4) \
+  if (sp.u >= 2) MI355_W8S(R4, MT4, 2); else MI355_W8S(R4, MT4, 1)
+#define MI355_W8S_MT(R4) \
+  if (mt4 == 1) { MI355_W8S_U(R4, 1); } else { MI355_W8S_U(R4, 2); }
+  if (sp.r4 >= 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
+#undef MI355_W8S_MT
+#undef MI355_W8S_U
+#undef MI355_W8S
+  return hip_status(hipLaunchKernel(kern, grid, block, args, lds, s), "w8a16 stream launch");
+}
+
+}  // namespace mi355

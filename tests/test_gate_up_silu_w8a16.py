@@ -62,8 +62,10 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
 @pytest.mark.parametrize("rows,k,n,dt", [
     (1, 1536, 8960, F16), (8, 1536, 8960, F16), (8, 1536, 8960, BF16), (16, 896, 4864, BF16),
     (24, 1536, 1000, F16), (32, 2048, 512, F16), (4, 3584, 18944, BF16),
-    # the 7B MLP at 1 and 8 rows: 2 weight-row groups, 2 waves per workgroup
+    # the 7B MLP at 1 and 8 rows
     (1, 3584, 18944, BF16), (8, 3584, 18944, BF16),
+    # decode rows with a partial last 256-column chunk and a ragged last workgroup
+    (3, 272, 1000, F16), (6, 1552, 520, BF16), (2, 4864, 904, F16),
     # prefill rows: the dual tiled GEMM (and the skinny tiles of small grids)
     (33, 256, 100, BF16), (64, 1536, 1000, F16), (200, 640, 10240, F16), (300, 1552, 520, BF16),
     (1024, 1536, 2048, F16),

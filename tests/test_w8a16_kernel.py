@@ -131,6 +131,26 @@ def test_bf16_matches_oracle(pkg, orc, cuda, M, K, N, bias):
     print(f"bf16 W8A16 [{M}x{K}] x [{N}x{K}]: {same:.5f} equal to the oracle")
 
 
+# Decode rows (<= 8: the lane-coalesced weight-streaming kernel) at every row
+# count of an 8-row tile, over narrow outputs (fewer 8-row workgroups than CUs:
+# 4-7 weight rows per workgroup), wide ones, a partial last 256-column chunk
+# and a ragged last workgroup.
+STREAM_CASES = [(m, K, N, F16 if (m + K) % 2 else BF16, m % 3 == 0)
+                for m in range(1, 9)
+                for K, N in ((8960, 1536), (1536, 8960), (272, 1000), (4864, 896), (1552, 37))]
+
+
+@pytest.mark.parametrize("M,K,N,dt,bias", STREAM_CASES)
+def test_decode_stream_kernel_matches_oracle(pkg, orc, cuda, M, K, N, dt, bias):
+    lin = _linear(K, N, bias, cuda, dtype=dt, seed=M + K)
+    q = pkg.QuantizedLinearInt8.from_linear(lin)
+    x = _x(M, K, dt, cuda, seed=M + 5)
+    got16 = pkg.w8a16_linear(x, q.weight_q, q.scale, q.bias)
+    got32 = pkg.w8a16_linear(x, q.weight_q, q.scale, q.bias, out_dtype=F32)
+    _check_kernel(orc, x, q, got16, got32)
+    assert torch.equal(got16, got32.to(dt)), "the 16-bit output must be the fp32 output rounded once"
+
+
 # Prefill shapes that land on each of the tiled GEMM's launch shapes (by the
 # number of 128 x 128 output tiles), with k tails and ragged edges.
 TILED_CASES = [
@@ -153,9 +173,10 @@ TILED_CASES = [
     # CU and 128 x 128 tiles do not: 192 x 128, registers capped at 128
     (1024, 272, 8960, BF16, False),   # 420 tiles
     (1200, 400, 8000, F16, True),     # 441 tiles: ragged rows and n, k tail
-    # (the 256 x 128 and 256 x 256 sub-step rings, now taken only at k > 4096,
-    # are checked bit for bit against this library by the w8_tile_cfg2 / 3
-    # variants in test_launch_variants.py)
+    # n > 2048 with k > 4096 and many 128 x 64 tiles: the launch plan weighs
+    # rounds of 128 x 64, 256 x 128 and 256 x 256 tiles (sub-step ring)
+    (512, 4608, 14336, F16, True),    # 256 x 128, 8 waves of 128 x 32
+    (1024, 4608, 14336, BF16, False), # 256 x 256, 8 waves of 64 x 128
     # 17 - 64 rows with >= 128 tile columns: the small tiled shapes
     (24, 1536, 8960, F16, True),      # 32 x 64
     (20, 256, 16400, BF16, False),    # n > 10000: 32 x 128
@@ -185,8 +206,16 @@ def test_scale_and_bias_dtypes(pkg, orc, cuda, sdt, bdt):
     got = pkg.w8a16_linear(x, q.weight_q, scale, bias)
     r = orc.w8a16_linear(storage(x.cpu()), q.weight_q.cpu().numpy(), storage(scale.cpu()), storage(bias.cpu()),
                          xdt="f16", sdt=DT_NAME[sdt], bdt=DT_NAME[bdt])
+    # every output within one ulp of the exact value plus the worst-case fp32
+    # summation error of its k products (the kernel's summation order is its
+    # own), and >= 99% equal to the oracle's single rounding
+    ex = r["out64"]
+    k_gamma = K * 2.0 ** -24 / (1 - K * 2.0 ** -24)
+    sc = scale.double().cpu().numpy()
+    tol = _ulp(ex, F16) + k_gamma * r["absacc"] * np.abs(sc) + 2.0 ** -22 * np.abs(ex)
+    assert np.all(np.abs(got.double().cpu().numpy() - ex) <= tol)
     d = orc.ulp_diff16(storage(got.cpu()), r["out"])
-    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    assert (d > 0).mean() < 0.01
 
 
 def test_kernel_handles_3d_input(pkg, cuda):
