@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-breg", "w8-layouts", "w8-stream-sweep", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "stage3",
                                       "e2e-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -138,8 +138,6 @@ class Ctx:
             self.probe.mi355_probe_w8a16_stream_loads.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                                                   vp, vp]
             self.probe.mi355_probe_w8a16_stream_loads.restype = ctypes.c_int
-            self.probe.mi355_probe_w8_tiled.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
-            self.probe.mi355_probe_w8_tiled.restype = ctypes.c_int
 
     def check(self, fn, st):
         if st:
@@ -308,20 +306,6 @@ class Ctx:
         def call():
             if f(*args, self.stream):
                 raise RuntimeError(f"probe w8a16 stream failed for {args[6:]}")
-        return call
-
-    def w8_tiled_call(self, x, q, scale, out, cfg, breg):
-        """The W8A16 prefill GEMM at tile configuration cfg with its weights
-        through LDS (breg 0, the library's kernel) or loaded into registers
-        (breg 1); fp16 x and out, fp32 scales (csrc/probe/w8_breg.hip)."""
-        M, K = x.shape
-        N = q.shape[0]
-        f = self.probe.mi355_probe_w8_tiled
-        args = (x.data_ptr(), q.data_ptr(), scale.data_ptr(), out.data_ptr(), M, K, N, cfg, breg)
-
-        def call():
-            if f(*args, self.stream):
-                raise RuntimeError(f"probe w8 tiled failed for {args[4:]}")
         return call
 
     def add2_call(self, a, b, dst):
@@ -987,10 +971,6 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"w8_stream_layouts": w8_layout_sweep(ctx)}), flush=True)
-    elif args.only == "w8-breg":
-        del sets
-        torch.cuda.empty_cache()
-        print(json.dumps({"w8a16_prefill_breg": w8_breg_compare(ctx)}), flush=True)
     elif args.only == "w8-decomp":
         del sets
         torch.cuda.empty_cache()
@@ -1322,63 +1302,6 @@ def w8_stream_sweep(ctx):
             f"{len(bad)} mismatches {bad[:3]}")
         del qs, scs
         torch.cuda.empty_cache()
-    return out
-
-
-# (rows, k, n, configurations) of the register-B comparison: the wide
-# projections the W8A16 plan sends to the 8-wave tiles (cfg 0: 128 x 128,
-# 3-stage ring; 1: 192 x 128, 2-stage ring, 128 VGPRs; 2: 128 x 128, 4 stages)
-W8_BREG_SHAPES = [(1024, 1536, 8960, (0, 1, 2)), (4096, 1536, 8960, (0, 1, 2)), (1400, 1536, 8960, (0, 1)),
-                  (2048, 3584, 18944, (0, 2))]
-
-
-def w8_breg_compare(ctx, iters=100):
-    """The W8A16 prefill GEMM with its int8 weights loaded straight into
-    registers (the LDS ring carrying x alone) against the library's kernel,
-    which DMAs both operands into LDS, at the same tile configurations, next
-    to the library's own launch and fp16 hipBLASLt: cold weights (rotating
-    sets over >= 1 GiB), min of eager and hipGraph timing, us.  Every
-    register-B output is checked bit for bit against the LDS kernel's at the
-    same configuration (same k order, same fp32 accumulation)."""
-    torch = ctx.torch
-    F16 = torch.float16
-    out = {}
-    for M, K, N, cfgs in W8_BREG_SHAPES:
-        sets = min(256, n_sets(N * K))
-        x = rand(ctx, (M, K), 2700 + M, F16)
-        g = torch.Generator(device=ctx.dev)
-        g.manual_seed(2800 + K + N)
-        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets)]
-        scs = [(torch.rand(N, generator=g, device=ctx.dev) * 1e-3 + 1e-4) for _ in range(sets)]
-        outs = [torch.empty((M, N), dtype=F16, device=ctx.dev) for _ in range(4)]
-        ref = torch.empty((M, N), dtype=F16, device=ctx.dev)
-        chk = torch.empty((M, N), dtype=F16, device=ctx.dev)
-
-        def timed(calls):
-            spin_up(ctx, calls)
-            return round(min(time_loop(ctx, calls, iters), time_graph(ctx, calls, max(2 * sets, 64))), 3)
-
-        d = {"weight_sets": sets,
-             "library_us": timed([ctx.w8a16_call(x, q, sc, outs[i % 4]) for i, (q, sc) in enumerate(zip(qs, scs))])}
-        for cfg in cfgs:
-            ctx.w8_tiled_call(x, qs[0], scs[0], ref, cfg, 0)()
-            ctx.w8_tiled_call(x, qs[0], scs[0], chk, cfg, 1)()
-            torch.cuda.synchronize()
-            same = bool(torch.equal(ref.view(torch.int16), chk.view(torch.int16)))
-            d[f"cfg{cfg}"] = {
-                "lds_us": timed([ctx.w8_tiled_call(x, q, sc, outs[i % 4], cfg, 0) for i, (q, sc) in enumerate(zip(qs, scs))]),
-                "breg_us": timed([ctx.w8_tiled_call(x, q, sc, outs[i % 4], cfg, 1) for i, (q, sc) in enumerate(zip(qs, scs))]),
-                "bit_identical": same}
-        del qs, scs
-        torch.cuda.empty_cache()
-        bsets = min(256, n_sets(N * K * 2))
-        ws = [rand(ctx, (N, K), 2900 + i, F16, std=0.02) for i in range(bsets)]
-        d["hipblaslt_fp16_us"] = timed([(lambda w=w, o=outs[i % 4]: torch.matmul(x, w.T, out=o))
-                                        for i, w in enumerate(ws)])
-        del ws
-        torch.cuda.empty_cache()
-        out[f"M{M}_K{K}_N{N}"] = d
-        log(f"  w8 breg M={M} K={K} N={N}: {json.dumps(d)}")
     return out
 
 
