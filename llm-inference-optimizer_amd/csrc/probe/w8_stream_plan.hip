@@ -21,7 +21,7 @@ namespace {
 // else: the same descriptors, lane offsets, chunk split and U-chunk groups,
 // every loaded dword folded into one XOR that guards a store the data never
 // trigger (so no load can be dropped); without X only the weights.
-template <int R4, int MT4, int U, bool X, bool XP>
+template <int R4, int MT4, int U, bool X>
 __global__ __launch_bounds__(1024) void w8a16_stream_loads(const mi355::W8Params p, const int rpw,
                                                            uint32_t* sink) {
   using namespace mi355;
@@ -34,14 +34,12 @@ __global__ __launch_bounds__(1024) void w8a16_stream_loads(const mi355::W8Params
                               static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
   const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((p.rows - 1) * p.xs + p.k) * 2));
   const int quad = lane & 3, set_row = (lane & 15) >> 2, kg = lane >> 4;
-  const int piece = XP ? 16 * (quad >> 1) + 32 * kg + 128 * (quad & 1) : 16 * quad + 64 * kg;
-  const int xpiece = XP ? 32 * kg + 8 * quad : piece;
-  const int pa = 16 * (quad >> 1) + 32 * kg, pb = pa + 128;
+  const int piece = 16 * quad + 64 * kg;
   uint32_t qoff[R4], xoff[MT4];
 #pragma unroll
   for (int r = 0; r < R4; ++r) qoff[r] = static_cast<uint32_t>((4 * r + set_row) * p.qs + piece);
 #pragma unroll
-  for (int t = 0; t < MT4; ++t) xoff[t] = static_cast<uint32_t>(((4 * t + set_row) * p.xs + xpiece) * 2);
+  for (int t = 0; t < MT4; ++t) xoff[t] = static_cast<uint32_t>(((4 * t + set_row) * p.xs + piece) * 2);
   const int nchunk = (p.k + 255) >> 8;
   const int c0 = (nchunk * wave) / nwave, c1 = (nchunk * (wave + 1)) / nwave;
   uint32_t h = 0;
@@ -56,14 +54,8 @@ __global__ __launch_bounds__(1024) void w8a16_stream_loads(const mi355::W8Params
 #pragma unroll
         for (int t = 0; t < MT4; ++t) {
           const uint32_t o = xoff[t] + 512u * (c + j);
-          if constexpr (XP) {
-            const bool in = c + j < c1;
-            xa[j][t][0] = buf_load16_cached(rx, in && 256 * (c + j) + pa < p.k ? o : kOob);
-            xa[j][t][1] = buf_load16_cached(rx, in && 256 * (c + j) + pb < p.k ? o + 256u : kOob);
-          } else {
-            xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
-            xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
-          }
+          xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
+          xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
         }
       }
     }
@@ -83,40 +75,17 @@ __global__ __launch_bounds__(1024) void w8a16_stream_loads(const mi355::W8Params
   if (h == 0x9e3779b9u) sink[threadIdx.x] = h;
 }
 
-template <int R4, int MT4, bool X, bool XP>
+template <int R4, int MT4, bool X>
 const void* loads_kernel(int u) {
-  if (u >= 2) return reinterpret_cast<const void*>(w8a16_stream_loads<R4, MT4, 2, X, XP>);
-  return reinterpret_cast<const void*>(w8a16_stream_loads<R4, MT4, 1, X, XP>);
+  if (u >= 2) return reinterpret_cast<const void*>(w8a16_stream_loads<R4, MT4, 2, X>);
+  return reinterpret_cast<const void*>(w8a16_stream_loads<R4, MT4, 1, X>);
 }
 
-template <bool X, bool XP>
+template <bool X>
 const void* loads_kernel_r4(int r4, int mt4, int u) {
-  if (r4 == 4) return mt4 == 1 ? loads_kernel<4, 1, X, XP>(u) : loads_kernel<4, 2, X, XP>(u);
-  if (r4 == 2) return mt4 == 1 ? loads_kernel<2, 1, X, XP>(u) : loads_kernel<2, 2, X, XP>(u);
-  return mt4 == 1 ? loads_kernel<1, 1, X, XP>(u) : loads_kernel<1, 2, X, XP>(u);
-}
-
-// The decode kernel at a forced launch shape, in x layout XP or not.
-template <bool DUAL, bool XP>
-const void* stream_kernel(int r4, int mt4, int u) {
-  using mi355::F16;
-  using mi355::w8a16_stream;
-  if (r4 >= 4) {
-    if (mt4 == 1) return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 1, 2, DUAL, XP>)
-                                : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 1, 1, DUAL, XP>);
-    return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 2, 2, DUAL, XP>)
-                  : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 2, 1, DUAL, XP>);
-  }
-  if (r4 == 2) {
-    if (mt4 == 1) return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 1, 2, DUAL, XP>)
-                                : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 1, 1, DUAL, XP>);
-    return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 2, 2, DUAL, XP>)
-                  : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 2, 1, DUAL, XP>);
-  }
-  if (mt4 == 1) return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 1, 2, DUAL, XP>)
-                              : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 1, 1, DUAL, XP>);
-  return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 2, 2, DUAL, XP>)
-                : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 2, 1, DUAL, XP>);
+  if (r4 == 4) return mt4 == 1 ? loads_kernel<4, 1, X>(u) : loads_kernel<4, 2, X>(u);
+  if (r4 == 2) return mt4 == 1 ? loads_kernel<2, 1, X>(u) : loads_kernel<2, 2, X>(u);
+  return mt4 == 1 ? loads_kernel<1, 1, X>(u) : loads_kernel<1, 2, X>(u);
 }
 
 }  // namespace
@@ -134,22 +103,18 @@ extern "C" __attribute__((visibility("default"))) void mi355_probe_w8a16_stream_
 
 // The loads of the W8A16 decode kernel alone (w8a16_stream_loads above) at
 // launch shape (rpw, r4, waves, u) for x [rows <= 8, k] fp16 and q [n, k]
-// int8: the weights only (with_x 0) or the weights and x (with_x 1), in lane
-// layout xp (0: each quad's pieces on 64 contiguous k; 1: the paired x
-// layout, the even quads' pieces in the first 128 k of a chunk).  `sink`
+// int8: the weights only (with_x 0) or the weights and x (with_x 1).  `sink`
 // holds at least 1024 dwords.  Returns 0, -1 on bad arguments, -3 on a
 // launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_loads(
-    const void* x, const void* q, int rows, int k, int n, int rpw, int r4, int waves, int u, int with_x, int xp,
-    void* sink, void* stream) {
+    const void* x, const void* q, int rows, int k, int n, int rpw, int r4, int waves, int u, int with_x, void* sink,
+    void* stream) {
   if (!x || !q || !sink || rows < 1 || rows > 8 || k < 16 || (k & 15) || n < 1 || rpw < 1 ||
-      (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2) ||
-      (xp != 0 && xp != 1))
+      (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2))
     return -1;
   const mi355::W8Params p{x, q, nullptr, nullptr, nullptr, rows, k, n, k, k, n, MI355_F32, -1, nullptr, nullptr};
   const int mt4 = rows <= 4 ? 1 : 2;
-  const void* kern = with_x ? (xp ? loads_kernel_r4<true, true>(r4, mt4, u) : loads_kernel_r4<true, false>(r4, mt4, u))
-                            : (xp ? loads_kernel_r4<false, true>(r4, mt4, u) : loads_kernel_r4<false, false>(r4, mt4, u));
+  const void* kern = with_x ? loads_kernel_r4<true>(r4, mt4, u) : loads_kernel_r4<false>(r4, mt4, u);
   int rpw_arg = rpw;
   void* args[] = {const_cast<mi355::W8Params*>(&p), &rpw_arg, &sink};
   const unsigned grid = static_cast<unsigned>((n + rpw - 1) / rpw);
@@ -162,26 +127,19 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_l
 // NULL: the gate/up + SiLU-and-mul kernel with q, scale the gate and q2,
 // scale2 the up weights), launched with rpw weight rows per workgroup, r4
 // 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves and u chunks in flight
-// (1 or 2), lane layout xp (as above).  rows <= 8, k a multiple of 16, every
-// pointer 16-byte aligned.  Returns 0, -1 on bad arguments, -3 on a launch
-// error.
+// (1 or 2).  rows <= 8, k a multiple of 16, every pointer 16-byte
+// aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
     const void* x, const void* q, const void* scale, const void* q2, const void* scale2, void* out, int rows, int k,
-    int n, int rpw, int r4, int waves, int u, int xp, void* stream) {
+    int n, int rpw, int r4, int waves, int u, void* stream) {
   if (!x || !q || !scale || !out || rows < 1 || rows > 8 || k < 16 || (k & 15) || n < 1 || rpw < 1 ||
       (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2) ||
-      (!q2) != (!scale2) || (xp != 0 && xp != 1))
+      (!q2) != (!scale2))
     return -1;
   const mi355::W8Params p{x, q, scale, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, q2, scale2};
-  const int mt4 = rows <= 4 ? 1 : 2;
-  const bool dual = q2 != nullptr;
-  const void* kern = dual ? (xp ? stream_kernel<true, true>(r4, mt4, u) : stream_kernel<true, false>(r4, mt4, u))
-                          : (xp ? stream_kernel<false, true>(r4, mt4, u) : stream_kernel<false, false>(r4, mt4, u));
-  const size_t lds = static_cast<size_t>(waves) * (dual ? 2 : 1) * r4 * mt4 * 16 * sizeof(float);
-  int rpw_arg = rpw;
-  void* args[] = {const_cast<mi355::W8Params*>(&p), &rpw_arg};
-  const unsigned grid = static_cast<unsigned>((n + rpw - 1) / rpw);
-  if (hipLaunchKernel(kern, dim3(grid), dim3(64 * waves), args, lds, static_cast<hipStream_t>(stream)) != hipSuccess)
-    return -3;
-  return 0;
+  const mi355::StreamPlan sp{rpw, r4, waves, u};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int st = q2 ? mi355::w8_stream_launch<mi355::F16, mi355::F16, true>(p, sp, s)
+                    : mi355::w8_stream_launch<mi355::F16, mi355::F16, false>(p, sp, s);
+  return st == MI355_OK ? 0 : -3;
 }

@@ -91,22 +91,7 @@ struct StreamPlan {
   int u;      // 256-byte chunks in flight per wave (1 or 2)
 };
 
-template <int CTRL> __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
-}
-
-// XP x loads: lanes l and l ^ 1 each loaded half (l & 1) of the even lane's
-// piece (a) and of the odd lane's piece (b); one DPP exchange gives each lane
-// both halves of its own: lo = k 0..7, hi = k 8..15 of its piece.
-__device__ __forceinline__ void x_pair(const u32x4 a, const u32x4 b, const bool even, u32x4& lo, u32x4& hi) {
-  const u32x4 send = even ? b : a;
-  const u32x4 recv = u32x4{dpp_u32<0xb1>(send.x), dpp_u32<0xb1>(send.y), dpp_u32<0xb1>(send.z),
-                           dpp_u32<0xb1>(send.w)};  // quad_perm [1,0,3,2]
-  lo = even ? a : recv;
-  hi = even ? recv : b;
-}
-
-template <typename T, typename TO, int R4, int MT4, int U, bool DUAL, bool XP = false>
+template <typename T, typename TO, int R4, int MT4, int U, bool DUAL>
 __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int rpw) {
   using TB = typename T::bits;
   constexpr int NQ = DUAL ? 2 : 1;
@@ -130,20 +115,12 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
   const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((p.rows - 1) * p.xs + p.k) * sizeof(TB)));
 
   const int quad = lane & 3, set_row = (lane & 15) >> 2, kg = lane >> 4;
-  // the lane's 16 k of a 256-column chunk; XP: the even quads' pieces fill
-  // the first 128 k, the odd quads' the rest, so that each of the two x
-  // loads of a set reads 4 rows x 256 contiguous bytes
-  const int piece = XP ? 16 * (quad >> 1) + 32 * kg + 128 * (quad & 1) : 16 * quad + 64 * kg;
-  // XP x loads: load a reads half (quad & 1) of the piece of quad & 2, load b
-  // that of quad | 1 (element 32 kg + 8 quad, and 128 further)
-  const int xpiece = XP ? 32 * kg + 8 * quad : piece;
-  const int pa = 16 * (quad >> 1) + 32 * kg, pb = pa + 128;  // XP: the pieces loads a and b belong to
-  const bool even = (quad & 1) == 0;
+  const int piece = 16 * quad + 64 * kg;  // the lane's 16 k of a 256-column chunk
   uint32_t qoff[R4], xoff[MT4];
 #pragma unroll
   for (int r = 0; r < R4; ++r) qoff[r] = static_cast<uint32_t>((4 * r + set_row) * p.qs + piece);
 #pragma unroll
-  for (int t = 0; t < MT4; ++t) xoff[t] = static_cast<uint32_t>(((4 * t + set_row) * p.xs + xpiece) * sizeof(TB));
+  for (int t = 0; t < MT4; ++t) xoff[t] = static_cast<uint32_t>(((4 * t + set_row) * p.xs + piece) * sizeof(TB));
 
   // Scales (and bias) of the outputs this thread stores, loaded now so their
   // latency hides behind the weight stream instead of following it.
@@ -185,24 +162,14 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
 #pragma unroll
       for (int t = 0; t < MT4; ++t) {
         const uint32_t o = xoff[t] + 256u * sizeof(TB) * (c + j);
-        if constexpr (XP) {
-          const bool in = c + j < c1;
-          xa[j][t][0] = buf_load16_cached(rx, in && 256 * (c + j) + pa < p.k ? o : kOob);
-          xa[j][t][1] = buf_load16_cached(rx, in && 256 * (c + j) + pb < p.k ? o + 128u * sizeof(TB) : kOob);
-        } else {
-          xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
-          xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
-        }
+        xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
+        xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
       }
     }
     // every load of the group ahead of its MFMAs: U chunks in flight per wave
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-      if constexpr (XP) {
-#pragma unroll
-        for (int t = 0; t < MT4; ++t) x_pair(xa[j][t][0], xa[j][t][1], even, xa[j][t][0], xa[j][t][1]);
-      }
 #pragma unroll
       for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
@@ -267,7 +234,7 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
 // matrices when dual), fitted to a graph-timed sweep of rows per workgroup x
 // waves x chunks in flight on MI355X over the Qwen2.5-0.5B, 1.5B and 7B
 // decode projections and MLPs at 1, 4 and 8 rows (bench.py --only
-// w8-stream-sweep; every pick within 1.11x of the best sampled shape, 1.03x
+// w8-stream-sweep; every pick within 1.08x of the best sampled shape, 1.02x
 // on geometric average, the best one at the 1.5B gate/up and down and the 7B
 // projections with 8 rows):
 //   rows per workgroup: 8 (two 4-row sets); narrow outputs (n <= 2048, or
