@@ -131,7 +131,7 @@ class Ctx:
             self.probe.mi355_probe_w8_stream.restype = ctypes.c_int
             vp = ctypes.c_void_p
             self.probe.mi355_probe_w8a16_stream.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32,
-                                                            i32, i32, vp]
+                                                            i32, vp]
             self.probe.mi355_probe_w8a16_stream.restype = ctypes.c_int
             self.probe.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
             self.probe.mi355_probe_w8a16_stream_plan.restype = None
@@ -294,15 +294,14 @@ class Ctx:
                 raise RuntimeError(f"probe w8a16 stream loads failed for {args[2:10]}")
         return call
 
-    def w8_stream_plan_call(self, x, q, scale, out, rpw, r4, waves, u, q2=None, scale2=None, pf=0):
+    def w8_stream_plan_call(self, x, q, scale, out, rpw, r4, waves, u, q2=None, scale2=None):
         """The W8A16 decode kernel with a forced launch shape (fp16 x and out,
-        fp32 scales; pf 1: the rolling prefetch; csrc/probe/w8_stream_plan.hip)."""
+        fp32 scales; csrc/probe/w8_stream_plan.hip)."""
         M, K = x.shape
         N = q.shape[0]
         f = self.probe.mi355_probe_w8a16_stream
         args = (x.data_ptr(), q.data_ptr(), scale.data_ptr(), q2.data_ptr() if q2 is not None else None,
-                scale2.data_ptr() if scale2 is not None else None, out.data_ptr(), M, K, N, rpw, r4, waves, u,
-                int(pf))
+                scale2.data_ptr() if scale2 is not None else None, out.data_ptr(), M, K, N, rpw, r4, waves, u)
 
         def call():
             if f(*args, self.stream):
@@ -1157,15 +1156,6 @@ def w8_decode_decomposition(ctx):
         d["weight_and_x_loads_us"] = graph_us([ctx.w8_stream_loads_call(x, q, sink, rpw, r4, waves, u, True)
                                                for q in qs])
         d["kernel_us"] = graph_us([ctx.w8a16_call(x, q, sc, o) for q, sc in zip(qs, scales)])
-        # grouped loads (pf 0) vs the rolling prefetch (pf 1), both through the probe's forced shape
-        ref = o.clone()
-        for pf in (0, 1):
-            calls = [ctx.w8_stream_plan_call(x, q, sc, o, rpw, r4, waves, u, pf=pf) for q, sc in zip(qs, scales)]
-            d[f"pf{pf}_kernel_us"] = graph_us(calls)
-            ctx.w8a16_call(x, qs[0], scales[0], ref)()
-            calls[0]()
-            torch.cuda.synchronize()
-            d[f"pf{pf}_max_abs_diff_vs_library"] = float((o.float() - ref.float()).abs().max().item())
         d["read_floor_GBps"] = round(wbytes / d["read_floor_us"] / 1e3, 1)
         d["kernel_GBps"] = round((wbytes + 4 * N + 2 * M * (K + N)) / d["kernel_us"] / 1e3, 1)
         d["kernel_over_weight_loads"] = round(d["kernel_us"] / d["weight_loads_us"], 3)

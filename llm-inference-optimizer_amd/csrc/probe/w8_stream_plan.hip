@@ -123,55 +123,23 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_l
   return 0;
 }
 
-// The decode kernel at a forced launch shape, with the rolling prefetch (PF)
-// or the grouped loads.
-template <bool DUAL, bool PF>
-const void* stream_kernel(int r4, int mt4, int u) {
-  using mi355::F16;
-  using mi355::w8a16_stream;
-  if (r4 >= 4) {
-    if (mt4 == 1) return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 1, 2, DUAL, PF>)
-                                : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 1, 1, DUAL, PF>);
-    return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 2, 2, DUAL, PF>)
-                  : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 4, 2, 1, DUAL, PF>);
-  }
-  if (r4 == 2) {
-    if (mt4 == 1) return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 1, 2, DUAL, PF>)
-                                : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 1, 1, DUAL, PF>);
-    return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 2, 2, DUAL, PF>)
-                  : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 2, 2, 1, DUAL, PF>);
-  }
-  if (mt4 == 1) return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 1, 2, DUAL, PF>)
-                              : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 1, 1, DUAL, PF>);
-  return u >= 2 ? reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 2, 2, DUAL, PF>)
-                : reinterpret_cast<const void*>(w8a16_stream<F16, F16, 1, 2, 1, DUAL, PF>);
-}
-
 // out [rows, n] = W8A16(x [rows, k], q [n, k], scale [n]) (q2 / scale2 not
 // NULL: the gate/up + SiLU-and-mul kernel with q, scale the gate and q2,
 // scale2 the up weights), launched with rpw weight rows per workgroup, r4
 // 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves and u chunks in flight
-// (1 or 2; pf 1: the rolling prefetch, u ignored).  rows <= 8, k a multiple
-// of 16, every pointer 16-byte aligned.  Returns 0, -1 on bad arguments, -3
-// on a launch error.
+// (1 or 2).  rows <= 8, k a multiple of 16, every pointer 16-byte
+// aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
     const void* x, const void* q, const void* scale, const void* q2, const void* scale2, void* out, int rows, int k,
-    int n, int rpw, int r4, int waves, int u, int pf, void* stream) {
+    int n, int rpw, int r4, int waves, int u, void* stream) {
   if (!x || !q || !scale || !out || rows < 1 || rows > 8 || k < 16 || (k & 15) || n < 1 || rpw < 1 ||
       (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2) ||
-      (!q2) != (!scale2) || (pf != 0 && pf != 1))
+      (!q2) != (!scale2))
     return -1;
   const mi355::W8Params p{x, q, scale, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, q2, scale2};
-  const int mt4 = rows <= 4 ? 1 : 2;
-  const bool dual = q2 != nullptr;
-  if (pf) u = 1;
-  const void* kern = dual ? (pf ? stream_kernel<true, true>(r4, mt4, u) : stream_kernel<true, false>(r4, mt4, u))
-                          : (pf ? stream_kernel<false, true>(r4, mt4, u) : stream_kernel<false, false>(r4, mt4, u));
-  const size_t lds = static_cast<size_t>(waves) * (dual ? 2 : 1) * r4 * mt4 * 16 * sizeof(float);
-  int rpw_arg = rpw;
-  void* args[] = {const_cast<mi355::W8Params*>(&p), &rpw_arg};
-  const unsigned grid = static_cast<unsigned>((n + rpw - 1) / rpw);
-  if (hipLaunchKernel(kern, dim3(grid), dim3(64 * waves), args, lds, static_cast<hipStream_t>(stream)) != hipSuccess)
-    return -3;
-  return 0;
+  const mi355::StreamPlan sp{rpw, r4, waves, u};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int st = q2 ? mi355::w8_stream_launch<mi355::F16, mi355::F16, true>(p, sp, s)
+                    : mi355::w8_stream_launch<mi355::F16, mi355::F16, false>(p, sp, s);
+  return st == MI355_OK ? 0 : -3;
 }

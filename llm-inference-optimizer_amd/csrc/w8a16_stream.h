@@ -91,7 +91,7 @@ struct StreamPlan {
   int u;      // 256-byte chunks in flight per wave (1 or 2)
 };
 
-template <typename T, typename TO, int R4, int MT4, int U, bool DUAL, bool PF = false>
+template <typename T, typename TO, int R4, int MT4, int U, bool DUAL>
 __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int rpw) {
   using TB = typename T::bits;
   constexpr int NQ = DUAL ? 2 : 1;
@@ -149,85 +149,37 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
 
   const int nchunk = (p.k + 255) >> 8;
   const int c0 = (nchunk * wave) / nwave, c1 = (nchunk * (wave + 1)) / nwave;
-  // the loads of chunk c into one register set (chunks past the wave's range
-  // or past k read 0 without memory traffic)
-  auto load = [&](int c, u32x4 (&wq)[NQ][R4], u32x4 (&xa)[MT4][2]) {
-    const bool live = c < c1 && 256 * c + piece < p.k;
+  for (int c = c0; c < c1; c += U) {
+    u32x4 wq[U][NQ][R4], xa[U][MT4][2];
 #pragma unroll
-    for (int qi = 0; qi < NQ; ++qi) {
+    for (int j = 0; j < U; ++j) {
+      const bool live = c + j < c1 && 256 * (c + j) + piece < p.k;
 #pragma unroll
-      for (int r = 0; r < R4; ++r) wq[qi][r] = buf_load16(rq[qi], live ? qoff[r] + 256u * c : kOob);
-    }
+      for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-    for (int t = 0; t < MT4; ++t) {
-      const uint32_t o = xoff[t] + 256u * sizeof(TB) * c;
-      xa[t][0] = buf_load16_cached(rx, live ? o : kOob);
-      xa[t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
-    }
-  };
-  auto compute = [&](const u32x4 (&wq)[NQ][R4], const u32x4 (&xa)[MT4][2]) {
+        for (int r = 0; r < R4; ++r) wq[j][qi][r] = buf_load16(rq[qi], live ? qoff[r] + 256u * (c + j) : kOob);
+      }
 #pragma unroll
-    for (int qi = 0; qi < NQ; ++qi) {
-#pragma unroll
-      for (int r = 0; r < R4; ++r) {
-        u32x4 b0, b1;
-        widen_i8x16<T>(wq[qi][r], b0, b1);
-#pragma unroll
-        for (int t = 0; t < MT4; ++t) {
-          acc[qi][r][t] = mfma16<T>(xa[t][0], b0, acc[qi][r][t]);
-          acc[qi][r][t] = mfma16<T>(xa[t][1], b1, acc[qi][r][t]);
-        }
+      for (int t = 0; t < MT4; ++t) {
+        const uint32_t o = xoff[t] + 256u * sizeof(TB) * (c + j);
+        xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
+        xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
       }
     }
-  };
-  if constexpr (PF) {
-    // rolling prefetch: chunk c + 1's loads are issued before chunk c's
-    // MFMAs, so each wave has one chunk in flight while it computes
-    u32x4 wa[NQ][R4], xa_[MT4][2], wb[NQ][R4], xb[MT4][2];
-    if (c0 < c1) load(c0, wa, xa_);
-    for (int c = c0; c < c1; c += 2) {
-      load(c + 1, wb, xb);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(wa, xa_);
-      if (c + 1 < c1) {
-        load(c + 2, wa, xa_);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(wb, xb);
-      }
-    }
-  } else {
-    for (int c = c0; c < c1; c += U) {
-      u32x4 wq[U][NQ][R4], xa[U][MT4][2];
+    // every load of the group ahead of its MFMAs: U chunks in flight per wave
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < U; ++j) {
-        const bool live = c + j < c1 && 256 * (c + j) + piece < p.k;
+    for (int j = 0; j < U; ++j) {
 #pragma unroll
-        for (int qi = 0; qi < NQ; ++qi) {
+      for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-          for (int r = 0; r < R4; ++r) wq[j][qi][r] = buf_load16(rq[qi], live ? qoff[r] + 256u * (c + j) : kOob);
-        }
+        for (int r = 0; r < R4; ++r) {
+          u32x4 b0, b1;
+          widen_i8x16<T>(wq[j][qi][r], b0, b1);
 #pragma unroll
-        for (int t = 0; t < MT4; ++t) {
-          const uint32_t o = xoff[t] + 256u * sizeof(TB) * (c + j);
-          xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
-          xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
-        }
-      }
-      // every load of the group ahead of its MFMAs: U chunks in flight per wave
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < U; ++j) {
-#pragma unroll
-        for (int qi = 0; qi < NQ; ++qi) {
-#pragma unroll
-          for (int r = 0; r < R4; ++r) {
-            u32x4 b0, b1;
-            widen_i8x16<T>(wq[j][qi][r], b0, b1);
-#pragma unroll
-            for (int t = 0; t < MT4; ++t) {
-              acc[qi][r][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][r][t]);
-              acc[qi][r][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][r][t]);
-            }
+          for (int t = 0; t < MT4; ++t) {
+            acc[qi][r][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][r][t]);
+            acc[qi][r][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][r][t]);
           }
         }
       }
