@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stage3",
                                       "e2e-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -138,6 +138,8 @@ class Ctx:
             self.probe.mi355_probe_w8a16_stream_loads.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                                                   vp, vp]
             self.probe.mi355_probe_w8a16_stream_loads.restype = ctypes.c_int
+            self.probe.mi355_probe_gate_up16_stream.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]
+            self.probe.mi355_probe_gate_up16_stream.restype = ctypes.c_int
 
     def check(self, fn, st):
         if st:
@@ -306,6 +308,19 @@ class Ctx:
         def call():
             if f(*args, self.stream):
                 raise RuntimeError(f"probe w8a16 stream failed for {args[6:]}")
+        return call
+
+    def gate_up16_stream_call(self, x, wg, wu, out, rpw, r4, waves, u):
+        """The 16-bit gate/up + SiLU-and-mul through the weight-streaming
+        kernel at a forced launch shape (fp16; csrc/probe/w8_stream_plan.hip)."""
+        M, K = x.shape
+        N = wg.shape[0]
+        f = self.probe.mi355_probe_gate_up16_stream
+        args = (x.data_ptr(), wg.data_ptr(), wu.data_ptr(), out.data_ptr(), M, K, N, rpw, r4, waves, u)
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError(f"probe gate_up16 stream failed for {args[4:]}")
         return call
 
     def add2_call(self, a, b, dst):
@@ -480,24 +495,24 @@ KNOWN_LAUNCHES = {
     ("rmsnorm_block_rows<mi355::BF16, mi355::BF16, mi355::BF16, 2, 1, false>", 4194304): (
         "C4 RMSNorm [16384,3584] bf16", (2 * 16384 * 3584 + 3584) * 2),
     ("stream_copy", 67108864): ("copy probe, 1 GiB", 2 << 30),
-    ("gate_up_silu_skinny<mi355::F16, mi355::F16, 1, 4, 1, 6>", 8960 // 8 * 256): (
+    ("w8a16_stream<mi355::F16, mi355::F16, 1, 2, 2, true, 2>", 8960 // 4 * 64 * 2): (
         "gate/up + SiLU-and-mul, 8 rows, [8960,1536] weights, fp16",
         2 * 8960 * 1536 * 2 + 8 * 1536 * 2 + 8 * 8960 * 2),
     # W8A16 decode (w8a16_stream) at its launch plan, 8 rows: grid = workgroups x 64 x waves
-    ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 1, false>", 1120 * 64 * 2): (
+    ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 1, false, 1>", 1120 * 64 * 2): (
         "W8A16 1.5B gate/up, 8 rows, [8960,1536] int8, fp16", 8960 * 1536 + 4 * 8960 + 8 * 1536 * 2 + 8 * 8960 * 2),
-    ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 1, false>", 256 * 64 * 12): (
+    ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 1, false, 1>", 256 * 64 * 12): (
         "W8A16 1.5B down, 8 rows, [1536,8960] int8, fp16", 1536 * 8960 + 4 * 1536 + 8 * 8960 * 2 + 8 * 1536 * 2),
-    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, false>", 1184 * 64 * 2): (
+    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, false, 1>", 1184 * 64 * 2): (
         "W8A16 7B gate/up, 8 rows, [18944,3584] int8, bf16",
         18944 * 3584 + 4 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
-    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, false>", 224 * 64 * 8): (
+    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, false, 1>", 224 * 64 * 8): (
         "W8A16 7B down, 8 rows, [3584,18944] int8, bf16",
         3584 * 18944 + 4 * 3584 + 8 * 18944 * 2 + 8 * 3584 * 2),
-    ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 1, true>", 1120 * 64 * 2): (
+    ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 1, true, 1>", 1120 * 64 * 2): (
         "int8 gate/up + SiLU-and-mul 1.5B, 8 rows, 2 x [8960,1536] int8, fp16",
         2 * 8960 * 1536 + 8 * 8960 + 8 * 1536 * 2 + 8 * 8960 * 2),
-    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, true>", 1184 * 64 * 3): (
+    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, true, 1>", 1184 * 64 * 3): (
         "int8 gate/up + SiLU-and-mul 7B, 8 rows, 2 x [18944,3584] int8, bf16",
         2 * 18944 * 3584 + 8 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
     ("linear16_skinny<mi355::F16, mi355::F16, 1, 1, 2>", 192 * 512): (
@@ -745,6 +760,12 @@ def main():
     silu_us = time_loop(ctx, [s[1] for s in sets], iters)
     rms_us = time_loop(ctx, [s[0] for s in sets], iters)
     rms_graph_us = time_graph(ctx, [s[0] for s in sets], 200)
+    # the same launches through the product API (fused_rmsnorm: the C++
+    # launcher extension, which also allocates the output) and an empty
+    # kernel through the C ABI, eager back to back: the host's share of C1
+    pkg = ctx.pkg
+    rms_api_us = time_loop(ctx, [(lambda x=t[0]: pkg.fused_rmsnorm(x, w, 1e-6)) for _, _, t in sets], iters)
+    empty_us = time_loop(ctx, [ctx.empty_call()], iters)
     silu_warm_us = time_loop(ctx, [sets[0][1]], iters)
     rms_warm_graph_us = time_graph(ctx, [sets[0][0]], 200)
     kernels = {
@@ -754,13 +775,18 @@ def main():
                                                  {"timing": "events over back-to-back launches, cold"}),
         "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows", rms_bytes,
                                                        rms_graph_us, {"timing": "hipGraph of 200 launches, cold"}),
+        "c1_rmsnorm_f16_2048x1536_api": kernel_entry("rmsnorm_wave_rows", rms_bytes, rms_api_us,
+                                                     {"timing": "fused_rmsnorm (product API), events over "
+                                                                "back-to-back calls, cold"}),
+        "empty_kernel_eager_us": round(empty_us, 3),
         "c2_silu_mul_f16_2048x8960_warm": kernel_entry("silu_mul_chunks", silu_bytes, silu_warm_us,
                                                        {"timing": "same buffers every launch (MALL-warm)"}),
         "c1_rmsnorm_f16_2048x1536_warm_graph": kernel_entry("rmsnorm_wave_rows", rms_bytes, rms_warm_graph_us,
                                                             {"timing": "hipGraph, same buffers (MALL-warm)"}),
     }
     for k, v in kernels.items():
-        log(f"  {k}: {v['us']:.2f} us, {v['GBps']:.0f} GB/s ({v['frac_of_peak']:.1%})")
+        if isinstance(v, dict):
+            log(f"  {k}: {v['us']:.2f} us, {v['GBps']:.0f} GB/s ({v['frac_of_peak']:.1%})")
 
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -849,6 +875,9 @@ def per_config(full):
         "C4_silu_mul_bf16_16384x18944": entry(c4["c4_silu_mul_bf16_16384x18944"], 16384,
                                               "C4 SiLU-and-mul [16384,18944] bf16"),
     }
+    if "c1_rmsnorm_f16_2048x1536_api" in k:
+        pc["C1_rmsnorm_f16_2048x1536"]["api_us"] = k["c1_rmsnorm_f16_2048x1536_api"]["us"]
+        pc["C1_rmsnorm_f16_2048x1536"]["empty_kernel_eager_us"] = k["empty_kernel_eager_us"]
     c3 = {}
     for m, d in dec.items():
         if not m.startswith("M="):
@@ -963,6 +992,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"e2e_stage3": bench_e2e_compact(ctx)}), flush=True)
+    elif args.only == "gu16-stream-sweep":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"gate_up16_stream_sweep": gu16_stream_sweep(ctx)}), flush=True)
     elif args.only == "w8-stream-sweep":
         del sets
         torch.cuda.empty_cache()
@@ -1305,6 +1338,59 @@ def w8_stream_sweep(ctx):
     return out
 
 
+# (label, rows, k, n) of the 16-bit gate/up + SiLU-and-mul decode sweep: the
+# Qwen2.5-0.5B, 1.5B and 7B MLPs at 1, 4 and 8 rows
+GU16_SWEEP_SHAPES = [("gu1.5b_M1", 1, 1536, 8960), ("gu1.5b_M4", 4, 1536, 8960), ("gu1.5b_M8", 8, 1536, 8960),
+                     ("gu0.5b_M1", 1, 896, 4864), ("gu0.5b_M8", 8, 896, 4864),
+                     ("gu7b_M1", 1, 3584, 18944), ("gu7b_M8", 8, 3584, 18944)]
+
+
+def gu16_stream_sweep(ctx):
+    """The 16-bit gate/up + SiLU-and-mul at decode rows: the library's
+    launch (mi355_gate_up_silu_fwd) against the weight-streaming kernel of
+    w8a16_stream.h with 16-bit weights over launch shapes (rows per
+    workgroup 4-16 x waves 1-16 x chunks in flight 1-2), graph-node us over
+    cold weights, fp16; each shape's output checked against the library's
+    (within 2e-3 of the largest output)."""
+    torch = ctx.torch
+    F16 = torch.float16
+    out = {}
+    for label, M, K, N in GU16_SWEEP_SHAPES:
+        sets = n_sets(2 * N * K * 2)
+        ws = [(rand(ctx, (N, K), 3100 + 2 * i, F16, std=2.0 * K ** -0.5), rand(ctx, (N, K), 3101 + 2 * i, F16,
+                                                                                std=K ** -0.5))
+              for i in range(sets)]
+        x = rand(ctx, (M, K), 3000 + M, F16)
+        o = torch.empty((M, N), dtype=F16, device=ctx.dev)
+        ref = torch.empty_like(o)
+        nodes = max(2 * sets, 64)
+        lib_calls = [ctx.gate_up_call(x, wg, wu, o) for wg, wu in ws]
+        ctx.gate_up_call(x, ws[0][0], ws[0][1], ref)()
+        torch.cuda.synchronize()
+        tol = 2e-3 * ref.float().abs().max().item()
+        res, bad = {}, []
+        nchunk = -(-K // 128)
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, 1 if M <= 4 else 2):
+            calls = [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u) for wg, wu in ws]
+            calls[0]()
+            torch.cuda.synchronize()
+            err = (o.float() - ref.float()).abs().max().item()
+            if not err <= tol:
+                bad.append((rpw, r4, waves, u, err))
+            spin_up(ctx, calls, ms=3.0)
+            res[f"rpw{rpw}_w{waves}_u{u}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
+        spin_up(ctx, lib_calls, ms=5.0)
+        res["library_us"] = round(time_graph(ctx, lib_calls, nodes, replays=5), 3)
+        best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
+        out[label] = {"best": best, "best_us": res[best], "library_us": res["library_us"], "mismatches": bad,
+                      "shapes": res}
+        log(f"  gu16 stream sweep {label}: library {res['library_us']} us, best {best} {res[best]} us, "
+            f"{len(bad)} mismatches {bad[:3]}")
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_add_rms(ctx, iters):
     """Residual add + RMSNorm at the C1 shape (beyond the reference): the fused
     kernel vs the unfused pair (torch's add, then the RMSNorm kernel), cold."""
@@ -1477,11 +1563,11 @@ def bench_gate_up(ctx, shapes=GATE_UP_SHAPES, iters=400, baselines=True):
         us = time_loop(ctx, fused, iters)
         us_graph = time_graph(ctx, fused, 4 * layers)
         key = f"{label}_M{M}_{dname}"
-        entry = kernel_entry("gate_up_silu_skinny", nbytes, us,
+        kname = "w8a16_stream (16-bit weights)" if M <= 8 else ("gate_up_silu_skinny" if M <= 16 else
+                                                                  "gate_up_silu_skinny or tiled_gemm")
+        entry = kernel_entry(kname, nbytes, us,
                              {"weight_sets": layers, "graph_us": round(us_graph, 3),
                               "graph_GBps": round(nbytes / us_graph / 1e3, 1)})
-        if (M, K, I, dname) == (8, 1536, 8960, "f16"):
-            entry["traffic"] = read_traffic("gate/up + SiLU-and-mul, 8 rows, [8960,1536] weights, fp16")
         if baselines:
             silu = ctx.pkg.fused_silu_mul
 

@@ -143,3 +143,20 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
                     : mi355::w8_stream_launch<mi355::F16, mi355::F16, false>(p, sp, s);
   return st == MI355_OK ? 0 : -3;
 }
+
+// out [rows, n] = silu(x @ wg^T) * (x @ wu^T) for x [rows, k] and 16-bit
+// weights [n, k] (fp16), by the weight-streaming kernel of w8a16_stream.h
+// with 16-bit weights (WB = 2) at launch shape (rpw, r4, waves, u).  rows <=
+// 8, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on bad
+// arguments, -3 on a launch error.
+extern "C" __attribute__((visibility("default"))) int mi355_probe_gate_up16_stream(
+    const void* x, const void* wg, const void* wu, void* out, int rows, int k, int n, int rpw, int r4, int waves,
+    int u, void* stream) {
+  if (!x || !wg || !wu || !out || rows < 1 || rows > 8 || k < 8 || (k & 7) || n < 1 || rpw < 1 ||
+      (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2))
+    return -1;
+  const mi355::W8Params p{x, wg, nullptr, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, wu, nullptr};
+  const mi355::StreamPlan sp{rpw, r4, waves, u};
+  const int st = mi355::w8_stream_launch<mi355::F16, mi355::F16, true, 2>(p, sp, static_cast<hipStream_t>(stream));
+  return st == MI355_OK ? 0 : -3;
+}

@@ -1,6 +1,8 @@
 // The W8A16 decode kernel (up to 8 rows of x): int8 weight streaming with
 // lane-coalesced loads, plus its launch plan.  Shared by the W8A16 linear and
-// the int8 gate/up + SiLU-and-mul launchers (w8a16.hip).
+// the int8 gate/up + SiLU-and-mul launchers (w8a16.hip) and, with 16-bit
+// weights (template argument WB = 2, below), by the 16-bit gate/up +
+// SiLU-and-mul launcher (gate_up_silu.hip).
 //
 //   out[m, n] = round(acc * scale[n] + bias[n]),  acc = sum_k x[m, k] * q[n, k]
 //   (DUAL: out[m, n] = round(silu(acc_g * scale_g[n]) * (acc_u * scale_u[n])))
@@ -91,10 +93,19 @@ struct StreamPlan {
   int u;      // 256-byte chunks in flight per wave (1 or 2)
 };
 
-template <typename T, typename TO, int R4, int MT4, int U, bool DUAL>
+// WB: bytes per weight element -- 1 (int8 weights with per-row scales, the
+// W8A16 linear and the int8 gate/up + SiLU-and-mul) or 2 (weights of x's
+// 16-bit type, no scales: the 16-bit gate/up + SiLU-and-mul, DUAL only).  A
+// lane's 16-byte weight load is then 8 k, one B operand as loaded, a chunk
+// of a weight row's 256 bytes is 128 k, and one 16-byte x load per 4-row x
+// set matches it.
+template <typename T, typename TO, int R4, int MT4, int U, bool DUAL, int WB = 1>
 __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int rpw) {
   using TB = typename T::bits;
   constexpr int NQ = DUAL ? 2 : 1;
+  constexpr bool W16 = WB == 2;
+  constexpr int KC = 256 / WB;  // k per 256-byte chunk of a weight row
+  static_assert(WB == 1 || (WB == 2 && DUAL), "16-bit weights: the gate/up kernel only");
   extern __shared__ float red[];  // [nwave][NQ][R4][MT4][16]
 
   const int lane = threadIdx.x & 63;
@@ -107,18 +118,19 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
   // workgroup's share and x rows past `rows` (offset >= rows * stride >= the
   // extent) read 0.
   rsrc_t rq[NQ];
-  rq[0] = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs,
-                    static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+  rq[0] = make_rsrc(static_cast<const int8_t*>(p.q) + static_cast<int64_t>(n0) * p.qs * WB,
+                    static_cast<uint32_t>(((nrows_w - 1) * p.qs + p.k) * WB));
   if constexpr (DUAL)
-    rq[1] = make_rsrc(static_cast<const int8_t*>(p.q2) + static_cast<int64_t>(n0) * p.qs,
-                      static_cast<uint32_t>((nrows_w - 1) * p.qs + p.k));
+    rq[1] = make_rsrc(static_cast<const int8_t*>(p.q2) + static_cast<int64_t>(n0) * p.qs * WB,
+                      static_cast<uint32_t>(((nrows_w - 1) * p.qs + p.k) * WB));
   const rsrc_t rx = make_rsrc(p.x, static_cast<uint32_t>(((p.rows - 1) * p.xs + p.k) * sizeof(TB)));
 
   const int quad = lane & 3, set_row = (lane & 15) >> 2, kg = lane >> 4;
-  const int piece = 16 * quad + 64 * kg;  // the lane's 16 k of a 256-column chunk
+  // the lane's 16 bytes of a weight row's 256-byte chunk: 16 k (int8) or 8 k
+  const int piece = (16 * quad + 64 * kg) >> (WB - 1);
   uint32_t qoff[R4], xoff[MT4];
 #pragma unroll
-  for (int r = 0; r < R4; ++r) qoff[r] = static_cast<uint32_t>((4 * r + set_row) * p.qs + piece);
+  for (int r = 0; r < R4; ++r) qoff[r] = static_cast<uint32_t>(((4 * r + set_row) * p.qs + piece) * WB);
 #pragma unroll
   for (int t = 0; t < MT4; ++t) xoff[t] = static_cast<uint32_t>(((4 * t + set_row) * p.xs + piece) * sizeof(TB));
 
@@ -129,6 +141,7 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
   float osc[OPT][NQ], obias[OPT];
 #pragma unroll
   for (int i = 0; i < OPT; ++i) {
+    if constexpr (W16) break;  // no scales
     const int o = threadIdx.x + i * blockDim.x;
     const int nn = 4 * ((o >> 4) % R4) + (o & 3);
     const bool mine = o < NOUT && nn < nrows_w;
@@ -147,13 +160,13 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
     }
   }
 
-  const int nchunk = (p.k + 255) >> 8;
+  const int nchunk = (p.k + KC - 1) >> (W16 ? 7 : 8);
   const int c0 = (nchunk * wave) / nwave, c1 = (nchunk * (wave + 1)) / nwave;
   for (int c = c0; c < c1; c += U) {
     u32x4 wq[U][NQ][R4], xa[U][MT4][2];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-      const bool live = c + j < c1 && 256 * (c + j) + piece < p.k;
+      const bool live = c + j < c1 && KC * (c + j) + piece < p.k;
 #pragma unroll
       for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
@@ -161,9 +174,9 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
       }
 #pragma unroll
       for (int t = 0; t < MT4; ++t) {
-        const uint32_t o = xoff[t] + 256u * sizeof(TB) * (c + j);
+        const uint32_t o = xoff[t] + KC * sizeof(TB) * (c + j);
         xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
-        xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
+        if constexpr (!W16) xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
       }
     }
     // every load of the group ahead of its MFMAs: U chunks in flight per wave
@@ -174,12 +187,17 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
       for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
         for (int r = 0; r < R4; ++r) {
-          u32x4 b0, b1;
-          widen_i8x16<T>(wq[j][qi][r], b0, b1);
+          if constexpr (W16) {
 #pragma unroll
-          for (int t = 0; t < MT4; ++t) {
-            acc[qi][r][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][r][t]);
-            acc[qi][r][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][r][t]);
+            for (int t = 0; t < MT4; ++t) acc[qi][r][t] = mfma16<T>(xa[j][t][0], wq[j][qi][r], acc[qi][r][t]);
+          } else {
+            u32x4 b0, b1;
+            widen_i8x16<T>(wq[j][qi][r], b0, b1);
+#pragma unroll
+            for (int t = 0; t < MT4; ++t) {
+              acc[qi][r][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][r][t]);
+              acc[qi][r][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][r][t]);
+            }
           }
         }
       }
@@ -222,7 +240,9 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
       for (int w = 0; w < nwave; ++w) sum[qi] += red[(((w * NQ + qi) * R4 + r) * MT4 + t) * 16 + slot];
     }
     const int64_t off = static_cast<int64_t>(m) * p.os + n0 + nn;
-    if constexpr (DUAL) {
+    if constexpr (W16) {
+      store_elem<TO>(p.out, off, silu_mul_f32(sum[0], sum[NQ - 1]));
+    } else if constexpr (DUAL) {
       store_elem<TO>(p.out, off, silu_mul_f32(sum[0] * osc[i][0], sum[NQ - 1] * osc[i][NQ - 1]));
     } else {
       store_elem<TO>(p.out, off, p.bdt >= 0 ? __builtin_fmaf(sum[0], osc[i][0], obias[i]) : sum[0] * osc[i][0]);
@@ -277,9 +297,26 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
   return sp;
 }
 
-// Launches w8a16_stream with plan `sp` (rows <= 8; k, qs multiples of 16,
-// xs a multiple of 8, x and q 16-byte aligned -- the launcher checks these).
-template <typename T, typename TO, bool DUAL>
+// Launch plan of the 16-bit gate/up + SiLU-and-mul (WB = 2) for `rows` <= 8
+// rows of x against two [n, k] weight matrices, from a graph-timed sweep of
+// rows per workgroup x waves x chunks in flight on MI355X over the
+// Qwen2.5-0.5B, 1.5B and 7B MLPs at 1, 4 and 8 rows (bench.py --only
+// gu16-stream-sweep): up to k = 2048, 4 weight rows per workgroup, 2 waves,
+// 2 chunks in flight (the most workgroups; 1.5B, 8 rows 11.17 us against
+// 12.59 us for gate_up_silu_skinny); deeper (7B), 4 rows and 8 waves with 2
+// chunks in flight up to 4 rows of x (39.84 vs 42.77 us), 16 rows and 8
+// waves with one chunk beyond, where every workgroup re-reads the long x
+// (42.07 vs 44.48 us).
+inline StreamPlan gu16_stream_plan(int rows, int k) {
+  if (k <= 2048) return StreamPlan{4, 1, 2, 2};
+  if (rows <= 4) return StreamPlan{4, 1, 8, 2};
+  return StreamPlan{16, 4, 8, 1};
+}
+
+// Launches w8a16_stream with plan `sp` (rows <= 8; k, qs multiples of 16 --
+// of 8 for 16-bit weights --, xs a multiple of 8, x and the weights 16-byte
+// aligned: the callers check these).
+template <typename T, typename TO, bool DUAL, int WB = 1>
 int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   constexpr int NQ = DUAL ? 2 : 1;
   const int mt4 = p.rows <= 4 ? 1 : 2;
@@ -288,7 +325,7 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   const size_t lds = static_cast<size_t>(sp.waves) * NQ * sp.r4 * mt4 * 16 * sizeof(float);
   void* args[] = {const_cast<W8Params*>(&p), const_cast<int*>(&sp.rpw)};
   const void* kern = nullptr;
-#define MI355_W8S(R4, MT4, U) kern = reinterpret_cast<const void*>(w8a16_stream<T, TO, R4, MT4, U, DUAL>)
+#define MI355_W8S(R4, MT4, U) kern = reinterpret_cast<const void*>(w8a16_stream<T, TO, R4, MT4, U, DUAL, WB>)
 #define MI355_W8S_U(R4, MT4) \
   if (sp.u >= 2) MI355_W8S(R4, MT4, 2); else MI355_W8S(R4, MT4, 1)
 #define MI355_W8S_MT(R4) \

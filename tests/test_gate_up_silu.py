@@ -72,6 +72,9 @@ def _check_vs_oracle(orc, got16, got32, x, wg, wu, dt):
 @pytest.mark.parametrize("rows,k,n,dt", [
     (8, 1536, 8960, F16), (1, 1536, 8960, BF16), (32, 1536, 8960, F16), (16, 896, 4864, BF16),
     (4, 3584, 18944, BF16), (5, 72, 40, F16), (33, 40, 24, BF16), (3, 8, 7, F16), (100, 256, 100, BF16),
+    # up to 8 rows: the weight-streaming kernel's three launch shapes, k tails past a 128-column chunk,
+    # ragged weight-row counts
+    (6, 3584, 1000, BF16), (7, 136, 520, F16), (2, 2056, 264, F16), (8, 2048, 4099, BF16), (1, 24, 1, F16),
     (17, 2048, 1000, F16),
     # prefill rows: the tiled GEMM (each of its three launch shapes, k tails, ragged edges)
     (64, 1536, 1000, F16), (200, 640, 10240, BF16), (300, 1552, 520, F16), (257, 96, 333, BF16),
