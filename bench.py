@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stage3",
                                       "e2e-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -996,6 +996,11 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"gate_up16_stream_sweep": gu16_stream_sweep(ctx)}), flush=True)
+    elif args.only == "stream-sweep16":  # 9 - 16 rows: both decode sweeps
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP16_SHAPES),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP16_SHAPES)}), flush=True)
     elif args.only == "w8-stream-sweep":
         del sets
         torch.cuda.empty_cache()
@@ -1247,12 +1252,14 @@ def _w8_stream_shapes(nchunk, dual, mt4):
     out = []
     for rpw in (4, 6, 8, 12, 16):
         r4 = 1 if rpw <= 4 else (2 if rpw <= 8 else 4)
+        if mt4 > 2 and r4 == 4:  # 12 or 16 rows of x: 16-row workgroups spill registers
+            continue
         for waves in (1, 2, 3, 4, 6, 8, 12, 16):
             if waves > nchunk:
                 continue
             per_wave = -(-nchunk // waves)
             for u in (1, 2):
-                if u > 1 and u > per_wave:
+                if u > 1 and (u > per_wave or mt4 > 2):
                     continue
                 if dual and r4 == 4 and u >= 2:  # spills registers
                     continue
@@ -1274,7 +1281,18 @@ W8_STREAM_SWEEP_SHAPES = [
 ]
 
 
-def w8_stream_sweep(ctx):
+# 9 - 16 rows of x (four 4-row x sets at most): the Qwen2.5-0.5B, 1.5B and 7B
+# projections and MLPs at 12 and 16 rows
+W8_STREAM_SWEEP16_SHAPES = [
+    ("down_M12", 12, 8960, 1536, False), ("down_M16", 16, 8960, 1536, False),
+    ("gateup_M12", 12, 1536, 8960, False), ("gateup_M16", 16, 1536, 8960, False),
+    ("dual_gateup_M16", 16, 1536, 8960, True), ("down7b_M16", 16, 18944, 3584, False),
+    ("gateup7b_M16", 16, 3584, 18944, False), ("o1.5b_M16", 16, 1536, 1536, False),
+    ("down0.5b_M16", 16, 4864, 896, False), ("dual7b_M16", 16, 3584, 18944, True),
+]
+
+
+def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES):
     """The W8A16 decode kernel (w8a16_stream) over launch shapes, through the
     probe library's forced-shape entry point, at the Qwen2.5-1.5B down and
     gate/up projections and the int8 gate/up + SiLU-and-mul MLP, 1 and 8 rows
@@ -1285,7 +1303,7 @@ def w8_stream_sweep(ctx):
     F16 = torch.float16
     cus = torch.cuda.get_device_properties(ctx.dev).multi_processor_count
     out = {}
-    for label, M, K, N, dual in W8_STREAM_SWEEP_SHAPES:
+    for label, M, K, N, dual in shapes:
         nq = 2 if dual else 1
         sets = n_sets(nq * N * K)
         g = torch.Generator(device=ctx.dev)
@@ -1308,7 +1326,7 @@ def w8_stream_sweep(ctx):
         tol = 2e-3 * ref.float().abs().max().item()
         bad = []
         nchunk = -(-K // 256)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, 1 if M <= 4 else 2):
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, -(-M // 4)):
             def mk(q, sc):
                 if dual:
                     return ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u, q[1], sc[1])
@@ -1343,9 +1361,11 @@ def w8_stream_sweep(ctx):
 GU16_SWEEP_SHAPES = [("gu1.5b_M1", 1, 1536, 8960), ("gu1.5b_M4", 4, 1536, 8960), ("gu1.5b_M8", 8, 1536, 8960),
                      ("gu0.5b_M1", 1, 896, 4864), ("gu0.5b_M8", 8, 896, 4864),
                      ("gu7b_M1", 1, 3584, 18944), ("gu7b_M8", 8, 3584, 18944)]
+GU16_SWEEP16_SHAPES = [("gu1.5b_M12", 12, 1536, 8960), ("gu1.5b_M16", 16, 1536, 8960),
+                       ("gu0.5b_M16", 16, 896, 4864), ("gu7b_M16", 16, 3584, 18944)]
 
 
-def gu16_stream_sweep(ctx):
+def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES):
     """The 16-bit gate/up + SiLU-and-mul at decode rows: the library's
     launch (mi355_gate_up_silu_fwd) against the weight-streaming kernel of
     w8a16_stream.h with 16-bit weights over launch shapes (rows per
@@ -1355,7 +1375,7 @@ def gu16_stream_sweep(ctx):
     torch = ctx.torch
     F16 = torch.float16
     out = {}
-    for label, M, K, N in GU16_SWEEP_SHAPES:
+    for label, M, K, N in shapes:
         sets = n_sets(2 * N * K * 2)
         ws = [(rand(ctx, (N, K), 3100 + 2 * i, F16, std=2.0 * K ** -0.5), rand(ctx, (N, K), 3101 + 2 * i, F16,
                                                                                 std=K ** -0.5))
@@ -1370,7 +1390,7 @@ def gu16_stream_sweep(ctx):
         tol = 2e-3 * ref.float().abs().max().item()
         res, bad = {}, []
         nchunk = -(-K // 128)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, 1 if M <= 4 else 2):
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, -(-M // 4)):
             calls = [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u) for wg, wu in ws]
             calls[0]()
             torch.cuda.synchronize()

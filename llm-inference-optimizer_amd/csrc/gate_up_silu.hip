@@ -364,25 +364,24 @@ int gate_up_tiled(const GateUpParams& p, hipStream_t s) {
 
 template <typename T, typename TO>
 int gate_up_typed(const GateUpParams& p, hipStream_t s) {
-  // Up to 8 rows: the lane-coalesced weight-streaming kernel of
+  // Up to 16 rows: the lane-coalesced weight-streaming kernel of
   // w8a16_stream.h with 16-bit weights (its x descriptor must span under
-  // 2^32 bytes); 9 - 16 rows: the skinny kernel above with the fewest
-  // 8-row MFMA tiles that cover the rows.  More rows take the tiled GEMM when its
+  // 2^32 bytes; else the skinny kernel above with the fewest 8-row MFMA
+  // tiles that cover the rows).  More rows take the tiled GEMM when its
   // descriptors fit -- from 17 rows its small tiles read each weight byte
   // once from HBM and x once per workgroup, where 3 or 4 skinny x tiles
   // re-load x per weight piece (1.5B, 32 rows 20.0 -> 15.5 us; 7B 66.7 ->
   // 53.8 us), as long as the output has >= 128 tile columns to spread over
   // the CUs -- else 24- or 32-row skinny tiles along grid y.
-  if (p.rows <= 8) {
+  if (p.rows <= 16) {
     const int64_t x_bytes = ((p.rows - 1) * p.xs + p.k) * static_cast<int64_t>(sizeof(typename T::bits));
     if (x_bytes < (int64_t{1} << 32)) {
       const W8Params w{p.x, p.wg, nullptr, nullptr, p.out, p.rows, p.k, p.n_out, p.xs, p.ws, p.os, MI355_F32, -1,
                        p.wu, nullptr};
       return w8_stream_launch<T, TO, true, 2>(w, gu16_stream_plan(p.rows, p.k), s);
     }
-    return gate_up_shape<T, TO, 1>(p, s);
+    return p.rows <= 8 ? gate_up_shape<T, TO, 1>(p, s) : gate_up_shape<T, TO, 2>(p, s);
   }
-  if (p.rows <= 16) return gate_up_shape<T, TO, 2>(p, s);
   const bool tiled_fits = int64_t{256} * p.xs * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31) &&
                           int64_t{128} * p.ws * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31);
   const int bn = p.n_out > 10000 ? 128 : 64;

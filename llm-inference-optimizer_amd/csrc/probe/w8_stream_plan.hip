@@ -123,40 +123,79 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_l
   return 0;
 }
 
+namespace {
+
+// The decode kernel at any launch shape the probes accept: R4 in {1, 2, 4},
+// MT4 = ceil(rows / 4) in 1 .. 4 (16 rows of x), U in {1, 2} (U = 1 only
+// for MT4 > 2); fp16 x, weights of WB bytes.
+template <bool DUAL, int WB, int R4, int MT4>
+const void* sk_u(int u) {
+  using mi355::F16;
+  if constexpr (MT4 <= 2) {
+    if (u >= 2) return reinterpret_cast<const void*>(mi355::w8a16_stream<F16, F16, R4, MT4, 2, DUAL, WB>);
+  }
+  return reinterpret_cast<const void*>(mi355::w8a16_stream<F16, F16, R4, MT4, 1, DUAL, WB>);
+}
+template <bool DUAL, int WB, int R4>
+const void* sk_mt(int mt4, int u) {
+  if (mt4 == 1) return sk_u<DUAL, WB, R4, 1>(u);
+  if (mt4 == 2) return sk_u<DUAL, WB, R4, 2>(u);
+  if (mt4 == 3) return sk_u<DUAL, WB, R4, 3>(u);
+  return sk_u<DUAL, WB, R4, 4>(u);
+}
+template <bool DUAL, int WB>
+const void* stream_kernel(int r4, int mt4, int u) {
+  if (r4 >= 4) return sk_mt<DUAL, WB, 4>(mt4, u);
+  if (r4 == 2) return sk_mt<DUAL, WB, 2>(mt4, u);
+  return sk_mt<DUAL, WB, 1>(mt4, u);
+}
+
+bool shape_ok(int rows, int n, int rpw, int r4, int waves, int u) {
+  const int mt4 = (rows + 3) / 4;
+  return rows >= 1 && rows <= 16 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4) && rpw <= 4 * r4 &&
+         waves >= 1 && waves <= 16 && (u == 1 || (u == 2 && mt4 <= 2));
+}
+
+int launch_stream(const void* kern, const mi355::W8Params& p, int rpw, int r4, int waves, int nq, void* stream) {
+  const int mt4 = (p.rows + 3) / 4;
+  const size_t lds = static_cast<size_t>(waves) * nq * r4 * mt4 * 16 * sizeof(float);
+  int rpw_arg = rpw;
+  void* args[] = {const_cast<mi355::W8Params*>(&p), &rpw_arg};
+  const unsigned grid = static_cast<unsigned>((p.n + rpw - 1) / rpw);
+  return hipLaunchKernel(kern, dim3(grid), dim3(64 * waves), args, lds, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? 0
+             : -3;
+}
+
+}  // namespace
+
 // out [rows, n] = W8A16(x [rows, k], q [n, k], scale [n]) (q2 / scale2 not
 // NULL: the gate/up + SiLU-and-mul kernel with q, scale the gate and q2,
 // scale2 the up weights), launched with rpw weight rows per workgroup, r4
 // 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves and u chunks in flight
-// (1 or 2).  rows <= 8, k a multiple of 16, every pointer 16-byte
-// aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.
+// (1 or 2; 1 above 8 rows).  rows <= 16, k a multiple of 16, every pointer
+// 16-byte aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
     const void* x, const void* q, const void* scale, const void* q2, const void* scale2, void* out, int rows, int k,
     int n, int rpw, int r4, int waves, int u, void* stream) {
-  if (!x || !q || !scale || !out || rows < 1 || rows > 8 || k < 16 || (k & 15) || n < 1 || rpw < 1 ||
-      (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2) ||
+  if (!x || !q || !scale || !out || k < 16 || (k & 15) || !shape_ok(rows, n, rpw, r4, waves, u) ||
       (!q2) != (!scale2))
     return -1;
   const mi355::W8Params p{x, q, scale, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, q2, scale2};
-  const mi355::StreamPlan sp{rpw, r4, waves, u};
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int st = q2 ? mi355::w8_stream_launch<mi355::F16, mi355::F16, true>(p, sp, s)
-                    : mi355::w8_stream_launch<mi355::F16, mi355::F16, false>(p, sp, s);
-  return st == MI355_OK ? 0 : -3;
+  const int mt4 = (rows + 3) / 4;
+  const void* kern = q2 ? stream_kernel<true, 1>(r4, mt4, u) : stream_kernel<false, 1>(r4, mt4, u);
+  return launch_stream(kern, p, rpw, r4, waves, q2 ? 2 : 1, stream);
 }
 
 // out [rows, n] = silu(x @ wg^T) * (x @ wu^T) for x [rows, k] and 16-bit
 // weights [n, k] (fp16), by the weight-streaming kernel of w8a16_stream.h
 // with 16-bit weights (WB = 2) at launch shape (rpw, r4, waves, u).  rows <=
-// 8, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on bad
-// arguments, -3 on a launch error.
+// 16, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on
+// bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_gate_up16_stream(
     const void* x, const void* wg, const void* wu, void* out, int rows, int k, int n, int rpw, int r4, int waves,
     int u, void* stream) {
-  if (!x || !wg || !wu || !out || rows < 1 || rows > 8 || k < 8 || (k & 7) || n < 1 || rpw < 1 ||
-      (r4 != 1 && r4 != 2 && r4 != 4) || rpw > 4 * r4 || waves < 1 || waves > 16 || (u != 1 && u != 2))
-    return -1;
+  if (!x || !wg || !wu || !out || k < 8 || (k & 7) || !shape_ok(rows, n, rpw, r4, waves, u)) return -1;
   const mi355::W8Params p{x, wg, nullptr, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, wu, nullptr};
-  const mi355::StreamPlan sp{rpw, r4, waves, u};
-  const int st = mi355::w8_stream_launch<mi355::F16, mi355::F16, true, 2>(p, sp, static_cast<hipStream_t>(stream));
-  return st == MI355_OK ? 0 : -3;
+  return launch_stream(stream_kernel<true, 2>(r4, (rows + 3) / 4, u), p, rpw, r4, waves, 2, stream);
 }

@@ -1,4 +1,4 @@
-// The W8A16 decode kernel (up to 8 rows of x): int8 weight streaming with
+// The W8A16 decode kernel (up to 16 rows of x): int8 weight streaming with
 // lane-coalesced loads, plus its launch plan.  Shared by the W8A16 linear and
 // the int8 gate/up + SiLU-and-mul launchers (w8a16.hip) and, with 16-bit
 // weights (template argument WB = 2, below), by the 16-bit gate/up +
@@ -29,8 +29,9 @@
 //   acc(x row m', weight row r') = sum_q D[4 m' + q][4 r' + q],
 // which lane 16 m' + 4 r' + q holds in its register q: each lane keeps its own
 // register l % 4 and a quad sum (two DPP adds, one fixed order) finishes it.
-// An 8-row x tile takes two A sets (MT4 = 2), so the MFMA work is twice the
-// minimum -- far below what the weight stream leaves idle.
+// An x tile of up to 16 rows takes MT4 = ceil(rows / 4) A sets, so the MFMA
+// work is up to four times the minimum -- far below what the weight stream
+// leaves idle.
 //
 // Decomposition.  A workgroup owns rpw <= 4 R4 consecutive weight rows and all
 // rows of x; its waves split the 256-byte chunks of K into contiguous ranges
@@ -269,14 +270,19 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
 //     of 4 above 8 when there is at most one workgroup per CU, so the CU's
 //     4 SIMDs carry equal loads (14 waves: 1.06x the time of 12);
 //   1 chunk in flight per wave (the CU's waves keep enough bytes in flight).
+// 9 - 16 rows of x (three or four x sets; bench.py --only stream-sweep16, 12
+// and 16 rows): at most 8 weight rows per workgroup (16 spill registers),
+// about 8 waves per CU with one workgroup per CU, else 5 (1.5B down, 16 rows
+// 8.69 us against 12.47 us for w8a16_skinny; 7B down 26.9 vs 31.0 us).
 inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
-  const bool two_sets = rows > 4;  // x rows in two 4-row sets
+  const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
+  const bool four_sets = rows > 8;  // three or four sets: at most 8 weight rows per workgroup
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
   if (n <= 2048 || (n + 7) / 8 < cus) {
     sp.rpw = (n + cus - 1) / cus;
     sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
-  } else if (two_sets && k >= 3072) {
+  } else if (two_sets && k >= 3072 && !four_sets) {
     sp.rpw = 16;
   }
   if (dual && sp.rpw < 16) sp.rpw = two_sets ? 8 : 4;
@@ -286,7 +292,7 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
   if (dual) {
     waves = two_sets && sp.rpw < 16 ? 2 : 3;
   } else {
-    const int per_cu = sp.rpw == 16 ? 7 : (two_sets ? (wgs <= cus ? 12 : 10) : 14);
+    const int per_cu = sp.rpw == 16 ? 7 : (four_sets ? (wgs <= cus ? 8 : 5) : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
   }
   if (waves > 16) waves = 16;
@@ -297,7 +303,7 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
   return sp;
 }
 
-// Launch plan of the 16-bit gate/up + SiLU-and-mul (WB = 2) for `rows` <= 8
+// Launch plan of the 16-bit gate/up + SiLU-and-mul (WB = 2) for `rows` <= 16
 // rows of x against two [n, k] weight matrices, from a graph-timed sweep of
 // rows per workgroup x waves x chunks in flight on MI355X over the
 // Qwen2.5-0.5B, 1.5B and 7B MLPs at 1, 4 and 8 rows (bench.py --only
@@ -306,20 +312,28 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
 // 12.59 us for gate_up_silu_skinny); deeper (7B), 4 rows and 8 waves with 2
 // chunks in flight up to 4 rows of x (39.84 vs 42.77 us), 16 rows and 8
 // waves with one chunk beyond, where every workgroup re-reads the long x
-// (42.07 vs 44.48 us).
+// (42.07 vs 44.48 us); 9 - 16 rows (bench.py --only stream-sweep16), 8 rows
+// per workgroup and one chunk in flight, 2 waves up to k = 2048 (1.5B, 16
+// rows 13.44 vs 15.73 us), else 8 (7B: 50.09 vs 51.02 us).
 inline StreamPlan gu16_stream_plan(int rows, int k) {
+  if (rows > 8) return k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{8, 2, 8, 1};
   if (k <= 2048) return StreamPlan{4, 1, 2, 2};
   if (rows <= 4) return StreamPlan{4, 1, 8, 2};
   return StreamPlan{16, 4, 8, 1};
 }
 
-// Launches w8a16_stream with plan `sp` (rows <= 8; k, qs multiples of 16 --
+// Launches w8a16_stream with plan `sp` (rows <= 16; k, qs multiples of 16 --
 // of 8 for 16-bit weights --, xs a multiple of 8, x and the weights 16-byte
 // aligned: the callers check these).
 template <typename T, typename TO, bool DUAL, int WB = 1>
 int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   constexpr int NQ = DUAL ? 2 : 1;
-  const int mt4 = p.rows <= 4 ? 1 : 2;
+  const int mt4 = (p.rows + 3) / 4;  // 4-row x sets: 1 .. 4
+  if (mt4 > 2 && (sp.r4 > 2 || sp.u > 1)) {
+    set_error("w8a16 stream launch: more than 8 rows of x take at most 8 weight rows per workgroup and one chunk "
+              "in flight (r4 %d, u %d)", sp.r4, sp.u);
+    return MI355_ERR_UNSUPPORTED;
+  }
   const dim3 grid(static_cast<unsigned>((p.n + sp.rpw - 1) / sp.rpw));
   const dim3 block(64 * sp.waves);
   const size_t lds = static_cast<size_t>(sp.waves) * NQ * sp.r4 * mt4 * 16 * sizeof(float);
@@ -330,7 +344,16 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   if (sp.u >= 2) MI355_W8S(R4, MT4, 2); else MI355_W8S(R4, MT4, 1)
 #define MI355_W8S_MT(R4) \
   if (mt4 == 1) { MI355_W8S_U(R4, 1); } else { MI355_W8S_U(R4, 2); }
-  if (sp.r4 >= 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
+  // three or four x sets: one chunk in flight, at most two 4-row weight
+  // sets (16-row workgroups spill registers there)
+#define MI355_W8S_MT4(R4) \
+  if (mt4 == 3) { MI355_W8S(R4, 3, 1); } else { MI355_W8S(R4, 4, 1); }
+  if (mt4 <= 2) {
+    if (sp.r4 >= 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
+  } else {
+    if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
+  }
+#undef MI355_W8S_MT4
 #undef MI355_W8S_MT
 #undef MI355_W8S_U
 #undef MI355_W8S

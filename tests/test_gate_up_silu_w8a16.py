@@ -66,6 +66,8 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
     (1, 3584, 18944, BF16), (8, 3584, 18944, BF16),
     # decode rows with a partial last 256-column chunk and a ragged last workgroup
     (3, 272, 1000, F16), (6, 1552, 520, BF16), (2, 4864, 904, F16),
+    # 9 - 16 rows: three and four x sets; the 7B MLP (on the skinny kernel)
+    (12, 1536, 8960, F16), (13, 272, 1000, BF16), (16, 1552, 520, F16), (16, 3584, 18944, BF16),
     # prefill rows: the dual tiled GEMM (and the skinny tiles of small grids)
     (33, 256, 100, BF16), (64, 1536, 1000, F16), (200, 640, 10240, F16), (300, 1552, 520, BF16),
     (1024, 1536, 2048, F16),
