@@ -199,3 +199,13 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_gate_up16_stre
   const mi355::W8Params p{x, wg, nullptr, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, wu, nullptr};
   return launch_stream(stream_kernel<true, 2>(r4, (rows + 3) / 4, u), p, rpw, r4, waves, 2, stream);
 }
+
+// The 16-bit gate/up + SiLU-and-mul's launch plan (gu16_stream_plan) for
+// `rows` x k: out4 = {rpw, r4, waves, u}.
+extern "C" __attribute__((visibility("default"))) void mi355_probe_gate_up16_stream_plan(int rows, int k, int* out4) {
+  const mi355::StreamPlan sp = mi355::gu16_stream_plan(rows, k);
+  out4[0] = sp.rpw;
+  out4[1] = sp.r4;
+  out4[2] = sp.waves;
+  out4[3] = sp.u;
+}

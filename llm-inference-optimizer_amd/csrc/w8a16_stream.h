@@ -316,10 +316,13 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
 // per workgroup and one chunk in flight, 2 waves up to k = 2048 (1.5B, 16
 // rows 13.44 vs 15.73 us), else 8 (7B: 50.09 vs 51.02 us).
 inline StreamPlan gu16_stream_plan(int rows, int k) {
-  if (rows > 8) return k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{8, 2, 8, 1};
-  if (k <= 2048) return StreamPlan{4, 1, 2, 2};
-  if (rows <= 4) return StreamPlan{4, 1, 8, 2};
-  return StreamPlan{16, 4, 8, 1};
+  StreamPlan sp{16, 4, 8, 1};
+  if (rows > 8) sp = k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{8, 2, 8, 1};
+  else if (k <= 2048) sp = StreamPlan{4, 1, 2, 2};
+  else if (rows <= 4) sp = StreamPlan{4, 1, 8, 2};
+  const int nchunk = (k + 127) / 128;  // no more waves than 128-column chunks
+  if (sp.waves > nchunk) sp.waves = nchunk;
+  return sp;
 }
 
 // Launches w8a16_stream with plan `sp` (rows <= 16; k, qs multiples of 16 --
