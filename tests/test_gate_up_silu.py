@@ -150,8 +150,9 @@ def test_misaligned_k_is_rejected(pkg, cuda):
         pkg.fused_gate_up_silu(x, w, w)
 
 
-def test_graph_replays_match_eager(pkg, cuda):
-    rows, k, n = 8, 1536, 8960
+@pytest.mark.parametrize("rows", [8, 16])
+def test_graph_replays_match_eager(pkg, cuda, rows):
+    k, n = 1536, 8960
     x, wg, wu = (t.to(cuda) for t in _inputs(rows, k, n, BF16, seed=11))
     xs = x.clone()
     s = torch.cuda.Stream()

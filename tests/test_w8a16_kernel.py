@@ -355,7 +355,7 @@ def test_out_row_stride_through_abi(pkg, cuda):
     assert torch.all(out[:, N:] == 7.0)
 
 
-@pytest.mark.parametrize("M", [8, 100])
+@pytest.mark.parametrize("M", [8, 16, 100])
 def test_graph_replays_match_eager(pkg, cuda, M):
     K, N = 1536, 8960
     lin = _linear(K, N, False, cuda, seed=15)
