@@ -11,10 +11,14 @@
 //
 // At decode shapes (rows <= 32) the work is weight streaming: each weight
 // element is read once per call (2 * n_out * k elements) and meets at most 32
-// rows of x, so the skinny kernel below is bound by HBM bandwidth on the
-// weights, not by MFMA.  More rows are a GEMM (MFMA-bound): they run the
-// LDS-tiled kernel of tiled_gemm.h with both weight matrices as B operands
-// and SiLU-and-mul in its epilogue.
+// rows of x, so the kernel is bound by HBM bandwidth on the weights, not by
+// MFMA.  Up to 16 rows the launcher runs the lane-coalesced weight-streaming
+// kernel of w8a16_stream.h with 16-bit weights; the skinny kernel below
+// serves 17 - 32 rows where the small tiled shapes do not pay, and any
+// decode call whose x would span more than a buffer descriptor reaches.
+// More rows are a GEMM (MFMA-bound): they run the LDS-tiled kernel of
+// tiled_gemm.h with both weight matrices as B operands and SiLU-and-mul in
+// its epilogue.
 //
 // Operand layout.  The v_mfma_f32_16x16x32 B operand gives lane l column
 // n = l % 16 and k-group l / 16 (8 consecutive k each).  Giving the 16

@@ -251,7 +251,7 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
   }
 }
 
-// Launch plan for `rows` <= 8 rows of x against [n, k] int8 weights (two
+// Launch plan for `rows` <= 16 rows of x against [n, k] int8 weights (two
 // matrices when dual), fitted to a graph-timed sweep of rows per workgroup x
 // waves x chunks in flight on MI355X over the Qwen2.5-0.5B, 1.5B and 7B
 // decode projections and MLPs at 1, 4 and 8 rows (bench.py --only
