@@ -75,7 +75,7 @@ def parse_args():
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
                                       "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stage3",
-                                      "e2e-compact"],
+                                      "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
     p.add_argument("--e2e-int8", action="store_true",
@@ -823,6 +823,8 @@ def main():
         if not args.skip_e2e:
             full["e2e"] = bench_e2e_compact(ctx)
             result["e2e_stage3"] = full["e2e"]
+            full["e2e_int8"] = bench_e2e_int8_compact(ctx)
+            result["e2e_stage7_int8"] = full["e2e_int8"]
         result["roofline"]["per_config"] = per_config(full)
 
     if not args.skip_cpu:
@@ -992,6 +994,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"e2e_stage3": bench_e2e_compact(ctx)}), flush=True)
+    elif args.only == "e2e-int8-compact":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"e2e_stage7_int8": bench_e2e_int8_compact(ctx)}), flush=True)
     elif args.only == "gu16-stream-sweep":
         del sets
         torch.cuda.empty_cache()
@@ -2164,31 +2170,19 @@ def bench_e2e(args):
           flush=True)
 
 
-def bench_e2e_int8(args):
-    """fp16 vs int8 weights end to end, after the reference's
-    benchmarks/run_stage7_e2e.py: one model instance is measured in fp16,
+def _int8_phases(torch, pkg, dev, S, GEN, TRIALS, batches, full):
+    """fp16 vs int8 weights end to end on one model instance, after the
+    reference's benchmarks/run_stage7_e2e.py: the model is measured in fp16,
     quantised in place with quantize_model_int8 (196 linears -> W8A16 HIP
-    kernels) and measured again, then also patched with the fused RMSNorm /
-    SiLU-and-mul kernels.  Per phase: transformer-layer weight MB; the HF
-    path (eager decode over HF's KV cache) at batch 1 and 8 -- TTFT, decode
-    tok/s, peak memory -- for prompts of 128 tokens and 64 generated; and
-    decode tok/s with the whole step replayed as one HIP graph
-    (GraphedGreedyDecoder) at batch 1 and 8.  Random-init Qwen2 with
-    Qwen2.5-1.5B's architecture, fp16, sdpa (no Hub access here)."""
-    import torch
-    from transformers import Qwen2Config, Qwen2ForCausalLM
-
-    sys.path.insert(0, str(ROOT))
-    pkg = importlib.import_module(PKG)
-    dev = torch.device("cuda:0")
-    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
-                      num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=32768,
-                      rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True, attn_implementation="sdpa")
-    torch.manual_seed(0)
-    with torch.device(dev):
-        model = Qwen2ForCausalLM(cfg)
-    model = model.half().eval()
-    S, GEN, TRIALS = 128, 64, args.trials
+    kernels) and measured again (with `full`, then also patched with the
+    fused RMSNorm / SiLU-and-mul kernels, then with the int8 gate/up +
+    SiLU-and-mul fused).  Per phase: transformer-layer weight MB; the HF path
+    (eager decode over HF's KV cache) per batch -- TTFT, decode tok/s, peak
+    memory -- for prompts of S tokens and GEN generated; and decode tok/s with
+    the whole step replayed as one HIP graph (GraphedGreedyDecoder).
+    Random-init Qwen2 with Qwen2.5-1.5B's architecture, fp16, sdpa."""
+    model = _e2e_model(torch, dev)
+    cfg = model.config
 
     def layer_weight_mb():
         total = 0
@@ -2244,7 +2238,7 @@ def bench_e2e_int8(args):
 
     def phase(label):
         r = {"layer_weight_mb": round(layer_weight_mb(), 1), "hf": {}, "graphed_decode_tok_s": {}}
-        for B in (1, 8):
+        for B in batches:
             ids = ids_for(B, 5)
             for _ in range(2):
                 hf_run(ids)
@@ -2257,27 +2251,61 @@ def bench_e2e_int8(args):
                 f"tok/s, peak {r['hf'][B]['peak_mb']:.0f} MB; graphed decode {r['graphed_decode_tok_s'][B]:.1f} tok/s")
         return r
 
-    fp16 = phase("fp16")
-    stats = pkg.quantize_model_int8(model)
-    log(f"quantized {stats}")
-    int8 = phase("int8")
-    counts = pkg.patch_model_with_fused_kernels(model, fuse_residual=True)
-    log(f"patched {counts}")
-    int8_fused = phase("int8+fused")
-    n_gu = 0
-    for m in model.modules():
-        if isinstance(m, pkg.FusedMLP) and m.gate_up_kind() == "int8":
-            m.fuse_gate_up = True
-            n_gu += 1
-    log(f"int8 gate/up + SiLU-and-mul fused in {n_gu} MLPs")
-    int8_gu = phase("int8+fused+int8_gate_up")
+    res = {"fp16": phase("fp16")}
+    res["quantize_stats"] = pkg.quantize_model_int8(model)
+    log(f"quantized {res['quantize_stats']}")
+    res["int8"] = phase("int8")
+    if full:
+        res["patched"] = pkg.patch_model_with_fused_kernels(model, fuse_residual=True)
+        log(f"patched {res['patched']}")
+        res["int8_fused_kernels"] = phase("int8+fused")
+        n_gu = 0
+        for m in model.modules():
+            if isinstance(m, pkg.FusedMLP) and m.gate_up_kind() == "int8":
+                m.fuse_gate_up = True
+                n_gu += 1
+        log(f"int8 gate/up + SiLU-and-mul fused in {n_gu} MLPs")
+        res["int8_fused_kernels_int8_gate_up"] = phase("int8+fused+int8_gate_up")
+        res["int8_gate_up_mlps"] = n_gu
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_e2e_int8(args):
+    """fp16 vs int8 weights end to end (bench.py --e2e-int8): every phase of
+    _int8_phases at batch 1 and 8, prompts of 128 tokens, 64 generated."""
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    pkg = importlib.import_module(PKG)
+    S, GEN = 128, 64
+    res = _int8_phases(torch, pkg, torch.device("cuda:0"), S, GEN, args.trials, (1, 8), True)
     print(json.dumps({"metric": "fp16 vs int8-weight (W8A16) decode tok/s, after run_stage7_e2e.py",
                       "model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16 activations, sdpa",
-                      "seq_len": S, "gen_len": GEN, "trials": TRIALS, "quantize_stats": stats,
-                      "fp16": fp16, "int8": int8, "int8_fused_kernels": int8_fused,
-                      "int8_fused_kernels_int8_gate_up": int8_gu, "int8_gate_up_mlps": n_gu, "patched": counts}),
-          flush=True)
+                      "seq_len": S, "gen_len": GEN, "trials": args.trials, **res}), flush=True)
 
+
+def bench_e2e_int8_compact(ctx, S=128, GEN=32, trials=3):
+    """The reference's Stage 7 end-to-end comparison (benchmarks/
+    run_stage7_e2e.py, results in benchmarks/results/stage7_e2e.json) in the
+    default bench run, compact: fp16 against int8 weights (W8A16 kernels) at
+    batch 1 and 8 -- layer weight MB, TTFT, eager HF decode tok/s and
+    hipGraph decode tok/s -- on one model instance."""
+    r = _int8_phases(ctx.torch, ctx.pkg, ctx.dev, S, GEN, trials, (1, 8), False)
+    out = {"model": "random-init Qwen2 (Qwen2.5-1.5B architecture), fp16 activations, sdpa", "seq_len": S,
+           "gen_len": GEN, "trials": trials, "batch": [1, 8],
+           "linears_quantized": r["quantize_stats"].get("layers_quantized")}
+    for ph in ("fp16", "int8"):
+        d = r[ph]
+        out[ph] = {"layer_weight_mb": d["layer_weight_mb"],
+                   "ttft_ms": [d["hf"][B]["ttft_ms"] for B in (1, 8)],
+                   "decode_tok_s": [d["hf"][B]["decode_tok_s"] for B in (1, 8)],
+                   "graphed_decode_tok_s": [d["graphed_decode_tok_s"][B] for B in (1, 8)],
+                   "peak_mb": [d["hf"][B]["peak_mb"] for B in (1, 8)]}
+    out["int8_over_fp16_graphed_decode"] = [round(out["int8"]["graphed_decode_tok_s"][i] /
+                                                  out["fp16"]["graphed_decode_tok_s"][i], 3) for i in range(2)]
+    return out
 
 if __name__ == "__main__":
     main()
