@@ -981,8 +981,9 @@ def run_only(ctx, args, sets):
         elif args.only == "w8a16-prefill":  # kernel only, the 1.5B gate/up and down projections at 1024 rows
             log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 1024 and s[2] in (8960, 1536)
                                                     and s[1] in (1536, 8960)][-2:], iters=iters, baselines=False)))
-        else:  # the two decode shapes profiled under profiles/, kernel only
-            log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 8 and s[2] in (8960, 18944)],
+        else:  # the 8-row gate/up and down projections of 1.5B and 7B, kernel only
+            log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 8 and s[4] in
+                                                    ("gate/up proj", "down proj", "7b gate/up proj", "7b down proj")],
                                        iters=iters, baselines=False)))
     elif args.only == "prefill-core":
         print(json.dumps(bench_prefill_core(ctx)), flush=True)
