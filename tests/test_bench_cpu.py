@@ -55,6 +55,18 @@ def test_tiled_gemm_fragments_name_every_template_argument(bench):
         assert len(frag[len("tiled_gemm<"):-1].split(",")) == arity, frag
 
 
+def test_stream_kernel_fragments_name_every_template_argument(bench):
+    # as above, for the weight-streaming decode kernel
+    src = (ROOT / "llm-inference-optimizer_amd" / "csrc" / "w8a16_stream.h").read_text()
+    decl = re.search(r"template <([^>]*)>\s*__global__[^\n]*w8a16_stream\(", src)
+    assert decl, "w8a16_stream kernel declaration not found"
+    arity = len(decl.group(1).split(","))
+    frags = [frag for frag, _ in bench.KNOWN_LAUNCHES if frag.startswith("w8a16_stream<")]
+    assert frags
+    for frag in frags:
+        assert len(frag[len("w8a16_stream<"):-1].split(",")) == arity, frag
+
+
 def _write(path, rows):
     with open(path, "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=list(rows[0]))
@@ -118,6 +130,8 @@ def test_per_config_block_carries_every_config_and_decode_latency(bench):
     # fractions, same-size probe times, and the C3 decode latencies per M
     k = {"c1_rmsnorm_f16_2048x1536": _kernel(bench, 12_585_984, 4.0),
          "c1_rmsnorm_f16_2048x1536_graph": _kernel(bench, 12_585_984, 3.5),
+         "c1_rmsnorm_f16_2048x1536_api": _kernel(bench, 12_585_984, 3.7),
+         "empty_kernel_eager_us": 1.5,
          "c2_silu_mul_f16_2048x8960": _kernel(bench, 110_100_480, 18.0)}
     c4 = {"c4_rmsnorm_bf16_16384x3584": _kernel(bench, 234_888_192, 39.5),
           "c4_silu_mul_bf16_16384x18944": _kernel(bench, 1_862_270_976, 286.0)}
@@ -130,6 +144,8 @@ def test_per_config_block_carries_every_config_and_decode_latency(bench):
                            "copy_ceiling": {"frac_of_peak": 0.82}})
     assert pc["C1_rmsnorm_f16_2048x1536"]["frac"] == round(12_585_984 / 4.0 / 1e3 / 8000, 4)
     assert pc["C1_rmsnorm_f16_2048x1536"]["graph_us"] == 3.5
+    assert pc["C1_rmsnorm_f16_2048x1536"]["api_us"] == 3.7
+    assert pc["C1_rmsnorm_f16_2048x1536"]["empty_kernel_eager_us"] == 1.5
     assert pc["C4_silu_mul_bf16_16384x18944"]["frac"] == round(1_862_270_976 / 286.0 / 1e3 / 8000, 4)
     assert set(pc["C3_decode_f16_latency"]) == {"M1", "M2", "M4", "M8", "M32"}
     assert pc["C3_decode_f16_latency"]["M8"]["graph_node_us"] == 1.78
