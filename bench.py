@@ -760,6 +760,7 @@ def main():
     silu_us = time_loop(ctx, [s[1] for s in sets], iters)
     rms_us = time_loop(ctx, [s[0] for s in sets], iters)
     rms_graph_us = time_graph(ctx, [s[0] for s in sets], 200)
+    silu_graph_us = time_graph(ctx, [s[1] for s in sets], 200)
     # the same launches through the product API (fused_rmsnorm: the C++
     # launcher extension, which also allocates the output) and an empty
     # kernel through the C ABI, eager back to back: the host's share of C1
@@ -775,6 +776,8 @@ def main():
                                                  {"timing": "events over back-to-back launches, cold"}),
         "c1_rmsnorm_f16_2048x1536_graph": kernel_entry("rmsnorm_wave_rows", rms_bytes,
                                                        rms_graph_us, {"timing": "hipGraph of 200 launches, cold"}),
+        "c2_silu_mul_f16_2048x8960_graph": kernel_entry("silu_mul_chunks", silu_bytes,
+                                                        silu_graph_us, {"timing": "hipGraph of 200 launches, cold"}),
         "c1_rmsnorm_f16_2048x1536_api": kernel_entry("rmsnorm_wave_rows", rms_bytes, rms_api_us,
                                                      {"timing": "fused_rmsnorm (product API), events over "
                                                                 "back-to-back calls, cold"}),
@@ -871,7 +874,8 @@ def per_config(full):
         "C1_rmsnorm_f16_2048x1536": entry(k["c1_rmsnorm_f16_2048x1536"], 2048, "C1 RMSNorm [2048,1536] fp16",
                                           k["c1_rmsnorm_f16_2048x1536_graph"]),
         "C2_silu_mul_f16_2048x8960": entry(k["c2_silu_mul_f16_2048x8960"], 2048,
-                                           "C2 SiLU-and-mul [2048,8960] fp16"),
+                                           "C2 SiLU-and-mul [2048,8960] fp16",
+                                           k.get("c2_silu_mul_f16_2048x8960_graph")),
         "C4_rmsnorm_bf16_16384x3584": entry(c4["c4_rmsnorm_bf16_16384x3584"], 16384,
                                             "C4 RMSNorm [16384,3584] bf16"),
         "C4_silu_mul_bf16_16384x18944": entry(c4["c4_silu_mul_bf16_16384x18944"], 16384,
