@@ -305,3 +305,39 @@ def test_torch_launchers_keep_the_reference_messages(pkg):
         pkg.fused_silu_mul(x, torch.randn(4, 65, dtype=torch.float16))
     with pytest.raises(AssertionError, match="out_dtype must be torch.float16 or float32"):
         pkg.linear16(x, x, out_dtype=torch.float64)
+
+
+def test_header_is_plain_c_and_links(tmp_path):
+    """A C99 caller (the INTEGRATION guide's route for a compiled host):
+    include/mi355_fused.h compiles as strict C, every entry point's
+    prototype type-checks, and a program linked against the library reads
+    the ABI version and gets the argument-check status back -- no GPU call."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    so = PKG_DIR / "libmi355_fused.so"
+    if gcc is None or not so.exists():
+        pytest.skip("gcc or the built library missing")
+    src = tmp_path / "caller.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include "mi355_fused.h"
+int main(void) {
+  if (mi355_abi_version() != MI355_ABI_VERSION) return 2;
+  /* n = 0 is rejected before any HIP call */
+  int st = mi355_rmsnorm_fwd((const void*)0, (const void*)0, (void*)0, 1, 0, 0, 0, 1e-6f,
+                             MI355_F16, MI355_F16, MI355_F16, (void*)0);
+  if (st != MI355_ERR_INVALID) return 3;
+  printf("%s\n", mi355_last_error());
+  return 0;
+}
+''')
+    exe = tmp_path / "caller"
+    cmd = [gcc, "-std=c99", "-Wall", "-Werror", "-pedantic", f"-I{ROOT / 'include'}", str(src), str(so),
+           f"-Wl,-rpath,{PKG_DIR}", "-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stdout + res.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, (run.returncode, run.stdout, run.stderr)
+    assert "mi355_rmsnorm_fwd" in run.stdout
