@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1007,6 +1007,11 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"gate_up16_stream_sweep": gu16_stream_sweep(ctx)}), flush=True)
+    elif args.only == "stream-sweep16-wide":  # 12 / 16 rows with 16-row workgroups too
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP16_WIDE_SHAPES, True)}),
+              flush=True)
     elif args.only == "stream-sweep16":  # 9 - 16 rows: both decode sweeps
         del sets
         torch.cuda.empty_cache()
@@ -1256,14 +1261,14 @@ def w8_layout_sweep(ctx):
     return out
 
 
-def _w8_stream_shapes(nchunk, dual, mt4):
+def _w8_stream_shapes(nchunk, dual, mt4, wide16=False):
     """Launch shapes (rpw, r4, waves, u) of the W8A16 decode kernel sampled by
     w8_stream_sweep: rows per workgroup 4-16, 1-16 waves, 1 or 2 chunks in
     flight, without the register-spilling combinations."""
     out = []
     for rpw in (4, 6, 8, 12, 16):
         r4 = 1 if rpw <= 4 else (2 if rpw <= 8 else 4)
-        if mt4 > 2 and r4 == 4:  # 12 or 16 rows of x: 16-row workgroups spill registers
+        if mt4 > 2 and r4 == 4 and (dual or not wide16):  # 12 or 16 rows of x: 16-row workgroups spill
             continue
         for waves in (1, 2, 3, 4, 6, 8, 12, 16):
             if waves > nchunk:
@@ -1294,6 +1299,11 @@ W8_STREAM_SWEEP_SHAPES = [
 
 # 9 - 16 rows of x (four 4-row x sets at most): the Qwen2.5-0.5B, 1.5B and 7B
 # projections and MLPs at 12 and 16 rows
+# the wide, deep 7B gate/up projection at 12 and 16 rows, with 12- and
+# 16-row workgroups too (the single kernel: a few registers spill at 16 rows)
+W8_STREAM_SWEEP16_WIDE_SHAPES = [("gateup7b_M9", 9, 3584, 18944, False), ("gateup7b_M12", 12, 3584, 18944, False),
+                                 ("gateup7b_M16", 16, 3584, 18944, False), ("down7b_M12", 12, 18944, 3584, False),
+                                 ("gateup_M16", 16, 1536, 8960, False)]
 W8_STREAM_SWEEP16_SHAPES = [
     ("down_M12", 12, 8960, 1536, False), ("down_M16", 16, 8960, 1536, False),
     ("gateup_M12", 12, 1536, 8960, False), ("gateup_M16", 16, 1536, 8960, False),
@@ -1303,7 +1313,7 @@ W8_STREAM_SWEEP16_SHAPES = [
 ]
 
 
-def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES):
+def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
     """The W8A16 decode kernel (w8a16_stream) over launch shapes, through the
     probe library's forced-shape entry point, at the Qwen2.5-1.5B down and
     gate/up projections and the int8 gate/up + SiLU-and-mul MLP, 1 and 8 rows
@@ -1337,7 +1347,7 @@ def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES):
         tol = 2e-3 * ref.float().abs().max().item()
         bad = []
         nchunk = -(-K // 256)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, -(-M // 4)):
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, -(-M // 4), wide16):
             def mk(q, sc):
                 if dual:
                     return ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u, q[1], sc[1])
@@ -1808,12 +1818,14 @@ def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
     return res
 
 
-def w8a16_kernel_name(M, N):
+def w8a16_kernel_name(M, N, K=0):
     """The kernel mi355_w8a16_linear_fwd runs for this shape (aligned inputs,
-    tiles that fit): the weight-streaming kernel up to 8 rows, the skinny
-    split-K kernel up to 32 rows (or the small tiled shapes where they pay)
-    and for small grids, the tiled MFMA GEMM otherwise."""
-    if M <= 8:
+    tiles that fit): the weight-streaming kernel up to 8 rows, and up to 16
+    but for wide, deep outputs (n > 10000, k > 2048) at 13-16 rows (9-16 for
+    k < 3072), the skinny split-K kernel up to 32 rows (or the small tiled
+    shapes where they pay) and for small grids, the tiled MFMA GEMM
+    otherwise."""
+    if M <= 8 or (M <= 16 and not (N > 10000 and K > 2048)) or (M <= 12 and K >= 3072):
         return "w8a16_stream"
     bn = 128 if (M <= 32 and N > 10000) else 64
     if 16 < M <= 64 and -(-N // bn) >= 128:
@@ -1850,7 +1862,7 @@ def bench_w8a16(ctx, shapes=W8A16_SHAPES, iters=300, baselines=True):
         spin_up(ctx, calls)
         us = time_loop(ctx, calls, iters)
         us_graph = time_graph(ctx, calls, max(2 * sets, 64) if sets <= 256 else sets)
-        kname = w8a16_kernel_name(M, N)
+        kname = w8a16_kernel_name(M, N, K)
         entry = kernel_entry(kname, nbytes, min(us, us_graph),
                              {"layer": label, "M": M, "K": K, "N": N, "dtype": dname, "weight_sets": sets,
                               "eager_us": round(us, 3), "graph_us": round(us_graph, 3),

@@ -273,16 +273,21 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
 // 9 - 16 rows of x (three or four x sets; bench.py --only stream-sweep16, 12
 // and 16 rows): at most 8 weight rows per workgroup (16 spill registers),
 // about 8 waves per CU with one workgroup per CU, else 5 (1.5B down, 16 rows
-// 8.69 us against 12.47 us for w8a16_skinny; 7B down 26.9 vs 31.0 us).
+// 8.69 us against 12.47 us for w8a16_skinny; 7B down 26.9 vs 31.0 us);
+// except 9 - 12 rows of x against one matrix with k >= 3072, where the
+// 16-row workgroup fits its registers (bench.py --only stream-sweep16-wide):
+// 16 rows as with 5 - 8 rows of x (7B gate/up, 12 rows 18.2 us against
+// 21.2 us for w8a16_skinny; 7B down 18.8 vs 22.7 us for 8-row workgroups).
 inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
   const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
-  const bool four_sets = rows > 8;  // three or four sets: at most 8 weight rows per workgroup
+  const bool four_sets = rows > 8;  // three or four sets: at most 8 weight rows per workgroup ...
+  const bool wide3 = four_sets && rows <= 12 && !dual;  // ... but 16 with three sets and one matrix
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
   if (n <= 2048 || (n + 7) / 8 < cus) {
     sp.rpw = (n + cus - 1) / cus;
     sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
-  } else if (two_sets && k >= 3072 && !four_sets) {
+  } else if (two_sets && k >= 3072 && (!four_sets || wide3)) {
     sp.rpw = 16;
   }
   if (dual && sp.rpw < 16) sp.rpw = two_sets ? 8 : 4;
@@ -331,10 +336,12 @@ inline StreamPlan gu16_stream_plan(int rows, int k) {
 template <typename T, typename TO, bool DUAL, int WB = 1>
 int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   constexpr int NQ = DUAL ? 2 : 1;
+  constexpr bool kWide3 = !DUAL && WB == 1;  // 16 weight rows x three x sets fit the registers
   const int mt4 = (p.rows + 3) / 4;  // 4-row x sets: 1 .. 4
-  if (mt4 > 2 && (sp.r4 > 2 || sp.u > 1)) {
-    set_error("w8a16 stream launch: more than 8 rows of x take at most 8 weight rows per workgroup and one chunk "
-              "in flight (r4 %d, u %d)", sp.r4, sp.u);
+  const bool wide3 = kWide3 && mt4 == 3 && sp.r4 == 4 && sp.u == 1;
+  if (mt4 > 2 && !wide3 && (sp.r4 > 2 || sp.u > 1)) {
+    set_error("w8a16 stream launch: more than 8 rows of x take at most 8 weight rows per workgroup (16 for 9 - 12 "
+              "rows against one int8 matrix) and one chunk in flight (r4 %d, u %d)", sp.r4, sp.u);
     return MI355_ERR_UNSUPPORTED;
   }
   const dim3 grid(static_cast<unsigned>((p.n + sp.rpw - 1) / sp.rpw));
@@ -348,11 +355,14 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
 #define MI355_W8S_MT(R4) \
   if (mt4 == 1) { MI355_W8S_U(R4, 1); } else { MI355_W8S_U(R4, 2); }
   // three or four x sets: one chunk in flight, at most two 4-row weight
-  // sets (16-row workgroups spill registers there)
+  // sets (16-row workgroups spill registers there), but for three x sets
+  // against one int8 matrix
 #define MI355_W8S_MT4(R4) \
   if (mt4 == 3) { MI355_W8S(R4, 3, 1); } else { MI355_W8S(R4, 4, 1); }
   if (mt4 <= 2) {
     if (sp.r4 >= 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
+  } else if (wide3) {
+    if constexpr (kWide3) MI355_W8S(4, 3, 1);
   } else {
     if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
   }

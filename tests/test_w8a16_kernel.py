@@ -139,10 +139,13 @@ STREAM_CASES = [(m, K, N, F16 if (m + K) % 2 else BF16, m % 3 == 0)
                 for m in range(1, 9)
                 for K, N in ((8960, 1536), (1536, 8960), (272, 1000), (4864, 896), (1552, 37))]
 # 9 - 16 rows: three or four 4-row x sets, and the wide, deep outputs the
-# launcher keeps on the skinny kernel (n > 10000, k > 2048)
+# launcher keeps on the skinny kernel at 13 - 16 rows (n > 10000, k > 2048)
+# and gives 16-row workgroups at 9 - 12 (k >= 3072), as it does k >= 3072
+# with n > 2048 (here a partial last chunk and a ragged last workgroup)
 STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 0)
                  for m in (9, 12, 13, 16)
                  for K, N in ((8960, 1536), (1536, 8960), (272, 1000), (1552, 37), (3584, 10008))]
+STREAM_CASES += [(m, 3104, 2900, F16 if m % 2 else BF16, m % 2 == 1) for m in (9, 10, 11, 12)]
 
 
 @pytest.mark.parametrize("M,K,N,dt,bias", STREAM_CASES)
