@@ -512,7 +512,7 @@ KNOWN_LAUNCHES = {
     ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 1, true, 1>", 1120 * 64 * 2): (
         "int8 gate/up + SiLU-and-mul 1.5B, 8 rows, 2 x [8960,1536] int8, fp16",
         2 * 8960 * 1536 + 8 * 8960 + 8 * 1536 * 2 + 8 * 8960 * 2),
-    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, true, 1>", 1184 * 64 * 3): (
+    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, true, 1>", 1184 * 64 * 1): (
         "int8 gate/up + SiLU-and-mul 7B, 8 rows, 2 x [18944,3584] int8, bf16",
         2 * 18944 * 3584 + 8 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
     ("linear16_skinny<mi355::F16, mi355::F16, 1, 1, 2>", 192 * 512): (
@@ -1010,7 +1010,8 @@ def run_only(ctx, args, sets):
     elif args.only == "stream-sweep16-wide":  # 12 / 16 rows with 16-row workgroups too
         del sets
         torch.cuda.empty_cache()
-        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP16_WIDE_SHAPES, True)}),
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP16_WIDE_SHAPES, True),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP16_WIDE_SHAPES, True)}),
               flush=True)
     elif args.only == "stream-sweep16":  # 9 - 16 rows: both decode sweeps
         del sets
@@ -1261,14 +1262,24 @@ def w8_layout_sweep(ctx):
     return out
 
 
-def _w8_stream_shapes(nchunk, dual, mt4, wide16=False):
+def stream_max_waves(r4, mt4, u, dual, wb=1):
+    """Most waves per workgroup of the decode stream kernel's instantiation
+    (stream_max_threads of csrc/w8a16_stream.h / 64): 16, or 8 where its
+    accumulators and loads in flight need 112 VGPRs or more."""
+    nq = 2 if dual else 1
+    est = 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (8 if wb == 1 else 4) * mt4)
+    return 8 if est >= 112 else 16
+
+
+def _w8_stream_shapes(nchunk, dual, mt4, wide16=False, wb=1):
     """Launch shapes (rpw, r4, waves, u) of the W8A16 decode kernel sampled by
-    w8_stream_sweep: rows per workgroup 4-16, 1-16 waves, 1 or 2 chunks in
-    flight, without the register-spilling combinations."""
+    w8_stream_sweep: rows per workgroup 4-16, 1-16 waves (at most
+    stream_max_waves), 1 or 2 chunks in flight; 16-row workgroups with more
+    than 8 rows of x only when `wide16`."""
     out = []
     for rpw in (4, 6, 8, 12, 16):
         r4 = 1 if rpw <= 4 else (2 if rpw <= 8 else 4)
-        if mt4 > 2 and r4 == 4 and (dual or not wide16):  # 12 or 16 rows of x: 16-row workgroups spill
+        if mt4 > 2 and r4 == 4 and not wide16:
             continue
         for waves in (1, 2, 3, 4, 6, 8, 12, 16):
             if waves > nchunk:
@@ -1277,7 +1288,7 @@ def _w8_stream_shapes(nchunk, dual, mt4, wide16=False):
             for u in (1, 2):
                 if u > 1 and (u > per_wave or mt4 > 2):
                     continue
-                if dual and r4 == 4 and u >= 2:  # spills registers
+                if waves > stream_max_waves(r4, mt4, u, dual, wb):
                     continue
                 out.append((rpw, r4, waves, u))
     return out
@@ -1303,7 +1314,11 @@ W8_STREAM_SWEEP_SHAPES = [
 # 16-row workgroups too (the single kernel: a few registers spill at 16 rows)
 W8_STREAM_SWEEP16_WIDE_SHAPES = [("gateup7b_M9", 9, 3584, 18944, False), ("gateup7b_M12", 12, 3584, 18944, False),
                                  ("gateup7b_M16", 16, 3584, 18944, False), ("down7b_M12", 12, 18944, 3584, False),
-                                 ("gateup_M16", 16, 1536, 8960, False)]
+                                 ("down7b_M16", 16, 18944, 3584, False), ("down_M16", 16, 8960, 1536, False),
+                                 ("dual7b_M8", 8, 3584, 18944, True), ("dual7b_M12", 12, 3584, 18944, True),
+                                 ("dual7b_M16", 16, 3584, 18944, True), ("dual_gateup_M16", 16, 1536, 8960, True)]
+GU16_SWEEP16_WIDE_SHAPES = [("gu7b_M12", 12, 3584, 18944), ("gu7b_M16", 16, 3584, 18944),
+                            ("gu1.5b_M16", 16, 1536, 8960)]
 W8_STREAM_SWEEP16_SHAPES = [
     ("down_M12", 12, 8960, 1536, False), ("down_M16", 16, 8960, 1536, False),
     ("gateup_M12", 12, 1536, 8960, False), ("gateup_M16", 16, 1536, 8960, False),
@@ -1386,7 +1401,7 @@ GU16_SWEEP16_SHAPES = [("gu1.5b_M12", 12, 1536, 8960), ("gu1.5b_M16", 16, 1536, 
                        ("gu0.5b_M16", 16, 896, 4864), ("gu7b_M16", 16, 3584, 18944)]
 
 
-def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES):
+def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False):
     """The 16-bit gate/up + SiLU-and-mul at decode rows: the library's
     launch (mi355_gate_up_silu_fwd) against the weight-streaming kernel of
     w8a16_stream.h with 16-bit weights over launch shapes (rows per
@@ -1411,7 +1426,7 @@ def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES):
         tol = 2e-3 * ref.float().abs().max().item()
         res, bad = {}, []
         nchunk = -(-K // 128)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, -(-M // 4)):
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, -(-M // 4), wide16, wb=2):
             calls = [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u) for wg, wu in ws]
             calls[0]()
             torch.cuda.synchronize()

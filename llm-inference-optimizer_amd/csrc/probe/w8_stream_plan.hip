@@ -150,10 +150,11 @@ const void* stream_kernel(int r4, int mt4, int u) {
   return sk_mt<DUAL, WB, 1>(mt4, u);
 }
 
-bool shape_ok(int rows, int n, int rpw, int r4, int waves, int u) {
+bool shape_ok(int rows, int n, int rpw, int r4, int waves, int u, bool dual, int wb) {
   const int mt4 = (rows + 3) / 4;
   return rows >= 1 && rows <= 16 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4) && rpw <= 4 * r4 &&
-         waves >= 1 && waves <= 16 && (u == 1 || (u == 2 && mt4 <= 2));
+         waves >= 1 && 64 * waves <= mi355::stream_max_threads(r4, mt4, u, dual, wb) &&
+         (u == 1 || (u == 2 && mt4 <= 2));
 }
 
 int launch_stream(const void* kern, const mi355::W8Params& p, int rpw, int r4, int waves, int nq, void* stream) {
@@ -172,13 +173,14 @@ int launch_stream(const void* kern, const mi355::W8Params& p, int rpw, int r4, i
 // out [rows, n] = W8A16(x [rows, k], q [n, k], scale [n]) (q2 / scale2 not
 // NULL: the gate/up + SiLU-and-mul kernel with q, scale the gate and q2,
 // scale2 the up weights), launched with rpw weight rows per workgroup, r4
-// 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves and u chunks in flight
-// (1 or 2; 1 above 8 rows).  rows <= 16, k a multiple of 16, every pointer
+// 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves (at most
+// stream_max_threads / 64: 16 or 8) and u chunks in flight (1 or 2; 1 above
+// 8 rows).  rows <= 16, k a multiple of 16, every pointer
 // 16-byte aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
     const void* x, const void* q, const void* scale, const void* q2, const void* scale2, void* out, int rows, int k,
     int n, int rpw, int r4, int waves, int u, void* stream) {
-  if (!x || !q || !scale || !out || k < 16 || (k & 15) || !shape_ok(rows, n, rpw, r4, waves, u) ||
+  if (!x || !q || !scale || !out || k < 16 || (k & 15) || !shape_ok(rows, n, rpw, r4, waves, u, q2 != nullptr, 1) ||
       (!q2) != (!scale2))
     return -1;
   const mi355::W8Params p{x, q, scale, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, q2, scale2};
@@ -195,9 +197,15 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
 extern "C" __attribute__((visibility("default"))) int mi355_probe_gate_up16_stream(
     const void* x, const void* wg, const void* wu, void* out, int rows, int k, int n, int rpw, int r4, int waves,
     int u, void* stream) {
-  if (!x || !wg || !wu || !out || k < 8 || (k & 7) || !shape_ok(rows, n, rpw, r4, waves, u)) return -1;
+  if (!x || !wg || !wu || !out || k < 8 || (k & 7) || !shape_ok(rows, n, rpw, r4, waves, u, true, 2)) return -1;
   const mi355::W8Params p{x, wg, nullptr, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, wu, nullptr};
   return launch_stream(stream_kernel<true, 2>(r4, (rows + 3) / 4, u), p, rpw, r4, waves, 2, stream);
+}
+
+// Most threads per workgroup of w8a16_stream<.., r4, mt4, u, dual, wb>.
+extern "C" __attribute__((visibility("default"))) int mi355_probe_stream_max_threads(int r4, int mt4, int u,
+                                                                                      int dual, int wb) {
+  return mi355::stream_max_threads(r4, mt4, u, dual != 0, wb);
 }
 
 // The 16-bit gate/up + SiLU-and-mul's launch plan (gu16_stream_plan) for

@@ -15,9 +15,8 @@
 //   w8a16_stream   rows <= 16 (decode; w8a16_stream.h): weight streaming with
 //                  lane-coalesced loads, every weight byte read once per call
 //                  at HBM bandwidth, MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
-//   w8a16_skinny   17 - 32 rows (and 13 - 16 of the wide, deep 7B gate/up
-//                  projections, 9 - 16 of their dual form), and a few 32-row
-//                  tiles where the tiled grid
+//   w8a16_skinny   17 - 32 rows (and 9 - 16 of wide outputs with 2048 < k <
+//                  3072), and a few 32-row tiles where the tiled grid
 //                  would be small: weight streaming with up to 32 rows of x
 //                  per workgroup (MFMA, the same instruction).
 //   tiled_gemm     more rows (prefill): the LDS-tiled MFMA GEMM of
@@ -534,17 +533,15 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
     const int64_t waves = static_cast<int64_t>(p.n) * ((p.rows + kGenRows - 1) / kGenRows);
     return launch_w8(w8a16_generic<T, TO, DUAL>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, p, s);
   }
-  // Up to 8 rows, and up to 16 except for wide, deep outputs (the 7B gate/up
-  // projections at 16 rows: 22.7 us for w8a16_skinny against 22.5 for the
-  // best stream shape, whose 16-row workgroups spill registers there; at 9 -
-  // 12 rows against one matrix they do not, and win: 21.2 -> 18.2 us at 12
-  // rows; everywhere else in the sweep the stream kernel wins, 1.5B down
+  // Up to 16 rows, but 9 - 16 rows of wide outputs with 2048 < k < 3072
+  // (w8a16_skinny there; at k >= 3072 the stream kernel's 16-row workgroups
+  // win, the 7B gate/up at 16 rows 22.9 -> 20.6 us, its dual form 36.2 ->
+  // 33.4 us; everywhere else in the sweep the stream kernel wins, 1.5B down
   // 12.5 -> 8.7 us, gate/up 8.9 -> 7.5 us at 16 rows).
   // (The stream kernel's x descriptor spans all rows of x: under 2^32 bytes.)
   const bool x_fits = ((p.rows - 1) * p.xs + p.k) * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 32);
-  const bool wide_deep = p.n > 10000 && p.k > 2048;
-  const bool stream16 = !DUAL && p.rows <= 12 && p.k >= 3072;
-  if (x_fits && (p.rows <= 8 || (p.rows <= 16 && (!wide_deep || stream16))))
+  const bool wide_mid = p.n > 10000 && p.k > 2048 && p.k < 3072;
+  if (x_fits && (p.rows <= 8 || (p.rows <= 16 && !wide_mid)))
     return w8_stream_launch<T, TO, DUAL>(p, w8_stream_plan(p.rows, p.k, p.n, DUAL, cus), s);
   if (p.rows <= 16) return w8_skinny_shape<T, TO, 2, DUAL>(p, s, cus);
   if (small_tiles_pay(p.rows, p.n) && tiled_fits(p, DUAL)) return w8_tiled_small<T, TO, DUAL>(p, s);

@@ -100,8 +100,21 @@ struct StreamPlan {
 // lane's 16-byte weight load is then 8 k, one B operand as loaded, a chunk
 // of a weight row's 256 bytes is 128 k, and one 16-byte x load per 4-row x
 // set matches it.
+// Most threads per workgroup of w8a16_stream<R4, MT4, U, DUAL, WB>: 1024 (16
+// waves, 128 VGPRs per lane) while its accumulators and the registers its
+// loads keep in flight come to less than 112 VGPRs (4 per 16x16 accumulator
+// tile, NQ * R4 * MT4 of them; per chunk in flight 4 per weight set and 8
+// -- 4 with 16-bit weights -- per x set), else 512 (8 waves, 256 VGPRs):
+// the shapes at or above that estimate spilled 16 - 432 B per lane under the
+// 128-register budget (hipcc -Rpass-analysis=kernel-resource-usage).
+constexpr int stream_max_threads(int r4, int mt4, int u, bool dual, int wb) {
+  const int nq = dual ? 2 : 1;
+  return 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (wb == 1 ? 8 : 4) * mt4) >= 112 ? 512 : 1024;
+}
+
 template <typename T, typename TO, int R4, int MT4, int U, bool DUAL, int WB = 1>
-__global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int rpw) {
+__global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a16_stream(const W8Params p,
+                                                                                          const int rpw) {
   using TB = typename T::bits;
   constexpr int NQ = DUAL ? 2 : 1;
   constexpr bool W16 = WB == 2;
@@ -264,45 +277,48 @@ __global__ __launch_bounds__(1024) void w8a16_stream(const W8Params p, const int
 //     workgroup re-reads a long x (half the x re-reads of 8); the dual
 //     kernel 4 with up to 4 rows of x, else 8 (or 16 as above);
 //   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
-//     8-row workgroups); else about 14 per CU with up to 4 rows of x, 12 (one
-//     workgroup per CU) or 10 with more, 7 for 16-row workgroups; at least 2
-//     and at most 16 waves, no more than 256-column chunks, and a multiple
-//     of 4 above 8 when there is at most one workgroup per CU, so the CU's
-//     4 SIMDs carry equal loads (14 waves: 1.06x the time of 12);
+//     8-row workgroups, 1 with 16-row workgroups); else about 14 per CU with
+//     up to 4 rows of x, 12 (one workgroup per CU) or 10 with more, 7 for
+//     16-row workgroups (6 with more than 8 rows of x); at least 2 (but for
+//     the dual kernel's 1) and at most 16 waves (8 where stream_max_threads
+//     gives 512 threads), no more than 256-column chunks, and a multiple of
+//     4 above 8 when there is at most one workgroup per CU, so the CU's 4
+//     SIMDs carry equal loads (14 waves: 1.06x the time of 12);
 //   1 chunk in flight per wave (the CU's waves keep enough bytes in flight).
-// 9 - 16 rows of x (three or four x sets; bench.py --only stream-sweep16, 12
-// and 16 rows): at most 8 weight rows per workgroup (16 spill registers),
+// 9 - 16 rows of x (three or four x sets; bench.py --only stream-sweep16 and
+// stream-sweep16-wide, 9, 12 and 16 rows): 8 weight rows per workgroup,
 // about 8 waves per CU with one workgroup per CU, else 5 (1.5B down, 16 rows
-// 8.69 us against 12.47 us for w8a16_skinny; 7B down 26.9 vs 31.0 us);
-// except 9 - 12 rows of x against one matrix with k >= 3072, where the
-// 16-row workgroup fits its registers (bench.py --only stream-sweep16-wide):
-// 16 rows as with 5 - 8 rows of x (7B gate/up, 12 rows 18.2 us against
-// 21.2 us for w8a16_skinny; 7B down 18.8 vs 22.7 us for 8-row workgroups).
+// 8.69 us against 12.47 us for w8a16_skinny), 16 rows at k >= 3072 as above
+// (7B down, 16 rows 20.5 - 21.7 us against 27.0 for 8-row workgroups; 7B
+// gate/up 20.6 vs 22.9 us for w8a16_skinny, its dual form 33.4 vs 36.2).
 inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
   const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
-  const bool four_sets = rows > 8;  // three or four sets: at most 8 weight rows per workgroup ...
-  const bool wide3 = four_sets && rows <= 12 && !dual;  // ... but 16 with three sets and one matrix
+  const bool four_sets = rows > 8;  // three or four sets
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
   if (n <= 2048 || (n + 7) / 8 < cus) {
     sp.rpw = (n + cus - 1) / cus;
     sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
-  } else if (two_sets && k >= 3072 && (!four_sets || wide3)) {
+  } else if (two_sets && k >= 3072) {
     sp.rpw = 16;
   }
   if (dual && sp.rpw < 16) sp.rpw = two_sets ? 8 : 4;
   sp.r4 = sp.rpw <= 4 ? 1 : (sp.rpw <= 8 ? 2 : 4);
   const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
   int64_t waves;
+  int min_waves = 2;
   if (dual) {
-    waves = two_sets && sp.rpw < 16 ? 2 : 3;
+    waves = sp.rpw == 16 ? 1 : (two_sets ? 2 : 3);
+    min_waves = sp.rpw == 16 ? 1 : 2;
   } else {
-    const int per_cu = sp.rpw == 16 ? 7 : (four_sets ? (wgs <= cus ? 8 : 5) : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
+    const int per_cu = sp.rpw == 16 ? (four_sets ? 6 : 7)
+                                    : (four_sets ? (wgs <= cus ? 8 : 5) : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
   }
-  if (waves > 16) waves = 16;
+  const int max_waves = stream_max_threads(sp.r4, (rows + 3) / 4, sp.u, dual, 1) / 64;
+  if (waves > max_waves) waves = max_waves;
   if (waves > nchunk) waves = nchunk;
-  if (waves < 2) waves = nchunk < 2 ? nchunk : 2;
+  if (waves < min_waves) waves = nchunk < min_waves ? nchunk : min_waves;
   if (wgs <= cus && waves > 8) waves = waves / 4 * 4;
   sp.waves = static_cast<int>(waves);
   return sp;
@@ -317,16 +333,19 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
 // 12.59 us for gate_up_silu_skinny); deeper (7B), 4 rows and 8 waves with 2
 // chunks in flight up to 4 rows of x (39.84 vs 42.77 us), 16 rows and 8
 // waves with one chunk beyond, where every workgroup re-reads the long x
-// (42.07 vs 44.48 us); 9 - 16 rows (bench.py --only stream-sweep16), 8 rows
-// per workgroup and one chunk in flight, 2 waves up to k = 2048 (1.5B, 16
-// rows 13.44 vs 15.73 us), else 8 (7B: 50.09 vs 51.02 us).
+// (42.07 vs 44.48 us); 9 - 16 rows (bench.py --only stream-sweep16 and
+// stream-sweep16-wide), one chunk in flight, up to k = 2048 8 rows per
+// workgroup and 2 waves (1.5B, 16 rows 13.44 vs 15.73 us), deeper 16 rows
+// and one wave (7B, 16 rows 46.1 vs 50.3 us for 8 rows and 8 waves).
 inline StreamPlan gu16_stream_plan(int rows, int k) {
   StreamPlan sp{16, 4, 8, 1};
-  if (rows > 8) sp = k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{8, 2, 8, 1};
+  if (rows > 8) sp = k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{16, 4, 1, 1};
   else if (k <= 2048) sp = StreamPlan{4, 1, 2, 2};
   else if (rows <= 4) sp = StreamPlan{4, 1, 8, 2};
   const int nchunk = (k + 127) / 128;  // no more waves than 128-column chunks
   if (sp.waves > nchunk) sp.waves = nchunk;
+  const int max_waves = stream_max_threads(sp.r4, (rows + 3) / 4, sp.u, true, 2) / 64;
+  if (sp.waves > max_waves) sp.waves = max_waves;
   return sp;
 }
 
@@ -336,12 +355,14 @@ inline StreamPlan gu16_stream_plan(int rows, int k) {
 template <typename T, typename TO, bool DUAL, int WB = 1>
 int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   constexpr int NQ = DUAL ? 2 : 1;
-  constexpr bool kWide3 = !DUAL && WB == 1;  // 16 weight rows x three x sets fit the registers
   const int mt4 = (p.rows + 3) / 4;  // 4-row x sets: 1 .. 4
-  const bool wide3 = kWide3 && mt4 == 3 && sp.r4 == 4 && sp.u == 1;
-  if (mt4 > 2 && !wide3 && (sp.r4 > 2 || sp.u > 1)) {
-    set_error("w8a16 stream launch: more than 8 rows of x take at most 8 weight rows per workgroup (16 for 9 - 12 "
-              "rows against one int8 matrix) and one chunk in flight (r4 %d, u %d)", sp.r4, sp.u);
+  if (mt4 > 2 && sp.u > 1) {
+    set_error("w8a16 stream launch: more than 8 rows of x take one chunk in flight (u %d)", sp.u);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  const int max_threads = stream_max_threads(sp.r4 >= 4 ? 4 : sp.r4, mt4, sp.u >= 2 ? 2 : 1, DUAL, WB);
+  if (sp.waves < 1 || 64 * sp.waves > max_threads) {
+    set_error("w8a16 stream launch: %d waves per workgroup, this shape takes 1 - %d", sp.waves, max_threads / 64);
     return MI355_ERR_UNSUPPORTED;
   }
   const dim3 grid(static_cast<unsigned>((p.n + sp.rpw - 1) / sp.rpw));
@@ -354,17 +375,13 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   if (sp.u >= 2) MI355_W8S(R4, MT4, 2); else MI355_W8S(R4, MT4, 1)
 #define MI355_W8S_MT(R4) \
   if (mt4 == 1) { MI355_W8S_U(R4, 1); } else { MI355_W8S_U(R4, 2); }
-  // three or four x sets: one chunk in flight, at most two 4-row weight
-  // sets (16-row workgroups spill registers there), but for three x sets
-  // against one int8 matrix
+  // three or four x sets: one chunk in flight
 #define MI355_W8S_MT4(R4) \
   if (mt4 == 3) { MI355_W8S(R4, 3, 1); } else { MI355_W8S(R4, 4, 1); }
   if (mt4 <= 2) {
     if (sp.r4 >= 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
-  } else if (wide3) {
-    if constexpr (kWide3) MI355_W8S(4, 3, 1);
   } else {
-    if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
+    if (sp.r4 >= 4) { MI355_W8S_MT4(4) } else if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
   }
 #undef MI355_W8S_MT4
 #undef MI355_W8S_MT

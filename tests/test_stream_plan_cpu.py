@@ -2,17 +2,26 @@
 (``w8_stream_plan`` and ``gu16_stream_plan`` in csrc/w8a16_stream.h, reached
 through the probe library's plan exports; no GPU call): every plan the
 launchers can produce for 1 - 16 rows must be one the launcher accepts --
-at most 16 waves and no more waves than 256-byte chunks, rows per workgroup
-within its 4-row sets, and for more than 8 rows of x at most two weight sets
-and one chunk in flight (the instantiations the launcher has) -- and fit
-the kernel's LDS."""
+at most the kernel's thread limit (16 waves, 8 where its registers need
+more room) and no more waves than 256-byte chunks, rows per workgroup
+within its 4-row sets, and for more than 8 rows of x one chunk in flight
+(the instantiations the launcher has) -- and fit the kernel's LDS."""
 import ctypes
+import importlib.util
 import itertools
 from pathlib import Path
 
 import pytest
 
 PROBE = Path(__file__).resolve().parents[1] / "llm-inference-optimizer_amd" / "libmi355_probe.so"
+
+
+@pytest.fixture(scope="module")
+def bench():
+    spec = importlib.util.spec_from_file_location("bench_for_plans", PROBE.parents[1] / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
 
 
 @pytest.fixture(scope="module")
@@ -23,18 +32,20 @@ def probe():
     i32 = ctypes.c_int
     lib.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
     lib.mi355_probe_gate_up16_stream_plan.argtypes = [i32, i32, ctypes.POINTER(i32)]
+    lib.mi355_probe_stream_max_threads.argtypes = [i32] * 5
     return lib
 
 
-def _check(plan, rows, kbytes, nq):
+def _check(plan, rows, kbytes, nq, lib, wb=1):
     rpw, r4, waves, u = plan
     nchunk = -(-kbytes // 256)
     assert r4 in (1, 2, 4) and 1 <= rpw <= 4 * r4, plan
     assert 1 <= waves <= 16 and waves <= max(1, nchunk), (plan, nchunk)
     assert u in (1, 2), plan
     mt4 = -(-rows // 4)
-    if mt4 > 2:  # 16-row workgroups only with three x sets against one int8 matrix
-        assert (r4 <= 2 or (mt4 == 3 and nq == 1)) and u == 1, (rows, plan)
+    if mt4 > 2:  # one chunk in flight with three or four x sets
+        assert u == 1, (rows, plan)
+    assert 64 * waves <= lib.mi355_probe_stream_max_threads(r4, mt4, u, nq - 1, wb), (rows, plan)
     assert waves * nq * r4 * mt4 * 16 * 4 <= 64 * 1024
 
 
@@ -47,11 +58,29 @@ def test_w8a16_plan_is_launchable(probe, cus):
     out = (ctypes.c_int * 4)()
     for rows, k, n, dual in itertools.product(range(1, 17), KS, NS, (0, 1)):
         probe.mi355_probe_w8a16_stream_plan(rows, k, n, dual, cus, out)
-        _check(tuple(out), rows, k, 2 if dual else 1)
+        _check(tuple(out), rows, k, 2 if dual else 1, probe)
 
 
 def test_gate_up16_plan_is_launchable(probe):
     out = (ctypes.c_int * 4)()
     for rows, k in itertools.product(range(1, 17), (8, 24, 136, 896, 1536, 2048, 2056, 3584, 8192)):
         probe.mi355_probe_gate_up16_stream_plan(rows, k, out)
-        _check(tuple(out), rows, 2 * k, 2)
+        _check(tuple(out), rows, 2 * k, 2, probe, wb=2)
+
+
+def test_thread_limit_matches_the_bench_sweep(probe, bench):
+    """bench.py's sweep samples only launch shapes the kernel takes: its
+    stream_max_waves is the kernel's own thread limit / 64, and the limit
+    drops to 512 exactly where the register estimate reaches 112."""
+    for r4, mt4, u, dual, wb in itertools.product((1, 2, 4), (1, 2, 3, 4), (1, 2), (0, 1), (1, 2)):
+        lim = probe.mi355_probe_stream_max_threads(r4, mt4, u, dual, wb)
+        assert lim in (512, 1024)
+        assert bench.stream_max_waves(r4, mt4, u, bool(dual), wb) == lim // 64, (r4, mt4, u, dual, wb)
+    # the shapes that spilled under 128 VGPRs take 512 threads; those in use
+    # without spills keep 1024
+    assert probe.mi355_probe_stream_max_threads(4, 4, 1, 0, 1) == 512
+    assert probe.mi355_probe_stream_max_threads(2, 4, 1, 1, 1) == 512
+    assert probe.mi355_probe_stream_max_threads(4, 2, 1, 1, 1) == 512
+    assert probe.mi355_probe_stream_max_threads(4, 3, 1, 0, 1) == 1024
+    assert probe.mi355_probe_stream_max_threads(4, 2, 1, 1, 2) == 1024
+    assert probe.mi355_probe_stream_max_threads(2, 4, 1, 1, 2) == 1024
