@@ -70,11 +70,11 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--skip-e2e", action="store_true", help="no end-to-end before/after leg")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "gate-up",
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "linear16-table", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "l16-stream-sweep", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -140,6 +140,8 @@ class Ctx:
             self.probe.mi355_probe_w8a16_stream_loads.restype = ctypes.c_int
             self.probe.mi355_probe_gate_up16_stream.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]
             self.probe.mi355_probe_gate_up16_stream.restype = ctypes.c_int
+            self.probe.mi355_probe_linear16_stream.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]
+            self.probe.mi355_probe_linear16_stream.restype = ctypes.c_int
 
     def check(self, fn, st):
         if st:
@@ -321,6 +323,20 @@ class Ctx:
         def call():
             if f(*args, self.stream):
                 raise RuntimeError(f"probe gate_up16 stream failed for {args[4:]}")
+        return call
+
+    def linear16_stream_call(self, x, w, out, rpw, r4, waves, u, bias=None):
+        """The 16-bit linear through the weight-streaming kernel at a forced
+        launch shape (fp16, bias fp16 or none; csrc/probe/w8_stream_plan.hip)."""
+        M, K = x.shape
+        N = w.shape[0]
+        f = self.probe.mi355_probe_linear16_stream
+        args = (x.data_ptr(), w.data_ptr(), bias.data_ptr() if bias is not None else None, out.data_ptr(), M, K, N,
+                rpw, r4, waves, u)
+
+        def call():
+            if f(*args, self.stream):
+                raise RuntimeError(f"probe linear16 stream failed for {args[4:]}")
         return call
 
     def add2_call(self, a, b, dst):
@@ -515,9 +531,9 @@ KNOWN_LAUNCHES = {
     ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, true, 1>", 1184 * 64 * 1): (
         "int8 gate/up + SiLU-and-mul 7B, 8 rows, 2 x [18944,3584] int8, bf16",
         2 * 18944 * 3584 + 8 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
-    ("linear16_skinny<mi355::F16, mi355::F16, 1, 1, 2>", 192 * 512): (
+    ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 2, false, 2>", 256 * 64 * 8): (
         "16-bit linear, 8 rows, [1536,8960] weights, fp16 (1.5B down)", 1536 * 8960 * 2 + 8 * 8960 * 2 + 8 * 1536 * 2),
-    ("linear16_skinny<mi355::BF16, mi355::BF16, 1, 2, 2>", 224 * 512): (
+    ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, false, 2>", 224 * 64 * 8): (
         "16-bit linear, 8 rows, [3584,18944] weights, bf16 (7B down)", 3584 * 18944 * 2 + 8 * 18944 * 2 + 8 * 3584 * 2),
     # MFMA-bound prefill GEMMs: (label, algorithmic bytes, flops)
     # (the 1.5B gate/up at 1024 and 4096 rows runs as a column split: whole
@@ -953,6 +969,10 @@ def run_only(ctx, args, sets):
         torch.cuda.empty_cache()
         log(json.dumps(bench_gate_up_w8(ctx, shapes=[s for s in GATE_UP_W8_SHAPES if s[0] == 8], iters=iters,
                                         baselines=False)))
+    elif args.only == "linear16-table":  # every decode row count of the down projection, with torch's linear
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"linear16_down": bench_linear16(ctx)}), flush=True)
     elif args.only == "linear16":  # kernel only, the 1.5B down projection at 8 rows and the 7B one at 8 rows
         del sets
         torch.cuda.empty_cache()
@@ -1007,6 +1027,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"gate_up16_stream_sweep": gu16_stream_sweep(ctx)}), flush=True)
+    elif args.only == "l16-stream-sweep":  # the 16-bit linear on the weight-streaming kernel
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"linear16_stream_sweep": l16_stream_sweep(ctx)}), flush=True)
     elif args.only == "stream-sweep16-wide":  # 12 / 16 rows with 16-row workgroups too
         del sets
         torch.cuda.empty_cache()
@@ -1401,6 +1425,57 @@ GU16_SWEEP16_SHAPES = [("gu1.5b_M12", 12, 1536, 8960), ("gu1.5b_M16", 16, 1536, 
                        ("gu0.5b_M16", 16, 896, 4864), ("gu7b_M16", 16, 3584, 18944)]
 
 
+# (label, rows, k, n) of the 16-bit linear sweep: the MLP down projections
+# of Qwen2.5-0.5B, 1.5B and 7B at decode rows
+L16_SWEEP_SHAPES = [("down1.5b_M1", 1, 8960, 1536), ("down1.5b_M8", 8, 8960, 1536), ("down1.5b_M16", 16, 8960, 1536),
+                    ("down7b_M1", 1, 18944, 3584), ("down7b_M8", 8, 18944, 3584), ("down7b_M16", 16, 18944, 3584),
+                    ("down0.5b_M8", 8, 4864, 896), ("down1.5b_M4", 4, 8960, 1536)]
+
+
+def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
+    """The 16-bit linear at decode rows: the library's launch
+    (mi355_linear16_fwd) against the weight-streaming kernel of
+    w8a16_stream.h with one 16-bit matrix over launch shapes (rows per
+    workgroup 4-16 x waves 1-16 x chunks in flight 1-2), graph-node us over
+    cold weights, fp16; each shape's output checked against the library's
+    (within 2e-3 of the largest output)."""
+    torch = ctx.torch
+    F16 = torch.float16
+    out = {}
+    for label, M, K, N in shapes:
+        sets = n_sets(N * K * 2)
+        ws = [rand(ctx, (N, K), 3300 + i, F16, std=K ** -0.5) for i in range(sets)]
+        x = rand(ctx, (M, K), 3200 + M, F16)
+        o = torch.empty((M, N), dtype=F16, device=ctx.dev)
+        ref = torch.empty_like(o)
+        nodes = max(2 * sets, 64)
+        lib_calls = [ctx.linear16_call(x, w, o) for w in ws]
+        ctx.linear16_call(x, ws[0], ref)()
+        torch.cuda.synchronize()
+        tol = 2e-3 * ref.float().abs().max().item()
+        res, bad = {}, []
+        nchunk = -(-K // 128)
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, False, -(-M // 4), True, wb=2):
+            calls = [ctx.linear16_stream_call(x, w, o, rpw, r4, waves, u) for w in ws]
+            calls[0]()
+            torch.cuda.synchronize()
+            err = (o.float() - ref.float()).abs().max().item()
+            if not err <= tol:
+                bad.append((rpw, r4, waves, u, err))
+            spin_up(ctx, calls, ms=3.0)
+            res[f"rpw{rpw}_w{waves}_u{u}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
+        spin_up(ctx, lib_calls, ms=5.0)
+        res["library_us"] = round(time_graph(ctx, lib_calls, nodes, replays=5), 3)
+        best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
+        out[label] = {"best": best, "best_us": res[best], "library_us": res["library_us"], "mismatches": bad,
+                      "shapes": res}
+        log(f"  l16 stream sweep {label}: library {res['library_us']} us, best {best} {res[best]} us, "
+            f"{len(bad)} mismatches {bad[:3]}")
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False):
     """The 16-bit gate/up + SiLU-and-mul at decode rows: the library's
     launch (mi355_gate_up_silu_fwd) against the weight-streaming kernel of
@@ -1786,8 +1861,9 @@ W8A16_RAGGED_PREFILL_SHAPES = [(1400, 1536, 8960, "f16", "gate/up proj"), (2900,
 
 # (rows, k, n, dtype name, label): the MLP down projections of Qwen2.5-1.5B and -7B at decode rows
 LINEAR16_SHAPES = [(1, 8960, 1536, "f16", "qwen2.5-1.5b down"), (8, 8960, 1536, "f16", "qwen2.5-1.5b down"),
-                   (32, 8960, 1536, "f16", "qwen2.5-1.5b down"), (1, 18944, 3584, "bf16", "qwen2.5-7b down"),
-                   (8, 18944, 3584, "bf16", "qwen2.5-7b down")]
+                   (16, 8960, 1536, "f16", "qwen2.5-1.5b down"), (32, 8960, 1536, "f16", "qwen2.5-1.5b down"),
+                   (1, 18944, 3584, "bf16", "qwen2.5-7b down"), (8, 18944, 3584, "bf16", "qwen2.5-7b down"),
+                   (16, 18944, 3584, "bf16", "qwen2.5-7b down")]
 
 
 def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
@@ -1814,7 +1890,7 @@ def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
         us_graph = time_graph(ctx, calls, 4 * layers)
         best = min(us, us_graph)
         key = f"{label}_M{M}_{dname}"
-        entry = kernel_entry("linear16_skinny", nbytes, best,
+        entry = kernel_entry("w8a16_stream (16-bit weights)" if M <= 16 else "linear16_skinny", nbytes, best,
                              {"rows": M, "k": K, "n": N, "weight_sets": layers, "eager_us": round(us, 3),
                               "graph_us": round(us_graph, 3)})
         if (M, K, N, dname) == (8, 8960, 1536, "f16"):

@@ -11,11 +11,14 @@
 // bandwidth (about 21 us for the 27.5 MB down projection of Qwen2.5-1.5B at
 // 1 to 8 rows on MI355X).
 //
-// Three kernels, picked by the launcher:
-//   linear16_skinny   rows <= 32 (decode), and a few 32-row tiles where the
-//                     tiled grid would be small: every weight byte is read once
-//                     per call with non-temporal loads and meets up to 32 rows
-//                     of x on MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
+// Four kernels, picked by the launcher:
+//   w8a16_stream      rows <= 16 (decode; w8a16_stream.h with one 16-bit
+//                     matrix): lane-coalesced weight streaming, every weight
+//                     byte read once per call, MFMA (v_mfma_f32_16x16x32_*).
+//   linear16_skinny   17 - 32 rows, and a few 32-row tiles where the tiled
+//                     grid would be small: every weight byte is read once per
+//                     call with non-temporal loads and meets up to 32 rows of
+//                     x on MFMA (the same instruction).
 //   tiled_gemm        more rows: the LDS-tiled MFMA GEMM of tiled_gemm.h with
 //                     the weights as a 16-bit B operand and the bias in its
 //                     epilogue (EPI_LINEAR).
@@ -40,6 +43,7 @@
 // in LDS in a fixed order, so a call's bits do not depend on scheduling.
 #include "common.h"
 #include "tiled_gemm.h"
+#include "w8a16_stream.h"
 
 namespace mi355 {
 namespace {
@@ -315,6 +319,17 @@ int l16_typed(const L16Params& p, hipStream_t s, int cus) {
   if (!vec) {
     const int64_t waves = static_cast<int64_t>(p.n) * ((p.rows + kGenRows - 1) / kGenRows);
     return launch_l16(linear16_generic<T, TO>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, p, s);
+  }
+  // Up to 16 rows: the weight-streaming kernel of w8a16_stream.h with one
+  // 16-bit matrix, whose x descriptor spans all rows of x and each
+  // workgroup's weight descriptor up to 16 weight rows (both under 2^32
+  // bytes); else the skinny kernel below.
+  const int64_t tb = sizeof(typename T::bits);
+  if (p.rows <= 16 && ((p.rows - 1) * p.xs + p.k) * tb < (int64_t{1} << 32) &&
+      (15 * p.ws + p.k) * tb < (int64_t{1} << 32)) {
+    const W8Params w{p.x, p.w, nullptr, p.bias, p.out, p.rows, p.k, p.n, p.xs, p.ws, p.os, MI355_F32, p.bdt,
+                     nullptr, nullptr};
+    return w8_stream_launch<T, TO, false, 2>(w, l16_stream_plan(p.rows, p.k, p.n, cus), s);
   }
   if (p.rows <= 8) return l16_skinny_shape<T, TO, 1>(p, s, cus);
   if (p.rows <= 16) return l16_skinny_shape<T, TO, 2>(p, s, cus);

@@ -202,6 +202,31 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_gate_up16_stre
   return launch_stream(stream_kernel<true, 2>(r4, (rows + 3) / 4, u), p, rpw, r4, waves, 2, stream);
 }
 
+// out [rows, n] = x @ w^T (+ bias) for x [rows, k] and 16-bit weights [n, k]
+// (fp16; bias fp16 or NULL), by the weight-streaming kernel of w8a16_stream.h
+// with one 16-bit matrix (WB = 2) at launch shape (rpw, r4, waves, u).  rows
+// <= 16, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on
+// bad arguments, -3 on a launch error.
+extern "C" __attribute__((visibility("default"))) int mi355_probe_linear16_stream(
+    const void* x, const void* w, const void* bias, void* out, int rows, int k, int n, int rpw, int r4, int waves,
+    int u, void* stream) {
+  if (!x || !w || !out || k < 8 || (k & 7) || !shape_ok(rows, n, rpw, r4, waves, u, false, 2)) return -1;
+  const mi355::W8Params p{x, w, nullptr, bias, out, rows, k, n, k, k, n, MI355_F32, bias ? MI355_F16 : -1,
+                          nullptr, nullptr};
+  return launch_stream(stream_kernel<false, 2>(r4, (rows + 3) / 4, u), p, rpw, r4, waves, 1, stream);
+}
+
+// The 16-bit linear's launch plan (l16_stream_plan) for `rows` x k x n on
+// `cus` CUs: out4 = {rpw, r4, waves, u}.
+extern "C" __attribute__((visibility("default"))) void mi355_probe_linear16_stream_plan(int rows, int k, int n,
+                                                                                         int cus, int* out4) {
+  const mi355::StreamPlan sp = mi355::l16_stream_plan(rows, k, n, cus);
+  out4[0] = sp.rpw;
+  out4[1] = sp.r4;
+  out4[2] = sp.waves;
+  out4[3] = sp.u;
+}
+
 // Most threads per workgroup of w8a16_stream<.., r4, mt4, u, dual, wb>.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_stream_max_threads(int r4, int mt4, int u,
                                                                                       int dual, int wb) {

@@ -96,10 +96,10 @@ struct StreamPlan {
 
 // WB: bytes per weight element -- 1 (int8 weights with per-row scales, the
 // W8A16 linear and the int8 gate/up + SiLU-and-mul) or 2 (weights of x's
-// 16-bit type, no scales: the 16-bit gate/up + SiLU-and-mul, DUAL only).  A
-// lane's 16-byte weight load is then 8 k, one B operand as loaded, a chunk
-// of a weight row's 256 bytes is 128 k, and one 16-byte x load per 4-row x
-// set matches it.
+// 16-bit type, no scales: the 16-bit gate/up + SiLU-and-mul when DUAL, else
+// the 16-bit linear, out = acc + bias).  A lane's 16-byte weight load is then
+// 8 k, one B operand as loaded, a chunk of a weight row's 256 bytes is 128 k,
+// and one 16-byte x load per 4-row x set matches it.
 // Most threads per workgroup of w8a16_stream<R4, MT4, U, DUAL, WB>: 1024 (16
 // waves, 128 VGPRs per lane) while its accumulators and the registers its
 // loads keep in flight come to less than 112 VGPRs (4 per 16x16 accumulator
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
   constexpr int NQ = DUAL ? 2 : 1;
   constexpr bool W16 = WB == 2;
   constexpr int KC = 256 / WB;  // k per 256-byte chunk of a weight row
-  static_assert(WB == 1 || (WB == 2 && DUAL), "16-bit weights: the gate/up kernel only");
+  static_assert(WB == 1 || WB == 2, "int8 or 16-bit weights");
   extern __shared__ float red[];  // [nwave][NQ][R4][MT4][16]
 
   const int lane = threadIdx.x & 63;
@@ -155,12 +155,14 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
   float osc[OPT][NQ], obias[OPT];
 #pragma unroll
   for (int i = 0; i < OPT; ++i) {
-    if constexpr (W16) break;  // no scales
+    if constexpr (W16 && DUAL) break;  // no scales, no bias
     const int o = threadIdx.x + i * blockDim.x;
     const int nn = 4 * ((o >> 4) % R4) + (o & 3);
     const bool mine = o < NOUT && nn < nrows_w;
-    osc[i][0] = mine ? load_dyn(p.scale, n0 + nn, p.sdt) : 0.f;
-    if constexpr (DUAL) osc[i][NQ - 1] = mine ? load_dyn(p.scale2, n0 + nn, p.sdt) : 0.f;
+    if constexpr (!W16) {
+      osc[i][0] = mine ? load_dyn(p.scale, n0 + nn, p.sdt) : 0.f;
+      if constexpr (DUAL) osc[i][NQ - 1] = mine ? load_dyn(p.scale2, n0 + nn, p.sdt) : 0.f;
+    }
     obias[i] = mine && !DUAL && p.bdt >= 0 ? load_dyn(p.bias, n0 + nn, p.bdt) : 0.f;
   }
 
@@ -238,7 +240,8 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
   __syncthreads();
 
   // Output (x row 4 t + m', weight row 4 r + r') = sum over waves, in order;
-  // then the epilogue of w8_store / w8_store_silu with the preloaded scales.
+  // then the epilogue of w8_store / w8_store_silu with the preloaded scales
+  // (16-bit weights: no scales; the single matrix adds the bias in fp32).
 #pragma unroll
   for (int i = 0; i < OPT; ++i) {
     const int o = threadIdx.x + i * blockDim.x;
@@ -254,8 +257,10 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
       for (int w = 0; w < nwave; ++w) sum[qi] += red[(((w * NQ + qi) * R4 + r) * MT4 + t) * 16 + slot];
     }
     const int64_t off = static_cast<int64_t>(m) * p.os + n0 + nn;
-    if constexpr (W16) {
+    if constexpr (W16 && DUAL) {
       store_elem<TO>(p.out, off, silu_mul_f32(sum[0], sum[NQ - 1]));
+    } else if constexpr (W16) {
+      store_elem<TO>(p.out, off, p.bdt >= 0 ? sum[0] + obias[i] : sum[0]);
     } else if constexpr (DUAL) {
       store_elem<TO>(p.out, off, silu_mul_f32(sum[0] * osc[i][0], sum[NQ - 1] * osc[i][NQ - 1]));
     } else {
@@ -346,6 +351,43 @@ inline StreamPlan gu16_stream_plan(int rows, int k) {
   if (sp.waves > nchunk) sp.waves = nchunk;
   const int max_waves = stream_max_threads(sp.r4, (rows + 3) / 4, sp.u, true, 2) / 64;
   if (sp.waves > max_waves) sp.waves = max_waves;
+  return sp;
+}
+
+// Launch plan of the 16-bit linear (WB = 2, one matrix) for `rows` <= 16
+// rows of x against [n, k] weights, from a graph-timed sweep over the
+// Qwen2.5-0.5B, 1.5B and 7B MLP down projections at 1, 4, 8 and 16 rows
+// (bench.py --only l16-stream-sweep): the int8 kernel's plan for the same
+// bytes per weight row (2 k), except
+//   - narrow outputs (its plan's 4 - 8 rows per workgroup) with up to 8 rows
+//     of x: 2 chunks in flight, about 12 waves per CU with one x set, 8 with
+//     two (1.5B down, 1 row 6.36 us against 6.72 with one chunk; 0.5B down,
+//     8 rows 4.71 vs 5.04);
+//   - 16-row workgroups with more than 8 rows of x: about 7 waves per CU,
+//     as with fewer rows (7B down, 16 rows: 8 waves 27.7 us, 7 waves 29.2).
+// linear16_skinny, which served these rows before, took 10.27 / 14.75 us
+// at the 1.5B down with 8 / 16 rows (now 7.76 / 9.94) and 27.37 / 35.41 us
+// at the 7B down (now 23.42 / 27.7).
+inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
+  StreamPlan sp = w8_stream_plan(rows, 2 * k, n, false, cus);
+  const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
+  int per_cu = 0;
+  if (sp.rpw <= 8 && (n <= 2048 || (n + 7) / 8 < cus) && rows <= 8) {
+    sp.u = 2;
+    per_cu = rows <= 4 ? 12 : 8;
+  } else if (sp.rpw == 16 && rows > 8) {
+    per_cu = 7;
+  }
+  if (per_cu > 0) {
+    int64_t waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
+    const int nchunk = (k + 127) / 128;
+    const int max_waves = stream_max_threads(sp.r4, (rows + 3) / 4, sp.u, false, 2) / 64;
+    if (waves > max_waves) waves = max_waves;
+    if (waves > nchunk) waves = nchunk;
+    if (waves < 1) waves = 1;
+    if (wgs <= cus && waves > 8) waves = waves / 4 * 4;
+    sp.waves = static_cast<int>(waves);
+  }
   return sp;
 }
 

@@ -1,5 +1,6 @@
 """CPU checks of the weight-streaming decode kernel's launch plans
-(``w8_stream_plan`` and ``gu16_stream_plan`` in csrc/w8a16_stream.h, reached
+(``w8_stream_plan``, ``l16_stream_plan`` and ``gu16_stream_plan`` in
+csrc/w8a16_stream.h, reached
 through the probe library's plan exports; no GPU call): every plan the
 launchers can produce for 1 - 16 rows must be one the launcher accepts --
 at most the kernel's thread limit (16 waves, 8 where its registers need
@@ -33,6 +34,7 @@ def probe():
     lib.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
     lib.mi355_probe_gate_up16_stream_plan.argtypes = [i32, i32, ctypes.POINTER(i32)]
     lib.mi355_probe_stream_max_threads.argtypes = [i32] * 5
+    lib.mi355_probe_linear16_stream_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(i32)]
     return lib
 
 
@@ -59,6 +61,14 @@ def test_w8a16_plan_is_launchable(probe, cus):
     for rows, k, n, dual in itertools.product(range(1, 17), KS, NS, (0, 1)):
         probe.mi355_probe_w8a16_stream_plan(rows, k, n, dual, cus, out)
         _check(tuple(out), rows, k, 2 if dual else 1, probe)
+
+
+@pytest.mark.parametrize("cus", [80, 256, 304])
+def test_linear16_plan_is_launchable(probe, cus):
+    out = (ctypes.c_int * 4)()
+    for rows, k, n in itertools.product(range(1, 17), (8, 24, 136, 896, 1536, 2056, 3584, 8960, 18944), NS):
+        probe.mi355_probe_linear16_stream_plan(rows, k, n, cus, out)
+        _check(tuple(out), rows, 2 * k, 1, probe, wb=2)
 
 
 def test_gate_up16_plan_is_launchable(probe):
