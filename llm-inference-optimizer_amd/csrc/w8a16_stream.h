@@ -1,11 +1,14 @@
 // The W8A16 decode kernel (up to 16 rows of x): int8 weight streaming with
-// lane-coalesced loads, plus its launch plan.  Shared by the W8A16 linear and
+// lane-coalesced loads, plus its launch plans.  Shared by the W8A16 linear and
 // the int8 gate/up + SiLU-and-mul launchers (w8a16.hip) and, with 16-bit
 // weights (template argument WB = 2, below), by the 16-bit gate/up +
-// SiLU-and-mul launcher (gate_up_silu.hip).
+// SiLU-and-mul launcher (gate_up_silu.hip) and the 16-bit linear
+// (linear16.hip).
 //
 //   out[m, n] = round(acc * scale[n] + bias[n]),  acc = sum_k x[m, k] * q[n, k]
 //   (DUAL: out[m, n] = round(silu(acc_g * scale_g[n]) * (acc_u * scale_u[n])))
+//   (16-bit weights: no scales; out = round(acc + bias[n]), or the SiLU-and-mul
+//   of the two sums when DUAL)
 //
 // Load layout.  The weights are read 4 rows x 256 bytes per load instruction:
 // lane l reads 16 bytes of weight row 4 r + (l % 16) / 4 (4-row set r of the
