@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "l16-stream-sweep", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "l16-stream-sweep", "stream-sweep32", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1027,6 +1027,12 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"gate_up16_stream_sweep": gu16_stream_sweep(ctx)}), flush=True)
+    elif args.only == "stream-sweep32":  # 17 - 32 rows: all three forms of the decode kernel
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP32_SHAPES, True),
+                          "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP32_SHAPES),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP32_SHAPES, True)}), flush=True)
     elif args.only == "l16-stream-sweep":  # the 16-bit linear on the weight-streaming kernel
         del sets
         torch.cuda.empty_cache()
@@ -1289,10 +1295,16 @@ def w8_layout_sweep(ctx):
 def stream_max_waves(r4, mt4, u, dual, wb=1):
     """Most waves per workgroup of the decode stream kernel's instantiation
     (stream_max_threads of csrc/w8a16_stream.h / 64): 16, or 8 where its
-    accumulators and loads in flight need 112 VGPRs or more."""
+    estimated live registers (stream_regs) reach 112, 0 above 224."""
     nq = 2 if dual else 1
-    est = 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (8 if wb == 1 else 4) * mt4)
-    return 8 if est >= 112 else 16
+    est = 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (8 if wb == 1 else 4) * mt4) + r4 + mt4
+    return 0 if est > 224 else (8 if est >= 112 else 16)
+
+
+def stream_x_sets(rows):
+    """4-row x sets of the decode stream kernel (stream_x_sets of
+    csrc/w8a16_stream.h): ceil(rows / 4) up to 16 rows, then 6 or 8."""
+    return -(-rows // 4) if rows <= 16 else (6 if rows <= 24 else 8)
 
 
 def _w8_stream_shapes(nchunk, dual, mt4, wide16=False, wb=1):
@@ -1341,6 +1353,17 @@ W8_STREAM_SWEEP16_WIDE_SHAPES = [("gateup7b_M9", 9, 3584, 18944, False), ("gateu
                                  ("down7b_M16", 16, 18944, 3584, False), ("down_M16", 16, 8960, 1536, False),
                                  ("dual7b_M8", 8, 3584, 18944, True), ("dual7b_M12", 12, 3584, 18944, True),
                                  ("dual7b_M16", 16, 3584, 18944, True), ("dual_gateup_M16", 16, 1536, 8960, True)]
+# 17 - 32 rows (6 and 8 x sets): the Qwen2.5-1.5B and 7B projections and MLPs
+W8_STREAM_SWEEP32_SHAPES = [("down_M24", 24, 8960, 1536, False), ("down_M32", 32, 8960, 1536, False),
+                            ("gateup_M32", 32, 1536, 8960, False), ("o1.5b_M32", 32, 1536, 1536, False),
+                            ("down7b_M32", 32, 18944, 3584, False), ("gateup7b_M32", 32, 3584, 18944, False),
+                            ("dual_gateup_M32", 32, 1536, 8960, True), ("dual7b_M32", 32, 3584, 18944, True),
+                            ("gateup0.5b_M32", 32, 896, 4864, False), ("down0.5b_M32", 32, 4864, 896, False),
+                            ("dual0.5b_M32", 32, 896, 4864, True), ("o7b_M32", 32, 3584, 3584, False),
+                            ("down_M20", 20, 8960, 1536, False)]
+GU16_SWEEP32_SHAPES = [("gu1.5b_M32", 32, 1536, 8960), ("gu7b_M32", 32, 3584, 18944), ("gu0.5b_M32", 32, 896, 4864)]
+L16_SWEEP32_SHAPES = [("down1.5b_M24", 24, 8960, 1536), ("down1.5b_M32", 32, 8960, 1536),
+                      ("down7b_M32", 32, 18944, 3584), ("down0.5b_M32", 32, 4864, 896), ("o7b_M32", 32, 3584, 3584)]
 GU16_SWEEP16_WIDE_SHAPES = [("gu7b_M12", 12, 3584, 18944), ("gu7b_M16", 16, 3584, 18944),
                             ("gu1.5b_M16", 16, 1536, 8960)]
 W8_STREAM_SWEEP16_SHAPES = [
@@ -1386,7 +1409,7 @@ def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
         tol = 2e-3 * ref.float().abs().max().item()
         bad = []
         nchunk = -(-K // 256)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, -(-M // 4), wide16):
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, stream_x_sets(M), wide16):
             def mk(q, sc):
                 if dual:
                     return ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u, q[1], sc[1])
@@ -1455,7 +1478,7 @@ def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
         tol = 2e-3 * ref.float().abs().max().item()
         res, bad = {}, []
         nchunk = -(-K // 128)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, False, -(-M // 4), True, wb=2):
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, False, stream_x_sets(M), True, wb=2):
             calls = [ctx.linear16_stream_call(x, w, o, rpw, r4, waves, u) for w in ws]
             calls[0]()
             torch.cuda.synchronize()
@@ -1501,7 +1524,7 @@ def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False):
         tol = 2e-3 * ref.float().abs().max().item()
         res, bad = {}, []
         nchunk = -(-K // 128)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, -(-M // 4), wide16, wb=2):
+        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, stream_x_sets(M), wide16, wb=2):
             calls = [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u) for wg, wu in ws]
             calls[0]()
             torch.cuda.synchronize()
@@ -1890,7 +1913,9 @@ def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
         us_graph = time_graph(ctx, calls, 4 * layers)
         best = min(us, us_graph)
         key = f"{label}_M{M}_{dname}"
-        entry = kernel_entry("w8a16_stream (16-bit weights)" if M <= 16 else "linear16_skinny", nbytes, best,
+        small_tiles = 16 < M <= 64 and -(-N // (128 if (M <= 32 and N > 10000) else 64)) >= 128
+        entry = kernel_entry("w8a16_stream (16-bit weights)" if M <= 32 and not small_tiles else "linear16 tiled",
+                             nbytes, best,
                              {"rows": M, "k": K, "n": N, "weight_sets": layers, "eager_us": round(us, 3),
                               "graph_us": round(us_graph, 3)})
         if (M, K, N, dname) == (8, 8960, 1536, "f16"):
@@ -1911,16 +1936,16 @@ def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
 
 def w8a16_kernel_name(M, N, K=0):
     """The kernel mi355_w8a16_linear_fwd runs for this shape (aligned inputs,
-    tiles that fit): the weight-streaming kernel up to 8 rows, and up to 16
-    but for wide, deep outputs (n > 10000, k > 2048) at 13-16 rows (9-16 for
-    k < 3072), the skinny split-K kernel up to 32 rows (or the small tiled
-    shapes where they pay) and for small grids, the tiled MFMA GEMM
+    descriptors that fit): the weight-streaming kernel up to 32 rows, but
+    for wide outputs with 2048 < k < 3072 beyond 8 rows (the skinny split-K
+    kernel) and where the small tiled shapes pay (17 - 64 rows, >= 128 tile
+    columns); the skinny kernel for small grids, the tiled MFMA GEMM
     otherwise."""
-    if M <= 8 or (M <= 16 and not (N > 10000 and K > 2048)) or (M <= 12 and K >= 3072):
-        return "w8a16_stream"
     bn = 128 if (M <= 32 and N > 10000) else 64
     if 16 < M <= 64 and -(-N // bn) >= 128:
         return "tiled_gemm<int8 B> (small tiles)"
+    if M <= 8 or (M <= 32 and not (N > 10000 and 2048 < K < 3072)):
+        return "w8a16_stream"
     if M <= 32:
         return "w8a16_skinny"
     tiles64 = ((N + 63) // 64) * ((M + 63) // 64)

@@ -12,10 +12,10 @@
 // At decode shapes (rows <= 32) the work is weight streaming: each weight
 // element is read once per call (2 * n_out * k elements) and meets at most 32
 // rows of x, so the kernel is bound by HBM bandwidth on the weights, not by
-// MFMA.  Up to 16 rows the launcher runs the lane-coalesced weight-streaming
-// kernel of w8a16_stream.h with 16-bit weights; the skinny kernel below
-// serves 17 - 32 rows where the small tiled shapes do not pay, and any
-// decode call whose x would span more than a buffer descriptor reaches.
+// MFMA.  Up to 32 rows the launcher runs the lane-coalesced weight-streaming
+// kernel of w8a16_stream.h with 16-bit weights (from 17 rows where the small
+// tiled shapes do not pay); the skinny kernel below serves any decode call
+// whose inputs would span more than that kernel's buffer descriptors reach.
 // More rows are a GEMM (MFMA-bound): they run the LDS-tiled kernel of
 // tiled_gemm.h with both weight matrices as B operands and SiLU-and-mul in
 // its epilogue.
@@ -376,20 +376,22 @@ int gate_up_typed(const GateUpParams& p, hipStream_t s) {
   // once from HBM and x once per workgroup, where 3 or 4 skinny x tiles
   // re-load x per weight piece (1.5B, 32 rows 20.0 -> 15.5 us; 7B 66.7 ->
   // 53.8 us), as long as the output has >= 128 tile columns to spread over
-  // the CUs -- else 24- or 32-row skinny tiles along grid y.
+  // the CUs -- else the stream kernel again with 6 or 8 x sets (0.5B, 32
+  // rows 10.5 -> 9.0 us against 32-row skinny tiles), or 24- or 32-row
+  // skinny tiles along grid y where its descriptors cannot span the inputs.
+  const int64_t tb = sizeof(typename T::bits);
+  const bool stream_fits = p.rows <= 32 && ((p.rows - 1) * p.xs + p.k) * tb < (int64_t{1} << 32) &&
+                           (15 * p.ws + p.k) * tb < (int64_t{1} << 32);
+  const W8Params w{p.x, p.wg, nullptr, nullptr, p.out, p.rows, p.k, p.n_out, p.xs, p.ws, p.os, MI355_F32, -1,
+                   p.wu, nullptr};
   if (p.rows <= 16) {
-    const int64_t x_bytes = ((p.rows - 1) * p.xs + p.k) * static_cast<int64_t>(sizeof(typename T::bits));
-    if (x_bytes < (int64_t{1} << 32)) {
-      const W8Params w{p.x, p.wg, nullptr, nullptr, p.out, p.rows, p.k, p.n_out, p.xs, p.ws, p.os, MI355_F32, -1,
-                       p.wu, nullptr};
-      return w8_stream_launch<T, TO, true, 2>(w, gu16_stream_plan(p.rows, p.k), s);
-    }
+    if (stream_fits) return w8_stream_launch<T, TO, true, 2>(w, gu16_stream_plan(p.rows, p.k), s);
     return p.rows <= 8 ? gate_up_shape<T, TO, 1>(p, s) : gate_up_shape<T, TO, 2>(p, s);
   }
-  const bool tiled_fits = int64_t{256} * p.xs * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31) &&
-                          int64_t{128} * p.ws * static_cast<int64_t>(sizeof(typename T::bits)) < (int64_t{1} << 31);
+  const bool tiled_fits = int64_t{256} * p.xs * tb < (int64_t{1} << 31) && int64_t{128} * p.ws * tb < (int64_t{1} << 31);
   const int bn = p.n_out > 10000 ? 128 : 64;
   if (tiled_fits && (p.rows > 32 || (p.n_out + bn - 1) / bn >= 128)) return gate_up_tiled<T, TO>(p, s);
+  if (stream_fits) return w8_stream_launch<T, TO, true, 2>(w, gu16_stream_plan(p.rows, p.k), s);
   if (p.rows <= 24) return gate_up_shape<T, TO, 3>(p, s);
   return gate_up_shape<T, TO, 4>(p, s);
 }

@@ -126,22 +126,26 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_l
 namespace {
 
 // The decode kernel at any launch shape the probes accept: R4 in {1, 2, 4},
-// MT4 = ceil(rows / 4) in 1 .. 4 (16 rows of x), U in {1, 2} (U = 1 only
-// for MT4 > 2); fp16 x, weights of WB bytes.
+// MT4 = stream_x_sets(rows) in 1 .. 4, 6, 8 (32 rows of x), U in {1, 2}
+// (U = 1 only for MT4 > 2); fp16 x, weights of WB bytes.
 template <bool DUAL, int WB, int R4, int MT4>
 const void* sk_u(int u) {
   using mi355::F16;
   if constexpr (MT4 <= 2) {
     if (u >= 2) return reinterpret_cast<const void*>(mi355::w8a16_stream<F16, F16, R4, MT4, 2, DUAL, WB>);
   }
-  return reinterpret_cast<const void*>(mi355::w8a16_stream<F16, F16, R4, MT4, 1, DUAL, WB>);
+  // shapes without a kernel (stream_max_threads 0): shape_ok rejects them
+  if constexpr (mi355::stream_max_threads(R4, MT4, 1, DUAL, WB) == 0) return nullptr;
+  else return reinterpret_cast<const void*>(mi355::w8a16_stream<F16, F16, R4, MT4, 1, DUAL, WB>);
 }
 template <bool DUAL, int WB, int R4>
 const void* sk_mt(int mt4, int u) {
   if (mt4 == 1) return sk_u<DUAL, WB, R4, 1>(u);
   if (mt4 == 2) return sk_u<DUAL, WB, R4, 2>(u);
   if (mt4 == 3) return sk_u<DUAL, WB, R4, 3>(u);
-  return sk_u<DUAL, WB, R4, 4>(u);
+  if (mt4 == 4) return sk_u<DUAL, WB, R4, 4>(u);
+  if (mt4 == 6) return sk_u<DUAL, WB, R4, 6>(u);
+  return sk_u<DUAL, WB, R4, 8>(u);
 }
 template <bool DUAL, int WB>
 const void* stream_kernel(int r4, int mt4, int u) {
@@ -151,14 +155,14 @@ const void* stream_kernel(int r4, int mt4, int u) {
 }
 
 bool shape_ok(int rows, int n, int rpw, int r4, int waves, int u, bool dual, int wb) {
-  const int mt4 = (rows + 3) / 4;
-  return rows >= 1 && rows <= 16 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4) && rpw <= 4 * r4 &&
+  const int mt4 = mi355::stream_x_sets(rows);
+  return rows >= 1 && rows <= 32 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4) && rpw <= 4 * r4 &&
          waves >= 1 && 64 * waves <= mi355::stream_max_threads(r4, mt4, u, dual, wb) &&
          (u == 1 || (u == 2 && mt4 <= 2));
 }
 
 int launch_stream(const void* kern, const mi355::W8Params& p, int rpw, int r4, int waves, int nq, void* stream) {
-  const int mt4 = (p.rows + 3) / 4;
+  const int mt4 = mi355::stream_x_sets(p.rows);
   const size_t lds = static_cast<size_t>(waves) * nq * r4 * mt4 * 16 * sizeof(float);
   int rpw_arg = rpw;
   void* args[] = {const_cast<mi355::W8Params*>(&p), &rpw_arg};
@@ -175,7 +179,7 @@ int launch_stream(const void* kern, const mi355::W8Params& p, int rpw, int r4, i
 // scale2 the up weights), launched with rpw weight rows per workgroup, r4
 // 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves (at most
 // stream_max_threads / 64: 16 or 8) and u chunks in flight (1 or 2; 1 above
-// 8 rows).  rows <= 16, k a multiple of 16, every pointer
+// 8 rows).  rows <= 32, k a multiple of 16, every pointer
 // 16-byte aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
     const void* x, const void* q, const void* scale, const void* q2, const void* scale2, void* out, int rows, int k,
@@ -184,7 +188,7 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
       (!q2) != (!scale2))
     return -1;
   const mi355::W8Params p{x, q, scale, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, q2, scale2};
-  const int mt4 = (rows + 3) / 4;
+  const int mt4 = mi355::stream_x_sets(rows);
   const void* kern = q2 ? stream_kernel<true, 1>(r4, mt4, u) : stream_kernel<false, 1>(r4, mt4, u);
   return launch_stream(kern, p, rpw, r4, waves, q2 ? 2 : 1, stream);
 }
@@ -192,20 +196,20 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream(
 // out [rows, n] = silu(x @ wg^T) * (x @ wu^T) for x [rows, k] and 16-bit
 // weights [n, k] (fp16), by the weight-streaming kernel of w8a16_stream.h
 // with 16-bit weights (WB = 2) at launch shape (rpw, r4, waves, u).  rows <=
-// 16, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on
+// 32, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on
 // bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_gate_up16_stream(
     const void* x, const void* wg, const void* wu, void* out, int rows, int k, int n, int rpw, int r4, int waves,
     int u, void* stream) {
   if (!x || !wg || !wu || !out || k < 8 || (k & 7) || !shape_ok(rows, n, rpw, r4, waves, u, true, 2)) return -1;
   const mi355::W8Params p{x, wg, nullptr, nullptr, out, rows, k, n, k, k, n, MI355_F32, -1, wu, nullptr};
-  return launch_stream(stream_kernel<true, 2>(r4, (rows + 3) / 4, u), p, rpw, r4, waves, 2, stream);
+  return launch_stream(stream_kernel<true, 2>(r4, mi355::stream_x_sets(rows), u), p, rpw, r4, waves, 2, stream);
 }
 
 // out [rows, n] = x @ w^T (+ bias) for x [rows, k] and 16-bit weights [n, k]
 // (fp16; bias fp16 or NULL), by the weight-streaming kernel of w8a16_stream.h
 // with one 16-bit matrix (WB = 2) at launch shape (rpw, r4, waves, u).  rows
-// <= 16, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on
+// <= 32, k a multiple of 8, every pointer 16-byte aligned.  Returns 0, -1 on
 // bad arguments, -3 on a launch error.
 extern "C" __attribute__((visibility("default"))) int mi355_probe_linear16_stream(
     const void* x, const void* w, const void* bias, void* out, int rows, int k, int n, int rpw, int r4, int waves,
@@ -213,7 +217,7 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_linear16_strea
   if (!x || !w || !out || k < 8 || (k & 7) || !shape_ok(rows, n, rpw, r4, waves, u, false, 2)) return -1;
   const mi355::W8Params p{x, w, nullptr, bias, out, rows, k, n, k, k, n, MI355_F32, bias ? MI355_F16 : -1,
                           nullptr, nullptr};
-  return launch_stream(stream_kernel<false, 2>(r4, (rows + 3) / 4, u), p, rpw, r4, waves, 1, stream);
+  return launch_stream(stream_kernel<false, 2>(r4, mi355::stream_x_sets(rows), u), p, rpw, r4, waves, 1, stream);
 }
 
 // The 16-bit linear's launch plan (l16_stream_plan) for `rows` x k x n on

@@ -12,13 +12,14 @@
 // rounding to the output type.  Here scale and bias go through one fma.
 //
 // Four kernels, picked by the launcher:
-//   w8a16_stream   rows <= 16 (decode; w8a16_stream.h): weight streaming with
+//   w8a16_stream   rows <= 16 (decode; w8a16_stream.h), and 17 - 32 where
+//                  the small tiled shapes do not pay: weight streaming with
 //                  lane-coalesced loads, every weight byte read once per call
 //                  at HBM bandwidth, MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
-//   w8a16_skinny   17 - 32 rows (and 9 - 16 of wide outputs with 2048 < k <
-//                  3072), and a few 32-row tiles where the tiled grid
-//                  would be small: weight streaming with up to 32 rows of x
-//                  per workgroup (MFMA, the same instruction).
+//   w8a16_skinny   9 - 32 rows of wide outputs with 2048 < k < 3072, x
+//                  descriptors past 2^32 bytes, and a few 32-row tiles where
+//                  the tiled grid would be small: weight streaming with up to
+//                  32 rows of x per workgroup (MFMA, the same instruction).
 //   tiled_gemm     more rows (prefill): the LDS-tiled MFMA GEMM of
 //                  tiled_gemm.h with int8 weights kept int8 in LDS and widened
 //                  after each LDS read, scale and bias in its epilogue.
@@ -545,6 +546,11 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
     return w8_stream_launch<T, TO, DUAL>(p, w8_stream_plan(p.rows, p.k, p.n, DUAL, cus), s);
   if (p.rows <= 16) return w8_skinny_shape<T, TO, 2, DUAL>(p, s, cus);
   if (small_tiles_pay(p.rows, p.n) && tiled_fits(p, DUAL)) return w8_tiled_small<T, TO, DUAL>(p, s);
+  // 17 - 32 rows where the small tiles do not pay: the stream kernel with 6
+  // or 8 x sets (1.5B down, 32 rows 20.6 -> 13.0 us; 7B down 44.4 -> 30.1;
+  // 0.5B down 12.6 -> 7.3; the int8 gate/up + SiLU-and-mul, 0.5B 9.7 -> 8.9).
+  if (p.rows <= 32 && x_fits && !wide_mid)
+    return w8_stream_launch<T, TO, DUAL>(p, w8_stream_plan(p.rows, p.k, p.n, DUAL, cus), s);
   if (p.rows <= 24) return w8_skinny_shape<T, TO, 3, DUAL>(p, s, cus);
   if (p.rows <= 32) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);
   // More rows: the tiled GEMM, except where 32-row skinny tiles with split K,

@@ -1,4 +1,4 @@
-// The W8A16 decode kernel (up to 16 rows of x): int8 weight streaming with
+// The W8A16 decode kernel (up to 32 rows of x): int8 weight streaming with
 // lane-coalesced loads, plus its launch plans.  Shared by the W8A16 linear and
 // the int8 gate/up + SiLU-and-mul launchers (w8a16.hip) and, with 16-bit
 // weights (template argument WB = 2, below), by the 16-bit gate/up +
@@ -32,9 +32,9 @@
 //   acc(x row m', weight row r') = sum_q D[4 m' + q][4 r' + q],
 // which lane 16 m' + 4 r' + q holds in its register q: each lane keeps its own
 // register l % 4 and a quad sum (two DPP adds, one fixed order) finishes it.
-// An x tile of up to 16 rows takes MT4 = ceil(rows / 4) A sets, so the MFMA
-// work is up to four times the minimum -- far below what the weight stream
-// leaves idle.
+// An x tile of up to 32 rows takes MT4 = stream_x_sets(rows) A sets
+// (ceil(rows / 4) up to 16 rows, then 6 or 8), so the MFMA work is up to
+// four times the minimum -- far below what the weight stream leaves idle.
 //
 // Decomposition.  A workgroup owns rpw <= 4 R4 consecutive weight rows and all
 // rows of x; its waves split the 256-byte chunks of K into contiguous ranges
@@ -103,17 +103,28 @@ struct StreamPlan {
 // the 16-bit linear, out = acc + bias).  A lane's 16-byte weight load is then
 // 8 k, one B operand as loaded, a chunk of a weight row's 256 bytes is 128 k,
 // and one 16-byte x load per 4-row x set matches it.
-// Most threads per workgroup of w8a16_stream<R4, MT4, U, DUAL, WB>: 1024 (16
-// waves, 128 VGPRs per lane) while its accumulators and the registers its
-// loads keep in flight come to less than 112 VGPRs (4 per 16x16 accumulator
-// tile, NQ * R4 * MT4 of them; per chunk in flight 4 per weight set and 8
-// -- 4 with 16-bit weights -- per x set), else 512 (8 waves, 256 VGPRs):
-// the shapes at or above that estimate spilled 16 - 432 B per lane under the
-// 128-register budget (hipcc -Rpass-analysis=kernel-resource-usage).
-constexpr int stream_max_threads(int r4, int mt4, int u, bool dual, int wb) {
+// Registers w8a16_stream<R4, MT4, U, DUAL, WB> keeps live per lane, as an
+// estimate: 4 per 16x16 accumulator tile (NQ * R4 * MT4 of them), per chunk
+// in flight 4 per weight set and 8 -- 4 with 16-bit weights -- per x set,
+// and one load offset per weight set and per x set.
+constexpr int stream_regs(int r4, int mt4, int u, bool dual, int wb) {
   const int nq = dual ? 2 : 1;
-  return 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (wb == 1 ? 8 : 4) * mt4) >= 112 ? 512 : 1024;
+  return 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (wb == 1 ? 8 : 4) * mt4) + r4 + mt4;
 }
+
+// Most threads per workgroup of that instantiation: 1024 (16 waves, 128
+// VGPRs per lane) below 112 estimated registers, else 512 (8 waves, 256
+// VGPRs), and 0 -- no such kernel -- above 224: the shapes at or above 112
+// spilled 8 - 432 B per lane under the 128-register budget, those above 224
+// spilled under 256 (hipcc -Rpass-analysis=kernel-resource-usage).
+constexpr int stream_max_threads(int r4, int mt4, int u, bool dual, int wb) {
+  const int e = stream_regs(r4, mt4, u, dual, wb);
+  return e > 224 ? 0 : (e >= 112 ? 512 : 1024);
+}
+
+// 4-row x sets (MT4) for `rows` of x: ceil(rows / 4) up to 16 rows, then 6
+// (17 - 24 rows) or 8 (25 - 32); x rows past `rows` read zeros.
+constexpr int stream_x_sets(int rows) { return rows <= 16 ? (rows + 3) / 4 : (rows <= 24 ? 6 : 8); }
 
 template <typename T, typename TO, int R4, int MT4, int U, bool DUAL, int WB = 1>
 __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a16_stream(const W8Params p,
@@ -299,15 +310,20 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 // 8.69 us against 12.47 us for w8a16_skinny), 16 rows at k >= 3072 as above
 // (7B down, 16 rows 20.5 - 21.7 us against 27.0 for 8-row workgroups; 7B
 // gate/up 20.6 vs 22.9 us for w8a16_skinny, its dual form 33.4 vs 36.2).
+// 17 - 32 rows (6 or 8 x sets; bench.py --only stream-sweep32, 20, 24 and
+// 32 rows, where the launchers' small tiled shapes do not pay): the same,
+// with 7 waves per CU for 16-row workgroups and at most 8 weight rows per
+// workgroup for the dual kernel (1.5B down, 32 rows 12.95 us against 20.59
+// for w8a16_skinny; 7B down 30.1 vs 44.4; 0.5B down 7.29 vs 12.63).
 inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
   const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
-  const bool four_sets = rows > 8;  // three or four sets
+  const bool four_sets = rows > 8;  // three or more sets
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
   if (n <= 2048 || (n + 7) / 8 < cus) {
     sp.rpw = (n + cus - 1) / cus;
     sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
-  } else if (two_sets && k >= 3072) {
+  } else if (two_sets && k >= 3072 && !(dual && rows > 16)) {
     sp.rpw = 16;
   }
   if (dual && sp.rpw < 16) sp.rpw = two_sets ? 8 : 4;
@@ -319,11 +335,11 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
     waves = sp.rpw == 16 ? 1 : (two_sets ? 2 : 3);
     min_waves = sp.rpw == 16 ? 1 : 2;
   } else {
-    const int per_cu = sp.rpw == 16 ? (four_sets ? 6 : 7)
+    const int per_cu = sp.rpw == 16 ? (four_sets && rows <= 16 ? 6 : 7)
                                     : (four_sets ? (wgs <= cus ? 8 : 5) : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
   }
-  const int max_waves = stream_max_threads(sp.r4, (rows + 3) / 4, sp.u, dual, 1) / 64;
+  const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, 1) / 64;
   if (waves > max_waves) waves = max_waves;
   if (waves > nchunk) waves = nchunk;
   if (waves < min_waves) waves = nchunk < min_waves ? nchunk : min_waves;
@@ -347,12 +363,13 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
 // and one wave (7B, 16 rows 46.1 vs 50.3 us for 8 rows and 8 waves).
 inline StreamPlan gu16_stream_plan(int rows, int k) {
   StreamPlan sp{16, 4, 8, 1};
-  if (rows > 8) sp = k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{16, 4, 1, 1};
+  if (rows > 16) sp = StreamPlan{8, 2, 2, 1};  // 17 - 32 rows: 0.5B, 32 rows 9.04 us vs 10.52 for skinny tiles
+  else if (rows > 8) sp = k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{16, 4, 1, 1};
   else if (k <= 2048) sp = StreamPlan{4, 1, 2, 2};
   else if (rows <= 4) sp = StreamPlan{4, 1, 8, 2};
   const int nchunk = (k + 127) / 128;  // no more waves than 128-column chunks
   if (sp.waves > nchunk) sp.waves = nchunk;
-  const int max_waves = stream_max_threads(sp.r4, (rows + 3) / 4, sp.u, true, 2) / 64;
+  const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, true, 2) / 64;
   if (sp.waves > max_waves) sp.waves = max_waves;
   return sp;
 }
@@ -384,7 +401,7 @@ inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
   if (per_cu > 0) {
     int64_t waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
     const int nchunk = (k + 127) / 128;
-    const int max_waves = stream_max_threads(sp.r4, (rows + 3) / 4, sp.u, false, 2) / 64;
+    const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, false, 2) / 64;
     if (waves > max_waves) waves = max_waves;
     if (waves > nchunk) waves = nchunk;
     if (waves < 1) waves = 1;
@@ -394,18 +411,23 @@ inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
   return sp;
 }
 
-// Launches w8a16_stream with plan `sp` (rows <= 16; k, qs multiples of 16 --
+// Launches w8a16_stream with plan `sp` (rows <= 32; k, qs multiples of 16 --
 // of 8 for 16-bit weights --, xs a multiple of 8, x and the weights 16-byte
 // aligned: the callers check these).
 template <typename T, typename TO, bool DUAL, int WB = 1>
 int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   constexpr int NQ = DUAL ? 2 : 1;
-  const int mt4 = (p.rows + 3) / 4;  // 4-row x sets: 1 .. 4
-  if (mt4 > 2 && sp.u > 1) {
-    set_error("w8a16 stream launch: more than 8 rows of x take one chunk in flight (u %d)", sp.u);
+  const int mt4 = stream_x_sets(p.rows);  // 4-row x sets: 1 .. 4, 6, 8
+  if (p.rows < 1 || p.rows > 32 || (mt4 > 2 && sp.u > 1)) {
+    set_error("w8a16 stream launch: %d rows of x (1 - 32; more than 8 take one chunk in flight, u %d)", p.rows,
+              sp.u);
     return MI355_ERR_UNSUPPORTED;
   }
   const int max_threads = stream_max_threads(sp.r4 >= 4 ? 4 : sp.r4, mt4, sp.u >= 2 ? 2 : 1, DUAL, WB);
+  if (max_threads == 0) {
+    set_error("w8a16 stream launch: no kernel for %d rows of x with %d weight rows per workgroup", p.rows, sp.rpw);
+    return MI355_ERR_UNSUPPORTED;
+  }
   if (sp.waves < 1 || 64 * sp.waves > max_threads) {
     set_error("w8a16 stream launch: %d waves per workgroup, this shape takes 1 - %d", sp.waves, max_threads / 64);
     return MI355_ERR_UNSUPPORTED;
@@ -423,15 +445,29 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   // three or four x sets: one chunk in flight
 #define MI355_W8S_MT4(R4) \
   if (mt4 == 3) { MI355_W8S(R4, 3, 1); } else { MI355_W8S(R4, 4, 1); }
+  // six or eight x sets: one chunk in flight, and only the shapes whose
+  // registers fit (stream_max_threads > 0; the others were rejected above)
+#define MI355_W8S_IF(R4, MT4) \
+  if constexpr (stream_max_threads(R4, MT4, 1, DUAL, WB) > 0) MI355_W8S(R4, MT4, 1);
+#define MI355_W8S_MT8(R4) \
+  if (mt4 == 6) { MI355_W8S_IF(R4, 6) } else { MI355_W8S_IF(R4, 8) }
   if (mt4 <= 2) {
     if (sp.r4 >= 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
-  } else {
+  } else if (mt4 <= 4) {
     if (sp.r4 >= 4) { MI355_W8S_MT4(4) } else if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
+  } else {
+    if (sp.r4 >= 4) { MI355_W8S_MT8(4) } else if (sp.r4 == 2) { MI355_W8S_MT8(2) } else { MI355_W8S_MT8(1) }
   }
+#undef MI355_W8S_MT8
+#undef MI355_W8S_IF
 #undef MI355_W8S_MT4
 #undef MI355_W8S_MT
 #undef MI355_W8S_U
 #undef MI355_W8S
+  if (!kern) {
+    set_error("w8a16 stream launch: no kernel for %d rows of x with %d weight rows per workgroup", p.rows, sp.rpw);
+    return MI355_ERR_UNSUPPORTED;
+  }
   return hip_status(hipLaunchKernel(kern, grid, block, args, lds, s), "w8a16 stream launch");
 }
 

@@ -76,7 +76,7 @@ def _check_vs_oracle(orc, got16, got32, x, wg, wu, dt):
     # ragged weight-row counts
     (6, 3584, 1000, BF16), (7, 136, 520, F16), (2, 2056, 264, F16), (8, 2048, 4099, BF16), (1, 24, 1, F16),
     (12, 1536, 8960, F16), (13, 136, 1000, BF16), (16, 3584, 2000, F16), (9, 2056, 37, BF16),
-    (11, 3104, 2900, BF16),
+    (11, 3104, 2900, BF16), (32, 896, 4864, BF16), (21, 3104, 2900, F16),
     (17, 2048, 1000, F16),
     # prefill rows: the tiled GEMM (each of its three launch shapes, k tails, ragged edges)
     (64, 1536, 1000, F16), (200, 640, 10240, BF16), (300, 1552, 520, F16), (257, 96, 333, BF16),

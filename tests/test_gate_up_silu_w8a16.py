@@ -70,6 +70,8 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
     # workgroups, one wave; a partial last chunk and a ragged last workgroup at k 3104 x n 2900)
     (12, 1536, 8960, F16), (13, 272, 1000, BF16), (16, 1552, 520, F16), (16, 3584, 18944, BF16),
     (12, 3584, 18944, BF16), (10, 3104, 2900, F16), (6, 3104, 2900, BF16), (15, 3104, 2900, BF16),
+    # 17 - 32 rows where the small tiled shapes do not pay: the stream kernel with 6 and 8 x sets
+    (20, 896, 4864, F16), (32, 3104, 2900, BF16), (25, 1552, 520, F16),
     # prefill rows: the dual tiled GEMM (and the skinny tiles of small grids)
     (33, 256, 100, BF16), (64, 1536, 1000, F16), (200, 640, 10240, F16), (300, 1552, 520, BF16),
     (1024, 1536, 2048, F16),

@@ -2,7 +2,7 @@
 (``w8_stream_plan``, ``l16_stream_plan`` and ``gu16_stream_plan`` in
 csrc/w8a16_stream.h, reached
 through the probe library's plan exports; no GPU call): every plan the
-launchers can produce for 1 - 16 rows must be one the launcher accepts --
+launchers can produce for 1 - 32 rows must be one the launcher accepts --
 at most the kernel's thread limit (16 waves, 8 where its registers need
 more room) and no more waves than 256-byte chunks, rows per workgroup
 within its 4-row sets, and for more than 8 rows of x one chunk in flight
@@ -44,8 +44,8 @@ def _check(plan, rows, kbytes, nq, lib, wb=1):
     assert r4 in (1, 2, 4) and 1 <= rpw <= 4 * r4, plan
     assert 1 <= waves <= 16 and waves <= max(1, nchunk), (plan, nchunk)
     assert u in (1, 2), plan
-    mt4 = -(-rows // 4)
-    if mt4 > 2:  # one chunk in flight with three or four x sets
+    mt4 = -(-rows // 4) if rows <= 16 else (6 if rows <= 24 else 8)  # stream_x_sets
+    if mt4 > 2:  # one chunk in flight with three or more x sets
         assert u == 1, (rows, plan)
     assert 64 * waves <= lib.mi355_probe_stream_max_threads(r4, mt4, u, nq - 1, wb), (rows, plan)
     assert waves * nq * r4 * mt4 * 16 * 4 <= 64 * 1024
@@ -58,7 +58,7 @@ NS = (1, 7, 37, 256, 896, 1000, 1536, 2048, 3584, 4864, 8960, 18944, 29568, 6553
 @pytest.mark.parametrize("cus", [80, 256, 304])
 def test_w8a16_plan_is_launchable(probe, cus):
     out = (ctypes.c_int * 4)()
-    for rows, k, n, dual in itertools.product(range(1, 17), KS, NS, (0, 1)):
+    for rows, k, n, dual in itertools.product(range(1, 33), KS, NS, (0, 1)):
         probe.mi355_probe_w8a16_stream_plan(rows, k, n, dual, cus, out)
         _check(tuple(out), rows, k, 2 if dual else 1, probe)
 
@@ -66,14 +66,14 @@ def test_w8a16_plan_is_launchable(probe, cus):
 @pytest.mark.parametrize("cus", [80, 256, 304])
 def test_linear16_plan_is_launchable(probe, cus):
     out = (ctypes.c_int * 4)()
-    for rows, k, n in itertools.product(range(1, 17), (8, 24, 136, 896, 1536, 2056, 3584, 8960, 18944), NS):
+    for rows, k, n in itertools.product(range(1, 33), (8, 24, 136, 896, 1536, 2056, 3584, 8960, 18944), NS):
         probe.mi355_probe_linear16_stream_plan(rows, k, n, cus, out)
         _check(tuple(out), rows, 2 * k, 1, probe, wb=2)
 
 
 def test_gate_up16_plan_is_launchable(probe):
     out = (ctypes.c_int * 4)()
-    for rows, k in itertools.product(range(1, 17), (8, 24, 136, 896, 1536, 2048, 2056, 3584, 8192)):
+    for rows, k in itertools.product(range(1, 33), (8, 24, 136, 896, 1536, 2048, 2056, 3584, 8192)):
         probe.mi355_probe_gate_up16_stream_plan(rows, k, out)
         _check(tuple(out), rows, 2 * k, 2, probe, wb=2)
 
@@ -82,9 +82,11 @@ def test_thread_limit_matches_the_bench_sweep(probe, bench):
     """bench.py's sweep samples only launch shapes the kernel takes: its
     stream_max_waves is the kernel's own thread limit / 64, and the limit
     drops to 512 exactly where the register estimate reaches 112."""
-    for r4, mt4, u, dual, wb in itertools.product((1, 2, 4), (1, 2, 3, 4), (1, 2), (0, 1), (1, 2)):
+    for r4, mt4, u, dual, wb in itertools.product((1, 2, 4), (1, 2, 3, 4, 6, 8), (1, 2), (0, 1), (1, 2)):
         lim = probe.mi355_probe_stream_max_threads(r4, mt4, u, dual, wb)
-        assert lim in (512, 1024)
+        assert lim in (0, 512, 1024)
+        if mt4 <= 4 and u == 1:  # every shape up to 16 rows with one chunk in flight has a kernel
+            assert lim > 0, (r4, mt4, dual, wb)
         assert bench.stream_max_waves(r4, mt4, u, bool(dual), wb) == lim // 64, (r4, mt4, u, dual, wb)
     # the shapes that spilled under 128 VGPRs take 512 threads; those in use
     # without spills keep 1024

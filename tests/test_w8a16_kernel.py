@@ -146,6 +146,10 @@ STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 0)
                  for m in (9, 12, 13, 16)
                  for K, N in ((8960, 1536), (1536, 8960), (272, 1000), (1552, 37), (3584, 10008))]
 STREAM_CASES += [(m, 3104, 2900, F16 if m % 2 else BF16, m % 2 == 1) for m in (9, 10, 11, 12)]
+# 17 - 32 rows where the small tiled shapes do not pay: 6 and 8 x sets
+STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 0)
+                 for m in (17, 24, 25, 32)
+                 for K, N in ((8960, 1536), (4864, 896), (3104, 2900), (1552, 37))]
 
 
 @pytest.mark.parametrize("M,K,N,dt,bias", STREAM_CASES)
