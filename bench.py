@@ -70,7 +70,7 @@ def parse_args():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--skip-e2e", action="store_true", help="no end-to-end before/after leg")
-    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "linear16-table", "silu-persist", "gate-up",
+    p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "linear16-table", "gate-up",
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
@@ -142,8 +142,6 @@ class Ctx:
             self.probe.mi355_probe_gate_up16_stream.restype = ctypes.c_int
             self.probe.mi355_probe_linear16_stream.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]
             self.probe.mi355_probe_linear16_stream.restype = ctypes.c_int
-            self.probe.mi355_probe_silu_persist.argtypes = [vp, vp, vp, ctypes.c_int64, i32, i32, i32, vp]
-            self.probe.mi355_probe_silu_persist.restype = ctypes.c_int
 
     def check(self, fn, st):
         if st:
@@ -339,17 +337,6 @@ class Ctx:
         def call():
             if f(*args, self.stream):
                 raise RuntimeError(f"probe linear16 stream failed for {args[4:]}")
-        return call
-
-    def silu_persist_call(self, g, u, o, grid, block, unroll):
-        """SiLU-and-mul (fp16) on the probe's persistent grid
-        (csrc/probe/silu_persist.hip)."""
-        f = self.probe.mi355_probe_silu_persist
-        args = (g.data_ptr(), u.data_ptr(), o.data_ptr(), g.numel(), grid, block, unroll)
-
-        def call():
-            if f(*args, self.stream):
-                raise RuntimeError(f"probe silu persist failed for {args[3:]}")
         return call
 
     def add2_call(self, a, b, dst):
@@ -942,8 +929,6 @@ def run_only(ctx, args, sets):
     elif args.only == "c1-rms":
         us = time_loop(ctx, [s[0] for s in sets], iters)
         log(f"c1-rms avg {us:.3f} us")
-    elif args.only == "silu-persist":  # C2 on persistent grids (probe) against the one-shot library kernel
-        print(json.dumps({"silu_persist": silu_persist_sweep(ctx, sets, iters)}), flush=True)
     elif args.only == "c1-add-rms":
         del sets
         torch.cuda.empty_cache()
@@ -2064,47 +2049,6 @@ def bench_prefill_core(ctx, shapes=((1024, 1536, 8960), (1024, 8960, 1536), (409
         del qs, sc, calls, outs
         torch.cuda.empty_cache()
     return res
-
-
-def silu_persist_sweep(ctx, sets, iters, rounds=3):
-    """C2 SiLU-and-mul [2048, 8960] fp16 on the headline's rotating buffer
-    sets: the library's one-shot grid (silu_mul_chunks) against the probe's
-    persistent grid (workgroups per CU x lanes x packets per lane per step)
-    and the same-size add2 probe, HIP events over back-to-back launches,
-    interleaved rounds, min per variant; every persistent variant's output
-    checked bit for bit against the library's."""
-    torch = ctx.torch
-    cus = torch.cuda.get_device_properties(ctx.dev).multi_processor_count
-    tens = [t for _, _, t in sets]
-    lib = [s_ for _, s_, _ in sets]
-    variants = {"library": lib}
-    if ctx.probe is not None:
-        variants["add2_probe"] = [ctx.add2_call(g, u, o) for _, _, g, u, o in tens]
-    ref = torch.empty_like(tens[0][4])
-    ctx.silu_call(tens[0][2], tens[0][3], ref)()
-    torch.cuda.synchronize()
-    bad = []
-    for wpc in (1, 2, 4, 8):
-        for block in (256, 512):
-            for unroll in (1, 2, 4):
-                if block * wpc > 2048:
-                    continue
-                key = f"persist_wpc{wpc}_b{block}_u{unroll}"
-                variants[key] = [ctx.silu_persist_call(g, u, o, wpc * cus, block, unroll) for _, _, g, u, o in tens]
-                variants[key][0]()
-                torch.cuda.synchronize()
-                if not torch.equal(tens[0][4], ref):
-                    bad.append(key)
-    res = {k: [] for k in variants}
-    for _ in range(rounds):
-        for k, calls in variants.items():
-            spin_up(ctx, calls, ms=2.0)
-            res[k].append(time_loop(ctx, calls, iters))
-    out = {k: round(min(v), 3) for k, v in res.items()}
-    best = min((k for k in out if k.startswith("persist")), key=lambda k: out[k])
-    log(f"  silu persist: library {out['library']} us, add2 probe {out.get('add2_probe')} us, "
-        f"best {best} {out[best]} us, {len(bad)} mismatches {bad[:3]}")
-    return {"us": out, "best": best, "mismatches": bad}
 
 
 def bench_copy(ctx, nbytes=1 << 30, iters=30):
