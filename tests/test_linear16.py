@@ -170,8 +170,8 @@ def test_abi_rejects_bad_arguments(pkg, cuda):
         pkg.linear16(x, w.to(BF16))
 
 
-def test_graph_replays_match_eager(pkg, cuda):
-    rows, k, n = 8, 8960, 1536
+@pytest.mark.parametrize("rows,k,n", [(8, 8960, 1536), (32, 8960, 1536), (13, 18944, 3584)])
+def test_graph_replays_match_eager(pkg, cuda, rows, k, n):
     x, w, b = (t.to(cuda) for t in _inputs(rows, k, n, F16, seed=11, bias_dt=F32))
     xs = x.clone()
     s = torch.cuda.Stream()

@@ -364,9 +364,10 @@ def test_out_row_stride_through_abi(pkg, cuda, M):
     assert torch.all(out[:, N:] == 7.0)
 
 
-@pytest.mark.parametrize("M", [8, 16, 100])
-def test_graph_replays_match_eager(pkg, cuda, M):
-    K, N = 1536, 8960
+@pytest.mark.parametrize("M,K,N", [(8, 1536, 8960), (16, 1536, 8960), (100, 1536, 8960),
+                                   # 17 - 32 rows on the stream kernel (6 and 8 x sets)
+                                   (32, 8960, 1536), (20, 4864, 896)])
+def test_graph_replays_match_eager(pkg, cuda, M, K, N):
     lin = _linear(K, N, False, cuda, seed=15)
     q = pkg.QuantizedLinearInt8.from_linear(lin)
     x = _x(M, K, F16, cuda, seed=16)
