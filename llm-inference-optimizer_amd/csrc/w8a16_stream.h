@@ -103,6 +103,7 @@ struct StreamPlan {
 // the 16-bit linear, out = acc + bias).  A lane's 16-byte weight load is then
 // 8 k, one B operand as loaded, a chunk of a weight row's 256 bytes is 128 k,
 // and one 16-byte x load per 4-row x set matches it.
+//
 // Registers w8a16_stream<R4, MT4, U, DUAL, WB> keeps live per lane, as an
 // estimate: 4 per 16x16 accumulator tile (NQ * R4 * MT4 of them), per chunk
 // in flight 4 per weight set and 8 -- 4 with 16-bit weights -- per x set,
@@ -423,7 +424,11 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
               sp.u);
     return MI355_ERR_UNSUPPORTED;
   }
-  const int max_threads = stream_max_threads(sp.r4 >= 4 ? 4 : sp.r4, mt4, sp.u >= 2 ? 2 : 1, DUAL, WB);
+  if ((sp.r4 != 1 && sp.r4 != 2 && sp.r4 != 4) || sp.rpw < 1 || sp.rpw > 4 * sp.r4) {
+    set_error("w8a16 stream launch: %d weight rows per workgroup in %d 4-row sets (1, 2 or 4)", sp.rpw, sp.r4);
+    return MI355_ERR_UNSUPPORTED;
+  }
+  const int max_threads = stream_max_threads(sp.r4, mt4, sp.u >= 2 ? 2 : 1, DUAL, WB);
   if (max_threads == 0) {
     set_error("w8a16 stream launch: no kernel for %d rows of x with %d weight rows per workgroup", p.rows, sp.rpw);
     return MI355_ERR_UNSUPPORTED;
@@ -452,11 +457,11 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
 #define MI355_W8S_MT8(R4) \
   if (mt4 == 6) { MI355_W8S_IF(R4, 6) } else { MI355_W8S_IF(R4, 8) }
   if (mt4 <= 2) {
-    if (sp.r4 >= 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
+    if (sp.r4 == 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
   } else if (mt4 <= 4) {
-    if (sp.r4 >= 4) { MI355_W8S_MT4(4) } else if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
+    if (sp.r4 == 4) { MI355_W8S_MT4(4) } else if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
   } else {
-    if (sp.r4 >= 4) { MI355_W8S_MT8(4) } else if (sp.r4 == 2) { MI355_W8S_MT8(2) } else { MI355_W8S_MT8(1) }
+    if (sp.r4 == 4) { MI355_W8S_MT8(4) } else if (sp.r4 == 2) { MI355_W8S_MT8(2) } else { MI355_W8S_MT8(1) }
   }
 #undef MI355_W8S_MT8
 #undef MI355_W8S_IF
