@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "l16-stream-sweep", "stream-sweep32", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -134,6 +134,7 @@ class Ctx:
                                                             i32, vp]
             self.probe.mi355_probe_w8a16_stream.restype = ctypes.c_int
             self.probe.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
+            self.probe.mi355_probe_linear16_stream_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(i32)]
             self.probe.mi355_probe_w8a16_stream_plan.restype = None
             self.probe.mi355_probe_w8a16_stream_loads.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                                                   vp, vp]
@@ -284,6 +285,12 @@ class Ctx:
         same source the library compiles."""
         out4 = (ctypes.c_int * 4)()
         self.probe.mi355_probe_w8a16_stream_plan(rows, k, n, int(dual), cus, out4)
+        return tuple(out4)
+
+    def l16_stream_plan(self, rows, k, n, cus):
+        """The 16-bit linear's stream launch plan (rpw, r4, waves, u)."""
+        out4 = (ctypes.c_int * 4)()
+        self.probe.mi355_probe_linear16_stream_plan(rows, k, n, cus, out4)
         return tuple(out4)
 
     def w8_stream_loads_call(self, x, q, sink, rpw, r4, waves, u, with_x):
@@ -1033,6 +1040,11 @@ def run_only(ctx, args, sets):
         print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP32_SHAPES, True),
                           "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP32_SHAPES),
                           "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP32_SHAPES, True)}), flush=True)
+    elif args.only == "stream-sweep64":  # 33 - 64 rows of the narrow projections
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP64_SHAPES, True),
+                          "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP64_SHAPES)}), flush=True)
     elif args.only == "l16-stream-sweep":  # the 16-bit linear on the weight-streaming kernel
         del sets
         torch.cuda.empty_cache()
@@ -1303,8 +1315,10 @@ def stream_max_waves(r4, mt4, u, dual, wb=1):
 
 def stream_x_sets(rows):
     """4-row x sets of the decode stream kernel (stream_x_sets of
-    csrc/w8a16_stream.h): ceil(rows / 4) up to 16 rows, then 6 or 8."""
-    return -(-rows // 4) if rows <= 16 else (6 if rows <= 24 else 8)
+    csrc/w8a16_stream.h): ceil(rows / 4) up to 16 rows, then 6, 8, 12 or 16."""
+    if rows <= 16:
+        return -(-rows // 4)
+    return 6 if rows <= 24 else (8 if rows <= 32 else (12 if rows <= 48 else 16))
 
 
 def _w8_stream_shapes(nchunk, dual, mt4, wide16=False, wb=1):
@@ -1361,6 +1375,15 @@ W8_STREAM_SWEEP32_SHAPES = [("down_M24", 24, 8960, 1536, False), ("down_M32", 32
                             ("gateup0.5b_M32", 32, 896, 4864, False), ("down0.5b_M32", 32, 4864, 896, False),
                             ("dual0.5b_M32", 32, 896, 4864, True), ("o7b_M32", 32, 3584, 3584, False),
                             ("down_M20", 20, 8960, 1536, False)]
+# 33 - 64 rows (12 and 16 x sets) of the narrow projections
+W8_STREAM_SWEEP64_SHAPES = [("down_M48", 48, 8960, 1536, False), ("down_M64", 64, 8960, 1536, False),
+                            ("down7b_M64", 64, 18944, 3584, False), ("o1.5b_M64", 64, 1536, 1536, False),
+                            ("down0.5b_M64", 64, 4864, 896, False), ("down7b_M48", 48, 18944, 3584, False),
+                            ("o7b_M48", 48, 3584, 3584, False), ("down_M40", 40, 8960, 1536, False),
+                            ("down0.5b_M48", 48, 4864, 896, False), ("dual0.5b_M48", 48, 896, 4864, True)]
+L16_SWEEP64_SHAPES = [("down1.5b_M64", 64, 8960, 1536), ("down7b_M48", 48, 18944, 3584),
+                      ("down7b_M64", 64, 18944, 3584), ("o7b_M64", 64, 3584, 3584), ("down1.5b_M48", 48, 8960, 1536),
+                      ("down0.5b_M64", 64, 4864, 896), ("o1.5b_M64", 64, 1536, 1536)]
 GU16_SWEEP32_SHAPES = [("gu1.5b_M32", 32, 1536, 8960), ("gu7b_M32", 32, 3584, 18944), ("gu0.5b_M32", 32, 896, 4864)]
 L16_SWEEP32_SHAPES = [("down1.5b_M24", 24, 8960, 1536), ("down1.5b_M32", 32, 8960, 1536),
                       ("down7b_M32", 32, 18944, 3584), ("down0.5b_M32", 32, 4864, 896), ("o7b_M32", 32, 3584, 3584)]
@@ -1464,6 +1487,7 @@ def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
     (within 2e-3 of the largest output)."""
     torch = ctx.torch
     F16 = torch.float16
+    cus = torch.cuda.get_device_properties(ctx.dev).multi_processor_count
     out = {}
     for label, M, K, N in shapes:
         sets = n_sets(N * K * 2)
@@ -1490,10 +1514,12 @@ def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
         spin_up(ctx, lib_calls, ms=5.0)
         res["library_us"] = round(time_graph(ctx, lib_calls, nodes, replays=5), 3)
         best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
-        out[label] = {"best": best, "best_us": res[best], "library_us": res["library_us"], "mismatches": bad,
-                      "shapes": res}
-        log(f"  l16 stream sweep {label}: library {res['library_us']} us, best {best} {res[best]} us, "
-            f"{len(bad)} mismatches {bad[:3]}")
+        prpw, _, pwaves, pu = ctx.l16_stream_plan(M, K, N, cus)
+        plan = f"rpw{prpw}_w{pwaves}_u{pu}"
+        out[label] = {"best": best, "best_us": res[best], "plan": plan, "plan_us": res.get(plan),
+                      "library_us": res["library_us"], "mismatches": bad, "shapes": res}
+        log(f"  l16 stream sweep {label}: library {res['library_us']} us, plan {plan} {res.get(plan)} us, "
+            f"best {best} {res[best]} us, {len(bad)} mismatches {bad[:3]}")
         del ws
         torch.cuda.empty_cache()
     return out

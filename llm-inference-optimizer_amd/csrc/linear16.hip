@@ -13,7 +13,7 @@
 //
 // Four kernels, picked by the launcher:
 //   w8a16_stream      rows <= 16 (decode; w8a16_stream.h with one 16-bit
-//                     matrix), and 17 - 32 where the small tiled shapes do not
+//                     matrix), and 17 - 64 where the small tiled shapes do not
 //                     pay: lane-coalesced weight streaming, every weight byte
 //                     read once per call, MFMA (v_mfma_f32_16x16x32_*).
 //   linear16_skinny   inputs the stream kernel's descriptors cannot span, and
@@ -322,14 +322,15 @@ int l16_typed(const L16Params& p, hipStream_t s, int cus) {
     const int64_t waves = static_cast<int64_t>(p.n) * ((p.rows + kGenRows - 1) / kGenRows);
     return launch_l16(linear16_generic<T, TO>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, p, s);
   }
-  // Up to 16 rows, and 17 - 32 where the small tiled shapes below do not
+  // Up to 16 rows, and 17 - 64 where the small tiled shapes below do not
   // pay: the weight-streaming kernel of w8a16_stream.h with one 16-bit
   // matrix, whose x descriptor spans all rows of x and each workgroup's
   // weight descriptor up to 16 weight rows (both under 2^32 bytes); else the
-  // skinny kernel (1.5B down, 32 rows 22.1 -> 14.4 us on the stream kernel;
-  // 7B down 51.9 -> 37.3; 0.5B down 13.2 -> 7.9).
+  // skinny kernel (1.5B down, 32 rows 22.1 -> 14.4 us on the stream kernel,
+  // 64 rows 43.7 -> 22.2 against the small tiles; 7B down 51.9 -> 37.3 at
+  // 32 rows, 90.3 -> 83.1 at 64; 0.5B down 13.2 -> 7.9 at 32 rows).
   const int64_t tb = sizeof(typename T::bits);
-  const bool stream_fits = p.rows <= 32 && ((p.rows - 1) * p.xs + p.k) * tb < (int64_t{1} << 32) &&
+  const bool stream_fits = p.rows <= 64 && ((p.rows - 1) * p.xs + p.k) * tb < (int64_t{1} << 32) &&
                            (15 * p.ws + p.k) * tb < (int64_t{1} << 32);
   const W8Params w{p.x, p.w, nullptr, p.bias, p.out, p.rows, p.k, p.n, p.xs, p.ws, p.os, MI355_F32, p.bdt,
                    nullptr, nullptr};
@@ -339,7 +340,7 @@ int l16_typed(const L16Params& p, hipStream_t s, int cus) {
   if (p.rows <= 16) return l16_skinny_shape<T, TO, 2>(p, s, cus);
   if (p.rows <= 64 && l16_tiled_fits(p)) {
     const int bn = (p.rows <= 32 && p.n > 10000) ? 128 : 64;
-    if (p.rows > 32 || (p.n + bn - 1) / bn >= 128) return l16_tiled_small<T, TO>(p, s);
+    if ((p.n + bn - 1) / bn >= 128 || (p.rows > 32 && !stream_fits)) return l16_tiled_small<T, TO>(p, s);
   }
   if (stream_fits) return w8_stream_launch<T, TO, false, 2>(w, l16_stream_plan(p.rows, p.k, p.n, cus), s);
   if (p.rows <= 24) return l16_skinny_shape<T, TO, 3>(p, s, cus);

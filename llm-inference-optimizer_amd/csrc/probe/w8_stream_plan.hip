@@ -126,7 +126,7 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_l
 namespace {
 
 // The decode kernel at any launch shape the probes accept: R4 in {1, 2, 4},
-// MT4 = stream_x_sets(rows) in 1 .. 4, 6, 8 (32 rows of x), U in {1, 2}
+// MT4 = stream_x_sets(rows) in 1 .. 4, 6, 8, 12, 16 (64 rows of x), U in {1, 2}
 // (U = 1 only for MT4 > 2); fp16 x, weights of WB bytes.
 template <bool DUAL, int WB, int R4, int MT4>
 const void* sk_u(int u) {
@@ -145,7 +145,9 @@ const void* sk_mt(int mt4, int u) {
   if (mt4 == 3) return sk_u<DUAL, WB, R4, 3>(u);
   if (mt4 == 4) return sk_u<DUAL, WB, R4, 4>(u);
   if (mt4 == 6) return sk_u<DUAL, WB, R4, 6>(u);
-  return sk_u<DUAL, WB, R4, 8>(u);
+  if (mt4 == 8) return sk_u<DUAL, WB, R4, 8>(u);
+  if (mt4 == 12) return sk_u<DUAL, WB, R4, 12>(u);
+  return sk_u<DUAL, WB, R4, 16>(u);
 }
 template <bool DUAL, int WB>
 const void* stream_kernel(int r4, int mt4, int u) {
@@ -156,7 +158,7 @@ const void* stream_kernel(int r4, int mt4, int u) {
 
 bool shape_ok(int rows, int n, int rpw, int r4, int waves, int u, bool dual, int wb) {
   const int mt4 = mi355::stream_x_sets(rows);
-  return rows >= 1 && rows <= 32 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4) && rpw <= 4 * r4 &&
+  return rows >= 1 && rows <= 64 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4) && rpw <= 4 * r4 &&
          waves >= 1 && 64 * waves <= mi355::stream_max_threads(r4, mt4, u, dual, wb) &&
          (u == 1 || (u == 2 && mt4 <= 2));
 }

@@ -1,4 +1,4 @@
-// The W8A16 decode kernel (up to 32 rows of x): int8 weight streaming with
+// The W8A16 decode kernel (up to 64 rows of x): int8 weight streaming with
 // lane-coalesced loads, plus its launch plans.  Shared by the W8A16 linear and
 // the int8 gate/up + SiLU-and-mul launchers (w8a16.hip) and, with 16-bit
 // weights (template argument WB = 2, below), by the 16-bit gate/up +
@@ -32,9 +32,10 @@
 //   acc(x row m', weight row r') = sum_q D[4 m' + q][4 r' + q],
 // which lane 16 m' + 4 r' + q holds in its register q: each lane keeps its own
 // register l % 4 and a quad sum (two DPP adds, one fixed order) finishes it.
-// An x tile of up to 32 rows takes MT4 = stream_x_sets(rows) A sets
-// (ceil(rows / 4) up to 16 rows, then 6 or 8), so the MFMA work is up to
-// four times the minimum -- far below what the weight stream leaves idle.
+// An x tile of up to 64 rows takes MT4 = stream_x_sets(rows) A sets
+// (ceil(rows / 4) up to 16 rows, then 6, 8, 12 or 16), so the MFMA work is
+// up to four times the minimum -- far below what the weight stream leaves
+// idle.
 //
 // Decomposition.  A workgroup owns rpw <= 4 R4 consecutive weight rows and all
 // rows of x; its waves split the 256-byte chunks of K into contiguous ranges
@@ -124,8 +125,11 @@ constexpr int stream_max_threads(int r4, int mt4, int u, bool dual, int wb) {
 }
 
 // 4-row x sets (MT4) for `rows` of x: ceil(rows / 4) up to 16 rows, then 6
-// (17 - 24 rows) or 8 (25 - 32); x rows past `rows` read zeros.
-constexpr int stream_x_sets(int rows) { return rows <= 16 ? (rows + 3) / 4 : (rows <= 24 ? 6 : 8); }
+// (17 - 24 rows), 8 (25 - 32), 12 (33 - 48) or 16 (49 - 64); x rows past
+// `rows` read zeros.
+constexpr int stream_x_sets(int rows) {
+  return rows <= 16 ? (rows + 3) / 4 : (rows <= 24 ? 6 : (rows <= 32 ? 8 : (rows <= 48 ? 12 : 16)));
+}
 
 template <typename T, typename TO, int R4, int MT4, int U, bool DUAL, int WB = 1>
 __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a16_stream(const W8Params p,
@@ -316,7 +320,13 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 // with 7 waves per CU for 16-row workgroups and at most 8 weight rows per
 // workgroup for the dual kernel (1.5B down, 32 rows 12.95 us against 20.59
 // for w8a16_skinny; 7B down 30.1 vs 44.4; 0.5B down 7.29 vs 12.63).
-inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
+// 33 - 64 rows (12 or 16 x sets, one matrix; bench.py --only stream-sweep64):
+// the same, with as many 4-row weight sets as the registers of that many x
+// sets allow (16-bit weights: 2, int8 weights: 2 up to 48 rows, then 1), and
+// 7 waves per CU with more workgroups than CUs (7B down, 64 rows of 16-bit
+// weights: 4 waves 78.9 us, 3 waves 83.4).
+// `wb` is the weight element size the plan is for (k counts bytes).
+inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int wb = 1) {
   const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
   const bool four_sets = rows > 8;  // three or more sets
   const int nchunk = (k + 255) / 256;
@@ -329,6 +339,11 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
   }
   if (dual && sp.rpw < 16) sp.rpw = two_sets ? 8 : 4;
   sp.r4 = sp.rpw <= 4 ? 1 : (sp.rpw <= 8 ? 2 : 4);
+  // fewer 4-row weight sets where this many x sets leave no registers for more
+  while (sp.r4 > 1 && stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, wb) == 0) {
+    sp.r4 /= 2;
+    if (sp.rpw > 4 * sp.r4) sp.rpw = 4 * sp.r4;
+  }
   const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
   int64_t waves;
   int min_waves = 2;
@@ -337,10 +352,11 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus) {
     min_waves = sp.rpw == 16 ? 1 : 2;
   } else {
     const int per_cu = sp.rpw == 16 ? (four_sets && rows <= 16 ? 6 : 7)
-                                    : (four_sets ? (wgs <= cus ? 8 : 5) : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
+                                    : (four_sets ? (wgs <= cus ? 8 : (rows > 32 ? 7 : 5))
+                                                 : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
   }
-  const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, 1) / 64;
+  const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, wb) / 64;
   if (waves > max_waves) waves = max_waves;
   if (waves > nchunk) waves = nchunk;
   if (waves < min_waves) waves = nchunk < min_waves ? nchunk : min_waves;
@@ -390,7 +406,7 @@ inline StreamPlan gu16_stream_plan(int rows, int k) {
 // at the 1.5B down with 8 / 16 rows (now 7.76 / 9.94) and 27.37 / 35.41 us
 // at the 7B down (now 23.42 / 27.7).
 inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
-  StreamPlan sp = w8_stream_plan(rows, 2 * k, n, false, cus);
+  StreamPlan sp = w8_stream_plan(rows, 2 * k, n, false, cus, 2);
   const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
   int per_cu = 0;
   if (sp.rpw <= 8 && (n <= 2048 || (n + 7) / 8 < cus) && rows <= 8) {
@@ -412,16 +428,16 @@ inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
   return sp;
 }
 
-// Launches w8a16_stream with plan `sp` (rows <= 32; k, qs multiples of 16 --
-// of 8 for 16-bit weights --, xs a multiple of 8, x and the weights 16-byte
-// aligned: the callers check these).
+// Launches w8a16_stream with plan `sp` (rows <= 64, <= 32 when DUAL; k, qs
+// multiples of 16 -- of 8 for 16-bit weights --, xs a multiple of 8, x and
+// the weights 16-byte aligned: the callers check these).
 template <typename T, typename TO, bool DUAL, int WB = 1>
 int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   constexpr int NQ = DUAL ? 2 : 1;
-  const int mt4 = stream_x_sets(p.rows);  // 4-row x sets: 1 .. 4, 6, 8
-  if (p.rows < 1 || p.rows > 32 || (mt4 > 2 && sp.u > 1)) {
-    set_error("w8a16 stream launch: %d rows of x (1 - 32; more than 8 take one chunk in flight, u %d)", p.rows,
-              sp.u);
+  const int mt4 = stream_x_sets(p.rows);  // 4-row x sets: 1 .. 4, 6, 8, 12, 16
+  if (p.rows < 1 || p.rows > (DUAL ? 32 : 64) || (mt4 > 2 && sp.u > 1)) {
+    set_error("w8a16 stream launch: %d rows of x (1 - %d; more than 8 take one chunk in flight, u %d)", p.rows,
+              DUAL ? 32 : 64, sp.u);
     return MI355_ERR_UNSUPPORTED;
   }
   if ((sp.r4 != 1 && sp.r4 != 2 && sp.r4 != 4) || sp.rpw < 1 || sp.rpw > 4 * sp.r4) {
@@ -456,13 +472,21 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   if constexpr (stream_max_threads(R4, MT4, 1, DUAL, WB) > 0) MI355_W8S(R4, MT4, 1);
 #define MI355_W8S_MT8(R4) \
   if (mt4 == 6) { MI355_W8S_IF(R4, 6) } else { MI355_W8S_IF(R4, 8) }
+  // 12 or 16 x sets (33 - 64 rows): one matrix only
+#define MI355_W8S_MT16(R4) \
+  if constexpr (!DUAL) {                                   \
+    if (mt4 == 12) { MI355_W8S_IF(R4, 12) } else { MI355_W8S_IF(R4, 16) } \
+  }
   if (mt4 <= 2) {
     if (sp.r4 == 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
   } else if (mt4 <= 4) {
     if (sp.r4 == 4) { MI355_W8S_MT4(4) } else if (sp.r4 == 2) { MI355_W8S_MT4(2) } else { MI355_W8S_MT4(1) }
-  } else {
+  } else if (mt4 <= 8) {
     if (sp.r4 == 4) { MI355_W8S_MT8(4) } else if (sp.r4 == 2) { MI355_W8S_MT8(2) } else { MI355_W8S_MT8(1) }
+  } else {
+    if (sp.r4 == 4) { MI355_W8S_MT16(4) } else if (sp.r4 == 2) { MI355_W8S_MT16(2) } else { MI355_W8S_MT16(1) }
   }
+#undef MI355_W8S_MT16
 #undef MI355_W8S_MT8
 #undef MI355_W8S_IF
 #undef MI355_W8S_MT4

@@ -69,6 +69,7 @@ def _check_vs_oracle(orc, got16, got32, x, w, b, dt):
     (12, 18944, 3584, BF16, "f32"), (16, 8960, 1536, F16, "same"), (13, 3104, 2900, F16, None),
     (1, 136, 1000, BF16, "f16"), (6, 3584, 18944, F16, None),
     (17, 4864, 896, BF16, "f32"), (29, 3104, 2900, F16, None), (32, 18944, 3584, BF16, "same"),
+    (57, 3104, 2900, F16, "f32"), (64, 4864, 896, BF16, None), (40, 1552, 37, F16, "same"),
     # k tails (not a multiple of 64), ragged n, tiny shapes
     (5, 72, 40, F16, "f32"), (7, 8, 3, BF16, None), (9, 1000, 77, F16, "same"), (1, 8, 1, F16, None),
     # more than 32 rows: the tiled GEMM (k tails, ragged edges, small grids)
@@ -170,7 +171,7 @@ def test_abi_rejects_bad_arguments(pkg, cuda):
         pkg.linear16(x, w.to(BF16))
 
 
-@pytest.mark.parametrize("rows,k,n", [(8, 8960, 1536), (32, 8960, 1536), (13, 18944, 3584)])
+@pytest.mark.parametrize("rows,k,n", [(8, 8960, 1536), (32, 8960, 1536), (13, 18944, 3584), (64, 8960, 1536)])
 def test_graph_replays_match_eager(pkg, cuda, rows, k, n):
     x, w, b = (t.to(cuda) for t in _inputs(rows, k, n, F16, seed=11, bias_dt=F32))
     xs = x.clone()

@@ -2,8 +2,8 @@
 (``w8_stream_plan``, ``l16_stream_plan`` and ``gu16_stream_plan`` in
 csrc/w8a16_stream.h, reached
 through the probe library's plan exports; no GPU call): every plan the
-launchers can produce for 1 - 32 rows must be one the launcher accepts --
-at most the kernel's thread limit (16 waves, 8 where its registers need
+launchers can produce (1 - 64 rows; 32 for the dual kernel) must be one
+the launcher accepts -- at most the kernel's thread limit (16 waves, 8 where its registers need
 more room) and no more waves than 256-byte chunks, rows per workgroup
 within its 4-row sets, and for more than 8 rows of x one chunk in flight
 (the instantiations the launcher has) -- and fit the kernel's LDS."""
@@ -44,7 +44,7 @@ def _check(plan, rows, kbytes, nq, lib, wb=1):
     assert r4 in (1, 2, 4) and 1 <= rpw <= 4 * r4, plan
     assert 1 <= waves <= 16 and waves <= max(1, nchunk), (plan, nchunk)
     assert u in (1, 2), plan
-    mt4 = -(-rows // 4) if rows <= 16 else (6 if rows <= 24 else 8)  # stream_x_sets
+    mt4 = -(-rows // 4) if rows <= 16 else (6 if rows <= 24 else (8 if rows <= 32 else (12 if rows <= 48 else 16)))
     if mt4 > 2:  # one chunk in flight with three or more x sets
         assert u == 1, (rows, plan)
     assert 64 * waves <= lib.mi355_probe_stream_max_threads(r4, mt4, u, nq - 1, wb), (rows, plan)
@@ -58,7 +58,9 @@ NS = (1, 7, 37, 256, 896, 1000, 1536, 2048, 3584, 4864, 8960, 18944, 29568, 6553
 @pytest.mark.parametrize("cus", [80, 256, 304])
 def test_w8a16_plan_is_launchable(probe, cus):
     out = (ctypes.c_int * 4)()
-    for rows, k, n, dual in itertools.product(range(1, 33), KS, NS, (0, 1)):
+    for rows, k, n, dual in itertools.product(range(1, 49), KS, NS, (0, 1)):
+        if dual and rows > 32:  # the dual kernel serves up to 32 rows
+            continue
         probe.mi355_probe_w8a16_stream_plan(rows, k, n, dual, cus, out)
         _check(tuple(out), rows, k, 2 if dual else 1, probe)
 
@@ -66,7 +68,7 @@ def test_w8a16_plan_is_launchable(probe, cus):
 @pytest.mark.parametrize("cus", [80, 256, 304])
 def test_linear16_plan_is_launchable(probe, cus):
     out = (ctypes.c_int * 4)()
-    for rows, k, n in itertools.product(range(1, 33), (8, 24, 136, 896, 1536, 2056, 3584, 8960, 18944), NS):
+    for rows, k, n in itertools.product(range(1, 65), (8, 24, 136, 896, 1536, 2056, 3584, 8960, 18944), NS):
         probe.mi355_probe_linear16_stream_plan(rows, k, n, cus, out)
         _check(tuple(out), rows, 2 * k, 1, probe, wb=2)
 

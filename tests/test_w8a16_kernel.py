@@ -150,6 +150,10 @@ STREAM_CASES += [(m, 3104, 2900, F16 if m % 2 else BF16, m % 2 == 1) for m in (9
 STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 0)
                  for m in (17, 24, 25, 32)
                  for K, N in ((8960, 1536), (4864, 896), (3104, 2900), (1552, 37))]
+# 33 - 48 rows (12 x sets, one matrix) where the small tiled shapes do not pay
+STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 1)
+                 for m in (33, 48)
+                 for K, N in ((8960, 1536), (3104, 2900), (1552, 37))]
 
 
 @pytest.mark.parametrize("M,K,N,dt,bias", STREAM_CASES)
@@ -365,8 +369,8 @@ def test_out_row_stride_through_abi(pkg, cuda, M):
 
 
 @pytest.mark.parametrize("M,K,N", [(8, 1536, 8960), (16, 1536, 8960), (100, 1536, 8960),
-                                   # 17 - 32 rows on the stream kernel (6 and 8 x sets)
-                                   (32, 8960, 1536), (20, 4864, 896)])
+                                   # 17 - 48 rows on the stream kernel (6, 8 and 12 x sets)
+                                   (32, 8960, 1536), (20, 4864, 896), (44, 8960, 1536)])
 def test_graph_replays_match_eager(pkg, cuda, M, K, N):
     lin = _linear(K, N, False, cuda, seed=15)
     q = pkg.QuantizedLinearInt8.from_linear(lin)
