@@ -1940,7 +1940,7 @@ def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
         best = min(us, us_graph)
         key = f"{label}_M{M}_{dname}"
         small_tiles = 16 < M <= 64 and -(-N // (128 if (M <= 32 and N > 10000) else 64)) >= 128
-        entry = kernel_entry("w8a16_stream (16-bit weights)" if M <= 32 and not small_tiles else "linear16 tiled",
+        entry = kernel_entry("w8a16_stream (16-bit weights)" if M <= 64 and not small_tiles else "linear16 tiled",
                              nbytes, best,
                              {"rows": M, "k": K, "n": N, "weight_sets": layers, "eager_us": round(us, 3),
                               "graph_us": round(us_graph, 3)})
@@ -1962,7 +1962,7 @@ def bench_linear16(ctx, shapes=LINEAR16_SHAPES, iters=300, baselines=True):
 
 def w8a16_kernel_name(M, N, K=0):
     """The kernel mi355_w8a16_linear_fwd runs for this shape (aligned inputs,
-    descriptors that fit): the weight-streaming kernel up to 32 rows, but
+    descriptors that fit): the weight-streaming kernel up to 48 rows, but
     for wide outputs with 2048 < k < 3072 beyond 8 rows (the skinny split-K
     kernel) and where the small tiled shapes pay (17 - 64 rows, >= 128 tile
     columns); the skinny kernel for small grids, the tiled MFMA GEMM
@@ -1970,7 +1970,7 @@ def w8a16_kernel_name(M, N, K=0):
     bn = 128 if (M <= 32 and N > 10000) else 64
     if 16 < M <= 64 and -(-N // bn) >= 128:
         return "tiled_gemm<int8 B> (small tiles)"
-    if M <= 8 or (M <= 32 and not (N > 10000 and 2048 < K < 3072)):
+    if M <= 8 or (M <= 48 and not (N > 10000 and 2048 < K < 3072)):
         return "w8a16_stream"
     if M <= 32:
         return "w8a16_skinny"
