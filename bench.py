@@ -135,6 +135,7 @@ class Ctx:
             self.probe.mi355_probe_w8a16_stream.restype = ctypes.c_int
             self.probe.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
             self.probe.mi355_probe_linear16_stream_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(i32)]
+            self.probe.mi355_probe_gate_up16_stream_plan.argtypes = [i32, i32, ctypes.POINTER(i32)]
             self.probe.mi355_probe_w8a16_stream_plan.restype = None
             self.probe.mi355_probe_w8a16_stream_loads.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                                                   vp, vp]
@@ -285,6 +286,12 @@ class Ctx:
         same source the library compiles."""
         out4 = (ctypes.c_int * 4)()
         self.probe.mi355_probe_w8a16_stream_plan(rows, k, n, int(dual), cus, out4)
+        return tuple(out4)
+
+    def gu16_stream_plan(self, rows, k):
+        """The 16-bit gate/up + SiLU-and-mul's stream launch plan."""
+        out4 = (ctypes.c_int * 4)()
+        self.probe.mi355_probe_gate_up16_stream_plan(rows, k, out4)
         return tuple(out4)
 
     def l16_stream_plan(self, rows, k, n, cus):
@@ -1398,6 +1405,44 @@ W8_STREAM_SWEEP16_SHAPES = [
 ]
 
 
+def _stream_sweep_shape(ctx, tag, label, M, nchunk, dual, wb, wide16, o, ref, lib_calls, make_calls, plan=None):
+    """The body the decode-kernel sweeps share, for one (rows, k, n): every
+    launch shape _w8_stream_shapes samples (make_calls(rpw, r4, waves, u)
+    builds its calls over the rotating weight sets, writing `o`), checked
+    against `ref` (the library's output, within 2e-3 of its largest value:
+    the fp32 summation order differs with the split of K) and timed as
+    graph nodes, then the library's own calls; `plan` (rpw, r4, waves, u) is
+    the launcher's plan, reported with its time."""
+    torch = ctx.torch
+    nodes = max(2 * len(lib_calls), 64)
+    tol = 2e-3 * ref.float().abs().max().item()
+    res, bad = {}, []
+    for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, stream_x_sets(M), wide16, wb):
+        calls = make_calls(rpw, r4, waves, u)
+        calls[0]()
+        torch.cuda.synchronize()
+        err = (o.float() - ref.float()).abs().max().item()
+        if not err <= tol:
+            bad.append((rpw, r4, waves, u, err))
+        spin_up(ctx, calls, ms=3.0)
+        res[f"rpw{rpw}_w{waves}_u{u}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
+    # the library's own launch last, on a device already warm from the
+    # shapes (timed first it read 3-10% high: clocks still ramping)
+    spin_up(ctx, lib_calls, ms=5.0)
+    res["library_us"] = round(time_graph(ctx, lib_calls, nodes, replays=5), 3)
+    best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
+    rec = {"best": best, "best_us": res[best]}
+    plan_msg = ""
+    if plan is not None:
+        key = f"rpw{plan[0]}_w{plan[2]}_u{plan[3]}"
+        rec.update(plan=key, plan_us=res.get(key))
+        plan_msg = f", plan {key} {res.get(key)} us"
+    rec.update(library_us=res["library_us"], mismatches=bad, shapes=res)
+    log(f"  {tag} stream sweep {label}: library {res['library_us']} us{plan_msg}, best {best} {res[best]} us, "
+        f"{len(bad)} mismatches {bad[:3]}")
+    return rec
+
+
 def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
     """The W8A16 decode kernel (w8a16_stream) over launch shapes, through the
     probe library's forced-shape entry point, at the Qwen2.5-1.5B down and
@@ -1420,7 +1465,6 @@ def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
         x = rand(ctx, (M, K), 2600 + M, F16)
         o = torch.empty((M, N), dtype=F16, device=ctx.dev)
         ref = torch.empty_like(o)
-        nodes = max(2 * sets, 64)
         if dual:
             lib_calls = [ctx.gate_up_w8_call(x, q[0], sc[0], q[1], sc[1], o) for q, sc in zip(qs, scs)]
             ctx.gate_up_w8_call(x, qs[0][0], scs[0][0], qs[0][1], scs[0][1], ref)()
@@ -1428,35 +1472,14 @@ def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
             lib_calls = [ctx.w8a16_call(x, q[0], sc[0], o) for q, sc in zip(qs, scs)]
             ctx.w8a16_call(x, qs[0][0], scs[0][0], ref)()
         torch.cuda.synchronize()
-        res = {}
-        tol = 2e-3 * ref.float().abs().max().item()
-        bad = []
-        nchunk = -(-K // 256)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, stream_x_sets(M), wide16):
-            def mk(q, sc):
-                if dual:
-                    return ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u, q[1], sc[1])
-                return ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u)
-            calls = [mk(q, sc) for q, sc in zip(qs, scs)]
-            calls[0]()
-            torch.cuda.synchronize()
-            err = (o.float() - ref.float()).abs().max().item()
-            if not err <= tol:
-                bad.append((rpw, r4, waves, u, err))
-            spin_up(ctx, calls, ms=3.0)
-            res[f"rpw{rpw}_w{waves}_u{u}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
-        # the library's own launch last, on a device already warm from the
-        # shapes (timed first it read 3-10% high: clocks still ramping)
-        spin_up(ctx, lib_calls, ms=5.0)
-        res["library_us"] = round(time_graph(ctx, lib_calls, nodes, replays=5), 3)
-        best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
-        prpw, _, pwaves, pu = ctx.w8_stream_plan(M, K, N, dual, cus)
-        plan = f"rpw{prpw}_w{pwaves}_u{pu}"
-        out[label] = {"best": best, "best_us": res[best], "plan": plan, "plan_us": res.get(plan),
-                      "library_us": res["library_us"], "mismatches": bad, "shapes": res}
-        log(f"  w8 stream sweep {label}: library {res['library_us']} us, plan {plan} {res.get(plan)} us, "
-            f"best {best} {res[best]} us, "
-            f"{len(bad)} mismatches {bad[:3]}")
+
+        def make_calls(rpw, r4, waves, u):
+            if dual:
+                return [ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u, q[1], sc[1])
+                        for q, sc in zip(qs, scs)]
+            return [ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u) for q, sc in zip(qs, scs)]
+        out[label] = _stream_sweep_shape(ctx, "w8", label, M, -(-K // 256), dual, 1, wide16, o, ref, lib_calls,
+                                         make_calls, plan=ctx.w8_stream_plan(M, K, N, dual, cus))
         del qs, scs
         torch.cuda.empty_cache()
     return out
@@ -1495,31 +1518,13 @@ def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
         x = rand(ctx, (M, K), 3200 + M, F16)
         o = torch.empty((M, N), dtype=F16, device=ctx.dev)
         ref = torch.empty_like(o)
-        nodes = max(2 * sets, 64)
         lib_calls = [ctx.linear16_call(x, w, o) for w in ws]
         ctx.linear16_call(x, ws[0], ref)()
         torch.cuda.synchronize()
-        tol = 2e-3 * ref.float().abs().max().item()
-        res, bad = {}, []
-        nchunk = -(-K // 128)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, False, stream_x_sets(M), True, wb=2):
-            calls = [ctx.linear16_stream_call(x, w, o, rpw, r4, waves, u) for w in ws]
-            calls[0]()
-            torch.cuda.synchronize()
-            err = (o.float() - ref.float()).abs().max().item()
-            if not err <= tol:
-                bad.append((rpw, r4, waves, u, err))
-            spin_up(ctx, calls, ms=3.0)
-            res[f"rpw{rpw}_w{waves}_u{u}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
-        spin_up(ctx, lib_calls, ms=5.0)
-        res["library_us"] = round(time_graph(ctx, lib_calls, nodes, replays=5), 3)
-        best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
-        prpw, _, pwaves, pu = ctx.l16_stream_plan(M, K, N, cus)
-        plan = f"rpw{prpw}_w{pwaves}_u{pu}"
-        out[label] = {"best": best, "best_us": res[best], "plan": plan, "plan_us": res.get(plan),
-                      "library_us": res["library_us"], "mismatches": bad, "shapes": res}
-        log(f"  l16 stream sweep {label}: library {res['library_us']} us, plan {plan} {res.get(plan)} us, "
-            f"best {best} {res[best]} us, {len(bad)} mismatches {bad[:3]}")
+        out[label] = _stream_sweep_shape(
+            ctx, "l16", label, M, -(-K // 128), False, 2, True, o, ref, lib_calls,
+            lambda rpw, r4, waves, u: [ctx.linear16_stream_call(x, w, o, rpw, r4, waves, u) for w in ws],
+            plan=ctx.l16_stream_plan(M, K, N, cus))
         del ws
         torch.cuda.empty_cache()
     return out
@@ -1543,29 +1548,13 @@ def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False):
         x = rand(ctx, (M, K), 3000 + M, F16)
         o = torch.empty((M, N), dtype=F16, device=ctx.dev)
         ref = torch.empty_like(o)
-        nodes = max(2 * sets, 64)
         lib_calls = [ctx.gate_up_call(x, wg, wu, o) for wg, wu in ws]
         ctx.gate_up_call(x, ws[0][0], ws[0][1], ref)()
         torch.cuda.synchronize()
-        tol = 2e-3 * ref.float().abs().max().item()
-        res, bad = {}, []
-        nchunk = -(-K // 128)
-        for rpw, r4, waves, u in _w8_stream_shapes(nchunk, True, stream_x_sets(M), wide16, wb=2):
-            calls = [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u) for wg, wu in ws]
-            calls[0]()
-            torch.cuda.synchronize()
-            err = (o.float() - ref.float()).abs().max().item()
-            if not err <= tol:
-                bad.append((rpw, r4, waves, u, err))
-            spin_up(ctx, calls, ms=3.0)
-            res[f"rpw{rpw}_w{waves}_u{u}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
-        spin_up(ctx, lib_calls, ms=5.0)
-        res["library_us"] = round(time_graph(ctx, lib_calls, nodes, replays=5), 3)
-        best = min((k for k in res if k != "library_us"), key=lambda k: res[k])
-        out[label] = {"best": best, "best_us": res[best], "library_us": res["library_us"], "mismatches": bad,
-                      "shapes": res}
-        log(f"  gu16 stream sweep {label}: library {res['library_us']} us, best {best} {res[best]} us, "
-            f"{len(bad)} mismatches {bad[:3]}")
+        out[label] = _stream_sweep_shape(
+            ctx, "gu16", label, M, -(-K // 128), True, 2, wide16, o, ref, lib_calls,
+            lambda rpw, r4, waves, u: [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u) for wg, wu in ws],
+            plan=ctx.gu16_stream_plan(M, K))
         del ws
         torch.cuda.empty_cache()
     return out
