@@ -288,8 +288,8 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
   }
 }
 
-// Launch plan for `rows` <= 16 rows of x against [n, k] int8 weights (two
-// matrices when dual), fitted to a graph-timed sweep of rows per workgroup x
+// Launch plan for `rows` <= 64 rows of x (32 when dual) against [n, k] int8
+// weights (two matrices when dual), fitted to a graph-timed sweep of rows per workgroup x
 // waves x chunks in flight on MI355X over the Qwen2.5-0.5B, 1.5B and 7B
 // decode projections and MLPs at 1, 4 and 8 rows (bench.py --only
 // w8-stream-sweep; every pick within 1.08x of the best sampled shape, 1.02x
@@ -365,7 +365,7 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   return sp;
 }
 
-// Launch plan of the 16-bit gate/up + SiLU-and-mul (WB = 2) for `rows` <= 16
+// Launch plan of the 16-bit gate/up + SiLU-and-mul (WB = 2) for `rows` <= 32
 // rows of x against two [n, k] weight matrices, from a graph-timed sweep of
 // rows per workgroup x waves x chunks in flight on MI355X over the
 // Qwen2.5-0.5B, 1.5B and 7B MLPs at 1, 4 and 8 rows (bench.py --only
@@ -391,10 +391,11 @@ inline StreamPlan gu16_stream_plan(int rows, int k) {
   return sp;
 }
 
-// Launch plan of the 16-bit linear (WB = 2, one matrix) for `rows` <= 16
-// rows of x against [n, k] weights, from a graph-timed sweep over the
-// Qwen2.5-0.5B, 1.5B and 7B MLP down projections at 1, 4, 8 and 16 rows
-// (bench.py --only l16-stream-sweep): the int8 kernel's plan for the same
+// Launch plan of the 16-bit linear (WB = 2, one matrix) for `rows` <= 64
+// rows of x against [n, k] weights, from graph-timed sweeps over the
+// Qwen2.5-0.5B, 1.5B and 7B MLP down projections at 1 - 64 rows (bench.py
+// --only l16-stream-sweep, stream-sweep32, stream-sweep64): the int8
+// kernel's plan for the same
 // bytes per weight row (2 k), except
 //   - narrow outputs (its plan's 4 - 8 rows per workgroup) with up to 8 rows
 //     of x: 2 chunks in flight, about 12 waves per CU with one x set, 8 with
