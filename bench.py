@@ -71,7 +71,7 @@ def parse_args():
     p.add_argument("--skip-extras", action="store_true", help="headline only (no C4 / decode / copy)")
     p.add_argument("--skip-e2e", action="store_true", help="no end-to-end before/after leg")
     p.add_argument("--only", choices=["c2-silu", "c1-rms", "c1-add-rms", "c4-silu", "c4-rms", "c1-decomp", "copy", "ceilings", "decode", "linear16", "linear16-table", "gate-up",
-                                      "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode",
+                                      "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
                                       "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
@@ -545,6 +545,18 @@ KNOWN_LAUNCHES = {
     ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, true, 1>", 1184 * 64 * 1): (
         "int8 gate/up + SiLU-and-mul 7B, 8 rows, 2 x [18944,3584] int8, bf16",
         2 * 18944 * 3584 + 8 * 18944 + 8 * 3584 * 2 + 8 * 18944 * 2),
+    # the stream kernel at 32 - 64 rows (bench.py --only decode-wide-rows), at their launch plans
+    ("w8a16_stream<mi355::F16, mi355::F16, 2, 8, 1, false, 1>", 256 * 64 * 8): (
+        "W8A16 1.5B down, 32 rows, [1536,8960] int8, fp16", 1536 * 8960 + 4 * 1536 + 32 * 8960 * 2 + 32 * 1536 * 2),
+    ("w8a16_stream<mi355::BF16, mi355::BF16, 2, 12, 1, false, 1>", 448 * 64 * 4): (
+        "W8A16 7B down, 48 rows, [3584,18944] int8, bf16",
+        3584 * 18944 + 4 * 3584 + 48 * 18944 * 2 + 48 * 3584 * 2),
+    ("w8a16_stream<mi355::F16, mi355::F16, 2, 8, 1, false, 2>", 256 * 64 * 8): (
+        "16-bit linear, 32 rows, [1536,8960] weights, fp16 (1.5B down)",
+        1536 * 8960 * 2 + 32 * 8960 * 2 + 32 * 1536 * 2),
+    ("w8a16_stream<mi355::BF16, mi355::BF16, 2, 16, 1, false, 2>", 448 * 64 * 4): (
+        "16-bit linear, 64 rows, [3584,18944] weights, bf16 (7B down)",
+        3584 * 18944 * 2 + 64 * 18944 * 2 + 64 * 3584 * 2),
     ("w8a16_stream<mi355::F16, mi355::F16, 2, 2, 2, false, 2>", 256 * 64 * 8): (
         "16-bit linear, 8 rows, [1536,8960] weights, fp16 (1.5B down)", 1536 * 8960 * 2 + 8 * 8960 * 2 + 8 * 1536 * 2),
     ("w8a16_stream<mi355::BF16, mi355::BF16, 4, 2, 1, false, 2>", 224 * 64 * 8): (
@@ -1023,6 +1035,15 @@ def run_only(ctx, args, sets):
             log(json.dumps(bench_w8a16(ctx, shapes=[s for s in W8A16_SHAPES if s[0] == 8 and s[4] in
                                                     ("gate/up proj", "down proj", "7b gate/up proj", "7b down proj")],
                                        iters=iters, baselines=False)))
+    elif args.only == "decode-wide-rows":  # kernel only: the stream kernel at 32 - 64 rows (for PMC runs)
+        del sets
+        torch.cuda.empty_cache()
+        log(json.dumps(bench_w8a16(ctx, shapes=[(32, 8960, 1536, "f16", "down proj"),
+                                                (48, 18944, 3584, "bf16", "7b down proj")],
+                                   iters=iters, baselines=False)))
+        log(json.dumps(bench_linear16(ctx, shapes=[(32, 8960, 1536, "f16", "qwen2.5-1.5b down"),
+                                                   (64, 18944, 3584, "bf16", "qwen2.5-7b down")],
+                                      iters=iters, baselines=False)))
     elif args.only == "prefill-core":
         print(json.dumps(bench_prefill_core(ctx)), flush=True)
     elif args.only == "stage3":
