@@ -84,7 +84,7 @@ def test_thread_limit_matches_the_bench_sweep(probe, bench):
     """bench.py's sweep samples only launch shapes the kernel takes: its
     stream_max_waves is the kernel's own thread limit / 64, and the limit
     drops to 512 exactly where the register estimate reaches 112."""
-    for r4, mt4, u, dual, wb in itertools.product((1, 2, 4), (1, 2, 3, 4, 6, 8), (1, 2), (0, 1), (1, 2)):
+    for r4, mt4, u, dual, wb in itertools.product((1, 2, 4), (1, 2, 3, 4, 6, 8, 12, 16), (1, 2), (0, 1), (1, 2)):
         lim = probe.mi355_probe_stream_max_threads(r4, mt4, u, dual, wb)
         assert lim in (0, 512, 1024)
         if mt4 <= 4 and u == 1:  # every shape up to 16 rows with one chunk in flight has a kernel
@@ -98,3 +98,9 @@ def test_thread_limit_matches_the_bench_sweep(probe, bench):
     assert probe.mi355_probe_stream_max_threads(4, 3, 1, 0, 1) == 1024
     assert probe.mi355_probe_stream_max_threads(4, 2, 1, 1, 2) == 1024
     assert probe.mi355_probe_stream_max_threads(2, 4, 1, 1, 2) == 1024
+    # 33 - 64 rows of one matrix: two weight sets with 16-bit weights at 16 x
+    # sets, with int8 weights at 12 (not 16), one at 16
+    assert probe.mi355_probe_stream_max_threads(2, 16, 1, 0, 2) == 512
+    assert probe.mi355_probe_stream_max_threads(2, 12, 1, 0, 1) == 512
+    assert probe.mi355_probe_stream_max_threads(2, 16, 1, 0, 1) == 0
+    assert probe.mi355_probe_stream_max_threads(1, 16, 1, 0, 1) == 512
