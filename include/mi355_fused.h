@@ -248,9 +248,9 @@ int mi355_quantize_int8_fwd(const void* w, void* w_q, void* scale,
  * Replaces the down projection of the reference's FusedMLP,
  * `self.down_proj(activated)` (src/engine/fused_norm_activation_patch.py:64),
  * an nn.Linear that torch runs on hipBLASLt.  At decode batch sizes that call
- * streams the whole weight matrix for a few rows; rows <= 32 here read every
- * weight byte once at HBM bandwidth on MFMA.  More rows run the LDS-tiled
- * MFMA GEMM (32-row weight-streaming tiles on small grids).  The fp32 sums
+ * streams the whole weight matrix for a few rows; rows <= 32 here (64 on
+ * outputs narrower than 128 64-column tiles) read every weight byte once at
+ * HBM bandwidth on MFMA.  More rows run the LDS-tiled MFMA GEMM.  The fp32 sums
  * run in this library's own order, so results may differ from hipBLASLt's
  * in the last output bit.
  *

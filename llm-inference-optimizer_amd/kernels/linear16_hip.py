@@ -6,8 +6,8 @@ The reference's FusedMLP ends with ``self.down_proj(activated)``
 (src/engine/fused_norm_activation_patch.py:64), an nn.Linear that torch runs on
 hipBLASLt; at decode batch sizes that call streams the whole weight matrix for
 a handful of rows and hipBLASLt runs it well below HBM bandwidth.  Here up to
-32 rows read every weight byte once, at HBM bandwidth, on MFMA; more rows run
-an LDS-tiled MFMA GEMM.  Sums are fp32 in this library's own order and the
+32 rows (64 on narrow outputs) read every weight byte once, at HBM
+bandwidth, on MFMA; more rows run an LDS-tiled MFMA GEMM.  Sums are fp32 in this library's own order and the
 bias is added in fp32 before the one rounding to x's dtype, so results may
 differ from torch's linear in the last output bit.  FusedMLP uses it only on
 request (``hip_down=True``) and only for inputs of at most ``LINEAR16_MAX_ROWS``
