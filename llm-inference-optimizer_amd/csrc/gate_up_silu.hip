@@ -14,8 +14,9 @@
 // rows of x, so the kernel is bound by HBM bandwidth on the weights, not by
 // MFMA.  Up to 32 rows the launcher runs the lane-coalesced weight-streaming
 // kernel of w8a16_stream.h with 16-bit weights (from 17 rows where the small
-// tiled shapes do not pay); the skinny kernel below serves any decode call
-// whose inputs would span more than that kernel's buffer descriptors reach.
+// tiled shapes do not pay); the skinny kernel below serves more rows whose
+// row strides (2^22 elements or more) the tiled kernel's buffer descriptors
+// cannot span.
 // More rows are a GEMM (MFMA-bound): they run the LDS-tiled kernel of
 // tiled_gemm.h with both weight matrices as B operands and SiLU-and-mul in
 // its epilogue.
