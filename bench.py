@@ -1494,7 +1494,7 @@ def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
             ctx.w8a16_call(x, qs[0][0], scs[0][0], ref)()
         torch.cuda.synchronize()
 
-        def make_calls(rpw, r4, waves, u):
+        def make_calls(rpw, r4, waves, u, x=x, qs=qs, scs=scs, o=o, dual=dual):
             if dual:
                 return [ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u, q[1], sc[1])
                         for q, sc in zip(qs, scs)]
@@ -1544,7 +1544,8 @@ def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
         torch.cuda.synchronize()
         out[label] = _stream_sweep_shape(
             ctx, "l16", label, M, -(-K // 128), False, 2, True, o, ref, lib_calls,
-            lambda rpw, r4, waves, u: [ctx.linear16_stream_call(x, w, o, rpw, r4, waves, u) for w in ws],
+            lambda rpw, r4, waves, u, x=x, ws=ws, o=o: [ctx.linear16_stream_call(x, w, o, rpw, r4, waves, u)
+                                                         for w in ws],
             plan=ctx.l16_stream_plan(M, K, N, cus))
         del ws
         torch.cuda.empty_cache()
@@ -1574,7 +1575,8 @@ def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False):
         torch.cuda.synchronize()
         out[label] = _stream_sweep_shape(
             ctx, "gu16", label, M, -(-K // 128), True, 2, wide16, o, ref, lib_calls,
-            lambda rpw, r4, waves, u: [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u) for wg, wu in ws],
+            lambda rpw, r4, waves, u, x=x, ws=ws, o=o: [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u)
+                                                         for wg, wu in ws],
             plan=ctx.gu16_stream_plan(M, K))
         del ws
         torch.cuda.empty_cache()
