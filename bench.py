@@ -1501,7 +1501,7 @@ def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
             return [ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u) for q, sc in zip(qs, scs)]
         out[label] = _stream_sweep_shape(ctx, "w8", label, M, -(-K // 256), dual, 1, wide16, o, ref, lib_calls,
                                          make_calls, plan=ctx.w8_stream_plan(M, K, N, dual, cus))
-        del qs, scs
+        del qs, scs, make_calls, lib_calls
         torch.cuda.empty_cache()
     return out
 
