@@ -1335,15 +1335,9 @@ def w8_layout_sweep(ctx):
 def stream_max_waves(r4, mt4, u, dual, wb=1):
     """Most waves per workgroup of the decode stream kernel's instantiation
     (stream_max_threads of csrc/w8a16_stream.h / 64): 16, or 8 where its
-    estimated live registers (stream_regs; int8 shapes above 224 with x
-    loaded in two halves) reach 112, 0 above 224."""
+    estimated live registers (stream_regs) reach 112, 0 above 224."""
     nq = 2 if dual else 1
-
-    def regs(w):
-        return 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (8 if w == 1 else 4) * mt4) + r4 + mt4
-    est = regs(wb)
-    if wb == 1 and u == 1 and est > 224:  # stream_split_x: x loaded in two halves
-        est = regs(2)
+    est = 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (8 if wb == 1 else 4) * mt4) + r4 + mt4
     return 0 if est > 224 else (8 if est >= 112 else 16)
 
 

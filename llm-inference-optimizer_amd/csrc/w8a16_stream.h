@@ -114,23 +114,13 @@ constexpr int stream_regs(int r4, int mt4, int u, bool dual, int wb) {
   return 4 * nq * r4 * mt4 + u * (4 * nq * r4 + (wb == 1 ? 8 : 4) * mt4) + r4 + mt4;
 }
 
-// Whether that instantiation loads each chunk's x in two halves: int8
-// weights with one chunk in flight whose estimate passes 224 registers.  The
-// first 16 bytes of every x set arrive with the weights and meet the first
-// B operands, then the second 16 bytes load into the same registers (one
-// more L2 round trip per chunk) -- 4 registers per x set in flight, not 8.
-constexpr bool stream_split_x(int r4, int mt4, int u, bool dual, int wb) {
-  return wb == 1 && u == 1 && stream_regs(r4, mt4, u, dual, wb) > 224;
-}
-
 // Most threads per workgroup of that instantiation: 1024 (16 waves, 128
 // VGPRs per lane) below 112 estimated registers, else 512 (8 waves, 256
-// VGPRs), and 0 -- no such kernel -- above 224 even with x split: the shapes
-// at or above 112 spilled 8 - 432 B per lane under the 128-register budget,
-// those above 224 spilled under 256 (hipcc -Rpass-analysis=kernel-resource-usage).
+// VGPRs), and 0 -- no such kernel -- above 224: the shapes at or above 112
+// spilled 8 - 432 B per lane under the 128-register budget, those above 224
+// spilled under 256 (hipcc -Rpass-analysis=kernel-resource-usage).
 constexpr int stream_max_threads(int r4, int mt4, int u, bool dual, int wb) {
-  // (split x: 4 registers per x set in flight, as with 16-bit weights)
-  const int e = stream_regs(r4, mt4, u, dual, stream_split_x(r4, mt4, u, dual, wb) ? 2 : wb);
+  const int e = stream_regs(r4, mt4, u, dual, wb);
   return e > 224 ? 0 : (e >= 112 ? 512 : 1024);
 }
 
@@ -207,79 +197,41 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 
   const int nchunk = (p.k + KC - 1) >> (W16 ? 7 : 8);
   const int c0 = (nchunk * wave) / nwave, c1 = (nchunk * (wave + 1)) / nwave;
-  if constexpr (stream_split_x(R4, MT4, U, DUAL, WB)) {
-    for (int c = c0; c < c1; ++c) {
-      const bool live = KC * c + piece < p.k;
-      u32x4 wq[NQ][R4], xh[MT4];
+  for (int c = c0; c < c1; c += U) {
+    u32x4 wq[U][NQ][R4], xa[U][MT4][2];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const bool live = c + j < c1 && KC * (c + j) + piece < p.k;
 #pragma unroll
       for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-        for (int r = 0; r < R4; ++r) wq[qi][r] = buf_load16(rq[qi], live ? qoff[r] + 256u * c : kOob);
+        for (int r = 0; r < R4; ++r) wq[j][qi][r] = buf_load16(rq[qi], live ? qoff[r] + 256u * (c + j) : kOob);
       }
 #pragma unroll
-      for (int t = 0; t < MT4; ++t) xh[t] = buf_load16_cached(rx, live ? xoff[t] + KC * sizeof(TB) * c : kOob);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
-#pragma unroll
-        for (int r = 0; r < R4; ++r) {
-          u32x4 b0, b1;
-          widen_i8x16<T>(wq[qi][r], b0, b1);
-#pragma unroll
-          for (int t = 0; t < MT4; ++t) acc[qi][r][t] = mfma16<T>(xh[t], b0, acc[qi][r][t]);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < MT4; ++t)
-        xh[t] = buf_load16_cached(rx, live ? xoff[t] + KC * sizeof(TB) * c + 16u : kOob);
-#pragma unroll
-      for (int qi = 0; qi < NQ; ++qi) {
-#pragma unroll
-        for (int r = 0; r < R4; ++r) {
-          u32x4 b0, b1;
-          widen_i8x16<T>(wq[qi][r], b0, b1);
-#pragma unroll
-          for (int t = 0; t < MT4; ++t) acc[qi][r][t] = mfma16<T>(xh[t], b1, acc[qi][r][t]);
-        }
+      for (int t = 0; t < MT4; ++t) {
+        const uint32_t o = xoff[t] + KC * sizeof(TB) * (c + j);
+        xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
+        if constexpr (!W16) xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
       }
     }
-  } else {
-    for (int c = c0; c < c1; c += U) {
-      u32x4 wq[U][NQ][R4], xa[U][MT4][2];
+    // every load of the group ahead of its MFMAs: U chunks in flight per wave
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < U; ++j) {
-        const bool live = c + j < c1 && KC * (c + j) + piece < p.k;
+    for (int j = 0; j < U; ++j) {
 #pragma unroll
-        for (int qi = 0; qi < NQ; ++qi) {
+      for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-          for (int r = 0; r < R4; ++r) wq[j][qi][r] = buf_load16(rq[qi], live ? qoff[r] + 256u * (c + j) : kOob);
-        }
+        for (int r = 0; r < R4; ++r) {
+          if constexpr (W16) {
 #pragma unroll
-        for (int t = 0; t < MT4; ++t) {
-          const uint32_t o = xoff[t] + KC * sizeof(TB) * (c + j);
-          xa[j][t][0] = buf_load16_cached(rx, live ? o : kOob);
-          if constexpr (!W16) xa[j][t][1] = buf_load16_cached(rx, live ? o + 16u : kOob);
-        }
-      }
-      // every load of the group ahead of its MFMAs: U chunks in flight per wave
-      __builtin_amdgcn_sched_barrier(0);
+            for (int t = 0; t < MT4; ++t) acc[qi][r][t] = mfma16<T>(xa[j][t][0], wq[j][qi][r], acc[qi][r][t]);
+          } else {
+            u32x4 b0, b1;
+            widen_i8x16<T>(wq[j][qi][r], b0, b1);
 #pragma unroll
-      for (int j = 0; j < U; ++j) {
-#pragma unroll
-        for (int qi = 0; qi < NQ; ++qi) {
-#pragma unroll
-          for (int r = 0; r < R4; ++r) {
-            if constexpr (W16) {
-#pragma unroll
-              for (int t = 0; t < MT4; ++t) acc[qi][r][t] = mfma16<T>(xa[j][t][0], wq[j][qi][r], acc[qi][r][t]);
-            } else {
-              u32x4 b0, b1;
-              widen_i8x16<T>(wq[j][qi][r], b0, b1);
-#pragma unroll
-              for (int t = 0; t < MT4; ++t) {
-                acc[qi][r][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][r][t]);
-                acc[qi][r][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][r][t]);
-              }
+            for (int t = 0; t < MT4; ++t) {
+              acc[qi][r][t] = mfma16<T>(xa[j][t][0], b0, acc[qi][r][t]);
+              acc[qi][r][t] = mfma16<T>(xa[j][t][1], b1, acc[qi][r][t]);
             }
           }
         }

@@ -99,10 +99,8 @@ def test_thread_limit_matches_the_bench_sweep(probe, bench):
     assert probe.mi355_probe_stream_max_threads(4, 2, 1, 1, 2) == 1024
     assert probe.mi355_probe_stream_max_threads(2, 4, 1, 1, 2) == 1024
     # 33 - 64 rows of one matrix: two weight sets with 16-bit weights at 16 x
-    # sets, with int8 weights at 12, and at 16 with x loaded in two halves;
-    # four int8 weight sets at 12 x sets do not fit even so
+    # sets, with int8 weights at 12 (not 16), one at 16
     assert probe.mi355_probe_stream_max_threads(2, 16, 1, 0, 2) == 512
     assert probe.mi355_probe_stream_max_threads(2, 12, 1, 0, 1) == 512
-    assert probe.mi355_probe_stream_max_threads(2, 16, 1, 0, 1) == 512
+    assert probe.mi355_probe_stream_max_threads(2, 16, 1, 0, 1) == 0
     assert probe.mi355_probe_stream_max_threads(1, 16, 1, 0, 1) == 512
-    assert probe.mi355_probe_stream_max_threads(4, 12, 1, 0, 1) == 0
