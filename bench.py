@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1077,6 +1077,18 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"linear16_stream_sweep": l16_stream_sweep(ctx)}), flush=True)
+    elif args.only == "stream-sweep-m4":  # 1 - 4 rows on the deep projections that are not narrow
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_M4_SHAPES, rpws=(8, 12, 16)),
+                          "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP_M4_SHAPES),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_M4_SHAPES)}), flush=True)
+    elif args.only == "stream-sweep-r8":  # wide outputs with 17 - 32 weight rows per workgroup too
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_R8_SHAPES, rpws=STREAM_R8_RPWS),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_R8_SHAPES,
+                                                                      rpws=STREAM_R8_RPWS)}), flush=True)
     elif args.only == "stream-sweep16-wide":  # 12 / 16 rows with 16-row workgroups too
         del sets
         torch.cuda.empty_cache()
@@ -1236,13 +1248,15 @@ def bench_stage3_table(ctx, rows=STAGE3_ROWS, hidden=1536, inter=8960, trials=20
 # The decomposed decode shapes: (label, rows, k, n) of the Qwen2.5-1.5B down
 # and gate/up projections.
 W8_DECOMP_SHAPES = [("down_M1", 1, 8960, 1536), ("down_M8", 8, 8960, 1536),
-                    ("gateup_M1", 1, 1536, 8960), ("gateup_M8", 8, 1536, 8960)]
+                    ("gateup_M1", 1, 1536, 8960), ("gateup_M8", 8, 1536, 8960),
+                    ("7b_down_M8", 8, 18944, 3584), ("7b_gateup_M8", 8, 3584, 18944)]
 
 
 def w8_decode_decomposition(ctx):
     """Where the W8A16 decode kernel's time goes, at the Qwen2.5-1.5B down
     (k 8960, n 1536) and gate/up (k 1536, n 8960) projections with 1 and 8
-    rows of fp16 x, every figure a hipGraph node over cold weights (sets
+    rows of fp16 x and the Qwen2.5-7B ones (k 18944, n 3584; k 3584, n 18944)
+    with 8 rows, every figure a hipGraph node over cold weights (sets
     rotating over >= 1 GiB): an empty kernel; the read floor (the weights'
     bytes read by the copy probe's shape) and a copy moving the same bytes;
     the kernel's own loads alone at its launch plan (csrc/probe/
@@ -1349,14 +1363,17 @@ def stream_x_sets(rows):
     return 6 if rows <= 24 else (8 if rows <= 32 else (12 if rows <= 48 else 16))
 
 
-def _w8_stream_shapes(nchunk, dual, mt4, wide16=False, wb=1):
+def _w8_stream_shapes(nchunk, dual, mt4, wide16=False, wb=1, rpws=(4, 6, 8, 12, 16)):
     """Launch shapes (rpw, r4, waves, u) of the W8A16 decode kernel sampled by
-    w8_stream_sweep: rows per workgroup 4-16, 1-16 waves (at most
+    w8_stream_sweep: rows per workgroup `rpws` (4-16 by default; 17-32 take
+    eight 4-row weight sets, up to 8 rows of x), 1-16 waves (at most
     stream_max_waves), 1 or 2 chunks in flight; 16-row workgroups with more
     than 8 rows of x only when `wide16`."""
     out = []
-    for rpw in (4, 6, 8, 12, 16):
-        r4 = 1 if rpw <= 4 else (2 if rpw <= 8 else 4)
+    for rpw in rpws:
+        r4 = 1 if rpw <= 4 else (2 if rpw <= 8 else (4 if rpw <= 16 else 8))
+        if r4 == 8 and mt4 > 2:
+            continue
         if mt4 > 2 and r4 == 4 and not wide16:
             continue
         for waves in (1, 2, 3, 4, 6, 8, 12, 16):
@@ -1415,6 +1432,27 @@ L16_SWEEP64_SHAPES = [("down1.5b_M64", 64, 8960, 1536), ("down7b_M48", 48, 18944
 GU16_SWEEP32_SHAPES = [("gu1.5b_M32", 32, 1536, 8960), ("gu7b_M32", 32, 3584, 18944), ("gu0.5b_M32", 32, 896, 4864)]
 L16_SWEEP32_SHAPES = [("down1.5b_M24", 24, 8960, 1536), ("down1.5b_M32", 32, 8960, 1536),
                       ("down7b_M32", 32, 18944, 3584), ("down0.5b_M32", 32, 4864, 896), ("o7b_M32", 32, 3584, 3584)]
+# wide outputs at up to 8 rows of x with 17 - 32 weight rows per workgroup
+# (eight 4-row weight sets) beside 12 - 16: fewer workgroups re-read x
+STREAM_R8_RPWS = (8, 12, 14, 16, 20, 24, 28, 32)
+W8_STREAM_SWEEP_R8_SHAPES = [("gateup_M4", 4, 1536, 8960, False), ("gateup_M8", 8, 1536, 8960, False),
+                             ("gateup7b_M1", 1, 3584, 18944, False), ("gateup7b_M4", 4, 3584, 18944, False),
+                             ("gateup7b_M8", 8, 3584, 18944, False), ("down7b_M8", 8, 18944, 3584, False),
+                             ("o7b_M8", 8, 3584, 3584, False), ("dual_gateup_M8", 8, 1536, 8960, True),
+                             ("dual7b_M4", 4, 3584, 18944, True), ("dual7b_M8", 8, 3584, 18944, True)]
+# 1 - 4 rows of x (one x set) on the deep projections that are not narrow
+# (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
+W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M2", 2, 3584, 18944, False), ("gateup7b_M3", 3, 3584, 18944, False),
+                             ("gateup7b_M4", 4, 3584, 18944, False), ("down7b_M1", 1, 18944, 3584, False),
+                             ("down7b_M2", 2, 18944, 3584, False), ("down7b_M4", 4, 18944, 3584, False),
+                             ("down7b_M3", 3, 18944, 3584, False), ("o7b_M1", 1, 3584, 3584, False),
+                             ("o7b_M2", 2, 3584, 3584, False), ("o7b_M3", 3, 3584, 3584, False),
+                             ("o7b_M4", 4, 3584, 3584, False),
+                             ("dual7b_M2", 2, 3584, 18944, True), ("dual7b_M3", 3, 3584, 18944, True),
+                             ("dual7b_M4", 4, 3584, 18944, True)]
+L16_SWEEP_M4_SHAPES = [("down7b_M2", 2, 18944, 3584), ("down7b_M4", 4, 18944, 3584), ("o7b_M4", 4, 3584, 3584)]
+GU16_SWEEP_M4_SHAPES = [("gu7b_M2", 2, 3584, 18944), ("gu7b_M3", 3, 3584, 18944)]
+GU16_SWEEP_R8_SHAPES = [("gu1.5b_M8", 8, 1536, 8960), ("gu7b_M4", 4, 3584, 18944), ("gu7b_M8", 8, 3584, 18944)]
 GU16_SWEEP16_WIDE_SHAPES = [("gu7b_M12", 12, 3584, 18944), ("gu7b_M16", 16, 3584, 18944),
                             ("gu1.5b_M16", 16, 1536, 8960)]
 W8_STREAM_SWEEP16_SHAPES = [
@@ -1426,7 +1464,8 @@ W8_STREAM_SWEEP16_SHAPES = [
 ]
 
 
-def _stream_sweep_shape(ctx, tag, label, M, nchunk, dual, wb, wide16, o, ref, lib_calls, make_calls, plan=None):
+def _stream_sweep_shape(ctx, tag, label, M, nchunk, dual, wb, wide16, o, ref, lib_calls, make_calls, plan=None,
+                        rpws=(4, 6, 8, 12, 16)):
     """The body the decode-kernel sweeps share, for one (rows, k, n): every
     launch shape _w8_stream_shapes samples (make_calls(rpw, r4, waves, u)
     builds its calls over the rotating weight sets, writing `o`), checked
@@ -1438,7 +1477,7 @@ def _stream_sweep_shape(ctx, tag, label, M, nchunk, dual, wb, wide16, o, ref, li
     nodes = max(2 * len(lib_calls), 64)
     tol = 2e-3 * ref.float().abs().max().item()
     res, bad = {}, []
-    for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, stream_x_sets(M), wide16, wb):
+    for rpw, r4, waves, u in _w8_stream_shapes(nchunk, dual, stream_x_sets(M), wide16, wb, rpws):
         calls = make_calls(rpw, r4, waves, u)
         calls[0]()
         torch.cuda.synchronize()
@@ -1464,7 +1503,7 @@ def _stream_sweep_shape(ctx, tag, label, M, nchunk, dual, wb, wide16, o, ref, li
     return rec
 
 
-def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
+def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False, rpws=(4, 6, 8, 12, 16)):
     """The W8A16 decode kernel (w8a16_stream) over launch shapes, through the
     probe library's forced-shape entry point, at the Qwen2.5-1.5B down and
     gate/up projections and the int8 gate/up + SiLU-and-mul MLP, 1 and 8 rows
@@ -1500,7 +1539,7 @@ def w8_stream_sweep(ctx, shapes=W8_STREAM_SWEEP_SHAPES, wide16=False):
                         for q, sc in zip(qs, scs)]
             return [ctx.w8_stream_plan_call(x, q[0], sc[0], o, rpw, r4, waves, u) for q, sc in zip(qs, scs)]
         out[label] = _stream_sweep_shape(ctx, "w8", label, M, -(-K // 256), dual, 1, wide16, o, ref, lib_calls,
-                                         make_calls, plan=ctx.w8_stream_plan(M, K, N, dual, cus))
+                                         make_calls, plan=ctx.w8_stream_plan(M, K, N, dual, cus), rpws=rpws)
         del qs, scs, make_calls, lib_calls
         torch.cuda.empty_cache()
     return out
@@ -1552,7 +1591,7 @@ def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
     return out
 
 
-def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False):
+def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False, rpws=(4, 6, 8, 12, 16)):
     """The 16-bit gate/up + SiLU-and-mul at decode rows: the library's
     launch (mi355_gate_up_silu_fwd) against the weight-streaming kernel of
     w8a16_stream.h with 16-bit weights over launch shapes (rows per
@@ -1577,7 +1616,7 @@ def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False):
             ctx, "gu16", label, M, -(-K // 128), True, 2, wide16, o, ref, lib_calls,
             lambda rpw, r4, waves, u, x=x, ws=ws, o=o: [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u)
                                                          for wg, wu in ws],
-            plan=ctx.gu16_stream_plan(M, K))
+            plan=ctx.gu16_stream_plan(M, K), rpws=rpws)
         del ws
         torch.cuda.empty_cache()
     return out

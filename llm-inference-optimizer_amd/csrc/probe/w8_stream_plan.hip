@@ -125,13 +125,14 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8a16_stream_l
 
 namespace {
 
-// The decode kernel at any launch shape the probes accept: R4 in {1, 2, 4},
-// MT4 = stream_x_sets(rows) in 1 .. 4, 6, 8, 12, 16 (64 rows of x), U in {1, 2}
-// (U = 1 only for MT4 > 2); fp16 x, weights of WB bytes.
+// The decode kernel at any launch shape the probes accept: R4 in {1, 2, 4}
+// (and 8 with up to 8 rows of x), MT4 = stream_x_sets(rows) in 1 .. 4, 6, 8,
+// 12, 16 (64 rows of x), U in {1, 2} (U = 1 only for MT4 > 2); fp16 x,
+// weights of WB bytes.
 template <bool DUAL, int WB, int R4, int MT4>
 const void* sk_u(int u) {
   using mi355::F16;
-  if constexpr (MT4 <= 2) {
+  if constexpr (MT4 <= 2 && mi355::stream_max_threads(R4, MT4, 2, DUAL, WB) > 0) {
     if (u >= 2) return reinterpret_cast<const void*>(mi355::w8a16_stream<F16, F16, R4, MT4, 2, DUAL, WB>);
   }
   // shapes without a kernel (stream_max_threads 0): shape_ok rejects them
@@ -151,6 +152,7 @@ const void* sk_mt(int mt4, int u) {
 }
 template <bool DUAL, int WB>
 const void* stream_kernel(int r4, int mt4, int u) {
+  if (r4 == 8) return mt4 == 1 ? sk_u<DUAL, WB, 8, 1>(u) : (mt4 == 2 ? sk_u<DUAL, WB, 8, 2>(u) : nullptr);
   if (r4 >= 4) return sk_mt<DUAL, WB, 4>(mt4, u);
   if (r4 == 2) return sk_mt<DUAL, WB, 2>(mt4, u);
   return sk_mt<DUAL, WB, 1>(mt4, u);
@@ -158,7 +160,8 @@ const void* stream_kernel(int r4, int mt4, int u) {
 
 bool shape_ok(int rows, int n, int rpw, int r4, int waves, int u, bool dual, int wb) {
   const int mt4 = mi355::stream_x_sets(rows);
-  return rows >= 1 && rows <= 64 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4) && rpw <= 4 * r4 &&
+  return rows >= 1 && rows <= 64 && n >= 1 && rpw >= 1 && (r4 == 1 || r4 == 2 || r4 == 4 || (r4 == 8 && mt4 <= 2)) &&
+         rpw <= 4 * r4 &&
          waves >= 1 && 64 * waves <= mi355::stream_max_threads(r4, mt4, u, dual, wb) &&
          (u == 1 || (u == 2 && mt4 <= 2));
 }
@@ -179,7 +182,7 @@ int launch_stream(const void* kern, const mi355::W8Params& p, int rpw, int r4, i
 // out [rows, n] = W8A16(x [rows, k], q [n, k], scale [n]) (q2 / scale2 not
 // NULL: the gate/up + SiLU-and-mul kernel with q, scale the gate and q2,
 // scale2 the up weights), launched with rpw weight rows per workgroup, r4
-// 4-row sets (1, 2 or 4; rpw <= 4 r4), `waves` waves (at most
+// 4-row sets (1, 2 or 4, or 8 up to 8 rows; rpw <= 4 r4), `waves` waves (at most
 // stream_max_threads / 64: 16 or 8) and u chunks in flight (1 or 2; 1 above
 // 8 rows).  rows <= 32, k a multiple of 16, every pointer
 // 16-byte aligned.  Returns 0, -1 on bad arguments, -3 on a launch error.

@@ -297,11 +297,15 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 // projections with 8 rows):
 //   rows per workgroup: 8 (two 4-row sets); narrow outputs (n <= 2048, or
 //     fewer 8-row workgroups than CUs) as few as give every CU a workgroup,
-//     4 to 8; 16 with more than 4 rows of x and k >= 3072, where every
-//     workgroup re-reads a long x (half the x re-reads of 8); the dual
-//     kernel 4 with up to 4 rows of x, else 8 (or 16 as above);
+//     4 to 8; 16 at k >= 3072 with more than 4 rows of x, or with 2 - 4 (4
+//     with 16-bit weights) where that leaves every CU a workgroup or k >=
+//     8192, since every workgroup re-reads a long x (half the x re-reads of
+//     8); the dual kernel 4 with one row of x (or with up to 4
+//     below k = 3072 or on narrow outputs), else 8 (16 as above with more
+//     than 4 rows);
 //   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
-//     8-row workgroups, 1 with 16-row workgroups); else about 14 per CU with
+//     8-row workgroups, 8 with 2 - 4 rows at k >= 3072 on outputs that are
+//     not narrow, 1 with 16-row workgroups); else about 14 per CU with
 //     up to 4 rows of x, 12 (one workgroup per CU) or 10 with more, 7 for
 //     16-row workgroups (6 with more than 8 rows of x); at least 2 (but for
 //     the dual kernel's 1) and at most 16 waves (8 where stream_max_threads
@@ -325,19 +329,36 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 // sets allow (16-bit weights: 2, int8 weights: 2 up to 48 rows, then 1), and
 // 7 waves per CU with more workgroups than CUs (7B down, 64 rows of 16-bit
 // weights: 4 waves 78.9 us, 3 waves 83.4).
+// 2 - 4 rows on deep rows (bench.py --only stream-sweep-m4, the 7B
+// projections and MLP at 1 - 4 rows): 16-row workgroups (7B gate/up, 3 / 4
+// rows 12.72 / 12.74 us against 14.34 / 14.87 with 8 rows; 7B down, 4 rows
+// 13.61 vs 15.34; with 16-bit weights from 4 rows, 21.77 vs 22.98), and the
+// dual kernel on 8-row workgroups of 8 waves (7B, 3 / 4 rows 22.33 / 22.82
+// us against 23.85 / 25.27 on 4-row workgroups of 3); with one row of x the
+// 8-row (dual: 4-row) workgroups stay ahead (7B down 12.51 vs 12.92 us),
+// and so they do at k = 3584 where 16-row workgroups leave CUs idle (7B q/o,
+// 2 / 3 rows 4.48 / 4.65 us against 4.79 / 4.82).
 // `wb` is the weight element size the plan is for (k counts bytes).
 inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int wb = 1) {
   const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
   const bool four_sets = rows > 8;  // three or more sets
+  // x re-read by every 8-row workgroup is at least half its weight bytes
+  // (2 rows of x with int8 weights, 4 with 16-bit): on deep rows (k >= 3072
+  // bytes) larger workgroups pay from there -- with one x set only where
+  // 16-row workgroups still give every CU one, or the rows are longer still
+  const bool x_heavy =
+      k >= 3072 && (two_sets || (rows >= 2 * wb && (k >= 8192 || (n + 15) / 16 >= cus)));
+  const bool narrow = n <= 2048 || (n + 7) / 8 < cus;
+  const bool deep_dual = dual && !two_sets && x_heavy && !narrow;  // 2 - 4 rows, two matrices
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
-  if (n <= 2048 || (n + 7) / 8 < cus) {
+  if (narrow) {
     sp.rpw = (n + cus - 1) / cus;
     sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
-  } else if (two_sets && k >= 3072 && !(dual && rows > 16)) {
+  } else if ((dual ? two_sets : x_heavy) && k >= 3072 && !(dual && rows > 16)) {
     sp.rpw = 16;
   }
-  if (dual && sp.rpw < 16) sp.rpw = two_sets ? 8 : 4;
+  if (dual && sp.rpw < 16) sp.rpw = two_sets || deep_dual ? 8 : 4;
   sp.r4 = sp.rpw <= 4 ? 1 : (sp.rpw <= 8 ? 2 : 4);
   // fewer 4-row weight sets where this many x sets leave no registers for more
   while (sp.r4 > 1 && stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, wb) == 0) {
@@ -348,7 +369,7 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   int64_t waves;
   int min_waves = 2;
   if (dual) {
-    waves = sp.rpw == 16 ? 1 : (two_sets ? 2 : 3);
+    waves = sp.rpw == 16 ? 1 : (two_sets ? 2 : (deep_dual ? 8 : 3));
     min_waves = sp.rpw == 16 ? 1 : 2;
   } else {
     const int per_cu = sp.rpw == 16 ? (four_sets && rows <= 16 ? 6 : 7)

@@ -66,6 +66,9 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
     (1, 3584, 18944, BF16), (8, 3584, 18944, BF16),
     # decode rows with a partial last 256-column chunk and a ragged last workgroup
     (3, 272, 1000, F16), (6, 1552, 520, BF16), (2, 4864, 904, F16),
+    # 2 - 4 rows at k >= 3072 (8-row workgroups of 8 waves; a partial last
+    # chunk and a ragged last workgroup at 3104 x 4204)
+    (2, 3584, 18944, F16), (3, 3104, 4204, F16), (4, 3104, 4204, BF16),
     # 9 - 16 rows: three and four x sets; the 7B MLP and k >= 3072 with n > 2048 (16-row
     # workgroups, one wave; a partial last chunk and a ragged last workgroup at k 3104 x n 2900)
     (12, 1536, 8960, F16), (13, 272, 1000, BF16), (16, 1552, 520, F16), (16, 3584, 18944, BF16),

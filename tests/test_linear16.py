@@ -68,6 +68,9 @@ def _check_vs_oracle(orc, got16, got32, x, w, b, dt):
     (8, 18944, 3584, BF16, None), (3, 4864, 896, BF16, None), (24, 3584, 3584, F16, None),
     (12, 18944, 3584, BF16, "f32"), (16, 8960, 1536, F16, "same"), (13, 3104, 2900, F16, None),
     (1, 136, 1000, BF16, "f16"), (6, 3584, 18944, F16, None),
+    # 4 rows on deep rows of outputs that are not narrow: 16-row workgroups
+    # (a partial last chunk and a ragged last workgroup at k 3104 x n 4204)
+    (4, 3104, 4204, BF16, "f32"), (4, 18944, 3584, F16, None),
     (17, 4864, 896, BF16, "f32"), (29, 3104, 2900, F16, None), (32, 18944, 3584, BF16, "same"),
     (57, 3104, 2900, F16, "f32"), (64, 4864, 896, BF16, None), (40, 1552, 37, F16, "same"),
     # k tails (not a multiple of 64), ragged n, tiny shapes
