@@ -1442,7 +1442,8 @@ W8_STREAM_SWEEP_R8_SHAPES = [("gateup_M4", 4, 1536, 8960, False), ("gateup_M8", 
                              ("dual7b_M4", 4, 3584, 18944, True), ("dual7b_M8", 8, 3584, 18944, True)]
 # 1 - 4 rows of x (one x set) on the deep projections that are not narrow
 # (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
-W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M2", 2, 3584, 18944, False), ("gateup7b_M3", 3, 3584, 18944, False),
+W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M1", 1, 3584, 18944, False), ("dual7b_M1", 1, 3584, 18944, True),
+                             ("gateup7b_M2", 2, 3584, 18944, False), ("gateup7b_M3", 3, 3584, 18944, False),
                              ("gateup7b_M4", 4, 3584, 18944, False), ("down7b_M1", 1, 18944, 3584, False),
                              ("down7b_M2", 2, 18944, 3584, False), ("down7b_M4", 4, 18944, 3584, False),
                              ("down7b_M3", 3, 18944, 3584, False), ("o7b_M1", 1, 3584, 3584, False),

@@ -298,9 +298,10 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 //   rows per workgroup: 8 (two 4-row sets); narrow outputs (n <= 2048, or
 //     fewer 8-row workgroups than CUs) as few as give every CU a workgroup,
 //     4 to 8; 16 at k >= 3072 with more than 4 rows of x, or with 2 - 4 (4
-//     with 16-bit weights) where that leaves every CU a workgroup or k >=
-//     8192, since every workgroup re-reads a long x (half the x re-reads of
-//     8); the dual kernel 4 with one row of x (or with up to 4
+//     with 16-bit weights) where that leaves every CU a workgroup (one matrix
+//     of int8 weights: 1 - 4 rows) or k >= 8192, since every workgroup
+//     re-reads a long x (half the x re-reads of 8); the dual kernel 4 with
+//     one row of x (or with up to 4
 //     below k = 3072 or on narrow outputs), else 8 (16 as above with more
 //     than 4 rows);
 //   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
@@ -335,9 +336,10 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 // 13.61 vs 15.34; with 16-bit weights from 4 rows, 21.77 vs 22.98), and the
 // dual kernel on 8-row workgroups of 8 waves (7B, 3 / 4 rows 22.33 / 22.82
 // us against 23.85 / 25.27 on 4-row workgroups of 3); with one row of x the
-// 8-row (dual: 4-row) workgroups stay ahead (7B down 12.51 vs 12.92 us),
-// and so they do at k = 3584 where 16-row workgroups leave CUs idle (7B q/o,
-// 2 / 3 rows 4.48 / 4.65 us against 4.79 / 4.82).
+// 8-row (dual: 4-row) workgroups stay ahead (7B down 12.51 vs 12.92 us) but
+// where 16-row ones still fill the CUs (7B gate/up, 12.59 vs 13.18), and so
+// they do at k = 3584 where 16-row workgroups leave CUs idle (7B q/o, 2 / 3
+// rows 4.48 / 4.65 us against 4.79 / 4.82).
 // `wb` is the weight element size the plan is for (k counts bytes).
 inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int wb = 1) {
   const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
@@ -345,11 +347,12 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   // x re-read by every 8-row workgroup is at least half its weight bytes
   // (2 rows of x with int8 weights, 4 with 16-bit): on deep rows (k >= 3072
   // bytes) larger workgroups pay from there -- with one x set only where
-  // 16-row workgroups still give every CU one, or the rows are longer still
-  const bool x_heavy =
-      k >= 3072 && (two_sets || (rows >= 2 * wb && (k >= 8192 || (n + 15) / 16 >= cus)));
+  // 16-row workgroups still give every CU one (so too with one row of x and
+  // int8 weights), or the rows are longer still
+  const bool x_heavy = k >= 3072 && (two_sets || (rows >= 2 * wb && k >= 8192) ||
+                                     ((wb == 1 || rows >= 4) && (n + 15) / 16 >= cus));
   const bool narrow = n <= 2048 || (n + 7) / 8 < cus;
-  const bool deep_dual = dual && !two_sets && x_heavy && !narrow;  // 2 - 4 rows, two matrices
+  const bool deep_dual = dual && rows >= 2 && !two_sets && x_heavy && !narrow;  // 2 - 4 rows, two matrices
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
   if (narrow) {

@@ -118,7 +118,8 @@ def test_plans_picked_by_the_deep_row_sweep(probe):
     (k >= 3072 bytes) of outputs that are not narrow -- from 4 rows with
     16-bit weights, and at k < 8192 only where every CU gets a 16-row
     workgroup --, the dual kernel on 8-row workgroups of 8 waves at 2 - 4
-    rows; with one row of x the earlier 8-row (dual: 4-row) plans."""
+    rows; with one row of x the earlier 8-row (dual: 4-row) plans but where
+    every CU gets a 16-row workgroup of one int8 matrix."""
     w8 = probe.mi355_probe_w8a16_stream_plan
     l16 = probe.mi355_probe_linear16_stream_plan
     for rows in (2, 3, 4):
@@ -128,7 +129,8 @@ def test_plans_picked_by_the_deep_row_sweep(probe):
         assert _plan(probe, w8, rows, 1536, 8960, 0, 256)[0] == 8, rows             # 1.5B gate/up: k < 3072
         assert _plan(probe, w8, rows, 8960, 1536, 0, 256)[0] <= 8, rows             # narrow: every CU a workgroup
         assert _plan(probe, w8, rows, 3584, 3584, 0, 256) == (8, 2, 8, 1), rows     # 7B q/o: 224 16-row groups
-    assert _plan(probe, w8, 1, 3584, 18944, 0, 256)[0] == 8
+    assert _plan(probe, w8, 1, 3584, 18944, 0, 256) == (16, 4, 2, 1)   # every CU a 16-row workgroup
+    assert _plan(probe, w8, 1, 3584, 3584, 0, 256)[0] == 8
     assert _plan(probe, w8, 1, 18944, 3584, 0, 256) == (8, 2, 8, 1)
     assert _plan(probe, w8, 1, 3584, 18944, 1, 256)[:3] == (4, 1, 3)
     assert _plan(probe, w8, 8, 3584, 18944, 1, 256) == (16, 4, 1, 1)

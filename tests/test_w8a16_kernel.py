@@ -146,11 +146,11 @@ STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 0)
                  for m in (9, 12, 13, 16)
                  for K, N in ((8960, 1536), (1536, 8960), (272, 1000), (1552, 37), (3584, 10008))]
 STREAM_CASES += [(m, 3104, 2900, F16 if m % 2 else BF16, m % 2 == 1) for m in (9, 10, 11, 12)]
-# 2 - 4 rows on deep rows (k >= 3072) of outputs with at least a CU's worth
+# 1 - 4 rows on deep rows (k >= 3072) of outputs with at least a CU's worth
 # of 16-row workgroups: 16-row workgroups (a partial last chunk and a ragged
 # last workgroup at 3104 x 4204); below that (3104 x 2900) 8-row workgroups
 STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 1)
-                 for m in (2, 3, 4)
+                 for m in (1, 2, 3, 4)
                  for K, N in ((3104, 4204), (3584, 10008), (3104, 2900))]
 STREAM_CASES += [(3, 18944, 3584, BF16, False)]
 # 17 - 32 rows where the small tiled shapes do not pay: 6 and 8 x sets
