@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1104,6 +1104,10 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx)}), flush=True)
+    elif args.only == "w8-layouts8":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8_stream_layouts8": w8_layout8_sweep(ctx)}), flush=True)
     elif args.only == "w8-layouts":
         del sets
         torch.cuda.empty_cache()
@@ -1341,6 +1345,42 @@ def w8_layout_sweep(ctx):
                             time_graph(ctx, calls, nodes, replays=5), 3)
         out[label] = res
         log(f"  w8 layouts {label}: {json.dumps(res)}")
+        del qs
+        torch.cuda.empty_cache()
+    return out
+
+
+# The weight-stream probe at the decode kernel's 8-row launch plans (rpw,
+# waves, G 8-row groups, U blocks in flight: one 256-byte chunk of each 4-row
+# set): its lane layout (WL 3 with the kernel's x loads, XL 5) against 8 rows x
+# 128 bytes with pairs of lanes on 32 bytes (WL 4, x to match: XL 4)
+W8_LAYOUT8_SHAPES = [("down", 8960, 1536, (6, 12, 1, 2)), ("gateup", 1536, 8960, (8, 2, 1, 2)),
+                     ("down7b", 18944, 3584, (16, 8, 2, 2)), ("gateup7b", 3584, 18944, (16, 2, 2, 2))]
+
+
+def w8_layout8_sweep(ctx):
+    """WL 3 / XL 5 (the decode kernel's loads) against WL 4 / XL 4 in the
+    weight-stream probe (csrc/probe/w8_stream.hip), weights alone and with 8
+    rows of fp16 x, at the kernel's 8-row launch plans: graph-node us, cold
+    weights."""
+    torch = ctx.torch
+    sink = torch.zeros(1024, dtype=torch.int32, device=ctx.dev)
+    out = {}
+    for label, K, N, (rpw, wv, gg, uu) in W8_LAYOUT8_SHAPES:
+        sets = n_sets(N * K)
+        g = torch.Generator(device=ctx.dev)
+        g.manual_seed(2700 + K)
+        qs = [torch.randint(-127, 128, (N, K), generator=g, device=ctx.dev, dtype=torch.int8) for _ in range(sets)]
+        x = rand(ctx, (8, K), 2800, torch.float16)
+        nodes = max(2 * sets, 64)
+        res = {}
+        for wl, xl in ((3, 0), (4, 0), (3, 5), (4, 4)):
+            calls = [ctx.w8_stream_call(q, sink, rpw, wv, gg, uu, layout=wl, x=x if xl else None, xl=xl or 1)
+                     for q in qs]
+            spin_up(ctx, calls, ms=3.0)
+            res[f"WL{wl}_XL{xl}"] = round(time_graph(ctx, calls, nodes, replays=5), 3)
+        out[label] = res
+        log(f"  w8 layouts (8 rows) {label} rpw{rpw} w{wv} G{gg} U{uu}: {json.dumps(res)}")
         del qs
         torch.cuda.empty_cache()
     return out

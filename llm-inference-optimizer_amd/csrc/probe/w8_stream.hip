@@ -63,11 +63,16 @@ struct StreamParams {
 //   WL 0  lane l: row l % 8, bytes 64 ((l / 8) % 2) + 16 (l / 16)   (w8a16_skinny)
 //   WL 2  lane l: row l / 8, bytes 16 (l % 8)                        (lanes in row order)
 //   WL 3  rows 4 (s % 2) + (l % 16) / 4, bytes 256 (s / 2) + 16 (l % 4) + 64 (l / 16)
+//   WL 4  lane l: row (l % 16) / 2, bytes 16 (l % 2) + 32 (l / 16)   (pairs of lanes on 32 bytes)
 // x lane layouts of the two 16-byte loads per block (8 x rows x 128 columns
 // of 16-bit x), XL:
 //   1  lane l: x row l % 8, byte 2 (64 ((l / 8) % 2) + 16 (l / 16)) and +16  (w8a16_skinny)
 //   2  load a: x row l / 16, bytes 16 (l % 16); load b: rows 4 + l / 16
 //   3  x rows 2 (s % 4) and 2 (s % 4) + 1, 1 KiB each at byte 1024 (s / 4) + 16 l
+//   4  lane l: x row (l % 16) / 2, columns 16 (l % 2) + 32 (l / 16) .. + 8 and + 8 .. + 16
+//      (the k of WL 4's bytes)
+//   5  x rows 4 (s % 2) + (l % 16) / 4, columns 256 (s / 2) + 16 (l % 4) + 64 (l / 16)
+//      .. + 8 and + 8 .. + 16 (the decode kernel's x loads beside WL 3)
 // STAGGER rotates each wave's walk over its blocks by the workgroup index.
 template <int G, int U, int WL, int XL>
 __global__ __launch_bounds__(1024) void w8_stream_mfma_layout(const StreamParams p, int stagger) {
@@ -91,6 +96,9 @@ __global__ __launch_bounds__(1024) void w8_stream_mfma_layout(const StreamParams
     } else if constexpr (WL == 2) {
       row = lane >> 3;
       off = 128 * s + 16 * (lane & 7);
+    } else if constexpr (WL == 4) {
+      row = (lane & 15) >> 1;
+      off = 128 * s + 16 * (lane & 1) + 32 * (lane >> 4);
     } else {
       row = 4 * (s & 1) + ((lane & 15) >> 2);
       off = 256 * (s >> 1) + 16 * (lane & 3) + 64 * (lane >> 4);
@@ -123,6 +131,20 @@ __global__ __launch_bounds__(1024) void w8_stream_mfma_layout(const StreamParams
         const bool la = in && xr < p.rows && c < p.k, lb = in && xr + 4 < p.rows && c < p.k;
         xa[j][0] = ld(rx, la ? static_cast<uint32_t>((xr * p.xs + c) * 2) : kOob);
         xa[j][1] = ld(rx, lb ? static_cast<uint32_t>(((xr + 4) * p.xs + c) * 2) : kOob);
+      } else if constexpr (XL == 4) {
+        const int xr = (lane & 15) >> 1;
+        const int c = 128 * s + 16 * (lane & 1) + 32 * (lane >> 4);
+        const bool live = in && xr < p.rows && c < p.k;
+        const uint32_t o = static_cast<uint32_t>((xr * p.xs + c) * 2);
+        xa[j][0] = ld(rx, live ? o : kOob);
+        xa[j][1] = ld(rx, live ? o + 16u : kOob);
+      } else if constexpr (XL == 5) {
+        const int xr = 4 * (s & 1) + ((lane & 15) >> 2);
+        const int c = 256 * (s >> 1) + 16 * (lane & 3) + 64 * (lane >> 4);
+        const bool live = in && xr < p.rows && c < p.k;
+        const uint32_t o = static_cast<uint32_t>((xr * p.xs + c) * 2);
+        xa[j][0] = ld(rx, live ? o : kOob);
+        xa[j][1] = ld(rx, live ? o + 16u : kOob);
       } else if constexpr (XL == 3) {
         const int xr = 2 * (s & 3);
         const int c = 512 * (s >> 2) + 8 * lane;
@@ -196,6 +218,8 @@ const void* mfma_layout_kernel_x(int xl, int g, int u) {
     case 1: return mfma_layout_kernel_g<WL, 1>(g, u);
     case 2: return mfma_layout_kernel_g<WL, 2>(g, u);
     case 3: return mfma_layout_kernel_g<WL, 3>(g, u);
+    case 4: return mfma_layout_kernel_g<WL, 4>(g, u);
+    case 5: return mfma_layout_kernel_g<WL, 5>(g, u);
     default: return nullptr;
   }
 }
@@ -218,8 +242,8 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_read(const voi
 // Streams the int8 weights q [n, qs] (k columns, q and qs 16-byte aligned)
 // with `waves` waves per workgroup over ceil(n / rpw) workgroups, U pieces in
 // flight per wave.  layout 1: one row x 1 KiB per load (G 1, no x); layout
-// 0, 2 or 3: the weight lane layouts WL above (G 8-row groups per piece), with
-// x [rows <= 8, xs] of 16-bit values loaded in x layout xl (1-3) when x is
+// 0, 2, 3 or 4: the weight lane layouts WL above (G 8-row groups per piece),
+// with x [rows <= 8, xs] of 16-bit values loaded in x layout xl (1-5) when x is
 // not NULL; stagger != 0 rotates each wave's walk by the workgroup index.
 // `sink` holds at least 1024 dwords.  Returns 0, -1 on bad arguments, -3 on a
 // launch error.
@@ -235,10 +259,11 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_w8_stream(
     if (rpw > 8 * g || (x && (rows < 1 || rows > 8 || xs < k || (xs & 7) || (reinterpret_cast<uintptr_t>(x) & 15))))
       return -1;
     if (!x) xl = 0;
-    else if (xl < 1 || xl > 3) return -1;
+    else if (xl < 1 || xl > 5) return -1;
     if (layout == 0) kern = mfma_layout_kernel_x<0>(xl, g, u);
     else if (layout == 2) kern = mfma_layout_kernel_x<2>(xl, g, u);
     else if (layout == 3) kern = mfma_layout_kernel_x<3>(xl, g, u);
+    else if (layout == 4) kern = mfma_layout_kernel_x<4>(xl, g, u);
   } else if (g == 1 && !x) {
     if (u == 1) kern = reinterpret_cast<const void*>(w8_stream_row_layout<1>);
     else if (u == 2) kern = reinterpret_cast<const void*>(w8_stream_row_layout<2>);
