@@ -932,6 +932,7 @@ def per_config(full):
             continue
         rows = int(m[2:])
         c3["M" + m[2:]] = {"rms_api_us": d["rmsnorm_api_us"], "silu_api_us": d["silu_mul_api_us"],
+                           "rms_call_us": d.get("rmsnorm_call_us"), "silu_call_us": d.get("silu_mul_call_us"),
                            "rms_dev_us": d["rmsnorm_device_us"], "silu_dev_us": d["silu_mul_device_us"],
                            "graph_node_us": d["graph_per_kernel_us"], "graph_28_layers_us": d["graph_replay_us"],
                            "rms_rows_per_s": round(rows / d["rmsnorm_device_us"] * 1e6),
@@ -1733,10 +1734,12 @@ def bench_c4(ctx, iters=60, which=None):
 
 
 def bench_decode(ctx, layers=28):
-    """C3: decode shapes.  Per call through the Python API (host-inclusive,
-    synchronised like the reference's _time_cuda), device-only from events
-    over back-to-back ABI launches, and inside a hipGraph of `layers` x
-    (RMSNorm, SiLU-and-mul, RMSNorm) on per-layer buffers."""
+    """C3: decode shapes.  Per call through the Python API, two ways: the
+    host's wall clock around the call and a synchronize (`*_api_us`, median),
+    and events around the call as the reference's _time_cuda records them
+    (`*_call_us`, mean; benchmarks/run_stage3_kernels.py:34-49); device-only
+    from events over back-to-back ABI launches; and inside a hipGraph of
+    `layers` x (RMSNorm, SiLU-and-mul, RMSNorm) on per-layer buffers."""
     torch = ctx.torch
     F16 = torch.float16
     N, I = 1536, 8960
@@ -1761,6 +1764,8 @@ def bench_decode(ctx, layers=28):
 
         rms_api = api_us(lambda: ctx.pkg.fused_rmsnorm(x, w))
         silu_api = api_us(lambda: ctx.pkg.fused_silu_mul(g, u))
+        rms_call = _time_per_call(torch, lambda: ctx.pkg.fused_rmsnorm(x, w), 200)
+        silu_call = _time_per_call(torch, lambda: ctx.pkg.fused_silu_mul(g, u), 200)
         y = torch.empty_like(x)
         o = torch.empty_like(g)
         rms_dev = time_loop(ctx, [ctx.rms_call(x, w, y)], 2000)
@@ -1782,6 +1787,7 @@ def bench_decode(ctx, layers=28):
         replay_us = per_kernel * len(calls)
         res[f"M={M}"] = {
             "rmsnorm_api_us": round(rms_api, 2), "silu_mul_api_us": round(silu_api, 2),
+            "rmsnorm_call_us": round(rms_call, 2), "silu_mul_call_us": round(silu_call, 2),
             "rmsnorm_device_us": round(rms_dev, 3), "silu_mul_device_us": round(silu_dev, 3),
             "graph_replay_us": round(replay_us, 2), "graph_per_layer_us": round(replay_us / layers, 3),
             "graph_per_kernel_us": round(per_kernel, 3),

@@ -135,7 +135,8 @@ def test_per_config_block_carries_every_config_and_decode_latency(bench):
          "c2_silu_mul_f16_2048x8960": _kernel(bench, 110_100_480, 18.0)}
     c4 = {"c4_rmsnorm_bf16_16384x3584": _kernel(bench, 234_888_192, 39.5),
           "c4_silu_mul_bf16_16384x18944": _kernel(bench, 1_862_270_976, 286.0)}
-    dec = {f"M={m}": {"rmsnorm_api_us": 15.0, "silu_mul_api_us": 15.5, "rmsnorm_device_us": 3.9,
+    dec = {f"M={m}": {"rmsnorm_api_us": 15.0, "silu_mul_api_us": 15.5, "rmsnorm_call_us": 7.2,
+                      "silu_mul_call_us": 7.4, "rmsnorm_device_us": 3.9,
                       "silu_mul_device_us": 4.1, "graph_per_kernel_us": 1.7 + m / 100,
                       "graph_replay_us": 84 * (1.7 + m / 100)} for m in (1, 2, 4, 8, 32)}
     dec["floor"] = {"empty_kernel_graph_node_us": 1.6, "row_copy_graph_node_us": 1.6}
@@ -149,6 +150,7 @@ def test_per_config_block_carries_every_config_and_decode_latency(bench):
     assert pc["C4_silu_mul_bf16_16384x18944"]["frac"] == round(1_862_270_976 / 286.0 / 1e3 / 8000, 4)
     assert set(pc["C3_decode_f16_latency"]) == {"M1", "M2", "M4", "M8", "M32"}
     assert pc["C3_decode_f16_latency"]["M8"]["graph_node_us"] == 1.78
+    assert pc["C3_decode_f16_latency"]["M8"]["rms_call_us"] == 7.2
     assert all("probe_us" in pc[c] for c in ("C1_rmsnorm_f16_2048x1536", "C2_silu_mul_f16_2048x8960",
                                              "C4_rmsnorm_bf16_16384x3584", "C4_silu_mul_bf16_16384x18944"))
     import json
