@@ -1,4 +1,5 @@
-"""Seeded random decode shapes (1 - 64 rows) through the launchers that use
+"""Seeded random decode shapes (1 - 64 rows; and 1 - 6 rows on deep rows of
+wide outputs) through the launchers that use
 the weight-streaming kernel of csrc/w8a16_stream.h: the W8A16 linear and its
 int8 gate/up + SiLU-and-mul, the 16-bit linear and the 16-bit gate/up +
 SiLU-and-mul.  Their launch plans (rows per workgroup, 4-row weight and x
@@ -32,11 +33,25 @@ def _shapes(seed, count, rows, k_step, k_max, n_max):
     return out
 
 
+def _deep_shapes(seed, count, rows, k_step):
+    """A few rows on deep rows of wide outputs (k 3072 - 12000, n 4100 -
+    12000, n k <= 6e7): the 16-row workgroups of one x set and the dual
+    kernel's 8-row workgroups of 8 waves."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        r, k, n = int(rng.integers(rows[0], rows[1] + 1)), int(rng.integers(3072 // k_step, 12000 // k_step + 1)) * k_step, \
+            int(rng.integers(4100, 12001))
+        if n * k <= 6e7:
+            out.append((r, k, n, F16 if len(out) % 2 == 0 else BF16, bool(rng.integers(0, 2))))
+    return out
+
+
 # (rows, k, n, dtype, x as a row-strided view); n below 8192 keeps the small
 # tiled shapes of 17 - 64 rows out, so every case takes the stream kernel
-W8A16 = _shapes(3031, 12, (1, 48), 16, 4096, 4000)
-W8A16_DUAL = _shapes(3032, 10, (1, 32), 16, 4096, 4000)
-LINEAR16 = _shapes(3033, 12, (1, 64), 8, 4096, 4000)
+W8A16 = _shapes(3031, 12, (1, 48), 16, 4096, 4000) + _deep_shapes(3035, 6, (1, 4), 16)
+W8A16_DUAL = _shapes(3032, 10, (1, 32), 16, 4096, 4000) + _deep_shapes(3036, 4, (2, 4), 16)
+LINEAR16 = _shapes(3033, 12, (1, 64), 8, 4096, 4000) + _deep_shapes(3037, 4, (3, 6), 8)
 GATE_UP16 = _shapes(3034, 10, (1, 32), 8, 4096, 4000)
 
 
