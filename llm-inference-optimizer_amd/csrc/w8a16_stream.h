@@ -301,9 +301,8 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 //     with 16-bit weights) where that leaves every CU a workgroup (one matrix
 //     of int8 weights: 1 - 4 rows) or k >= 8192, since every workgroup
 //     re-reads a long x (half the x re-reads of 8); the dual kernel 4 with
-//     one row of x (or with up to 4
-//     below k = 3072 or on narrow outputs), else 8 (16 as above with more
-//     than 4 rows);
+//     one row of x (or with up to 4 below k = 3072 or on narrow outputs),
+//     else 8 (16 as above with more than 4 rows);
 //   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
 //     8-row workgroups, 8 with 2 - 4 rows at k >= 3072 on outputs that are
 //     not narrow, 1 with 16-row workgroups); else about 14 per CU with
@@ -330,7 +329,7 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 // sets allow (16-bit weights: 2, int8 weights: 2 up to 48 rows, then 1), and
 // 7 waves per CU with more workgroups than CUs (7B down, 64 rows of 16-bit
 // weights: 4 waves 78.9 us, 3 waves 83.4).
-// 2 - 4 rows on deep rows (bench.py --only stream-sweep-m4, the 7B
+// 1 - 4 rows on deep rows (bench.py --only stream-sweep-m4, the 7B
 // projections and MLP at 1 - 4 rows): 16-row workgroups (7B gate/up, 3 / 4
 // rows 12.72 / 12.74 us against 14.34 / 14.87 with 8 rows; 7B down, 4 rows
 // 13.61 vs 15.34; with 16-bit weights from 4 rows, 21.77 vs 22.98), and the
@@ -344,21 +343,22 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int wb = 1) {
   const bool two_sets = rows > 4;  // x rows in two (or more) 4-row sets
   const bool four_sets = rows > 8;  // three or more sets
-  // x re-read by every 8-row workgroup is at least half its weight bytes
-  // (2 rows of x with int8 weights, 4 with 16-bit): on deep rows (k >= 3072
-  // bytes) larger workgroups pay from there -- with one x set only where
-  // 16-row workgroups still give every CU one (so too with one row of x and
-  // int8 weights), or the rows are longer still
-  const bool x_heavy = k >= 3072 && (two_sets || (rows >= 2 * wb && k >= 8192) ||
-                                     ((wb == 1 || rows >= 4) && (n + 15) / 16 >= cus));
+  // 16-row workgroups for one matrix on deep rows (k >= 3072 bytes), where
+  // every 8-row workgroup re-reads a long x: with more than 4 rows of x, and
+  // with 2 - 4 (4 with 16-bit weights, whose x is half as many bytes per
+  // weight byte) at k >= 8192 or where 16-row workgroups still give every CU
+  // one -- there with one row of x of int8 weights too
+  const bool deep16 = k >= 3072 && (two_sets || (rows >= 2 * wb && k >= 8192) ||
+                                    ((wb == 1 || rows >= 4) && (n + 15) / 16 >= cus));
   const bool narrow = n <= 2048 || (n + 7) / 8 < cus;
-  const bool deep_dual = dual && rows >= 2 && !two_sets && x_heavy && !narrow;  // 2 - 4 rows, two matrices
+  // the dual kernel at 2 - 4 rows where one matrix would take 16-row workgroups
+  const bool deep_dual = dual && rows >= 2 && !two_sets && deep16 && !narrow;
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
   if (narrow) {
     sp.rpw = (n + cus - 1) / cus;
     sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
-  } else if ((dual ? two_sets : x_heavy) && k >= 3072 && !(dual && rows > 16)) {
+  } else if (dual ? two_sets && rows <= 16 && k >= 3072 : deep16) {
     sp.rpw = 16;
   }
   if (dual && sp.rpw < 16) sp.rpw = two_sets || deep_dual ? 8 : 4;
