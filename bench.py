@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -135,7 +135,7 @@ class Ctx:
             self.probe.mi355_probe_w8a16_stream.restype = ctypes.c_int
             self.probe.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
             self.probe.mi355_probe_linear16_stream_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(i32)]
-            self.probe.mi355_probe_gate_up16_stream_plan.argtypes = [i32, i32, ctypes.POINTER(i32)]
+            self.probe.mi355_probe_gate_up16_stream_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(i32)]
             self.probe.mi355_probe_w8a16_stream_plan.restype = None
             self.probe.mi355_probe_w8a16_stream_loads.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                                                   vp, vp]
@@ -288,10 +288,10 @@ class Ctx:
         self.probe.mi355_probe_w8a16_stream_plan(rows, k, n, int(dual), cus, out4)
         return tuple(out4)
 
-    def gu16_stream_plan(self, rows, k):
+    def gu16_stream_plan(self, rows, k, n, cus):
         """The 16-bit gate/up + SiLU-and-mul's stream launch plan."""
         out4 = (ctypes.c_int * 4)()
-        self.probe.mi355_probe_gate_up16_stream_plan(rows, k, out4)
+        self.probe.mi355_probe_gate_up16_stream_plan(rows, k, n, cus, out4)
         return tuple(out4)
 
     def l16_stream_plan(self, rows, k, n, cus):
@@ -1078,6 +1078,18 @@ def run_only(ctx, args, sets):
         del sets
         torch.cuda.empty_cache()
         print(json.dumps({"linear16_stream_sweep": l16_stream_sweep(ctx)}), flush=True)
+    elif args.only == "stream-sweep16-k":  # 9 - 16 rows, k < 3072, with 16-row workgroups too
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP16_K_SHAPES, True),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP16_K_SHAPES, True)}),
+              flush=True)
+    elif args.only == "stream-sweep-dualn":  # the dual kernels by workgroups per CU
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_DUALN_SHAPES, True),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_DUALN_SHAPES, True)}),
+              flush=True)
     elif args.only == "stream-sweep-m4":  # 1 - 4 rows on the deep projections that are not narrow
         del sets
         torch.cuda.empty_cache()
@@ -1481,6 +1493,20 @@ W8_STREAM_SWEEP_R8_SHAPES = [("gateup_M4", 4, 1536, 8960, False), ("gateup_M8", 
                              ("gateup7b_M8", 8, 3584, 18944, False), ("down7b_M8", 8, 18944, 3584, False),
                              ("o7b_M8", 8, 3584, 3584, False), ("dual_gateup_M8", 8, 1536, 8960, True),
                              ("dual7b_M4", 4, 3584, 18944, True), ("dual7b_M8", 8, 3584, 18944, True)]
+# 9 - 16 rows on the shallower wide projections (k < 3072), with 16-row
+# workgroups too: each 8-row workgroup re-reads x worth 2 - 4 times its weights
+W8_STREAM_SWEEP16_K_SHAPES = [("gateup_M12", 12, 1536, 8960, False), ("gateup_M16", 16, 1536, 8960, False),
+                              ("gateup0.5b_M16", 16, 896, 4864, False), ("gateup_M10", 10, 1536, 8960, False),
+                              ("dual_gateup_M12", 12, 1536, 8960, True), ("dual0.5b_M16", 16, 896, 4864, True)]
+GU16_SWEEP16_K_SHAPES = [("gu1.5b_M12", 12, 1536, 8960), ("gu0.5b_M16", 16, 896, 4864)]
+# the dual kernels where 8-row workgroups number few per CU (0.5B MLP: 608)
+# against more (1.5B: 1120, 3B: 1376), 5 - 32 rows
+W8_STREAM_SWEEP_DUALN_SHAPES = [("dual0.5b_M6", 6, 896, 4864, True), ("dual0.5b_M12", 12, 896, 4864, True),
+                                ("dual0.5b_M24", 24, 896, 4864, True), ("dual3b_M8", 8, 2048, 11008, True),
+                                ("dual3b_M16", 16, 2048, 11008, True), ("dual_gateup_M16", 16, 1536, 8960, True),
+                                ("dual_gateup_M24", 24, 1536, 8960, True)]
+GU16_SWEEP_DUALN_SHAPES = [("gu0.5b_M10", 10, 896, 4864), ("gu0.5b_M12", 12, 896, 4864),
+                           ("gu3b_M16", 16, 2048, 11008), ("gu0.5b_M24", 24, 896, 4864)]
 # 1 - 4 rows of x (one x set) on the deep projections that are not narrow
 # (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
 W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M1", 1, 3584, 18944, False), ("dual7b_M1", 1, 3584, 18944, True),
@@ -1642,6 +1668,7 @@ def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False, rpws=(4, 6, 8
     (within 2e-3 of the largest output)."""
     torch = ctx.torch
     F16 = torch.float16
+    cus = torch.cuda.get_device_properties(ctx.dev).multi_processor_count
     out = {}
     for label, M, K, N in shapes:
         sets = n_sets(2 * N * K * 2)
@@ -1658,7 +1685,7 @@ def gu16_stream_sweep(ctx, shapes=GU16_SWEEP_SHAPES, wide16=False, rpws=(4, 6, 8
             ctx, "gu16", label, M, -(-K // 128), True, 2, wide16, o, ref, lib_calls,
             lambda rpw, r4, waves, u, x=x, ws=ws, o=o: [ctx.gate_up16_stream_call(x, wg, wu, o, rpw, r4, waves, u)
                                                          for wg, wu in ws],
-            plan=ctx.gu16_stream_plan(M, K), rpws=rpws)
+            plan=ctx.gu16_stream_plan(M, K, N, cus), rpws=rpws)
         del ws
         torch.cuda.empty_cache()
     return out

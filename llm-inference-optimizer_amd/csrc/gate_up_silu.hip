@@ -385,14 +385,20 @@ int gate_up_typed(const GateUpParams& p, hipStream_t s) {
                            (15 * p.ws + p.k) * tb < (int64_t{1} << 32);
   const W8Params w{p.x, p.wg, nullptr, nullptr, p.out, p.rows, p.k, p.n_out, p.xs, p.ws, p.os, MI355_F32, -1,
                    p.wu, nullptr};
+  auto stream = [&]() {
+    int cus = 0;
+    const int st = compute_units(&cus);
+    if (st != MI355_OK) return st;
+    return w8_stream_launch<T, TO, true, 2>(w, gu16_stream_plan(p.rows, p.k, p.n_out, cus), s);
+  };
   if (p.rows <= 16) {
-    if (stream_fits) return w8_stream_launch<T, TO, true, 2>(w, gu16_stream_plan(p.rows, p.k), s);
+    if (stream_fits) return stream();
     return p.rows <= 8 ? gate_up_shape<T, TO, 1>(p, s) : gate_up_shape<T, TO, 2>(p, s);
   }
   const bool tiled_fits = int64_t{256} * p.xs * tb < (int64_t{1} << 31) && int64_t{128} * p.ws * tb < (int64_t{1} << 31);
   const int bn = p.n_out > 10000 ? 128 : 64;
   if (tiled_fits && (p.rows > 32 || (p.n_out + bn - 1) / bn >= 128)) return gate_up_tiled<T, TO>(p, s);
-  if (stream_fits) return w8_stream_launch<T, TO, true, 2>(w, gu16_stream_plan(p.rows, p.k), s);
+  if (stream_fits) return stream();
   if (p.rows <= 24) return gate_up_shape<T, TO, 3>(p, s);
   return gate_up_shape<T, TO, 4>(p, s);
 }

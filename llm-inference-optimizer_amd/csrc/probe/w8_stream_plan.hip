@@ -243,9 +243,10 @@ extern "C" __attribute__((visibility("default"))) int mi355_probe_stream_max_thr
 }
 
 // The 16-bit gate/up + SiLU-and-mul's launch plan (gu16_stream_plan) for
-// `rows` x k: out4 = {rpw, r4, waves, u}.
-extern "C" __attribute__((visibility("default"))) void mi355_probe_gate_up16_stream_plan(int rows, int k, int* out4) {
-  const mi355::StreamPlan sp = mi355::gu16_stream_plan(rows, k);
+// `rows` x k x n on `cus` CUs: out4 = {rpw, r4, waves, u}.
+extern "C" __attribute__((visibility("default"))) void mi355_probe_gate_up16_stream_plan(int rows, int k, int n, int cus,
+                                                                                          int* out4) {
+  const mi355::StreamPlan sp = mi355::gu16_stream_plan(rows, k, n, cus);
   out4[0] = sp.rpw;
   out4[1] = sp.r4;
   out4[2] = sp.waves;

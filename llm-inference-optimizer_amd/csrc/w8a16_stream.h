@@ -301,8 +301,9 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 //     with 16-bit weights) where that leaves every CU a workgroup (one matrix
 //     of int8 weights: 1 - 4 rows) or k >= 8192, since every workgroup
 //     re-reads a long x (half the x re-reads of 8); the dual kernel 4 with
-//     one row of x (or with up to 4 below k = 3072 or on narrow outputs),
-//     else 8 (16 as above with more than 4 rows);
+//     one row of x (or with up to 4 below k = 3072 or on narrow outputs, or
+//     with more where 8-row workgroups would number under 4 per CU), else 8
+//     (16 as above with more than 4 rows);
 //   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
 //     8-row workgroups, 8 with 2 - 4 rows at k >= 3072 on outputs that are
 //     not narrow, 1 with 16-row workgroups); else about 14 per CU with
@@ -361,7 +362,10 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   } else if (dual ? two_sets && rows <= 16 && k >= 3072 : deep16) {
     sp.rpw = 16;
   }
-  if (dual && sp.rpw < 16) sp.rpw = two_sets || deep_dual ? 8 : 4;
+  // the dual kernel's 8-row workgroups with more than 4 rows of x only where
+  // they number at least 4 per CU (0.5B MLP, 608 of them: 4-row workgroups
+  // 5 - 10% faster at 6 - 32 rows)
+  if (dual && sp.rpw < 16) sp.rpw = (two_sets && (n + 7) / 8 >= 4 * cus) || deep_dual ? 8 : 4;
   sp.r4 = sp.rpw <= 4 ? 1 : (sp.rpw <= 8 ? 2 : 4);
   // fewer 4-row weight sets where this many x sets leave no registers for more
   while (sp.r4 > 1 && stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, wb) == 0) {
@@ -399,15 +403,31 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
 // chunks in flight up to 4 rows of x (39.84 vs 42.77 us), 16 rows and 8
 // waves with one chunk beyond, where every workgroup re-reads the long x
 // (42.07 vs 44.48 us); 9 - 16 rows (bench.py --only stream-sweep16 and
-// stream-sweep16-wide), one chunk in flight, up to k = 2048 8 rows per
-// workgroup and 2 waves (1.5B, 16 rows 13.44 vs 15.73 us), deeper 16 rows
-// and one wave (7B, 16 rows 46.1 vs 50.3 us for 8 rows and 8 waves).
-inline StreamPlan gu16_stream_plan(int rows, int k) {
+// stream-sweep16-wide), one chunk in flight, below k = 2048 8 rows per
+// workgroup and 2 waves (1.5B, 16 rows 13.44 vs 15.73 us) or 4 rows where
+// 8-row workgroups would number under 4 per CU (0.5B, 10 / 12 rows 6.00 /
+// 5.92 us against 6.62 / 6.50; bench.py --only stream-sweep-dualn), from
+// k = 2048 16 rows and about 5 waves per CU (7B, 16 rows one wave, 46.1 vs
+// 50.3 us for 8 rows and 8 waves; 3B, 16 rows two, 18.43 vs 20.06).
+inline StreamPlan gu16_stream_plan(int rows, int k, int n, int cus) {
   StreamPlan sp{16, 4, 8, 1};
-  if (rows > 16) sp = StreamPlan{8, 2, 2, 1};  // 17 - 32 rows: 0.5B, 32 rows 9.04 us vs 10.52 for skinny tiles
-  else if (rows > 8) sp = k <= 2048 ? StreamPlan{8, 2, 2, 1} : StreamPlan{16, 4, 1, 1};
-  else if (k <= 2048) sp = StreamPlan{4, 1, 2, 2};
-  else if (rows <= 4) sp = StreamPlan{4, 1, 8, 2};
+  if (rows > 16) {
+    sp = StreamPlan{8, 2, 2, 1};  // 17 - 32 rows: 0.5B, 32 rows 9.04 us vs 10.52 for skinny tiles
+  } else if (rows > 8) {
+    if (k < 2048) {
+      // 4-row workgroups where 8-row ones would number under 4 per CU
+      sp = (n + 7) / 8 < 4 * cus ? StreamPlan{4, 1, 2, 1} : StreamPlan{8, 2, 2, 1};
+    } else {
+      // 16-row workgroups with about 5 waves per CU (3B, 16 rows: 2 waves)
+      const int64_t wgs = (n + 15) / 16;
+      const int64_t w = (5 * static_cast<int64_t>(cus) + wgs / 2) / wgs;
+      sp = StreamPlan{16, 4, static_cast<int>(w < 1 ? 1 : (w > 8 ? 8 : w)), 1};
+    }
+  } else if (k <= 2048) {
+    sp = StreamPlan{4, 1, 2, 2};
+  } else if (rows <= 4) {
+    sp = StreamPlan{4, 1, 8, 2};
+  }
   const int nchunk = (k + 127) / 128;  // no more waves than 128-column chunks
   if (sp.waves > nchunk) sp.waves = nchunk;
   const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, true, 2) / 64;

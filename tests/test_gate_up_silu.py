@@ -78,6 +78,9 @@ def _check_vs_oracle(orc, got16, got32, x, wg, wu, dt):
     (12, 1536, 8960, F16), (13, 136, 1000, BF16), (16, 3584, 2000, F16), (9, 2056, 37, BF16),
     (11, 3104, 2900, BF16), (32, 896, 4864, BF16), (21, 3104, 2900, F16),
     (17, 2048, 1000, F16),
+    # 9 - 16 rows: 4-row workgroups where 8-row ones would number under 4 per
+    # CU (ragged last workgroup), 16-row ones of about 5 waves per CU from k = 2048
+    (10, 896, 4874, F16), (12, 2048, 11008, BF16),
     # prefill rows: the tiled GEMM (each of its three launch shapes, k tails, ragged edges)
     (64, 1536, 1000, F16), (200, 640, 10240, BF16), (300, 1552, 520, F16), (257, 96, 333, BF16),
     # 17 - 64 rows: the small tiled shapes (32 x 64, 32 x 128 for n_out > 10000, 64 x 64)

@@ -32,7 +32,7 @@ def probe():
     lib = ctypes.CDLL(str(PROBE))
     i32 = ctypes.c_int
     lib.mi355_probe_w8a16_stream_plan.argtypes = [i32, i32, i32, i32, i32, ctypes.POINTER(i32)]
-    lib.mi355_probe_gate_up16_stream_plan.argtypes = [i32, i32, ctypes.POINTER(i32)]
+    lib.mi355_probe_gate_up16_stream_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(i32)]
     lib.mi355_probe_stream_max_threads.argtypes = [i32] * 5
     lib.mi355_probe_linear16_stream_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(i32)]
     return lib
@@ -73,10 +73,11 @@ def test_linear16_plan_is_launchable(probe, cus):
         _check(tuple(out), rows, 2 * k, 1, probe, wb=2)
 
 
-def test_gate_up16_plan_is_launchable(probe):
+@pytest.mark.parametrize("cus", [80, 256, 304])
+def test_gate_up16_plan_is_launchable(probe, cus):
     out = (ctypes.c_int * 4)()
-    for rows, k in itertools.product(range(1, 33), (8, 24, 136, 896, 1536, 2048, 2056, 3584, 8192)):
-        probe.mi355_probe_gate_up16_stream_plan(rows, k, out)
+    for rows, k, n in itertools.product(range(1, 33), (8, 24, 136, 896, 1536, 2048, 2056, 3584, 8192), NS):
+        probe.mi355_probe_gate_up16_stream_plan(rows, k, n, cus, out)
         _check(tuple(out), rows, 2 * k, 2, probe, wb=2)
 
 
@@ -136,4 +137,25 @@ def test_plans_picked_by_the_deep_row_sweep(probe):
     assert _plan(probe, w8, 8, 3584, 18944, 1, 256) == (16, 4, 1, 1)
     assert _plan(probe, l16, 4, 18944, 3584, 256)[:3] == (16, 4, 8)
     assert _plan(probe, l16, 3, 18944, 3584, 256)[0] == 8
+
+
+def test_dual_plans_by_workgroups_per_cu(probe):
+    """The gate/up + SiLU-and-mul plans the sweep by workgroups per CU
+    picked (256 CUs): with more than 4 (int8) or 8 (16-bit) rows of x, 4-row
+    workgroups of 2 waves where 8-row ones would number under 4 per CU (the
+    0.5B MLP, k 896 x n 4864), 8-row ones of 2 waves where they do not (1.5B,
+    k 1536 x n 8960; int8 3B, k 2048 x n 11008); 16-bit weights from k = 2048
+    on 16-row workgroups of about 5 waves per CU (3B: 2, 7B: 1)."""
+    w8 = probe.mi355_probe_w8a16_stream_plan
+    gu = probe.mi355_probe_gate_up16_stream_plan
+    for rows in (6, 8, 12, 16, 24, 32):
+        assert _plan(probe, w8, rows, 896, 4864, 1, 256)[:3] == (4, 1, 2), rows
+        assert _plan(probe, w8, rows, 1536, 8960, 1, 256)[:3] == (8, 2, 2), rows
+    assert _plan(probe, w8, 16, 2048, 11008, 1, 256)[:3] == (8, 2, 2)
+    for rows in (10, 12, 16):
+        assert _plan(probe, gu, rows, 896, 4864, 256) == (4, 1, 2, 1), rows
+        assert _plan(probe, gu, rows, 1536, 8960, 256) == (8, 2, 2, 1), rows
+        assert _plan(probe, gu, rows, 2048, 11008, 256) == (16, 4, 2, 1), rows
+        assert _plan(probe, gu, rows, 3584, 18944, 256) == (16, 4, 1, 1), rows
+    assert _plan(probe, gu, 24, 896, 4864, 256) == (8, 2, 2, 1)
     assert _plan(probe, w8, 8, 3584, 3584, 0, 256)[0] == 16
