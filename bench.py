@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1090,6 +1090,12 @@ def run_only(ctx, args, sets):
         print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_DUALN_SHAPES, True),
                           "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_DUALN_SHAPES, True)}),
               flush=True)
+    elif args.only == "stream-sweep-dual32":  # 17 - 32 rows of the gate/up kernels vs the small tiles
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_DUAL32_SHAPES, True),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_DUAL32_SHAPES, True)}),
+              flush=True)
     elif args.only == "stream-sweep-m4":  # 1 - 4 rows on the deep projections that are not narrow
         del sets
         torch.cuda.empty_cache()
@@ -1507,6 +1513,14 @@ W8_STREAM_SWEEP_DUALN_SHAPES = [("dual0.5b_M6", 6, 896, 4864, True), ("dual0.5b_
                                 ("dual_gateup_M24", 24, 1536, 8960, True)]
 GU16_SWEEP_DUALN_SHAPES = [("gu0.5b_M10", 10, 896, 4864), ("gu0.5b_M12", 12, 896, 4864),
                            ("gu3b_M16", 16, 2048, 11008), ("gu0.5b_M24", 24, 896, 4864)]
+# 17 - 32 rows of the gate/up + SiLU-and-mul kernels on the MLPs where the
+# launchers take the small tiled shapes (>= 128 tile columns)
+W8_STREAM_SWEEP_DUAL32_SHAPES = [("dual_gateup_M18", 18, 1536, 8960, True), ("dual_gateup_M20", 20, 1536, 8960, True),
+                                 ("dual_gateup_M24", 24, 1536, 8960, True), ("dual_gateup_M28", 28, 1536, 8960, True),
+                                 ("dual_gateup_M32", 32, 1536, 8960, True), ("dual3b_M24", 24, 2048, 11008, True),
+                                 ("dual3b_M32", 32, 2048, 11008, True), ("dual7b_M20", 20, 3584, 18944, True)]
+GU16_SWEEP_DUAL32_SHAPES = [("gu1.5b_M20", 20, 1536, 8960), ("gu1.5b_M24", 24, 1536, 8960),
+                            ("gu3b_M24", 24, 2048, 11008)]
 # 1 - 4 rows of x (one x set) on the deep projections that are not narrow
 # (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
 W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M1", 1, 3584, 18944, False), ("dual7b_M1", 1, 3584, 18944, True),

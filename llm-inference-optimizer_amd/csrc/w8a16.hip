@@ -546,7 +546,12 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   if (x_fits && (p.rows <= 8 || (p.rows <= 16 && !wide_mid)))
     return w8_stream_launch<T, TO, DUAL>(p, w8_stream_plan(p.rows, p.k, p.n, DUAL, cus), s);
   if (p.rows <= 16) return w8_skinny_shape<T, TO, 2, DUAL>(p, s, cus);
-  if (small_tiles_pay(p.rows, p.n) && tiled_fits(p, DUAL)) return w8_tiled_small<T, TO, DUAL>(p, s);
+  // The int8 gate/up + SiLU-and-mul at 17 - 24 rows of MLPs with k <= 2048:
+  // the stream kernel's 8-row workgroups of one wave beat the small tiles
+  // (1.5B, 18 / 24 rows 15.46 / 15.50 -> 13.40 / 13.77 us; from 28 rows the
+  // tiles lead, 15.53 vs 15.85, and at the 7B MLP, 20 rows 40.7 vs 45.8).
+  const bool dual_stream = DUAL && p.rows <= 24 && p.k <= 2048;
+  if (small_tiles_pay(p.rows, p.n) && tiled_fits(p, DUAL) && !dual_stream) return w8_tiled_small<T, TO, DUAL>(p, s);
   // 17 - 32 rows where the small tiles do not pay: the stream kernel with 6
   // or 8 x sets (1.5B down, 32 rows 20.6 -> 13.0 us; 7B down 44.4 -> 30.1;
   // 0.5B down 12.6 -> 7.3; the int8 gate/up + SiLU-and-mul, 0.5B 9.7 -> 8.9),

@@ -305,8 +305,9 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
 //     with more where 8-row workgroups would number under 4 per CU), else 8
 //     (16 as above with more than 4 rows);
 //   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
-//     8-row workgroups, 8 with 2 - 4 rows at k >= 3072 on outputs that are
-//     not narrow, 1 with 16-row workgroups); else about 14 per CU with
+//     8-row workgroups -- 1 beyond 16 rows --, 8 with 2 - 4 rows at k >= 3072
+//     on outputs that are not narrow, 1 with 16-row workgroups); else about
+//     14 per CU with
 //     up to 4 rows of x, 12 (one workgroup per CU) or 10 with more, 7 for
 //     16-row workgroups (6 with more than 8 rows of x); at least 2 (but for
 //     the dual kernel's 1) and at most 16 waves (8 where stream_max_threads
@@ -376,8 +377,11 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   int64_t waves;
   int min_waves = 2;
   if (dual) {
-    waves = sp.rpw == 16 ? 1 : (two_sets ? 2 : (deep_dual ? 8 : 3));
-    min_waves = sp.rpw == 16 ? 1 : 2;
+    // 8-row workgroups with 6 or 8 x sets: one wave (1.5B MLP, 24 rows 13.77
+    // us against 15.50 with two; 3B, 32 rows 21.29 vs 25.68)
+    const bool one_wave = sp.rpw == 16 || (sp.rpw == 8 && rows > 16);
+    waves = one_wave ? 1 : (two_sets ? 2 : (deep_dual ? 8 : 3));
+    min_waves = one_wave ? 1 : 2;
   } else {
     const int per_cu = sp.rpw == 16 ? (four_sets && rows <= 16 ? 6 : 7)
                                     : (four_sets ? (wgs <= cus ? 8 : (rows > 32 ? 7 : 5))

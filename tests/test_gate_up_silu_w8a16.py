@@ -72,6 +72,10 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
     # 5 - 32 rows where 8-row workgroups would number under 4 per CU: 4-row
     # workgroups of 2 waves (ragged last workgroup)
     (6, 896, 4874, BF16), (12, 896, 4864, F16), (24, 1024, 3002, BF16),
+    # 17 - 32 rows on 8-row workgroups of one wave: at 17 - 24 rows of MLPs
+    # with k <= 2048 in place of the small tiles (ragged last workgroup), and
+    # where the small tiles do not pay (3B MLP)
+    (20, 1536, 8964, F16), (24, 2048, 11008, BF16), (30, 2048, 11008, F16),
     # 9 - 16 rows: three and four x sets; the 7B MLP and k >= 3072 with n > 2048 (16-row
     # workgroups, one wave; a partial last chunk and a ragged last workgroup at k 3104 x n 2900)
     (12, 1536, 8960, F16), (13, 272, 1000, BF16), (16, 1552, 520, F16), (16, 3584, 18944, BF16),

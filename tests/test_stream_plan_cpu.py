@@ -144,14 +144,16 @@ def test_dual_plans_by_workgroups_per_cu(probe):
     picked (256 CUs): with more than 4 (int8) or 8 (16-bit) rows of x, 4-row
     workgroups of 2 waves where 8-row ones would number under 4 per CU (the
     0.5B MLP, k 896 x n 4864), 8-row ones of 2 waves where they do not (1.5B,
-    k 1536 x n 8960; int8 3B, k 2048 x n 11008); 16-bit weights from k = 2048
+    k 1536 x n 8960; int8 3B, k 2048 x n 11008), of one wave beyond 16 rows
+    of x; 16-bit weights from k = 2048
     on 16-row workgroups of about 5 waves per CU (3B: 2, 7B: 1)."""
     w8 = probe.mi355_probe_w8a16_stream_plan
     gu = probe.mi355_probe_gate_up16_stream_plan
     for rows in (6, 8, 12, 16, 24, 32):
         assert _plan(probe, w8, rows, 896, 4864, 1, 256)[:3] == (4, 1, 2), rows
-        assert _plan(probe, w8, rows, 1536, 8960, 1, 256)[:3] == (8, 2, 2), rows
+        assert _plan(probe, w8, rows, 1536, 8960, 1, 256)[:3] == (8, 2, 2 if rows <= 16 else 1), rows
     assert _plan(probe, w8, 16, 2048, 11008, 1, 256)[:3] == (8, 2, 2)
+    assert _plan(probe, w8, 24, 2048, 11008, 1, 256)[:3] == (8, 2, 1)  # 6 or 8 x sets: one wave
     for rows in (10, 12, 16):
         assert _plan(probe, gu, rows, 896, 4864, 256) == (4, 1, 2, 1), rows
         assert _plan(probe, gu, rows, 1536, 8960, 256) == (8, 2, 2, 1), rows
