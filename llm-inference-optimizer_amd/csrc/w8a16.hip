@@ -14,7 +14,8 @@
 // Four kernels, picked by the launcher:
 //   w8a16_stream   rows <= 16 (decode; w8a16_stream.h), and 17 - 32 (33 -
 //                  48 for one matrix) where the small tiled shapes do not
-//                  pay: weight streaming with
+//                  pay (and the gate/up + SiLU-and-mul at 17 - 24 rows with
+//                  k <= 2048): weight streaming with
 //                  lane-coalesced loads, every weight byte read once per call
 //                  at HBM bandwidth, MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
 //   w8a16_skinny   9 - 32 rows of wide outputs with 2048 < k < 3072, x
