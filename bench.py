@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "stream-sweep-3b14b", "stream-sweep-bal", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1096,6 +1096,21 @@ def run_only(ctx, args, sets):
         print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_DUAL32_SHAPES, True),
                           "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_DUAL32_SHAPES, True)}),
               flush=True)
+    elif args.only == "stream-sweep-3b14b":  # the 3B and 14B shapes
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_3B14B_SHAPES, True),
+                          "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP_3B14B_SHAPES),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_3B14B_SHAPES, True)}),
+              flush=True)
+    elif args.only == "stream-sweep-bal":  # rows per workgroup that balance the CUs
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_BAL_SHAPES, True,
+                                                                rpws=STREAM_BAL_RPWS),
+                          "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP_BAL_SHAPES, rpws=STREAM_BAL_RPWS),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_BAL_SHAPES, True,
+                                                                      rpws=STREAM_BAL_RPWS)}), flush=True)
     elif args.only == "stream-sweep-m4":  # 1 - 4 rows on the deep projections that are not narrow
         del sets
         torch.cuda.empty_cache()
@@ -1521,6 +1536,27 @@ W8_STREAM_SWEEP_DUAL32_SHAPES = [("dual_gateup_M18", 18, 1536, 8960, True), ("du
                                  ("dual3b_M32", 32, 2048, 11008, True), ("dual7b_M20", 20, 3584, 18944, True)]
 GU16_SWEEP_DUAL32_SHAPES = [("gu1.5b_M20", 20, 1536, 8960), ("gu1.5b_M24", 24, 1536, 8960),
                             ("gu3b_M24", 24, 2048, 11008)]
+# Qwen2.5-3B (hidden 2048, MLP 11008) and 14B (hidden 5120, MLP 13824)
+# projections and MLPs, which the fitted sweeps did not sample
+W8_STREAM_SWEEP_3B14B_SHAPES = [("gateup3b_M8", 8, 2048, 11008, False), ("gateup3b_M24", 24, 2048, 11008, False),
+                                ("down3b_M8", 8, 11008, 2048, False), ("down3b_M32", 32, 11008, 2048, False),
+                                ("o3b_M8", 8, 2048, 2048, False), ("gateup14b_M8", 8, 5120, 13824, False),
+                                ("down14b_M8", 8, 13824, 5120, False), ("down14b_M32", 32, 13824, 5120, False),
+                                ("o14b_M8", 8, 5120, 5120, False), ("dual14b_M8", 8, 5120, 13824, True),
+                                ("dual14b_M16", 16, 5120, 13824, True), ("dual3b_M4", 4, 2048, 11008, True)]
+L16_SWEEP_3B14B_SHAPES = [("down3b_M8", 8, 11008, 2048), ("down3b_M32", 32, 11008, 2048),
+                          ("down14b_M8", 8, 13824, 5120), ("down14b_M16", 16, 13824, 5120)]
+GU16_SWEEP_3B14B_SHAPES = [("gu3b_M8", 8, 2048, 11008), ("gu14b_M8", 8, 5120, 13824), ("gu14b_M16", 16, 5120, 13824)]
+# rows per workgroup that spread the weight rows evenly over the CUs (10 at
+# n 5120, 14 at n 3584, 15 at n 18944) beside 8, 12 and 16
+STREAM_BAL_RPWS = (8, 10, 12, 14, 15, 16)
+W8_STREAM_SWEEP_BAL_SHAPES = [("down14b_M8", 8, 13824, 5120, False), ("down14b_M32", 32, 13824, 5120, False),
+                              ("o14b_M8", 8, 5120, 5120, False), ("gateup14b_M8", 8, 5120, 13824, False),
+                              ("down7b_M8", 8, 18944, 3584, False), ("o7b_M8", 8, 3584, 3584, False),
+                              ("gateup7b_M8", 8, 3584, 18944, False), ("down7b_M4", 4, 18944, 3584, False),
+                              ("dual14b_M8", 8, 5120, 13824, True), ("gateup3b_M24", 24, 2048, 11008, False)]
+L16_SWEEP_BAL_SHAPES = [("down14b_M8", 8, 13824, 5120), ("down7b_M8", 8, 18944, 3584)]
+GU16_SWEEP_BAL_SHAPES = [("gu14b_M8", 8, 5120, 13824)]
 # 1 - 4 rows of x (one x set) on the deep projections that are not narrow
 # (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
 W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M1", 1, 3584, 18944, False), ("dual7b_M1", 1, 3584, 18944, True),
@@ -1643,7 +1679,7 @@ L16_SWEEP_SHAPES = [("down1.5b_M1", 1, 8960, 1536), ("down1.5b_M8", 8, 8960, 153
                     ("down0.5b_M8", 8, 4864, 896), ("down1.5b_M4", 4, 8960, 1536)]
 
 
-def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
+def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES, rpws=(4, 6, 8, 12, 16)):
     """The 16-bit linear at decode rows: the library's launch
     (mi355_linear16_fwd) against the weight-streaming kernel of
     w8a16_stream.h with one 16-bit matrix over launch shapes (rows per
@@ -1667,7 +1703,7 @@ def l16_stream_sweep(ctx, shapes=L16_SWEEP_SHAPES):
             ctx, "l16", label, M, -(-K // 128), False, 2, True, o, ref, lib_calls,
             lambda rpw, r4, waves, u, x=x, ws=ws, o=o: [ctx.linear16_stream_call(x, w, o, rpw, r4, waves, u)
                                                          for w in ws],
-            plan=ctx.l16_stream_plan(M, K, N, cus))
+            plan=ctx.l16_stream_plan(M, K, N, cus), rpws=rpws)
         del ws
         torch.cuda.empty_cache()
     return out

@@ -288,6 +288,18 @@ __global__ __launch_bounds__(stream_max_threads(R4, MT4, U, DUAL, WB)) void w8a1
   }
 }
 
+// Rows per workgroup of a plan of 16-row workgroups, spread evenly over the
+// CUs: the fewest rounds of 16 rows per CU, then as few rows per workgroup as
+// fill those rounds (8 - 16 where n >= 8 CUs).  Qwen2.5-14B, n 5120: 10 rows
+// (512 workgroups, two per CU, where 16 rows leave 320: the down projection
+// with 8 rows of x 22.19 -> 17.79 us, the 16-bit one 32.96 -> 25.41); 7B,
+// n 3584: 14 (256), n 18944: 15 (1263) (bench.py --only stream-sweep-bal).
+inline int balanced_rows16(int n, int cus) {
+  const int64_t per_round = 16 * static_cast<int64_t>(cus);
+  const int64_t rounds = (n + per_round - 1) / per_round;
+  return static_cast<int>((n + rounds * cus - 1) / (rounds * cus));
+}
+
 // Launch plan for `rows` <= 64 rows of x (32 when dual) against [n, k] int8
 // weights (two matrices when dual), fitted to a graph-timed sweep of rows per workgroup x
 // waves x chunks in flight on MI355X over the Qwen2.5-0.5B, 1.5B and 7B
@@ -357,16 +369,18 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   const bool deep_dual = dual && rows >= 2 && !two_sets && deep16 && !narrow;
   const int nchunk = (k + 255) / 256;
   StreamPlan sp{8, 2, 1, 1};
+  bool wg16 = false;  // the 16-row class (balanced_rows16)
   if (narrow) {
     sp.rpw = (n + cus - 1) / cus;
     sp.rpw = sp.rpw < 4 ? 4 : (sp.rpw > 8 ? 8 : sp.rpw);
   } else if (dual ? two_sets && rows <= 16 && k >= 3072 : deep16) {
-    sp.rpw = 16;
+    wg16 = true;
+    sp.rpw = balanced_rows16(n, cus);
   }
   // the dual kernel's 8-row workgroups with more than 4 rows of x only where
   // they number at least 4 per CU (0.5B MLP, 608 of them: 4-row workgroups
   // 5 - 10% faster at 6 - 32 rows)
-  if (dual && sp.rpw < 16) sp.rpw = (two_sets && (n + 7) / 8 >= 4 * cus) || deep_dual ? 8 : 4;
+  if (dual && !wg16) sp.rpw = (two_sets && (n + 7) / 8 >= 4 * cus) || deep_dual ? 8 : 4;
   sp.r4 = sp.rpw <= 4 ? 1 : (sp.rpw <= 8 ? 2 : 4);
   // fewer 4-row weight sets where this many x sets leave no registers for more
   while (sp.r4 > 1 && stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, wb) == 0) {
@@ -379,11 +393,11 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   if (dual) {
     // 8-row workgroups with 6 or 8 x sets: one wave (1.5B MLP, 24 rows 13.77
     // us against 15.50 with two; 3B, 32 rows 21.29 vs 25.68)
-    const bool one_wave = sp.rpw == 16 || (sp.rpw == 8 && rows > 16);
+    const bool one_wave = wg16 || (sp.rpw == 8 && rows > 16);
     waves = one_wave ? 1 : (two_sets ? 2 : (deep_dual ? 8 : 3));
     min_waves = one_wave ? 1 : 2;
   } else {
-    const int per_cu = sp.rpw == 16 ? (four_sets && rows <= 16 ? 6 : 7)
+    const int per_cu = wg16 && sp.r4 == 4 ? (four_sets && rows <= 16 ? 6 : 7)
                                     : (four_sets ? (wgs <= cus ? 8 : (rows > 32 ? 7 : 5))
                                                  : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
@@ -393,6 +407,9 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   if (waves > nchunk) waves = nchunk;
   if (waves < min_waves) waves = nchunk < min_waves ? nchunk : min_waves;
   if (wgs <= cus && waves > 8) waves = waves / 4 * 4;
+  // one workgroup per CU: 8 waves, not 7, so each SIMD carries two (7B down
+  // with 14-row workgroups, 8 rows of x: 15.28 us against 15.53 with 6)
+  if (wgs <= cus && waves == 7 && max_waves >= 8 && nchunk >= 8) waves = 8;
   sp.waves = static_cast<int>(waves);
   return sp;
 }
@@ -423,15 +440,20 @@ inline StreamPlan gu16_stream_plan(int rows, int k, int n, int cus) {
       sp = (n + 7) / 8 < 4 * cus ? StreamPlan{4, 1, 2, 1} : StreamPlan{8, 2, 2, 1};
     } else {
       // 16-row workgroups with about 5 waves per CU (3B, 16 rows: 2 waves)
-      const int64_t wgs = (n + 15) / 16;
+      sp = StreamPlan{16, 4, 1, 1};
+      if (n >= 8 * cus) sp.rpw = balanced_rows16(n, cus);
+      const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
       const int64_t w = (5 * static_cast<int64_t>(cus) + wgs / 2) / wgs;
-      sp = StreamPlan{16, 4, static_cast<int>(w < 1 ? 1 : (w > 8 ? 8 : w)), 1};
+      sp.waves = static_cast<int>(w < 1 ? 1 : (w > 8 ? 8 : w));
     }
   } else if (k <= 2048) {
     sp = StreamPlan{4, 1, 2, 2};
   } else if (rows <= 4) {
     sp = StreamPlan{4, 1, 8, 2};
+  } else if (n >= 8 * cus) {
+    sp.rpw = balanced_rows16(n, cus);  // 14B, 8 rows: 14 rows 44.03 us against 46.84 with 16
   }
+  if (sp.rpw <= 8 && sp.r4 == 4) sp.r4 = 2;
   const int nchunk = (k + 127) / 128;  // no more waves than 128-column chunks
   if (sp.waves > nchunk) sp.waves = nchunk;
   const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, true, 2) / 64;
@@ -461,7 +483,7 @@ inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
   if (sp.rpw <= 8 && (n <= 2048 || (n + 7) / 8 < cus) && rows <= 8) {
     sp.u = 2;
     per_cu = rows <= 4 ? 12 : 8;
-  } else if (sp.rpw == 16 && rows > 8) {
+  } else if (sp.rpw > 8 && rows > 8) {
     per_cu = 7;
   }
   if (per_cu > 0) {
@@ -472,6 +494,7 @@ inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
     if (waves > nchunk) waves = nchunk;
     if (waves < 1) waves = 1;
     if (wgs <= cus && waves > 8) waves = waves / 4 * 4;
+    if (wgs <= cus && waves == 7 && max_waves >= 8 && nchunk >= 8) waves = 8;  // as in w8_stream_plan
     sp.waves = static_cast<int>(waves);
   }
   return sp;

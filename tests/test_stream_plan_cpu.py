@@ -124,18 +124,18 @@ def test_plans_picked_by_the_deep_row_sweep(probe):
     w8 = probe.mi355_probe_w8a16_stream_plan
     l16 = probe.mi355_probe_linear16_stream_plan
     for rows in (2, 3, 4):
-        assert _plan(probe, w8, rows, 3584, 18944, 0, 256) == (16, 4, 2, 1), rows   # 7B gate/up
-        assert _plan(probe, w8, rows, 18944, 3584, 0, 256) == (16, 4, 8, 1), rows   # 7B down
+        assert _plan(probe, w8, rows, 3584, 18944, 0, 256) == (15, 4, 2, 1), rows   # 7B gate/up
+        assert _plan(probe, w8, rows, 18944, 3584, 0, 256) == (14, 4, 8, 1), rows   # 7B down
         assert _plan(probe, w8, rows, 3584, 18944, 1, 256) == (8, 2, 8, 1), rows    # 7B dual gate/up
         assert _plan(probe, w8, rows, 1536, 8960, 0, 256)[0] == 8, rows             # 1.5B gate/up: k < 3072
         assert _plan(probe, w8, rows, 8960, 1536, 0, 256)[0] <= 8, rows             # narrow: every CU a workgroup
         assert _plan(probe, w8, rows, 3584, 3584, 0, 256) == (8, 2, 8, 1), rows     # 7B q/o: 224 16-row groups
-    assert _plan(probe, w8, 1, 3584, 18944, 0, 256) == (16, 4, 2, 1)   # every CU a 16-row workgroup
+    assert _plan(probe, w8, 1, 3584, 18944, 0, 256) == (15, 4, 2, 1)   # every CU a 16-row workgroup
     assert _plan(probe, w8, 1, 3584, 3584, 0, 256)[0] == 8
     assert _plan(probe, w8, 1, 18944, 3584, 0, 256) == (8, 2, 8, 1)
     assert _plan(probe, w8, 1, 3584, 18944, 1, 256)[:3] == (4, 1, 3)
-    assert _plan(probe, w8, 8, 3584, 18944, 1, 256) == (16, 4, 1, 1)
-    assert _plan(probe, l16, 4, 18944, 3584, 256)[:3] == (16, 4, 8)
+    assert _plan(probe, w8, 8, 3584, 18944, 1, 256) == (15, 4, 1, 1)
+    assert _plan(probe, l16, 4, 18944, 3584, 256)[:3] == (14, 4, 8)
     assert _plan(probe, l16, 3, 18944, 3584, 256)[0] == 8
 
 
@@ -145,8 +145,8 @@ def test_dual_plans_by_workgroups_per_cu(probe):
     workgroups of 2 waves where 8-row ones would number under 4 per CU (the
     0.5B MLP, k 896 x n 4864), 8-row ones of 2 waves where they do not (1.5B,
     k 1536 x n 8960; int8 3B, k 2048 x n 11008), of one wave beyond 16 rows
-    of x; 16-bit weights from k = 2048
-    on 16-row workgroups of about 5 waves per CU (3B: 2, 7B: 1)."""
+    of x; 16-bit weights from k = 2048 on workgroups of the 16-row class
+    (balanced over the CUs: 15 rows) of about 5 waves per CU (3B: 2, 7B: 1)."""
     w8 = probe.mi355_probe_w8a16_stream_plan
     gu = probe.mi355_probe_gate_up16_stream_plan
     for rows in (6, 8, 12, 16, 24, 32):
@@ -157,7 +157,7 @@ def test_dual_plans_by_workgroups_per_cu(probe):
     for rows in (10, 12, 16):
         assert _plan(probe, gu, rows, 896, 4864, 256) == (4, 1, 2, 1), rows
         assert _plan(probe, gu, rows, 1536, 8960, 256) == (8, 2, 2, 1), rows
-        assert _plan(probe, gu, rows, 2048, 11008, 256) == (16, 4, 2, 1), rows
-        assert _plan(probe, gu, rows, 3584, 18944, 256) == (16, 4, 1, 1), rows
+        assert _plan(probe, gu, rows, 2048, 11008, 256) == (15, 4, 2, 1), rows   # balanced_rows16
+        assert _plan(probe, gu, rows, 3584, 18944, 256) == (15, 4, 1, 1), rows
     assert _plan(probe, gu, 24, 896, 4864, 256) == (8, 2, 2, 1)
-    assert _plan(probe, w8, 8, 3584, 3584, 0, 256)[0] == 16
+    assert _plan(probe, w8, 8, 3584, 3584, 0, 256)[0] == 14
