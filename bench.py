@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "stream-sweep-3b14b", "stream-sweep-bal", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "stream-sweep-3b14b", "stream-sweep-bal", "stream-sweep-few16", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1111,6 +1111,11 @@ def run_only(ctx, args, sets):
                           "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP_BAL_SHAPES, rpws=STREAM_BAL_RPWS),
                           "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_BAL_SHAPES, True,
                                                                       rpws=STREAM_BAL_RPWS)}), flush=True)
+    elif args.only == "stream-sweep-few16":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_FEW16_SHAPES, True,
+                                                                rpws=(8, 12, 14, 15, 16))}), flush=True)
     elif args.only == "stream-sweep-m4":  # 1 - 4 rows on the deep projections that are not narrow
         del sets
         torch.cuda.empty_cache()
@@ -1557,6 +1562,13 @@ W8_STREAM_SWEEP_BAL_SHAPES = [("down14b_M8", 8, 13824, 5120, False), ("down14b_M
                               ("dual14b_M8", 8, 5120, 13824, True), ("gateup3b_M24", 24, 2048, 11008, False)]
 L16_SWEEP_BAL_SHAPES = [("down14b_M8", 8, 13824, 5120), ("down7b_M8", 8, 18944, 3584)]
 GU16_SWEEP_BAL_SHAPES = [("gu14b_M8", 8, 5120, 13824)]
+# the dual kernel at 5 - 16 rows where 16-row workgroups number under 4 per
+# CU (14B MLP) against the 7B MLP, and the 3B gate/up at 17 - 32 rows
+W8_STREAM_SWEEP_FEW16_SHAPES = [("dual14b_M5", 5, 5120, 13824, True), ("dual14b_M8", 8, 5120, 13824, True),
+                                ("dual14b_M12", 12, 5120, 13824, True), ("dual14b_M16", 16, 5120, 13824, True),
+                                ("dual7b_M8", 8, 3584, 18944, True), ("dual7b_M16", 16, 3584, 18944, True),
+                                ("gateup3b_M17", 17, 2048, 11008, False), ("gateup3b_M20", 20, 2048, 11008, False),
+                                ("gateup3b_M28", 28, 2048, 11008, False), ("gateup3b_M32", 32, 2048, 11008, False)]
 # 1 - 4 rows of x (one x set) on the deep projections that are not narrow
 # (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
 W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M1", 1, 3584, 18944, False), ("dual7b_M1", 1, 3584, 18944, True),

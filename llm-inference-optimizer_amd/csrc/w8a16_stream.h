@@ -309,17 +309,18 @@ inline int balanced_rows16(int n, int cus) {
 // projections with 8 rows):
 //   rows per workgroup: 8 (two 4-row sets); narrow outputs (n <= 2048, or
 //     fewer 8-row workgroups than CUs) as few as give every CU a workgroup,
-//     4 to 8; 16 at k >= 3072 with more than 4 rows of x, or with 2 - 4 (4
-//     with 16-bit weights) where that leaves every CU a workgroup (one matrix
-//     of int8 weights: 1 - 4 rows) or k >= 8192, since every workgroup
-//     re-reads a long x (half the x re-reads of 8); the dual kernel 4 with
+//     4 to 8; 16 (the class of balanced_rows16) at k >= 3072 with more than
+//     4 rows of x (k >= 2048 beyond 16 rows of int8 weights), or with 2 - 4
+//     (4 with 16-bit weights) where that leaves every CU a workgroup (one
+//     matrix of int8 weights: 1 - 4 rows) or k >= 8192, since every
+//     workgroup re-reads a long x (half the x re-reads of 8); the dual kernel 4 with
 //     one row of x (or with up to 4 below k = 3072 or on narrow outputs, or
 //     with more where 8-row workgroups would number under 4 per CU), else 8
 //     (16 as above with more than 4 rows);
 //   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
 //     8-row workgroups -- 1 beyond 16 rows --, 8 with 2 - 4 rows at k >= 3072
-//     on outputs that are not narrow, 1 with 16-row workgroups); else about
-//     14 per CU with
+//     on outputs that are not narrow, 1 with 16-row workgroups where they
+//     number at least 4 per CU, else 2); else about 14 per CU with
 //     up to 4 rows of x, 12 (one workgroup per CU) or 10 with more, 7 for
 //     16-row workgroups (6 with more than 8 rows of x); at least 2 (but for
 //     the dual kernel's 1) and at most 16 waves (8 where stream_max_threads
@@ -362,8 +363,12 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   // with 2 - 4 (4 with 16-bit weights, whose x is half as many bytes per
   // weight byte) at k >= 8192 or where 16-row workgroups still give every CU
   // one -- there with one row of x of int8 weights too
-  const bool deep16 = k >= 3072 && (two_sets || (rows >= 2 * wb && k >= 8192) ||
-                                    ((wb == 1 || rows >= 4) && (n + 15) / 16 >= cus));
+  // (beyond 16 rows of x, with 4 or more times its bytes re-read per 8-row
+  // workgroup, from k = 2048 for int8 weights: 3B gate/up, 32 rows 19.68 ->
+  // 13.72 us, 20 rows 12.11 -> 11.11)
+  const int deep_k = rows > 16 && wb == 1 ? 2048 : 3072;
+  const bool deep16 = k >= deep_k && (two_sets || (rows >= 2 * wb && k >= 8192) ||
+                                      ((wb == 1 || rows >= 4) && (n + 15) / 16 >= cus));
   const bool narrow = n <= 2048 || (n + 7) / 8 < cus;
   // the dual kernel at 2 - 4 rows where one matrix would take 16-row workgroups
   const bool deep_dual = dual && rows >= 2 && !two_sets && deep16 && !narrow;
@@ -392,8 +397,11 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   int min_waves = 2;
   if (dual) {
     // 8-row workgroups with 6 or 8 x sets: one wave (1.5B MLP, 24 rows 13.77
-    // us against 15.50 with two; 3B, 32 rows 21.29 vs 25.68)
-    const bool one_wave = wg16 || (sp.rpw == 8 && rows > 16);
+    // us against 15.50 with two; 3B, 32 rows 21.29 vs 25.68); the 16-row
+    // class one where its workgroups number at least 4 per CU, else two (7B
+    // MLP, 1263 of them, 16 rows 33.17 us against 39.60 with two; 14B, 988,
+    // 35.33 vs 38.15 with one)
+    const bool one_wave = (wg16 && wgs >= 4 * static_cast<int64_t>(cus)) || (sp.rpw == 8 && rows > 16);
     waves = one_wave ? 1 : (two_sets ? 2 : (deep_dual ? 8 : 3));
     min_waves = one_wave ? 1 : 2;
   } else {

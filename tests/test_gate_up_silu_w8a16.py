@@ -76,6 +76,9 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
     # with k <= 2048 in place of the small tiles (ragged last workgroup), and
     # where the small tiles do not pay (3B MLP)
     (20, 1536, 8964, F16), (24, 2048, 11008, BF16), (30, 2048, 11008, F16),
+    # 5 - 16 rows at k >= 3072 where the 16-row class numbers under 4
+    # workgroups per CU: two waves (ragged last workgroup, partial last chunk)
+    (6, 3104, 6004, F16), (12, 3104, 6004, BF16),
     # 9 - 16 rows: three and four x sets; the 7B MLP and k >= 3072 with n > 2048 (16-row
     # workgroups, one wave; a partial last chunk and a ragged last workgroup at k 3104 x n 2900)
     (12, 1536, 8960, F16), (13, 272, 1000, BF16), (16, 1552, 520, F16), (16, 3584, 18944, BF16),

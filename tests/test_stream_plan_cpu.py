@@ -160,4 +160,19 @@ def test_dual_plans_by_workgroups_per_cu(probe):
         assert _plan(probe, gu, rows, 2048, 11008, 256) == (15, 4, 2, 1), rows   # balanced_rows16
         assert _plan(probe, gu, rows, 3584, 18944, 256) == (15, 4, 1, 1), rows
     assert _plan(probe, gu, 24, 896, 4864, 256) == (8, 2, 2, 1)
+    # the int8 dual kernel's 16-row class: one wave with at least 4 workgroups
+    # per CU (7B MLP), two with fewer (14B MLP)
+    assert _plan(probe, w8, 8, 3584, 18944, 1, 256) == (15, 4, 1, 1)
+    assert _plan(probe, w8, 12, 5120, 13824, 1, 256) == (14, 4, 2, 1)
+
+
+def test_wide_rows_from_k_2048_beyond_16_rows(probe):
+    """Beyond 16 rows of x one int8 matrix takes the 16-row class from k =
+    2048 (3B gate/up: 15 rows per workgroup, 2 waves), the 16-bit linear
+    still from k = 3072 bytes."""
+    w8 = probe.mi355_probe_w8a16_stream_plan
+    for rows in (17, 24, 32):
+        assert _plan(probe, w8, rows, 2048, 11008, 0, 256) == (15, 4, 2, 1), rows
+    assert _plan(probe, w8, 16, 2048, 11008, 0, 256)[0] == 8
+    assert _plan(probe, w8, 24, 896, 4864, 0, 256)[0] == 8
     assert _plan(probe, w8, 8, 3584, 3584, 0, 256)[0] == 14
