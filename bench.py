@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "stream-sweep-3b14b", "stream-sweep-bal", "stream-sweep-few16", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "stream-sweep-3b14b", "stream-sweep-bal", "stream-sweep-few16", "stream-sweep-dual4", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1116,6 +1116,13 @@ def run_only(ctx, args, sets):
         torch.cuda.empty_cache()
         print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_FEW16_SHAPES, True,
                                                                 rpws=(8, 12, 14, 15, 16))}), flush=True)
+    elif args.only == "stream-sweep-dual4":
+        del sets
+        torch.cuda.empty_cache()
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_DUAL4_SHAPES, True,
+                                                                rpws=(4, 8, 12, 14, 16)),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_DUAL4_SHAPES, True,
+                                                                      rpws=(4, 8, 12, 14, 15, 16))}), flush=True)
     elif args.only == "stream-sweep-m4":  # 1 - 4 rows on the deep projections that are not narrow
         del sets
         torch.cuda.empty_cache()
@@ -1569,6 +1576,13 @@ W8_STREAM_SWEEP_FEW16_SHAPES = [("dual14b_M5", 5, 5120, 13824, True), ("dual14b_
                                 ("dual7b_M8", 8, 3584, 18944, True), ("dual7b_M16", 16, 3584, 18944, True),
                                 ("gateup3b_M17", 17, 2048, 11008, False), ("gateup3b_M20", 20, 2048, 11008, False),
                                 ("gateup3b_M28", 28, 2048, 11008, False), ("gateup3b_M32", 32, 2048, 11008, False)]
+# the gate/up + SiLU-and-mul kernels at 2 - 4 rows below k = 3072
+W8_STREAM_SWEEP_DUAL4_SHAPES = [("dual_gateup_M2", 2, 1536, 8960, True), ("dual_gateup_M3", 3, 1536, 8960, True),
+                                ("dual_gateup_M4", 4, 1536, 8960, True), ("dual3b_M2", 2, 2048, 11008, True),
+                                ("dual3b_M3", 3, 2048, 11008, True), ("dual3b_M4", 4, 2048, 11008, True),
+                                ("dual0.5b_M4", 4, 896, 4864, True), ("dual14b_M4", 4, 5120, 13824, True)]
+GU16_SWEEP_DUAL4_SHAPES = [("gu1.5b_M4", 4, 1536, 8960), ("gu3b_M4", 4, 2048, 11008), ("gu3b_M8", 8, 2048, 11008),
+                           ("gu14b_M16", 16, 5120, 13824), ("gu14b_M12", 12, 5120, 13824)]
 # 1 - 4 rows of x (one x set) on the deep projections that are not narrow
 # (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
 W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M1", 1, 3584, 18944, False), ("dual7b_M1", 1, 3584, 18944, True),

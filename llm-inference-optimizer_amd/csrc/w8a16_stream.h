@@ -317,7 +317,8 @@ inline int balanced_rows16(int n, int cus) {
 //     one row of x (or with up to 4 below k = 3072 or on narrow outputs, or
 //     with more where 8-row workgroups would number under 4 per CU), else 8
 //     (16 as above with more than 4 rows);
-//   waves per workgroup: the dual kernel 3 (2 with more than 4 rows of x and
+//   waves per workgroup: the dual kernel 3 (half the chunks, two in flight
+//     each, with 2 - 4 rows below k = 3072; 2 with more than 4 rows of x and
 //     8-row workgroups -- 1 beyond 16 rows --, 8 with 2 - 4 rows at k >= 3072
 //     on outputs that are not narrow, 1 with 16-row workgroups where they
 //     number at least 4 per CU, else 2); else about 14 per CU with
@@ -327,7 +328,8 @@ inline int balanced_rows16(int n, int cus) {
 //     gives 512 threads), no more than 256-column chunks, and a multiple of
 //     4 above 8 when there is at most one workgroup per CU, so the CU's 4
 //     SIMDs carry equal loads (14 waves: 1.06x the time of 12);
-//   1 chunk in flight per wave (the CU's waves keep enough bytes in flight).
+//   1 chunk in flight per wave (the CU's waves keep enough bytes in flight;
+//     the dual kernel's 2 - 4 rows below k = 3072 as above).
 // 9 - 16 rows of x (three or four x sets; bench.py --only stream-sweep16 and
 // stream-sweep16-wide, 9, 12 and 16 rows): 8 weight rows per workgroup,
 // about 8 waves per CU with one workgroup per CU, else 5 (1.5B down, 16 rows
@@ -395,7 +397,14 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
   int64_t waves;
   int min_waves = 2;
-  if (dual) {
+  if (dual && rows >= 2 && !two_sets && !deep_dual && !wg16 && !narrow && nchunk >= 2) {
+    // 2 - 4 rows below k = 3072: every chunk of a wave in flight at once, two
+    // per wave (0.5B MLP, 4 rows 4.16 us against 4.66 with 3 waves of one;
+    // 3B, 2 rows 9.20 vs 9.39; bench.py --only stream-sweep-dual4)
+    sp.u = 2;
+    waves = (nchunk + 1) / 2;
+    min_waves = 1;
+  } else if (dual) {
     // 8-row workgroups with 6 or 8 x sets: one wave (1.5B MLP, 24 rows 13.77
     // us against 15.50 with two; 3B, 32 rows 21.29 vs 25.68); the 16-row
     // class one where its workgroups number at least 4 per CU, else two (7B
@@ -436,8 +445,8 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
 // workgroup and 2 waves (1.5B, 16 rows 13.44 vs 15.73 us) or 4 rows where
 // 8-row workgroups would number under 4 per CU (0.5B, 10 / 12 rows 6.00 /
 // 5.92 us against 6.62 / 6.50; bench.py --only stream-sweep-dualn), from
-// k = 2048 16 rows and about 5 waves per CU (7B, 16 rows one wave, 46.1 vs
-// 50.3 us for 8 rows and 8 waves; 3B, 16 rows two, 18.43 vs 20.06).
+// k = 2048 the 16-row class and about 6 waves per CU (7B, 16 rows one wave,
+// 46.1 vs 50.3 us for 8 rows and 8 waves; 3B, 16 rows two, 18.43 vs 20.06).
 inline StreamPlan gu16_stream_plan(int rows, int k, int n, int cus) {
   StreamPlan sp{16, 4, 8, 1};
   if (rows > 16) {
@@ -447,11 +456,12 @@ inline StreamPlan gu16_stream_plan(int rows, int k, int n, int cus) {
       // 4-row workgroups where 8-row ones would number under 4 per CU
       sp = (n + 7) / 8 < 4 * cus ? StreamPlan{4, 1, 2, 1} : StreamPlan{8, 2, 2, 1};
     } else {
-      // 16-row workgroups with about 5 waves per CU (3B, 16 rows: 2 waves)
+      // the 16-row class with about 6 waves per CU (3B, 16 rows: 2 waves;
+      // 14B: 2, 48.03 us at 12 rows against 51.47 with one; 7B: 1)
       sp = StreamPlan{16, 4, 1, 1};
       if (n >= 8 * cus) sp.rpw = balanced_rows16(n, cus);
       const int64_t wgs = (n + sp.rpw - 1) / sp.rpw;
-      const int64_t w = (5 * static_cast<int64_t>(cus) + wgs / 2) / wgs;
+      const int64_t w = (6 * static_cast<int64_t>(cus) + wgs / 2) / wgs;
       sp.waves = static_cast<int>(w < 1 ? 1 : (w > 8 ? 8 : w));
     }
   } else if (k <= 2048) {

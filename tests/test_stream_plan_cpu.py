@@ -164,6 +164,12 @@ def test_dual_plans_by_workgroups_per_cu(probe):
     # per CU (7B MLP), two with fewer (14B MLP)
     assert _plan(probe, w8, 8, 3584, 18944, 1, 256) == (15, 4, 1, 1)
     assert _plan(probe, w8, 12, 5120, 13824, 1, 256) == (14, 4, 2, 1)
+    # 2 - 4 rows below k = 3072: half the chunks as waves, two in flight each
+    assert _plan(probe, w8, 4, 896, 4864, 1, 256) == (4, 1, 2, 2)
+    assert _plan(probe, w8, 2, 2048, 11008, 1, 256) == (4, 1, 4, 2)
+    assert _plan(probe, w8, 1, 1536, 8960, 1, 256) == (4, 1, 3, 1)
+    # the 16-bit kernel's 16-row class: about 6 waves per CU
+    assert _plan(probe, gu, 12, 5120, 13824, 256) == (14, 4, 2, 1)
 
 
 def test_wide_rows_from_k_2048_beyond_16_rows(probe):
