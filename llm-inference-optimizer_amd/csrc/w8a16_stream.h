@@ -313,10 +313,10 @@ inline int balanced_rows16(int n, int cus) {
 //     4 rows of x (k >= 2048 beyond 16 rows of int8 weights), or with 2 - 4
 //     (4 with 16-bit weights) where that leaves every CU a workgroup (one
 //     matrix of int8 weights: 1 - 4 rows) or k >= 8192, since every
-//     workgroup re-reads a long x (half the x re-reads of 8); the dual kernel 4 with
-//     one row of x (or with up to 4 below k = 3072 or on narrow outputs, or
-//     with more where 8-row workgroups would number under 4 per CU), else 8
-//     (16 as above with more than 4 rows);
+//     workgroup re-reads a long x (half the x re-reads of 8); the dual
+//     kernel 4 with one row of x (or with up to 4 below k = 3072 or on
+//     narrow outputs, or with more where 8-row workgroups would number under
+//     4 per CU), else 8 (16 as above with more than 4 rows);
 //   waves per workgroup: the dual kernel 3 (half the chunks, two in flight
 //     each, with 2 - 4 rows below k = 3072; 2 with more than 4 rows of x and
 //     8-row workgroups -- 1 beyond 16 rows --, 8 with 2 - 4 rows at k >= 3072
@@ -327,7 +327,8 @@ inline int balanced_rows16(int n, int cus) {
 //     the dual kernel's 1) and at most 16 waves (8 where stream_max_threads
 //     gives 512 threads), no more than 256-column chunks, and a multiple of
 //     4 above 8 when there is at most one workgroup per CU, so the CU's 4
-//     SIMDs carry equal loads (14 waves: 1.06x the time of 12);
+//     SIMDs carry equal loads (14 waves: 1.06x the time of 12; 8 in place
+//     of 7);
 //   1 chunk in flight per wave (the CU's waves keep enough bytes in flight;
 //     the dual kernel's 2 - 4 rows below k = 3072 as above).
 // 9 - 16 rows of x (three or four x sets; bench.py --only stream-sweep16 and
