@@ -345,8 +345,8 @@ inline int balanced_rows16(int n, int cus) {
 // 33 - 64 rows (12 or 16 x sets, one matrix; bench.py --only stream-sweep64):
 // the same, with as many 4-row weight sets as the registers of that many x
 // sets allow (16-bit weights: 2, int8 weights: 2 up to 48 rows, then 1), and
-// 7 waves per CU with more workgroups than CUs (7B down, 64 rows of 16-bit
-// weights: 4 waves 78.9 us, 3 waves 83.4).
+// 7 waves per CU with more workgroups than CUs, at least 4 per workgroup
+// (7B down, 64 rows of 16-bit weights: 4 waves 78.9 us, 3 waves 83.4).
 // 1 - 4 rows on deep rows (bench.py --only stream-sweep-m4, the 7B
 // projections and MLP at 1 - 4 rows): 16-row workgroups (7B gate/up, 3 / 4
 // rows 12.72 / 12.74 us against 14.34 / 14.87 with 8 rows; 7B down, 4 rows
@@ -419,6 +419,10 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
                                     : (four_sets ? (wgs <= cus ? 8 : (rows > 32 ? 7 : 5))
                                                  : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
+    // beyond 32 rows with more workgroups than CUs at least 4 (14B o, 48
+    // rows 26.79 us against 29.34 with 3; the 16-bit 14B down, 64 rows
+    // 85.83 vs 88.61; bench.py --only stream-sweep-14b-wide)
+    if (rows > 32 && wgs > cus && waves < 4) waves = 4;
   }
   const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, wb) / 64;
   if (waves > max_waves) waves = max_waves;
@@ -451,7 +455,10 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
 inline StreamPlan gu16_stream_plan(int rows, int k, int n, int cus) {
   StreamPlan sp{16, 4, 8, 1};
   if (rows > 16) {
-    sp = StreamPlan{8, 2, 2, 1};  // 17 - 32 rows: 0.5B, 32 rows 9.04 us vs 10.52 for skinny tiles
+    // 17 - 32 rows: 0.5B, 32 rows 9.04 us vs 10.52 for skinny tiles; one
+    // wave from k = 2048 (14B, 24 / 32 rows 58.94 / 69.05 us against 68.94 /
+    // 78.49 with two; bench.py --only stream-sweep-14b-wide)
+    sp = StreamPlan{8, 2, k >= 2048 ? 1 : 2, 1};
   } else if (rows > 8) {
     if (k < 2048) {
       // 4-row workgroups where 8-row ones would number under 4 per CU
