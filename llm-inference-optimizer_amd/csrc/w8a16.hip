@@ -12,10 +12,10 @@
 // rounding to the output type.  Here scale and bias go through one fma.
 //
 // Four kernels, picked by the launcher:
-//   w8a16_stream   rows <= 16 (decode; w8a16_stream.h), and 17 - 32 (33 -
-//                  48 for one matrix) where the small tiled shapes do not
-//                  pay (and the gate/up + SiLU-and-mul at 17 - 24 rows with
-//                  k <= 2048): weight streaming with
+//   w8a16_stream   rows <= 16 (decode; w8a16_stream.h), and 17 - 48 (49 -
+//                  64 for one matrix of at most 8 MB) where the small tiled
+//                  shapes do not pay (and the gate/up + SiLU-and-mul at 17 -
+//                  24 rows with k <= 2048): weight streaming with
 //                  lane-coalesced loads, every weight byte read once per call
 //                  at HBM bandwidth, MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
 //   w8a16_skinny   9 - 32 rows of wide outputs with 2048 < k < 3072, x
@@ -556,11 +556,15 @@ int w8_typed(const W8Params& p, hipStream_t s, int cus) {
   // 17 - 32 rows where the small tiles do not pay: the stream kernel with 6
   // or 8 x sets (1.5B down, 32 rows 20.6 -> 13.0 us; 7B down 44.4 -> 30.1;
   // 0.5B down 12.6 -> 7.3; the int8 gate/up + SiLU-and-mul, 0.5B 9.7 -> 8.9),
-  // and with 12 x sets up to 48 rows against one matrix (1.5B down, 48 rows
-  // 31.4 -> 16.4 us; 7B down 79.5 -> 59.8; 7B o 19.9 -> 15.5).  From 49 rows
-  // int8 weights leave registers for one 4-row weight set only, and the
-  // deep projections measured slower there (7B down, 64 rows 115.9 vs 82.2).
-  if ((p.rows <= 32 || (!DUAL && p.rows <= 48)) && x_fits && !wide_mid)
+  // and with 12 x sets up to 48 rows (1.5B down, 48 rows 31.4 -> 16.4 us;
+  // 7B down 79.5 -> 59.8; 7B o 19.9 -> 15.5; the int8 gate/up +
+  // SiLU-and-mul, 0.5B 15.6 -> 11.4).  From 49 rows int8 weights leave
+  // registers for one 4-row weight set only (the dual kernel none): one
+  // matrix of at most 8 MB still streams faster (0.5B down, 64 rows 14.6 ->
+  // 10.8 us; 1.5B o 9.3 -> 8.0), the deep projections do not (1.5B down,
+  // 13.8 MB, 30.9 vs 28.7 us for the skinny tiles; 7B down 115.9 vs 82.2).
+  const bool small_w = static_cast<int64_t>(p.n) * p.k <= (int64_t{8} << 20);
+  if ((p.rows <= 48 || (!DUAL && p.rows <= 64 && small_w)) && x_fits && !wide_mid)
     return w8_stream_launch<T, TO, DUAL>(p, w8_stream_plan(p.rows, p.k, p.n, DUAL, cus), s);
   if (p.rows <= 24) return w8_skinny_shape<T, TO, 3, DUAL>(p, s, cus);
   if (p.rows <= 32) return w8_skinny_shape<T, TO, 4, DUAL>(p, s, cus);

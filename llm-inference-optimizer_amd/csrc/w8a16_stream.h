@@ -300,7 +300,7 @@ inline int balanced_rows16(int n, int cus) {
   return static_cast<int>((n + rounds * cus - 1) / (rounds * cus));
 }
 
-// Launch plan for `rows` <= 64 rows of x (32 when dual) against [n, k] int8
+// Launch plan for `rows` <= 64 rows of x (48 when dual) against [n, k] int8
 // weights (two matrices when dual), fitted to a graph-timed sweep of rows per workgroup x
 // waves x chunks in flight on MI355X over the Qwen2.5-0.5B, 1.5B and 7B
 // decode projections and MLPs at 1, 4 and 8 rows (bench.py --only
@@ -407,11 +407,13 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
     min_waves = 1;
   } else if (dual) {
     // 8-row workgroups with 6 or 8 x sets: one wave (1.5B MLP, 24 rows 13.77
-    // us against 15.50 with two; 3B, 32 rows 21.29 vs 25.68); the 16-row
+    // us against 15.50 with two; 3B, 32 rows 21.29 vs 25.68), and so any
+    // workgroup with 12 x sets (0.5B, 48 rows 11.43 vs 13.20); the 16-row
     // class one where its workgroups number at least 4 per CU, else two (7B
     // MLP, 1263 of them, 16 rows 33.17 us against 39.60 with two; 14B, 988,
     // 35.33 vs 38.15 with one)
-    const bool one_wave = (wg16 && wgs >= 4 * static_cast<int64_t>(cus)) || (sp.rpw == 8 && rows > 16);
+    const bool one_wave = (wg16 && wgs >= 4 * static_cast<int64_t>(cus)) || (sp.rpw == 8 && rows > 16) ||
+                          rows > 32;
     waves = one_wave ? 1 : (two_sets ? 2 : (deep_dual ? 8 : 3));
     min_waves = one_wave ? 1 : 2;
   } else {
@@ -419,10 +421,11 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
                                     : (four_sets ? (wgs <= cus ? 8 : (rows > 32 ? 7 : 5))
                                                  : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
-    // beyond 32 rows with more workgroups than CUs at least 4 (14B o, 48
-    // rows 26.79 us against 29.34 with 3; the 16-bit 14B down, 64 rows
-    // 85.83 vs 88.61; bench.py --only stream-sweep-14b-wide)
-    if (rows > 32 && wgs > cus && waves < 4) waves = 4;
+    // beyond 32 rows with more workgroups than CUs a multiple of 4, at least
+    // 4 (14B o, 48 rows 26.79 us against 29.34 with 3; the 16-bit 14B down,
+    // 64 rows 85.83 vs 88.61; bench.py --only stream-sweep-14b-wide; 1.5B o,
+    // 64 rows 8.03 vs 10.70 with 5)
+    if (rows > 32 && wgs > cus) waves = waves < 4 ? 4 : waves / 4 * 4;
   }
   const int max_waves = stream_max_threads(sp.r4, stream_x_sets(rows), sp.u, dual, wb) / 64;
   if (waves > max_waves) waves = max_waves;
@@ -526,16 +529,16 @@ inline StreamPlan l16_stream_plan(int rows, int k, int n, int cus) {
   return sp;
 }
 
-// Launches w8a16_stream with plan `sp` (rows <= 64, <= 32 when DUAL; k, qs
+// Launches w8a16_stream with plan `sp` (rows <= 64, <= 48 when DUAL; k, qs
 // multiples of 16 -- of 8 for 16-bit weights --, xs a multiple of 8, x and
 // the weights 16-byte aligned: the callers check these).
 template <typename T, typename TO, bool DUAL, int WB = 1>
 int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   constexpr int NQ = DUAL ? 2 : 1;
   const int mt4 = stream_x_sets(p.rows);  // 4-row x sets: 1 .. 4, 6, 8, 12, 16
-  if (p.rows < 1 || p.rows > (DUAL ? 32 : 64) || (mt4 > 2 && sp.u > 1)) {
+  if (p.rows < 1 || p.rows > (DUAL ? 48 : 64) || (mt4 > 2 && sp.u > 1)) {
     set_error("w8a16 stream launch: %d rows of x (1 - %d; more than 8 take one chunk in flight, u %d)", p.rows,
-              DUAL ? 32 : 64, sp.u);
+              DUAL ? 48 : 64, sp.u);
     return MI355_ERR_UNSUPPORTED;
   }
   if ((sp.r4 != 1 && sp.r4 != 2 && sp.r4 != 4) || sp.rpw < 1 || sp.rpw > 4 * sp.r4) {
@@ -570,11 +573,10 @@ int w8_stream_launch(const W8Params& p, const StreamPlan& sp, hipStream_t s) {
   if constexpr (stream_max_threads(R4, MT4, 1, DUAL, WB) > 0) MI355_W8S(R4, MT4, 1);
 #define MI355_W8S_MT8(R4) \
   if (mt4 == 6) { MI355_W8S_IF(R4, 6) } else { MI355_W8S_IF(R4, 8) }
-  // 12 or 16 x sets (33 - 64 rows): one matrix only
+  // 12 or 16 x sets (33 - 64 rows; the dual kernel 12, with one 4-row weight
+  // set: the shapes whose registers fit)
 #define MI355_W8S_MT16(R4) \
-  if constexpr (!DUAL) {                                   \
-    if (mt4 == 12) { MI355_W8S_IF(R4, 12) } else { MI355_W8S_IF(R4, 16) } \
-  }
+  if (mt4 == 12) { MI355_W8S_IF(R4, 12) } else { MI355_W8S_IF(R4, 16) }
   if (mt4 <= 2) {
     if (sp.r4 == 4) { MI355_W8S_MT(4) } else if (sp.r4 == 2) { MI355_W8S_MT(2) } else { MI355_W8S_MT(1) }
   } else if (mt4 <= 4) {

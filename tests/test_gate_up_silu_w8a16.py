@@ -82,6 +82,9 @@ def _check(orc, x, qg, sg, qu, su, got16, got32):
     # 2 - 4 rows below k = 3072: two chunks in flight per wave (a ragged last
     # workgroup; a partial last chunk and an odd chunk count at k 2064)
     (2, 1536, 8960, F16), (4, 896, 4874, BF16), (3, 2064, 11008, F16),
+    # 33 - 48 rows where the small tiles do not pay: 12 x sets, one 4-row
+    # weight set per workgroup, one wave (a ragged last workgroup)
+    (40, 896, 4864, F16), (48, 896, 4874, BF16),
     # 9 - 16 rows: three and four x sets; the 7B MLP and k >= 3072 with n > 2048 (16-row
     # workgroups, one wave; a partial last chunk and a ragged last workgroup at k 3104 x n 2900)
     (12, 1536, 8960, F16), (13, 272, 1000, BF16), (16, 1552, 520, F16), (16, 3584, 18944, BF16),

@@ -2,7 +2,7 @@
 (``w8_stream_plan``, ``l16_stream_plan`` and ``gu16_stream_plan`` in
 csrc/w8a16_stream.h, reached
 through the probe library's plan exports; no GPU call): every plan the
-launchers can produce (1 - 64 rows; 32 for the dual kernel) must be one
+launchers can produce (1 - 64 rows; 48 for the dual kernel) must be one
 the launcher accepts -- at most the kernel's thread limit (16 waves, 8 where its registers need
 more room) and no more waves than 256-byte chunks, rows per workgroup
 within its 4-row sets, and for more than 8 rows of x one chunk in flight
@@ -59,7 +59,7 @@ NS = (1, 7, 37, 256, 896, 1000, 1536, 2048, 3584, 4864, 8960, 18944, 29568, 6553
 def test_w8a16_plan_is_launchable(probe, cus):
     out = (ctypes.c_int * 4)()
     for rows, k, n, dual in itertools.product(range(1, 49), KS, NS, (0, 1)):
-        if dual and rows > 32:  # the dual kernel serves up to 32 rows
+        if dual and rows > 48:  # the dual kernel serves up to 48 rows
             continue
         probe.mi355_probe_w8a16_stream_plan(rows, k, n, dual, cus, out)
         _check(tuple(out), rows, k, 2 if dual else 1, probe)

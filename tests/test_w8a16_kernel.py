@@ -153,6 +153,9 @@ STREAM_CASES += [(m, K, N, F16 if (m + K) % 2 else BF16, m % 2 == 1)
                  for m in (1, 2, 3, 4)
                  for K, N in ((3104, 4204), (3584, 10008), (3104, 2900))]
 STREAM_CASES += [(3, 18944, 3584, BF16, False)]
+# 49 - 64 rows of one matrix of at most 8 MB: 16 x sets, one 4-row weight set
+# per workgroup (narrow outputs, a ragged last workgroup, a partial last chunk)
+STREAM_CASES += [(56, 4864, 896, F16, True), (64, 1536, 1536, BF16, False), (60, 1552, 1002, F16, False)]
 # beyond 16 rows from k = 2048: the 16-row class (balanced over the CUs; a
 # ragged last workgroup and a partial last chunk at 2064 x 4204)
 STREAM_CASES += [(20, 2048, 11008, F16, True), (28, 2064, 4204, BF16, False), (32, 2048, 6000, F16, False)]
