@@ -5,7 +5,8 @@ output dtype and shapes of the reference's launcher
 (src/kernels/w8a16_matmul_triton.py:102-134); the Triton kernel it launched is
 replaced by hand-written HIP kernels behind the C ABI
 ``mi355_w8a16_linear_fwd``: a weight-streaming MFMA kernel for decode batches
-(<= 32 rows, 48 on narrow outputs), an LDS-tiled MFMA GEMM for larger ones.  Arithmetic as there:
+(<= 16 rows; up to 48 -- 64 for matrices of at most 8 MB -- where the
+small tiles do not pay), an LDS-tiled MFMA GEMM for larger ones.  Arithmetic as there:
 ``out = (sum_k x * w_q) * scale + bias`` with the integer dot product in fp32,
 the scale applied once, one rounding to x's dtype.
 
