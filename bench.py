@@ -74,7 +74,7 @@ def parse_args():
                                       "gate-up-prefill", "gate-up-w8", "gate-up-w8-decode", "w8a16", "w8a16-decode", "decode-wide-rows",
                                       "w8a16-prefill", "w8a16-prefill-1.5b", "prefill-core",
                                       "gate-up-w8-prefill", "w8a16-prefill-wide", "w8a16-prefill-narrow",
-                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "stream-sweep-3b14b", "stream-sweep-bal", "stream-sweep-few16", "stream-sweep-dual4", "stream-sweep-14b-wide", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
+                                      "gate-up-prefill-sweep", "w8a16-prefill-ragged", "w8-decomp", "w8-layouts", "w8-layouts8", "w8-stream-sweep", "gu16-stream-sweep", "stream-sweep16", "stream-sweep16-wide", "stream-sweep-r8", "stream-sweep-m4", "stream-sweep16-k", "stream-sweep-dualn", "stream-sweep-dual32", "stream-sweep-3b14b", "stream-sweep-bal", "stream-sweep-few16", "stream-sweep-dual4", "stream-sweep-14b-wide", "stream-sweep-smallm", "l16-stream-sweep", "stream-sweep32", "stream-sweep64", "stage3",
                                       "e2e-compact", "e2e-int8-compact"],
                    default=None,
                    help="run one kernel loop only (for profiler runs)")
@@ -1131,6 +1131,14 @@ def run_only(ctx, args, sets):
                           "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP_14B_WIDE_SHAPES, rpws=rp),
                           "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_14B_WIDE_SHAPES, True,
                                                                       rpws=rp)}), flush=True)
+    elif args.only == "stream-sweep-smallm":  # the 3B and 14B shapes at 1 - 4 rows
+        del sets
+        torch.cuda.empty_cache()
+        rp = (4, 6, 8, 10, 12, 14, 16)
+        print(json.dumps({"w8a16_stream_sweep": w8_stream_sweep(ctx, W8_STREAM_SWEEP_SMALLM_SHAPES, True, rpws=rp),
+                          "linear16_stream_sweep": l16_stream_sweep(ctx, L16_SWEEP_SMALLM_SHAPES, rpws=rp),
+                          "gate_up16_stream_sweep": gu16_stream_sweep(ctx, GU16_SWEEP_SMALLM_SHAPES, True,
+                                                                      rpws=rp)}), flush=True)
     elif args.only == "stream-sweep-m4":  # 1 - 4 rows on the deep projections that are not narrow
         del sets
         torch.cuda.empty_cache()
@@ -1598,6 +1606,16 @@ W8_STREAM_SWEEP_14B_WIDE_SHAPES = [("down14b_M48", 48, 13824, 5120, False), ("o1
 L16_SWEEP_14B_WIDE_SHAPES = [("down14b_M32", 32, 13824, 5120), ("down14b_M64", 64, 13824, 5120),
                              ("o14b_M32", 32, 5120, 5120)]
 GU16_SWEEP_14B_WIDE_SHAPES = [("gu14b_M24", 24, 5120, 13824), ("gu14b_M32", 32, 5120, 13824)]
+# the 3B and 14B shapes at 1 - 4 rows
+W8_STREAM_SWEEP_SMALLM_SHAPES = [("down14b_M1", 1, 13824, 5120, False), ("down14b_M4", 4, 13824, 5120, False),
+                                 ("o14b_M1", 1, 5120, 5120, False), ("o14b_M4", 4, 5120, 5120, False),
+                                 ("gateup14b_M1", 1, 5120, 13824, False), ("gateup14b_M4", 4, 5120, 13824, False),
+                                 ("dual14b_M1", 1, 5120, 13824, True), ("dual14b_M2", 2, 5120, 13824, True),
+                                 ("down3b_M1", 1, 11008, 2048, False), ("gateup3b_M1", 1, 2048, 11008, False),
+                                 ("dual3b_M1", 1, 2048, 11008, True)]
+L16_SWEEP_SMALLM_SHAPES = [("down14b_M1", 1, 13824, 5120), ("down14b_M4", 4, 13824, 5120),
+                           ("down3b_M1", 1, 11008, 2048), ("down3b_M4", 4, 11008, 2048)]
+GU16_SWEEP_SMALLM_SHAPES = [("gu14b_M1", 1, 5120, 13824), ("gu14b_M4", 4, 5120, 13824), ("gu3b_M1", 1, 2048, 11008)]
 # 1 - 4 rows of x (one x set) on the deep projections that are not narrow
 # (k >= 3072, more 8-row workgroups than CUs): 8- against 16-row workgroups
 W8_STREAM_SWEEP_M4_SHAPES = [("gateup7b_M1", 1, 3584, 18944, False), ("dual7b_M1", 1, 3584, 18944, True),

@@ -320,10 +320,11 @@ inline int balanced_rows16(int n, int cus) {
 //   waves per workgroup: the dual kernel 3 (half the chunks, two in flight
 //     each, with 2 - 4 rows below k = 3072; 2 with more than 4 rows of x and
 //     8-row workgroups -- 1 beyond 16 rows --, 8 with 2 - 4 rows at k >= 3072
-//     on outputs that are not narrow, 1 with 16-row workgroups where they
-//     number at least 4 per CU, else 2); else about 14 per CU with
-//     up to 4 rows of x, 12 (one workgroup per CU) or 10 with more, 7 for
-//     16-row workgroups (6 with more than 8 rows of x); at least 2 (but for
+//     on outputs that are not narrow, 8 with one row at k >= 2048, 1 with
+//     16-row workgroups where they number at least 4 per CU, else 2); else
+//     about 14 per CU with up to 4 rows of x, 12 (one workgroup per CU) or
+//     10 with more, 7 for 16-row workgroups (6 with more than 8 rows of x,
+//     12 with up to 4 and more workgroups than CUs); at least 2 (but for
 //     the dual kernel's 1) and at most 16 waves (8 where stream_max_threads
 //     gives 512 threads), no more than 256-column chunks, and a multiple of
 //     4 above 8 when there is at most one workgroup per CU, so the CU's 4
@@ -414,10 +415,15 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
     // 35.33 vs 38.15 with one)
     const bool one_wave = (wg16 && wgs >= 4 * static_cast<int64_t>(cus)) || (sp.rpw == 8 && rows > 16) ||
                           rows > 32;
-    waves = one_wave ? 1 : (two_sets ? 2 : (deep_dual ? 8 : 3));
+    // (one row of x: 8 waves from k = 2048, 14B MLP 22.61 us against 24.96
+    // with 3; 3B 8.99 vs 9.42)
+    waves = one_wave ? 1 : (two_sets ? 2 : (deep_dual || (rows == 1 && k >= 2048) ? 8 : 3));
     min_waves = one_wave ? 1 : 2;
   } else {
-    const int per_cu = wg16 && sp.r4 == 4 ? (four_sets && rows <= 16 ? 6 : 7)
+    // (the 16-row class with one x set and more workgroups than CUs: 12 per
+    // CU, its waves carrying few bytes each -- 14B down, 1 row 14.12 us
+    // against 15.71 with 7 per CU; bench.py --only stream-sweep-smallm)
+    const int per_cu = wg16 && sp.r4 == 4 ? (four_sets && rows <= 16 ? 6 : (two_sets || wgs <= cus ? 7 : 12))
                                     : (four_sets ? (wgs <= cus ? 8 : (rows > 32 ? 7 : 5))
                                                  : (two_sets ? (wgs <= cus ? 12 : 10) : 14));
     waves = (static_cast<int64_t>(per_cu) * cus + wgs / 2) / wgs;
