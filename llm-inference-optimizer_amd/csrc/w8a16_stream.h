@@ -312,7 +312,8 @@ inline int balanced_rows16(int n, int cus) {
 //     4 to 8; 16 (the class of balanced_rows16) at k >= 3072 with more than
 //     4 rows of x (k >= 2048 beyond 16 rows of int8 weights), or with 2 - 4
 //     (4 with 16-bit weights) where that leaves every CU a workgroup (one
-//     matrix of int8 weights: 1 - 4 rows) or k >= 8192, since every
+//     matrix of int8 weights: 1 - 4 rows, at 1 row 4 per CU) or k >= 8192,
+//     since every
 //     workgroup re-reads a long x (half the x re-reads of 8); the dual
 //     kernel 4 with one row of x (or with up to 4 below k = 3072 or on
 //     narrow outputs, or with more where 8-row workgroups would number under
@@ -371,8 +372,10 @@ inline StreamPlan w8_stream_plan(int rows, int k, int n, bool dual, int cus, int
   // workgroup, from k = 2048 for int8 weights: 3B gate/up, 32 rows 19.68 ->
   // 13.72 us, 20 rows 12.11 -> 11.11)
   const int deep_k = rows > 16 && wb == 1 ? 2048 : 3072;
+  // (with one row of x, 4 per CU: the 14B projections, 320 - 864 of them,
+  // run 1.4 - 4% faster on 8-row workgroups; the 7B gate/up has 1184)
   const bool deep16 = k >= deep_k && (two_sets || (rows >= 2 * wb && k >= 8192) ||
-                                      ((wb == 1 || rows >= 4) && (n + 15) / 16 >= cus));
+                                      ((wb == 1 || rows >= 4) && (n + 15) / 16 >= (rows == 1 ? 4 : 1) * cus));
   const bool narrow = n <= 2048 || (n + 7) / 8 < cus;
   // the dual kernel at 2 - 4 rows where one matrix would take 16-row workgroups
   const bool deep_dual = dual && rows >= 2 && !two_sets && deep16 && !narrow;

@@ -135,7 +135,8 @@ def test_plans_picked_by_the_deep_row_sweep(probe):
     assert _plan(probe, w8, 1, 18944, 3584, 0, 256) == (8, 2, 8, 1)
     assert _plan(probe, w8, 1, 3584, 18944, 1, 256)[:3] == (4, 1, 8)   # one row, k >= 2048: 8 waves
     assert _plan(probe, w8, 1, 1536, 8960, 1, 256)[:3] == (4, 1, 3)
-    assert _plan(probe, w8, 1, 13824, 5120, 0, 256) == (10, 4, 6, 1)  # 14B down: 12 waves per CU
+    assert _plan(probe, w8, 4, 13824, 5120, 0, 256) == (10, 4, 6, 1)  # 14B down: 12 waves per CU
+    assert _plan(probe, w8, 1, 13824, 5120, 0, 256)[0] == 8           # one row: under 4 per CU
     assert _plan(probe, w8, 8, 3584, 18944, 1, 256) == (15, 4, 1, 1)
     assert _plan(probe, l16, 4, 18944, 3584, 256)[:3] == (14, 4, 8)
     assert _plan(probe, l16, 3, 18944, 3584, 256)[0] == 8
