@@ -131,7 +131,8 @@ def test_closer_to_exact_than_the_unfused_chain(pkg, orc, cuda, rows):
     assert e_fused < e_chain
 
 
-@pytest.mark.parametrize("rows,k,n", [(8, 1536, 8960), (16, 1536, 8960), (512, 1536, 8960), (24, 896, 4864)])
+@pytest.mark.parametrize("rows,k,n", [(8, 1536, 8960), (16, 1536, 8960), (512, 1536, 8960), (24, 896, 4864),
+                                      (48, 896, 4864), (4, 896, 4864)])
 def test_graph_replays_match_eager(pkg, cuda, rows, k, n):
     x, qg, sg, qu, su = _inputs(rows, k, n, BF16, 9, cuda, pkg)
     xs = x.clone()

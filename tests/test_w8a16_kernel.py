@@ -382,8 +382,10 @@ def test_out_row_stride_through_abi(pkg, cuda, M):
 
 
 @pytest.mark.parametrize("M,K,N", [(8, 1536, 8960), (16, 1536, 8960), (100, 1536, 8960),
-                                   # 17 - 48 rows on the stream kernel (6, 8 and 12 x sets)
-                                   (32, 8960, 1536), (20, 4864, 896), (44, 8960, 1536)])
+                                   # 17 - 64 rows on the stream kernel (6, 8, 12 and 16 x sets)
+                                   (32, 8960, 1536), (20, 4864, 896), (44, 8960, 1536), (64, 4864, 896),
+                                   # the 16-row class balanced over the CUs
+                                   (8, 13824, 5120)])
 def test_graph_replays_match_eager(pkg, cuda, M, K, N):
     lin = _linear(K, N, False, cuda, seed=15)
     q = pkg.QuantizedLinearInt8.from_linear(lin)
